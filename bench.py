@@ -1,0 +1,345 @@
+"""Benchmark of the MI355X kernel set of the QLoRA step (BASELINE.json metric), one GPU.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--cpu-seconds S]
+
+A step is one pass of the hot path over one batch of synthetic input: every kernel of the
+solution/ set, forward and backward, once, at the 2048-token shape of Qwen2.5-1.5B
+(config 1, the CPU-runnable RMSNorm case, is the same RMSNorm
+shape).  Inputs are resident in HBM before the timed region.  Each launch is bracketed by HIP
+events on the stream it runs on (torch's current stream); the queue is kept ahead of the GPU
+(launches go straight through the C ABI with preallocated buffers, after a GPU-side prefill),
+so an event pair measures the kernel, not the host.  Two input sets per kernel alternate, and
+the other kernels of the step move > 600 MB between two launches of one kernel, so the
+256 MB Infinity Cache does not serve its inputs.
+
+Prints ONE JSON line: value = the set's aggregate compulsory HBM bytes / summed kernel time
+(GB/s), per-kernel us / GB/s / fraction of the 8 TB/s peak, the roofline of the dominant kernel,
+and the CPU baseline (the reference's eager PyTorch path on the host cores, oracle/baseline.py).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from testt_amd import _ext, workloads  # noqa: E402
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Case:
+    """One kernel at its BASELINE shape: algorithmic bytes and per-input-set launch args."""
+
+    def __init__(self, name, kernel, entry, nbytes, sets, cpu=None):
+        self.name, self.kernel, self.entry, self.nbytes = name, kernel, entry, nbytes
+        self.sets = sets            # list of (tensors kept alive, ctypes args without stream)
+        self.cpu = cpu              # cpu(ob) -> callable running the CPU eager path once, given
+                                    # the oracle.baseline module (imported by the CPU leg only)
+        self.fn = getattr(_ext.lib(), entry)
+        self.times = []
+
+    def launch(self, i, stream):
+        status = self.fn(*self.sets[i % len(self.sets)][1], stream)
+        if status:
+            raise _ext.SoupkError(f"{self.entry} failed with status {status}")
+
+
+def p(t):
+    return t.data_ptr() if t is not None else None
+
+
+def build_cases(dev, n_sets=2):
+    cases = []
+    H, I, NH, NKV, D, B, T = (workloads.HIDDEN, workloads.INTER, workloads.N_HEADS,
+                              workloads.N_KV, workloads.HEAD_DIM, workloads.BATCH, workloads.SEQ)
+    M = B * T
+
+    # nf4_unpack: gate|up [17920, 1536]
+    sets = []
+    for i in range(n_sets):
+        w = workloads.nf4_weight(2 * I, H, seed=1 + i, device=dev)
+        st = w.quant_state
+        out = torch.empty((2 * I, H), dtype=torch.float16, device=dev)
+        sets.append(((w, out), (p(w.data), p(st.absmax), p(st.state2.code), p(st.state2.absmax),
+                                p(st.offset), p(st.code), p(out), w.data.numel(), 64, 256)))
+    st = sets[0][0][0].quant_state
+    nbytes = (sets[0][0][0].data.numel() + st.absmax.numel() + 4 * st.state2.absmax.numel()
+              + 4 * 256 + 4 * 16 + 4 + 2 * 2 * sets[0][0][0].data.numel())
+
+    def nf4_cpu(ob):
+        w_cpu = workloads.nf4_weight(2 * I, H, seed=1)
+        return lambda: ob.nf4_unpack(w_cpu)
+
+    cases.append(Case("nf4_unpack", "nf4_unpack_vec_kernel", "soupk_nf4_unpack", nbytes, sets,
+                      cpu=nf4_cpu))
+
+    # add + RMSNorm forward (delta, pad output) and backward at [2048, 1536]
+    fsets, bsets = [], []
+    for i in range(n_sets):
+        x, delta, w, pad_idx, padded = workloads.rmsnorm_inputs(M, H, M, seed=2 + 10 * i,
+                                                                device=dev)
+        s = torch.empty_like(x)
+        y = torch.empty((M, H), dtype=torch.float16, device=dev)
+        ypad = torch.empty((M, H), dtype=torch.float32, device=dev)
+        rstd = torch.empty(M, dtype=torch.float32, device=dev)
+        fsets.append(((x, delta, w, pad_idx, s, y, ypad, rstd),
+                      (p(x), p(delta), p(w), p(s), p(y), p(ypad), p(pad_idx), None, p(rstd), M, M,
+                       H, 1e-6)))
+        dy, dypad, ds = workloads.rmsnorm_grads(M, H, M, seed=3 + 10 * i, device=dev)
+        s_b = x + delta.float()
+        rstd_b = torch.rsqrt(s_b.pow(2).mean(-1) + 1e-6)
+        dx = torch.empty_like(x)
+        dd = torch.empty((M, H), dtype=torch.float16, device=dev)
+        bsets.append(((s_b, rstd_b, w, dy, dypad, pad_idx, ds, dx, dd),
+                      (p(s_b), p(rstd_b), p(w), p(dy), p(dypad), p(pad_idx), p(ds), p(dx), p(dd),
+                       M, M, H)))
+    row_elems = M * H
+
+    def rms_cpu(ob, backward):
+        xc, dc, wc, pc, _ = workloads.rmsnorm_inputs(M, H, M, seed=2)
+        gyc, gpc, gsc = workloads.rmsnorm_grads(M, H, M, seed=3)
+        if backward:
+            return lambda: ob.rmsnorm_bwd(xc, dc, wc, 1e-6, pc, gyc, gpc, gsc)
+        return lambda: ob.rmsnorm_fwd(xc, dc, wc, 1e-6, pc, M)
+
+    cases.append(Case("rmsnorm_fwd", "rmsnorm_fwd_kernel", "soupk_rmsnorm_fwd",
+                      16 * row_elems + 4 * H + 4 * M + 8 * M, fsets,
+                      cpu=lambda ob: rms_cpu(ob, False)))
+    cases.append(Case("rmsnorm_bwd", "rmsnorm_bwd_kernel", "soupk_rmsnorm_bwd",
+                      20 * row_elems + 4 * H + 4 * M + 8 * M, bsets,
+                      cpu=lambda ob: rms_cpu(ob, True)))
+
+    # LoRA-add + RoPE + QKV pack forward / backward at M = 2048 (fp32 LoRA deltas)
+    fsets, bsets = [], []
+    cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
+    W = (NH + 2 * NKV) * D
+    for i in range(n_sets):
+        qkv, lq, lv, pos = workloads.rope_inputs((T,) * B, T, NH, NKV, D, torch.float32,
+                                                 seed=6 + 10 * i, device=dev)
+        q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
+        k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+        v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+        fsets.append(((qkv, lq, lv, pos, q, k, v),
+                      (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), None, p(q),
+                       p(k), p(v), M, B, T, NH, NKV, D)))
+        dq, dk, dv = workloads.rope_grads(B, T, NH, NKV, D, seed=7 + 10 * i, device=dev)
+        dqkv = torch.empty((M, W), dtype=torch.float16, device=dev)
+        bsets.append(((dq, dk, dv, pos, dqkv),
+                      (p(dq), p(dk), p(dv), p(cos), p(sin), p(pos), p(dqkv), M, B, T, NH, NKV,
+                       D)))
+    tab = 2 * T * D * 4
+
+    def rope_cpu(ob, backward):
+        qc, lqc, lvc, posc = workloads.rope_inputs((T,) * B, T, NH, NKV, D, torch.float32,
+                                                   seed=6)
+        cc, sc = workloads.rope_tables(T, D, workloads.ROPE_THETA)
+        if backward:
+            dqc, dkc, dvc = workloads.rope_grads(B, T, NH, NKV, D, seed=7)
+            return lambda: ob.rope_bwd(qc, cc, sc, posc, B, T, NH, NKV, D, dqc, dkc, dvc)
+        return lambda: ob.rope_fwd(qc, lqc, lvc, cc, sc, posc, B, T, NH, NKV, D)
+
+    cases.append(Case("rope_pack_fwd", "rope_pack_fwd_kernel", "soupk_rope_pack_fwd",
+                      M * W * 2 + M * NH * D * 4 + M * NKV * D * 4 + tab + 8 * M + M * W * 2,
+                      fsets, cpu=lambda ob: rope_cpu(ob, False)))
+    cases.append(Case("rope_pack_bwd", "rope_pack_bwd_kernel", "soupk_rope_pack_bwd",
+                      M * W * 2 + tab + 8 * M + M * W * 2, bsets,
+                      cpu=lambda ob: rope_cpu(ob, True)))
+
+    # SwiGLU forward and in-place backward at [2048, 2 x 8960]
+    fsets, bsets = [], []
+    for i in range(n_sets):
+        gu = workloads.swiglu_inputs(M, I, seed=4 + 10 * i, device=dev)
+        act = torch.empty((M, I), dtype=torch.float16, device=dev)
+        fsets.append(((gu, act), (p(gu), p(act), M, I)))
+        gu2 = workloads.swiglu_inputs(M, I, seed=5 + 10 * i, device=dev)
+        dact = workloads.swiglu_grad(M, I, seed=5 + 10 * i, device=dev)
+        bsets.append(((gu2, dact), (p(dact), p(gu2), M, I)))
+    def swi_cpu(ob, backward):
+        guc = workloads.swiglu_inputs(M, I, seed=4)
+        if backward:
+            dac = workloads.swiglu_grad(M, I, seed=5)
+            return lambda: ob.swiglu_bwd(dac, guc)
+        return lambda: ob.swiglu_fwd(guc)
+
+    cases.append(Case("swiglu_fwd", "swiglu_fwd_vec_kernel", "soupk_swiglu_fwd",
+                      M * 2 * I * 2 + M * I * 2, fsets, cpu=lambda ob: swi_cpu(ob, False)))
+    cases.append(Case("swiglu_bwd", "swiglu_bwd_vec_kernel", "soupk_swiglu_bwd_inplace",
+                      M * I * 2 + 2 * (M * 2 * I * 2), bsets, cpu=lambda ob: swi_cpu(ob, True)))
+
+    # vocab head: one 256-row chunk of logits [256, 151936]
+    sets = []
+    rows, V = 256, workloads.VOCAB
+    n_lab = 0
+    for i in range(n_sets):
+        z, tgt = workloads.head_logits(rows, V, seed=8 + 10 * i, device=dev)
+        ent = torch.empty(rows, dtype=torch.float32, device=dev)
+        loss = torch.empty(rows, dtype=torch.float32, device=dev)
+        cor = torch.empty(rows, dtype=torch.int32, device=dev)
+        sets.append(((z, tgt, ent, loss, cor),
+                     (p(z), p(tgt), p(ent), p(loss), p(cor), None, 64.0 / 1843.0, rows, V)))
+        if i == 0:
+            n_lab = int((tgt != -100).sum())
+    def head_cpu(ob):
+        zc, tc = workloads.head_logits(rows, V, seed=8)
+        return lambda: ob.head_stats_grad(zc, tc, 64.0 / 1843.0)
+
+    cases.append(Case("head_stats_grad", "head_stats_grad_kernel", "soupk_head_stats_grad",
+                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 12 * rows, sets, cpu=head_cpu))
+    return cases
+
+
+def prefill(buf, n):
+    """Queue n large fills so the host runs ahead of the GPU into the timed region."""
+    for _ in range(n):
+        buf.fill_(1.0)
+
+
+def time_gpu(cases, steps, warmup, dev):
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    busy = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)   # 1 GiB
+    for w in range(warmup):
+        for c in cases:
+            c.launch(w, sh)
+    torch.cuda.synchronize(dev)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in cases] for _ in range(steps)]
+    torch.cuda.synchronize(dev)
+    prefill(busy, 8)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        for j, c in enumerate(cases):
+            a, b = ev[s][j]
+            a.record(stream)
+            c.launch(s, sh)
+            b.record(stream)
+    host_enqueue = time.perf_counter() - t0
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    for j, c in enumerate(cases):
+        c.times = [ev[s][j][0].elapsed_time(ev[s][j][1]) * 1e3 for s in range(steps)]   # us
+    del busy
+    return host_enqueue, wall
+
+
+def cpu_baseline(cases, seconds):
+    from oracle import baseline as ob     # the CPU leg is the only user of oracle/ here
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    runs = [c.cpu(ob) for c in cases]
+    for run in runs:                      # warm-up pass (page faults, thread pool)
+        run()
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for run in runs:
+            run()
+        passes += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    elapsed = time.perf_counter() - t0
+    total = sum(c.nbytes for c in cases) * passes
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                         "")
+    except OSError:
+        pass
+    return {"value": round(total / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{passes} full pass(es) of the kernel set at the step shape (all 8 "
+                       f"kernels, BASELINE configs) through the reference's eager PyTorch path "
+                       f"on the CPU (oracle/baseline.py), {elapsed:.1f} s, {model}")}
+
+
+def median(xs):
+    s = sorted(xs)
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the kernel set has no cross-GPU exchange and this "
+              "build runs no multi-GPU configuration (see DESIGN.md, 'Sharding').",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _ext.lib()
+    log("building inputs")
+    cases = build_cases(dev)
+    torch.cuda.synchronize(dev)
+    log(f"timing {len(cases)} kernels: warmup {args.warmup}, steps {args.steps}")
+    host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
+    kernels = {}
+    total_us = 0.0
+    total_bytes = 0
+    for c in cases:
+        mean_us = sum(c.times) / len(c.times)
+        total_us += mean_us
+        total_bytes += c.nbytes
+        gbps = c.nbytes / (mean_us * 1e-6) / 1e9
+        kernels[c.name] = {"kernel": c.kernel, "us_mean": round(mean_us, 3),
+                           "us_median": round(median(c.times), 3),
+                           "us_min": round(min(c.times), 3), "bytes": c.nbytes,
+                           "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+        log(f"{c.name:16s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
+            f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s")
+    dom = max(cases, key=lambda c: sum(c.times))
+    dom_us = sum(dom.times) / len(dom.times)
+    dom_gbps = dom.nbytes / (dom_us * 1e-6) / 1e9
+    roofline = {"kernel": dom.kernel, "bound": "hbm", "achieved": round(dom_gbps, 1),
+                "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(dom_gbps / PEAK_HBM_GBPS, 4),
+                "traffic": None}
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(cases, args.cpu_seconds)
+    value = total_bytes / (total_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_us / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "solution/ kernel set fwd+bwd at the 2048-token step of "
+                               "Qwen2.5-1.5B (nf4 gate|up unpack, add+RMSNorm fwd/bwd, "
+                               "LoRA+RoPE+QKV pack fwd/bwd, SwiGLU fwd/in-place bwd, vocab-head "
+                               "stats+grad on one 256x151936 chunk)",
+                   "tokens": 2048, "hidden": workloads.HIDDEN, "intermediate": workloads.INTER,
+                   "vocab": workloads.VOCAB, "storage": "fp16/fp32, math fp32"},
+        "value_definition": "sum of compulsory HBM bytes of the 8 kernels / sum of their mean "
+                            "HIP-event durations",
+        "kernels": kernels,
+        "step_wall_ms": round(wall * 1e3 / args.steps, 4),
+        "host_enqueue_ms": round(host_enqueue * 1e3 / args.steps, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,155 @@
+/*
+ * soupk.h - C ABI of libsoupk.so, the gfx950 (MI355X / CDNA4) kernels behind the QLoRA
+ * fused-kernel set of SalReII/testt `solution/`.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element counts and a HIP stream (`void*`, a hipStream_t;
+ *     NULL is the legacy default stream), enqueues its kernels asynchronously and returns;
+ *   - never allocates, never synchronises, keeps no mutable global state (re-entrant: PyTorch
+ *     runs backward on its own worker thread);
+ *   - returns 0 on success, hipErrorInvalidValue (1) for arguments it rejects before
+ *     launching, or the hipError_t of the launch;
+ *   - bounds-checks every index it reads from device memory (positions, pad rows, labels):
+ *     an out-of-range index is skipped, never dereferenced.
+ * fp16 buffers are passed as uint16_t (IEEE binary16 bit patterns).
+ * Nullable pointers replace the reference's dummy-tensor + has_* flag convention
+ * (solution/rmsnorm.py:86-91,104-110, solution/rope.py:146-147,165-169).
+ */
+#ifndef SOUPK_H
+#define SOUPK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header; soupk_abi_version() returns the library's. */
+#define SOUPK_ABI_VERSION 1
+
+int soupk_abi_version(void);
+
+/* Human-readable text of a status code returned by any soupk_* call. */
+const char* soupk_status_string(int status);
+
+/*
+ * NF4 double-quant unpack (replaces the launch of nf4_unpack_kernel, solution/nf4.py:27-45,
+ * launched from unpack_into, solution/nf4.py:72-89).
+ *   absmax[b] = fp32(fp32(code2[absmax_u8[b]] * absmax2[b / qblock2]) + offset[0])
+ *   out[2i]   = fp16_rn(nf4[packed[i] >> 4] * absmax[i / (qblock/2)])
+ *   out[2i+1] = fp16_rn(nf4[packed[i] & 15] * absmax[i / (qblock/2)])
+ * Every product and sum is rounded separately (no fused multiply-add), as bitsandbytes does.
+ * packed: n_bytes; absmax_u8: ceil(n_bytes / (qblock/2)); absmax2: ceil(#absmax / qblock2);
+ * code2: 256; nf4: 16; offset: 1 fp32; out: 2*n_bytes fp16.  qblock even, qblock2 >= 1.
+ */
+int soupk_nf4_unpack(const uint8_t* packed, const uint8_t* absmax_u8, const float* code2,
+                     const float* absmax2, const float* offset, const float* nf4,
+                     uint16_t* out_f16, int64_t n_bytes, int32_t qblock, int32_t qblock2,
+                     void* stream);
+
+/*
+ * Inverse of a scatter index (no counterpart kernel in the reference: it lets the pad-layout
+ * writers of rmsnorm_fwd and rope_pack_fwd zero the unused rows in the same launch instead of
+ * a separate torch.zeros, solution/rmsnorm.py:82, solution/rope.py:141-143).
+ *   inv[p] = i if idx[i] == p, else -1, for p in [0, n_slots).  idx entries must be distinct;
+ *   entries outside [0, n_slots) are ignored.
+ */
+int soupk_index_inverse(const int64_t* idx, int64_t n, int32_t* inv, int64_t n_slots,
+                        void* stream);
+
+/*
+ * Residual add + Qwen2RMSNorm forward (replaces rmsnorm_fwd_kernel, solution/rmsnorm.py:24-43,
+ * launched from _launch_fwd, solution/rmsnorm.py:76-92).  Per row r of [rows, H]:
+ *   s = x + fp32(delta)            (stored to s_out when delta != NULL)
+ *   rstd = 1 / sqrt(sum(s*s) / H + eps)
+ *   y = fp16_rn((s * rstd) * w);   ypad[pad_idx[r]] = (s * rstd) * w  (fp32)
+ * delta, s_out: both NULL or both set.  ypad/pad_idx: both NULL or both set; ypad has
+ * pad_rows rows.  pad_inv (nullable, from soupk_index_inverse over pad_idx): rows p of ypad
+ * with pad_inv[p] < 0 are written with zeros in the same launch; with pad_inv NULL the caller
+ * owns the rows that no pad_idx entry names.
+ */
+int soupk_rmsnorm_fwd(const float* x, const uint16_t* delta, const float* w, float* s_out,
+                      uint16_t* y, float* ypad, const int64_t* pad_idx, const int32_t* pad_inv,
+                      float* rstd, int64_t rows, int64_t pad_rows, int32_t H, float eps,
+                      void* stream);
+
+/*
+ * Residual add + RMSNorm backward (replaces rmsnorm_bwd_kernel, solution/rmsnorm.py:46-69,
+ * launched from _launch_bwd, solution/rmsnorm.py:95-112).  Per row r:
+ *   g = (fp32(dy) + dypad[pad_idx[r]]) * w          (absent terms are 0)
+ *   n = s * rstd;  proj = sum(g * n) / H
+ *   dx = (g - n * proj) * rstd + ds;  ddelta = fp16_rn(dx)
+ * dy, dypad (with pad_idx, pad_rows rows), ds and ddelta are nullable.
+ */
+int soupk_rmsnorm_bwd(const float* s, const float* rstd, const float* w, const uint16_t* dy,
+                      const float* dypad, const int64_t* pad_idx, const float* ds, float* dx,
+                      uint16_t* ddelta, int64_t rows, int64_t pad_rows, int32_t H, void* stream);
+
+/* LoRA-delta element types for soupk_rope_pack_fwd. */
+#define SOUPK_DTYPE_F16 0
+#define SOUPK_DTYPE_F32 1
+
+/*
+ * LoRA add + RoPE + QKV pack forward (replaces rope_pack_fwd_kernel, solution/rope.py:24-75,
+ * launched from RopePack.forward, solution/rope.py:137-151).
+ * qkv: [rows, (NH + 2*NKV) * D] fp16 (q heads, then k heads, then v heads);
+ * lora_q: [rows, NH*D], lora_v: [rows, NKV*D] (nullable, element type lora_dtype);
+ * cos, sin: [T, D] fp32; pos: [rows] int64 padded positions b*T + t.
+ * Writes q [B, NH, T, D], k, v [B, NKV, T, D] fp16 at (b, h, t):
+ *   q = rot(qkv_q + lora_q), k = rot(qkv_k), v = qkv_v + lora_v, with
+ *   rot(x1, x2) = (x1*c1 - x2*s1, x2*c2 + x1*s2) in fp32 (x1, x2 the two halves of a head).
+ * pos_inv (nullable, soupk_index_inverse over pos with B*T slots): positions with
+ * pos_inv[p] < 0 are written with zeros in the same launch.  D even.
+ */
+int soupk_rope_pack_fwd(const uint16_t* qkv, const void* lora_q, const void* lora_v,
+                        int32_t lora_dtype, const float* cos, const float* sin,
+                        const int64_t* pos, const int32_t* pos_inv, uint16_t* q, uint16_t* k,
+                        uint16_t* v, int64_t rows, int32_t B, int32_t T, int32_t NH,
+                        int32_t NKV, int32_t D, void* stream);
+
+/*
+ * RoPE pack backward (replaces rope_pack_bwd_kernel, solution/rope.py:78-128, launched from
+ * RopePack.backward, solution/rope.py:153-176).  Gathers dq/dk/dv (each nullable = zero) at
+ * (b, h, t) of every token and writes dqkv [rows, (NH + 2*NKV) * D] fp16:
+ *   q, k: (g1*c1 + g2*s2, g2*c2 - g1*s1);  v: passthrough.
+ */
+int soupk_rope_pack_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv,
+                        const float* cos, const float* sin, const int64_t* pos, uint16_t* dqkv,
+                        int64_t rows, int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D,
+                        void* stream);
+
+/*
+ * Gated SiLU forward (replaces gated_silu_fwd_kernel, solution/mlp.py:31-40, launched from
+ * gated_silu, solution/mlp.py:61-68).  gu: [rows, 2I] fp16 = [gate | up];
+ *   act[r, c] = fp16_rn(gate / (1 + exp(-gate)) * up), in fp32.
+ */
+int soupk_swiglu_fwd(const uint16_t* gu, uint16_t* act, int64_t rows, int64_t I, void* stream);
+
+/*
+ * Gated SiLU backward, in place (replaces gated_silu_bwd_inplace_kernel, solution/mlp.py:43-58,
+ * launched from gated_silu_backward_, solution/mlp.py:71-77).  sig = 1/(1+exp(-gate)):
+ *   gu[:, :I] <- fp16_rn(dact * up * sig * (1 + gate * (1 - sig)))
+ *   gu[:, I:] <- fp16_rn(dact * (gate * sig))
+ */
+int soupk_swiglu_bwd_inplace(const uint16_t* dact, uint16_t* gu, int64_t rows, int64_t I,
+                             void* stream);
+
+/*
+ * Vocab-head statistics + in-place gradient (replaces head_stats_grad_kernel,
+ * solution/head.py:34-76, launched from FusedHeadLoss.forward, solution/head.py:108-110).
+ * logits: [rows, V] fp16, overwritten for labelled rows.  Per row, over z = fp32(logits):
+ *   lse = max + log(sum exp(z - max));  entropy = lse - sum(exp(z - max) * z) / sum(exp(z - max))
+ *   loss = lse - z[target] (0 when target == -100);  correct = argmax(z) == target (first max)
+ *   labelled rows: logits <- fp16_rn((exp(z - lse) - onehot(target)) * grad_scale)
+ * lse_out is nullable (an extra output the reference kernel does not store).  A target outside
+ * [0, V) other than -100 gives loss = NaN, correct = 0 and no onehot term.
+ */
+int soupk_head_stats_grad(uint16_t* logits, const int64_t* target, float* entropy, float* loss,
+                          int32_t* correct, float* lse_out, float grad_scale, int64_t rows,
+                          int64_t V, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOUPK_H */

@@ -1,0 +1,74 @@
+"""The C ABI (CPU only, no kernel launches): libsoupk.so loads, exports every entry point that
+include/soupk.h declares with the ctypes signature the Python layer binds, and rejects invalid
+arguments before touching the GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from testt_amd import _ext
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "soupk.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return dict(re.findall(r"\b(?:int|const char\*)\s+(soupk_\w+)\s*\(([^)]*)\)", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_ext.library_path()):
+        pytest.fail("libsoupk.so is not built: run `python -m testt_amd.build_ext`")
+    return _ext.lib()
+
+
+def test_header_and_binding_agree(lib):
+    decls = declared()
+    assert set(decls) == set(_ext.SIGNATURES) | {"soupk_abi_version", "soupk_status_string"}
+    for name, params in decls.items():
+        n = 0 if params.strip() in ("", "void") else params.count(",") + 1
+        if name in _ext.SIGNATURES:
+            assert len(_ext.SIGNATURES[name]) == n, name
+
+
+def test_every_declared_symbol_is_exported(lib):
+    handle = ctypes.CDLL(_ext.library_path())
+    for name in declared():
+        assert hasattr(handle, name), f"{name} missing from libsoupk.so"
+
+
+def test_version_and_status_strings(lib):
+    assert lib.soupk_abi_version() == _ext.ABI_VERSION
+    assert lib.soupk_status_string(0) == b"success"
+    assert b"invalid" in lib.soupk_status_string(1)
+
+
+@pytest.mark.parametrize("name,args", [
+    ("soupk_swiglu_fwd", (None, None, -1, 8, None)),
+    ("soupk_swiglu_bwd_inplace", (None, None, 4, 8, None)),
+    ("soupk_nf4_unpack", (None,) * 7 + (64, 63, 256, None)),
+    ("soupk_rmsnorm_fwd", (None,) * 9 + (4, 0, 0, 1e-6, None)),
+    ("soupk_rmsnorm_bwd", (None,) * 9 + (-1, 0, 16, None)),
+    ("soupk_rope_pack_fwd", (None,) * 3 + (7,) + (None,) * 7 + (1, 1, 1, 1, 1, 8, None)),
+    ("soupk_rope_pack_bwd", (None,) * 7 + (1, 1, 1, 1, 1, 7, None)),
+    ("soupk_head_stats_grad", (None,) * 6 + (1.0, 1, 0, None)),
+    ("soupk_index_inverse", (None, -1, None, 4, None)),
+])
+def test_invalid_arguments_rejected_before_launch(lib, name, args):
+    with pytest.raises(_ext.SoupkError, match="status 1"):
+        _ext.call(name, *args)
+
+
+@pytest.mark.parametrize("name,args", [
+    ("soupk_swiglu_fwd", (None, None, 0, 8960, None)),
+    ("soupk_nf4_unpack", (None,) * 7 + (0, 64, 256, None)),
+    ("soupk_head_stats_grad", (None,) * 6 + (1.0, 0, 151936, None)),
+    ("soupk_index_inverse", (None, 0, None, 0, None)),
+])
+def test_empty_work_is_a_no_op(lib, name, args):
+    _ext.call(name, *args)

@@ -1,0 +1,113 @@
+"""ctypes binding of libsoupk.so (C ABI: include/soupk.h).
+
+The library is loaded once, from this package's directory.  There is no fallback: if the
+library is missing or a call fails, the error is raised (the product path never routes through
+a CPU or PyTorch re-implementation).  Tensor checks (device, dtype, contiguity, shape) are done
+here, before any pointer crosses the boundary.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsoupk.so")
+_lock = threading.Lock()
+_lib = None
+
+ABI_VERSION = 1
+DTYPE_F16 = 0
+DTYPE_F32 = 1
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> argument types (every entry point returns int status)
+SIGNATURES = {
+    "soupk_nf4_unpack": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
+    "soupk_index_inverse": [_p, _i64, _p, _i64, _p],
+    "soupk_rmsnorm_fwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _f32, _p],
+    "soupk_rmsnorm_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
+    "soupk_rope_pack_fwd": [_p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32,
+                            _i32, _i32, _i32, _p],
+    "soupk_rope_pack_bwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p],
+    "soupk_swiglu_fwd": [_p, _p, _i64, _i64, _p],
+    "soupk_swiglu_bwd_inplace": [_p, _p, _i64, _i64, _p],
+    "soupk_head_stats_grad": [_p, _p, _p, _p, _p, _p, _f32, _i64, _i64, _p],
+}
+
+
+class SoupkError(RuntimeError):
+    """A soupk entry point rejected its arguments or its launch failed."""
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def lib():
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise SoupkError(
+                    f"{_LIB_PATH} is missing: build it with `python -m testt_amd.build_ext` "
+                    "(or __graft_entry__.build()) before using the kernels")
+            handle = ctypes.CDLL(_LIB_PATH)
+            handle.soupk_abi_version.restype = ctypes.c_int
+            handle.soupk_abi_version.argtypes = []
+            version = handle.soupk_abi_version()
+            if version != ABI_VERSION:
+                raise SoupkError(f"libsoupk ABI {version} != expected {ABI_VERSION}: rebuild")
+            handle.soupk_status_string.restype = ctypes.c_char_p
+            handle.soupk_status_string.argtypes = [ctypes.c_int]
+            for name, args in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = ctypes.c_int
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Invoke entry point `name`; raise SoupkError on a non-zero status."""
+    handle = lib()
+    status = getattr(handle, name)(*args)
+    if status != 0:
+        text = handle.soupk_status_string(status)
+        text = text.decode() if text else "?"
+        raise SoupkError(f"{name} failed with status {status}: {text}")
+
+
+def ptr(tensor):
+    """Device address of a tensor (None for None)."""
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_of(tensor):
+    """The current HIP stream of the tensor's device, as a raw handle."""
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def require(tensor, name, dtype=None, ndim=None, device=None):
+    """Kernel inputs must be contiguous HIP device tensors of the stated dtype."""
+    if not torch.is_tensor(tensor):
+        raise TypeError(f"{name} must be a tensor, got {type(tensor).__name__}")
+    if not tensor.is_cuda:
+        raise ValueError(f"{name} must be a HIP device tensor (got device {tensor.device}); "
+                         "the soupk kernels have no CPU path")
+    if device is not None and tensor.device != device:
+        raise ValueError(f"{name} is on {tensor.device}, expected {device}")
+    if dtype is not None and tensor.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {tensor.dtype}")
+    if ndim is not None and tensor.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(tensor.shape)}")
+    if not tensor.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return tensor

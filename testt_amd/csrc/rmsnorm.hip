@@ -1,0 +1,371 @@
+// Residual add + Qwen2RMSNorm, forward and backward, one wavefront per token row.
+//
+// Reference: solution/rmsnorm.py:24-43 (rmsnorm_fwd_kernel) and solution/rmsnorm.py:46-69
+// (rmsnorm_bwd_kernel), launched from _launch_fwd / _launch_bwd, solution/rmsnorm.py:76-112.
+// The normalisation is transformers' Qwen2RMSNorm (modeling_qwen2.py:247-252):
+// w * (s * rsqrt(mean(s^2) + eps)), with the product (s * rstd) rounded before the weight.
+//
+// Mapping (gfx950): a row of H fp32 is H/4 float4 chunks; lane l of the row's wavefront owns
+// chunks l, l+64, l+128, ... so every load or store instruction of the wave touches 1 KiB
+// (fp32) or 512 B (fp16) of contiguous memory.  The row's values stay in registers between the
+// load, the wave64 butterfly reduction and the stores (H <= 64 * 4 * kMaxCpl).  A workgroup is
+// four wavefronts = four rows.  In the forward pass extra workgroups after the row workgroups
+// zero the rows of the padded fp32 output that no token maps to (the pad rows), so the padded
+// tensor needs no separate memset.
+
+#include "soupk_common.hpp"
+
+namespace soupk {
+namespace {
+
+constexpr int kRowsPerBlock = 4;
+constexpr int kNormThreads = kWave * kRowsPerBlock;
+
+__device__ __forceinline__ f32x4 load_h4(const uint16_t* p) {
+  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+  return f32x4{lo_h(w.x), hi_h(w.x), lo_h(w.y), hi_h(w.y)};
+}
+__device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
+  *reinterpret_cast<u32x2*>(p) = u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
+}
+
+template <int CPL>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
+    const float* __restrict__ x, const uint16_t* __restrict__ delta, const float* __restrict__ w,
+    float* __restrict__ s_out, uint16_t* __restrict__ y, float* __restrict__ ypad,
+    const int64_t* __restrict__ pad_idx, const int32_t* __restrict__ pad_inv,
+    float* __restrict__ rstd_out, int64_t rows, int64_t pad_rows, int H, float eps,
+    int64_t row_blocks) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int nch = H / 4;
+  if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
+    // Zero the padded rows that no token row is scattered to.
+    const int64_t p = (static_cast<int64_t>(blockIdx.x) - row_blocks) * kRowsPerBlock + wave;
+    if (p >= pad_rows || pad_inv[p] >= 0) return;
+    f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
+    for (int c = lane; c < nch; c += kWave) dst[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave;
+  if (row >= rows) return;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * H);
+  f32x4 v[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = j * kWave + lane;
+    v[j] = c < nch ? xr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (delta != nullptr) {
+    const uint16_t* dr = delta + row * H;
+    f32x4 d[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = j * kWave + lane;
+      d[j] = c < nch ? load_h4(dr + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    f32x4* sr = reinterpret_cast<f32x4*>(s_out + row * H);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = j * kWave + lane;
+      v[j] = v[j] + d[j];
+      if (c < nch) sr[c] = v[j];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+    ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
+  uint16_t* yr = y + row * H;
+  const bool pad = ypad != nullptr;
+  int64_t dest = -1;
+  if (pad) {
+    dest = pad_idx[row];
+    if (dest < 0 || dest >= pad_rows) dest = -1;
+  }
+  f32x4* pr = dest >= 0 ? reinterpret_cast<f32x4*>(ypad + dest * H) : nullptr;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = j * kWave + lane;
+    if (c < nch) {
+      const f32x4 o = (v[j] * rstd) * wr[c];
+      store_h4(yr + 4 * c, o);
+      if (pr != nullptr) pr[c] = o;
+    }
+  }
+  if (lane == 0) rstd_out[row] = rstd;
+}
+
+template <int CPL>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
+    const float* __restrict__ s, const float* __restrict__ rstd_in, const float* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ dypad,
+    const int64_t* __restrict__ pad_idx, const float* __restrict__ ds, float* __restrict__ dx,
+    uint16_t* __restrict__ ddelta, int64_t rows, int64_t pad_rows, int H) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int nch = H / 4;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave;
+  if (row >= rows) return;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 g[CPL], n[CPL];
+  const f32x4* sr = reinterpret_cast<const f32x4*>(s + row * H);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = j * kWave + lane;
+    n[j] = c < nch ? sr[c] : zero;
+    g[j] = zero;
+  }
+  if (dy != nullptr) {
+    const uint16_t* dr = dy + row * H;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = j * kWave + lane;
+      if (c < nch) g[j] = g[j] + load_h4(dr + 4 * c);
+    }
+  }
+  if (dypad != nullptr) {
+    const int64_t src = pad_idx[row];
+    if (src >= 0 && src < pad_rows) {
+      const f32x4* pr = reinterpret_cast<const f32x4*>(dypad + src * H);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = j * kWave + lane;
+        if (c < nch) g[j] = g[j] + pr[c];
+      }
+    }
+  }
+  const float rstd = rstd_in[row];
+  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = j * kWave + lane;
+    if (c < nch) {
+      g[j] = g[j] * wr[c];
+      n[j] = n[j] * rstd;
+      const f32x4 p = g[j] * n[j];
+      dot += (p.x + p.y) + (p.z + p.w);
+    }
+  }
+  const float proj = wave_sum(dot) / static_cast<float>(H);
+  f32x4 d[CPL];
+  if (ds != nullptr) {
+    const f32x4* dsr = reinterpret_cast<const f32x4*>(ds + row * H);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = j * kWave + lane;
+      d[j] = c < nch ? dsr[c] : zero;
+    }
+  }
+  f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * H);
+  uint16_t* ddr = ddelta != nullptr ? ddelta + row * H : nullptr;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = j * kWave + lane;
+    if (c < nch) {
+      f32x4 o = (g[j] - n[j] * proj) * rstd;
+      if (ds != nullptr) o = o + d[j];
+      dxr[c] = o;
+      if (ddr != nullptr) store_h4(ddr + 4 * c, o);
+    }
+  }
+}
+
+// ---- generic forms: any H (one workgroup of 256 threads per row, two passes) -------------
+constexpr int kGenThreads = 256;
+
+__device__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < kGenThreads / kWave; ++i) t += red[i];
+  return t;
+}
+
+__global__ __launch_bounds__(kGenThreads) void rmsnorm_fwd_generic_kernel(
+    const float* __restrict__ x, const uint16_t* __restrict__ delta, const float* __restrict__ w,
+    float* __restrict__ s_out, uint16_t* __restrict__ y, float* __restrict__ ypad,
+    const int64_t* __restrict__ pad_idx, const int32_t* __restrict__ pad_inv,
+    float* __restrict__ rstd_out, int64_t rows, int64_t pad_rows, int H, float eps) {
+  __shared__ float red[kGenThreads / kWave];
+  const int64_t b = blockIdx.x;
+  if (b >= rows) {
+    const int64_t p = b - rows;
+    if (p >= pad_rows || pad_inv[p] >= 0) return;
+    for (int c = threadIdx.x; c < H; c += kGenThreads) ypad[p * H + c] = 0.f;
+    return;
+  }
+  const int64_t row = b;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < H; c += kGenThreads) {
+    float v = x[row * H + c];
+    if (delta != nullptr) {
+      v = v + h2f(delta[row * H + c]);
+      s_out[row * H + c] = v;
+    }
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  int64_t dest = -1;
+  if (ypad != nullptr) {
+    dest = pad_idx[row];
+    if (dest < 0 || dest >= pad_rows) dest = -1;
+  }
+  for (int c = threadIdx.x; c < H; c += kGenThreads) {
+    const float v = delta != nullptr ? s_out[row * H + c] : x[row * H + c];
+    const float o = (v * rstd) * w[c];
+    y[row * H + c] = static_cast<uint16_t>(pack_h2(o, 0.f) & 0xffffu);
+    if (dest >= 0) ypad[dest * H + c] = o;
+  }
+  if (threadIdx.x == 0) rstd_out[row] = rstd;
+}
+
+__global__ __launch_bounds__(kGenThreads) void rmsnorm_bwd_generic_kernel(
+    const float* __restrict__ s, const float* __restrict__ rstd_in, const float* __restrict__ w,
+    const uint16_t* __restrict__ dy, const float* __restrict__ dypad,
+    const int64_t* __restrict__ pad_idx, const float* __restrict__ ds, float* __restrict__ dx,
+    uint16_t* __restrict__ ddelta, int64_t rows, int64_t pad_rows, int H) {
+  __shared__ float red[kGenThreads / kWave];
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  int64_t src = -1;
+  if (dypad != nullptr) {
+    src = pad_idx[row];
+    if (src < 0 || src >= pad_rows) src = -1;
+  }
+  const float rstd = rstd_in[row];
+  float dot = 0.f;
+  for (int c = threadIdx.x; c < H; c += kGenThreads) {
+    float g = 0.f;
+    if (dy != nullptr) g = g + h2f(dy[row * H + c]);
+    if (src >= 0) g = g + dypad[src * H + c];
+    g = g * w[c];
+    dot += g * (s[row * H + c] * rstd);
+  }
+  const float proj = block_sum(dot, red) / static_cast<float>(H);
+  for (int c = threadIdx.x; c < H; c += kGenThreads) {
+    float g = 0.f;
+    if (dy != nullptr) g = g + h2f(dy[row * H + c]);
+    if (src >= 0) g = g + dypad[src * H + c];
+    g = g * w[c];
+    const float n = s[row * H + c] * rstd;
+    float o = (g - n * proj) * rstd;
+    if (ds != nullptr) o = o + ds[row * H + c];
+    dx[row * H + c] = o;
+    if (ddelta != nullptr) ddelta[row * H + c] = static_cast<uint16_t>(pack_h2(o, 0.f) & 0xffffu);
+  }
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Dispatch on the number of float4 chunks per lane.
+template <template <int> class Launch, typename... Args>
+int with_cpl(int cpl, Args... args) {
+  switch (cpl) {
+    case 1: return Launch<1>::run(args...);
+    case 2: return Launch<2>::run(args...);
+    case 3: return Launch<3>::run(args...);
+    case 4: return Launch<4>::run(args...);
+    case 5: case 6: return Launch<6>::run(args...);
+    case 7: case 8: return Launch<8>::run(args...);
+    case 9: case 10: case 11: case 12: return Launch<12>::run(args...);
+    case 13: case 14: case 15: case 16: return Launch<16>::run(args...);
+    default: return -1;
+  }
+}
+constexpr int kMaxCpl = 16;  // H <= 4096 on the register-resident path
+
+template <int CPL>
+struct FwdLaunch {
+  static int run(dim3 grid, hipStream_t st, const float* x, const uint16_t* delta, const float* w,
+                 float* s_out, uint16_t* y, float* ypad, const int64_t* pad_idx,
+                 const int32_t* pad_inv, float* rstd, int64_t rows, int64_t pad_rows, int H,
+                 float eps, int64_t row_blocks) {
+    rmsnorm_fwd_kernel<CPL><<<grid, kNormThreads, 0, st>>>(x, delta, w, s_out, y, ypad, pad_idx,
+                                                           pad_inv, rstd, rows, pad_rows, H, eps,
+                                                           row_blocks);
+    return launch_status();
+  }
+};
+
+template <int CPL>
+struct BwdLaunch {
+  static int run(dim3 grid, hipStream_t st, const float* s, const float* rstd, const float* w,
+                 const uint16_t* dy, const float* dypad, const int64_t* pad_idx, const float* ds,
+                 float* dx, uint16_t* ddelta, int64_t rows, int64_t pad_rows, int H) {
+    rmsnorm_bwd_kernel<CPL><<<grid, kNormThreads, 0, st>>>(s, rstd, w, dy, dypad, pad_idx, ds,
+                                                           dx, ddelta, rows, pad_rows, H);
+    return launch_status();
+  }
+};
+
+}  // namespace
+}  // namespace soupk
+
+using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_fwd(
+    const float* x, const uint16_t* delta, const float* w, float* s_out, uint16_t* y,
+    float* ypad, const int64_t* pad_idx, const int32_t* pad_inv, float* rstd, int64_t rows,
+    int64_t pad_rows, int32_t H, float eps, void* stream) {
+  if (rows < 0 || H <= 0 || pad_rows < 0) return kInvalid;
+  if ((delta == nullptr) != (s_out == nullptr)) return kInvalid;
+  if ((ypad == nullptr) != (pad_idx == nullptr)) return kInvalid;
+  if (pad_inv != nullptr && ypad == nullptr) return kInvalid;
+  const int64_t zero_rows = pad_inv != nullptr ? pad_rows : 0;
+  if (rows == 0 && zero_rows == 0) return kOk;
+  if (!x || !w || !y || !rstd) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int cpl = (H / 4 + kWave - 1) / kWave;
+  const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(x, 16) && aligned(w, 16) &&
+                   aligned(s_out, 16) && aligned(ypad, 16) && aligned(delta, 8) && aligned(y, 8);
+  if (vec) {
+    const int64_t row_blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int64_t blocks = row_blocks + (zero_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (blocks > 0x7fffffff) return kInvalid;
+    return with_cpl<FwdLaunch>(cpl, dim3(static_cast<unsigned>(blocks)), st, x, delta, w, s_out,
+                               y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows,
+                               static_cast<int>(H), eps, row_blocks);
+  }
+  const int64_t blocks = rows + zero_rows;
+  if (blocks > 0x7fffffff) return kInvalid;
+  rmsnorm_fwd_generic_kernel<<<static_cast<unsigned>(blocks), kGenThreads, 0, st>>>(
+      x, delta, w, s_out, y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows, H, eps);
+  return launch_status();
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_bwd(
+    const float* s, const float* rstd, const float* w, const uint16_t* dy, const float* dypad,
+    const int64_t* pad_idx, const float* ds, float* dx, uint16_t* ddelta, int64_t rows,
+    int64_t pad_rows, int32_t H, void* stream) {
+  if (rows < 0 || H <= 0 || pad_rows < 0) return kInvalid;
+  if (dypad != nullptr && pad_idx == nullptr) return kInvalid;
+  if (rows == 0) return kOk;
+  if (!s || !rstd || !w || !dx) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int cpl = (H / 4 + kWave - 1) / kWave;
+  const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(s, 16) && aligned(w, 16) &&
+                   aligned(dypad, 16) && aligned(ds, 16) && aligned(dx, 16) && aligned(dy, 8) &&
+                   aligned(ddelta, 8);
+  if (vec) {
+    const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (blocks > 0x7fffffff) return kInvalid;
+    return with_cpl<BwdLaunch>(cpl, dim3(static_cast<unsigned>(blocks)), st, s, rstd, w, dy,
+                               dypad, pad_idx, ds, dx, ddelta, rows, pad_rows,
+                               static_cast<int>(H));
+  }
+  if (rows > 0x7fffffff) return kInvalid;
+  rmsnorm_bwd_generic_kernel<<<static_cast<unsigned>(rows), kGenThreads, 0, st>>>(
+      s, rstd, w, dy, dypad, pad_idx, ds, dx, ddelta, rows, pad_rows, H);
+  return launch_status();
+}

@@ -1,0 +1,394 @@
+// LoRA add + rotary embedding + scatter of q/k/v into the padded [B, heads, T, D] layout, and
+// its backward (gather + transposed rotation).
+//
+// Reference: solution/rope.py:24-75 (rope_pack_fwd_kernel), solution/rope.py:78-128
+// (rope_pack_bwd_kernel), launched from RopePack, solution/rope.py:136-176.  The rotation is
+// transformers' apply_rotary_pos_emb / rotate_half (modeling_qwen2.py:105-135):
+// q*cos + rotate_half(q)*sin, i.e. (x1*c1 - x2*s1, x2*c2 + x1*s2) with each product rounded.
+//
+// Mapping (gfx950): a work item is one 8-dim slice of one head of one token, together with the
+// matching 8 dims of the head's other half (the rotation partner), so a thread does two 16-byte
+// fp16 loads of qkv, up to four 16-byte loads of fp32 LoRA delta, the cos/sin slices (a
+// [T, D] fp32 table that stays in L2), and two 16-byte stores.  Items are numbered token-major,
+// so a wavefront reads a token's 4 KiB qkv row in full.  In the forward pass the workgroups
+// after the token workgroups write zeros at the padded positions that no token maps to
+// (pos_inv[p] < 0), replacing the three torch.zeros memsets of the reference.
+
+#include "soupk_common.hpp"
+#include "fastdiv.hpp"
+
+namespace soupk {
+namespace {
+
+constexpr int kRopeThreads = 256;
+
+struct RopeDims {
+  int B, T, NH, NKV;
+  uint32_t items;   // (NH + 2*NKV) * HALF/8 items per token or position
+  FastDiv per_tok;  // divides by items
+};
+
+__device__ __forceinline__ void load8_f32(const float* p, float* v) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void load8_h(const uint16_t* p, float* v) {
+  const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+  v[0] = lo_h(w.x); v[1] = hi_h(w.x); v[2] = lo_h(w.y); v[3] = hi_h(w.y);
+  v[4] = lo_h(w.z); v[5] = hi_h(w.z); v[6] = lo_h(w.w); v[7] = hi_h(w.w);
+}
+__device__ __forceinline__ void store8_h(uint16_t* p, const float* v) {
+  *reinterpret_cast<u32x4*>(p) =
+      u32x4{pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7])};
+}
+__device__ __forceinline__ void add8_lora(float* x, const void* lora, int64_t off, bool f32) {
+  float l[8];
+  if (f32)
+    load8_f32(static_cast<const float*>(lora) + off, l);
+  else
+    load8_h(static_cast<const uint16_t*>(lora) + off, l);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = x[i] + l[i];
+}
+
+template <int HALF>
+__global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
+    const uint16_t* __restrict__ qkv, const void* __restrict__ lora_q,
+    const void* __restrict__ lora_v, int lora_f32, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
+    const int32_t* __restrict__ pos_inv, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    uint16_t* __restrict__ v, int64_t rows, RopeDims dm, int64_t tok_blocks) {
+  constexpr int D = 2 * HALF;
+  constexpr int CPH = HALF / 8;  // items per head
+  const int heads = dm.NH + 2 * dm.NKV;
+  const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
+  if (static_cast<int64_t>(blockIdx.x) >= tok_blocks) {
+    // Zero the padded positions with no token.
+    const uint32_t g = (blockIdx.x - static_cast<uint32_t>(tok_blocks)) * kRopeThreads +
+                       threadIdx.x;
+    const uint32_t p = dm.per_tok.div(g);
+    if (p >= slots || pos_inv[p] >= 0) return;
+    const int it = static_cast<int>(g - p * dm.items);
+    const int h = it / CPH, c = it % CPH;
+    const int b = static_cast<int>(p / dm.T), t = static_cast<int>(p % dm.T);
+    uint16_t* base;
+    if (h < dm.NH)
+      base = q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D;
+    else if (h < dm.NH + dm.NKV)
+      base = k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
+    else
+      base = v + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH - dm.NKV)) * dm.T + t) * D;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(base + 8 * c) = z;
+    *reinterpret_cast<u32x4*>(base + HALF + 8 * c) = z;
+    return;
+  }
+  const uint32_t g = blockIdx.x * kRopeThreads + threadIdx.x;
+  const uint32_t tok = dm.per_tok.div(g);
+  if (tok >= rows) return;
+  const int it = static_cast<int>(g - tok * dm.items);
+  const int h = it / CPH, c = it % CPH;
+  const int64_t p = pos[tok];
+  if (p < 0 || p >= slots) return;
+  const int b = static_cast<int>(p / dm.T), t = static_cast<int>(p % dm.T);
+
+  const uint16_t* row = qkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  float x1[8], x2[8];
+  load8_h(row, x1);
+  load8_h(row + HALF, x2);
+  uint16_t* dst;
+  if (h < dm.NH + dm.NKV) {
+    const bool is_q = h < dm.NH;
+    if (is_q && lora_q != nullptr) {
+      const int64_t off = static_cast<int64_t>(tok) * dm.NH * D + h * D + 8 * c;
+      add8_lora(x1, lora_q, off, lora_f32);
+      add8_lora(x2, lora_q, off + HALF, lora_f32);
+    }
+    float c1[8], c2[8], s1[8], s2[8];
+    const float* cr = cos_t + static_cast<int64_t>(t) * D + 8 * c;
+    const float* sr = sin_t + static_cast<int64_t>(t) * D + 8 * c;
+    load8_f32(cr, c1);
+    load8_f32(cr + HALF, c2);
+    load8_f32(sr, s1);
+    load8_f32(sr + HALF, s2);
+    float o1[8], o2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o1[i] = x1[i] * c1[i] - x2[i] * s1[i];
+      o2[i] = x2[i] * c2[i] + x1[i] * s2[i];
+    }
+    dst = is_q ? q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
+               : k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
+    store8_h(dst + 8 * c, o1);
+    store8_h(dst + HALF + 8 * c, o2);
+  } else {
+    const int hv = h - dm.NH - dm.NKV;
+    if (lora_v != nullptr) {
+      const int64_t off = static_cast<int64_t>(tok) * dm.NKV * D + hv * D + 8 * c;
+      add8_lora(x1, lora_v, off, lora_f32);
+      add8_lora(x2, lora_v, off + HALF, lora_f32);
+    }
+    dst = v + ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
+    store8_h(dst + 8 * c, x1);
+    store8_h(dst + HALF + 8 * c, x2);
+  }
+}
+
+template <int HALF>
+__global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
+    const uint16_t* __restrict__ dq, const uint16_t* __restrict__ dk,
+    const uint16_t* __restrict__ dv, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
+    uint16_t* __restrict__ dqkv, int64_t rows, RopeDims dm) {
+  constexpr int D = 2 * HALF;
+  constexpr int CPH = HALF / 8;
+  const int heads = dm.NH + 2 * dm.NKV;
+  const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
+  const uint32_t g = blockIdx.x * kRopeThreads + threadIdx.x;
+  const uint32_t tok = dm.per_tok.div(g);
+  if (tok >= rows) return;
+  const int it = static_cast<int>(g - tok * dm.items);
+  const int h = it / CPH, c = it % CPH;
+  uint16_t* out = dqkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  const int64_t p = pos[tok];
+  float g1[8], g2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) g1[i] = g2[i] = 0.f;
+  const bool valid = p >= 0 && p < slots;
+  const int b = valid ? static_cast<int>(p / dm.T) : 0;
+  const int t = valid ? static_cast<int>(p % dm.T) : 0;
+  if (h < dm.NH + dm.NKV) {
+    const bool is_q = h < dm.NH;
+    const uint16_t* src = is_q ? dq : dk;
+    if (valid && src != nullptr) {
+      const int64_t base =
+          is_q ? ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
+               : ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
+      load8_h(src + base + 8 * c, g1);
+      load8_h(src + base + HALF + 8 * c, g2);
+    }
+    float c1[8], c2[8], s1[8], s2[8];
+    const float* cr = cos_t + static_cast<int64_t>(t) * D + 8 * c;
+    const float* sr = sin_t + static_cast<int64_t>(t) * D + 8 * c;
+    load8_f32(cr, c1);
+    load8_f32(cr + HALF, c2);
+    load8_f32(sr, s1);
+    load8_f32(sr + HALF, s2);
+    float o1[8], o2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o1[i] = g1[i] * c1[i] + g2[i] * s2[i];
+      o2[i] = g2[i] * c2[i] - g1[i] * s1[i];
+    }
+    store8_h(out, o1);
+    store8_h(out + HALF, o2);
+  } else {
+    const int hv = h - dm.NH - dm.NKV;
+    if (valid && dv != nullptr) {
+      const int64_t base = ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
+      load8_h(dv + base + 8 * c, g1);
+      load8_h(dv + base + HALF + 8 * c, g2);
+    }
+    store8_h(out, g1);
+    store8_h(out + HALF, g2);
+  }
+}
+
+// ---- generic forms: any even D, one thread per (token or position, head, dim of first half)
+__global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_generic_kernel(
+    const uint16_t* __restrict__ qkv, const void* __restrict__ lora_q,
+    const void* __restrict__ lora_v, int lora_f32, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
+    const int32_t* __restrict__ pos_inv, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    uint16_t* __restrict__ v, int64_t rows, int B, int T, int NH, int NKV, int D,
+    int64_t tok_items) {
+  const int half = D / 2;
+  const int heads = NH + 2 * NKV;
+  const int64_t per = static_cast<int64_t>(heads) * half;
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kRopeThreads + threadIdx.x;
+  auto lora = [&](const void* l, int64_t off) -> float {
+    return lora_f32 ? static_cast<const float*>(l)[off] : h2f(static_cast<const uint16_t*>(l)[off]);
+  };
+  auto put = [&](uint16_t* base, int i, float a, float bv) {
+    base[i] = static_cast<uint16_t>(pack_h2(a, 0.f) & 0xffffu);
+    base[i + half] = static_cast<uint16_t>(pack_h2(bv, 0.f) & 0xffffu);
+  };
+  int64_t p, tok = -1;
+  int64_t it;
+  if (g < tok_items) {
+    tok = g / per;
+    it = g % per;
+    p = pos[tok];
+    if (p < 0 || p >= slots) return;
+  } else {
+    const int64_t z = g - tok_items;
+    p = z / per;
+    it = z % per;
+    if (p >= slots || pos_inv == nullptr || pos_inv[p] >= 0) return;
+  }
+  const int h = static_cast<int>(it / half), i = static_cast<int>(it % half);
+  const int b = static_cast<int>(p / T), t = static_cast<int>(p % T);
+  uint16_t* base;
+  if (h < NH)
+    base = q + ((static_cast<int64_t>(b) * NH + h) * T + t) * D;
+  else if (h < NH + NKV)
+    base = k + ((static_cast<int64_t>(b) * NKV + (h - NH)) * T + t) * D;
+  else
+    base = v + ((static_cast<int64_t>(b) * NKV + (h - NH - NKV)) * T + t) * D;
+  if (tok < 0) {
+    put(base, i, 0.f, 0.f);
+    return;
+  }
+  const uint16_t* row = qkv + tok * heads * D + h * D;
+  float x1 = h2f(row[i]), x2 = h2f(row[i + half]);
+  if (h < NH && lora_q != nullptr) {
+    const int64_t off = tok * NH * D + h * D + i;
+    x1 = x1 + lora(lora_q, off);
+    x2 = x2 + lora(lora_q, off + half);
+  }
+  if (h >= NH + NKV) {
+    if (lora_v != nullptr) {
+      const int64_t off = tok * NKV * D + (h - NH - NKV) * D + i;
+      x1 = x1 + lora(lora_v, off);
+      x2 = x2 + lora(lora_v, off + half);
+    }
+    put(base, i, x1, x2);
+    return;
+  }
+  const float* cr = cos_t + static_cast<int64_t>(t) * D;
+  const float* sr = sin_t + static_cast<int64_t>(t) * D;
+  put(base, i, x1 * cr[i] - x2 * sr[i], x2 * cr[i + half] + x1 * sr[i + half]);
+}
+
+__global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_generic_kernel(
+    const uint16_t* __restrict__ dq, const uint16_t* __restrict__ dk,
+    const uint16_t* __restrict__ dv, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
+    uint16_t* __restrict__ dqkv, int64_t rows, int B, int T, int NH, int NKV, int D) {
+  const int half = D / 2;
+  const int heads = NH + 2 * NKV;
+  const int64_t per = static_cast<int64_t>(heads) * half;
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kRopeThreads + threadIdx.x;
+  if (g >= rows * per) return;
+  const int64_t tok = g / per;
+  const int h = static_cast<int>((g % per) / half), i = static_cast<int>(g % half);
+  const int64_t p = pos[tok];
+  const bool valid = p >= 0 && p < slots;
+  const int b = valid ? static_cast<int>(p / T) : 0, t = valid ? static_cast<int>(p % T) : 0;
+  float g1 = 0.f, g2 = 0.f;
+  const uint16_t* src;
+  int64_t base;
+  if (h < NH) {
+    src = dq;
+    base = ((static_cast<int64_t>(b) * NH + h) * T + t) * D;
+  } else if (h < NH + NKV) {
+    src = dk;
+    base = ((static_cast<int64_t>(b) * NKV + (h - NH)) * T + t) * D;
+  } else {
+    src = dv;
+    base = ((static_cast<int64_t>(b) * NKV + (h - NH - NKV)) * T + t) * D;
+  }
+  if (valid && src != nullptr) {
+    g1 = h2f(src[base + i]);
+    g2 = h2f(src[base + i + half]);
+  }
+  float o1 = g1, o2 = g2;
+  if (h < NH + NKV) {
+    const float* cr = cos_t + static_cast<int64_t>(t) * D;
+    const float* sr = sin_t + static_cast<int64_t>(t) * D;
+    o1 = g1 * cr[i] + g2 * sr[i + half];
+    o2 = g2 * cr[i + half] - g1 * sr[i];
+  }
+  uint16_t* out = dqkv + tok * heads * D + h * D;
+  out[i] = static_cast<uint16_t>(pack_h2(o1, 0.f) & 0xffffu);
+  out[i + half] = static_cast<uint16_t>(pack_h2(o2, 0.f) & 0xffffu);
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+}  // namespace
+}  // namespace soupk
+
+using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
+    const uint16_t* qkv, const void* lora_q, const void* lora_v, int32_t lora_dtype,
+    const float* cos, const float* sin, const int64_t* pos, const int32_t* pos_inv, uint16_t* q,
+    uint16_t* k, uint16_t* v, int64_t rows, int32_t B, int32_t T, int32_t NH, int32_t NKV,
+    int32_t D, void* stream) {
+  if (rows < 0 || B < 0 || T < 0 || NH < 0 || NKV < 0 || D <= 0 || (D & 1)) return kInvalid;
+  if (lora_dtype != SOUPK_DTYPE_F16 && lora_dtype != SOUPK_DTYPE_F32) return kInvalid;
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  const int64_t zero_slots = pos_inv != nullptr ? slots : 0;
+  if ((rows == 0 && zero_slots == 0) || NH + 2 * NKV == 0) return kOk;
+  if (!q || !k || !v || !cos || !sin || (rows > 0 && (!qkv || !pos))) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int half = D / 2;
+  const int heads = NH + 2 * NKV;
+  const int lora_align = 16;
+  const bool vec = half == 64 && aligned(qkv, 16) && aligned(cos, 16) && aligned(sin, 16) &&
+                   aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                   aligned(lora_q, lora_align) && aligned(lora_v, lora_align);
+  if (vec) {
+    RopeDims dm;
+    dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
+    dm.items = static_cast<uint32_t>(heads * (half / 8));
+    dm.per_tok = FastDiv(dm.items);
+    const int64_t tok_items = rows * dm.items;
+    const int64_t zero_items = zero_slots * dm.items;
+    if (tok_items + zero_items >= (int64_t{1} << 31)) return kInvalid;
+    const int64_t tok_blocks = (tok_items + kRopeThreads - 1) / kRopeThreads;
+    const int64_t blocks = tok_blocks + (zero_items + kRopeThreads - 1) / kRopeThreads;
+    rope_pack_fwd_kernel<64><<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
+        qkv, lora_q, lora_v, lora_dtype == SOUPK_DTYPE_F32, cos, sin, pos, pos_inv, q, k, v, rows,
+        dm, tok_blocks);
+    return launch_status();
+  }
+  const int64_t per = static_cast<int64_t>(heads) * half;
+  const int64_t tok_items = rows * per;
+  const int64_t total = tok_items + zero_slots * per;
+  const int64_t blocks = (total + kRopeThreads - 1) / kRopeThreads;
+  if (blocks > 0x7fffffff) return kInvalid;
+  rope_pack_fwd_generic_kernel<<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
+      qkv, lora_q, lora_v, lora_dtype == SOUPK_DTYPE_F32, cos, sin, pos, pos_inv, q, k, v, rows, B,
+      T, NH, NKV, D, tok_items);
+  return launch_status();
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
+    const uint16_t* dq, const uint16_t* dk, const uint16_t* dv, const float* cos,
+    const float* sin, const int64_t* pos, uint16_t* dqkv, int64_t rows, int32_t B, int32_t T,
+    int32_t NH, int32_t NKV, int32_t D, void* stream) {
+  if (rows < 0 || B < 0 || T < 0 || NH < 0 || NKV < 0 || D <= 0 || (D & 1)) return kInvalid;
+  if (rows == 0 || NH + 2 * NKV == 0) return kOk;
+  if (!dqkv || !pos || !cos || !sin) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int half = D / 2;
+  const int heads = NH + 2 * NKV;
+  const bool vec = half == 64 && aligned(dq, 16) && aligned(dk, 16) && aligned(dv, 16) &&
+                   aligned(cos, 16) && aligned(sin, 16) && aligned(dqkv, 16);
+  if (vec) {
+    RopeDims dm;
+    dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
+    dm.items = static_cast<uint32_t>(heads * (half / 8));
+    dm.per_tok = FastDiv(dm.items);
+    const int64_t items = rows * dm.items;
+    if (items >= (int64_t{1} << 31)) return kInvalid;
+    rope_pack_bwd_kernel<64>
+        <<<static_cast<unsigned>((items + kRopeThreads - 1) / kRopeThreads), kRopeThreads, 0,
+           st>>>(dq, dk, dv, cos, sin, pos, dqkv, rows, dm);
+    return launch_status();
+  }
+  const int64_t total = rows * heads * half;
+  const int64_t blocks = (total + kRopeThreads - 1) / kRopeThreads;
+  if (blocks > 0x7fffffff) return kInvalid;
+  rope_pack_bwd_generic_kernel<<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
+      dq, dk, dv, cos, sin, pos, dqkv, rows, B, T, NH, NKV, D);
+  return launch_status();
+}

@@ -1,0 +1,90 @@
+// Host-side plumbing of libsoupk.so: ABI version, status strings, per-device CU count, and the
+// scatter-index inverse used by the pad-layout writers.
+
+#include <atomic>
+
+#include "soupk_common.hpp"
+
+namespace soupk {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // 0 = not queried yet (zero-initialised static)
+}  // namespace
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    n = 256;
+  g_cu_count[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+namespace {
+
+constexpr int kInvThreads = 1024;
+
+// Single workgroup: fill with -1, barrier, scatter.  Used while n_slots is small enough for one
+// workgroup to sweep quickly (every call in the QLoRA step: n_slots = batch * seq).
+__global__ __launch_bounds__(kInvThreads) void index_inverse_small_kernel(
+    const int64_t* __restrict__ idx, int64_t n, int32_t* __restrict__ inv, int64_t n_slots) {
+  for (int64_t p = threadIdx.x; p < n_slots; p += kInvThreads) inv[p] = -1;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < n; i += kInvThreads) {
+    const int64_t p = idx[i];
+    if (p >= 0 && p < n_slots) inv[p] = static_cast<int32_t>(i);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ dst, int64_t n,
+                                                       int32_t value) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) dst[i] = value;
+}
+
+__global__ __launch_bounds__(256) void scatter_rank_kernel(const int64_t* __restrict__ idx,
+                                                           int64_t n, int32_t* __restrict__ inv,
+                                                           int64_t n_slots) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t p = idx[i];
+  if (p >= 0 && p < n_slots) inv[p] = static_cast<int32_t>(i);
+}
+
+}  // namespace
+}  // namespace soupk
+
+using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_abi_version(void) {
+  return SOUPK_ABI_VERSION;
+}
+
+extern "C" __attribute__((visibility("default"))) const char* soupk_status_string(int status) {
+  if (status == kOk) return "success";
+  if (status == kInvalid) return "invalid argument (rejected before launch)";
+  return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_index_inverse(
+    const int64_t* idx, int64_t n, int32_t* inv, int64_t n_slots, void* stream) {
+  if (n < 0 || n_slots < 0 || n > 0x7fffffff) return kInvalid;
+  if (n_slots == 0) return kOk;
+  if (!inv || (n > 0 && !idx)) return kInvalid;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_slots <= (int64_t{1} << 16) && n <= (int64_t{1} << 16)) {
+    index_inverse_small_kernel<<<1, kInvThreads, 0, s>>>(idx, n, inv, n_slots);
+    return launch_status();
+  }
+  const int64_t g1 = (n_slots + 255) / 256;
+  if (g1 > 0x7fffffff) return kInvalid;
+  fill_i32_kernel<<<static_cast<int>(g1), 256, 0, s>>>(inv, n_slots, -1);
+  int st = launch_status();
+  if (st != kOk || n == 0) return st;
+  scatter_rank_kernel<<<static_cast<int>((n + 255) / 256), 256, 0, s>>>(idx, n, inv, n_slots);
+  return launch_status();
+}

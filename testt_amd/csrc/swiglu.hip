@@ -1,0 +1,191 @@
+// Gated SiLU (SwiGLU) forward and in-place backward over the fused [gate | up] GEMM output.
+//
+// Reference: solution/mlp.py:31-40 (gated_silu_fwd_kernel), solution/mlp.py:43-58
+// (gated_silu_bwd_inplace_kernel), launched from gated_silu / gated_silu_backward_,
+// solution/mlp.py:61-77.
+//
+// Pure HBM streaming.  The flat index space is rows * I/8 chunks of 8 fp16 (16 bytes); chunk c
+// lives in row r = c / (I/8), and because act is [rows, I] contiguous its chunk offset is 8c,
+// while gate sits at 8c + r*I and up at 8c + r*I + I of the [rows, 2I] buffer.  Each thread
+// issues all loads of kSwiUnroll chunks before any arithmetic so that every wave keeps several
+// KiB in flight.  Arithmetic is fp32: exp through v_exp_f32, the reciprocal through v_rcp_f32
+// (both about 1 ulp of fp32, far below the fp16 rounding of the result).
+
+#include "fastdiv.hpp"
+#include "soupk_common.hpp"
+
+namespace soupk {
+namespace {
+
+constexpr int kSwiThreads = 256;
+constexpr int kSwiUnroll = 2;
+
+__device__ __forceinline__ float sigmoid_f(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp(-g));
+}
+
+__device__ __forceinline__ uint32_t silu_mul_word(uint32_t gw, uint32_t uw) {
+  const float g0 = lo_h(gw), g1 = hi_h(gw);
+  const float u0 = lo_h(uw), u1 = hi_h(uw);
+  return pack_h2(g0 * sigmoid_f(g0) * u0, g1 * sigmoid_f(g1) * u1);
+}
+
+// Returns {d gate word, d up word} for one dword (two fp16) of dact, gate and up.
+__device__ __forceinline__ u32x2 silu_bwd_word(uint32_t dw, uint32_t gw, uint32_t uw) {
+  float dg[2], du[2];
+  const float d[2] = {lo_h(dw), hi_h(dw)};
+  const float g[2] = {lo_h(gw), hi_h(gw)};
+  const float u[2] = {lo_h(uw), hi_h(uw)};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float sig = sigmoid_f(g[j]);
+    const float d_silu = d[j] * u[j];
+    dg[j] = d_silu * sig * (1.0f + g[j] * (1.0f - sig));
+    du[j] = d[j] * (g[j] * sig);
+  }
+  return u32x2{pack_h2(dg[0], dg[1]), pack_h2(du[0], du[1])};
+}
+
+__global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec_kernel(
+    const u32x4* __restrict__ gu, u32x4* __restrict__ act, uint32_t n_chunks, FastDiv row_of,
+    uint32_t I_chunks) {
+  const uint32_t step = kSwiThreads * kSwiUnroll;
+  for (uint32_t base = blockIdx.x * step; base < n_chunks; base += gridDim.x * step) {
+    u32x4 g[kSwiUnroll], u[kSwiUnroll];
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
+      if (c < n_chunks) {
+        const uint64_t gi = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) *
+                                                           I_chunks;
+        g[k] = __builtin_nontemporal_load(gu + gi);
+        u[k] = __builtin_nontemporal_load(gu + gi + I_chunks);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
+      if (c < n_chunks) {
+        u32x4 r;
+        r.x = silu_mul_word(g[k].x, u[k].x);
+        r.y = silu_mul_word(g[k].y, u[k].y);
+        r.z = silu_mul_word(g[k].z, u[k].z);
+        r.w = silu_mul_word(g[k].w, u[k].w);
+        __builtin_nontemporal_store(r, act + c);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec_kernel(
+    const u32x4* __restrict__ dact, u32x4* __restrict__ gu, uint32_t n_chunks, FastDiv row_of,
+    uint32_t I_chunks) {
+  const uint32_t step = kSwiThreads * kSwiUnroll;
+  for (uint32_t base = blockIdx.x * step; base < n_chunks; base += gridDim.x * step) {
+    u32x4 d[kSwiUnroll], g[kSwiUnroll], u[kSwiUnroll];
+    uint64_t gi[kSwiUnroll];
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
+      gi[k] = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) * I_chunks;
+      if (c < n_chunks) {
+        d[k] = __builtin_nontemporal_load(dact + c);
+        g[k] = __builtin_nontemporal_load(gu + gi[k]);
+        u[k] = __builtin_nontemporal_load(gu + gi[k] + I_chunks);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
+      if (c < n_chunks) {
+        const u32x2 r0 = silu_bwd_word(d[k].x, g[k].x, u[k].x);
+        const u32x2 r1 = silu_bwd_word(d[k].y, g[k].y, u[k].y);
+        const u32x2 r2 = silu_bwd_word(d[k].z, g[k].z, u[k].z);
+        const u32x2 r3 = silu_bwd_word(d[k].w, g[k].w, u[k].w);
+        const u32x4 dg = {r0.x, r1.x, r2.x, r3.x};
+        const u32x4 du = {r0.y, r1.y, r2.y, r3.y};
+        __builtin_nontemporal_store(dg, gu + gi[k]);
+        __builtin_nontemporal_store(du, gu + gi[k] + I_chunks);
+      }
+    }
+  }
+}
+
+// Element-wise forms for shapes the vector kernels do not take (I % 8 != 0, unaligned).
+__global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_elem_kernel(
+    const uint16_t* __restrict__ gu, uint16_t* __restrict__ act, int64_t n, int64_t I) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kSwiThreads + threadIdx.x;
+  if (e >= n) return;
+  const int64_t r = e / I;
+  const int64_t gi = e + r * I;
+  const float g = h2f(gu[gi]), u = h2f(gu[gi + I]);
+  act[e] = static_cast<uint16_t>(pack_h2(g * sigmoid_f(g) * u, 0.0f) & 0xffffu);
+}
+
+__global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_elem_kernel(
+    const uint16_t* __restrict__ dact, uint16_t* __restrict__ gu, int64_t n, int64_t I) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kSwiThreads + threadIdx.x;
+  if (e >= n) return;
+  const int64_t gi = e + (e / I) * I;
+  const u32x2 r = silu_bwd_word(dact[e], gu[gi], gu[gi + I]);
+  gu[gi] = static_cast<uint16_t>(r.x & 0xffffu);
+  gu[gi + I] = static_cast<uint16_t>(r.y & 0xffffu);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int vec_grid(uint32_t n_chunks) {
+  const int64_t step = static_cast<int64_t>(kSwiThreads) * kSwiUnroll;
+  const int64_t steps = (static_cast<int64_t>(n_chunks) + step - 1) / step;
+  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 8;
+  return static_cast<int>(steps < cap ? steps : cap);
+}
+
+}  // namespace
+}  // namespace soupk
+
+using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_swiglu_fwd(const uint16_t* gu,
+                                                                        uint16_t* act,
+                                                                        int64_t rows, int64_t I,
+                                                                        void* stream) {
+  if (rows < 0 || I < 0) return kInvalid;
+  const int64_t n = rows * I;
+  if (n == 0) return kOk;
+  if (!gu || !act) return kInvalid;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && aligned16(gu) && aligned16(act)) {
+    const uint32_t n_chunks = static_cast<uint32_t>(n / 8);
+    const uint32_t I_chunks = static_cast<uint32_t>(I / 8);
+    swiglu_fwd_vec_kernel<<<vec_grid(n_chunks), kSwiThreads, 0, s>>>(
+        reinterpret_cast<const u32x4*>(gu), reinterpret_cast<u32x4*>(act), n_chunks,
+        FastDiv(I_chunks), I_chunks);
+    return launch_status();
+  }
+  const int64_t grid = (n + kSwiThreads - 1) / kSwiThreads;
+  if (grid > 0x7fffffff) return kInvalid;
+  swiglu_fwd_elem_kernel<<<static_cast<int>(grid), kSwiThreads, 0, s>>>(gu, act, n, I);
+  return launch_status();
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_swiglu_bwd_inplace(
+    const uint16_t* dact, uint16_t* gu, int64_t rows, int64_t I, void* stream) {
+  if (rows < 0 || I < 0) return kInvalid;
+  const int64_t n = rows * I;
+  if (n == 0) return kOk;
+  if (!gu || !dact) return kInvalid;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && aligned16(gu) && aligned16(dact)) {
+    const uint32_t n_chunks = static_cast<uint32_t>(n / 8);
+    const uint32_t I_chunks = static_cast<uint32_t>(I / 8);
+    swiglu_bwd_vec_kernel<<<vec_grid(n_chunks), kSwiThreads, 0, s>>>(
+        reinterpret_cast<const u32x4*>(dact), reinterpret_cast<u32x4*>(gu), n_chunks,
+        FastDiv(I_chunks), I_chunks);
+    return launch_status();
+  }
+  const int64_t grid = (n + kSwiThreads - 1) / kSwiThreads;
+  if (grid > 0x7fffffff) return kInvalid;
+  swiglu_bwd_elem_kernel<<<static_cast<int>(grid), kSwiThreads, 0, s>>>(dact, gu, n, I);
+  return launch_status();
+}

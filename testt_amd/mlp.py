@@ -1,0 +1,92 @@
+"""The Qwen2 MLP, down(silu(gate(x)) * up(x)), with frozen NF4 weights, as one autograd node.
+Drop-in for solution/mlp.py.
+
+- gate and up are one hipBLASLt GEMM against both weights unpacked into one [2I, H] buffer;
+- testt_amd/csrc/swiglu.hip reads the fp16 [tokens, 2I] result and writes silu(g) * u in fp16
+  (computed in fp32, rounded once to fp16 where the down projection reads it);
+- nothing of size [tokens, I] is saved: backward recomputes gate/up from the saved fp16 input
+  (one GEMM) and the in-place backward kernel turns the incoming gradient into the gate/up
+  gradients in the same buffer, so the input gradient is again a single GEMM.
+"""
+
+import torch
+
+from . import _ext
+from ._common import kernels_ok
+from .nf4 import unpack_concat
+
+RECOMPUTE_GATE_UP = True  # keep only the [tokens, H] input; recompute gate/up in backward
+# Columns one workgroup step covers per row in the reference's tiling (solution/mlp.py:28);
+# the HIP kernels stream the flat [rows, I] space in 16-byte chunks instead.
+COLS_PER_PROGRAM = 1024
+
+
+def gated_silu(gu):
+    """act[r, c] = fp16(silu(gu[r, c]) * gu[r, I + c]) for gu = [gate | up] fp16 [rows, 2I]."""
+    _ext.require(gu, "gu", dtype=torch.float16, ndim=2)
+    rows, two_i = gu.shape
+    if two_i % 2:
+        raise ValueError(f"gu width {two_i} is odd; expected [gate | up]")
+    inter = two_i // 2
+    act = torch.empty((rows, inter), dtype=torch.float16, device=gu.device)
+    if rows and inter:
+        _ext.call("soupk_swiglu_fwd", _ext.ptr(gu), _ext.ptr(act), rows, inter,
+                  _ext.stream_of(gu))
+    return act
+
+
+def gated_silu_backward_(dact, gu):
+    """Overwrites gu = [gate | up] with [d gate | d up] for the incoming gradient dact."""
+    _ext.require(gu, "gu", dtype=torch.float16, ndim=2)
+    rows, two_i = gu.shape
+    inter = two_i // 2
+    dact = dact.to(torch.float16).contiguous()
+    _ext.require(dact, "dact", dtype=torch.float16, ndim=2, device=gu.device)
+    if tuple(dact.shape) != (rows, inter):
+        raise ValueError(f"dact shape {tuple(dact.shape)} != {(rows, inter)}")
+    if rows and inter:
+        _ext.call("soupk_swiglu_bwd_inplace", _ext.ptr(dact), _ext.ptr(gu), rows, inter,
+                  _ext.stream_of(gu))
+    return gu
+
+
+class FusedNF4MLP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, gate_w, up_w, down_w):
+        gate_up = unpack_concat((gate_w, up_w), x.device)
+        gu = torch.matmul(x, gate_up.t())
+        del gate_up
+        act = gated_silu(gu)
+        if RECOMPUTE_GATE_UP:
+            del gu
+            ctx.save_for_backward(x)
+        else:
+            ctx.save_for_backward(x, gu)
+        down = unpack_concat((down_w,), x.device)
+        out = torch.matmul(act, down.t())
+        ctx.weights = (gate_w, up_w, down_w)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if not ctx.needs_input_grad[0]:
+            return None, None, None, None
+        gate_w, up_w, down_w = ctx.weights
+        saved = ctx.saved_tensors
+        x = saved[0]
+        grad_out = grad_out.to(torch.float16)
+        down = unpack_concat((down_w,), grad_out.device)
+        dact = torch.matmul(grad_out, down)
+        del down
+        gate_up = unpack_concat((gate_w, up_w), grad_out.device)
+        gu = torch.matmul(x, gate_up.t()) if RECOMPUTE_GATE_UP else saved[1]
+        gated_silu_backward_(dact, gu)
+        del dact
+        grad_x = torch.matmul(gu, gate_up)
+        return grad_x, None, None, None
+
+
+def fused_mlp(x, gate_w, up_w, down_w):
+    if not kernels_ok(x):
+        raise ValueError("fused_mlp: x must be a HIP device tensor (no CPU path)")
+    return FusedNF4MLP.apply(x.contiguous(), gate_w, up_w, down_w)

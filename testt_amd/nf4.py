@@ -1,0 +1,140 @@
+"""NF4 (bitsandbytes 4-bit, double quant) weight unpacking on gfx950, and the frozen 4-bit linear
+that uses it.  Drop-in for solution/nf4.py (same names, arguments and fallbacks).
+
+bitsandbytes stores a frozen projection as NF4: two 4-bit codes per byte (high nibble first),
+one absmax per `blocksize` (64) values, and with double quant ("nested") the absmax itself is
+an 8-bit code into a 256-entry table, scaled per 256 absmax blocks and shifted by one offset:
+
+    absmax[b] = code2[absmax_u8[b]] * absmax2[b // 256] + offset
+    w[i]      = nf4[q[i]] * absmax[i // 64]          (fp32, rounded once to fp16)
+
+`soupk_nf4_unpack` (testt_amd/csrc/nf4_unpack.hip) does this in one HBM pass, rounding each
+product and sum separately as bitsandbytes does, so the fp16 values are bit-identical to
+bitsandbytes' dequantize_4bit.  Several projections are unpacked into one buffer so that q/k/v
+or gate/up run as a single hipBLASLt GEMM (torch.matmul).
+"""
+
+import torch
+
+from . import _ext
+from ._common import kernels_ok
+
+# One workgroup step of the unpack kernel: 256 threads x 4 chunks x 16 packed bytes.
+# (solution/nf4.py:24 names the per-program tile of the Triton kernel the same way.)
+BYTES_PER_PROGRAM = 16384
+
+
+def _quant_state(weight):
+    return getattr(weight, "quant_state", None)
+
+
+def supports_fast_unpack(weight):
+    """True for the layout the kernel handles: NF4, nested absmax with 256-blocks, even sizes.
+
+    Same predicate as solution/nf4.py:52-62."""
+    state = _quant_state(weight)
+    if state is None or getattr(state, "quant_type", None) != "nf4" or not state.nested:
+        return False
+    if state.state2 is None or state.state2.blocksize != 256 or state.blocksize % 2:
+        return False
+    shape = tuple(state.shape)
+    if len(shape) != 2 or (shape[0] * shape[1]) % state.blocksize:
+        return False
+    return weight.data.dtype == torch.uint8 and weight.data.is_contiguous()
+
+
+def _on_device(weight, device):
+    state = _quant_state(weight)
+    tensors = (weight.data, state.absmax, state.code, state.state2.code, state.state2.absmax)
+    return all(t.device == device for t in tensors) and \
+        (not torch.is_tensor(state.offset) or state.offset.device == device)
+
+
+def _offset_tensor(state, device):
+    off = state.offset
+    if torch.is_tensor(off):
+        off = off.reshape(-1)[:1]
+        return off if off.dtype == torch.float32 else off.float()
+    return torch.tensor([float(off)], dtype=torch.float32, device=device)
+
+
+def _f32(t):
+    return t if t.dtype == torch.float32 and t.is_contiguous() else t.float().contiguous()
+
+
+def unpack_into(weight, out):
+    """Write the fp16 values of one bitsandbytes 4-bit weight ([N, K]) into `out` ([N, K]).
+
+    Mirrors solution/nf4.py:72-89: the HIP kernel for the supported layout on the device,
+    bitsandbytes' own dequantize_4bit for other layouts (as the reference does).  CPU tensors
+    are rejected: this build has no CPU path."""
+    state = _quant_state(weight)
+    if not kernels_ok(out):
+        raise ValueError("unpack_into: `out` must be a HIP device tensor (no CPU path)")
+    n_bytes = weight.data.numel()
+    if supports_fast_unpack(weight) and _on_device(weight, out.device):
+        _ext.require(out, "out", dtype=torch.float16)
+        if out.numel() != 2 * n_bytes:
+            raise ValueError(f"out has {out.numel()} elements, the weight holds {2 * n_bytes}")
+        if state.absmax.dtype != torch.uint8:
+            raise TypeError(f"nested absmax must be uint8, got {state.absmax.dtype}")
+        absmax = state.absmax.contiguous()
+        code2 = _f32(state.state2.code)
+        absmax2 = _f32(state.state2.absmax)
+        nf4 = _f32(state.code)
+        if code2.numel() < 256 or nf4.numel() < 16:
+            raise ValueError("quant state tables are too small (code2 needs 256, nf4 16 entries)")
+        n_blocks = -(-n_bytes // (state.blocksize // 2))
+        if absmax.numel() < n_blocks or absmax2.numel() < -(-n_blocks // 256):
+            raise ValueError("quant state absmax arrays do not cover the weight")
+        offset = _offset_tensor(state, out.device)
+        _ext.call("soupk_nf4_unpack", _ext.ptr(weight.data), _ext.ptr(absmax), _ext.ptr(code2),
+                  _ext.ptr(absmax2), _ext.ptr(offset), _ext.ptr(nf4), _ext.ptr(out), n_bytes,
+                  int(state.blocksize), int(state.state2.blocksize), _ext.stream_of(out))
+        return out
+    import bitsandbytes.functional as bnb_functional
+
+    out.copy_(bnb_functional.dequantize_4bit(weight.data, state).to(out.dtype).view_as(out))
+    return out
+
+
+def weight_shape(weight):
+    return tuple(_quant_state(weight).shape)
+
+
+def unpack_concat(weights, device):
+    """fp16 [sum N_i, K]: the weights stacked by rows, each unpacked in place."""
+    rows = [weight_shape(w)[0] for w in weights]
+    cols = weight_shape(weights[0])[1]
+    out = torch.empty((sum(rows), cols), dtype=torch.float16, device=device)
+    start = 0
+    for weight, n in zip(weights, rows):
+        unpack_into(weight, out[start:start + n])
+        start += n
+    return out
+
+
+class FrozenNF4Linear(torch.autograd.Function):
+    """y = x @ W^T (+ b) for frozen 4-bit weights stacked by rows, fp16 in and out.
+
+    Nothing large is saved: the weights are unpacked again in backward, and no input is kept
+    because W does not train (solution/nf4.py:108-127)."""
+
+    @staticmethod
+    def forward(ctx, x, bias, weights):
+        weight = unpack_concat(weights, x.device)
+        out = torch.nn.functional.linear(x, weight, bias)
+        ctx.weights = weights
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            weight = unpack_concat(ctx.weights, grad_out.device)
+            grad_x = grad_out.to(torch.float16) @ weight
+        return grad_x, None, None
+
+
+def frozen_linear(x, weights, bias=None):
+    return FrozenNF4Linear.apply(x, bias, tuple(weights))
