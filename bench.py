@@ -5,12 +5,12 @@
 A step is one pass of the hot path over one batch of synthetic input: every kernel of the
 solution/ set, forward and backward, once, at the 2048-token shape of Qwen2.5-1.5B
 (config 1, the CPU-runnable RMSNorm case, is the same RMSNorm
-shape).  Inputs are resident in HBM before the timed region.  Each launch is bracketed by HIP
-events on the stream it runs on (torch's current stream); the queue is kept ahead of the GPU
-(launches go straight through the C ABI with preallocated buffers, after a GPU-side prefill),
-so an event pair measures the kernel, not the host.  Two input sets per kernel alternate, and
-the other kernels of the step move > 600 MB between two launches of one kernel, so the
-256 MB Infinity Cache does not serve its inputs.
+shape).  Inputs are resident in HBM before the timed region.  Each launch carries a pair of
+HIP events on the stream it runs on (torch's current stream), recorded by the kernel dispatch
+itself (soupk_time_next_launch -> hipExtLaunchKernelGGL), so they time the kernel exactly as
+rocprofv3's kernel trace does; launches go straight through the C ABI with preallocated
+buffers.  Two input sets per kernel alternate, and the other kernels of the step move > 600 MB
+between two launches of one kernel, so the 256 MB Infinity Cache does not serve its inputs.
 
 Prints ONE JSON line: value = the set's aggregate compulsory HBM bytes / summed kernel time
 (GB/s), per-kernel us / GB/s / fraction of the 8 TB/s peak, the roofline of the dominant kernel,
@@ -18,6 +18,7 @@ and the CPU baseline (the reference's eager PyTorch path on the host cores, orac
 """
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -199,38 +200,83 @@ def build_cases(dev, n_sets=2):
     return cases
 
 
-def prefill(buf, n):
-    """Queue n large fills so the host runs ahead of the GPU into the timed region."""
-    for _ in range(n):
-        buf.fill_(1.0)
+class HipEvents:
+    """hipEvent_t pairs from the HIP runtime torch already loaded (RTLD_NOLOAD: the same one)."""
+
+    def __init__(self):
+        try:
+            self.hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | os.RTLD_GLOBAL)
+        except OSError:
+            self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.events = []
+
+    def new(self):
+        ev = ctypes.c_void_p()
+        if self.hip.hipEventCreate(ctypes.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        self.events.append(ev)
+        return ev
+
+    def elapsed_us(self, a, b):
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1e3
+
+    def close(self):
+        for ev in self.events:
+            self.hip.hipEventDestroy(ev)
+        self.events = []
 
 
 def time_gpu(cases, steps, warmup, dev):
+    """Per-launch kernel durations: soupk_time_next_launch() makes each launch record a HIP
+    event pair with its own dispatch (hipExtLaunchKernelGGL), on the stream it runs on."""
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    busy = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)   # 1 GiB
+    arm = _ext.lib().soupk_time_next_launch
+    hip = HipEvents()
     for w in range(warmup):
         for c in cases:
             c.launch(w, sh)
+    ev = [[(hip.new(), hip.new()) for _ in cases] for _ in range(steps)]
     torch.cuda.synchronize(dev)
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in cases] for _ in range(steps)]
-    torch.cuda.synchronize(dev)
-    prefill(busy, 8)
     t0 = time.perf_counter()
     for s in range(steps):
         for j, c in enumerate(cases):
             a, b = ev[s][j]
-            a.record(stream)
+            arm(a, b)
             c.launch(s, sh)
-            b.record(stream)
     host_enqueue = time.perf_counter() - t0
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
     for j, c in enumerate(cases):
-        c.times = [ev[s][j][0].elapsed_time(ev[s][j][1]) * 1e3 for s in range(steps)]   # us
-    del busy
+        c.times = [hip.elapsed_us(*ev[s][j]) for s in range(steps)]
+    hip.close()
     return host_enqueue, wall
+
+
+def copy_peak(dev, mib=1024, reps=6):
+    """Read+write GB/s of torch's device copy of `mib` MiB (the box's plain-copy reference)."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device=dev)
+    b = torch.empty(n, device=dev)
+    b.copy_(a)
+    torch.cuda.synchronize(dev)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b.copy_(a)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        ts.append(e0.elapsed_time(e1) * 1e-3)
+    del a, b
+    return round(2 * n * 4 / median(ts) / 1e9, 1)
 
 
 def cpu_baseline(cases, seconds):
@@ -294,6 +340,7 @@ def main():
     torch.cuda.synchronize(dev)
     log(f"timing {len(cases)} kernels: warmup {args.warmup}, steps {args.steps}")
     host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
+    copy_gbps = copy_peak(dev)
     kernels = {}
     total_us = 0.0
     total_bytes = 0
@@ -333,6 +380,9 @@ def main():
         "value_definition": "sum of compulsory HBM bytes of the 8 kernels / sum of their mean "
                             "HIP-event durations",
         "kernels": kernels,
+        "copy_peak_GBps": copy_gbps,
+        "timing": "per-launch HIP events recorded by the kernel dispatch itself "
+                  "(soupk_time_next_launch / hipExtLaunchKernelGGL), mean over steps",
         "step_wall_ms": round(wall * 1e3 / args.steps, 4),
         "host_enqueue_ms": round(host_enqueue * 1e3 / args.steps, 4),
         "roofline": roofline,

@@ -5,8 +5,9 @@
  * Every entry point:
  *   - takes plain device pointers, element counts and a HIP stream (`void*`, a hipStream_t;
  *     NULL is the legacy default stream), enqueues its kernels asynchronously and returns;
- *   - never allocates, never synchronises, keeps no mutable global state (re-entrant: PyTorch
- *     runs backward on its own worker thread);
+ *   - never allocates, never synchronises, and shares no mutable state between threads
+ *     (re-entrant: PyTorch runs backward on its own worker thread); the only state is the
+ *     per-thread benchmark hook of soupk_time_next_launch;
  *   - returns 0 on success, hipErrorInvalidValue (1) for arguments it rejects before
  *     launching, or the hipError_t of the launch;
  *   - bounds-checks every index it reads from device memory (positions, pad rows, labels):
@@ -31,6 +32,16 @@ int soupk_abi_version(void);
 
 /* Human-readable text of a status code returned by any soupk_* call. */
 const char* soupk_status_string(int status);
+
+/*
+ * Benchmark instrumentation (no counterpart in the reference, which times its Triton kernels
+ * with CUDA events around each launch, harness/_train.py:60-83): the next kernel launched by
+ * the calling thread through any soupk_* entry point records `start_event` when its dispatch
+ * begins and `stop_event` when it ends (hipExtLaunchKernelGGL), so the pair measures exactly
+ * that kernel.  Events (hipEvent_t, nullable) are created by the caller; the setting is per
+ * thread and is cleared by that launch.
+ */
+int soupk_time_next_launch(void* start_event, void* stop_event);
 
 /*
  * NF4 double-quant unpack (replaces the launch of nf4_unpack_kernel, solution/nf4.py:27-45,

@@ -32,7 +32,7 @@ def assert_rel(actual, expected, rtol, atol=0.0, what="value"):
     e = torch.as_tensor(expected).detach().cpu().double()
     err = (a - e).abs()
     bound = atol + rtol * e.abs()
-    bad = err > bound
+    bad = ~(err <= bound) & ~(torch.isnan(a) & torch.isnan(e))   # NaN where e is not: bad
     assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {bad.numel()} exceed "
                                  f"rtol={rtol} atol={atol}; worst rel "
                                  f"{float((err / e.abs().clamp_min(1e-30)).max()):.3e}")

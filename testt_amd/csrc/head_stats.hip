@@ -5,17 +5,23 @@
 // FusedHeadLoss.forward, solution/head.py:105-114.
 //
 // Mapping (gfx950): one workgroup of 1024 threads (16 wavefronts, a whole CU) per logits row.
-// Sweep 1 streams the row once with 16-byte loads (a wave reads 1 KiB per load instruction)
-// and keeps per lane a running max m, sum(e) and sum(e*z) with e = exp(z - m), plus the first
+// Register-resident form (V <= 1024 * 8 * kMaxCpt): each thread loads its share of the row --
+// chunk k*1024 + tid, 16 bytes each, every wave load instruction reading 1 KiB contiguous --
+// into VGPRs in one burst (a 151,936-column row is 297 KiB = 19 x 16 B per thread), computes
+// the statistics from the registers as the loads land, and after the workgroup reduction writes
+// the gradient from the same registers: the row crosses HBM once in and (for labelled rows) once
+// out, the compulsory traffic.  Larger vocabularies use the streaming form, which reads the row
+// twice (the second read served by L2 / the Infinity Cache).
+//
+// Statistics per lane: running max m, sum(e) and sum(e*z) with e = exp(z - m), and the first
 // column where the max was reached (lanes visit their columns in increasing order, so a strict
-// '>' keeps the first occurrence; the cross-lane merge breaks value ties on the smaller column,
-// which is torch.argmax's first-maximum rule).  The rescale of the running sums happens once
-// per 8-value chunk, only when the chunk raises the max.  The 16 wave results merge through
-// LDS.  Sweep 2 (labelled rows only) re-reads the row, now resident in L2 / the Infinity Cache,
-// and overwrites it with the gradient; the onehot term is applied to the one chunk holding the
-// label.  exp(x) is computed as 2^(x*log2 e) with v_exp_f32.
+// '>' keeps the first occurrence; merges across lanes break value ties on the smaller column,
+// which is torch.argmax's first-maximum rule).  The running sums are rescaled once per 8-value
+// chunk, only when the chunk raises the max.  exp(x) is computed as 2^(x*log2 e) (v_exp_f32).
 
 #include <limits.h>
+
+#include <type_traits>
 
 #include "soupk_common.hpp"
 
@@ -24,19 +30,25 @@ namespace {
 
 constexpr int kHeadThreads = 1024;
 constexpr int kHeadWaves = kHeadThreads / kWave;
-constexpr int kHeadUnroll = 2;  // 16-byte chunks per thread per sweep step
+constexpr int kStreamUnroll = 2;  // 16-byte chunks per thread per step, streaming form
+constexpr int kMaxCpt = 20;       // register-resident form: up to 20 chunks (80 VGPRs) / thread
 constexpr int64_t kIgnoreIndex = -100;
 
 struct RowStats {
-  float m;    // running max (also the best value for the argmax)
-  float se;   // sum exp(z - m)
-  float sd;   // sum exp(z - m) * z
-  int32_t ix; // first column holding m (INT_MAX: none yet)
+  float m;     // running max (also the best value for the argmax)
+  float se;    // sum exp(z - m)
+  float sd;    // sum exp(z - m) * z
+  int32_t ix;  // first column holding m (INT_MAX: none yet)
 };
 
 __device__ __forceinline__ float scale_to(float m_old, float m_new) {
   // exp(m_old - m_new); an empty accumulator (m_old = -inf) contributes nothing.
   return m_old == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_old - m_new) * kLog2e);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float* z) {
+  z[0] = lo_h(w.x); z[1] = hi_h(w.x); z[2] = lo_h(w.y); z[3] = hi_h(w.y);
+  z[4] = lo_h(w.z); z[5] = hi_h(w.z); z[6] = lo_h(w.w); z[7] = hi_h(w.w);
 }
 
 // Fold N consecutive columns z[0..N) starting at column col0 into the running statistics.
@@ -63,6 +75,37 @@ __device__ __forceinline__ void absorb(RowStats& st, const float* z, int32_t col
   }
 }
 
+// Fold one 16-byte chunk (8 fp16 columns starting at col0) into the running statistics.  The
+// chunk max is taken in packed fp16 (exact: a max selects one of its inputs), and the fp16
+// values feed the fp32 exp/dot arithmetic directly (v_fma_mix_f32), so the chunk is never
+// widened to eight fp32 registers.
+__device__ __forceinline__ void absorb_chunk(RowStats& st, const u32x4 w, int32_t col0) {
+  const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
+  const f16x2 m2 = __builtin_elementwise_max(__builtin_elementwise_max(a, b),
+                                             __builtin_elementwise_max(c, d));
+  const float bm = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
+  if (bm > st.m) {
+    const float f = scale_to(st.m, bm);
+    st.se = st.se * f;
+    st.sd = st.sd * f;
+    st.m = bm;
+    float z[8];
+    unpack8(w, z);
+#pragma unroll
+    for (int j = 7; j >= 0; --j)
+      if (z[j] == bm) st.ix = col0 + j;
+  }
+  const float shift = -st.m * kLog2e;
+  const f16 h[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float z = static_cast<float>(h[j]);
+    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, shift));
+    st.se = st.se + e;
+    st.sd = __builtin_fmaf(e, z, st.sd);
+  }
+}
+
 __device__ __forceinline__ void merge(RowStats& a, const RowStats& b) {
   const float M = fmaxf(a.m, b.m);
   const float fa = scale_to(a.m, M), fb = scale_to(b.m, M);
@@ -84,62 +127,28 @@ __device__ __forceinline__ void wave_merge(RowStats& s) {
   }
 }
 
-__device__ __forceinline__ void unpack8(const u32x4 w, float* z) {
-  z[0] = lo_h(w.x); z[1] = hi_h(w.x); z[2] = lo_h(w.y); z[3] = hi_h(w.y);
-  z[4] = lo_h(w.z); z[5] = hi_h(w.z); z[6] = lo_h(w.w); z[7] = hi_h(w.w);
+// Row geometry: columns [0, lead) precede the first 16-byte boundary of the row, [tail0, V)
+// follow its last whole 16-byte chunk; nvec chunks lie between.
+struct RowSpan {
+  int64_t lead, nvec, tail0;
+};
+
+__device__ __forceinline__ RowSpan row_span(const uint16_t* base, int64_t V) {
+  RowSpan r;
+  r.lead = ((16 - static_cast<int>(reinterpret_cast<uintptr_t>(base) & 15)) & 15) >> 1;
+  if (r.lead > V) r.lead = V;
+  r.nvec = (V - r.lead) >> 3;
+  r.tail0 = r.lead + r.nvec * 8;
+  return r;
 }
 
-__global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
-    uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
-    float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
-    float* __restrict__ lse_out, float grad_scale, int64_t V) {
-  __shared__ RowStats part[kHeadWaves];
-  __shared__ float row_lse;
-
-  const int64_t row = blockIdx.x;
-  uint16_t* base = logits + row * V;
-  const int64_t tgt = target[row];
-  const bool labelled = tgt != kIgnoreIndex;
-  const bool tgt_ok = tgt >= 0 && tgt < V;
-  const int tid = threadIdx.x;
-
-  // Columns [0, lead) precede the first 16-byte boundary; [tail0, V) follow the last whole chunk.
-  int64_t lead = ((16 - static_cast<int>(reinterpret_cast<uintptr_t>(base) & 15)) & 15) >> 1;
-  if (lead > V) lead = V;
-  const int64_t nvec = (V - lead) >> 3;
-  const int64_t tail0 = lead + nvec * 8;
-  const u32x4* vb = reinterpret_cast<const u32x4*>(base + lead);
-  constexpr int64_t kStep = static_cast<int64_t>(kHeadThreads) * kHeadUnroll;
-
-  // ---- sweep 1: statistics -------------------------------------------------------------
-  RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
-  if (tid < lead) {
-    const float z = h2f(base[tid]);
-    absorb<1>(st, &z, tid);
-  }
-  for (int64_t s0 = 0; s0 < nvec; s0 += kStep) {
-    u32x4 w[kHeadUnroll];
-#pragma unroll
-    for (int u = 0; u < kHeadUnroll; ++u) {
-      const int64_t c = s0 + u * kHeadThreads + tid;
-      if (c < nvec) w[u] = vb[c];
-    }
-#pragma unroll
-    for (int u = 0; u < kHeadUnroll; ++u) {
-      const int64_t c = s0 + u * kHeadThreads + tid;
-      if (c < nvec) {
-        float z[8];
-        unpack8(w[u], z);
-        absorb<8>(st, z, static_cast<int32_t>(lead + 8 * c));
-      }
-    }
-  }
-  if (tail0 + tid < V) {
-    const float z = h2f(base[tail0 + tid]);
-    absorb<1>(st, &z, static_cast<int32_t>(tail0 + tid));
-  }
+// Workgroup merge of the per-thread statistics and the per-row outputs; returns the row's lse
+// to every thread.  Thread 0 reads z[target] here, before any thread overwrites the row.
+__device__ float finish_row(RowStats st, RowStats* part, float* row_lse, const uint16_t* base,
+                            int64_t row, int64_t tgt, bool labelled, bool tgt_ok,
+                            float* entropy, float* loss, int32_t* correct, float* lse_out) {
   wave_merge(st);
-  const int wave = tid / kWave, lane = tid % kWave;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (lane == 0) part[wave] = st;
   __syncthreads();
   if (wave == 0) {
@@ -154,53 +163,168 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
       loss[row] = l;
       correct[row] = (labelled && tgt_ok && static_cast<int64_t>(arg) == tgt) ? 1 : 0;
       if (lse_out != nullptr) lse_out[row] = lse;
-      row_lse = lse;
+      *row_lse = lse;
     }
   }
   __syncthreads();
-  if (!labelled) return;
+  return *row_lse;
+}
 
-  // ---- sweep 2: gradient in place --------------------------------------------------------
-  const float shift = -row_lse * kLog2e;
-  const int64_t tchunk = (tgt_ok && tgt >= lead && tgt < tail0) ? (tgt - lead) >> 3 : -1;
-  auto grad1 = [&](int64_t col) {
-    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(h2f(base[col]), kLog2e, shift));
-    const float g = (col == tgt ? p - 1.0f : p) * grad_scale;
-    base[col] = static_cast<uint16_t>(pack_h2(g, 0.f) & 0xffffu);
-  };
-  if (tid < lead) grad1(tid);
-  u32x4* vw = reinterpret_cast<u32x4*>(base + lead);
-  for (int64_t s0 = 0; s0 < nvec; s0 += kStep) {
-    u32x4 w[kHeadUnroll];
+// Gradient of one 8-column chunk: fp16((exp(z - lse) - [col == tgt]) * grad_scale).
+__device__ __forceinline__ u32x4 grad_chunk(u32x4 w, float shift, float grad_scale,
+                                            int hit /* 0..7, or -1 */) {
+  float z[8];
+  unpack8(w, z);
 #pragma unroll
-    for (int u = 0; u < kHeadUnroll; ++u) {
+  for (int j = 0; j < 8; ++j) z[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[j], kLog2e, shift));
+  if (hit >= 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == hit) z[j] = z[j] - 1.0f;
+  }
+  return u32x4{pack_h2(z[0] * grad_scale, z[1] * grad_scale),
+               pack_h2(z[2] * grad_scale, z[3] * grad_scale),
+               pack_h2(z[4] * grad_scale, z[5] * grad_scale),
+               pack_h2(z[6] * grad_scale, z[7] * grad_scale)};
+}
+
+__device__ __forceinline__ void grad_scalar(uint16_t* base, int64_t col, int64_t tgt,
+                                            float shift, float grad_scale) {
+  const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(h2f(base[col]), kLog2e, shift));
+  const float g = (col == tgt ? p - 1.0f : p) * grad_scale;
+  base[col] = static_cast<uint16_t>(pack_h2(g, 0.f) & 0xffffu);
+}
+
+// ---- register-resident form ------------------------------------------------------------------
+template <int CPT>
+__global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
+    uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
+    float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
+    float* __restrict__ lse_out, float grad_scale, int64_t V) {
+  __shared__ RowStats part[kHeadWaves];
+  __shared__ float row_lse;
+  const int64_t row = blockIdx.x;
+  uint16_t* base = logits + row * V;
+  const int64_t tgt = target[row];
+  const bool labelled = tgt != kIgnoreIndex;
+  const bool tgt_ok = tgt >= 0 && tgt < V;
+  const int tid = threadIdx.x;
+  const RowSpan sp = row_span(base, V);
+  // The row's whole chunks as one range-checked buffer: every load is issued unconditionally
+  // (chunks past the row read as 0), and each chunk needs only a 32-bit offset register.
+  const __amdgpu_buffer_rsrc_t rsrc =
+      buffer_rsrc(base + sp.lead, static_cast<uint32_t>(sp.nvec * 16));
+  u32x4 w[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (k * kHeadThreads + tid) * 16, 0, 0);
+  float zlead = 0.f, ztail = 0.f;
+  const bool has_lead = tid < sp.lead, has_tail = sp.tail0 + tid < V;
+  if (has_lead) zlead = h2f(base[tid]);
+  if (has_tail) ztail = h2f(base[sp.tail0 + tid]);
+
+  // 32-bit chunk indices (a row has < 2^28 chunks): 64-bit ones would cost a register pair
+  // per chunk on top of the row.
+  const int32_t nvec = static_cast<int32_t>(sp.nvec), lead = static_cast<int32_t>(sp.lead);
+  RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
+  if (has_lead) absorb<1>(st, &zlead, tid);
+  // The scheduling fences keep one chunk's temporaries live at a time: the whole row already
+  // occupies 4*CPT VGPRs, and latency is hidden by the other 15 waves of the workgroup.
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int32_t c = k * kHeadThreads + tid;
+    if (c < nvec) absorb_chunk(st, w[k], lead + 8 * c);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (has_tail) absorb<1>(st, &ztail, static_cast<int32_t>(sp.tail0 + tid));
+
+  const float lse = finish_row(st, part, &row_lse, base, row, tgt, labelled, tgt_ok, entropy,
+                               loss, correct, lse_out);
+  if (!labelled) return;
+  const float shift = -lse * kLog2e;
+  const int32_t tc =
+      (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? static_cast<int32_t>((tgt - sp.lead) >> 3)
+                                                   : -1;
+  const int thit = static_cast<int>((tgt - sp.lead) & 7);
+  if (has_lead) grad_scalar(base, tid, tgt, shift, grad_scale);
+  // Store offsets are recomputed from an opaque copy of tid*16 (one add per chunk) rather than
+  // kept live from the load phase: CPT offset registers on top of the row would spill.
+  uint32_t lane_off = static_cast<uint32_t>(tid) * 16;
+  asm volatile("" : "+v"(lane_off));
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int32_t c = k * kHeadThreads + tid;
+    if (c < nvec)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          grad_chunk(w[k], shift, grad_scale, c == tc ? thit : -1), rsrc,
+          lane_off + k * kHeadThreads * 16, 0, kAuxNonTemporal);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (has_tail) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
+}
+
+// ---- streaming form (two reads of the row) -----------------------------------------------------
+__global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
+    uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
+    float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
+    float* __restrict__ lse_out, float grad_scale, int64_t V) {
+  __shared__ RowStats part[kHeadWaves];
+  __shared__ float row_lse;
+  const int64_t row = blockIdx.x;
+  uint16_t* base = logits + row * V;
+  const int64_t tgt = target[row];
+  const bool labelled = tgt != kIgnoreIndex;
+  const bool tgt_ok = tgt >= 0 && tgt < V;
+  const int tid = threadIdx.x;
+  const RowSpan sp = row_span(base, V);
+  u32x4* vb = reinterpret_cast<u32x4*>(base + sp.lead);
+  constexpr int64_t kStep = static_cast<int64_t>(kHeadThreads) * kStreamUnroll;
+
+  RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
+  if (tid < sp.lead) {
+    const float z = h2f(base[tid]);
+    absorb<1>(st, &z, tid);
+  }
+  for (int64_t s0 = 0; s0 < sp.nvec; s0 += kStep) {
+    u32x4 w[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
       const int64_t c = s0 + u * kHeadThreads + tid;
-      if (c < nvec) w[u] = vw[c];
+      w[u] = vb[c < sp.nvec ? c : sp.nvec - 1];
     }
 #pragma unroll
-    for (int u = 0; u < kHeadUnroll; ++u) {
+    for (int u = 0; u < kStreamUnroll; ++u) {
       const int64_t c = s0 + u * kHeadThreads + tid;
-      if (c < nvec) {
-        float z[8];
-        unpack8(w[u], z);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) z[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[j], kLog2e, shift));
-        if (c == tchunk) {
-          const int jj = static_cast<int>((tgt - lead) & 7);
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (j == jj) z[j] = z[j] - 1.0f;
-        }
-        u32x4 o;
-        o.x = pack_h2(z[0] * grad_scale, z[1] * grad_scale);
-        o.y = pack_h2(z[2] * grad_scale, z[3] * grad_scale);
-        o.z = pack_h2(z[4] * grad_scale, z[5] * grad_scale);
-        o.w = pack_h2(z[6] * grad_scale, z[7] * grad_scale);
-        __builtin_nontemporal_store(o, vw + c);
-      }
+      if (c < sp.nvec) absorb_chunk(st, w[u], static_cast<int32_t>(sp.lead + 8 * c));
     }
   }
-  if (tail0 + tid < V) grad1(tail0 + tid);
+  if (sp.tail0 + tid < V) {
+    const float z = h2f(base[sp.tail0 + tid]);
+    absorb<1>(st, &z, static_cast<int32_t>(sp.tail0 + tid));
+  }
+  const float lse = finish_row(st, part, &row_lse, base, row, tgt, labelled, tgt_ok, entropy,
+                               loss, correct, lse_out);
+  if (!labelled) return;
+  const float shift = -lse * kLog2e;
+  const int64_t tc = (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? (tgt - sp.lead) >> 3 : -1;
+  const int thit = static_cast<int>((tgt - sp.lead) & 7);
+  if (tid < sp.lead) grad_scalar(base, tid, tgt, shift, grad_scale);
+  for (int64_t s0 = 0; s0 < sp.nvec; s0 += kStep) {
+    u32x4 w[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      const int64_t c = s0 + u * kHeadThreads + tid;
+      w[u] = vb[c < sp.nvec ? c : sp.nvec - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      const int64_t c = s0 + u * kHeadThreads + tid;
+      if (c < sp.nvec)
+        __builtin_nontemporal_store(grad_chunk(w[u], shift, grad_scale, c == tc ? thit : -1),
+                                    vb + c);
+    }
+  }
+  if (sp.tail0 + tid < V) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
 }
 
 }  // namespace
@@ -216,8 +340,23 @@ extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
   if (rows > 0x7fffffff) return kInvalid;
   if (!logits || !target || !entropy || !loss || !correct) return kInvalid;
   if (reinterpret_cast<uintptr_t>(logits) & 1u) return kInvalid;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  head_stats_grad_kernel<<<static_cast<unsigned>(rows), kHeadThreads, 0, st>>>(
-      logits, target, entropy, loss, correct, lse_out, grad_scale, V);
-  return launch_status();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows)), block(kHeadThreads);
+  // Whole 16-byte chunks per thread: at most V/8 chunks per row over 1024 threads.
+  const int64_t cpt = (V / 8 + kHeadThreads - 1) / kHeadThreads;
+  auto run = [&](auto tag) {
+    constexpr int C = decltype(tag)::value;
+    return launch_kernel(head_stats_grad_kernel<C>, grid, block, s, logits, target, entropy,
+                         loss, correct, lse_out, grad_scale, V);
+  };
+  if (cpt <= 1) return run(std::integral_constant<int, 1>{});
+  if (cpt <= 2) return run(std::integral_constant<int, 2>{});
+  if (cpt <= 4) return run(std::integral_constant<int, 4>{});
+  if (cpt <= 8) return run(std::integral_constant<int, 8>{});
+  if (cpt <= 12) return run(std::integral_constant<int, 12>{});
+  if (cpt <= 16) return run(std::integral_constant<int, 16>{});
+  if (cpt <= 19) return run(std::integral_constant<int, 19>{});
+  if (cpt <= kMaxCpt) return run(std::integral_constant<int, kMaxCpt>{});
+  return launch_kernel(head_stats_grad_stream_kernel, grid, block, s, logits, target, entropy,
+                       loss, correct, lse_out, grad_scale, V);
 }

@@ -5,17 +5,17 @@
 // solution/nf4.py:8-9 with each product and sum rounded on its own (solution/nf4.py:84).
 //
 // Layout and mapping (gfx950):
-//   * one thread handles one 16-byte chunk of packed codes per step = 32 weights = 64 bytes of
-//     fp16 output (four 16-byte stores); a workgroup step covers 256 consecutive chunks, so each
-//     load instruction of a wave reads 1 KiB of contiguous HBM;
-//   * a 16-byte chunk never straddles an absmax block when qblock is a multiple of 32 (every
-//     bitsandbytes block size), so each chunk needs one scale: code2[absmax_u8[b]] *
-//     absmax2[b >> log2(qblock2)] + offset, three cache-resident loads per 32 weights;
+//   * the unit of work is one packed dword (4 bytes = 8 codes) -> one 16-byte fp16 store; lane l
+//     of a wavefront takes dword l, l+64, ... of the wave's slice, so every load instruction of
+//     a wave reads 256 contiguous bytes and every store instruction writes 1 KiB contiguous;
+//   * a workgroup tile is 256 threads x kNf4Dwords dwords; the block scales of the tile
+//     (code2[absmax_u8[b]] * absmax2[b >> log2(qblock2)] + offset, the double-quantised absmax)
+//     are computed once per block by the first threads into LDS, instead of once per lane;
 //   * the 16-entry NF4 codebook is expanded in LDS into a 256-entry table of (high, low) nibble
 //     value pairs, so one ds_read_b64 per packed byte yields both codes' fp32 values;
-//   * grid-stride over steps with a grid sized to the device's compute units.
-// Other layouts (qblock or qblock2 not a power of two, unaligned pointers) take a one-byte-per-
-// thread kernel with the same arithmetic.
+//   * one tile per workgroup (3,360 workgroups for a [17920, 1536] weight).
+// Other layouts (qblock or qblock2 not a power of two, qblock < 8, unaligned pointers) take a
+// one-byte-per-thread kernel with the same arithmetic, which also handles the last n_bytes % 4.
 
 #include "soupk_common.hpp"
 
@@ -23,65 +23,62 @@ namespace soupk {
 namespace {
 
 constexpr int kNf4Threads = 256;
-constexpr int kNf4Unroll = 4;  // chunks per thread per grid-stride step (loads issued together)
-
-__device__ __forceinline__ uint32_t nf4_pair_word(uint32_t byte, float scale,
-                                                  const float2* __restrict__ pair) {
-  const float2 t = pair[byte];
-  return pack_h2(t.x * scale, t.y * scale);
-}
+constexpr int kNf4Dwords = 4;                                // dwords per thread per tile
+constexpr int kNf4TileDwords = kNf4Threads * kNf4Dwords;     // 4 KiB of packed codes
 
 // 4 packed bytes (lowest address first) -> 8 fp16 weights (high nibble first within a byte).
 __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
                                                   const float2* __restrict__ pair) {
-  u32x4 r;
-  r.x = nf4_pair_word(w & 0xffu, scale, pair);
-  r.y = nf4_pair_word((w >> 8) & 0xffu, scale, pair);
-  r.z = nf4_pair_word((w >> 16) & 0xffu, scale, pair);
-  r.w = nf4_pair_word(w >> 24, scale, pair);
-  return r;
+  const float2 t0 = pair[w & 0xffu];
+  const float2 t1 = pair[(w >> 8) & 0xffu];
+  const float2 t2 = pair[(w >> 16) & 0xffu];
+  const float2 t3 = pair[w >> 24];
+  return u32x4{pack_h2(t0.x * scale, t0.y * scale), pack_h2(t1.x * scale, t1.y * scale),
+               pack_h2(t2.x * scale, t2.y * scale), pack_h2(t3.x * scale, t3.y * scale)};
 }
 
+// dword_block_shift = log2(dwords per absmax block) = log2(qblock / 8); block2_shift =
+// log2(qblock2).  Requires qblock a power of two in [8, 8192] (a dword never straddles two
+// blocks, and a tile spans whole blocks).  One tile per workgroup; the packed loads are issued
+// unconditionally (indices past the end clamped to the last dword, results dropped), because a
+// predicated load makes the compiler wait on it before issuing the next.
 __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
-    const u32x4* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
+    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
     const float* __restrict__ code2, const float* __restrict__ absmax2,
     const float* __restrict__ offset, const float* __restrict__ nf4, u32x4* __restrict__ out,
-    int64_t n_chunks, int chunk_block_shift, int block2_shift) {
+    int64_t n_dwords, int64_t n_blocks, int dword_block_shift, int block2_shift) {
   __shared__ float2 pair[256];
+  __shared__ float scale[kNf4TileDwords];  // enough for qblock >= 8 (1 block per dword)
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kNf4TileDwords;
+  uint32_t w[kNf4Dwords];
+#pragma unroll
+  for (int k = 0; k < kNf4Dwords; ++k) {
+    const int64_t d = d0 + k * kNf4Threads + threadIdx.x;
+    w[k] = __builtin_nontemporal_load(packed + (d < n_dwords ? d : n_dwords - 1));
+  }
   pair[threadIdx.x] = make_float2(nf4[threadIdx.x >> 4], nf4[threadIdx.x & 15]);
-  __syncthreads();
   const float off = offset[0];
-  const int64_t step_chunks = static_cast<int64_t>(kNf4Threads) * kNf4Unroll;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * step_chunks; base < n_chunks;
-       base += static_cast<int64_t>(gridDim.x) * step_chunks) {
-    u32x4 v[kNf4Unroll];
-    float prod[kNf4Unroll];
-#pragma unroll
-    for (int u = 0; u < kNf4Unroll; ++u) {
-      const int64_t c = base + u * kNf4Threads + threadIdx.x;
-      if (c < n_chunks) {
-        v[u] = __builtin_nontemporal_load(packed + c);
-        const int64_t blk = c >> chunk_block_shift;
-        prod[u] = code2[absmax_u8[blk]] * absmax2[blk >> block2_shift];
-      }
+  const int tile_blocks = kNf4TileDwords >> dword_block_shift;
+  const int64_t b0 = d0 >> dword_block_shift;
+  for (int i = threadIdx.x; i < tile_blocks; i += kNf4Threads) {
+    const int64_t b = b0 + i;
+    if (b < n_blocks) {
+      const float prod = code2[absmax_u8[b]] * absmax2[b >> block2_shift];
+      scale[i] = prod + off;
     }
+  }
+  __syncthreads();
 #pragma unroll
-    for (int u = 0; u < kNf4Unroll; ++u) {
-      const int64_t c = base + u * kNf4Threads + threadIdx.x;
-      if (c < n_chunks) {
-        const float scale = prod[u] + off;
-        u32x4* dst = out + 4 * c;
-        dst[0] = nf4_expand_dword(v[u].x, scale, pair);
-        dst[1] = nf4_expand_dword(v[u].y, scale, pair);
-        dst[2] = nf4_expand_dword(v[u].z, scale, pair);
-        dst[3] = nf4_expand_dword(v[u].w, scale, pair);
-      }
-    }
+  for (int k = 0; k < kNf4Dwords; ++k) {
+    const int64_t d = d0 + k * kNf4Threads + threadIdx.x;
+    const float s = scale[(k * kNf4Threads + threadIdx.x) >> dword_block_shift];
+    const u32x4 v = nf4_expand_dword(w[k], s, pair);
+    if (d < n_dwords) __builtin_nontemporal_store(v, out + d);
   }
 }
 
 // One packed byte per thread; any even qblock, any qblock2, any alignment.  Also used for the
-// bytes after the last whole 16-byte chunk of the vector kernel.
+// bytes after the last whole dword of the vector kernel.
 __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_byte_kernel(
     const uint8_t* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
     const float* __restrict__ code2, const float* __restrict__ absmax2,
@@ -104,7 +101,9 @@ inline int log2_exact(int64_t v) {
   while ((int64_t{1} << s) < v) ++s;
   return s;
 }
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
 
 }  // namespace
 }  // namespace soupk
@@ -120,21 +119,21 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack(
   if (!packed || !absmax_u8 || !code2 || !absmax2 || !offset || !nf4 || !out_f16) return kInvalid;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t bytes_per_block = qblock / 2;
+  const int64_t n_blocks = (n_bytes + bytes_per_block - 1) / bytes_per_block;
   int64_t vec_bytes = 0;
-  if (qblock % 32 == 0 && is_pow2(qblock) && is_pow2(qblock2) && aligned16(packed) &&
-      aligned16(out_f16)) {
-    const int64_t n_chunks = n_bytes / 16;
-    vec_bytes = n_chunks * 16;
-    if (n_chunks > 0) {
-      const int64_t step_chunks = static_cast<int64_t>(kNf4Threads) * kNf4Unroll;
-      const int64_t steps = (n_chunks + step_chunks - 1) / step_chunks;
-      const int64_t cap = static_cast<int64_t>(device_cu_count()) * 8;
-      const int grid = static_cast<int>(steps < cap ? steps : cap);
-      nf4_unpack_vec_kernel<<<grid, kNf4Threads, 0, s>>>(
-          reinterpret_cast<const u32x4*>(packed), absmax_u8, code2, absmax2, offset, nf4,
-          reinterpret_cast<u32x4*>(out_f16), n_chunks, log2_exact(qblock / 32),
+  // (qblock <= 8192: a tile of 1024 dwords spans whole absmax blocks)
+  if (qblock >= 8 && qblock <= 8192 && is_pow2(qblock) && is_pow2(qblock2) &&
+      aligned(packed, 4) && aligned(out_f16, 16)) {
+    const int64_t n_dwords = n_bytes / 4;
+    vec_bytes = n_dwords * 4;
+    if (n_dwords > 0) {
+      const int64_t tiles = (n_dwords + kNf4TileDwords - 1) / kNf4TileDwords;
+      if (tiles > 0x7fffffff) return kInvalid;
+      const int st = launch_kernel(
+          nf4_unpack_vec_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kNf4Threads), s,
+          reinterpret_cast<const uint32_t*>(packed), absmax_u8, code2, absmax2, offset, nf4,
+          reinterpret_cast<u32x4*>(out_f16), n_dwords, n_blocks, log2_exact(qblock / 8),
           log2_exact(qblock2));
-      const int st = launch_status();
       if (st != kOk) return st;
     }
   }
@@ -142,10 +141,10 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack(
   if (rest > 0) {
     const int64_t grid = (rest + kNf4Threads - 1) / kNf4Threads;
     if (grid > 0x7fffffff) return kInvalid;
-    nf4_unpack_byte_kernel<<<static_cast<int>(grid), kNf4Threads, 0, s>>>(
-        packed, absmax_u8, code2, absmax2, offset, nf4, out_f16, vec_bytes, n_bytes,
-        bytes_per_block, qblock2);
-    return launch_status();
+    return launch_kernel(nf4_unpack_byte_kernel, dim3(static_cast<unsigned>(grid)),
+                         dim3(kNf4Threads), s, packed, absmax_u8, code2, absmax2, offset, nf4,
+                         out_f16, vec_bytes, n_bytes, bytes_per_block,
+                         static_cast<int64_t>(qblock2));
   }
   return kOk;
 }

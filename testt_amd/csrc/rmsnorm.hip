@@ -291,10 +291,8 @@ struct FwdLaunch {
                  float* s_out, uint16_t* y, float* ypad, const int64_t* pad_idx,
                  const int32_t* pad_inv, float* rstd, int64_t rows, int64_t pad_rows, int H,
                  float eps, int64_t row_blocks) {
-    rmsnorm_fwd_kernel<CPL><<<grid, kNormThreads, 0, st>>>(x, delta, w, s_out, y, ypad, pad_idx,
-                                                           pad_inv, rstd, rows, pad_rows, H, eps,
-                                                           row_blocks);
-    return launch_status();
+    return launch_kernel(rmsnorm_fwd_kernel<CPL>, grid, dim3(kNormThreads), st, x, delta, w, s_out,
+                         y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows, H, eps, row_blocks);
   }
 };
 
@@ -303,9 +301,8 @@ struct BwdLaunch {
   static int run(dim3 grid, hipStream_t st, const float* s, const float* rstd, const float* w,
                  const uint16_t* dy, const float* dypad, const int64_t* pad_idx, const float* ds,
                  float* dx, uint16_t* ddelta, int64_t rows, int64_t pad_rows, int H) {
-    rmsnorm_bwd_kernel<CPL><<<grid, kNormThreads, 0, st>>>(s, rstd, w, dy, dypad, pad_idx, ds,
-                                                           dx, ddelta, rows, pad_rows, H);
-    return launch_status();
+    return launch_kernel(rmsnorm_bwd_kernel<CPL>, grid, dim3(kNormThreads), st, s, rstd, w, dy,
+                         dypad, pad_idx, ds, dx, ddelta, rows, pad_rows, H);
   }
 };
 
@@ -319,12 +316,15 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_fwd(
     float* ypad, const int64_t* pad_idx, const int32_t* pad_inv, float* rstd, int64_t rows,
     int64_t pad_rows, int32_t H, float eps, void* stream) {
   if (rows < 0 || H <= 0 || pad_rows < 0) return kInvalid;
-  if ((delta == nullptr) != (s_out == nullptr)) return kInvalid;
-  if ((ypad == nullptr) != (pad_idx == nullptr)) return kInvalid;
-  if (pad_inv != nullptr && ypad == nullptr) return kInvalid;
   const int64_t zero_rows = pad_inv != nullptr ? pad_rows : 0;
   if (rows == 0 && zero_rows == 0) return kOk;
-  if (!x || !w || !y || !rstd) return kInvalid;
+  if (zero_rows > 0 && ypad == nullptr) return kInvalid;
+  if (rows > 0) {
+    // (An empty tensor's data pointer may be null, so the pairings are checked only with rows.)
+    if (!x || !w || !y || !rstd) return kInvalid;
+    if ((delta == nullptr) != (s_out == nullptr)) return kInvalid;
+    if ((ypad == nullptr) != (pad_idx == nullptr)) return kInvalid;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int cpl = (H / 4 + kWave - 1) / kWave;
   const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(x, 16) && aligned(w, 16) &&
@@ -339,9 +339,9 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_fwd(
   }
   const int64_t blocks = rows + zero_rows;
   if (blocks > 0x7fffffff) return kInvalid;
-  rmsnorm_fwd_generic_kernel<<<static_cast<unsigned>(blocks), kGenThreads, 0, st>>>(
-      x, delta, w, s_out, y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows, H, eps);
-  return launch_status();
+  return launch_kernel(rmsnorm_fwd_generic_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kGenThreads), st, x, delta, w, s_out, y, ypad, pad_idx, pad_inv, rstd,
+                       rows, pad_rows, H, eps);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_bwd(
@@ -365,7 +365,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_bwd(
                                static_cast<int>(H));
   }
   if (rows > 0x7fffffff) return kInvalid;
-  rmsnorm_bwd_generic_kernel<<<static_cast<unsigned>(rows), kGenThreads, 0, st>>>(
-      s, rstd, w, dy, dypad, pad_idx, ds, dx, ddelta, rows, pad_rows, H);
-  return launch_status();
+  return launch_kernel(rmsnorm_bwd_generic_kernel, dim3(static_cast<unsigned>(rows)),
+                       dim3(kGenThreads), st, s, rstd, w, dy, dypad, pad_idx, ds, dx, ddelta, rows,
+                       pad_rows, H);
 }

@@ -345,20 +345,20 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
     if (tok_items + zero_items >= (int64_t{1} << 31)) return kInvalid;
     const int64_t tok_blocks = (tok_items + kRopeThreads - 1) / kRopeThreads;
     const int64_t blocks = tok_blocks + (zero_items + kRopeThreads - 1) / kRopeThreads;
-    rope_pack_fwd_kernel<64><<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
-        qkv, lora_q, lora_v, lora_dtype == SOUPK_DTYPE_F32, cos, sin, pos, pos_inv, q, k, v, rows,
-        dm, tok_blocks);
-    return launch_status();
+    return launch_kernel(rope_pack_fwd_kernel<64>, dim3(static_cast<unsigned>(blocks)),
+                         dim3(kRopeThreads), st, qkv, lora_q, lora_v,
+                         static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos, pos_inv,
+                         q, k, v, rows, dm, tok_blocks);
   }
   const int64_t per = static_cast<int64_t>(heads) * half;
   const int64_t tok_items = rows * per;
   const int64_t total = tok_items + zero_slots * per;
   const int64_t blocks = (total + kRopeThreads - 1) / kRopeThreads;
   if (blocks > 0x7fffffff) return kInvalid;
-  rope_pack_fwd_generic_kernel<<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
-      qkv, lora_q, lora_v, lora_dtype == SOUPK_DTYPE_F32, cos, sin, pos, pos_inv, q, k, v, rows, B,
-      T, NH, NKV, D, tok_items);
-  return launch_status();
+  return launch_kernel(rope_pack_fwd_generic_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kRopeThreads), st, qkv, lora_q, lora_v,
+                       static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos, pos_inv, q,
+                       k, v, rows, B, T, NH, NKV, D, tok_items);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
@@ -380,15 +380,14 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
     dm.per_tok = FastDiv(dm.items);
     const int64_t items = rows * dm.items;
     if (items >= (int64_t{1} << 31)) return kInvalid;
-    rope_pack_bwd_kernel<64>
-        <<<static_cast<unsigned>((items + kRopeThreads - 1) / kRopeThreads), kRopeThreads, 0,
-           st>>>(dq, dk, dv, cos, sin, pos, dqkv, rows, dm);
-    return launch_status();
+    return launch_kernel(rope_pack_bwd_kernel<64>,
+                         dim3(static_cast<unsigned>((items + kRopeThreads - 1) / kRopeThreads)),
+                         dim3(kRopeThreads), st, dq, dk, dv, cos, sin, pos, dqkv, rows, dm);
   }
   const int64_t total = rows * heads * half;
   const int64_t blocks = (total + kRopeThreads - 1) / kRopeThreads;
   if (blocks > 0x7fffffff) return kInvalid;
-  rope_pack_bwd_generic_kernel<<<static_cast<unsigned>(blocks), kRopeThreads, 0, st>>>(
-      dq, dk, dv, cos, sin, pos, dqkv, rows, B, T, NH, NKV, D);
-  return launch_status();
+  return launch_kernel(rope_pack_bwd_generic_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kRopeThreads), st, dq, dk, dv, cos, sin, pos, dqkv, rows, B, T, NH,
+                       NKV, D);
 }

@@ -2,6 +2,7 @@
 // memory accesses, fp32 arithmetic with round-to-nearest-even fp16 stores.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -32,17 +33,56 @@ inline int launch_status() { return static_cast<int>(hipGetLastError()); }
 // Number of compute units of the current device (256 on MI355X), cached per device ordinal.
 int device_cu_count();
 
+// Events set by soupk_time_next_launch() on the calling thread, handed to (and cleared by) the
+// next kernel launch of that thread.
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel launch of the library goes through here: a plain launch, or, when the calling
+// thread armed soupk_time_next_launch(), a launch whose dispatch itself records the two events
+// (hipExtLaunchKernelGGL), so they time the kernel and nothing else.
+template <typename... KArgs, typename... Args>
+int launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
+                  Args... args) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  take_timing_events(&start, &stop);
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0,
+                          static_cast<KArgs>(args)...);
+  else
+    kernel<<<grid, block, 0, stream>>>(static_cast<KArgs>(args)...);
+  return launch_status();
+}
+
 // ---- fp16 <-> fp32 ---------------------------------------------------------------------------
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits16)));
 }
+// One dword as two fp16.  Always pass a scalar: hipcc (clang 22) lowers
+// __builtin_bit_cast(f16x2, v.y) of an ext-vector element as a read of element 0.
+__device__ __forceinline__ f16x2 as_h2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
 __device__ __forceinline__ float lo_h(uint32_t w) { return h2f(w & 0xffffu); }
 __device__ __forceinline__ float hi_h(uint32_t w) { return h2f(w >> 16); }
 // Two fp32 -> one dword of two fp16 (round to nearest even), `a` at the lower address.
+// The empty asm makes a and b opaque fp32 values: without it the compiler may fuse the multiply
+// that produced them with the conversion into v_fma_mix*_f16, which rounds the exact product
+// once to fp16 instead of rounding to fp32 first (as the eager path and the reference do); the
+// two differ when the fp32 value lands on an fp16 rounding tie.
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  asm("" : "+v"(a), "+v"(b));
   f16x2 v = {static_cast<f16>(a), static_cast<f16>(b)};
   return __builtin_bit_cast(uint32_t, v);
 }
+
+// ---- buffer (MUBUF) access with hardware range checking ----------------------------------------
+// A raw buffer descriptor over [base, base + bytes): loads at offsets >= bytes return 0 and
+// stores there are dropped, so a kernel can issue whole-wave accesses past the end of a row
+// without a predicate (which would make the compiler wait on every load) and without a fault.
+// Word 3 (0x00020000) is the gfx9-family format word for raw 32-bit-addressed buffers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+constexpr int kAuxNonTemporal = 2;  // cache-policy bits of buffer ops: streaming (nt)
 
 // ---- wave64 reductions (butterfly: every lane ends with the result) -------------------------
 __device__ __forceinline__ float wave_sum(float v) {

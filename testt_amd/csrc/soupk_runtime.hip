@@ -10,7 +10,15 @@ namespace soupk {
 namespace {
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];  // 0 = not queried yet (zero-initialised static)
+thread_local hipEvent_t t_timing_start = nullptr;
+thread_local hipEvent_t t_timing_stop = nullptr;
 }  // namespace
+
+void take_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  *start = t_timing_start;
+  *stop = t_timing_stop;
+  t_timing_start = t_timing_stop = nullptr;
+}
 
 int device_cu_count() {
   int dev = 0;
@@ -70,6 +78,13 @@ extern "C" __attribute__((visibility("default"))) const char* soupk_status_strin
   return hipGetErrorString(static_cast<hipError_t>(status));
 }
 
+extern "C" __attribute__((visibility("default"))) int soupk_time_next_launch(void* start_event,
+                                                                              void* stop_event) {
+  t_timing_start = static_cast<hipEvent_t>(start_event);
+  t_timing_stop = static_cast<hipEvent_t>(stop_event);
+  return kOk;
+}
+
 extern "C" __attribute__((visibility("default"))) int soupk_index_inverse(
     const int64_t* idx, int64_t n, int32_t* inv, int64_t n_slots, void* stream) {
   if (n < 0 || n_slots < 0 || n > 0x7fffffff) return kInvalid;
@@ -77,14 +92,14 @@ extern "C" __attribute__((visibility("default"))) int soupk_index_inverse(
   if (!inv || (n > 0 && !idx)) return kInvalid;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (n_slots <= (int64_t{1} << 16) && n <= (int64_t{1} << 16)) {
-    index_inverse_small_kernel<<<1, kInvThreads, 0, s>>>(idx, n, inv, n_slots);
-    return launch_status();
+    return launch_kernel(index_inverse_small_kernel, dim3(1), dim3(kInvThreads), s, idx, n, inv,
+                         n_slots);
   }
   const int64_t g1 = (n_slots + 255) / 256;
   if (g1 > 0x7fffffff) return kInvalid;
-  fill_i32_kernel<<<static_cast<int>(g1), 256, 0, s>>>(inv, n_slots, -1);
-  int st = launch_status();
+  int st = launch_kernel(fill_i32_kernel, dim3(static_cast<unsigned>(g1)), dim3(256), s, inv,
+                         n_slots, -1);
   if (st != kOk || n == 0) return st;
-  scatter_rank_kernel<<<static_cast<int>((n + 255) / 256), 256, 0, s>>>(idx, n, inv, n_slots);
-  return launch_status();
+  return launch_kernel(scatter_rank_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
+                       dim3(256), s, idx, n, inv, n_slots);
 }

@@ -7,8 +7,8 @@
 // Pure HBM streaming.  The flat index space is rows * I/8 chunks of 8 fp16 (16 bytes); chunk c
 // lives in row r = c / (I/8), and because act is [rows, I] contiguous its chunk offset is 8c,
 // while gate sits at 8c + r*I and up at 8c + r*I + I of the [rows, 2I] buffer.  Each thread
-// issues all loads of kSwiUnroll chunks before any arithmetic so that every wave keeps several
-// KiB in flight.  Arithmetic is fp32: exp through v_exp_f32, the reciprocal through v_rcp_f32
+// issues all loads of its kSwiUnroll chunks back to back before any arithmetic, so every wave
+// keeps 8-12 KiB in flight.  Arithmetic is fp32: exp through v_exp_f32, the reciprocal through v_rcp_f32
 // (both about 1 ulp of fp32, far below the fp16 rounding of the result).
 
 #include "fastdiv.hpp"
@@ -18,7 +18,7 @@ namespace soupk {
 namespace {
 
 constexpr int kSwiThreads = 256;
-constexpr int kSwiUnroll = 2;
+constexpr int kSwiUnroll = 4;  // 16-byte chunks per thread (one workgroup tile: 16 KiB of act)
 
 __device__ __forceinline__ float sigmoid_f(float g) {
   return __builtin_amdgcn_rcpf(1.0f + fast_exp(-g));
@@ -46,67 +46,56 @@ __device__ __forceinline__ u32x2 silu_bwd_word(uint32_t dw, uint32_t gw, uint32_
   return u32x2{pack_h2(dg[0], dg[1]), pack_h2(du[0], du[1])};
 }
 
+// One workgroup = one tile of kSwiThreads * kSwiUnroll chunks; chunk k*kSwiThreads + tid of the
+// tile per thread, so each wave load/store instruction covers 1 KiB contiguous.  All loads are
+// issued unconditionally (indices past the end are clamped to the last chunk and their results
+// dropped): a predicated load would make the compiler wait on it before issuing the next.
 __global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec_kernel(
     const u32x4* __restrict__ gu, u32x4* __restrict__ act, uint32_t n_chunks, FastDiv row_of,
     uint32_t I_chunks) {
-  const uint32_t step = kSwiThreads * kSwiUnroll;
-  for (uint32_t base = blockIdx.x * step; base < n_chunks; base += gridDim.x * step) {
-    u32x4 g[kSwiUnroll], u[kSwiUnroll];
+  const uint32_t base = blockIdx.x * (kSwiThreads * kSwiUnroll) + threadIdx.x;
+  u32x4 g[kSwiUnroll], u[kSwiUnroll];
 #pragma unroll
-    for (int k = 0; k < kSwiUnroll; ++k) {
-      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
-      if (c < n_chunks) {
-        const uint64_t gi = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) *
-                                                           I_chunks;
-        g[k] = __builtin_nontemporal_load(gu + gi);
-        u[k] = __builtin_nontemporal_load(gu + gi + I_chunks);
-      }
-    }
+  for (int k = 0; k < kSwiUnroll; ++k) {
+    const uint32_t c = min(base + k * kSwiThreads, n_chunks - 1);
+    const uint64_t gi = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) *
+                                                       I_chunks;
+    g[k] = __builtin_nontemporal_load(gu + gi);
+    u[k] = __builtin_nontemporal_load(gu + gi + I_chunks);
+  }
 #pragma unroll
-    for (int k = 0; k < kSwiUnroll; ++k) {
-      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
-      if (c < n_chunks) {
-        u32x4 r;
-        r.x = silu_mul_word(g[k].x, u[k].x);
-        r.y = silu_mul_word(g[k].y, u[k].y);
-        r.z = silu_mul_word(g[k].z, u[k].z);
-        r.w = silu_mul_word(g[k].w, u[k].w);
-        __builtin_nontemporal_store(r, act + c);
-      }
-    }
+  for (int k = 0; k < kSwiUnroll; ++k) {
+    const uint32_t c = base + k * kSwiThreads;
+    const u32x4 r = {silu_mul_word(g[k].x, u[k].x), silu_mul_word(g[k].y, u[k].y),
+                     silu_mul_word(g[k].z, u[k].z), silu_mul_word(g[k].w, u[k].w)};
+    if (c < n_chunks) __builtin_nontemporal_store(r, act + c);
   }
 }
 
 __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec_kernel(
     const u32x4* __restrict__ dact, u32x4* __restrict__ gu, uint32_t n_chunks, FastDiv row_of,
     uint32_t I_chunks) {
-  const uint32_t step = kSwiThreads * kSwiUnroll;
-  for (uint32_t base = blockIdx.x * step; base < n_chunks; base += gridDim.x * step) {
-    u32x4 d[kSwiUnroll], g[kSwiUnroll], u[kSwiUnroll];
-    uint64_t gi[kSwiUnroll];
+  const uint32_t base = blockIdx.x * (kSwiThreads * kSwiUnroll) + threadIdx.x;
+  u32x4 d[kSwiUnroll], g[kSwiUnroll], u[kSwiUnroll];
+  uint64_t gi[kSwiUnroll];
 #pragma unroll
-    for (int k = 0; k < kSwiUnroll; ++k) {
-      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
-      gi[k] = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) * I_chunks;
-      if (c < n_chunks) {
-        d[k] = __builtin_nontemporal_load(dact + c);
-        g[k] = __builtin_nontemporal_load(gu + gi[k]);
-        u[k] = __builtin_nontemporal_load(gu + gi[k] + I_chunks);
-      }
-    }
+  for (int k = 0; k < kSwiUnroll; ++k) {
+    const uint32_t c = min(base + k * kSwiThreads, n_chunks - 1);
+    gi[k] = static_cast<uint64_t>(c) + static_cast<uint64_t>(row_of.div(c)) * I_chunks;
+    d[k] = __builtin_nontemporal_load(dact + c);
+    g[k] = __builtin_nontemporal_load(gu + gi[k]);
+    u[k] = __builtin_nontemporal_load(gu + gi[k] + I_chunks);
+  }
 #pragma unroll
-    for (int k = 0; k < kSwiUnroll; ++k) {
-      const uint32_t c = base + k * kSwiThreads + threadIdx.x;
-      if (c < n_chunks) {
-        const u32x2 r0 = silu_bwd_word(d[k].x, g[k].x, u[k].x);
-        const u32x2 r1 = silu_bwd_word(d[k].y, g[k].y, u[k].y);
-        const u32x2 r2 = silu_bwd_word(d[k].z, g[k].z, u[k].z);
-        const u32x2 r3 = silu_bwd_word(d[k].w, g[k].w, u[k].w);
-        const u32x4 dg = {r0.x, r1.x, r2.x, r3.x};
-        const u32x4 du = {r0.y, r1.y, r2.y, r3.y};
-        __builtin_nontemporal_store(dg, gu + gi[k]);
-        __builtin_nontemporal_store(du, gu + gi[k] + I_chunks);
-      }
+  for (int k = 0; k < kSwiUnroll; ++k) {
+    const uint32_t c = base + k * kSwiThreads;
+    const u32x2 r0 = silu_bwd_word(d[k].x, g[k].x, u[k].x);
+    const u32x2 r1 = silu_bwd_word(d[k].y, g[k].y, u[k].y);
+    const u32x2 r2 = silu_bwd_word(d[k].z, g[k].z, u[k].z);
+    const u32x2 r3 = silu_bwd_word(d[k].w, g[k].w, u[k].w);
+    if (c < n_chunks) {
+      __builtin_nontemporal_store(u32x4{r0.x, r1.x, r2.x, r3.x}, gu + gi[k]);
+      __builtin_nontemporal_store(u32x4{r0.y, r1.y, r2.y, r3.y}, gu + gi[k] + I_chunks);
     }
   }
 }
@@ -134,11 +123,9 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_elem_kernel(
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-inline int vec_grid(uint32_t n_chunks) {
-  const int64_t step = static_cast<int64_t>(kSwiThreads) * kSwiUnroll;
-  const int64_t steps = (static_cast<int64_t>(n_chunks) + step - 1) / step;
-  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 8;
-  return static_cast<int>(steps < cap ? steps : cap);
+inline unsigned vec_grid(uint32_t n_chunks) {
+  const uint32_t tile = kSwiThreads * kSwiUnroll;
+  return (n_chunks + tile - 1) / tile;
 }
 
 }  // namespace
@@ -158,15 +145,14 @@ extern "C" __attribute__((visibility("default"))) int soupk_swiglu_fwd(const uin
   if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && aligned16(gu) && aligned16(act)) {
     const uint32_t n_chunks = static_cast<uint32_t>(n / 8);
     const uint32_t I_chunks = static_cast<uint32_t>(I / 8);
-    swiglu_fwd_vec_kernel<<<vec_grid(n_chunks), kSwiThreads, 0, s>>>(
-        reinterpret_cast<const u32x4*>(gu), reinterpret_cast<u32x4*>(act), n_chunks,
-        FastDiv(I_chunks), I_chunks);
-    return launch_status();
+    return launch_kernel(swiglu_fwd_vec_kernel, dim3(vec_grid(n_chunks)), dim3(kSwiThreads), s,
+                         reinterpret_cast<const u32x4*>(gu), reinterpret_cast<u32x4*>(act),
+                         n_chunks, FastDiv(I_chunks), I_chunks);
   }
   const int64_t grid = (n + kSwiThreads - 1) / kSwiThreads;
   if (grid > 0x7fffffff) return kInvalid;
-  swiglu_fwd_elem_kernel<<<static_cast<int>(grid), kSwiThreads, 0, s>>>(gu, act, n, I);
-  return launch_status();
+  return launch_kernel(swiglu_fwd_elem_kernel, dim3(static_cast<unsigned>(grid)),
+                       dim3(kSwiThreads), s, gu, act, n, I);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_swiglu_bwd_inplace(
@@ -179,13 +165,12 @@ extern "C" __attribute__((visibility("default"))) int soupk_swiglu_bwd_inplace(
   if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && aligned16(gu) && aligned16(dact)) {
     const uint32_t n_chunks = static_cast<uint32_t>(n / 8);
     const uint32_t I_chunks = static_cast<uint32_t>(I / 8);
-    swiglu_bwd_vec_kernel<<<vec_grid(n_chunks), kSwiThreads, 0, s>>>(
-        reinterpret_cast<const u32x4*>(dact), reinterpret_cast<u32x4*>(gu), n_chunks,
-        FastDiv(I_chunks), I_chunks);
-    return launch_status();
+    return launch_kernel(swiglu_bwd_vec_kernel, dim3(vec_grid(n_chunks)), dim3(kSwiThreads), s,
+                         reinterpret_cast<const u32x4*>(dact), reinterpret_cast<u32x4*>(gu),
+                         n_chunks, FastDiv(I_chunks), I_chunks);
   }
   const int64_t grid = (n + kSwiThreads - 1) / kSwiThreads;
   if (grid > 0x7fffffff) return kInvalid;
-  swiglu_bwd_elem_kernel<<<static_cast<int>(grid), kSwiThreads, 0, s>>>(dact, gu, n, I);
-  return launch_status();
+  return launch_kernel(swiglu_bwd_elem_kernel, dim3(static_cast<unsigned>(grid)),
+                       dim3(kSwiThreads), s, dact, gu, n, I);
 }
