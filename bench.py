@@ -42,12 +42,12 @@ def log(msg):
 class Case:
     """One kernel at its BASELINE shape: algorithmic bytes and per-input-set launch args."""
 
-    def __init__(self, name, kernel, entry, nbytes, sets, cpu=None):
+    def __init__(self, name, kernel, entry, nbytes, sets, cpu=None, lib=None):
         self.name, self.kernel, self.entry, self.nbytes = name, kernel, entry, nbytes
         self.sets = sets            # list of (tensors kept alive, ctypes args without stream)
         self.cpu = cpu              # cpu(ob) -> callable running the CPU eager path once, given
                                     # the oracle.baseline module (imported by the CPU leg only)
-        self.fn = getattr(_ext.lib(), entry)
+        self.fn = getattr(lib if lib is not None else _ext.lib(), entry)
         self.times = []
 
     def launch(self, i, stream):
@@ -60,7 +60,9 @@ def p(t):
     return t.data_ptr() if t is not None else None
 
 
-def build_cases(dev, n_sets=2):
+def build_cases(dev, n_sets=2, lib=None):
+    """The eight kernels at the step shape; `lib` selects the soupk library (default: the
+    package's)."""
     cases = []
     H, I, NH, NKV, D, B, T = (workloads.HIDDEN, workloads.INTER, workloads.N_HEADS,
                               workloads.N_KV, workloads.HEAD_DIM, workloads.BATCH, workloads.SEQ)
@@ -83,7 +85,7 @@ def build_cases(dev, n_sets=2):
         return lambda: ob.nf4_unpack(w_cpu)
 
     cases.append(Case("nf4_unpack", "nf4_unpack_vec_kernel", "soupk_nf4_unpack", nbytes, sets,
-                      cpu=nf4_cpu))
+                      cpu=nf4_cpu, lib=lib))
 
     # add + RMSNorm forward (delta, pad output) and backward at [2048, 1536]
     fsets, bsets = [], []
@@ -116,10 +118,10 @@ def build_cases(dev, n_sets=2):
 
     cases.append(Case("rmsnorm_fwd", "rmsnorm_fwd_kernel", "soupk_rmsnorm_fwd",
                       16 * row_elems + 4 * H + 4 * M + 8 * M, fsets,
-                      cpu=lambda ob: rms_cpu(ob, False)))
+                      cpu=lambda ob: rms_cpu(ob, False), lib=lib))
     cases.append(Case("rmsnorm_bwd", "rmsnorm_bwd_kernel", "soupk_rmsnorm_bwd",
                       20 * row_elems + 4 * H + 4 * M + 8 * M, bsets,
-                      cpu=lambda ob: rms_cpu(ob, True)))
+                      cpu=lambda ob: rms_cpu(ob, True), lib=lib))
 
     # LoRA-add + RoPE + QKV pack forward / backward at M = 2048 (fp32 LoRA deltas)
     fsets, bsets = [], []
@@ -152,10 +154,10 @@ def build_cases(dev, n_sets=2):
 
     cases.append(Case("rope_pack_fwd", "rope_pack_fwd_kernel", "soupk_rope_pack_fwd",
                       M * W * 2 + M * NH * D * 4 + M * NKV * D * 4 + tab + 8 * M + M * W * 2,
-                      fsets, cpu=lambda ob: rope_cpu(ob, False)))
+                      fsets, cpu=lambda ob: rope_cpu(ob, False), lib=lib))
     cases.append(Case("rope_pack_bwd", "rope_pack_bwd_kernel", "soupk_rope_pack_bwd",
                       M * W * 2 + tab + 8 * M + M * W * 2, bsets,
-                      cpu=lambda ob: rope_cpu(ob, True)))
+                      cpu=lambda ob: rope_cpu(ob, True), lib=lib))
 
     # SwiGLU forward and in-place backward at [2048, 2 x 8960]
     fsets, bsets = [], []
@@ -174,9 +176,11 @@ def build_cases(dev, n_sets=2):
         return lambda: ob.swiglu_fwd(guc)
 
     cases.append(Case("swiglu_fwd", "swiglu_fwd_vec_kernel", "soupk_swiglu_fwd",
-                      M * 2 * I * 2 + M * I * 2, fsets, cpu=lambda ob: swi_cpu(ob, False)))
+                      M * 2 * I * 2 + M * I * 2, fsets, cpu=lambda ob: swi_cpu(ob, False),
+                      lib=lib))
     cases.append(Case("swiglu_bwd", "swiglu_bwd_vec_kernel", "soupk_swiglu_bwd_inplace",
-                      M * I * 2 + 2 * (M * 2 * I * 2), bsets, cpu=lambda ob: swi_cpu(ob, True)))
+                      M * I * 2 + 2 * (M * 2 * I * 2), bsets, cpu=lambda ob: swi_cpu(ob, True),
+                      lib=lib))
 
     # vocab head: one 256-row chunk of logits [256, 151936]
     sets = []
@@ -196,7 +200,8 @@ def build_cases(dev, n_sets=2):
         return lambda: ob.head_stats_grad(zc, tc, 64.0 / 1843.0)
 
     cases.append(Case("head_stats_grad", "head_stats_grad_kernel", "soupk_head_stats_grad",
-                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 12 * rows, sets, cpu=head_cpu))
+                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 12 * rows, sets, cpu=head_cpu,
+                      lib=lib))
     return cases
 
 
@@ -233,12 +238,12 @@ class HipEvents:
         self.events = []
 
 
-def time_gpu(cases, steps, warmup, dev):
+def time_gpu(cases, steps, warmup, dev, lib=None):
     """Per-launch kernel durations: soupk_time_next_launch() makes each launch record a HIP
     event pair with its own dispatch (hipExtLaunchKernelGGL), on the stream it runs on."""
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    arm = _ext.lib().soupk_time_next_launch
+    arm = (lib if lib is not None else _ext.lib()).soupk_time_next_launch
     hip = HipEvents()
     for w in range(warmup):
         for c in cases:

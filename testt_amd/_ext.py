@@ -49,30 +49,35 @@ def library_path():
     return _LIB_PATH
 
 
+def load_library(path):
+    """dlopen a soupk library at `path` and bind every entry point's signature."""
+    if not os.path.exists(path):
+        raise SoupkError(
+            f"{path} is missing: build it with `python -m testt_amd.build_ext` "
+            "(or __graft_entry__.build()) before using the kernels")
+    handle = ctypes.CDLL(path)
+    handle.soupk_abi_version.restype = ctypes.c_int
+    handle.soupk_abi_version.argtypes = []
+    version = handle.soupk_abi_version()
+    if version != ABI_VERSION:
+        raise SoupkError(f"{path}: ABI {version} != expected {ABI_VERSION}: rebuild")
+    handle.soupk_status_string.restype = ctypes.c_char_p
+    handle.soupk_status_string.argtypes = [ctypes.c_int]
+    for name, args in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = args
+    return handle
+
+
 def lib():
-    """The loaded library (raises if it has not been built)."""
+    """The package's library, loaded once (raises if it has not been built)."""
     global _lib
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(_LIB_PATH):
-                raise SoupkError(
-                    f"{_LIB_PATH} is missing: build it with `python -m testt_amd.build_ext` "
-                    "(or __graft_entry__.build()) before using the kernels")
-            handle = ctypes.CDLL(_LIB_PATH)
-            handle.soupk_abi_version.restype = ctypes.c_int
-            handle.soupk_abi_version.argtypes = []
-            version = handle.soupk_abi_version()
-            if version != ABI_VERSION:
-                raise SoupkError(f"libsoupk ABI {version} != expected {ABI_VERSION}: rebuild")
-            handle.soupk_status_string.restype = ctypes.c_char_p
-            handle.soupk_status_string.argtypes = [ctypes.c_int]
-            for name, args in SIGNATURES.items():
-                fn = getattr(handle, name)
-                fn.restype = ctypes.c_int
-                fn.argtypes = args
-            _lib = handle
+            _lib = load_library(_LIB_PATH)
     return _lib
 
 

@@ -41,32 +41,38 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(hipcc, src):
-    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc, *COMPILE_FLAGS, "-c", src, "-o", obj]
+def _compile(hipcc, src, build_dir, defines):
+    obj = os.path.join(build_dir, os.path.basename(src)[:-4] + ".o")
+    cmd = [hipcc, *COMPILE_FLAGS, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose=False):
-    """Compile every kernel source and link libsoupk.so; returns the library path."""
+def build(verbose=False, defines=(), out=None):
+    """Compile every kernel source and link libsoupk.so; returns the library path.
+
+    `defines` (e.g. "SOUPK_HEAD_PREFETCH=8") override the launch-shape constants of the
+    sources; with `out`, the library is written there instead (a tuning variant), from its
+    own object directory."""
     hipcc = _hipcc()
-    os.makedirs(BUILD, exist_ok=True)
+    lib_path = out or LIB_PATH
+    build_dir = BUILD if out is None else os.path.splitext(out)[0] + "_build"
+    os.makedirs(build_dir, exist_ok=True)
     srcs = sources()
     jobs = max(1, min(len(srcs), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(hipcc, s), srcs))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(pool.map(lambda s: _compile(hipcc, s, build_dir, defines), srcs))
+    tmp = lib_path + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link of {LIB_NAME} failed:\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", flush=True)
-    return LIB_PATH
+        print(f"built {lib_path} from {len(srcs)} sources", flush=True)
+    return lib_path
 
 
 if __name__ == "__main__":

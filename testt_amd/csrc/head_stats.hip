@@ -32,6 +32,10 @@ constexpr int kHeadThreads = 1024;
 constexpr int kHeadWaves = kHeadThreads / kWave;
 constexpr int kStreamUnroll = 2;  // 16-byte chunks per thread per step, streaming form
 constexpr int kMaxCpt = 20;       // register-resident form: up to 20 chunks (80 VGPRs) / thread
+#ifndef SOUPK_HEAD_PREFETCH
+#define SOUPK_HEAD_PREFETCH 6
+#endif
+constexpr int kHeadPrefetch = SOUPK_HEAD_PREFETCH;  // resident form: chunk loads in flight per lane
 constexpr int64_t kIgnoreIndex = -100;
 
 struct RowStats {
@@ -73,6 +77,23 @@ __device__ __forceinline__ void absorb(RowStats& st, const float* z, int32_t col
     st.se = st.se + e;
     st.sd = __builtin_fmaf(e, z[j], st.sd);
   }
+}
+
+// Fold one scalar column into the running statistics; with ties_win the column takes the
+// argmax on an equal value too (used for a column left of everything folded in before it).
+__device__ __forceinline__ void absorb_col(RowStats& st, float z, int32_t col, bool ties_win) {
+  if (z > st.m || (ties_win && z == st.m)) {
+    if (z > st.m) {
+      const float f = scale_to(st.m, z);
+      st.se = st.se * f;
+      st.sd = st.sd * f;
+      st.m = z;
+    }
+    st.ix = col;
+  }
+  const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -st.m * kLog2e));
+  st.se = st.se + e;
+  st.sd = __builtin_fmaf(e, z, st.sd);
 }
 
 // Fold one 16-byte chunk (8 fp16 columns starting at col0) into the running statistics.  The
@@ -196,11 +217,58 @@ __device__ __forceinline__ void grad_scalar(uint16_t* base, int64_t col, int64_t
 }
 
 // ---- register-resident form ------------------------------------------------------------------
+// Per-chunk statistics step of the resident form.  The chunk max uses v_pk_maximum3_f16 (exact:
+// a max selects one of its inputs); when it raises the running max the sums are rescaled and
+// only the chunk number is recorded -- the first column holding the max inside that chunk is
+// resolved once, after the sweep.
+__device__ __forceinline__ void absorb_resident(RowStats& st, int& kbest, const u32x4 w, int k) {
+  const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
+  const f16x2 m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
+                                                 __builtin_elementwise_maximum(c, d));
+  const float bm = __builtin_elementwise_maximum(static_cast<float>(m2[0]),
+                                                 static_cast<float>(m2[1]));
+  if (bm > st.m) {
+    const float f = scale_to(st.m, bm);
+    st.se = st.se * f;
+    st.sd = st.sd * f;
+    st.m = bm;
+    kbest = k;
+  }
+  const float shift = -st.m * kLog2e;
+  const f16 h[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float z = static_cast<float>(h[j]);
+    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, shift));
+    st.se = st.se + e;
+    st.sd = __builtin_fmaf(e, z, st.sd);
+  }
+}
+
+// Gradient chunk with the scale folded into the exponent: fp16(2^(z*log2e + fshift)) where
+// fshift = log2(grad_scale) - lse*log2e, i.e. exp(z - lse) * grad_scale; the target column
+// (hit = 0..7) subtracts grad_scale (the onehot term times the scale).
+__device__ __forceinline__ u32x4 grad_chunk_folded(u32x4 w, float fshift, float grad_scale,
+                                                   int hit) {
+  float z[8];
+  unpack8(w, z);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[j], kLog2e, fshift));
+  if (hit >= 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == hit) z[j] = z[j] - grad_scale;
+  }
+  return u32x4{pack_h2(z[0], z[1]), pack_h2(z[2], z[3]), pack_h2(z[4], z[5]),
+               pack_h2(z[6], z[7])};
+}
+
 template <int CPT>
 __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
     uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
     float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
     float* __restrict__ lse_out, float grad_scale, int64_t V) {
+  constexpr int P = CPT < kHeadPrefetch ? CPT : kHeadPrefetch;  // loads kept ahead of compute
   __shared__ RowStats part[kHeadWaves];
   __shared__ float row_lse;
   const int64_t row = blockIdx.x;
@@ -214,33 +282,59 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   // (chunks past the row read as 0), and each chunk needs only a 32-bit offset register.
   const __amdgpu_buffer_rsrc_t rsrc =
       buffer_rsrc(base + sp.lead, static_cast<uint32_t>(sp.nvec * 16));
+  const uint32_t off0 = static_cast<uint32_t>(tid) * 16;
+  constexpr uint32_t kChunkStride = kHeadThreads * 16;
+  // The scalar head/tail columns are loaded first: waiting for a load waits for every load
+  // issued before it, so they must not queue behind the chunk prefetch.
+  // Both are unconditional, at clamped in-row columns, so that no branch forces an early wait.
+  const bool has_lead = tid < sp.lead, has_tail = sp.tail0 + tid < V;
+  const float zlead = h2f(base[has_lead ? tid : 0]);
+  const float ztail = h2f(base[has_tail ? sp.tail0 + tid : V - 1]);
   u32x4 w[CPT];
 #pragma unroll
-  for (int k = 0; k < CPT; ++k)
-    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (k * kHeadThreads + tid) * 16, 0, 0);
-  float zlead = 0.f, ztail = 0.f;
-  const bool has_lead = tid < sp.lead, has_tail = sp.tail0 + tid < V;
-  if (has_lead) zlead = h2f(base[tid]);
-  if (has_tail) ztail = h2f(base[sp.tail0 + tid]);
+  for (int k = 0; k < P; ++k)
+    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + k * kChunkStride, 0,
+                                                 kAuxNonTemporal);
 
   // 32-bit chunk indices (a row has < 2^28 chunks): 64-bit ones would cost a register pair
   // per chunk on top of the row.
   const int32_t nvec = static_cast<int32_t>(sp.nvec), lead = static_cast<int32_t>(sp.lead);
   RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
-  if (has_lead) absorb<1>(st, &zlead, tid);
-  // The scheduling fences keep one chunk's temporaries live at a time: the whole row already
-  // occupies 4*CPT VGPRs, and latency is hidden by the other 15 waves of the workgroup.
+  int kbest = -1;
+  // Load k + P is issued before chunk k is folded in, so each wave keeps P chunks in flight and
+  // its arithmetic follows the data as it lands; the scheduling fences keep one chunk's
+  // temporaries live at a time (the row already occupies 4*CPT VGPRs).
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    const int32_t c = k * kHeadThreads + tid;
-    if (c < nvec) absorb_chunk(st, w[k], lead + 8 * c);
+    if (k + P < CPT)
+      w[k + P] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + (k + P) * kChunkStride, 0,
+                                                       kAuxNonTemporal);
+    if (k * kHeadThreads + tid < nvec) absorb_resident(st, kbest, w[k], k);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (has_tail) absorb<1>(st, &ztail, static_cast<int32_t>(sp.tail0 + tid));
+  if (kbest >= 0) {
+    // First column of the max inside chunk kbest (a select over the register-resident chunks).
+    u32x4 cw = w[0];
+#pragma unroll
+    for (int k = 1; k < CPT; ++k)
+      if (k == kbest) cw = w[k];
+    float z[8];
+    unpack8(cw, z);
+    int j0 = 7;
+#pragma unroll
+    for (int j = 6; j >= 0; --j)
+      if (z[j] == st.m) j0 = j;
+    st.ix = lead + 8 * (kbest * kHeadThreads + tid) + j0;
+  }
+  // The scalar columns come last (the sums do not depend on order): the head column lies left
+  // of every chunk, so it takes the argmax on ties; the tail column lies right of them all.
+  if (has_lead) absorb_col(st, zlead, tid, true);
+  if (has_tail) absorb_col(st, ztail, static_cast<int32_t>(sp.tail0 + tid), false);
 
   const float lse = finish_row(st, part, &row_lse, base, row, tgt, labelled, tgt_ok, entropy,
                                loss, correct, lse_out);
   if (!labelled) return;
+  const float fshift = log2f(grad_scale) - lse * kLog2e;  // log2(scale) - lse*log2(e)
   const float shift = -lse * kLog2e;
   const int32_t tc =
       (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? static_cast<int32_t>((tgt - sp.lead) >> 3)
@@ -249,15 +343,15 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   if (has_lead) grad_scalar(base, tid, tgt, shift, grad_scale);
   // Store offsets are recomputed from an opaque copy of tid*16 (one add per chunk) rather than
   // kept live from the load phase: CPT offset registers on top of the row would spill.
-  uint32_t lane_off = static_cast<uint32_t>(tid) * 16;
+  uint32_t lane_off = off0;
   asm volatile("" : "+v"(lane_off));
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int32_t c = k * kHeadThreads + tid;
     if (c < nvec)
       __builtin_amdgcn_raw_buffer_store_b128(
-          grad_chunk(w[k], shift, grad_scale, c == tc ? thit : -1), rsrc,
-          lane_off + k * kHeadThreads * 16, 0, kAuxNonTemporal);
+          grad_chunk_folded(w[k], fshift, grad_scale, c == tc ? thit : -1), rsrc,
+          lane_off + k * kChunkStride, 0, kAuxNonTemporal);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (has_tail) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
@@ -340,6 +434,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
   if (rows > 0x7fffffff) return kInvalid;
   if (!logits || !target || !entropy || !loss || !correct) return kInvalid;
   if (reinterpret_cast<uintptr_t>(logits) & 1u) return kInvalid;
+  if (!(grad_scale >= 0.f)) return kInvalid;  // negative or NaN (log2 of it is taken)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(rows)), block(kHeadThreads);
   // Whole 16-byte chunks per thread: at most V/8 chunks per row over 1024 threads.

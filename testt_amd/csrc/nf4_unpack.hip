@@ -13,7 +13,7 @@
 //     are computed once per block by the first threads into LDS, instead of once per lane;
 //   * the 16-entry NF4 codebook is expanded in LDS into a 256-entry table of (high, low) nibble
 //     value pairs, so one ds_read_b64 per packed byte yields both codes' fp32 values;
-//   * one tile per workgroup (3,360 workgroups for a [17920, 1536] weight).
+//   * one tile per workgroup (1,680 workgroups for a [17920, 1536] weight).
 // Other layouts (qblock or qblock2 not a power of two, qblock < 8, unaligned pointers) take a
 // one-byte-per-thread kernel with the same arithmetic, which also handles the last n_bytes % 4.
 
@@ -23,8 +23,11 @@ namespace soupk {
 namespace {
 
 constexpr int kNf4Threads = 256;
-constexpr int kNf4Dwords = 4;                                // dwords per thread per tile
-constexpr int kNf4TileDwords = kNf4Threads * kNf4Dwords;     // 4 KiB of packed codes
+#ifndef SOUPK_NF4_DWORDS
+#define SOUPK_NF4_DWORDS 8
+#endif
+constexpr int kNf4Dwords = SOUPK_NF4_DWORDS;                 // dwords per thread per tile
+constexpr int kNf4TileDwords = kNf4Threads * kNf4Dwords;     // 8 KiB of packed codes
 
 // 4 packed bytes (lowest address first) -> 8 fp16 weights (high nibble first within a byte).
 __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
@@ -38,8 +41,8 @@ __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
 }
 
 // dword_block_shift = log2(dwords per absmax block) = log2(qblock / 8); block2_shift =
-// log2(qblock2).  Requires qblock a power of two in [8, 8192] (a dword never straddles two
-// blocks, and a tile spans whole blocks).  One tile per workgroup; the packed loads are issued
+// log2(qblock2).  Requires qblock a power of two in [8, 8 * kNf4TileDwords] (a dword never
+// straddles two blocks, and a tile spans whole blocks).  One tile per workgroup; the packed loads are issued
 // unconditionally (indices past the end clamped to the last dword, results dropped), because a
 // predicated load makes the compiler wait on it before issuing the next.
 __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
@@ -121,8 +124,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack(
   const int64_t bytes_per_block = qblock / 2;
   const int64_t n_blocks = (n_bytes + bytes_per_block - 1) / bytes_per_block;
   int64_t vec_bytes = 0;
-  // (qblock <= 8192: a tile of 1024 dwords spans whole absmax blocks)
-  if (qblock >= 8 && qblock <= 8192 && is_pow2(qblock) && is_pow2(qblock2) &&
+  // (qblock / 8 <= kNf4TileDwords: a tile spans whole absmax blocks)
+  if (qblock >= 8 && qblock / 8 <= kNf4TileDwords && is_pow2(qblock) && is_pow2(qblock2) &&
       aligned(packed, 4) && aligned(out_f16, 16)) {
     const int64_t n_dwords = n_bytes / 4;
     vec_bytes = n_dwords * 4;

@@ -18,7 +18,10 @@
 namespace soupk {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
+#ifndef SOUPK_NORM_ROWS
+#define SOUPK_NORM_ROWS 4
+#endif
+constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // wavefronts (= rows) per workgroup
 constexpr int kNormThreads = kWave * kRowsPerBlock;
 
 __device__ __forceinline__ f32x4 load_h4(const uint16_t* p) {
@@ -29,6 +32,15 @@ __device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
   *reinterpret_cast<u32x2*>(p) = u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
 }
 
+// Row index of this wavefront, made wave-uniform for the compiler (per-row scalars such as
+// pad_idx[row] and rstd[row] then come through the scalar cache).
+__device__ __forceinline__ int64_t wave_row(int64_t first_row) {
+  return first_row + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+}
+
+// All loads of a row are issued before any arithmetic, at clamped (always valid) chunk indices;
+// lanes past the row's end zero their values with a select.  A predicated load would make the
+// compiler wait for it before issuing the next one.
 template <int CPL>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ delta, const float* __restrict__ w,
@@ -36,34 +48,38 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     const int64_t* __restrict__ pad_idx, const int32_t* __restrict__ pad_inv,
     float* __restrict__ rstd_out, int64_t rows, int64_t pad_rows, int H, float eps,
     int64_t row_blocks) {
-  const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
     // Zero the padded rows that no token row is scattered to.
-    const int64_t p = (static_cast<int64_t>(blockIdx.x) - row_blocks) * kRowsPerBlock + wave;
+    const int64_t p = wave_row((static_cast<int64_t>(blockIdx.x) - row_blocks) * kRowsPerBlock);
     if (p >= pad_rows || pad_inv[p] >= 0) return;
     f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
-    for (int c = lane; c < nch; c += kWave) dst[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = lane; c < nch; c += kWave) dst[c] = zero;
     return;
   }
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave;
+  const int64_t row = wave_row(static_cast<int64_t>(blockIdx.x) * kRowsPerBlock);
   if (row >= rows) return;
   const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * H);
-  f32x4 v[CPL];
+  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
+  f32x4 v[CPL], wv[CPL], d[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = j * kWave + lane;
-    v[j] = c < nch ? xr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+    const int c = min(j * kWave + lane, nch - 1);
+    v[j] = xr[c];
+    wv[j] = wr[c];
+    if (delta != nullptr) d[j] = load_h4(delta + row * H + 4 * c);
   }
-  if (delta != nullptr) {
-    const uint16_t* dr = delta + row * H;
-    f32x4 d[CPL];
+  int64_t dest = -1;
+  if (ypad != nullptr) {
+    dest = pad_idx[row];
+    if (dest < 0 || dest >= pad_rows) dest = -1;
+  }
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = j * kWave + lane;
-      d[j] = c < nch ? load_h4(dr + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  for (int j = 0; j < CPL; ++j)
+    if (j * kWave + lane >= nch) v[j] = zero;
+  if (delta != nullptr) {
     f32x4* sr = reinterpret_cast<f32x4*>(s_out + row * H);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -71,6 +87,9 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
       v[j] = v[j] + d[j];
       if (c < nch) sr[c] = v[j];
     }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      if (j * kWave + lane >= nch) v[j] = zero;
   }
   float ss = 0.f;
 #pragma unroll
@@ -78,20 +97,13 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
   ss = wave_sum(ss);
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
   uint16_t* yr = y + row * H;
-  const bool pad = ypad != nullptr;
-  int64_t dest = -1;
-  if (pad) {
-    dest = pad_idx[row];
-    if (dest < 0 || dest >= pad_rows) dest = -1;
-  }
   f32x4* pr = dest >= 0 ? reinterpret_cast<f32x4*>(ypad + dest * H) : nullptr;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = j * kWave + lane;
     if (c < nch) {
-      const f32x4 o = (v[j] * rstd) * wr[c];
+      const f32x4 o = (v[j] * rstd) * wv[j];
       store_h4(yr + 4 * c, o);
       if (pr != nullptr) pr[c] = o;
     }
@@ -105,62 +117,40 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
     const uint16_t* __restrict__ dy, const float* __restrict__ dypad,
     const int64_t* __restrict__ pad_idx, const float* __restrict__ ds, float* __restrict__ dx,
     uint16_t* __restrict__ ddelta, int64_t rows, int64_t pad_rows, int H) {
-  const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave;
+  const int64_t row = wave_row(static_cast<int64_t>(blockIdx.x) * kRowsPerBlock);
   if (row >= rows) return;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 g[CPL], n[CPL];
+  int64_t src = -1;
+  if (dypad != nullptr) {
+    src = pad_idx[row];
+    if (src < 0 || src >= pad_rows) src = -1;
+  }
   const f32x4* sr = reinterpret_cast<const f32x4*>(s + row * H);
+  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
+  const f32x4* pr = src >= 0 ? reinterpret_cast<const f32x4*>(dypad + src * H) : nullptr;
+  const f32x4* dsr = ds != nullptr ? reinterpret_cast<const f32x4*>(ds + row * H) : nullptr;
+  f32x4 n[CPL], g[CPL], wv[CPL], gp[CPL], dd[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = j * kWave + lane;
-    n[j] = c < nch ? sr[c] : zero;
-    g[j] = zero;
-  }
-  if (dy != nullptr) {
-    const uint16_t* dr = dy + row * H;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = j * kWave + lane;
-      if (c < nch) g[j] = g[j] + load_h4(dr + 4 * c);
-    }
-  }
-  if (dypad != nullptr) {
-    const int64_t src = pad_idx[row];
-    if (src >= 0 && src < pad_rows) {
-      const f32x4* pr = reinterpret_cast<const f32x4*>(dypad + src * H);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = j * kWave + lane;
-        if (c < nch) g[j] = g[j] + pr[c];
-      }
-    }
+    const int c = min(j * kWave + lane, nch - 1);
+    n[j] = sr[c];
+    wv[j] = wr[c];
+    g[j] = dy != nullptr ? load_h4(dy + row * H + 4 * c) : zero;
+    gp[j] = pr != nullptr ? pr[c] : zero;
+    dd[j] = dsr != nullptr ? dsr[c] : zero;
   }
   const float rstd = rstd_in[row];
-  const f32x4* wr = reinterpret_cast<const f32x4*>(w);
   float dot = 0.f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = j * kWave + lane;
-    if (c < nch) {
-      g[j] = g[j] * wr[c];
-      n[j] = n[j] * rstd;
-      const f32x4 p = g[j] * n[j];
-      dot += (p.x + p.y) + (p.z + p.w);
-    }
+    g[j] = (g[j] + gp[j]) * wv[j];
+    n[j] = n[j] * rstd;
+    const f32x4 p = g[j] * n[j];
+    if (j * kWave + lane < nch) dot += (p.x + p.y) + (p.z + p.w);
   }
   const float proj = wave_sum(dot) / static_cast<float>(H);
-  f32x4 d[CPL];
-  if (ds != nullptr) {
-    const f32x4* dsr = reinterpret_cast<const f32x4*>(ds + row * H);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = j * kWave + lane;
-      d[j] = c < nch ? dsr[c] : zero;
-    }
-  }
   f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * H);
   uint16_t* ddr = ddelta != nullptr ? ddelta + row * H : nullptr;
 #pragma unroll
@@ -168,7 +158,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
     const int c = j * kWave + lane;
     if (c < nch) {
       f32x4 o = (g[j] - n[j] * proj) * rstd;
-      if (ds != nullptr) o = o + d[j];
+      if (dsr != nullptr) o = o + dd[j];
       dxr[c] = o;
       if (ddr != nullptr) store_h4(ddr + 4 * c, o);
     }

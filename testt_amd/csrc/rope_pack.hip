@@ -8,8 +8,8 @@
 //
 // Mapping (gfx950): a work item is one 8-dim slice of one head of one token, together with the
 // matching 8 dims of the head's other half (the rotation partner), so a thread does two 16-byte
-// fp16 loads of qkv, up to four 16-byte loads of fp32 LoRA delta, the cos/sin slices (a
-// [T, D] fp32 table that stays in L2), and two 16-byte stores.  Items are numbered token-major,
+// fp16 loads of qkv, up to four 16-byte loads of fp32 LoRA delta, two 16-byte stores, and reads
+// its cos/sin slices from LDS, where the workgroup staged the rows of its tokens once.  Items are numbered token-major,
 // so a wavefront reads a token's 4 KiB qkv row in full.  In the forward pass the workgroups
 // after the token workgroups write zeros at the padded positions that no token maps to
 // (pos_inv[p] < 0), replacing the three torch.zeros memsets of the reference.
@@ -53,6 +53,36 @@ __device__ __forceinline__ void add8_lora(float* x, const void* lora, int64_t of
   for (int i = 0; i < 8; ++i) x[i] = x[i] + l[i];
 }
 
+// The cos/sin rows of the tokens a workgroup touches are staged once in LDS (per token 2*D fp32:
+// cos then sin), instead of every thread reading its 4 x 32 bytes of them from L1/L2.  A
+// workgroup's 256 items span at most kRopeMaxTok tokens (the host checks items per token).
+constexpr int kRopeMaxTok = 16;
+
+template <int HALF>
+__device__ __forceinline__ int stage_tables(f32x4* tab, const float* __restrict__ cos_t,
+                                            const float* __restrict__ sin_t,
+                                            const int64_t* __restrict__ pos, uint32_t tok0,
+                                            uint32_t ntok, const RopeDims& dm) {
+  constexpr int D = 2 * HALF;
+  constexpr int Q = D / 4;  // float4 per table row
+  const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
+  for (int i = threadIdx.x; i < static_cast<int>(ntok) * 2 * Q; i += kRopeThreads) {
+    const int j = i / (2 * Q), q = i % (2 * Q);
+    const int64_t p = pos[tok0 + j];
+    const int t = (p >= 0 && p < slots) ? static_cast<int>(p % dm.T) : 0;
+    const float* src = q < Q ? cos_t + static_cast<int64_t>(t) * D + 4 * q
+                             : sin_t + static_cast<int64_t>(t) * D + 4 * (q - Q);
+    tab[i] = *reinterpret_cast<const f32x4*>(src);
+  }
+  return 2 * Q;  // f32x4 per staged token
+}
+
+__device__ __forceinline__ void lds8(const f32x4* p, float* v) {
+  const f32x4 a = p[0], b = p[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 template <int HALF>
 __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     const uint16_t* __restrict__ qkv, const void* __restrict__ lora_q,
@@ -62,6 +92,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     uint16_t* __restrict__ v, int64_t rows, RopeDims dm, int64_t tok_blocks) {
   constexpr int D = 2 * HALF;
   constexpr int CPH = HALF / 8;  // items per head
+  __shared__ f32x4 tab[kRopeMaxTok * D / 2];
   const int heads = dm.NH + 2 * dm.NKV;
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
   if (static_cast<int64_t>(blockIdx.x) >= tok_blocks) {
@@ -85,52 +116,71 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     *reinterpret_cast<u32x4*>(base + HALF + 8 * c) = z;
     return;
   }
-  const uint32_t g = blockIdx.x * kRopeThreads + threadIdx.x;
+  const uint32_t g0 = blockIdx.x * kRopeThreads;
+  const uint32_t total = static_cast<uint32_t>(rows) * dm.items;
+  const uint32_t tok0 = dm.per_tok.div(g0);
+  const uint32_t ntok = dm.per_tok.div(min(g0 + kRopeThreads, total) - 1) - tok0 + 1;
+  // Threads past the last item take the last item's indices (so every address they form is in
+  // bounds), help stage the tables, and leave after the barrier.
+  const bool active = g0 + threadIdx.x < total;
+  const uint32_t g = active ? g0 + threadIdx.x : total - 1;
   const uint32_t tok = dm.per_tok.div(g);
-  if (tok >= rows) return;
   const int it = static_cast<int>(g - tok * dm.items);
   const int h = it / CPH, c = it % CPH;
+  const bool is_q = h < dm.NH, is_v = h >= dm.NH + dm.NKV;
+
+  // Issue this thread's qkv and LoRA loads, then stage the tables while they are in flight.
+  float x1[8], x2[8], l1[8], l2[8];
+  const uint16_t* row = qkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  load8_h(row, x1);
+  load8_h(row + HALF, x2);
+  const void* lora = is_q ? lora_q : (is_v ? lora_v : nullptr);
+  const bool has_lora = lora != nullptr;
+  if (has_lora) {
+    const int64_t off = is_q ? static_cast<int64_t>(tok) * dm.NH * D + h * D + 8 * c
+                             : static_cast<int64_t>(tok) * dm.NKV * D +
+                                   (h - dm.NH - dm.NKV) * D + 8 * c;
+    if (lora_f32) {
+      load8_f32(static_cast<const float*>(lora) + off, l1);
+      load8_f32(static_cast<const float*>(lora) + off + HALF, l2);
+    } else {
+      load8_h(static_cast<const uint16_t*>(lora) + off, l1);
+      load8_h(static_cast<const uint16_t*>(lora) + off + HALF, l2);
+    }
+  }
+  const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
+  __syncthreads();
+  if (!active) return;
   const int64_t p = pos[tok];
   if (p < 0 || p >= slots) return;
   const int b = static_cast<int>(p / dm.T), t = static_cast<int>(p % dm.T);
-
-  const uint16_t* row = qkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
-  float x1[8], x2[8];
-  load8_h(row, x1);
-  load8_h(row + HALF, x2);
-  uint16_t* dst;
-  if (h < dm.NH + dm.NKV) {
-    const bool is_q = h < dm.NH;
-    if (is_q && lora_q != nullptr) {
-      const int64_t off = static_cast<int64_t>(tok) * dm.NH * D + h * D + 8 * c;
-      add8_lora(x1, lora_q, off, lora_f32);
-      add8_lora(x2, lora_q, off + HALF, lora_f32);
+  if (has_lora) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x1[i] = x1[i] + l1[i];
+      x2[i] = x2[i] + l2[i];
     }
+  }
+  if (!is_v) {
+    const f32x4* tr = tab + (tok - tok0) * per;
     float c1[8], c2[8], s1[8], s2[8];
-    const float* cr = cos_t + static_cast<int64_t>(t) * D + 8 * c;
-    const float* sr = sin_t + static_cast<int64_t>(t) * D + 8 * c;
-    load8_f32(cr, c1);
-    load8_f32(cr + HALF, c2);
-    load8_f32(sr, s1);
-    load8_f32(sr + HALF, s2);
+    lds8(tr + 2 * c, c1);
+    lds8(tr + HALF / 4 + 2 * c, c2);
+    lds8(tr + D / 4 + 2 * c, s1);
+    lds8(tr + D / 4 + HALF / 4 + 2 * c, s2);
     float o1[8], o2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       o1[i] = x1[i] * c1[i] - x2[i] * s1[i];
       o2[i] = x2[i] * c2[i] + x1[i] * s2[i];
     }
-    dst = is_q ? q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
-               : k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
+    uint16_t* dst = is_q ? q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
+                         : k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
     store8_h(dst + 8 * c, o1);
     store8_h(dst + HALF + 8 * c, o2);
   } else {
     const int hv = h - dm.NH - dm.NKV;
-    if (lora_v != nullptr) {
-      const int64_t off = static_cast<int64_t>(tok) * dm.NKV * D + hv * D + 8 * c;
-      add8_lora(x1, lora_v, off, lora_f32);
-      add8_lora(x2, lora_v, off + HALF, lora_f32);
-    }
-    dst = v + ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
+    uint16_t* dst = v + ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
     store8_h(dst + 8 * c, x1);
     store8_h(dst + HALF + 8 * c, x2);
   }
@@ -144,38 +194,48 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
     uint16_t* __restrict__ dqkv, int64_t rows, RopeDims dm) {
   constexpr int D = 2 * HALF;
   constexpr int CPH = HALF / 8;
+  __shared__ f32x4 tab[kRopeMaxTok * D / 2];
   const int heads = dm.NH + 2 * dm.NKV;
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
-  const uint32_t g = blockIdx.x * kRopeThreads + threadIdx.x;
+  const uint32_t g0 = blockIdx.x * kRopeThreads;
+  const uint32_t total = static_cast<uint32_t>(rows) * dm.items;
+  const uint32_t tok0 = dm.per_tok.div(g0);
+  const uint32_t ntok = dm.per_tok.div(min(g0 + kRopeThreads, total) - 1) - tok0 + 1;
+  // Threads past the last item take the last item's indices (every address they form is in
+  // bounds), help stage the tables, and leave after the barrier.
+  const bool active = g0 + threadIdx.x < total;
+  const uint32_t g = active ? g0 + threadIdx.x : total - 1;
   const uint32_t tok = dm.per_tok.div(g);
-  if (tok >= rows) return;
   const int it = static_cast<int>(g - tok * dm.items);
   const int h = it / CPH, c = it % CPH;
-  uint16_t* out = dqkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  const bool is_q = h < dm.NH, is_v = h >= dm.NH + dm.NKV;
   const int64_t p = pos[tok];
-  float g1[8], g2[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) g1[i] = g2[i] = 0.f;
   const bool valid = p >= 0 && p < slots;
   const int b = valid ? static_cast<int>(p / dm.T) : 0;
   const int t = valid ? static_cast<int>(p % dm.T) : 0;
-  if (h < dm.NH + dm.NKV) {
-    const bool is_q = h < dm.NH;
-    const uint16_t* src = is_q ? dq : dk;
-    if (valid && src != nullptr) {
-      const int64_t base =
-          is_q ? ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
-               : ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
-      load8_h(src + base + 8 * c, g1);
-      load8_h(src + base + HALF + 8 * c, g2);
-    }
+  float g1[8], g2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) g1[i] = g2[i] = 0.f;
+  const uint16_t* src = is_q ? dq : (is_v ? dv : dk);
+  if (valid && src != nullptr) {
+    const int64_t base =
+        is_q ? ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
+             : (is_v ? ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH - dm.NKV)) * dm.T + t) * D
+                     : ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D);
+    load8_h(src + base + 8 * c, g1);
+    load8_h(src + base + HALF + 8 * c, g2);
+  }
+  const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
+  __syncthreads();
+  if (!active) return;
+  uint16_t* out = dqkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  if (!is_v) {
+    const f32x4* tr = tab + (tok - tok0) * per;
     float c1[8], c2[8], s1[8], s2[8];
-    const float* cr = cos_t + static_cast<int64_t>(t) * D + 8 * c;
-    const float* sr = sin_t + static_cast<int64_t>(t) * D + 8 * c;
-    load8_f32(cr, c1);
-    load8_f32(cr + HALF, c2);
-    load8_f32(sr, s1);
-    load8_f32(sr + HALF, s2);
+    lds8(tr + 2 * c, c1);
+    lds8(tr + HALF / 4 + 2 * c, c2);
+    lds8(tr + D / 4 + 2 * c, s1);
+    lds8(tr + D / 4 + HALF / 4 + 2 * c, s2);
     float o1[8], o2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -185,12 +245,6 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
     store8_h(out, o1);
     store8_h(out + HALF, o2);
   } else {
-    const int hv = h - dm.NH - dm.NKV;
-    if (valid && dv != nullptr) {
-      const int64_t base = ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
-      load8_h(dv + base + 8 * c, g1);
-      load8_h(dv + base + HALF + 8 * c, g2);
-    }
     store8_h(out, g1);
     store8_h(out + HALF, g2);
   }
@@ -332,9 +386,10 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
   const int half = D / 2;
   const int heads = NH + 2 * NKV;
   const int lora_align = 16;
-  const bool vec = half == 64 && aligned(qkv, 16) && aligned(cos, 16) && aligned(sin, 16) &&
-                   aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
-                   aligned(lora_q, lora_align) && aligned(lora_v, lora_align);
+  // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens)
+  const bool vec = half == 64 && heads * (half / 8) >= 18 && aligned(qkv, 16) &&
+                   aligned(cos, 16) && aligned(sin, 16) && aligned(q, 16) && aligned(k, 16) &&
+                   aligned(v, 16) && aligned(lora_q, lora_align) && aligned(lora_v, lora_align);
   if (vec) {
     RopeDims dm;
     dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
@@ -371,8 +426,9 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int half = D / 2;
   const int heads = NH + 2 * NKV;
-  const bool vec = half == 64 && aligned(dq, 16) && aligned(dk, 16) && aligned(dv, 16) &&
-                   aligned(cos, 16) && aligned(sin, 16) && aligned(dqkv, 16);
+  const bool vec = half == 64 && heads * (half / 8) >= 18 && aligned(dq, 16) &&
+                   aligned(dk, 16) && aligned(dv, 16) && aligned(cos, 16) && aligned(sin, 16) &&
+                   aligned(dqkv, 16);
   if (vec) {
     RopeDims dm;
     dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;

@@ -7,9 +7,10 @@
 // Pure HBM streaming.  The flat index space is rows * I/8 chunks of 8 fp16 (16 bytes); chunk c
 // lives in row r = c / (I/8), and because act is [rows, I] contiguous its chunk offset is 8c,
 // while gate sits at 8c + r*I and up at 8c + r*I + I of the [rows, 2I] buffer.  Each thread
-// issues all loads of its kSwiUnroll chunks back to back before any arithmetic, so every wave
-// keeps 8-12 KiB in flight.  Arithmetic is fp32: exp through v_exp_f32, the reciprocal through v_rcp_f32
-// (both about 1 ulp of fp32, far below the fp16 rounding of the result).
+// issues all loads of its kSwiUnroll chunks back to back before any arithmetic; one chunk per
+// thread (many small workgroups) measured fastest on MI355X.  Arithmetic is fp32: exp through
+// v_exp_f32, the reciprocal through v_rcp_f32 (both about 1 ulp of fp32, far below the fp16
+// rounding of the result).
 
 #include "fastdiv.hpp"
 #include "soupk_common.hpp"
@@ -18,7 +19,10 @@ namespace soupk {
 namespace {
 
 constexpr int kSwiThreads = 256;
-constexpr int kSwiUnroll = 4;  // 16-byte chunks per thread (one workgroup tile: 16 KiB of act)
+#ifndef SOUPK_SWI_UNROLL
+#define SOUPK_SWI_UNROLL 1
+#endif
+constexpr int kSwiUnroll = SOUPK_SWI_UNROLL;  // 16-byte chunks per thread per workgroup tile
 
 __device__ __forceinline__ float sigmoid_f(float g) {
   return __builtin_amdgcn_rcpf(1.0f + fast_exp(-g));
