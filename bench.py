@@ -33,6 +33,9 @@ from testt_amd import _ext, workloads  # noqa: E402
 
 PEAK_HBM_GBPS = 8000.0
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (written by
+# `bench.py --summarize-pmc`); the roofline's "traffic" field is read from this table.
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_step2048_pmc.md")
 
 
 def log(msg):
@@ -265,6 +268,47 @@ def time_gpu(cases, steps, warmup, dev, lib=None):
     return host_enqueue, wall
 
 
+def time_layer(dev, steps, warmup):
+    """One Qwen2.5-1.5B decoder layer (testt_amd/layer.py) at B=4 x T=512 = 2048 real tokens:
+    mean forward and forward+backward wall time on the GPU (torch events around the whole
+    layer: every kernel, GEMM and the attention)."""
+    from testt_amd import layer
+
+    B, T, H = workloads.BATCH, workloads.SEQ, workloads.HIDDEN
+    w = layer.synthetic_layer(dev)
+    pos = torch.arange(B * T, device=dev)
+    cos, sin = (t.to(dev) for t in workloads.rope_tables(T))
+    g = workloads.gen(10)
+    s0 = torch.randn(B * T, H, generator=g).to(dev)
+    d0 = (0.5 * torch.randn(B * T, H, generator=g)).to(torch.float16).to(dev)
+    gs = (1e-2 * torch.randn(B * T, H, generator=g)).to(dev)
+    gd = (1e-2 * torch.randn(B * T, H, generator=g)).to(torch.float16).to(dev)
+
+    def step(backward):
+        s_in = s0.detach().requires_grad_(True)
+        d_in = d0.detach().requires_grad_(True)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, None)
+        if backward:
+            torch.autograd.backward([s, d], [gs, gd])
+
+    for _ in range(warmup):
+        step(True)
+    out = {}
+    for name, bwd in (("fwd_us", False), ("fwd_bwd_us", True)):
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step(bwd)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        out[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 1)
+    out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
+               note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs and torch SDPA "
+                    "in fp16, every other op a soupk kernel (testt_amd/layer.py)")
+    return out
+
+
 def copy_peak(dev, mib=1024, reps=6):
     """Read+write GB/s of torch's device copy of `mib` MiB (the box's plain-copy reference)."""
     n = mib * (1 << 20) // 4
@@ -315,6 +359,92 @@ def cpu_baseline(cases, seconds):
                        f"on the CPU (oracle/baseline.py), {elapsed:.1f} s, {model}")}
 
 
+def pmc_traffic(kernel, path=TRAFFIC_TABLE):
+    """Measured HBM bytes per launch of `kernel` from the committed PMC table, or None."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
+                if len(cells) >= 6 and cells[0].split("<")[0] == kernel:
+                    return int(cells[5])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def _kernel_base(name):
+    return name.replace("soupk::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+
+def _read_csv(path):
+    import csv
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_stats(stats_csv, bench_json, command):
+    """Markdown summary of a rocprofv3 --kernel-trace --stats run beside bench.py's own timing."""
+    bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
+    out = ["# rocprofv3 kernel statistics: kernel set at the 2048-token step (bench.py)", "",
+           "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```", command, "```",
+           "", "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    for r in _read_csv(stats_csv):
+        if "soupk" in r["Name"]:
+            out.append(f"| `{_kernel_base(r['Name'])}` | {r['Calls']} | "
+                       f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                       f"{float(r['MaxNs']) / 1e3:.2f} |")
+    out += ["", "The same kernels timed by `python bench.py` (unprofiled run, dispatch-recorded "
+            "HIP events, mean us):", "", "| kernel | bench us | GB/s | % of 8 TB/s |",
+            "|---|---:|---:|---:|"]
+    for k, v in bench["kernels"].items():
+        out.append(f"| {k} (`{v['kernel']}`) | {v['us_mean']:.2f} | {v['GBps']:.0f} | "
+                   f"{100 * v['frac_of_peak']:.1f} |")
+    return "\n".join(out) + "\n"
+
+
+def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
+    """Markdown table of HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the 1 GiB device
+    copy that bench.py's copy_peak() makes (torch's copy_ -> __amd_rocclr_copyBuffer)."""
+    from collections import defaultdict
+    bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
+    algo = {v["kernel"]: v["bytes"] for v in bench["kernels"].values()}
+    fetch, write = _read_csv(fetch_csv), _read_csv(write_csv)
+    gib_kib = float(1 << 20)
+    copies = {r["Dispatch_Id"] for r in write if "copyBuffer" in r["Kernel_Name"]
+              and float(r["Counter_Value"]) > 0.9 * gib_kib}
+    if not copies:
+        raise SystemExit("no 1 GiB copy dispatch in the WRITE_SIZE run")
+    mean = lambda xs: sum(xs) / len(xs)
+    f_copy = mean([float(r["Counter_Value"]) for r in fetch if r["Dispatch_Id"] in copies])
+    w_copy = mean([float(r["Counter_Value"]) for r in write if r["Dispatch_Id"] in copies])
+    f_scale, w_scale = gib_kib / f_copy, gib_kib / w_copy
+    per = defaultdict(lambda: [[], []])
+    for i, rows in enumerate((fetch, write)):
+        for r in rows:
+            if "soupk" in r["Kernel_Name"]:
+                per[_kernel_base(r["Kernel_Name"])][i].append(float(r["Counter_Value"]))
+    out = ["# HBM traffic per launch (rocprofv3 PMC): kernel set at the 2048-token step", "",
+           "Commands (run from /tmp on the MI355X box, TMPDIR=/tmp), one counter per pass:", "",
+           "```", *commands, "```", "",
+           f"Scale factors from the 1 GiB device copy of `bench.py` (`copy_peak`, "
+           f"`__amd_rocclr_copyBuffer`, {len(copies)} dispatches): FETCH_SIZE reads "
+           f"{f_copy:.0f} KiB for 1048576 KiB read -> x{f_scale:.4f}; WRITE_SIZE reads "
+           f"{w_copy:.0f} KiB for 1048576 KiB written -> x{w_scale:.4f}.", "",
+           "traffic = (FETCH_SIZE x fetch scale + WRITE_SIZE x write scale) x 1024 bytes, mean "
+           "over dispatches; algorithmic = the compulsory bytes bench.py prices the kernel at.",
+           "", "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB | traffic "
+           "bytes | algorithmic bytes | traffic / algorithmic |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for name, (f, w) in per.items():
+        t = int(round((mean(f) * f_scale + mean(w) * w_scale) * 1024))
+        a = algo.get(name.split("<")[0])
+        ratio = f"{t / a:.3f}" if a else "-"
+        out.append(f"| `{name}` | {len(f)} | {mean(f):.1f} | {mean(w):.1f} | {t / 1e6:.2f} | "
+                   f"{t} | {a if a else '-'} | {ratio} |")
+    return "\n".join(out) + "\n"
+
+
 def median(xs):
     s = sorted(xs)
     n = len(s)
@@ -328,7 +458,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer timing")
+    ap.add_argument("--summarize-stats", nargs=3, metavar=("STATS_CSV", "BENCH_JSON", "CMD"),
+                    help="print a markdown summary of a rocprofv3 --stats run and exit (CPU)")
+    ap.add_argument("--summarize-pmc", nargs=5,
+                    metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "CMD1", "CMD2"),
+                    help="print the HBM traffic table of two rocprofv3 --pmc runs and exit (CPU)")
     args = ap.parse_args()
+    if args.summarize_stats:
+        sys.stdout.write(summarize_stats(*args.summarize_stats))
+        return
+    if args.summarize_pmc:
+        a = args.summarize_pmc
+        sys.stdout.write(summarize_pmc(a[0], a[1], a[2], a[3:]))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the kernel set has no cross-GPU exchange and this "
               "build runs no multi-GPU configuration (see DESIGN.md, 'Sharding').",
@@ -346,6 +489,11 @@ def main():
     log(f"timing {len(cases)} kernels: warmup {args.warmup}, steps {args.steps}")
     host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
+    layer_t = None
+    if not args.no_layer:
+        log("timing one decoder layer fwd+bwd at 2048 tokens")
+        layer_t = time_layer(dev, max(3, args.steps // 3), 2)
+        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us")
     kernels = {}
     total_us = 0.0
     total_bytes = 0
@@ -365,7 +513,8 @@ def main():
     dom_gbps = dom.nbytes / (dom_us * 1e-6) / 1e9
     roofline = {"kernel": dom.kernel, "bound": "hbm", "achieved": round(dom_gbps, 1),
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(dom_gbps / PEAK_HBM_GBPS, 4),
-                "traffic": None}
+                "traffic": pmc_traffic(dom.kernel), "algorithmic_bytes": dom.nbytes,
+                "traffic_source": os.path.relpath(TRAFFIC_TABLE, ROOT)}
     cpu = None
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
@@ -385,6 +534,7 @@ def main():
         "value_definition": "sum of compulsory HBM bytes of the 8 kernels / sum of their mean "
                             "HIP-event durations",
         "kernels": kernels,
+        "layer": layer_t,
         "copy_peak_GBps": copy_gbps,
         "timing": "per-launch HIP events recorded by the kernel dispatch itself "
                   "(soupk_time_next_launch / hipExtLaunchKernelGGL), mean over steps",

@@ -1,0 +1,103 @@
+"""GPU: one full decoder layer built from the drop-in ops (testt_amd/layer.py, the per-layer body
+of solution/model.py:235-255) against an fp32 eager layer with the same weights (dequantized by
+the oracle), on a ragged, padded batch; forward outputs and the gradients of the residual
+input, the previous block output and the LoRA parameters.
+
+The fused layer runs its GEMMs in fp16 (as the reference does under autocast), so the check is
+the reference step test's relative-norm tolerance (solution/test_model.py:118-127: 2e-2)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.nf4 import dequant_state
+from oracle.rope import apply_rotary
+from testt_amd import layer, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def rel_err(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def reference_layer(s0, d0, w, wd, pos, batch, seq, cos, sin, amask):
+    """fp32 eager layer: the same wiring with every GEMM and the attention in fp32."""
+    H = s0.shape[1]
+    nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
+    padded = batch * seq
+
+    def norm(x, weight):
+        return weight * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + w.eps))
+
+    s = s0 + d0.float()
+    y = norm(s, w.input_norm)
+    qkv = y @ torch.cat([wd["q"], wd["k"], wd["v"]]).t() + w.qkv_bias.float()
+    y_pad = torch.zeros(padded, H, device=DEV).index_copy(0, pos, y)
+    rows = y_pad.index_select(0, pos)
+    lq = (rows @ w.lora_q[0].t()) @ w.lora_q[1].t() * w.scaling
+    lv = (rows @ w.lora_v[0].t()) @ w.lora_v[1].t() * w.scaling
+    q = qkv[:, :nh * hd] + lq
+    k = qkv[:, nh * hd:(nh + nkv) * hd]
+    v = qkv[:, (nh + nkv) * hd:] + lv
+
+    def pad(flat, heads):
+        out = torch.zeros(padded, heads * hd, device=DEV).index_copy(0, pos, flat)
+        return out.view(batch, seq, heads, hd).transpose(1, 2)
+
+    qp, kp = apply_rotary(pad(q, nh), pad(k, nkv), cos, sin)
+    vp = pad(v, nkv)
+    rep = nh // nkv
+    kp = kp.repeat_interleave(rep, dim=1)
+    vp = vp.repeat_interleave(rep, dim=1)
+    scores = (qp @ kp.transpose(-1, -2).contiguous()) / np.sqrt(hd)
+    allowed = torch.ones(seq, seq, dtype=torch.bool, device=DEV).tril()[None, None] & \
+        amask.bool()[:, None, None, :]
+    scores = scores.masked_fill(~allowed, float("-inf"))
+    a = torch.softmax(scores, -1).nan_to_num(0.0) @ vp
+    a = a.transpose(1, 2).reshape(padded, nh * hd).index_select(0, pos)
+    s2 = s + a @ wd["o"].t()
+    y2 = norm(s2, w.post_norm)
+    d = (torch.nn.functional.silu(y2 @ wd["gate"].t()) * (y2 @ wd["up"].t())) @ wd["down"].t()
+    return s2, d
+
+
+def test_decoder_layer_matches_fp32_eager():
+    batch, seq = 2, 64
+    lengths = (64, 40)
+    w = layer.synthetic_layer(DEV, seed=9)
+    wd = {n: torch.from_numpy(dequant_state(getattr(w, n)).astype(np.float32)).to(DEV)
+          for n in ("q", "k", "v", "o", "gate", "up", "down")}
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(3)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+
+    s_in = s0.clone().requires_grad_(True)
+    d_in = d0.clone().requires_grad_(True)
+    s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                               layer.causal_pad_mask(amask))
+    torch.autograd.backward([s, d], [gs, gd])
+    fused = [s_in.grad, d_in.grad] + [p.grad for p in (*w.lora_q, *w.lora_v)]
+    for p in (*w.lora_q, *w.lora_v):
+        p.grad = None
+
+    rs_in = s0.clone().requires_grad_(True)
+    rd_in = d0.float().clone().requires_grad_(True)
+    rs, rd = reference_layer(rs_in, rd_in, w, wd, pos, batch, seq, cos, sin, amask)
+    torch.autograd.backward([rs, rd], [gs, gd.float()])
+    ref = [rs_in.grad, rd_in.grad] + [p.grad for p in (*w.lora_q, *w.lora_v)]
+
+    assert rel_err(s, rs) < 2e-2 and rel_err(d.float(), rd) < 2e-2
+    for name, a, b in zip(("d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"), fused, ref):
+        assert a is not None and b is not None, name
+        assert rel_err(a, b) < 2e-2, (name, rel_err(a, b))

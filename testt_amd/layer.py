@@ -1,0 +1,131 @@
+"""One Qwen2 decoder layer of the QLoRA training step, wired from the drop-in ops.
+
+Mirrors the per-layer body of the reference's fused_forward (solution/model.py:235-255) on the
+real (non-pad) tokens:
+
+  s, y, y_pad = add_rmsnorm(s, d)               residual add + input RMSNorm (HIP)
+  qkv        = y @ [Wq;Wk;Wv]^T + b               NF4 unpack (HIP) + one hipBLASLt GEMM
+  lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v, PyTorch (fp16 GEMMs)
+  q, k, v    = rope_pack(qkv, lq, lv)             LoRA add + RoPE + pack (HIP)
+  a          = SDPA(q, k, v, causal [+ pad mask])  PyTorch scaled_dot_product_attention (GQA)
+  o          = a[real tokens] @ Wo^T              NF4 unpack (HIP) + hipBLASLt
+  s, y2, _   = add_rmsnorm(s, o)                  residual add + post-attention RMSNorm (HIP)
+  d          = mlp(y2)                            NF4 unpack + GEMM + SwiGLU (HIP) + GEMM
+
+The reference takes these modules from a PEFT/bitsandbytes model; here they are plain tensors
+(`LayerWeights`), so one layer can be built from synthetic NF4 weights for measurement and
+tests.  The LoRA branch follows peft's `lora_B(lora_A(dropout(x))) * scaling` under fp16
+autocast (the matmuls in fp16, on the fp32 padded norm output so the dropout draws match).
+"""
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import workloads
+from .mlp import fused_mlp
+from .nf4 import frozen_linear
+from .rmsnorm import add_rmsnorm
+from .rope import rope_pack
+
+
+@dataclass
+class LayerWeights:
+    input_norm: torch.Tensor        # fp32 [H]
+    post_norm: torch.Tensor         # fp32 [H]
+    q: object                       # Params4bit-like NF4 weights (.data, .quant_state)
+    k: object
+    v: object
+    o: object
+    gate: object
+    up: object
+    down: object
+    qkv_bias: torch.Tensor          # fp16 [(NH + 2*NKV) * D]
+    lora_q: tuple                   # (A fp32 [r, H], B fp32 [NH*D, r]) trainable
+    lora_v: tuple                   # (A fp32 [r, H], B fp32 [NKV*D, r]) trainable
+    scaling: float
+    n_heads: int
+    n_kv: int
+    head_dim: int
+    eps: float = 1e-6
+    dropout: float = 0.0
+
+
+def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
+                    n_heads=workloads.N_HEADS, n_kv=workloads.N_KV, head_dim=workloads.HEAD_DIM,
+                    rank=16, alpha=32, dropout=0.0, seed=9):
+    """A Qwen2.5-1.5B-shaped layer: synthetic NF4 projections, LoRA r=16 on q/v."""
+    g = workloads.gen(seed)
+    qd, kvd = n_heads * head_dim, n_kv * head_dim
+    shapes = {"q": (qd, hidden), "k": (kvd, hidden), "v": (kvd, hidden), "o": (hidden, qd),
+              "gate": (inter, hidden), "up": (inter, hidden), "down": (hidden, inter)}
+    nf4w = {name: workloads.nf4_weight(*shape, seed=seed * 100 + i, device=device,
+                                       absmax2_range=(0.005, 0.02), offset=0.01)
+            for i, (name, shape) in enumerate(shapes.items())}
+
+    def lora(out_dim):
+        a = (torch.randn(rank, hidden, generator=g) / math.sqrt(hidden)).to(device)
+        b = (0.05 * torch.randn(out_dim, rank, generator=g)).to(device)
+        return a.requires_grad_(True), b.requires_grad_(True)
+
+    return LayerWeights(
+        input_norm=(1 + 0.02 * torch.randn(hidden, generator=g)).to(device),
+        post_norm=(1 + 0.02 * torch.randn(hidden, generator=g)).to(device),
+        qkv_bias=(0.1 * torch.randn(qd + 2 * kvd, generator=g)).to(torch.float16).to(device),
+        lora_q=lora(qd), lora_v=lora(kvd), scaling=alpha / rank, n_heads=n_heads, n_kv=n_kv,
+        head_dim=head_dim, dropout=dropout, **nf4w)
+
+
+def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
+    """peft's B(A(dropout(x))) * scaling for the real tokens, fp16 matmuls (solution/model.py:
+    195-206): the dropout runs on the padded fp32 norm output, A and B on the real rows."""
+    a, b = ab
+    hidden = y_pad.shape[-1]
+    dropped = torch.nn.functional.dropout(y_pad.view(batch, seq, hidden), dropout,
+                                          training=dropout > 0).view(batch * seq, hidden)
+    rows = dropped.index_select(0, pos_idx).to(torch.float16)
+    return (rows @ a.to(torch.float16).t()) @ b.to(torch.float16).t() * scaling
+
+
+def attention(q, k, v, mask):
+    """SDPA over the padded [B, heads, T, D] layout with grouped key/value heads."""
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    if mask is None:
+        return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                                scale=scale, enable_gqa=True)
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scale,
+                                                            enable_gqa=True)
+
+
+def causal_pad_mask(attention_mask):
+    """Boolean [B, 1, T, T] mask: causal and key-not-padding (None when nothing is padded)."""
+    if bool(attention_mask.all()):
+        return None
+    batch, seq = attention_mask.shape
+    causal = torch.ones(seq, seq, dtype=torch.bool, device=attention_mask.device).tril()
+    mask = causal[None, None] & attention_mask.bool()[:, None, None, :]
+    # a fully padded query row would be all False; let it see itself so SDPA stays finite
+    eye = torch.eye(seq, dtype=torch.bool, device=attention_mask.device)[None, None]
+    return mask | (eye & ~attention_mask.bool()[:, None, :, None])
+
+
+def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, mask):
+    """(s, d): the residual stream and the MLP output of one layer (the next layer's delta)."""
+    padded = batch * seq
+    nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
+    s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
+    qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias)
+    lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
+    lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
+    del y_pad
+    q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
+    del qkv, lq, lv
+    a = attention(q, k, v, mask)
+    del q, k, v
+    a = a.transpose(1, 2).reshape(padded, nh * hd).index_select(0, pos_idx)
+    o = frozen_linear(a, (w.o,), None)
+    del a
+    s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)
+    d = fused_mlp(y2, w.gate, w.up, w.down)
+    return s, d
