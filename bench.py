@@ -5,12 +5,13 @@
 A step is one pass of the hot path over one batch of synthetic input: every kernel of the
 solution/ set, forward and backward, once, at the 2048-token shape of Qwen2.5-1.5B
 (config 1, the CPU-runnable RMSNorm case, is the same RMSNorm
-shape).  Inputs are resident in HBM before the timed region.  Each launch carries a pair of
-HIP events on the stream it runs on (torch's current stream), recorded by the kernel dispatch
-itself (soupk_time_next_launch -> hipExtLaunchKernelGGL), so they time the kernel exactly as
-rocprofv3's kernel trace does; launches go straight through the C ABI with preallocated
-buffers.  Two input sets per kernel alternate, and the other kernels of the step move > 600 MB
-between two launches of one kernel, so the 256 MB Infinity Cache does not serve its inputs.
+shape).  Inputs are resident in HBM before the timed region; 20 warm-up steps, 200 timed.
+Each launch carries a pair of HIP events on the stream it runs on (torch's current stream),
+recorded by the kernel dispatch itself (soupk_time_next_launch -> hipExtLaunchKernelGGL), so
+they time the kernel exactly as rocprofv3's kernel trace does; launches go straight through
+the C ABI with preallocated buffers.  Three input sets per kernel rotate, and the other
+kernels of the step move > 600 MB between two launches of one kernel, so the 256 MB Infinity
+Cache does not serve its inputs.
 
 Prints ONE JSON line: value = the set's aggregate compulsory HBM bytes / summed kernel time
 (GB/s), per-kernel us / GB/s / fraction of the 8 TB/s peak, the roofline of the dominant kernel,
@@ -63,7 +64,7 @@ def p(t):
     return t.data_ptr() if t is not None else None
 
 
-def build_cases(dev, n_sets=2, lib=None):
+def build_cases(dev, n_sets=3, lib=None):
     """The eight kernels at the step shape; `lib` selects the soupk library (default: the
     package's)."""
     cases = []
@@ -454,8 +455,8 @@ def median(xs):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer timing")
@@ -492,7 +493,7 @@ def main():
     layer_t = None
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
-        layer_t = time_layer(dev, max(3, args.steps // 3), 2)
+        layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
         log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us")
     kernels = {}
     total_us = 0.0
