@@ -23,13 +23,19 @@ namespace {
 #endif
 constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // wavefronts (= rows) per workgroup
 constexpr int kNormThreads = kWave * kRowsPerBlock;
+#ifndef SOUPK_NORM_NT
+#define SOUPK_NORM_NT 1
+#endif
+// Row streams (x, delta, s, dy, dypad, ds in; s, y, ypad, dx, ddelta out) are touched once per
+// launch: non-temporal.  The weight, read by every row, stays cached.
+constexpr bool kNormNT = SOUPK_NORM_NT != 0;
 
 __device__ __forceinline__ f32x4 load_h4(const uint16_t* p) {
-  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+  const u32x2 w = ld<kNormNT>(reinterpret_cast<const u32x2*>(p));
   return f32x4{lo_h(w.x), hi_h(w.x), lo_h(w.y), hi_h(w.y)};
 }
 __device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
-  *reinterpret_cast<u32x2*>(p) = u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
+  st<kNormNT>(reinterpret_cast<u32x2*>(p), u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)});
 }
 
 // Row index of this wavefront, made wave-uniform for the compiler (per-row scalars such as
@@ -56,7 +62,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     const int64_t p = wave_row((static_cast<int64_t>(blockIdx.x) - row_blocks) * kRowsPerBlock);
     if (p >= pad_rows || pad_inv[p] >= 0) return;
     f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
-    for (int c = lane; c < nch; c += kWave) dst[c] = zero;
+    for (int c = lane; c < nch; c += kWave) st<kNormNT>(dst + c, zero);
     return;
   }
   const int64_t row = wave_row(static_cast<int64_t>(blockIdx.x) * kRowsPerBlock);
@@ -67,7 +73,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = min(j * kWave + lane, nch - 1);
-    v[j] = xr[c];
+    v[j] = ld<kNormNT>(xr + c);
     wv[j] = wr[c];
     if (delta != nullptr) d[j] = load_h4(delta + row * H + 4 * c);
   }
@@ -85,7 +91,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     for (int j = 0; j < CPL; ++j) {
       const int c = j * kWave + lane;
       v[j] = v[j] + d[j];
-      if (c < nch) sr[c] = v[j];
+      if (c < nch) st<kNormNT>(sr + c, v[j]);
     }
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
     if (c < nch) {
       const f32x4 o = (v[j] * rstd) * wv[j];
       store_h4(yr + 4 * c, o);
-      if (pr != nullptr) pr[c] = o;
+      if (pr != nullptr) st<kNormNT>(pr + c, o);
     }
   }
   if (lane == 0) rstd_out[row] = rstd;
@@ -135,11 +141,11 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = min(j * kWave + lane, nch - 1);
-    n[j] = sr[c];
+    n[j] = ld<kNormNT>(sr + c);
     wv[j] = wr[c];
     g[j] = dy != nullptr ? load_h4(dy + row * H + 4 * c) : zero;
-    gp[j] = pr != nullptr ? pr[c] : zero;
-    dd[j] = dsr != nullptr ? dsr[c] : zero;
+    gp[j] = pr != nullptr ? ld<kNormNT>(pr + c) : zero;
+    dd[j] = dsr != nullptr ? ld<kNormNT>(dsr + c) : zero;
   }
   const float rstd = rstd_in[row];
   float dot = 0.f;
@@ -159,7 +165,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
     if (c < nch) {
       f32x4 o = (g[j] - n[j] * proj) * rstd;
       if (dsr != nullptr) o = o + dd[j];
-      dxr[c] = o;
+      st<kNormNT>(dxr + c, o);
       if (ddr != nullptr) store_h4(ddr + 4 * c, o);
     }
   }

@@ -21,6 +21,12 @@ namespace soupk {
 namespace {
 
 constexpr int kRopeThreads = 256;
+#ifndef SOUPK_ROPE_NT
+#define SOUPK_ROPE_NT 1
+#endif
+// qkv, LoRA deltas, q/k/v and their gradients are touched once per launch: non-temporal.  The
+// cos/sin tables, shared by every token at a position, stay cached.
+constexpr bool kRopeNT = SOUPK_ROPE_NT != 0;
 
 struct RopeDims {
   int B, T, NH, NKV;
@@ -29,30 +35,21 @@ struct RopeDims {
 };
 
 __device__ __forceinline__ void load8_f32(const float* p, float* v) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  const f32x4 a = ld<kRopeNT>(reinterpret_cast<const f32x4*>(p));
+  const f32x4 b = ld<kRopeNT>(reinterpret_cast<const f32x4*>(p + 4));
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 __device__ __forceinline__ void load8_h(const uint16_t* p, float* v) {
-  const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 w = ld<kRopeNT>(reinterpret_cast<const u32x4*>(p));
   v[0] = lo_h(w.x); v[1] = hi_h(w.x); v[2] = lo_h(w.y); v[3] = hi_h(w.y);
   v[4] = lo_h(w.z); v[5] = hi_h(w.z); v[6] = lo_h(w.w); v[7] = hi_h(w.w);
 }
 __device__ __forceinline__ void store8_h(uint16_t* p, const float* v) {
-  *reinterpret_cast<u32x4*>(p) =
-      u32x4{pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7])};
+  st<kRopeNT>(reinterpret_cast<u32x4*>(p),
+              u32x4{pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
+                    pack_h2(v[6], v[7])});
 }
-__device__ __forceinline__ void add8_lora(float* x, const void* lora, int64_t off, bool f32) {
-  float l[8];
-  if (f32)
-    load8_f32(static_cast<const float*>(lora) + off, l);
-  else
-    load8_h(static_cast<const uint16_t*>(lora) + off, l);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = x[i] + l[i];
-}
-
 // The cos/sin rows of the tokens a workgroup touches are staged once in LDS (per token 2*D fp32:
 // cos then sin), instead of every thread reading its 4 x 32 bytes of them from L1/L2.  A
 // workgroup's 256 items span at most kRopeMaxTok tokens (the host checks items per token).
@@ -112,8 +109,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     else
       base = v + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH - dm.NKV)) * dm.T + t) * D;
     const u32x4 z = {0u, 0u, 0u, 0u};
-    *reinterpret_cast<u32x4*>(base + 8 * c) = z;
-    *reinterpret_cast<u32x4*>(base + HALF + 8 * c) = z;
+    st<kRopeNT>(reinterpret_cast<u32x4*>(base + 8 * c), z);
+    st<kRopeNT>(reinterpret_cast<u32x4*>(base + HALF + 8 * c), z);
     return;
   }
   const uint32_t g0 = blockIdx.x * kRopeThreads;

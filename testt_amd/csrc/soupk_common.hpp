@@ -84,6 +84,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 }
 constexpr int kAuxNonTemporal = 2;  // cache-policy bits of buffer ops: streaming (nt)
 
+// ---- streaming (non-temporal) or cached global access, chosen at compile time ---------------
+// Data read or written exactly once per launch streams past the caches when NT is true.
+template <bool NT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 // ---- wave64 reductions (butterfly: every lane ends with the result) -------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
