@@ -7,10 +7,11 @@
 // Mapping (gfx950): one workgroup of 1024 threads (16 wavefronts, a whole CU) per logits row.
 // Register-resident form (V <= 1024 * 8 * kMaxCpt): each thread loads its share of the row --
 // chunk k*1024 + tid, 16 bytes each, every wave load instruction reading 1 KiB contiguous --
-// into VGPRs in one burst (a 151,936-column row is 297 KiB = 19 x 16 B per thread), computes
-// the statistics from the registers as the loads land, and after the workgroup reduction writes
-// the gradient from the same registers: the row crosses HBM once in and (for labelled rows) once
-// out, the compulsory traffic.  Larger vocabularies use the streaming form, which reads the row
+// into VGPRs (a 151,936-column row is 297 KiB = 19 x 16 B per thread, loads kept 4 deep),
+// computes the statistics from the registers as the loads land -- replacing each chunk by its
+// exponentials -- and after the workgroup reduction writes the gradient from the same
+// registers: the row crosses HBM once in and (for labelled rows) once out, the compulsory
+// traffic.  Larger vocabularies use the streaming form, which reads the row
 // twice (the second read served by L2 / the Infinity Cache).
 //
 // Statistics per lane: running max m, sum(e) and sum(e*z) with e = exp(z - m), and the first
@@ -33,7 +34,7 @@ constexpr int kHeadWaves = kHeadThreads / kWave;
 constexpr int kStreamUnroll = 2;  // 16-byte chunks per thread per step, streaming form
 constexpr int kMaxCpt = 20;       // register-resident form: up to 20 chunks (80 VGPRs) / thread
 #ifndef SOUPK_HEAD_PREFETCH
-#define SOUPK_HEAD_PREFETCH 6
+#define SOUPK_HEAD_PREFETCH 4
 #endif
 constexpr int kHeadPrefetch = SOUPK_HEAD_PREFETCH;  // resident form: chunk loads in flight per lane
 constexpr int64_t kIgnoreIndex = -100;
@@ -81,7 +82,9 @@ __device__ __forceinline__ void absorb(RowStats& st, const float* z, int32_t col
 
 // Fold one scalar column into the running statistics; with ties_win the column takes the
 // argmax on an equal value too (used for a column left of everything folded in before it).
-__device__ __forceinline__ void absorb_col(RowStats& st, float z, int32_t col, bool ties_win) {
+// `lift` scales the exponentials by 2^lift, as the resident form keeps its sums.
+__device__ __forceinline__ void absorb_col(RowStats& st, float z, int32_t col, bool ties_win,
+                                           float lift) {
   if (z > st.m || (ties_win && z == st.m)) {
     if (z > st.m) {
       const float f = scale_to(st.m, z);
@@ -91,7 +94,7 @@ __device__ __forceinline__ void absorb_col(RowStats& st, float z, int32_t col, b
     }
     st.ix = col;
   }
-  const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -st.m * kLog2e));
+  const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, lift - st.m * kLog2e));
   st.se = st.se + e;
   st.sd = __builtin_fmaf(e, z, st.sd);
 }
@@ -164,10 +167,12 @@ __device__ __forceinline__ RowSpan row_span(const uint16_t* base, int64_t V) {
 }
 
 // Workgroup merge of the per-thread statistics and the per-row outputs; returns the row's lse
-// to every thread.  Thread 0 reads z[target] here, before any thread overwrites the row.
-__device__ float finish_row(RowStats st, RowStats* part, float* row_lse, const uint16_t* base,
-                            int64_t row, int64_t tgt, bool labelled, bool tgt_ok,
-                            float* entropy, float* loss, int32_t* correct, float* lse_out) {
+// to every thread.  Thread 0 reads z[target] here, before any thread overwrites the row, and
+// leaves it in *row_zt.  The sums carry a factor 2^lift (lse removes it; entropy is a ratio).
+__device__ float finish_row(RowStats st, RowStats* part, float* row_lse, float* row_zt,
+                            const uint16_t* base, int64_t row, int64_t tgt, bool labelled,
+                            bool tgt_ok, float* entropy, float* loss, int32_t* correct,
+                            float* lse_out, float lift) {
   wave_merge(st);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (lane == 0) part[wave] = st;
@@ -176,12 +181,14 @@ __device__ float finish_row(RowStats st, RowStats* part, float* row_lse, const u
     RowStats r = lane < kHeadWaves ? part[lane] : RowStats{-INFINITY, 0.f, 0.f, INT_MAX};
     wave_merge(r);
     if (lane == 0) {
-      const float lse = r.m + logf(r.se);
+      const float lse = r.m + (logf(r.se) - lift * kLn2);
       const int32_t arg = r.ix == INT_MAX ? 0 : r.ix;
       entropy[row] = lse - r.sd / r.se;
+      const float zt = tgt_ok ? h2f(base[tgt]) : 0.f;
       float l = 0.f;
-      if (labelled) l = tgt_ok ? lse - h2f(base[tgt]) : NAN;
+      if (labelled) l = tgt_ok ? lse - zt : NAN;
       loss[row] = l;
+      *row_zt = zt;
       correct[row] = (labelled && tgt_ok && static_cast<int64_t>(arg) == tgt) ? 1 : 0;
       if (lse_out != nullptr) lse_out[row] = lse;
       *row_lse = lse;
@@ -217,11 +224,23 @@ __device__ __forceinline__ void grad_scalar(uint16_t* base, int64_t col, int64_t
 }
 
 // ---- register-resident form ------------------------------------------------------------------
-// Per-chunk statistics step of the resident form.  The chunk max uses v_pk_maximum3_f16 (exact:
-// a max selects one of its inputs); when it raises the running max the sums are rescaled and
-// only the chunk number is recorded -- the first column holding the max inside that chunk is
-// resolved once, after the sweep.
-__device__ __forceinline__ void absorb_resident(RowStats& st, int& kbest, const u32x4 w, int k) {
+// The statistics pass keeps, in place of each 16-byte chunk of logits, the chunk's eight
+// exponentials e = 2^kLift * exp(z - m_k) as fp16 (m_k: the thread's running max when the chunk
+// was folded in, saved per chunk in LDS as fp16 -- exact, it is one of the fp16 logits).  The
+// gradient pass then needs one exponential per chunk, F_k = exp(m_k - lse) * grad_scale *
+// 2^-kLift, and one multiply per column: grad = e * F_k.  The factor 2^kLift keeps e out of the
+// fp16 subnormal range down to exp(z - m) = 2^-29, where the product is far below one fp16 ulp
+// of any gradient the scale can produce (grad_scale <= 2^15); above it e carries a relative
+// error <= 2^-11, so the product rounds to fp16 within one ulp of the exactly rounded value.
+// The target column (p - 1 cancels) is recomputed from its logit in full fp32.
+constexpr float kLift = 15.f;
+
+// Per-chunk statistics step: the chunk max uses v_pk_maximum3_f16 (exact: a max selects one of
+// its inputs).  When it raises the running max, the sums are rescaled and the chunk's raw
+// logits are kept in `best` (with its number in kbest) for the argmax, which is resolved once at
+// the end; then the chunk's registers are overwritten with its lifted exponentials.
+__device__ __forceinline__ void absorb_keep(RowStats& st, int& kbest, u32x4& best, u32x4& w,
+                                            int k) {
   const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
   const f16x2 m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
                                                  __builtin_elementwise_maximum(c, d));
@@ -233,34 +252,38 @@ __device__ __forceinline__ void absorb_resident(RowStats& st, int& kbest, const 
     st.sd = st.sd * f;
     st.m = bm;
     kbest = k;
+    best = w;
   }
-  const float shift = -st.m * kLog2e;
+  const float shift = kLift - st.m * kLog2e;
   const f16 h[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  float e[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float z = static_cast<float>(h[j]);
-    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, shift));
-    st.se = st.se + e;
-    st.sd = __builtin_fmaf(e, z, st.sd);
+    e[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, shift));
+    st.se = st.se + e[j];
+    st.sd = __builtin_fmaf(e[j], z, st.sd);
   }
+  w = u32x4{pack_h2(e[0], e[1]), pack_h2(e[2], e[3]), pack_h2(e[4], e[5]), pack_h2(e[6], e[7])};
 }
 
-// Gradient chunk with the scale folded into the exponent: fp16(2^(z*log2e + fshift)) where
-// fshift = log2(grad_scale) - lse*log2e, i.e. exp(z - lse) * grad_scale; the target column
-// (hit = 0..7) subtracts grad_scale (the onehot term times the scale).
-__device__ __forceinline__ u32x4 grad_chunk_folded(u32x4 w, float fshift, float grad_scale,
-                                                   int hit) {
-  float z[8];
-  unpack8(w, z);
+// Gradient of one chunk from its lifted exponentials: fp16(e * F); in the target's chunk the
+// column `hit` (0..7) takes `gt`, computed from the logit itself.
+__device__ __forceinline__ u32x4 grad_from_e(u32x4 w, float F, int hit, float gt) {
+  const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
+  const f16 h[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  float g[8];
+  // e * F as one fused multiply-add with a zero addend: v_fma_mix_f32 reads the fp16 e
+  // directly, and the result is the product rounded once, as a multiply would give.
 #pragma unroll
-  for (int j = 0; j < 8; ++j) z[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[j], kLog2e, fshift));
+  for (int j = 0; j < 8; ++j) g[j] = __builtin_fmaf(static_cast<float>(h[j]), F, 0.0f);
   if (hit >= 0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (j == hit) z[j] = z[j] - grad_scale;
+      if (j == hit) g[j] = gt;
   }
-  return u32x4{pack_h2(z[0], z[1]), pack_h2(z[2], z[3]), pack_h2(z[4], z[5]),
-               pack_h2(z[6], z[7])};
+  return u32x4{pack_h2(g[0], g[1]), pack_h2(g[2], g[3]), pack_h2(g[4], g[5]),
+               pack_h2(g[6], g[7])};
 }
 
 template <int CPT>
@@ -270,7 +293,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
     float* __restrict__ lse_out, float grad_scale, int64_t V) {
   constexpr int P = CPT < kHeadPrefetch ? CPT : kHeadPrefetch;  // loads kept ahead of compute
   __shared__ RowStats part[kHeadWaves];
-  __shared__ float row_lse;
+  __shared__ float row_lse, row_zt;
+  __shared__ f16 chunk_max[CPT * kHeadThreads];  // m_k of chunk k of thread t at [k*1024 + t]
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
   const int64_t tgt = target[row];
@@ -301,6 +325,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   const int32_t nvec = static_cast<int32_t>(sp.nvec), lead = static_cast<int32_t>(sp.lead);
   RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
   int kbest = -1;
+  u32x4 best = {0u, 0u, 0u, 0u};
   // Load k + P is issued before chunk k is folded in, so each wave keeps P chunks in flight and
   // its arithmetic follows the data as it lands; the scheduling fences keep one chunk's
   // temporaries live at a time (the row already occupies 4*CPT VGPRs).
@@ -309,17 +334,16 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
     if (k + P < CPT)
       w[k + P] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + (k + P) * kChunkStride, 0,
                                                        kAuxNonTemporal);
-    if (k * kHeadThreads + tid < nvec) absorb_resident(st, kbest, w[k], k);
+    if (k * kHeadThreads + tid < nvec) {
+      absorb_keep(st, kbest, best, w[k], k);
+      chunk_max[k * kHeadThreads + tid] = static_cast<f16>(st.m);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   if (kbest >= 0) {
-    // First column of the max inside chunk kbest (a select over the register-resident chunks).
-    u32x4 cw = w[0];
-#pragma unroll
-    for (int k = 1; k < CPT; ++k)
-      if (k == kbest) cw = w[k];
+    // First column of the max inside chunk kbest.
     float z[8];
-    unpack8(cw, z);
+    unpack8(best, z);
     int j0 = 7;
 #pragma unroll
     for (int j = 6; j >= 0; --j)
@@ -328,18 +352,22 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   }
   // The scalar columns come last (the sums do not depend on order): the head column lies left
   // of every chunk, so it takes the argmax on ties; the tail column lies right of them all.
-  if (has_lead) absorb_col(st, zlead, tid, true);
-  if (has_tail) absorb_col(st, ztail, static_cast<int32_t>(sp.tail0 + tid), false);
+  if (has_lead) absorb_col(st, zlead, tid, true, kLift);
+  if (has_tail) absorb_col(st, ztail, static_cast<int32_t>(sp.tail0 + tid), false, kLift);
 
-  const float lse = finish_row(st, part, &row_lse, base, row, tgt, labelled, tgt_ok, entropy,
-                               loss, correct, lse_out);
+  const float lse = finish_row(st, part, &row_lse, &row_zt, base, row, tgt, labelled, tgt_ok,
+                               entropy, loss, correct, lse_out, kLift);
   if (!labelled) return;
-  const float fshift = log2f(grad_scale) - lse * kLog2e;  // log2(scale) - lse*log2(e)
   const float shift = -lse * kLog2e;
+  // F_k = 2^(m_k*log2e + fbase) = exp(m_k - lse) * grad_scale * 2^-kLift.
+  const float fbase = (log2f(grad_scale) - kLift) - lse * kLog2e;
   const int32_t tc =
       (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? static_cast<int32_t>((tgt - sp.lead) >> 3)
                                                    : -1;
   const int thit = static_cast<int>((tgt - sp.lead) & 7);
+  // The target column: (exp(z_t - lse) - 1) * grad_scale in fp32 (used by one lane only).
+  const float gt =
+      (__builtin_amdgcn_exp2f(__builtin_fmaf(row_zt, kLog2e, shift)) - 1.0f) * grad_scale;
   if (has_lead) grad_scalar(base, tid, tgt, shift, grad_scale);
   // Store offsets are recomputed from an opaque copy of tid*16 (one add per chunk) rather than
   // kept live from the load phase: CPT offset registers on top of the row would spill.
@@ -348,10 +376,13 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
     const int32_t c = k * kHeadThreads + tid;
-    if (c < nvec)
-      __builtin_amdgcn_raw_buffer_store_b128(
-          grad_chunk_folded(w[k], fshift, grad_scale, c == tc ? thit : -1), rsrc,
-          lane_off + k * kChunkStride, 0, kAuxNonTemporal);
+    if (c < nvec) {
+      const float mk = static_cast<float>(chunk_max[k * kHeadThreads + tid]);
+      const float F = __builtin_amdgcn_exp2f(__builtin_fmaf(mk, kLog2e, fbase));
+      __builtin_amdgcn_raw_buffer_store_b128(grad_from_e(w[k], F, c == tc ? thit : -1, gt),
+                                             rsrc, lane_off + k * kChunkStride, 0,
+                                             kAuxNonTemporal);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   if (has_tail) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
@@ -363,7 +394,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
     float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
     float* __restrict__ lse_out, float grad_scale, int64_t V) {
   __shared__ RowStats part[kHeadWaves];
-  __shared__ float row_lse;
+  __shared__ float row_lse, row_zt;
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
   const int64_t tgt = target[row];
@@ -396,8 +427,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
     const float z = h2f(base[sp.tail0 + tid]);
     absorb<1>(st, &z, static_cast<int32_t>(sp.tail0 + tid));
   }
-  const float lse = finish_row(st, part, &row_lse, base, row, tgt, labelled, tgt_ok, entropy,
-                               loss, correct, lse_out);
+  const float lse = finish_row(st, part, &row_lse, &row_zt, base, row, tgt, labelled, tgt_ok,
+                               entropy, loss, correct, lse_out, 0.f);
   if (!labelled) return;
   const float shift = -lse * kLog2e;
   const int64_t tc = (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? (tgt - sp.lead) >> 3 : -1;

@@ -23,6 +23,7 @@ typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // ---- status codes (hipError_t values) -------------------------------------------------------
 constexpr int kOk = 0;
