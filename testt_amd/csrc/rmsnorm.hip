@@ -1,15 +1,17 @@
-// Residual add + Qwen2RMSNorm, forward and backward, one wavefront per token row.
+// Residual add + Qwen2RMSNorm, forward and backward, one or two wavefronts per token row.
 //
 // Reference: solution/rmsnorm.py:24-43 (rmsnorm_fwd_kernel) and solution/rmsnorm.py:46-69
 // (rmsnorm_bwd_kernel), launched from _launch_fwd / _launch_bwd, solution/rmsnorm.py:76-112.
 // The normalisation is transformers' Qwen2RMSNorm (modeling_qwen2.py:247-252):
 // w * (s * rsqrt(mean(s^2) + eps)), with the product (s * rstd) rounded before the weight.
 //
-// Mapping (gfx950): a row of H fp32 is H/4 float4 chunks; lane l of the row's wavefront owns
-// chunks l, l+64, l+128, ... so every load or store instruction of the wave touches 1 KiB
-// (fp32) or 512 B (fp16) of contiguous memory.  The row's values stay in registers between the
-// load, the wave64 butterfly reduction and the stores (H <= 64 * 4 * kMaxCpl).  A workgroup is
-// four wavefronts = four rows.  In the forward pass extra workgroups after the row workgroups
+// Mapping (gfx950): a row of H fp32 is H/4 float4 chunks, split over WPR wavefronts (2 forward,
+// 1 backward) owning alternate 64-chunk slices, so every load or store instruction of a wave
+// touches 1 KiB (fp32) or 512 B (fp16) of contiguous memory.  The row's values stay in registers
+// between the load, the wave64 butterfly reduction (combined across the row's waves in LDS) and
+// the stores.  In the forward pass two waves per row give 16 waves per CU at 2048 rows, which
+// hides HBM latency better than one (and 2 rows per wave, 4 waves per CU, ran 40% slower).  A
+// workgroup holds four rows.  In the forward pass extra workgroups after the row workgroups
 // zero the rows of the padded fp32 output that no token maps to (the pad rows), so the padded
 // tensor needs no separate memset.
 
@@ -21,8 +23,17 @@ namespace {
 #ifndef SOUPK_NORM_ROWS
 #define SOUPK_NORM_ROWS 4
 #endif
-constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // wavefronts (= rows) per workgroup
-constexpr int kNormThreads = kWave * kRowsPerBlock;
+constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // rows per workgroup
+// Wavefronts per row on the vector path (measured on MI355X at 2048 x 1536: the forward pass is
+// 17% faster with two, the backward pass 3% faster with one).
+#ifndef SOUPK_NORM_WPR_FWD
+#define SOUPK_NORM_WPR_FWD 2
+#endif
+#ifndef SOUPK_NORM_WPR_BWD
+#define SOUPK_NORM_WPR_BWD 1
+#endif
+constexpr int kWprFwd = SOUPK_NORM_WPR_FWD;
+constexpr int kWprBwd = SOUPK_NORM_WPR_BWD;
 #ifndef SOUPK_NORM_NT
 #define SOUPK_NORM_NT 1
 #endif
@@ -38,41 +49,45 @@ __device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
   st<kNormNT>(reinterpret_cast<u32x2*>(p), u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)});
 }
 
-// Row index of this wavefront, made wave-uniform for the compiler (per-row scalars such as
-// pad_idx[row] and rstd[row] then come through the scalar cache).
-__device__ __forceinline__ int64_t wave_row(int64_t first_row) {
-  return first_row + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-}
 
-// All loads of a row are issued before any arithmetic, at clamped (always valid) chunk indices;
-// lanes past the row's end zero their values with a select.  A predicated load would make the
-// compiler wait for it before issuing the next one.
-template <int CPL>
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
+// WPR wavefronts share a row: lane l of the row's wave `sub` owns the float4 chunks
+// j*64*WPR + sub*64 + l, so each wave load or store instruction touches 1 KiB (fp32) or
+// 512 B (fp16) of contiguous memory.  The row's sum of squares (forward) or dot product
+// (backward) is combined across the row's waves through LDS, always in the same order.  All
+// loads are issued before any arithmetic, at clamped (always valid) chunk indices; lanes past
+// the row's end zero their values with a select.  A predicated load would make the compiler
+// wait for it before issuing the next one.
+template <int CPL, int WPR>
+__global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ delta, const float* __restrict__ w,
     float* __restrict__ s_out, uint16_t* __restrict__ y, float* __restrict__ ypad,
     const int64_t* __restrict__ pad_idx, const int32_t* __restrict__ pad_inv,
     float* __restrict__ rstd_out, int64_t rows, int64_t pad_rows, int H, float eps,
     int64_t row_blocks) {
+  __shared__ float part[kRowsPerBlock][WPR];
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
-    // Zero the padded rows that no token row is scattered to.
-    const int64_t p = wave_row((static_cast<int64_t>(blockIdx.x) - row_blocks) * kRowsPerBlock);
+    // Zero the padded rows that no token row is scattered to (one row per wavefront).
+    const int64_t p =
+        (static_cast<int64_t>(blockIdx.x) - row_blocks) * (kRowsPerBlock * WPR) + wave;
     if (p >= pad_rows || pad_inv[p] >= 0) return;
     f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
     for (int c = lane; c < nch; c += kWave) st<kNormNT>(dst + c, zero);
     return;
   }
-  const int64_t row = wave_row(static_cast<int64_t>(blockIdx.x) * kRowsPerBlock);
-  if (row >= rows) return;
+  const int rib = wave / WPR, sub = wave % WPR;  // row in block, wave within the row
+  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rib;
+  const bool live = row_raw < rows;  // (all waves reach the barrier below)
+  const int64_t row = live ? row_raw : rows - 1;
   const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * H);
   const f32x4* wr = reinterpret_cast<const f32x4*>(w);
   f32x4 v[CPL], wv[CPL], d[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = min(j * kWave + lane, nch - 1);
+    const int c = min((j * WPR + sub) * kWave + lane, nch - 1);
     v[j] = ld<kNormNT>(xr + c);
     wv[j] = wr[c];
     if (delta != nullptr) d[j] = load_h4(delta + row * H + 4 * c);
@@ -84,49 +99,61 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_fwd_kernel(
   }
 #pragma unroll
   for (int j = 0; j < CPL; ++j)
-    if (j * kWave + lane >= nch) v[j] = zero;
+    if ((j * WPR + sub) * kWave + lane >= nch) v[j] = zero;
   if (delta != nullptr) {
     f32x4* sr = reinterpret_cast<f32x4*>(s_out + row * H);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = j * kWave + lane;
+      const int c = (j * WPR + sub) * kWave + lane;
       v[j] = v[j] + d[j];
-      if (c < nch) st<kNormNT>(sr + c, v[j]);
+      if (live && c < nch) st<kNormNT>(sr + c, v[j]);
     }
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      if (j * kWave + lane >= nch) v[j] = zero;
+      if ((j * WPR + sub) * kWave + lane >= nch) v[j] = zero;
   }
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j)
     ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
   ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    if (lane == 0) part[rib][sub] = ss;
+    __syncthreads();
+    ss = part[rib][0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) ss += part[rib][i];
+  }
+  if (!live) return;
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
   uint16_t* yr = y + row * H;
   f32x4* pr = dest >= 0 ? reinterpret_cast<f32x4*>(ypad + dest * H) : nullptr;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = j * kWave + lane;
+    const int c = (j * WPR + sub) * kWave + lane;
     if (c < nch) {
       const f32x4 o = (v[j] * rstd) * wv[j];
       store_h4(yr + 4 * c, o);
       if (pr != nullptr) st<kNormNT>(pr + c, o);
     }
   }
-  if (lane == 0) rstd_out[row] = rstd;
+  if (sub == 0 && lane == 0) rstd_out[row] = rstd;
 }
 
-template <int CPL>
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
+template <int CPL, int WPR>
+__global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kernel(
     const float* __restrict__ s, const float* __restrict__ rstd_in, const float* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ dypad,
     const int64_t* __restrict__ pad_idx, const float* __restrict__ ds, float* __restrict__ dx,
     uint16_t* __restrict__ ddelta, int64_t rows, int64_t pad_rows, int H) {
+  __shared__ float part[kRowsPerBlock][WPR];
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
-  const int64_t row = wave_row(static_cast<int64_t>(blockIdx.x) * kRowsPerBlock);
-  if (row >= rows) return;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int rib = wave / WPR, sub = wave % WPR;
+  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rib;
+  const bool live = row_raw < rows;  // (all waves reach the barrier below)
+  const int64_t row = live ? row_raw : rows - 1;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   int64_t src = -1;
   if (dypad != nullptr) {
@@ -140,7 +167,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
   f32x4 n[CPL], g[CPL], wv[CPL], gp[CPL], dd[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = min(j * kWave + lane, nch - 1);
+    const int c = min((j * WPR + sub) * kWave + lane, nch - 1);
     n[j] = ld<kNormNT>(sr + c);
     wv[j] = wr[c];
     g[j] = dy != nullptr ? load_h4(dy + row * H + 4 * c) : zero;
@@ -154,14 +181,23 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
     g[j] = (g[j] + gp[j]) * wv[j];
     n[j] = n[j] * rstd;
     const f32x4 p = g[j] * n[j];
-    if (j * kWave + lane < nch) dot += (p.x + p.y) + (p.z + p.w);
+    if ((j * WPR + sub) * kWave + lane < nch) dot += (p.x + p.y) + (p.z + p.w);
   }
-  const float proj = wave_sum(dot) / static_cast<float>(H);
+  dot = wave_sum(dot);
+  if constexpr (WPR > 1) {
+    if (lane == 0) part[rib][sub] = dot;
+    __syncthreads();
+    dot = part[rib][0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) dot += part[rib][i];
+  }
+  if (!live) return;
+  const float proj = dot / static_cast<float>(H);
   f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * H);
   uint16_t* ddr = ddelta != nullptr ? ddelta + row * H : nullptr;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = j * kWave + lane;
+    const int c = (j * WPR + sub) * kWave + lane;
     if (c < nch) {
       f32x4 o = (g[j] - n[j] * proj) * rstd;
       if (dsr != nullptr) o = o + dd[j];
@@ -279,7 +315,7 @@ int with_cpl(int cpl, Args... args) {
     default: return -1;
   }
 }
-constexpr int kMaxCpl = 16;  // H <= 4096 on the register-resident path
+constexpr int kMaxCpl = 16;  // H <= 4 * 64 * WPR * 16 on the register-resident path
 
 template <int CPL>
 struct FwdLaunch {
@@ -287,8 +323,9 @@ struct FwdLaunch {
                  float* s_out, uint16_t* y, float* ypad, const int64_t* pad_idx,
                  const int32_t* pad_inv, float* rstd, int64_t rows, int64_t pad_rows, int H,
                  float eps, int64_t row_blocks) {
-    return launch_kernel(rmsnorm_fwd_kernel<CPL>, grid, dim3(kNormThreads), st, x, delta, w, s_out,
-                         y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows, H, eps, row_blocks);
+    return launch_kernel(rmsnorm_fwd_kernel<CPL, kWprFwd>, grid,
+                         dim3(kWave * kRowsPerBlock * kWprFwd), st, x, delta, w, s_out, y, ypad,
+                         pad_idx, pad_inv, rstd, rows, pad_rows, H, eps, row_blocks);
   }
 };
 
@@ -297,8 +334,9 @@ struct BwdLaunch {
   static int run(dim3 grid, hipStream_t st, const float* s, const float* rstd, const float* w,
                  const uint16_t* dy, const float* dypad, const int64_t* pad_idx, const float* ds,
                  float* dx, uint16_t* ddelta, int64_t rows, int64_t pad_rows, int H) {
-    return launch_kernel(rmsnorm_bwd_kernel<CPL>, grid, dim3(kNormThreads), st, s, rstd, w, dy,
-                         dypad, pad_idx, ds, dx, ddelta, rows, pad_rows, H);
+    return launch_kernel(rmsnorm_bwd_kernel<CPL, kWprBwd>, grid,
+                         dim3(kWave * kRowsPerBlock * kWprBwd), st, s, rstd, w, dy, dypad,
+                         pad_idx, ds, dx, ddelta, rows, pad_rows, H);
   }
 };
 
@@ -322,12 +360,13 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_fwd(
     if ((ypad == nullptr) != (pad_idx == nullptr)) return kInvalid;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int cpl = (H / 4 + kWave - 1) / kWave;
+  const int cpl = (H / 4 + kWave * kWprFwd - 1) / (kWave * kWprFwd);
   const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(x, 16) && aligned(w, 16) &&
                    aligned(s_out, 16) && aligned(ypad, 16) && aligned(delta, 8) && aligned(y, 8);
   if (vec) {
     const int64_t row_blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    const int64_t blocks = row_blocks + (zero_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int64_t zero_per_block = kRowsPerBlock * kWprFwd;  // one pad row per wavefront
+    const int64_t blocks = row_blocks + (zero_rows + zero_per_block - 1) / zero_per_block;
     if (blocks > 0x7fffffff) return kInvalid;
     return with_cpl<FwdLaunch>(cpl, dim3(static_cast<unsigned>(blocks)), st, x, delta, w, s_out,
                                y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows,
@@ -349,7 +388,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_bwd(
   if (rows == 0) return kOk;
   if (!s || !rstd || !w || !dx) return kInvalid;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int cpl = (H / 4 + kWave - 1) / kWave;
+  const int cpl = (H / 4 + kWave * kWprBwd - 1) / (kWave * kWprBwd);
   const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(s, 16) && aligned(w, 16) &&
                    aligned(dypad, 16) && aligned(ds, 16) && aligned(dx, 16) && aligned(dy, 8) &&
                    aligned(ddelta, 8);
