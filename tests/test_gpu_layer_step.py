@@ -24,7 +24,9 @@ def rel_err(a, b):
 
 
 def reference_layer(s0, d0, w, wd, pos, batch, seq, cos, sin, amask):
-    """fp32 eager layer: the same wiring with every GEMM and the attention in fp32."""
+    """fp32 eager layer: the same wiring with every GEMM and the attention in fp32.  With LoRA
+    dropout the two branches draw their masks in the fused layer's order (q, then v) on the
+    padded [B, T, H] input, so a generator reseeded alike gives both layers the same masks."""
     H = s0.shape[1]
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
     padded = batch * seq
@@ -36,9 +38,18 @@ def reference_layer(s0, d0, w, wd, pos, batch, seq, cos, sin, amask):
     y = norm(s, w.input_norm)
     qkv = y @ torch.cat([wd["q"], wd["k"], wd["v"]]).t() + w.qkv_bias.float()
     y_pad = torch.zeros(padded, H, device=DEV).index_copy(0, pos, y)
-    rows = y_pad.index_select(0, pos)
-    lq = (rows @ w.lora_q[0].t()) @ w.lora_q[1].t() * w.scaling
-    lv = (rows @ w.lora_v[0].t()) @ w.lora_v[1].t() * w.scaling
+
+    def lora_rows():
+        x = y_pad
+        if w.dropout > 0:
+            x = torch.nn.functional.dropout(y_pad.view(batch, seq, H), w.dropout,
+                                            training=True).view(padded, H)
+        return x.index_select(0, pos)
+
+    rows_q = lora_rows()
+    rows_v = lora_rows()
+    lq = (rows_q @ w.lora_q[0].t()) @ w.lora_q[1].t() * w.scaling
+    lv = (rows_v @ w.lora_v[0].t()) @ w.lora_v[1].t() * w.scaling
     q = qkv[:, :nh * hd] + lq
     k = qkv[:, nh * hd:(nh + nkv) * hd]
     v = qkv[:, (nh + nkv) * hd:] + lv
@@ -64,10 +75,11 @@ def reference_layer(s0, d0, w, wd, pos, batch, seq, cos, sin, amask):
     return s2, d
 
 
-def test_decoder_layer_matches_fp32_eager():
-    batch, seq = 2, 64
-    lengths = (64, 40)
-    w = layer.synthetic_layer(DEV, seed=9)
+@pytest.mark.parametrize("lengths,dropout", [((64, 40), 0.0), ((64, 64), 0.0), ((64, 40), 0.1)])
+def test_decoder_layer_matches_fp32_eager(lengths, dropout):
+    print(f"decoder layer lengths={lengths} dropout={dropout}", flush=True)
+    batch, seq = len(lengths), 64
+    w = layer.synthetic_layer(DEV, seed=9, dropout=dropout)
     wd = {n: torch.from_numpy(dequant_state(getattr(w, n)).astype(np.float32)).to(DEV)
           for n in ("q", "k", "v", "o", "gate", "up", "down")}
     amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
@@ -84,6 +96,7 @@ def test_decoder_layer_matches_fp32_eager():
 
     s_in = s0.clone().requires_grad_(True)
     d_in = d0.clone().requires_grad_(True)
+    torch.manual_seed(1234)
     s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
                                layer.causal_pad_mask(amask))
     torch.autograd.backward([s, d], [gs, gd])
@@ -93,6 +106,7 @@ def test_decoder_layer_matches_fp32_eager():
 
     rs_in = s0.clone().requires_grad_(True)
     rd_in = d0.float().clone().requires_grad_(True)
+    torch.manual_seed(1234)
     rs, rd = reference_layer(rs_in, rd_in, w, wd, pos, batch, seq, cos, sin, amask)
     torch.autograd.backward([rs, rd], [gs, gd.float()])
     ref = [rs_in.grad, rd_in.grad] + [p.grad for p in (*w.lora_q, *w.lora_v)]

@@ -16,6 +16,13 @@ The reference takes these modules from a PEFT/bitsandbytes model; here they are 
 (`LayerWeights`), so one layer can be built from synthetic NF4 weights for measurement and
 tests.  The LoRA branch follows peft's `lora_B(lora_A(dropout(x))) * scaling` under fp16
 autocast (the matmuls in fp16, on the fp32 padded norm output so the dropout draws match).
+
+Without dropout the LoRA input fp16(y_pad[pos]) is exactly the fp16 norm output y that the
+projection GEMM reads (the norm kernel rounds the same fp32 value into both), so `QKVLora`
+runs the projection and both LoRA branches on y in one autograd node: A_q|A_v as one skinny
+GEMM, no padded fp32 copy, gather, casts or scatter-add, and in backward the LoRA input
+gradient accumulated into the projection's input-gradient GEMM.  The norm then writes no padded
+output at all.  With dropout the reference's path is kept (the padded layout fixes the draws).
 """
 
 import math
@@ -25,7 +32,7 @@ import torch
 
 from . import workloads
 from .mlp import fused_mlp
-from .nf4 import frozen_linear
+from .nf4 import frozen_linear, unpack_concat
 from .rmsnorm import add_rmsnorm
 from .rope import rope_pack
 
@@ -77,6 +84,56 @@ def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
         head_dim=head_dim, dropout=dropout, **nf4w)
 
 
+class QKVLora(torch.autograd.Function):
+    """(qkv, lora_q, lora_v) from the fp16 norm output y, for LoRA without dropout:
+    qkv = y @ [Wq;Wk;Wv]^T + b (frozen NF4, unpacked again in backward) and
+    lora_x = fp16(fp16(fp16(y @ fp16(A_x)^T) @ fp16(B_x)^T) * scaling), peft's branch under fp16
+    autocast (solution/model.py:195-206 with dropout p = 0)."""
+
+    @staticmethod
+    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights):
+        w = unpack_concat(weights, y16.device)
+        qkv = torch.nn.functional.linear(y16, w, bias)
+        del w
+        r = a_q.shape[0]
+        a16 = torch.cat([a_q.detach(), a_v.detach()]).to(torch.float16)
+        t = y16 @ a16.t()
+        bq16 = b_q.detach().to(torch.float16)
+        bv16 = b_v.detach().to(torch.float16)
+        lq = t[:, :r] @ bq16.t()
+        lv = t[:, r:] @ bv16.t()
+        if scaling != 1.0:
+            lq.mul_(scaling)
+            lv.mul_(scaling)
+        ctx.save_for_backward(y16, t, a16, bq16, bv16)
+        ctx.weights, ctx.scaling, ctx.rank = weights, scaling, r
+        return qkv, lq, lv
+
+    @staticmethod
+    def backward(ctx, g_qkv, g_lq, g_lv):
+        y16, t, a16, bq16, bv16 = ctx.saved_tensors
+        s, r = ctx.scaling, ctx.rank
+        m = y16.shape[0]
+        dt = torch.zeros((m, 2 * r), dtype=torch.float16, device=y16.device)
+        grads = [None, None, None, None]   # dA_q, dB_q, dA_v, dB_v
+        for i, (g, b16) in enumerate(((g_lq, bq16), (g_lv, bv16))):
+            if g is None:
+                continue
+            g = g.to(torch.float16)
+            if s != 1.0:
+                g = g * s                  # the grad of `* scaling` (fp16, as autograd does)
+            torch.mm(g, b16, out=dt[:, i * r:(i + 1) * r])
+            # fp16 products cast to the fp32 parameters, as autocast's backward gives them
+            grads[2 * i + 1] = (g.t() @ t[:, i * r:(i + 1) * r]).float()
+        da = (dt.t() @ y16).float()
+        grads[0], grads[2] = da[:r], da[r:]
+        dy = dt @ a16
+        if g_qkv is not None:
+            w = unpack_concat(ctx.weights, y16.device)
+            dy = torch.addmm(dy, g_qkv.to(torch.float16), w)
+        return dy, None, grads[0], grads[1], grads[2], grads[3], None, None
+
+
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
     """peft's B(A(dropout(x))) * scaling for the real tokens, fp16 matmuls (solution/model.py:
     195-206): the dropout runs on the padded fp32 norm output, A and B on the real rows."""
@@ -114,16 +171,23 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, mask):
     """(s, d): the residual stream and the MLP output of one layer (the next layer's delta)."""
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
-    s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
-    qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias)
-    lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
-    lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
-    del y_pad
+    if w.dropout == 0.0:
+        s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
+        qkv, lq, lv = QKVLora.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
+                                    (w.q, w.k, w.v))
+    else:
+        s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
+        qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias)
+        lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
+        lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
+        del y_pad
     q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
     del qkv, lq, lv
     a = attention(q, k, v, mask)
     del q, k, v
-    a = a.transpose(1, 2).reshape(padded, nh * hd).index_select(0, pos_idx)
+    a = a.transpose(1, 2).reshape(padded, nh * hd)
+    if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
+        a = a.index_select(0, pos_idx)
     o = frozen_linear(a, (w.o,), None)
     del a
     s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)
