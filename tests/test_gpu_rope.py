@@ -97,3 +97,56 @@ def test_inverse_map_is_cached_and_rebuilt():
     pos[0] = 7                                      # in-place change: the map is rebuilt
     inv2 = inverse_map(pos, 16)
     assert inv2 is not inv and int(inv2[7]) == 0 and int(inv2[0]) == -1
+
+
+def test_out_of_range_positions_are_skipped():
+    """Positions outside [0, B*T) are skipped by the forward pass (nothing written for that
+    token) and give zero gradient rows in the backward pass (the C ABI's bounds contract);
+    with B*T = 0 the forward pass writes nothing and the backward pass writes zeros."""
+    from testt_amd import _ext
+
+    lengths, seq, nh, nkv, d = (20, 12), 32, 12, 2, 128
+    qkv, lq, lv, pos = workloads.rope_inputs(lengths, seq, nh, nkv, d, seed=91)
+    cos, sin = workloads.rope_tables(seq, d)
+    m, w = pos.numel(), (nh + 2 * nkv) * d
+    bad = pos.clone()
+    bad[3], bad[17] = -1, 2 * seq + 5
+    keep = torch.ones(m, dtype=torch.bool)
+    keep[[3, 17]] = False
+    g = {n: t.to(DEV) for n, t in (("qkv", qkv), ("lq", lq), ("lv", lv), ("cos", cos),
+                                   ("sin", sin), ("bad", bad))}
+    sentinel = 0x3C00  # fp16 1.0: slots of the skipped tokens keep it
+    outs = [torch.full((2, h, seq, d), 1.0, dtype=torch.float16, device=DEV)
+            for h in (nh, nkv, nkv)]
+    st = torch.cuda.current_stream().cuda_stream
+    _ext.call("soupk_rope_pack_fwd", g["qkv"].data_ptr(), g["lq"].data_ptr(), g["lv"].data_ptr(),
+              _ext.DTYPE_F32, g["cos"].data_ptr(), g["sin"].data_ptr(), g["bad"].data_ptr(), None,
+              outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), m, 2, seq, nh, nkv, d,
+              st)
+    ref = rope_pack_fwd(qkv[keep], lq[keep], lv[keep], cos, sin, pos[keep], 2, seq, nh, nkv, d)
+    for got, r, name in zip(outs, ref, "qkv"):
+        got = got.cpu().permute(0, 2, 1, 3).reshape(2 * seq, -1, d)
+        r = r.permute(0, 2, 1, 3).reshape(2 * seq, -1, d)
+        assert_f16_ulp(got[pos[keep]], r[pos[keep]], 1, name)
+        skipped = got[pos[[3, 17]]].contiguous().view(torch.int16)
+        assert torch.all(skipped == sentinel), name
+
+    dq, dk, dv = (t.to(DEV) for t in workloads.rope_grads(2, seq, nh, nkv, d, seed=92))
+    dqkv = torch.full((m, w), 1.0, dtype=torch.float16, device=DEV)
+    _ext.call("soupk_rope_pack_bwd", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+              g["cos"].data_ptr(), g["sin"].data_ptr(), g["bad"].data_ptr(), dqkv.data_ptr(), m, 2,
+              seq, nh, nkv, d, st)
+    ref = rope_pack_bwd(qkv, None, None, cos, sin, pos, 2, seq, nh, nkv, d, dq.cpu(), dk.cpu(),
+                        dv.cpu())
+    got = dqkv.cpu()
+    assert_f16_ulp(got[keep], ref[keep], 1, "dqkv (valid rows)")
+    assert torch.all(got[~keep] == 0)
+
+    # B*T = 0: empty outputs and tables (null data pointers are allowed for them)
+    zpos = torch.tensor([0, 1], dtype=torch.int64, device=DEV)
+    _ext.call("soupk_rope_pack_fwd", g["qkv"].data_ptr(), None, None, _ext.DTYPE_F32, None,
+              None, zpos.data_ptr(), None, None, None, None, 2, 2, 0, nh, nkv, d, st)
+    dz = torch.full((2, w), 1.0, dtype=torch.float16, device=DEV)
+    _ext.call("soupk_rope_pack_bwd", None, None, None, None, None, zpos.data_ptr(),
+              dz.data_ptr(), 2, 2, 0, nh, nkv, d, st)
+    assert torch.all(dz.cpu() == 0)

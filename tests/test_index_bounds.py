@@ -5,7 +5,7 @@ When the item count is not a multiple of 256, the last workgroup holds threads p
 item; they must form only in-bounds addresses (they take the last item's indices).  This test
 replays that arithmetic for every thread of the launch grid with numpy and checks each global
 and LDS index against its buffer, for the GPU tests' shapes (including 53 tokens = 26.5
-workgroups).  No GPU is needed.
+workgroups) and head counts other than Qwen2.5-1.5B's.  No GPU is needed.
 """
 
 import numpy as np
@@ -26,7 +26,7 @@ def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
     tok_blocks = -(-total // THREADS)
     tid = np.arange(THREADS)
     worst = {"qkv": -1, "lq": -1, "lv": -1, "grad_q": -1, "grad_kv": -1, "out_q": -1,
-             "out_kv": -1, "lds": -1, "pos": -1, "ntok": 0}
+             "out_kv": -1, "lds": -1, "pos": -1, "tab": -1, "ntok": 0}
     pos = np.arange(rows) % slots                # any in-range positions
     for b in range(tok_blocks):
         g0 = b * THREADS
@@ -46,10 +46,14 @@ def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
         if v.any():
             lv = tok * NKV * D + (h - NH - NKV) * D + 8 * c + HALF + 7
             worst["lv"] = max(worst["lv"], int(lv[v].max()))
-        # table staging: i = tid, tid + 256, ... < ntok * D/2 float4
+        # table staging: i = tid, tid + 256, ... < ntok * D/2 float4; entry i is float4
+        # i % (D/2) of token tok0 + i // (D/2)'s row (cos, then sin), at t = pos % T
         stage = np.arange(0, ntok * (D // 2))
-        worst["pos"] = max(worst["pos"], int(tok0 + stage.max() // (D // 2)))
+        worst["pos"] = max(worst["pos"], int(tok0 + stage.max() // (D // 2)), int(tok.max()))
         worst["lds"] = max(worst["lds"], int(stage.max()))
+        t_st = pos[tok0 + stage // (D // 2)] % T
+        q4 = stage % (D // 2)
+        worst["tab"] = max(worst["tab"], int((t_st * D + 4 * (q4 % (D // 4)) + 3).max()))
         # after the barrier (active threads only)
         per = D // 2
         lds = (tok - tok0) * per + D // 4 + HALF // 4 + 2 * c + 1
@@ -85,11 +89,13 @@ def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
     return worst
 
 
+@pytest.mark.parametrize("heads", [(12, 2), (1, 1), (3, 0), (28, 4)])
 @pytest.mark.parametrize("lengths,seq", [((512,) * 4, 512), ((512, 152, 128, 96), 512),
                                          ((77, 75), 77), ((40, 0, 13), 64), ((30, 20), 32),
                                          ((1,), 1), ((3, 0, 0), 4)])
-def test_rope_vector_kernels_stay_in_bounds(lengths, seq):
-    NH, NKV, D = 12, 2, 128
+def test_rope_vector_kernels_stay_in_bounds(lengths, seq, heads):
+    NH, NKV = heads
+    D = 128
     B = len(lengths)
     rows = sum(lengths)
     w = _fwd_bwd_addresses(rows, B, seq, NH, NKV, D, with_inv=rows != B * seq)
@@ -97,6 +103,7 @@ def test_rope_vector_kernels_stay_in_bounds(lengths, seq):
     assert w["qkv"] < rows * (NH + 2 * NKV) * D
     assert w["lq"] < rows * NH * D and w["lv"] < rows * NKV * D
     assert w["pos"] < rows
+    assert w["tab"] < seq * D
     assert w["lds"] < MAX_TOK * D // 2
     assert w["out_q"] < B * NH * seq * D
     assert w["out_kv"] < B * NKV * seq * D

@@ -9,8 +9,12 @@
 // Mapping (gfx950): a work item is one 8-dim slice of one head of one token, together with the
 // matching 8 dims of the head's other half (the rotation partner), so a thread does two 16-byte
 // fp16 loads of qkv, up to four 16-byte loads of fp32 LoRA delta, two 16-byte stores, and reads
-// its cos/sin slices from LDS, where the workgroup staged the rows of its tokens once.  Items are numbered token-major,
-// so a wavefront reads a token's 4 KiB qkv row in full.  In the forward pass the workgroups
+// its cos/sin slices from LDS, where the workgroup staged the rows of its tokens once (one
+// 16-byte load per thread; eight per thread straight from the tables would make the vector
+// memory unit, not HBM, set the pace).  Items are numbered token-major, so a wavefront reads a
+// token's 4 KiB qkv row in full.  The token's position is loaded before the streaming loads
+// (its latency then overlaps theirs), and b = p / T, t = p % T use a 32-bit multiply-high
+// divider (a 64-bit division is a long instruction sequence on the path to the stores).  In the forward pass the workgroups
 // after the token workgroups write zeros at the padded positions that no token maps to
 // (pos_inv[p] < 0), replacing the three torch.zeros memsets of the reference.
 
@@ -32,7 +36,16 @@ struct RopeDims {
   int B, T, NH, NKV;
   uint32_t items;   // (NH + 2*NKV) * HALF/8 items per token or position
   FastDiv per_tok;  // divides by items
+  FastDiv per_seq;  // divides by T (positions are < B*T < 2^31, checked by the host)
 };
+
+// Position -> (b, t) for 0 <= p < B*T.
+__device__ __forceinline__ void split_pos(int64_t p, const RopeDims& dm, int& b, int& t) {
+  const uint32_t pu = static_cast<uint32_t>(p);
+  const uint32_t q = dm.per_seq.div(pu);
+  b = static_cast<int>(q);
+  t = static_cast<int>(pu - q * static_cast<uint32_t>(dm.T));
+}
 
 __device__ __forceinline__ void load8_f32(const float* p, float* v) {
   const f32x4 a = ld<kRopeNT>(reinterpret_cast<const f32x4*>(p));
@@ -66,7 +79,8 @@ __device__ __forceinline__ int stage_tables(f32x4* tab, const float* __restrict_
   for (int i = threadIdx.x; i < static_cast<int>(ntok) * 2 * Q; i += kRopeThreads) {
     const int j = i / (2 * Q), q = i % (2 * Q);
     const int64_t p = pos[tok0 + j];
-    const int t = (p >= 0 && p < slots) ? static_cast<int>(p % dm.T) : 0;
+    int b = 0, t = 0;  // (row 0 for an invalid position: the host guarantees T >= 1)
+    if (p >= 0 && p < slots) split_pos(p, dm, b, t);
     const float* src = q < Q ? cos_t + static_cast<int64_t>(t) * D + 4 * q
                              : sin_t + static_cast<int64_t>(t) * D + 4 * (q - Q);
     tab[i] = *reinterpret_cast<const f32x4*>(src);
@@ -100,7 +114,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     if (p >= slots || pos_inv[p] >= 0) return;
     const int it = static_cast<int>(g - p * dm.items);
     const int h = it / CPH, c = it % CPH;
-    const int b = static_cast<int>(p / dm.T), t = static_cast<int>(p % dm.T);
+    int b, t;
+    split_pos(p, dm, b, t);
     uint16_t* base;
     if (h < dm.NH)
       base = q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D;
@@ -126,6 +141,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
   const int h = it / CPH, c = it % CPH;
   const bool is_q = h < dm.NH, is_v = h >= dm.NH + dm.NKV;
 
+  const int64_t p = pos[tok];
   // Issue this thread's qkv and LoRA loads, then stage the tables while they are in flight.
   float x1[8], x2[8], l1[8], l2[8];
   const uint16_t* row = qkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
@@ -148,9 +164,9 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
   const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
   __syncthreads();
   if (!active) return;
-  const int64_t p = pos[tok];
   if (p < 0 || p >= slots) return;
-  const int b = static_cast<int>(p / dm.T), t = static_cast<int>(p % dm.T);
+  int b, t;
+  split_pos(p, dm, b, t);
   if (has_lora) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -208,8 +224,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
   const bool is_q = h < dm.NH, is_v = h >= dm.NH + dm.NKV;
   const int64_t p = pos[tok];
   const bool valid = p >= 0 && p < slots;
-  const int b = valid ? static_cast<int>(p / dm.T) : 0;
-  const int t = valid ? static_cast<int>(p % dm.T) : 0;
+  int b = 0, t = 0;
+  if (valid) split_pos(p, dm, b, t);
   float g1[8], g2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) g1[i] = g2[i] = 0.f;
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_generic_kernel(
     g2 = h2f(src[base + i + half]);
   }
   float o1 = g1, o2 = g2;
-  if (h < NH + NKV) {
+  if (valid && h < NH + NKV) {  // (an invalid position reads no table row; T may be 0)
     const float* cr = cos_t + static_cast<int64_t>(t) * D;
     const float* sr = sin_t + static_cast<int64_t>(t) * D;
     o1 = g1 * cr[i] + g2 * sr[i + half];
@@ -377,14 +393,16 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
   if (lora_dtype != SOUPK_DTYPE_F16 && lora_dtype != SOUPK_DTYPE_F32) return kInvalid;
   const int64_t slots = static_cast<int64_t>(B) * T;
   const int64_t zero_slots = pos_inv != nullptr ? slots : 0;
-  if ((rows == 0 && zero_slots == 0) || NH + 2 * NKV == 0) return kOk;
+  // No position exists (B*T = 0): no token has a destination, nothing to write.
+  if ((rows == 0 && zero_slots == 0) || NH + 2 * NKV == 0 || slots == 0) return kOk;
   if (!q || !k || !v || !cos || !sin || (rows > 0 && (!qkv || !pos))) return kInvalid;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int half = D / 2;
   const int heads = NH + 2 * NKV;
   const int lora_align = 16;
   // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens)
-  const bool vec = half == 64 && heads * (half / 8) >= 18 && aligned(qkv, 16) &&
+  const bool vec = half == 64 && heads * (half / 8) >= 18 && slots < (int64_t{1} << 31) &&
+                   aligned(qkv, 16) &&
                    aligned(cos, 16) && aligned(sin, 16) && aligned(q, 16) && aligned(k, 16) &&
                    aligned(v, 16) && aligned(lora_q, lora_align) && aligned(lora_v, lora_align);
   if (vec) {
@@ -392,6 +410,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
     dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
     dm.items = static_cast<uint32_t>(heads * (half / 8));
     dm.per_tok = FastDiv(dm.items);
+    dm.per_seq = FastDiv(static_cast<uint32_t>(T));
     const int64_t tok_items = rows * dm.items;
     const int64_t zero_items = zero_slots * dm.items;
     if (tok_items + zero_items >= (int64_t{1} << 31)) return kInvalid;
@@ -419,11 +438,17 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
     int32_t NH, int32_t NKV, int32_t D, void* stream) {
   if (rows < 0 || B < 0 || T < 0 || NH < 0 || NKV < 0 || D <= 0 || (D & 1)) return kInvalid;
   if (rows == 0 || NH + 2 * NKV == 0) return kOk;
-  if (!dqkv || !pos || !cos || !sin) return kInvalid;
+  // With B*T = 0 every position is out of range: the gradient rows are zeros and the (empty)
+  // tables are not read.
+  const bool no_slots = static_cast<int64_t>(B) * T == 0;
+  if (!dqkv || !pos || (!no_slots && (!cos || !sin))) return kInvalid;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int half = D / 2;
   const int heads = NH + 2 * NKV;
-  const bool vec = half == 64 && heads * (half / 8) >= 18 && aligned(dq, 16) &&
+  // (the vector kernel stages table row 0 for invalid positions, so it needs T >= 1)
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  const bool vec = half == 64 && heads * (half / 8) >= 18 && slots > 0 &&
+                   slots < (int64_t{1} << 31) && aligned(dq, 16) &&
                    aligned(dk, 16) && aligned(dv, 16) && aligned(cos, 16) && aligned(sin, 16) &&
                    aligned(dqkv, 16);
   if (vec) {
@@ -431,6 +456,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
     dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
     dm.items = static_cast<uint32_t>(heads * (half / 8));
     dm.per_tok = FastDiv(dm.items);
+    dm.per_seq = FastDiv(static_cast<uint32_t>(T));
     const int64_t items = rows * dm.items;
     if (items >= (int64_t{1} << 31)) return kInvalid;
     return launch_kernel(rope_pack_bwd_kernel<64>,
