@@ -51,7 +51,9 @@ def test_chunk_at_step_shape_from_gemm():
 
 
 @pytest.mark.parametrize("rows,vocab,scale", [(256, 151936, 1.0), (37, 5003, 3.0),
-                                              (3, 7, 1.0), (4, 1, 1.0)])
+                                              (3, 7, 1.0), (4, 1, 1.0),
+                                              (9, 151939, 2.0),    # rows not 16-byte aligned
+                                              (5, 200003, 1.0)])   # streaming form (> 20 x 8K)
 def test_chunk_synthetic(rows, vocab, scale):
     print(f"head rows={rows} vocab={vocab}", flush=True)
     z, targets = workloads.head_logits(rows, vocab, seed=rows + vocab, scale=scale)

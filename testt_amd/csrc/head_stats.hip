@@ -130,25 +130,73 @@ __device__ __forceinline__ void absorb_chunk(RowStats& st, const u32x4 w, int32_
   }
 }
 
-__device__ __forceinline__ void merge(RowStats& a, const RowStats& b) {
-  const float M = fmaxf(a.m, b.m);
-  const float fa = scale_to(a.m, M), fb = scale_to(b.m, M);
-  if (b.m > a.m || (b.m == a.m && b.ix < a.ix)) a.ix = b.ix;
-  a.se = a.se * fa + b.se * fb;
-  a.sd = a.sd * fa + b.sd * fb;
-  a.m = M;
+// ---- row reductions -------------------------------------------------------------------------
+// Lane-wise reductions without LDS round trips: four DPP steps combine the 16 lanes of each
+// row (quad swaps, then half-row and row mirrors: every lane ends with its row's result), and
+// v_readlane_b32 brings the four rows together.  The statistics are reduced as: the maximum
+// first; then every lane rescales its sums to that maximum (one exponential) and the sums are
+// added; the argmax is the smallest column among the lanes holding the maximum (first-maximum
+// rule).  (A butterfly of full merges would need an LDS permute and two exponentials per step.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppQuad1032 = 0xb1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4e;    // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuad1032>(v));
+  v = fmaxf(v, dpp_f<kDppQuad2301>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp_f<kDppQuad1032>(v);
+  v = v + dpp_f<kDppQuad2301>(v);
+  v = v + dpp_f<kDppHalfMirror>(v);
+  return v + dpp_f<kDppMirror>(v);
+}
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp_i<kDppQuad1032>(v));
+  v = min(v, dpp_i<kDppQuad2301>(v));
+  v = min(v, dpp_i<kDppHalfMirror>(v));
+  return min(v, dpp_i<kDppMirror>(v));
+}
+__device__ __forceinline__ float lanef(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-__device__ __forceinline__ void wave_merge(RowStats& s) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    RowStats t;
-    t.m = __shfl_xor(s.m, o, kWave);
-    t.se = __shfl_xor(s.se, o, kWave);
-    t.sd = __shfl_xor(s.sd, o, kWave);
-    t.ix = __shfl_xor(s.ix, o, kWave);
-    merge(s, t);
-  }
+// Statistics of 16 entries held by the 16 lanes of each row (every lane gets the result).
+__device__ __forceinline__ RowStats row16_stats(const RowStats& s) {
+  RowStats r;
+  r.m = row16_max(s.m);
+  const float f = scale_to(s.m, r.m);
+  r.se = row16_sum(s.se * f);
+  r.sd = row16_sum(s.sd * f);
+  r.ix = row16_min(s.m == r.m ? s.ix : INT_MAX);
+  return r;
+}
+
+// Statistics of the whole wavefront (uniform result).
+__device__ __forceinline__ RowStats wave_stats(const RowStats& s) {
+  RowStats r;
+  const float rm = row16_max(s.m);
+  r.m = fmaxf(fmaxf(lanef(rm, 0), lanef(rm, 16)), fmaxf(lanef(rm, 32), lanef(rm, 48)));
+  const float f = scale_to(s.m, r.m);
+  const float se = row16_sum(s.se * f), sd = row16_sum(s.sd * f);
+  const int ix = row16_min(s.m == r.m ? s.ix : INT_MAX);
+  r.se = (lanef(se, 0) + lanef(se, 16)) + (lanef(se, 32) + lanef(se, 48));
+  r.sd = (lanef(sd, 0) + lanef(sd, 16)) + (lanef(sd, 32) + lanef(sd, 48));
+  r.ix = min(min(__builtin_amdgcn_readlane(ix, 0), __builtin_amdgcn_readlane(ix, 16)),
+             min(__builtin_amdgcn_readlane(ix, 32), __builtin_amdgcn_readlane(ix, 48)));
+  return r;
 }
 
 // Row geometry: columns [0, lead) precede the first 16-byte boundary of the row, [tail0, V)
@@ -167,35 +215,31 @@ __device__ __forceinline__ RowSpan row_span(const uint16_t* base, int64_t V) {
 }
 
 // Workgroup merge of the per-thread statistics and the per-row outputs; returns the row's lse
-// to every thread.  Thread 0 reads z[target] here, before any thread overwrites the row, and
-// leaves it in *row_zt.  The sums carry a factor 2^lift (lse removes it; entropy is a ratio).
-__device__ float finish_row(RowStats st, RowStats* part, float* row_lse, float* row_zt,
-                            const uint16_t* base, int64_t row, int64_t tgt, bool labelled,
-                            bool tgt_ok, float* entropy, float* loss, int32_t* correct,
-                            float* lse_out, float lift) {
-  wave_merge(st);
+// to every thread.  Each wavefront reduces its lanes and posts the result in LDS; after one
+// barrier every wavefront reduces the 16 posted results itself (lanes l and l+16k read entry
+// l), so no second barrier is needed.  zt is z[target] (0 without a valid target), read by the
+// caller at the start of the kernel, before any thread overwrites the row.  The sums carry a
+// factor 2^lift (lse removes it; entropy is a ratio).
+__device__ float finish_row(RowStats st, RowStats* part, float zt, int64_t row, int64_t tgt,
+                            bool labelled, bool tgt_ok, float* entropy, float* loss,
+                            int32_t* correct, float* lse_out, float lift) {
+  static_assert(kHeadWaves == 16, "one posted entry per lane of a 16-lane row");
+  const RowStats w = wave_stats(st);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane == 0) part[wave] = st;
+  if (lane == 0) part[wave] = w;
   __syncthreads();
-  if (wave == 0) {
-    RowStats r = lane < kHeadWaves ? part[lane] : RowStats{-INFINITY, 0.f, 0.f, INT_MAX};
-    wave_merge(r);
-    if (lane == 0) {
-      const float lse = r.m + (logf(r.se) - lift * kLn2);
-      const int32_t arg = r.ix == INT_MAX ? 0 : r.ix;
-      entropy[row] = lse - r.sd / r.se;
-      const float zt = tgt_ok ? h2f(base[tgt]) : 0.f;
-      float l = 0.f;
-      if (labelled) l = tgt_ok ? lse - zt : NAN;
-      loss[row] = l;
-      *row_zt = zt;
-      correct[row] = (labelled && tgt_ok && static_cast<int64_t>(arg) == tgt) ? 1 : 0;
-      if (lse_out != nullptr) lse_out[row] = lse;
-      *row_lse = lse;
-    }
+  const RowStats r = row16_stats(part[lane % kHeadWaves]);
+  const float lse = r.m + (logf(r.se) - lift * kLn2);
+  if (threadIdx.x == 0) {
+    const int32_t arg = r.ix == INT_MAX ? 0 : r.ix;
+    entropy[row] = lse - r.sd / r.se;
+    float l = 0.f;
+    if (labelled) l = tgt_ok ? lse - zt : NAN;
+    loss[row] = l;
+    correct[row] = (labelled && tgt_ok && static_cast<int64_t>(arg) == tgt) ? 1 : 0;
+    if (lse_out != nullptr) lse_out[row] = lse;
   }
-  __syncthreads();
-  return *row_lse;
+  return lse;
 }
 
 // Gradient of one 8-column chunk: fp16((exp(z - lse) - [col == tgt]) * grad_scale).
@@ -293,7 +337,6 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
     float* __restrict__ lse_out, float grad_scale, int64_t V) {
   constexpr int P = CPT < kHeadPrefetch ? CPT : kHeadPrefetch;  // loads kept ahead of compute
   __shared__ RowStats part[kHeadWaves];
-  __shared__ float row_lse, row_zt;
   __shared__ f16 chunk_max[CPT * kHeadThreads];  // m_k of chunk k of thread t at [k*1024 + t]
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
@@ -311,9 +354,13 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   // The scalar head/tail columns are loaded first: waiting for a load waits for every load
   // issued before it, so they must not queue behind the chunk prefetch.
   // Both are unconditional, at clamped in-row columns, so that no branch forces an early wait.
+  // The target's logit is read here too (every thread, one address), for the loss and the
+  // gradient of the target column.
   const bool has_lead = tid < sp.lead, has_tail = sp.tail0 + tid < V;
   const float zlead = h2f(base[has_lead ? tid : 0]);
   const float ztail = h2f(base[has_tail ? sp.tail0 + tid : V - 1]);
+  const float zt_raw = h2f(base[tgt_ok ? tgt : 0]);
+  const float zt = tgt_ok ? zt_raw : 0.f;
   u32x4 w[CPT];
 #pragma unroll
   for (int k = 0; k < P; ++k)
@@ -355,8 +402,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   if (has_lead) absorb_col(st, zlead, tid, true, kLift);
   if (has_tail) absorb_col(st, ztail, static_cast<int32_t>(sp.tail0 + tid), false, kLift);
 
-  const float lse = finish_row(st, part, &row_lse, &row_zt, base, row, tgt, labelled, tgt_ok,
-                               entropy, loss, correct, lse_out, kLift);
+  const float lse = finish_row(st, part, zt, row, tgt, labelled, tgt_ok, entropy,
+                               loss, correct, lse_out, kLift);
   if (!labelled) return;
   const float shift = -lse * kLog2e;
   // F_k = 2^(m_k*log2e + fbase) = exp(m_k - lse) * grad_scale * 2^-kLift.
@@ -367,7 +414,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   const int thit = static_cast<int>((tgt - sp.lead) & 7);
   // The target column: (exp(z_t - lse) - 1) * grad_scale in fp32 (used by one lane only).
   const float gt =
-      (__builtin_amdgcn_exp2f(__builtin_fmaf(row_zt, kLog2e, shift)) - 1.0f) * grad_scale;
+      (__builtin_amdgcn_exp2f(__builtin_fmaf(zt, kLog2e, shift)) - 1.0f) * grad_scale;
   if (has_lead) grad_scalar(base, tid, tgt, shift, grad_scale);
   // Store offsets are recomputed from an opaque copy of tid*16 (one add per chunk) rather than
   // kept live from the load phase: CPT offset registers on top of the row would spill.
@@ -394,7 +441,6 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
     float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
     float* __restrict__ lse_out, float grad_scale, int64_t V) {
   __shared__ RowStats part[kHeadWaves];
-  __shared__ float row_lse, row_zt;
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
   const int64_t tgt = target[row];
@@ -404,6 +450,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
   const RowSpan sp = row_span(base, V);
   u32x4* vb = reinterpret_cast<u32x4*>(base + sp.lead);
   constexpr int64_t kStep = static_cast<int64_t>(kHeadThreads) * kStreamUnroll;
+  const float zt_raw = h2f(base[tgt_ok ? tgt : 0]);  // (before any write)
+  const float zt = tgt_ok ? zt_raw : 0.f;
 
   RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
   if (tid < sp.lead) {
@@ -427,8 +475,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
     const float z = h2f(base[sp.tail0 + tid]);
     absorb<1>(st, &z, static_cast<int32_t>(sp.tail0 + tid));
   }
-  const float lse = finish_row(st, part, &row_lse, &row_zt, base, row, tgt, labelled, tgt_ok,
-                               entropy, loss, correct, lse_out, 0.f);
+  const float lse = finish_row(st, part, zt, row, tgt, labelled, tgt_ok, entropy,
+                               loss, correct, lse_out, 0.f);
   if (!labelled) return;
   const float shift = -lse * kLog2e;
   const int64_t tc = (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? (tgt - sp.lead) >> 3 : -1;
