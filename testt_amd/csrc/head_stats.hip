@@ -131,48 +131,10 @@ __device__ __forceinline__ void absorb_chunk(RowStats& st, const u32x4 w, int32_
 }
 
 // ---- row reductions -------------------------------------------------------------------------
-// Lane-wise reductions without LDS round trips: four DPP steps combine the 16 lanes of each
-// row (quad swaps, then half-row and row mirrors: every lane ends with its row's result), and
-// v_readlane_b32 brings the four rows together.  The statistics are reduced as: the maximum
+// With the DPP row reductions of soupk_common.hpp.  The statistics are reduced as: the maximum
 // first; then every lane rescales its sums to that maximum (one exponential) and the sums are
 // added; the argmax is the smallest column among the lanes holding the maximum (first-maximum
 // rule).  (A butterfly of full merges would need an LDS permute and two exponentials per step.)
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
-}
-constexpr int kDppQuad1032 = 0xb1;    // quad_perm [1,0,3,2]
-constexpr int kDppQuad2301 = 0x4e;    // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141; // row_half_mirror
-constexpr int kDppMirror = 0x140;     // row_mirror
-
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kDppQuad1032>(v));
-  v = fmaxf(v, dpp_f<kDppQuad2301>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  return fmaxf(v, dpp_f<kDppMirror>(v));
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v = v + dpp_f<kDppQuad1032>(v);
-  v = v + dpp_f<kDppQuad2301>(v);
-  v = v + dpp_f<kDppHalfMirror>(v);
-  return v + dpp_f<kDppMirror>(v);
-}
-__device__ __forceinline__ int row16_min(int v) {
-  v = min(v, dpp_i<kDppQuad1032>(v));
-  v = min(v, dpp_i<kDppQuad2301>(v));
-  v = min(v, dpp_i<kDppHalfMirror>(v));
-  return min(v, dpp_i<kDppMirror>(v));
-}
-__device__ __forceinline__ float lanef(float v, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-
 // Statistics of 16 entries held by the 16 lanes of each row (every lane gets the result).
 __device__ __forceinline__ RowStats row16_stats(const RowStats& s) {
   RowStats r;

@@ -98,11 +98,49 @@ __device__ __forceinline__ void st(T* p, T v) {
   else *p = v;
 }
 
-// ---- wave64 reductions (butterfly: every lane ends with the result) -------------------------
+// ---- wave64 reductions (every lane ends with the result) -------------------------------------
+// Four DPP steps combine the 16 lanes of each row (quad swaps, then the half-row and row
+// mirrors: every lane ends with its row's result) and v_readlane_b32 brings the four rows
+// together: no LDS permute round trips (a shuffle butterfly needs six, one after another).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppQuad1032 = 0xb1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4e;     // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp_f<kDppQuad1032>(v);
+  v = v + dpp_f<kDppQuad2301>(v);
+  v = v + dpp_f<kDppHalfMirror>(v);
+  return v + dpp_f<kDppMirror>(v);
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuad1032>(v));
+  v = fmaxf(v, dpp_f<kDppQuad2301>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp_i<kDppQuad1032>(v));
+  v = min(v, dpp_i<kDppQuad2301>(v));
+  v = min(v, dpp_i<kDppHalfMirror>(v));
+  return min(v, dpp_i<kDppMirror>(v));
+}
+// Value of lane l (a wave-uniform constant or register) as a wave-uniform float.
+__device__ __forceinline__ float lanef(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  v = row16_sum(v);
+  return (lanef(v, 0) + lanef(v, 16)) + (lanef(v, 32) + lanef(v, 48));
 }
 
 // ---- exp via the hardware base-2 exponential ------------------------------------------------
