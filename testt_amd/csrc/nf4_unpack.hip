@@ -45,6 +45,15 @@ __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
 // straddles two blocks, and a tile spans whole blocks).  One tile per workgroup; the packed loads are issued
 // unconditionally (indices past the end clamped to the last dword, results dropped), because a
 // predicated load makes the compiler wait on it before issuing the next.
+// Cache policy of the packed codes and the fp16 output (1 = non-temporal: each is touched once).
+#ifndef SOUPK_NF4_NT_LD
+#define SOUPK_NF4_NT_LD 1
+#endif
+#ifndef SOUPK_NF4_NT_ST
+#define SOUPK_NF4_NT_ST 1
+#endif
+constexpr bool kNf4NtLd = SOUPK_NF4_NT_LD != 0, kNf4NtSt = SOUPK_NF4_NT_ST != 0;
+
 __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
     const uint32_t* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
     const float* __restrict__ code2, const float* __restrict__ absmax2,
@@ -57,7 +66,7 @@ __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
 #pragma unroll
   for (int k = 0; k < kNf4Dwords; ++k) {
     const int64_t d = d0 + k * kNf4Threads + threadIdx.x;
-    w[k] = __builtin_nontemporal_load(packed + (d < n_dwords ? d : n_dwords - 1));
+    w[k] = ld<kNf4NtLd>(packed + (d < n_dwords ? d : n_dwords - 1));
   }
   pair[threadIdx.x] = make_float2(nf4[threadIdx.x >> 4], nf4[threadIdx.x & 15]);
   const float off = offset[0];
@@ -76,7 +85,7 @@ __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
     const int64_t d = d0 + k * kNf4Threads + threadIdx.x;
     const float s = scale[(k * kNf4Threads + threadIdx.x) >> dword_block_shift];
     const u32x4 v = nf4_expand_dword(w[k], s, pair);
-    if (d < n_dwords) __builtin_nontemporal_store(v, out + d);
+    if (d < n_dwords) st<kNf4NtSt>(out + d, v);
   }
 }
 

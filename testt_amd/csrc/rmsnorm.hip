@@ -8,7 +8,7 @@
 // Mapping (gfx950): a row of H fp32 is H/4 float4 chunks, split over WPR wavefronts (2 forward,
 // 1 backward) owning alternate 64-chunk slices, so every load or store instruction of a wave
 // touches 1 KiB (fp32) or 512 B (fp16) of contiguous memory.  The row's values stay in registers
-// between the load, the wave64 butterfly reduction (combined across the row's waves in LDS) and
+// between the load, the wave64 reduction (DPP steps; combined across the row's waves in LDS) and
 // the stores.  In the forward pass two waves per row give 16 waves per CU at 2048 rows, which
 // hides HBM latency better than one (and 2 rows per wave, 4 waves per CU, ran 40% slower).  A
 // workgroup holds four rows.  In the forward pass extra workgroups after the row workgroups
@@ -34,19 +34,24 @@ constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // rows per workgroup
 #endif
 constexpr int kWprFwd = SOUPK_NORM_WPR_FWD;
 constexpr int kWprBwd = SOUPK_NORM_WPR_BWD;
-#ifndef SOUPK_NORM_NT
-#define SOUPK_NORM_NT 1
+#ifndef SOUPK_NORM_NT_LD
+#define SOUPK_NORM_NT_LD 1
+#endif
+#ifndef SOUPK_NORM_NT_ST
+#define SOUPK_NORM_NT_ST 1
 #endif
 // Row streams (x, delta, s, dy, dypad, ds in; s, y, ypad, dx, ddelta out) are touched once per
-// launch: non-temporal.  The weight, read by every row, stays cached.
-constexpr bool kNormNT = SOUPK_NORM_NT != 0;
+// launch: non-temporal (1).  The weight, read by every row, stays cached.  (Cached row loads
+// made the backward pass 2% faster on MI355X but the RoPE forward kernel that follows it in a
+// training step 10% slower.)
+constexpr bool kNormNtLd = SOUPK_NORM_NT_LD != 0, kNormNtSt = SOUPK_NORM_NT_ST != 0;
 
 __device__ __forceinline__ f32x4 load_h4(const uint16_t* p) {
-  const u32x2 w = ld<kNormNT>(reinterpret_cast<const u32x2*>(p));
+  const u32x2 w = ld<kNormNtLd>(reinterpret_cast<const u32x2*>(p));
   return f32x4{lo_h(w.x), hi_h(w.x), lo_h(w.y), hi_h(w.y)};
 }
 __device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
-  st<kNormNT>(reinterpret_cast<u32x2*>(p), u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)});
+  st<kNormNtSt>(reinterpret_cast<u32x2*>(p), u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)});
 }
 
 
@@ -75,7 +80,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
         (static_cast<int64_t>(blockIdx.x) - row_blocks) * (kRowsPerBlock * WPR) + wave;
     if (p >= pad_rows || pad_inv[p] >= 0) return;
     f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
-    for (int c = lane; c < nch; c += kWave) st<kNormNT>(dst + c, zero);
+    for (int c = lane; c < nch; c += kWave) st<kNormNtSt>(dst + c, zero);
     return;
   }
   const int rib = wave / WPR, sub = wave % WPR;  // row in block, wave within the row
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = min((j * WPR + sub) * kWave + lane, nch - 1);
-    v[j] = ld<kNormNT>(xr + c);
+    v[j] = ld<kNormNtLd>(xr + c);
     wv[j] = wr[c];
     if (delta != nullptr) d[j] = load_h4(delta + row * H + 4 * c);
   }
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
     for (int j = 0; j < CPL; ++j) {
       const int c = (j * WPR + sub) * kWave + lane;
       v[j] = v[j] + d[j];
-      if (live && c < nch) st<kNormNT>(sr + c, v[j]);
+      if (live && c < nch) st<kNormNtSt>(sr + c, v[j]);
     }
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
     if (c < nch) {
       const f32x4 o = (v[j] * rstd) * wv[j];
       store_h4(yr + 4 * c, o);
-      if (pr != nullptr) st<kNormNT>(pr + c, o);
+      if (pr != nullptr) st<kNormNtSt>(pr + c, o);
     }
   }
   if (sub == 0 && lane == 0) rstd_out[row] = rstd;
@@ -168,11 +173,11 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kerne
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = min((j * WPR + sub) * kWave + lane, nch - 1);
-    n[j] = ld<kNormNT>(sr + c);
+    n[j] = ld<kNormNtLd>(sr + c);
     wv[j] = wr[c];
     g[j] = dy != nullptr ? load_h4(dy + row * H + 4 * c) : zero;
-    gp[j] = pr != nullptr ? ld<kNormNT>(pr + c) : zero;
-    dd[j] = dsr != nullptr ? ld<kNormNT>(dsr + c) : zero;
+    gp[j] = pr != nullptr ? ld<kNormNtLd>(pr + c) : zero;
+    dd[j] = dsr != nullptr ? ld<kNormNtLd>(dsr + c) : zero;
   }
   const float rstd = rstd_in[row];
   float dot = 0.f;
@@ -201,7 +206,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kerne
     if (c < nch) {
       f32x4 o = (g[j] - n[j] * proj) * rstd;
       if (dsr != nullptr) o = o + dd[j];
-      st<kNormNT>(dxr + c, o);
+      st<kNormNtSt>(dxr + c, o);
       if (ddr != nullptr) store_h4(ddr + 4 * c, o);
     }
   }
