@@ -310,6 +310,38 @@ def time_layer(dev, steps, warmup):
     return out
 
 
+def copy_reference(cases, dev, reps=60, pool_mib=768):
+    """Mean duration of a plain non-temporal device copy (soupk_bench_copy) moving each kernel's
+    algorithmic byte count (half read, half written), timed like the kernels.  Every launch
+    copies a different slice of two pool_mib pools, so more than 600 MB of other traffic lies
+    between two uses of one slice and the Infinity Cache cannot serve them.  Returns
+    {case name: us}."""
+    lib = _ext.lib()
+    pool = pool_mib << 20
+    src = torch.empty(pool, dtype=torch.uint8, device=dev)
+    dst = torch.empty(pool, dtype=torch.uint8, device=dev)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    hip = HipEvents()
+    out = {}
+    for c in cases:
+        size = (c.nbytes // 2) // 4096 * 4096
+        slots = max(1, pool // size)
+        evs = [(hip.new(), hip.new()) for _ in range(reps)]
+        for r in range(reps + 10):
+            off = (r % slots) * size
+            if r >= 10:
+                lib.soupk_time_next_launch(*evs[r - 10])
+            st = lib.soupk_bench_copy(src.data_ptr() + off, dst.data_ptr() + off, size, sh)
+            if st:
+                raise _ext.SoupkError(f"soupk_bench_copy failed with status {st}")
+        torch.cuda.synchronize(dev)
+        ts = [hip.elapsed_us(a, b) for a, b in evs]
+        out[c.name] = sum(ts) / len(ts) * (c.nbytes / (2 * size))
+        hip.close()
+    del src, dst
+    return out
+
+
 def copy_peak(dev, mib=1024, reps=6):
     """Read+write GB/s of torch's device copy of `mib` MiB (the box's plain-copy reference)."""
     n = mib * (1 << 20) // 4
@@ -490,6 +522,7 @@ def main():
     log(f"timing {len(cases)} kernels: warmup {args.warmup}, steps {args.steps}")
     host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
+    copy_us = copy_reference(cases, dev)
     layer_t = None
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
@@ -506,9 +539,12 @@ def main():
         kernels[c.name] = {"kernel": c.kernel, "us_mean": round(mean_us, 3),
                            "us_median": round(median(c.times), 3),
                            "us_min": round(min(c.times), 3), "bytes": c.nbytes,
-                           "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+                           "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                           "copy_us": round(copy_us[c.name], 3),
+                           "copy_over_kernel": round(copy_us[c.name] / mean_us, 3)}
         log(f"{c.name:16s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
-            f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s")
+            f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s  (same-size copy "
+            f"{copy_us[c.name]:6.2f} us)")
     dom = max(cases, key=lambda c: sum(c.times))
     dom_us = sum(dom.times) / len(dom.times)
     dom_gbps = dom.nbytes / (dom_us * 1e-6) / 1e9
@@ -537,6 +573,10 @@ def main():
         "kernels": kernels,
         "layer": layer_t,
         "copy_peak_GBps": copy_gbps,
+        "copy_reference": "kernels[*].copy_us: a plain 16-byte non-temporal device copy "
+                          "(soupk_bench_copy) moving the kernel's algorithmic bytes, half read "
+                          "and half written, timed the same way; copy_over_kernel = copy_us / "
+                          "us_mean",
         "timing": "per-launch HIP events recorded by the kernel dispatch itself "
                   "(soupk_time_next_launch / hipExtLaunchKernelGGL), mean over steps",
         "step_wall_ms": round(wall * 1e3 / args.steps, 4),

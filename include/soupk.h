@@ -44,6 +44,14 @@ const char* soupk_status_string(int status);
 int soupk_time_next_launch(void* start_event, void* stop_event);
 
 /*
+ * Benchmark reference (no counterpart in the reference): a plain device-to-device copy of
+ * `bytes` (a positive multiple of 16; both pointers 16-byte aligned) with 16-byte non-temporal
+ * loads and stores.  bench.py times it at each kernel's byte count, so every kernel is reported
+ * beside what a bare copy of the same size reaches on the same GPU.
+ */
+int soupk_bench_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/*
  * NF4 double-quant unpack (replaces the launch of nf4_unpack_kernel, solution/nf4.py:27-45,
  * launched from unpack_into, solution/nf4.py:72-89).
  *   absmax[b] = fp32(fp32(code2[absmax_u8[b]] * absmax2[b / qblock2]) + offset[0])

@@ -58,6 +58,9 @@ def test_version_and_status_strings(lib):
     ("soupk_rope_pack_bwd", (None,) * 7 + (1, 1, 1, 1, 1, 7, None)),
     ("soupk_head_stats_grad", (None,) * 6 + (1.0, 1, 0, None)),
     ("soupk_index_inverse", (None, -1, None, 4, None)),
+    ("soupk_bench_copy", (None, None, 4096, None)),
+    ("soupk_bench_copy", (16, 32, 24, None)),        # not a multiple of 16 bytes
+    ("soupk_bench_copy", (16, 32, 0, None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

@@ -38,6 +38,7 @@ SIGNATURES = {
     "soupk_swiglu_bwd_inplace": [_p, _p, _i64, _i64, _p],
     "soupk_head_stats_grad": [_p, _p, _p, _p, _p, _p, _f32, _i64, _i64, _p],
     "soupk_time_next_launch": [_p, _p],
+    "soupk_bench_copy": [_p, _p, _i64, _p],
 }
 
 

@@ -63,10 +63,44 @@ __global__ __launch_bounds__(256) void scatter_rank_kernel(const int64_t* __rest
   if (p >= 0 && p < n_slots) inv[p] = static_cast<int32_t>(i);
 }
 
+// Plain streaming copy for the benchmark's size-matched reference: 16-byte non-temporal loads
+// and stores, 8 per thread (all loads issued before the stores), one tile of 256 x 8 chunks per
+// workgroup, consecutive lanes on consecutive chunks.
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 8;
+__global__ __launch_bounds__(kCopyThreads) void bench_copy_kernel(const u32x4* __restrict__ src,
+                                                                  u32x4* __restrict__ dst,
+                                                                  int64_t n) {
+  const int64_t base =
+      static_cast<int64_t>(blockIdx.x) * (kCopyThreads * kCopyUnroll) + threadIdx.x;
+  u32x4 v[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u)
+    v[u] = __builtin_nontemporal_load(src + min(base + u * kCopyThreads, n - 1));
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u)
+    if (base + u * kCopyThreads < n) __builtin_nontemporal_store(v[u], dst + base + u * kCopyThreads);
+}
+
 }  // namespace
 }  // namespace soupk
 
 using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_bench_copy(const void* src, void* dst,
+                                                                       int64_t bytes,
+                                                                       void* stream) {
+  if (bytes <= 0 || (bytes & 15) != 0 || !src || !dst) return kInvalid;
+  if ((reinterpret_cast<uintptr_t>(src) & 15) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15) != 0)
+    return kInvalid;
+  const int64_t n = bytes / 16;
+  const int64_t per = static_cast<int64_t>(kCopyThreads) * kCopyUnroll;
+  const int64_t grid = (n + per - 1) / per;
+  if (grid > 0x7fffffff) return kInvalid;
+  return launch_kernel(bench_copy_kernel, dim3(static_cast<unsigned>(grid)), dim3(kCopyThreads),
+                       static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                       static_cast<u32x4*>(dst), n);
+}
 
 extern "C" __attribute__((visibility("default"))) int soupk_abi_version(void) {
   return SOUPK_ABI_VERSION;
