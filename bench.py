@@ -292,10 +292,10 @@ def time_layer(dev, steps, warmup):
         if backward:
             torch.autograd.backward([s, d], [gs, gd])
 
-    for _ in range(warmup):
-        step(True)
     out = {}
-    for name, bwd in (("fwd_us", False), ("fwd_bwd_us", True)):
+    for name, bwd in (("fwd_bwd_us", True), ("fwd_us", False)):
+        for _ in range(warmup):         # (per mode, as in time_step)
+            step(bwd)
         torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -307,6 +307,51 @@ def time_layer(dev, steps, warmup):
     out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
                note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs and torch SDPA "
                     "in fp16, every other op a soupk kernel (testt_amd/layer.py)")
+    return out
+
+
+def time_step(dev, steps, warmup, n_layers=28):
+    """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model (testt_amd/model.py: 28
+    decoder layers, final norm, the chunked fused head loss over the 151,936-token vocabulary)
+    at B=4 x T=512 = 2048 real tokens, prompt tokens unlabelled: mean forward and
+    forward+backward wall time on the GPU (torch events around the whole step)."""
+    from testt_amd import model
+
+    B, T = workloads.BATCH, workloads.SEQ
+    m = model.synthetic_model(dev, n_layers=n_layers)
+    g = workloads.gen(12)
+    ids = torch.randint(0, workloads.VOCAB, (B, T), generator=g).to(dev)
+    mask = torch.ones(B, T, dtype=torch.int64, device=dev)
+    labels = ids.clone()
+    labels[:, :T // 4] = -100                        # prompt tokens carry no label
+    params = model.lora_parameters(m)
+
+    def step(backward):
+        for p in params:
+            p.grad = None
+        loss, _ = model.fused_forward(m, ids, mask, labels)
+        if backward:
+            loss.backward()
+
+    out = {}
+    # Each mode is warmed up before it is timed: the caching allocator's pool then fits that
+    # mode's allocation pattern, and no device allocation falls inside the timed steps.
+    for name, bwd in (("fwd_bwd_ms", True), ("fwd_ms", False)):
+        for _ in range(warmup):
+            step(bwd)
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step(bwd)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        out[name] = round(e0.elapsed_time(e1) / steps, 3)
+    out.update(tokens=B * T, batch=B, seq=T, layers=n_layers,
+               tokens_per_s=round(B * T / (out["fwd_bwd_ms"] * 1e-3), 1),
+               note="synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; "
+                    "hipBLASLt GEMMs and torch SDPA in fp16, every other op a soupk kernel")
+    del m
     return out
 
 
@@ -492,6 +537,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer timing")
+    ap.add_argument("--no-step", action="store_true",
+                    help="skip the whole-model training-step timing")
     ap.add_argument("--summarize-stats", nargs=3, metavar=("STATS_CSV", "BENCH_JSON", "CMD"),
                     help="print a markdown summary of a rocprofv3 --stats run and exit (CPU)")
     ap.add_argument("--summarize-pmc", nargs=5,
@@ -528,6 +575,12 @@ def main():
         log("timing one decoder layer fwd+bwd at 2048 tokens")
         layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
         log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us")
+    step_t = None
+    if not args.no_step:
+        log("timing one training step of the 28-layer model at 2048 tokens")
+        step_t = time_step(dev, 5, 2)
+        log(f"step fwd {step_t['fwd_ms']} ms, fwd+bwd {step_t['fwd_bwd_ms']} ms, "
+            f"{step_t['tokens_per_s']} tokens/s")
     kernels = {}
     total_us = 0.0
     total_bytes = 0
@@ -572,6 +625,7 @@ def main():
                             "HIP-event durations",
         "kernels": kernels,
         "layer": layer_t,
+        "step": step_t,
         "copy_peak_GBps": copy_gbps,
         "copy_reference": "kernels[*].copy_us: a plain 16-byte non-temporal device copy "
                           "(soupk_bench_copy) moving the kernel's algorithmic bytes, half read "

@@ -89,14 +89,17 @@ def test_golden_f64_fixture():
     assert_f16_ulp(new, torch.from_numpy(fx["new_logits"]), 1, "grad / untouched rows")
 
 
+@pytest.mark.parametrize("chunk", [256, 1000, head.CHUNK_ROWS])
 @pytest.mark.parametrize("rows,hidden,vocab", [(700, 64, 5003), (300, 256, 32000)])
-def test_fused_head_loss_end_to_end(rows, hidden, vocab):
-    """FusedHeadLoss over several 256-row chunks vs float64.  The oracle's logits come from a
+def test_fused_head_loss_end_to_end(rows, hidden, vocab, chunk, monkeypatch):
+    """FusedHeadLoss over one or several row chunks (256 rows: the reference's chunk, so the
+    labelled rows end inside a chunk; 1000; the default) vs float64.  The oracle's logits come from a
     CPU GEMM whose fp16 results differ by an ulp here and there from hipBLASLt's, so this test
     uses the reference's own end-to-end tolerances (solution/test_kernels.py:189-196): loss
     1e-4, entropy and token loss 1e-3, correct exact, hidden gradient 2e-2.  The north-star
     tolerances are held by the kernel-level tests above, which feed both sides the same
     logits."""
+    monkeypatch.setattr(head, "CHUNK_ROWS", chunk)
     g = torch.Generator().manual_seed(rows)
     h = torch.randn(rows, hidden, generator=g).to(torch.float16)
     w = (torch.randn(vocab, hidden, generator=g) * 0.2).to(torch.float16)
