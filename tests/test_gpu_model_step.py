@@ -19,6 +19,7 @@ import pytest
 import torch
 
 from oracle.nf4 import dequant_state, quantize_nf4
+from testt_amd import metrics
 from testt_amd import model as fused_model
 from testt_amd import workloads
 
@@ -165,9 +166,10 @@ def run_fused(fused, lora, ids, mask, labels, n_items):
     (loss * 1024).backward()
     loss = loss.detach()
     assert isinstance(stats, fused_model.HeadStats)
-    entropy = float(stats.entropy_sum / mask.sum())
-    accuracy = float(stats.correct / stats.labelled)
-    return float(loss), grads_of(lora), entropy, accuracy, stats.row_losses()
+    m = metrics.trl_metrics(stats, mask)          # the trainer glue's reduction of HeadStats
+    assert m["num_tokens_in_batch"] == int(mask.sum())
+    return float(loss), grads_of(lora), m["entropy"], m["mean_token_accuracy"], \
+        stats.row_losses()
 
 
 @pytest.mark.parametrize("dropout", [0.0, 0.05])
