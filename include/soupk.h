@@ -167,6 +167,35 @@ int soupk_head_stats_grad(uint16_t* logits, const int64_t* target, float* entrop
                           int32_t* correct, float* lse_out, float grad_scale, int64_t rows,
                           int64_t V, void* stream);
 
+/*
+ * Causal grouped-query attention, forward (widening beyond the reference's kernel set: it
+ * replaces torch's scaled_dot_product_attention in the layer loop of fused_forward,
+ * solution/model.py:246-247).  q [B, NH, T, D], k and v [B, NKV, T, D] fp16 (NH a multiple of
+ * NKV; D = 128); query i of row b attends to key j iff j <= i and key_valid[b*T + j] != 0
+ * (every key when key_valid is NULL).  Writes out[(b*T + t)*NH*D + h*D + d] fp16 (token-major,
+ * the layout the o-projection reads) and lse[(b*NH + h)*T + t] (natural log-sum-exp of the
+ * scaled scores; +inf for a query with no visible key, whose output is 0).  All fp16 pointers
+ * 16-byte aligned.
+ */
+int soupk_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const uint8_t* key_valid, uint16_t* out, float* lse, int32_t B,
+                        int32_t T, int32_t NH, int32_t NKV, int32_t D, float scale,
+                        void* stream);
+
+/*
+ * Causal grouped-query attention, backward (the gradient half of the same replacement).  Inputs
+ * as soupk_attention_fwd, plus its out and lse and dout (the output gradient, token-major like
+ * out).  Writes dq [B, NH, T, D] and dk, dv [B, NKV, T, D] fp16 (dk, dv summed over each
+ * key/value head's NH/NKV query heads in a fixed order: deterministic).  workspace: fp32 device
+ * memory of  round_up(B*NH*T, 4) + 2*B*NH*T*D  floats, 16-byte aligned (D and the partial dK,
+ * dV of every query head).
+ */
+int soupk_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const uint8_t* key_valid, const uint16_t* out, const uint16_t* dout,
+                        const float* lse, float* workspace, uint16_t* dq, uint16_t* dk,
+                        uint16_t* dv, int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D,
+                        float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
