@@ -305,8 +305,8 @@ def time_layer(dev, steps, warmup):
         torch.cuda.synchronize(dev)
         out[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 1)
     out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
-               note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs and torch SDPA "
-                    "in fp16, every other op a soupk kernel (testt_amd/layer.py)")
+               note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs in fp16, "
+                    "every other op (attention included) a soupk kernel (testt_amd/layer.py)")
     return out
 
 
@@ -350,7 +350,7 @@ def time_step(dev, steps, warmup, n_layers=28):
     out.update(tokens=B * T, batch=B, seq=T, layers=n_layers,
                tokens_per_s=round(B * T / (out["fwd_bwd_ms"] * 1e-3), 1),
                note="synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; "
-                    "hipBLASLt GEMMs and torch SDPA in fp16, every other op a soupk kernel")
+                    "hipBLASLt GEMMs in fp16, every other op (attention included) a soupk kernel")
     del m
     return out
 

@@ -98,7 +98,7 @@ def test_decoder_layer_matches_fp32_eager(lengths, dropout):
     d_in = d0.clone().requires_grad_(True)
     torch.manual_seed(1234)
     s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
-                               layer.causal_pad_mask(amask))
+                               layer.key_valid_of(amask))
     torch.autograd.backward([s, d], [gs, gd])
     fused = [s_in.grad, d_in.grad] + [p.grad for p in (*w.lora_q, *w.lora_v)]
     for p in (*w.lora_q, *w.lora_v):

@@ -59,6 +59,52 @@ def test_fused_mlp_matches_dequantized_reference(hidden, inter, rows):
     close(x.grad, xr.grad)
 
 
+def test_fused_mlp_recompute_modes_agree(monkeypatch):
+    """Keeping the forward's gate/up buffer or recomputing it in backward (RECOMPUTE_GATE_UP),
+    and keeping the unpacked weights or unpacking again (nf4.KEEP_UNPACKED_FOR_BACKWARD), run
+    the same GEMMs on the same inputs: identical outputs and input gradients.  With the
+    buffer kept, a second backward through the graph raises (the first one overwrote it)."""
+    gate, _ = quantized(256, 128, 6)
+    up, _ = quantized(256, 128, 7)
+    down, _ = quantized(128, 256, 8)
+    g = torch.Generator().manual_seed(2)
+    x0 = torch.randn(33, 128, generator=g).to(torch.float16).to(DEV)
+    grad = torch.randn(33, 128, generator=g).to(torch.float16).to(DEV)
+    results = []
+    for recompute, keep in ((True, False), (False, True), (False, False)):
+        monkeypatch.setattr(mlp, "RECOMPUTE_GATE_UP", recompute)
+        monkeypatch.setattr(nf4, "KEEP_UNPACKED_FOR_BACKWARD", keep)
+        x = x0.clone().requires_grad_(True)
+        out = mlp.fused_mlp(x, gate, up, down)
+        out.backward(grad, retain_graph=True)
+        results.append((out.detach(), x.grad.clone()))
+        if recompute:
+            out.backward(grad)         # recomputed: a second backward is allowed
+            assert torch.equal(x.grad, 2 * results[-1][1])
+        else:
+            with pytest.raises(RuntimeError, match="RECOMPUTE_GATE_UP"):
+                out.backward(grad)
+    for out, grad in results[1:]:
+        assert torch.equal(results[0][0], out)
+        assert torch.equal(results[0][1], grad)
+
+
+@pytest.mark.parametrize("keep", [True, False])
+def test_frozen_linear_keep_modes_agree(monkeypatch, keep):
+    """The backward GEMM reads the forward's unpacked weight or a fresh unpack: same bits."""
+    w, _ = quantized(192, 128, 9)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(17, 128, generator=g).to(torch.float16).to(DEV).requires_grad_(True)
+    grad = torch.randn(17, 192, generator=g).to(torch.float16).to(DEV)
+    monkeypatch.setattr(nf4, "KEEP_UNPACKED_FOR_BACKWARD", keep)
+    out = nf4.frozen_linear(x, (w,))
+    out.backward(grad, retain_graph=True)
+    first = x.grad.clone()
+    out.backward(grad)                 # a second backward unpacks again when nothing is kept
+    assert torch.equal(x.grad, 2 * first)
+    assert torch.equal(first, grad @ nf4.unpack_concat((w,), DEV))
+
+
 def test_frozen_linear_qkv_with_bias():
     q, q_ref = quantized(1536, 1536, 6)
     k, k_ref = quantized(256, 1536, 7)

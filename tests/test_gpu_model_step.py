@@ -59,10 +59,11 @@ def nf4_of(w16, seed):
     return p, torch.from_numpy(dequant_state(p).astype(np.float16))
 
 
-def build(dropout):
+def build(dropout, hidden=256):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
-    cfg = Qwen2Config(vocab_size=1000, hidden_size=256, intermediate_size=512,
+    # 4 heads: hidden 256 gives head dim 64 (torch SDPA), 512 head dim 128 (the HIP attention)
+    cfg = Qwen2Config(vocab_size=1000, hidden_size=hidden, intermediate_size=512,
                       num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
                       max_position_embeddings=256, tie_word_embeddings=True)
     cfg._attn_implementation = "sdpa"
@@ -172,10 +173,11 @@ def run_fused(fused, lora, ids, mask, labels, n_items):
         stats.row_losses()
 
 
-@pytest.mark.parametrize("dropout", [0.0, 0.05])
-def test_fused_step_matches_unpatched_model(dropout):
-    print(f"model step: tiny Qwen2 + NF4 + LoRA r=16, lora dropout {dropout}", flush=True)
-    hf, fused, lora = build(dropout)
+@pytest.mark.parametrize("dropout,hidden", [(0.0, 256), (0.05, 256), (0.0, 512), (0.05, 512)])
+def test_fused_step_matches_unpatched_model(dropout, hidden):
+    print(f"model step: tiny Qwen2 (hidden {hidden}) + NF4 + LoRA r=16, lora dropout {dropout}",
+          flush=True)
+    hf, fused, lora = build(dropout, hidden)
     ids, mask, labels = batch()
     n_items = (labels[:, 1:] != -100).sum()
     ref = run_unpatched(hf, lora, ids, mask, labels, n_items)

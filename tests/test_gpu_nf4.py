@@ -51,6 +51,20 @@ def test_unpack_concat_quantized_weights():
     assert np.array_equal(bits(out), ref.view(np.int16))
 
 
+def test_cached_plan_follows_replaced_state():
+    """unpack_into caches each weight's checked kernel arguments; replacing a state tensor
+    (new absmax codes, a new offset) must be seen by the next unpack."""
+    w = workloads.nf4_weight(64, 256, seed=43, device=DEV)
+    out = torch.empty(64, 256, dtype=torch.float16, device=DEV)
+    nf4.unpack_into(w, out)
+    assert np.array_equal(bits(out), dequant_state(w).view(np.int16))
+    st = w.quant_state
+    st.absmax = torch.flip(st.absmax, [0]).contiguous()
+    st.offset = 0.25
+    nf4.unpack_into(w, out)
+    assert np.array_equal(bits(out), dequant_state(w).view(np.int16))
+
+
 def test_golden_fixture_through_abi():
     fx = np.load(GOLDEN)
     t = {k: torch.from_numpy(np.ascontiguousarray(fx[k])).to(DEV)

@@ -5,8 +5,9 @@ functions, autograd.Function signatures and constants):
 
 - nf4.py      NF4 double-quant unpack + frozen 4-bit linear (hipBLASLt GEMM)
 - rmsnorm.py  residual add + RMSNorm, forward and backward
-- rope.py     LoRA add + rotary + scatter of q/k/v to SDPA's layout, forward and backward
-- mlp.py      gate/up GEMM + SwiGLU in fp16 + recompute in backward
+- rope.py     LoRA add + rotary + scatter of q/k/v to the attention's layout, fwd and bwd
+- attention.py causal GQA flash attention (head dim 128), forward and backward
+- mlp.py      gate/up GEMM + SwiGLU in fp16, gate/up kept (or recomputed) for backward
 - head.py     fused head + loss + entropy + accuracy + per-row loss, no full logits
 - warmup.py   start/wait hooks (the kernels are prebuilt, nothing compiles at run time)
 
@@ -15,7 +16,7 @@ include/soupk.h (`python -m testt_amd.build_ext`) and called through ctypes with
 current stream.  There is no CPU or Triton path.
 """
 
-__all__ = ["apply", "nf4", "rmsnorm", "rope", "mlp", "head", "warmup"]
+__all__ = ["apply", "nf4", "rmsnorm", "rope", "attention", "mlp", "head", "warmup"]
 
 
 def apply():

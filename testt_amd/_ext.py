@@ -101,8 +101,10 @@ def ptr(tensor):
 
 
 def stream_of(tensor):
-    """The current HIP stream of the tensor's device, as a raw handle."""
-    return torch.cuda.current_stream(tensor.device).cuda_stream
+    """The current HIP stream of the tensor's device, as a raw handle (torch's raw-stream query:
+    the same handle as torch.cuda.current_stream(device).cuda_stream, without building a
+    Stream object on every kernel call)."""
+    return torch._C._cuda_getCurrentRawStream(tensor.device.index)
 
 
 def require(tensor, name, dtype=None, ndim=None, device=None):

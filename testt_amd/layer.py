@@ -7,7 +7,7 @@ real (non-pad) tokens:
   qkv        = y @ [Wq;Wk;Wv]^T + b               NF4 unpack (HIP) + one hipBLASLt GEMM
   lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v, PyTorch (fp16 GEMMs)
   q, k, v    = rope_pack(qkv, lq, lv)             LoRA add + RoPE + pack (HIP)
-  a          = SDPA(q, k, v, causal [+ pad mask])  PyTorch scaled_dot_product_attention (GQA)
+  a          = attention(q, k, v, causal + pad)   causal GQA flash attention (HIP), token-major
   o          = a[real tokens] @ Wo^T              NF4 unpack (HIP) + hipBLASLt
   s, y2, _   = add_rmsnorm(s, o)                  residual add + post-attention RMSNorm (HIP)
   d          = mlp(y2)                            NF4 unpack + GEMM + SwiGLU (HIP) + GEMM
@@ -30,9 +30,10 @@ from dataclasses import dataclass
 
 import torch
 
+from . import attention as _attention
 from . import workloads
 from .mlp import fused_mlp
-from .nf4 import frozen_linear, unpack_concat
+from .nf4 import frozen_linear, keep_for_backward, unpack_concat, unpacked_for_backward
 from .rmsnorm import add_rmsnorm
 from .rope import rope_pack
 
@@ -86,7 +87,8 @@ def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
 
 class QKVLora(torch.autograd.Function):
     """(qkv, lora_q, lora_v) from the fp16 norm output y, for LoRA without dropout:
-    qkv = y @ [Wq;Wk;Wv]^T + b (frozen NF4, unpacked again in backward) and
+    qkv = y @ [Wq;Wk;Wv]^T + b (frozen NF4; the unpacked weight kept for backward, or unpacked
+    again there: nf4.KEEP_UNPACKED_FOR_BACKWARD) and
     lora_x = fp16(fp16(fp16(y @ fp16(A_x)^T) @ fp16(B_x)^T) * scaling), peft's branch under fp16
     autocast (solution/model.py:195-206 with dropout p = 0)."""
 
@@ -94,6 +96,7 @@ class QKVLora(torch.autograd.Function):
     def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights):
         w = unpack_concat(weights, y16.device)
         qkv = torch.nn.functional.linear(y16, w, bias)
+        keep_for_backward(ctx, w)
         del w
         r = a_q.shape[0]
         a16 = torch.cat([a_q.detach(), a_v.detach()]).to(torch.float16)
@@ -129,7 +132,7 @@ class QKVLora(torch.autograd.Function):
         grads[0], grads[2] = da[:r], da[r:]
         dy = dt @ a16
         if g_qkv is not None:
-            w = unpack_concat(ctx.weights, y16.device)
+            w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy = torch.addmm(dy, g_qkv.to(torch.float16), w)
         return dy, None, grads[0], grads[1], grads[2], grads[3], None, None
 
@@ -145,14 +148,33 @@ def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
     return (rows @ a.to(torch.float16).t()) @ b.to(torch.float16).t() * scaling
 
 
-def attention(q, k, v, mask):
-    """SDPA over the padded [B, heads, T, D] layout with grouped key/value heads."""
-    scale = 1.0 / math.sqrt(q.shape[-1])
+def attention(q, k, v, key_valid):
+    """Causal GQA attention of the padded [B, heads, T, D] layout -> token-major [B*T, NH*D].
+
+    Query i of row b sees key j iff j <= i and the key is real (key_valid[b, j] != 0; every key
+    when key_valid is None): transformers' causal + padding mask.  Head dim 128 (Qwen2.5) runs
+    testt_amd/csrc/attention.hip; other head dims torch's scaled_dot_product_attention on the
+    same mask, as the reference runs every shape (solution/model.py:246-247)."""
+    B, NH, T, D = q.shape
+    if _attention.supported(q, k, v):
+        return _attention.causal_attention(q, k, v, key_valid)
+    mask = None if key_valid is None else causal_pad_mask(key_valid)
+    scale = 1.0 / math.sqrt(D)
     if mask is None:
-        return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
-                                                                scale=scale, enable_gqa=True)
-    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scale,
-                                                            enable_gqa=True)
+        a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                             scale=scale, enable_gqa=True)
+    else:
+        a = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask,
+                                                             scale=scale, enable_gqa=True)
+    return a.transpose(1, 2).reshape(B * T, NH * D)
+
+
+def key_valid_of(attention_mask):
+    """uint8 [B, T] key-is-real flags of a [B, T] attention_mask, or None when nothing is
+    padded (the kernels then skip the flag reads)."""
+    if bool(attention_mask.all()):
+        return None
+    return (attention_mask != 0).to(torch.uint8).contiguous()
 
 
 def causal_pad_mask(attention_mask):
@@ -167,8 +189,10 @@ def causal_pad_mask(attention_mask):
     return mask | (eye & ~attention_mask.bool()[:, None, :, None])
 
 
-def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, mask):
-    """(s, d): the residual stream and the MLP output of one layer (the next layer's delta)."""
+def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
+    """(s, d): the residual stream and the MLP output of one layer (the next layer's delta).
+    key_valid: uint8 [batch, seq] (key_valid_of(attention_mask)), or None when nothing is
+    padded."""
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
     if w.dropout == 0.0:
@@ -183,9 +207,8 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, mask):
         del y_pad
     q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
     del qkv, lq, lv
-    a = attention(q, k, v, mask)
+    a = attention(q, k, v, key_valid)
     del q, k, v
-    a = a.transpose(1, 2).reshape(padded, nh * hd)
     if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
         a = a.index_select(0, pos_idx)
     o = frozen_linear(a, (w.o,), None)

@@ -4,18 +4,26 @@ Drop-in for solution/mlp.py.
 - gate and up are one hipBLASLt GEMM against both weights unpacked into one [2I, H] buffer;
 - testt_amd/csrc/swiglu.hip reads the fp16 [tokens, 2I] result and writes silu(g) * u in fp16
   (computed in fp32, rounded once to fp16 where the down projection reads it);
-- nothing of size [tokens, I] is saved: backward recomputes gate/up from the saved fp16 input
-  (one GEMM) and the in-place backward kernel turns the incoming gradient into the gate/up
-  gradients in the same buffer, so the input gradient is again a single GEMM.
+- backward turns the incoming gradient into the gate/up gradients in place, in the [tokens, 2I]
+  gate/up buffer, so the input gradient is again a single GEMM.
+
+RECOMPUTE_GATE_UP (solution/mlp.py:27) chooses where that buffer comes from.  The reference
+recomputes it in backward (one more [tokens, H] x [H, 2I] GEMM) to keep nothing of size
+[tokens, I] alive between the passes.  On MI355X the buffer of the 2048-token step is 73 MB per
+layer (2 GB for 28 layers, under 1% of 288 GB of HBM) while the recompute GEMM is 113 GFLOP
+per layer, so the default here keeps the forward's buffer; True restores the reference's
+memory profile.  Both give identical results (the same GEMM on the same inputs).  The kept
+buffer is consumed by the in-place backward, so a second backward through the same graph
+raises instead of reading gradients as activations.
 """
 
 import torch
 
 from . import _ext
 from ._common import kernels_ok
-from .nf4 import unpack_concat
+from .nf4 import keep_for_backward, unpack_concat
 
-RECOMPUTE_GATE_UP = True  # keep only the [tokens, H] input; recompute gate/up in backward
+RECOMPUTE_GATE_UP = False  # True: keep only the [tokens, H] input, recompute gate/up
 # Columns one workgroup step covers per row in the reference's tiling (solution/mlp.py:28);
 # the HIP kernels stream the flat [rows, I] space in 16-byte chunks instead.
 COLS_PER_PROGRAM = 1024
@@ -55,9 +63,10 @@ class FusedNF4MLP(torch.autograd.Function):
     def forward(ctx, x, gate_w, up_w, down_w):
         gate_up = unpack_concat((gate_w, up_w), x.device)
         gu = torch.matmul(x, gate_up.t())
-        del gate_up
         act = gated_silu(gu)
-        if RECOMPUTE_GATE_UP:
+        ctx.recompute = RECOMPUTE_GATE_UP
+        ctx.consumed = False
+        if ctx.recompute:
             del gu
             ctx.save_for_backward(x)
         else:
@@ -65,6 +74,7 @@ class FusedNF4MLP(torch.autograd.Function):
         down = unpack_concat((down_w,), x.device)
         out = torch.matmul(act, down.t())
         ctx.weights = (gate_w, up_w, down_w)
+        keep_for_backward(ctx, (gate_up, down))
         return out
 
     @staticmethod
@@ -75,11 +85,24 @@ class FusedNF4MLP(torch.autograd.Function):
         saved = ctx.saved_tensors
         x = saved[0]
         grad_out = grad_out.to(torch.float16)
-        down = unpack_concat((down_w,), grad_out.device)
+        kept = getattr(ctx, "unpacked", None)
+        ctx.unpacked = None
+        gate_up, down = kept if kept is not None else (None, None)
+        if down is None:
+            down = unpack_concat((down_w,), grad_out.device)
         dact = torch.matmul(grad_out, down)
         del down
-        gate_up = unpack_concat((gate_w, up_w), grad_out.device)
-        gu = torch.matmul(x, gate_up.t()) if RECOMPUTE_GATE_UP else saved[1]
+        if gate_up is None:
+            gate_up = unpack_concat((gate_w, up_w), grad_out.device)
+        if ctx.recompute:
+            gu = torch.matmul(x, gate_up.t())
+        else:
+            if ctx.consumed:
+                raise RuntimeError("FusedNF4MLP: backward ran twice through a graph whose kept "
+                                   "gate/up buffer the first backward overwrote; set "
+                                   "mlp.RECOMPUTE_GATE_UP = True to backpropagate twice")
+            ctx.consumed = True
+            gu = saved[1]
         gated_silu_backward_(dact, gu)
         del dact
         grad_x = torch.matmul(gu, gate_up)

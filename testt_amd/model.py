@@ -5,7 +5,7 @@ Mirrors the reference's fused_forward (solution/model.py:209-279) and HeadStats
 pos_idx = attention_mask.nonzero(), solution/model.py:220):
 
   s          = embedding(input_ids[real])             fp16 table -> fp32 rows
-  per layer  : testt_amd.layer.decoder_layer          norm, QKV + LoRA, RoPE pack, SDPA, o-proj,
+  per layer  : testt_amd.layer.decoder_layer          norm, QKV + LoRA, RoPE pack, attention, o-proj,
                                                        norm, NF4 MLP (the reference's loop body,
                                                        solution/model.py:235-255)
   y          = add_rmsnorm(s, d, final norm)           (solution/model.py:257)
@@ -99,11 +99,11 @@ def fused_forward(model, input_ids, attention_mask, labels, num_items_in_batch=N
     ids = input_ids.reshape(-1).index_select(0, pos_idx)
     s = torch.nn.functional.embedding(ids, model.embed).float()
     cos, sin = rotary_tables(model.inv_freq, seq)
-    mask = _layer.causal_pad_mask(attention_mask)
+    key_valid = _layer.key_valid_of(attention_mask)
 
     delta = None
     for w in model.layers:
-        s, delta = _layer.decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, mask)
+        s, delta = _layer.decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid)
     _, y, _ = add_rmsnorm(s, delta, model.final_norm, model.eps)
     del s, delta
 

@@ -23,6 +23,27 @@ from ._common import kernels_ok
 # (solution/nf4.py:24 names the per-program tile of the Triton kernel the same way.)
 BYTES_PER_PROGRAM = 16384
 
+# The reference unpacks every frozen weight twice per step, in forward and again in backward
+# (solution/nf4.py:125, solution/mlp.py:105-108), so that no fp16 weight outlives its GEMM.
+# On MI355X the fp16 weights of all 28 layers of Qwen2.5-1.5B are 2.6 GB (under 1% of 288 GB
+# of HBM), so by default the forward's unpacked weight is kept for the backward GEMM and
+# dropped there: one unpack pass per step instead of two, identical results (the unpack is
+# deterministic).  False restores the reference's memory profile.
+KEEP_UNPACKED_FOR_BACKWARD = True
+
+
+def keep_for_backward(ctx, weight):
+    """Hold the forward's unpacked fp16 `weight` in ctx when a backward will read it."""
+    keep = KEEP_UNPACKED_FOR_BACKWARD and torch.is_grad_enabled() and any(ctx.needs_input_grad)
+    ctx.unpacked = weight if keep else None
+
+
+def unpacked_for_backward(ctx, weights, device):
+    """The weight the forward kept (released from ctx), else `weights` unpacked again."""
+    weight = getattr(ctx, "unpacked", None)
+    ctx.unpacked = None
+    return weight if weight is not None else unpack_concat(weights, device)
+
 
 def _quant_state(weight):
     return getattr(weight, "quant_state", None)
@@ -62,38 +83,65 @@ def _f32(t):
     return t if t.dtype == torch.float32 and t.is_contiguous() else t.float().contiguous()
 
 
+def _plan(weight, device):
+    """The kernel arguments of one weight on `device` (pointers into its quant state, converted
+    tables kept alive), checked once and cached on the weight; None for a layout or device the
+    kernel does not take.  The cache is keyed by the addresses of the state tensors, so a
+    weight whose state is replaced is checked again."""
+    state = _quant_state(weight)
+    try:
+        key = (device, weight.data.data_ptr(), state.absmax.data_ptr(), state.code.data_ptr(),
+               state.state2.code.data_ptr(), state.state2.absmax.data_ptr(), id(state.offset))
+    except AttributeError:
+        return None
+    cached = getattr(weight, "_soupk_plan", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    if not (supports_fast_unpack(weight) and _on_device(weight, device)):
+        return None
+    if state.absmax.dtype != torch.uint8:
+        raise TypeError(f"nested absmax must be uint8, got {state.absmax.dtype}")
+    n_bytes = weight.data.numel()
+    absmax = state.absmax.contiguous()
+    code2 = _f32(state.state2.code)
+    absmax2 = _f32(state.state2.absmax)
+    nf4 = _f32(state.code)
+    if code2.numel() < 256 or nf4.numel() < 16:
+        raise ValueError("quant state tables are too small (code2 needs 256, nf4 16 entries)")
+    n_blocks = -(-n_bytes // (state.blocksize // 2))
+    if absmax.numel() < n_blocks or absmax2.numel() < -(-n_blocks // 256):
+        raise ValueError("quant state absmax arrays do not cover the weight")
+    offset = _offset_tensor(state, device)
+    plan = ((_ext.ptr(weight.data), _ext.ptr(absmax), _ext.ptr(code2), _ext.ptr(absmax2),
+             _ext.ptr(offset), _ext.ptr(nf4)), n_bytes, int(state.blocksize),
+            int(state.state2.blocksize), (absmax, code2, absmax2, nf4, offset))
+    try:
+        weight._soupk_plan = (key, plan)
+    except AttributeError:          # objects without a __dict__ are checked on every call
+        pass
+    return plan
+
+
 def unpack_into(weight, out):
     """Write the fp16 values of one bitsandbytes 4-bit weight ([N, K]) into `out` ([N, K]).
 
     Mirrors solution/nf4.py:72-89: the HIP kernel for the supported layout on the device,
     bitsandbytes' own dequantize_4bit for other layouts (as the reference does).  CPU tensors
     are rejected: this build has no CPU path."""
-    state = _quant_state(weight)
     if not kernels_ok(out):
         raise ValueError("unpack_into: `out` must be a HIP device tensor (no CPU path)")
-    n_bytes = weight.data.numel()
-    if supports_fast_unpack(weight) and _on_device(weight, out.device):
+    plan = _plan(weight, out.device)
+    if plan is not None:
+        ptrs, n_bytes, qblock, qblock2, _ = plan
         _ext.require(out, "out", dtype=torch.float16)
         if out.numel() != 2 * n_bytes:
             raise ValueError(f"out has {out.numel()} elements, the weight holds {2 * n_bytes}")
-        if state.absmax.dtype != torch.uint8:
-            raise TypeError(f"nested absmax must be uint8, got {state.absmax.dtype}")
-        absmax = state.absmax.contiguous()
-        code2 = _f32(state.state2.code)
-        absmax2 = _f32(state.state2.absmax)
-        nf4 = _f32(state.code)
-        if code2.numel() < 256 or nf4.numel() < 16:
-            raise ValueError("quant state tables are too small (code2 needs 256, nf4 16 entries)")
-        n_blocks = -(-n_bytes // (state.blocksize // 2))
-        if absmax.numel() < n_blocks or absmax2.numel() < -(-n_blocks // 256):
-            raise ValueError("quant state absmax arrays do not cover the weight")
-        offset = _offset_tensor(state, out.device)
-        _ext.call("soupk_nf4_unpack", _ext.ptr(weight.data), _ext.ptr(absmax), _ext.ptr(code2),
-                  _ext.ptr(absmax2), _ext.ptr(offset), _ext.ptr(nf4), _ext.ptr(out), n_bytes,
-                  int(state.blocksize), int(state.state2.blocksize), _ext.stream_of(out))
+        _ext.call("soupk_nf4_unpack", *ptrs, out.data_ptr(), n_bytes, qblock, qblock2,
+                  _ext.stream_of(out))
         return out
     import bitsandbytes.functional as bnb_functional
 
+    state = _quant_state(weight)
     out.copy_(bnb_functional.dequantize_4bit(weight.data, state).to(out.dtype).view_as(out))
     return out
 
@@ -117,21 +165,22 @@ def unpack_concat(weights, device):
 class FrozenNF4Linear(torch.autograd.Function):
     """y = x @ W^T (+ b) for frozen 4-bit weights stacked by rows, fp16 in and out.
 
-    Nothing large is saved: the weights are unpacked again in backward, and no input is kept
-    because W does not train (solution/nf4.py:108-127)."""
+    No input is kept because W does not train (solution/nf4.py:108-127); the unpacked weight
+    is kept for backward or unpacked again there (KEEP_UNPACKED_FOR_BACKWARD)."""
 
     @staticmethod
     def forward(ctx, x, bias, weights):
         weight = unpack_concat(weights, x.device)
         out = torch.nn.functional.linear(x, weight, bias)
         ctx.weights = weights
+        keep_for_backward(ctx, weight)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
         grad_x = None
         if ctx.needs_input_grad[0]:
-            weight = unpack_concat(ctx.weights, grad_out.device)
+            weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
             grad_x = grad_out.to(torch.float16) @ weight
         return grad_x, None, None
 
