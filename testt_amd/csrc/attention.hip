@@ -1,29 +1,37 @@
 // Causal grouped-query attention over the padded [B, heads, T, D] layout, forward and backward,
-// for head_dim 128 on gfx950 MFMA (v_mfma_f32_16x16x16_f16).
+// for head_dim 128 on gfx950 MFMA (v_mfma_f32_16x16x32_f16).
 //
 // Replaces torch's scaled_dot_product_attention in the layer loop of the reference's
 // fused_forward (solution/model.py:246-247, transformers' sdpa_attention_forward with the causal
 // + key-padding mask of create_causal_mask): query i of a row attends to key j iff j <= i and
 // key j is a real token (key_valid[b, j] != 0, or every key when key_valid is NULL).
 //
+// MFMA operand layouts (16x16x32 f16, checked on the device): A[16 x 32]: lane l holds row
+// l%16, k = 8(l/16)..+7; B[32 x 16]: lane l holds column l%16, k = 8(l/16)..+7; C[16 x 16]:
+// lane l holds column l%16, rows 4(l/16)..+3.  Below, a lane's "group" is l/16 and its
+// "column" l%16.
+//
 // Forward (flash attention, online softmax): a workgroup is 4 wavefronts and 64 queries of one
 // (batch, head); wavefront w owns queries 16w..16w+15.  Key blocks of 64 rows are staged in LDS
 // -- K row-major, V transposed (key-contiguous) -- and each wavefront computes
-//   S^T (64 keys x 16 queries) = K Q^T       (A = K from LDS, B = Q^T from registers)
-// so that, in the MFMA output layout, lane l holds the scores of query l%16 for keys
-// 16n + 4(l/16) + i: exactly the B operand of
-//   O^T (128 x 16) += V^T P^T                 (A = V^T from LDS, B = P^T from registers),
-// and the online-softmax rescale of O^T is local to the lane (its query is l%16 too).  The four
-// lanes of a query (l%16 + 16r) combine their block maxima with two cross-row shuffles; their
-// partial sums are combined once, at the end.  Scores are kept in base 2:
-// x = s * scale * log2(e), p = 2^(x - m).  The output is written token-major,
-// out[(b*T + t), h*D + d], the layout the o-projection GEMM reads, and the per-query
-// log-sum-exp (natural log) for the backward pass; a query with no visible key gets output 0
-// and lse = +inf (so its backward probabilities are 0).
+//   S^T (64 keys x 16 queries) = K Q^T        (A = K rows from LDS, B = Q^T from registers)
+// so that, in the C layout, lane l holds the scores of query l%16 for keys 16n + 4(l/16) + i
+// of key tile n.  Two C tiles (n = 2m, 2m+1) together are the B operand of
+//   O^T (128 x 16) += V^T P^T                  (A = V^T from LDS, B = P^T from registers)
+// when the contraction index j of group gr stands for key 32m + 4gr + j (j < 4) or
+// 32m + 16 + 4gr + (j - 4): the A operand is read in the same order, as two 8-byte runs of a
+// V^T row.  The online-softmax state of a query is local to its four lanes (l%16 + 16r), which
+// combine block maxima and final sums with v_permlane16_swap / v_permlane32_swap (no LDS).
+// Scores are kept in base 2: x = s * scale * log2(e), p = 2^(x - m).  The reference value m of
+// a query is raised only when a block maximum exceeds it by more than 8 (p <= 2^8 otherwise,
+// exact in fp16 and fp32), so the accumulators are rarely rescaled.  The output is written
+// token-major, out[(b*T + t), h*D + d], the layout the o-projection GEMM reads, and the
+// per-query log-sum-exp (natural log) for the backward pass; a query with no visible key gets
+// output 0 and lse = +inf (so its backward probabilities are 0).
 //
-// MFMA operand layouts (16x16x16, checked on the device): A[16 x 16]: lane l holds row l%16,
-// k = 4(l/16)..+3; B[16 x 16]: lane l holds column l%16, k = 4(l/16)..+3; C: lane l holds
-// column l%16, rows 4(l/16)..+3.
+// LDS strides: row-major tiles [64][136] halves (16-byte reads of 8 lanes hit 8 distinct
+// 4-bank groups), transposed tiles [128][68] halves (8-byte reads of 16 lanes hit 16 distinct
+// 2-bank pairs).
 
 #include "soupk_common.hpp"
 
@@ -31,157 +39,246 @@ namespace soupk {
 namespace {
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;               // head dim
 constexpr int kBQ = 64;               // queries per workgroup (4 wavefronts x 16)
 constexpr int kBK = 64;               // keys per block
 constexpr int kAttnThreads = 256;
-constexpr int kKStride = kD + 8;      // Ks row stride (halves): 272 B, conflict-free 8-B reads
-constexpr int kVStride = kBK + 8;     // Vt row stride (halves): 144 B
+constexpr int kRStride = kD + 8;      // row-major tile row stride (halves), 272 B
+constexpr int kTStride = kBK + 4;     // transposed tile row stride (halves), 136 B
+constexpr float kRescaleMargin = 8.f;  // log2 of the largest unnormalised probability kept
 
-__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ h4 lds_h4(const _Float16* p) {
-  return *reinterpret_cast<const h4*>(p);
+__device__ __forceinline__ h8 lds_h8(const _Float16* p) {
+  return *reinterpret_cast<const h8*>(p);
 }
 
-// Stage key block kb of (b, g): Ks[key][d] row-major, Vt[d][key] transposed, and the 64 key
-// flags (1 = visible).  Rows past T read as zeros and are flagged invisible.
-__device__ __forceinline__ void stage_kv(_Float16* Ks, _Float16* Vt, uint8_t* kflag,
-                                         const uint16_t* __restrict__ kbase,
-                                         const uint16_t* __restrict__ vbase,
-                                         const uint8_t* __restrict__ valid, int key0, int T) {
-  const int tid = threadIdx.x;
-  // K: 64 keys x 16 chunks of 8 halves, 4 chunks per thread
+// The A operand of a product contracted over keys (or queries) from a transposed tile row:
+// elements 32m + 4gr .. +3, then 32m + 16 + 4gr .. +3 (the order of two C tiles 2m, 2m+1).
+__device__ __forceinline__ h8 lds_runs(const _Float16* row, int m, int gr) {
+  const h4 lo = *reinterpret_cast<const h4*>(row + 32 * m + 4 * gr);
+  const h4 hi = *reinterpret_cast<const h4*>(row + 32 * m + 16 + 4 * gr);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Max / sum over the four lanes of a column (l%16 + 16r, r = 0..3): rows 0<->1 and 2<->3 are
+// exchanged, then the two halves.  Every lane of the column gets the same bits (the operands
+// are combined in lane order on all four).
+__device__ __forceinline__ float column_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float column_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// A [64 x 128] fp16 tile (64 rows of one head) is staged through registers: thread item
+// it (0, 1) covers rows 2rp, 2rp+1 (rp = item % 32) at dims 8dc..8dc+7 (dc = item / 32), so
+// one pair of 16-byte row loads gives both the row-major LDS copy and, packed two rows to a
+// 4-byte word, the transposed one.  The loads of block i+1 are issued before block i is
+// computed and written to LDS after the next barrier, so their latency overlaps the MFMAs.
+// Row indices past the end clamp to the last row (a finite value): the callers give such rows
+// zero weight (key flags, query bounds), so no branch guards the loads.  The pointers these
+// loads go through are not __restrict__: that keeps the compiler from moving them past the
+// barriers (it would otherwise issue them just before their LDS stores, hiding nothing).
+struct TileRegs {
+  u32x4 a[2], b[2];
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* src, int64_t stride,
+                                          int r0, int nrows) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tid + kAttnThreads * r;
-    const int key = c >> 4, dc = c & 15;
-    const int t = key0 + key;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (t < T) w = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(t) * kD + 8 * dc);
-    *reinterpret_cast<u32x4*>(Ks + key * kKStride + 8 * dc) = w;
+  for (int it = 0; it < 2; ++it) {
+    const int item = threadIdx.x + kAttnThreads * it;
+    const int rp = item & 31, dc = item >> 5;
+    const int t0 = min(r0 + 2 * rp, nrows - 1), t1 = min(r0 + 2 * rp + 1, nrows - 1);
+    r.a[it] = *reinterpret_cast<const u32x4*>(src + t0 * stride + 8 * dc);
+    r.b[it] = *reinterpret_cast<const u32x4*>(src + t1 * stride + 8 * dc);
   }
-  // V transposed: 32 key pairs x 16 chunks of 8 d; per item two 16-B row loads and eight
-  // 4-byte LDS words (the pair's values at one d).
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int item = tid + kAttnThreads * r;
-    const int kp = item & 31, dc = item >> 5;
-    const int t0 = key0 + 2 * kp;
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (t0 < T) a = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(t0) * kD + 8 * dc);
-    if (t0 + 1 < T)
-      b = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(t0 + 1) * kD + 8 * dc);
+}
+
+// A compiler-only barrier (no instruction, no wait): the prefetch loads above it stay above it
+// instead of being moved down to their use in the next iteration.
+__device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
+
+// Rows (2rp, 2rp+1) x 8 dims: row-major into `rm` ([64][kRStride]) and/or transposed into
+// `tr` ([128][kTStride]).
+template <bool RM, bool TR>
+__device__ __forceinline__ void stage_pair(_Float16* rm, _Float16* tr, u32x4 a, u32x4 b, int rp,
+                                           int dc) {
+  if constexpr (RM) {
+    *reinterpret_cast<u32x4*>(rm + (2 * rp) * kRStride + 8 * dc) = a;
+    *reinterpret_cast<u32x4*>(rm + (2 * rp + 1) * kRStride + 8 * dc) = b;
+  }
+  if constexpr (TR) {
     const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    uint32_t* col = reinterpret_cast<uint32_t*>(Vt + (8 * dc) * kVStride + 2 * kp);
+    uint32_t* col = reinterpret_cast<uint32_t*>(tr + (8 * dc) * kTStride + 2 * rp);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // d = 8dc + 2j (low halves) and 8dc + 2j + 1 (high halves)
-      col[(2 * j) * (kVStride / 2)] = (aw[j] & 0xffffu) | (bw[j] << 16);
-      col[(2 * j + 1) * (kVStride / 2)] = (aw[j] >> 16) | (bw[j] & 0xffff0000u);
+      col[(2 * j) * (kTStride / 2)] = (aw[j] & 0xffffu) | (bw[j] << 16);
+      col[(2 * j + 1) * (kTStride / 2)] = (aw[j] >> 16) | (bw[j] & 0xffff0000u);
     }
-  }
-  if (tid < kBK) {
-    const int t = key0 + tid;
-    kflag[tid] = (t < T && (valid == nullptr || valid[t] != 0)) ? 1 : 0;
   }
 }
 
+template <bool RM, bool TR>
+__device__ __forceinline__ void store_tile(_Float16* rm, _Float16* tr, const TileRegs& r) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = threadIdx.x + kAttnThreads * it;
+    stage_pair<RM, TR>(rm, tr, r.a[it], r.b[it], item & 31, item >> 5);
+  }
+}
+
+// The key-valid byte of key key0 + threadIdx.x % 64, loaded unconditionally (from `any`, a
+// readable address, when there is no flag array) and tested only when stored, so that the
+// test does not wait for the tile loads issued with it.
+__device__ __forceinline__ uint8_t load_flag_raw(const uint8_t* valid, const void* any, int key0,
+                                                 int T) {
+  const int t = min(key0 + (threadIdx.x & (kBK - 1)), T - 1);
+  return *(valid != nullptr ? valid + t : static_cast<const uint8_t*>(any));
+}
+
+__device__ __forceinline__ uint8_t key_flag(uint8_t raw, bool has_valid, int key0, int T) {
+  const int t = key0 + (threadIdx.x & (kBK - 1));
+  return (t < T && (!has_valid || raw != 0)) ? 1 : 0;
+}
+
+// Flags of keys 16n + 4gr .. +3 of the staged block, one byte each.
+__device__ __forceinline__ uint32_t flag_word(const uint8_t* kflag, int n, int gr) {
+  return *reinterpret_cast<const uint32_t*>(kflag + 16 * n + 4 * gr);
+}
+
+// Grid: x = head, y = batch row, z = block index from the heaviest (most key blocks) down, so
+// that the longest workgroups are dispatched first.
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint8_t* __restrict__ key_valid,
-    uint16_t* __restrict__ out, float* __restrict__ lse, int T, int NH, int NKV,
-    float scale_log2) {
-  __shared__ __align__(16) _Float16 Ks[kBK * kKStride];
-  __shared__ __align__(16) _Float16 Vt[kD * kVStride];
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
+    const uint8_t* key_valid, uint16_t* __restrict__ out, float* __restrict__ lse, int T, int NH,
+    int NKV, float scale_log2) {
+  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
+  __shared__ __align__(16) _Float16 Vt[kD * kTStride];
   __shared__ __align__(16) uint8_t kflag[kBK];
   const int nqb = (T + kBQ - 1) / kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // longest (latest) blocks first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.z);
+  const int h = blockIdx.x, b = blockIdx.y;
   const int g = h / (NH / NKV);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  const int ql = lane & 15, kq = lane >> 4;
+  const int ql = lane & 15, gr = lane >> 4;
   const int q_abs = qb * kBQ + 16 * w + ql;
   const uint16_t* qrow = q + ((static_cast<int64_t>(b) * NH + h) * T + min(q_abs, T - 1)) * kD;
   const uint16_t* kbase = k + (static_cast<int64_t>(b) * NKV + g) * T * kD;
   const uint16_t* vbase = v + (static_cast<int64_t>(b) * NKV + g) * T * kD;
   const uint8_t* valid = key_valid != nullptr ? key_valid + static_cast<int64_t>(b) * T : nullptr;
+  const bool has_valid = valid != nullptr;
 
-  // Q^T operand: 8 k-steps of 16 dims, lane holds Q[q][16s + 4kq .. +3]
-  h4 qf[8];
+  // Q^T operand: 4 k-steps of 32 dims, lane holds Q[q][32s + 8gr .. +7]
+  h8 qf[4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const u32x2 wq = *reinterpret_cast<const u32x2*>(qrow + 16 * s + 4 * kq);
-    qf[s] = __builtin_bit_cast(h4, wq);
-  }
+  for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const h8*>(qrow + 32 * s + 8 * gr);
   f4 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, lsum = 0.f;
+  float m_ref = -INFINITY, lsum = 0.f;
 
-  const int kb_last = min(qb, (T - 1) / kBK);
-  for (int kb = 0; kb <= kb_last; ++kb) {
+  TileRegs kr, vr;
+  load_tile(kr, kbase, kD, 0, T);
+  load_tile(vr, vbase, kD, 0, T);
+  uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
+  for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
-    stage_kv(Ks, Vt, kflag, kbase, vbase, valid, kb * kBK, T);
+    store_tile<true, false>(Ks, nullptr, kr);
+    store_tile<false, true>(nullptr, Vt, vr);
+    if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
+    load_tile(kr, kbase, kD, (kb + 1) * kBK, T);   // the next block (clamped past the end)
+    load_tile(vr, vbase, kD, (kb + 1) * kBK, T);
+    fl_raw = load_flag_raw(valid, kbase, (kb + 1) * kBK, T);
+    issue_here();
     // S^T for the 4 key tiles
-    f4 s4[4];
+    f4 sc[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
+      h8 kf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[s] = lds_h8(Ks + (16 * n + ql) * kRStride + 32 * s + 8 * gr);
       f4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
-        c = mfma16(lds_h4(Ks + (16 * n + ql) * kKStride + 16 * s + 4 * kq), qf[s], c);
-      s4[n] = c;
+      for (int s = 0; s < 4; ++s) c = mfma32(kf[s], qf[s], c);
+      sc[n] = c;
     }
-    // mask, scale, block max
+    // scale, mask (the diagonal block, or keys with flags), block max.  Keys of an interior
+    // block (kb < qb) precede every query of this workgroup and lie below T.
     float x[4][4];
     float mx = -INFINITY;
+    if (kb == qb || has_valid) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const uint32_t fl = *reinterpret_cast<const uint32_t*>(kflag + 16 * n + 4 * kq);
+      for (int n = 0; n < 4; ++n) {
+        const uint32_t fl = flag_word(kflag, n, gr);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb * kBK + 16 * n + 4 * kq + i;
-        const bool vis = key <= q_abs && ((fl >> (8 * i)) & 0xffu) != 0;
-        x[n][i] = vis ? s4[n][i] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[n][i]);
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb * kBK + 16 * n + 4 * gr + i;
+          const bool vis = key <= q_abs && ((fl >> (8 * i)) & 0xffu) != 0;
+          x[n][i] = vis ? sc[n][i] * scale_log2 : -INFINITY;
+          mx = fmaxf(mx, x[n][i]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[n][i] = sc[n][i] * scale_log2;
+          mx = fmaxf(mx, x[n][i]);
+        }
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_use);
-    m = m_new;
+    mx = column_max(mx);
+    if (__any(mx > m_ref + kRescaleMargin)) {   // (m_ref = -inf: any visible key)
+      const float m_new = fmaxf(m_ref, mx);
+      const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = acc[t] * alpha;
+      m_ref = m_new;
+    }
+    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
     float ps = 0.f;
-    h4 pb[4];
+    h8 pb[2];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = __builtin_amdgcn_exp2f(x[n][i] - m_use);  // 2^-inf = 0
         ps += p;
-        pb[n][i] = static_cast<_Float16>(p);
+        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p);
       }
     }
-    lsum = lsum * alpha + ps;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = acc[t] * alpha;
+    lsum += ps;
     // O^T += V^T P^T
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int t = 0; t < 8; ++t) {
+      const _Float16* vrow = Vt + (16 * t + ql) * kTStride;
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        acc[t] = mfma16(lds_h4(Vt + (16 * t + ql) * kVStride + 16 * n + 4 * kq), pb[n], acc[t]);
+      for (int m = 0; m < 2; ++m) acc[t] = mfma32(lds_runs(vrow, m, gr), pb[m], acc[t]);
     }
   }
-  float l_tot = lsum + __shfl_xor(lsum, 16, kWave);
-  l_tot = l_tot + __shfl_xor(l_tot, 32, kWave);
+  const float l_tot = column_sum(lsum);
   if (q_abs >= T) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   uint16_t* orow = out + (static_cast<int64_t>(b) * T + q_abs) * (static_cast<int64_t>(NH) * kD) +
@@ -189,12 +286,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const f4 o = acc[t] * inv;
-    *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * kq) = u32x2{pack_h2(o[0], o[1]),
+    *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
                                                                 pack_h2(o[2], o[3])};
   }
-  if (kq == 0)
+  if (gr == 0)
     lse[(static_cast<int64_t>(b) * NH + h) * T + q_abs] =
-        l_tot > 0.f ? (m + log2f(l_tot)) * kLn2 : INFINITY;
+        l_tot > 0.f ? (m_ref + log2f(l_tot)) * kLn2 : INFINITY;
 }
 
 // ---- backward ------------------------------------------------------------------------------
@@ -203,69 +300,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
 // dK = scale * dS^T Q,  dV = P^T dO.  Three launches:
 //   attn_bwd_dq_kernel   (b, head, 64 queries): D for its queries (written for the next kernel),
 //                        then over its key blocks S^T = K Q^T, dP^T = V dO^T (the forward's
-//                        orientation: query = lane % 16), dQ^T += K^T dS^T;
+//                        orientation: query = lane column), dQ^T += K^T dS^T;
 //   attn_bwd_dkdv_kernel (b, head, 64 keys): over the query blocks that see them,
-//                        S = Q K^T, dP = dO V^T (key = lane % 16), dV^T += dO^T P,
+//                        S = Q K^T, dP = dO V^T (key = lane column), dV^T += dO^T P,
 //                        dK^T += Q^T dS, into fp32 partials per query head;
 //   attn_bwd_reduce_kernel: dK, dV of a key/value head = the sum of its query heads' partials
 //                        (a fixed order: deterministic), fp16.
-// Every operand a MFMA reads from LDS is laid out so that a lane's four k-values are 8
-// contiguous bytes: row-major tiles for operands contracted over the head dim, transposed
-// (row-contiguous) tiles for operands contracted over queries or keys.
-
-// Two rows (2rp, 2rp+1) x 8 dims of a [64 x 128] tile: row-major into `rm` (stride kKStride)
-// and/or transposed into `tr` ([128][kVStride]), from one pair of 16-byte loads.
-template <bool RM, bool TR>
-__device__ __forceinline__ void stage_pair(_Float16* rm, _Float16* tr, u32x4 a, u32x4 b, int rp,
-                                           int dc) {
-  if constexpr (RM) {
-    *reinterpret_cast<u32x4*>(rm + (2 * rp) * kKStride + 8 * dc) = a;
-    *reinterpret_cast<u32x4*>(rm + (2 * rp + 1) * kKStride + 8 * dc) = b;
-  }
-  if constexpr (TR) {
-    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    uint32_t* col = reinterpret_cast<uint32_t*>(tr + (8 * dc) * kVStride + 2 * rp);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      col[(2 * j) * (kVStride / 2)] = (aw[j] & 0xffffu) | (bw[j] << 16);
-      col[(2 * j + 1) * (kVStride / 2)] = (aw[j] >> 16) | (bw[j] & 0xffff0000u);
-    }
-  }
-}
-
-// Stage 64 rows of 128 fp16 (row r at src + r*stride; rows r0+r >= nrows read as 0).
-template <bool RM, bool TR>
-__device__ __forceinline__ void stage_tile(_Float16* rm, _Float16* tr,
-                                           const uint16_t* __restrict__ src, int64_t stride,
-                                           int r0, int nrows) {
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int item = threadIdx.x + kAttnThreads * r;
-    const int rp = item & 31, dc = item >> 5;
-    const int t0 = r0 + 2 * rp;
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (t0 < nrows) a = *reinterpret_cast<const u32x4*>(src + t0 * stride + 8 * dc);
-    if (t0 + 1 < nrows) b = *reinterpret_cast<const u32x4*>(src + (t0 + 1) * stride + 8 * dc);
-    stage_pair<RM, TR>(rm, tr, a, b, rp, dc);
-  }
-}
+// Operands contracted over the head dim are read from row-major tiles (16-byte reads);
+// operands contracted over keys or queries from transposed tiles, in the order of the C tiles
+// they meet (lds_runs).
 
 __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint8_t* __restrict__ key_valid,
-    const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
+    const uint8_t* key_valid, const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, float* __restrict__ delta, uint16_t* __restrict__ dq, int T,
     int NH, int NKV, float scale, float scale_log2) {
-  __shared__ __align__(16) _Float16 Ks[kBK * kKStride];
-  __shared__ __align__(16) _Float16 Vs[kBK * kKStride];
-  __shared__ __align__(16) _Float16 Kt[kD * kVStride];
+  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
+  __shared__ __align__(16) _Float16 Vs[kBK * kRStride];
+  __shared__ __align__(16) _Float16 Kt[kD * kTStride];
   __shared__ __align__(16) uint8_t kflag[kBK];
   const int nqb = (T + kBQ - 1) / kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.z);
+  const int h = blockIdx.x, b = blockIdx.y;
   const int g = h / (NH / NKV);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  const int ql = lane & 15, kq = lane >> 4;
+  const int ql = lane & 15, gr = lane >> 4;
   const int q_abs = qb * kBQ + 16 * w + ql;
   const int qc = min(q_abs, T - 1);
   const int64_t HD = static_cast<int64_t>(NH) * kD;
@@ -275,60 +334,72 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
   const uint16_t* kbase = k + (static_cast<int64_t>(b) * NKV + g) * T * kD;
   const uint16_t* vbase = v + (static_cast<int64_t>(b) * NKV + g) * T * kD;
   const uint8_t* valid = key_valid != nullptr ? key_valid + static_cast<int64_t>(b) * T : nullptr;
+  const bool has_valid = valid != nullptr;
 
-  h4 qf[8], dof[8];
+  h8 qf[4], dof[4];
   float dsum = 0.f;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    qf[s] = __builtin_bit_cast(h4, *reinterpret_cast<const u32x2*>(qrow + 16 * s + 4 * kq));
-    dof[s] = __builtin_bit_cast(h4, *reinterpret_cast<const u32x2*>(dorow + 16 * s + 4 * kq));
-    const h4 of = __builtin_bit_cast(h4, *reinterpret_cast<const u32x2*>(orow + 16 * s + 4 * kq));
+  for (int s = 0; s < 4; ++s) {
+    qf[s] = *reinterpret_cast<const h8*>(qrow + 32 * s + 8 * gr);
+    dof[s] = *reinterpret_cast<const h8*>(dorow + 32 * s + 8 * gr);
+    const h8 of = *reinterpret_cast<const h8*>(orow + 32 * s + 8 * gr);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
       dsum = dsum + static_cast<float>(dof[s][i]) * static_cast<float>(of[i]);
   }
-  dsum = dsum + __shfl_xor(dsum, 16, kWave);
-  dsum = dsum + __shfl_xor(dsum, 32, kWave);
+  dsum = column_sum(dsum);
   const float lse_q = lse[(static_cast<int64_t>(b) * NH + h) * T + qc];
   const float lse2 = lse_q * kLog2e;  // +inf: no visible key, every p = 0
-  if (kq == 0 && q_abs < T) delta[(static_cast<int64_t>(b) * NH + h) * T + q_abs] = dsum;
+  if (gr == 0 && q_abs < T) delta[(static_cast<int64_t>(b) * NH + h) * T + q_abs] = dsum;
 
   f4 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  const int kb_last = min(qb, (T - 1) / kBK);
-  for (int kb = 0; kb <= kb_last; ++kb) {
+  TileRegs kr, vr;
+  load_tile(kr, kbase, kD, 0, T);
+  load_tile(vr, vbase, kD, 0, T);
+  uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
+  for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
-    stage_tile<true, true>(Ks, Kt, kbase, kD, kb * kBK, T);
-    stage_tile<true, false>(Vs, nullptr, vbase, kD, kb * kBK, T);
-    if (threadIdx.x < kBK) {
-      const int t = kb * kBK + threadIdx.x;
-      kflag[threadIdx.x] = (t < T && (valid == nullptr || valid[t] != 0)) ? 1 : 0;
-    }
+    store_tile<true, true>(Ks, Kt, kr);
+    store_tile<true, false>(Vs, nullptr, vr);
+    if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
-    h4 dsb[4];
+    load_tile(kr, kbase, kD, (kb + 1) * kBK, T);   // the next block (clamped past the end)
+    load_tile(vr, vbase, kD, (kb + 1) * kBK, T);
+    fl_raw = load_flag_raw(valid, kbase, (kb + 1) * kBK, T);
+    issue_here();
+    const bool masked = kb == qb || has_valid;
+    h8 dsb[2];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
+      h8 kf[4], vf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        kf[s] = lds_h8(Ks + (16 * n + ql) * kRStride + 32 * s + 8 * gr);
+        vf[s] = lds_h8(Vs + (16 * n + ql) * kRStride + 32 * s + 8 * gr);
+      }
       f4 sc = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        sc = mfma16(lds_h4(Ks + (16 * n + ql) * kKStride + 16 * s + 4 * kq), qf[s], sc);
-        dp = mfma16(lds_h4(Vs + (16 * n + ql) * kKStride + 16 * s + 4 * kq), dof[s], dp);
+      for (int s = 0; s < 4; ++s) {
+        sc = mfma32(kf[s], qf[s], sc);
+        dp = mfma32(vf[s], dof[s], dp);
       }
-      const uint32_t fl = *reinterpret_cast<const uint32_t*>(kflag + 16 * n + 4 * kq);
+      const uint32_t fl = masked ? flag_word(kflag, n, gr) : 0x01010101u;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = kb * kBK + 16 * n + 4 * kq + i;
-        const bool vis = key <= q_abs && ((fl >> (8 * i)) & 0xffu) != 0;
+        const int key = kb * kBK + 16 * n + 4 * gr + i;
+        const bool vis = !masked || (key <= q_abs && ((fl >> (8 * i)) & 0xffu) != 0);
         const float p = vis ? __builtin_amdgcn_exp2f(sc[i] * scale_log2 - lse2) : 0.f;
-        dsb[n][i] = static_cast<_Float16>(p * (dp[i] - dsum));
+        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - dsum));
       }
     }
+    // dQ^T += K^T dS^T
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int t = 0; t < 8; ++t) {
+      const _Float16* krow = Kt + (16 * t + ql) * kTStride;
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        acc[t] = mfma16(lds_h4(Kt + (16 * t + ql) * kVStride + 16 * n + 4 * kq), dsb[n], acc[t]);
+      for (int m = 0; m < 2; ++m) acc[t] = mfma32(lds_runs(krow, m, gr), dsb[m], acc[t]);
     }
   }
   if (q_abs >= T) return;
@@ -336,32 +407,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const f4 o = acc[t] * scale;
-    *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * kq) = u32x2{pack_h2(o[0], o[1]),
+    *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
                                                                  pack_h2(o[2], o[3])};
   }
 }
 
 __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint8_t* __restrict__ key_valid,
-    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, float* __restrict__ dk_part, float* __restrict__ dv_part,
+    const uint16_t* q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint8_t* __restrict__ key_valid, const uint16_t* dout, const float* lse,
+    const float* delta, float* __restrict__ dk_part, float* __restrict__ dv_part,
     int T, int NH, int NKV, float scale, float scale_log2) {
-  __shared__ __align__(16) _Float16 Qs[kBQ * kKStride];
-  __shared__ __align__(16) _Float16 Qt[kD * kVStride];
-  __shared__ __align__(16) _Float16 Ds[kBQ * kKStride];   // dO row-major
-  __shared__ __align__(16) _Float16 Dt[kD * kVStride];    // dO transposed
+  __shared__ __align__(16) _Float16 Qs[kBQ * kRStride];
+  __shared__ __align__(16) _Float16 Qt[kD * kTStride];
+  __shared__ __align__(16) _Float16 Ds[kBQ * kRStride];   // dO row-major
+  __shared__ __align__(16) _Float16 Dt[kD * kTStride];    // dO transposed
   __shared__ float lse2_s[kBQ], delta_s[kBQ];
-  const int nkb = (T + kBK - 1) / kBK;
-  const int kb = static_cast<int>(blockIdx.x);  // block 0 sees the most query blocks
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int kb = static_cast<int>(blockIdx.z);  // block 0 sees the most query blocks
+  const int h = blockIdx.x, b = blockIdx.y;
   const int g = h / (NH / NKV);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  const int kl = lane & 15, qq = lane >> 4;
+  const int kl = lane & 15, gr = lane >> 4;
   const int key_abs = kb * kBK + 16 * w + kl;
   const int kc = min(key_abs, T - 1);
   const bool key_vis = key_abs < T && (key_valid == nullptr ||
                                        key_valid[static_cast<int64_t>(b) * T + key_abs] != 0);
+  const bool has_valid = key_valid != nullptr;
   const int64_t HD = static_cast<int64_t>(NH) * kD;
   const uint16_t* krow = k + ((static_cast<int64_t>(b) * NKV + g) * T + kc) * kD;
   const uint16_t* vrow = v + ((static_cast<int64_t>(b) * NKV + g) * T + kc) * kD;
@@ -371,66 +441,88 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
   const float* del_bh = delta + (static_cast<int64_t>(b) * NH + h) * T;
 
   // K^T and V^T operands (B of S = Q K^T and of dP = dO V^T): lane holds row key of K / V,
-  // dims 16s + 4qq .. +3
-  h4 kf[8], vf[8];
+  // dims 32s + 8gr .. +7
+  h8 kf[4], vf[4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    kf[s] = __builtin_bit_cast(h4, *reinterpret_cast<const u32x2*>(krow + 16 * s + 4 * qq));
-    vf[s] = __builtin_bit_cast(h4, *reinterpret_cast<const u32x2*>(vrow + 16 * s + 4 * qq));
+  for (int s = 0; s < 4; ++s) {
+    kf[s] = *reinterpret_cast<const h8*>(krow + 32 * s + 8 * gr);
+    vf[s] = *reinterpret_cast<const h8*>(vrow + 32 * s + 8 * gr);
   }
   f4 dk[8], dv[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) dk[t] = dv[t] = f4{0.f, 0.f, 0.f, 0.f};
-  (void)nkb;
   const int nqb = (T + kBQ - 1) / kBQ;
+  TileRegs qr, dr;
+  float lse_raw, del_raw;   // tested against T only when stored (see load_flag_raw)
+  auto load_block = [&](int q0) {
+    load_tile(qr, qbase, kD, q0, T);
+    load_tile(dr, dobase, HD, q0, T);
+    const int t = min(q0 + (threadIdx.x & (kBQ - 1)), T - 1);
+    lse_raw = lse_bh[t];
+    del_raw = del_bh[t];
+  };
+  load_block(kb * kBQ);
   for (int qb = kb; qb < nqb; ++qb) {
     __syncthreads();
-    stage_tile<true, true>(Qs, Qt, qbase, kD, qb * kBQ, T);
-    stage_tile<true, true>(Ds, Dt, dobase, HD, qb * kBQ, T);
+    store_tile<true, true>(Qs, Qt, qr);
+    store_tile<true, true>(Ds, Dt, dr);
     if (threadIdx.x < kBQ) {
-      const int t = qb * kBQ + threadIdx.x;
-      lse2_s[threadIdx.x] = t < T ? lse_bh[t] * kLog2e : INFINITY;
-      delta_s[threadIdx.x] = t < T ? del_bh[t] : 0.f;
+      const bool in = qb * kBQ + static_cast<int>(threadIdx.x) < T;
+      lse2_s[threadIdx.x] = in ? lse_raw * kLog2e : INFINITY;
+      delta_s[threadIdx.x] = in ? del_raw : 0.f;
     }
     __syncthreads();
-    h4 pb[4], dsb[4];
+    load_block((qb + 1) * kBQ);   // the next block (clamped past the end)
+    issue_here();
+    // Every (query, key) pair of an interior block is visible: the queries follow the keys,
+    // lie below T, and no flags apply.
+    const bool masked = qb == kb || has_valid || (qb + 1) * kBQ > T;
+    h8 pb[2], dsb[2];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
+      h8 qa[4], da[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        qa[s] = lds_h8(Qs + (16 * n + kl) * kRStride + 32 * s + 8 * gr);
+        da[s] = lds_h8(Ds + (16 * n + kl) * kRStride + 32 * s + 8 * gr);
+      }
       f4 sc = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        sc = mfma16(lds_h4(Qs + (16 * n + kl) * kKStride + 16 * s + 4 * qq), kf[s], sc);
-        dp = mfma16(lds_h4(Ds + (16 * n + kl) * kKStride + 16 * s + 4 * qq), vf[s], dp);
+      for (int s = 0; s < 4; ++s) {
+        sc = mfma32(qa[s], kf[s], sc);
+        dp = mfma32(da[s], vf[s], dp);
       }
-      // C: rows = queries 16n + 4qq + i, column = this lane's key
+      // C: rows = queries 16n + 4gr + i, column = this lane's key
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int qi = 16 * n + 4 * qq + i;
+        const int qi = 16 * n + 4 * gr + i;
         const int q_abs = qb * kBQ + qi;
-        const bool vis = key_vis && key_abs <= q_abs && q_abs < T;
+        const bool vis = !masked || (key_vis && key_abs <= q_abs && q_abs < T);
         const float p = vis ? __builtin_amdgcn_exp2f(sc[i] * scale_log2 - lse2_s[qi]) : 0.f;
-        pb[n][i] = static_cast<_Float16>(p);
-        dsb[n][i] = static_cast<_Float16>(p * (dp[i] - delta_s[qi]));
+        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p);
+        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - delta_s[qi]));
       }
     }
-    // dV^T += dO^T P, dK^T += Q^T dS  (k = queries)
+    // dV^T += dO^T P, dK^T += Q^T dS  (contraction over the block's queries)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int t = 0; t < 8; ++t) {
+      const _Float16* drow = Dt + (16 * t + kl) * kTStride;
+      const _Float16* qtrow = Qt + (16 * t + kl) * kTStride;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        dv[t] = mfma16(lds_h4(Dt + (16 * t + kl) * kVStride + 16 * n + 4 * qq), pb[n], dv[t]);
-        dk[t] = mfma16(lds_h4(Qt + (16 * t + kl) * kVStride + 16 * n + 4 * qq), dsb[n], dk[t]);
+      for (int m = 0; m < 2; ++m) {
+        dv[t] = mfma32(lds_runs(drow, m, gr), pb[m], dv[t]);
+        dk[t] = mfma32(lds_runs(qtrow, m, gr), dsb[m], dk[t]);
       }
     }
   }
   if (key_abs >= T) return;
-  // C: rows = dims 16t + 4qq + i, column = this lane's key
+  // C: rows = dims 16t + 4gr + i, column = this lane's key
   float* dkp = dk_part + ((static_cast<int64_t>(b) * NH + h) * T + key_abs) * kD;
   float* dvp = dv_part + ((static_cast<int64_t>(b) * NH + h) * T + key_abs) * kD;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    *reinterpret_cast<f4*>(dkp + 16 * t + 4 * qq) = dk[t] * scale;
-    *reinterpret_cast<f4*>(dvp + 16 * t + 4 * qq) = dv[t];
+    *reinterpret_cast<f4*>(dkp + 16 * t + 4 * gr) = dk[t] * scale;
+    *reinterpret_cast<f4*>(dvp + 16 * t + 4 * gr) = dv[t];
   }
 }
 
@@ -455,6 +547,15 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
   reinterpret_cast<u32x2*>(dv)[i] = u32x2{pack_h2(sv[0], sv[1]), pack_h2(sv[2], sv[3])};
 }
 
+// Shape checks shared by both entry points.
+int check_shape(int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D, float scale) {
+  if (B < 0 || T < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
+  if (!(scale > 0.f)) return kInvalid;
+  if (B > 65535 || (T + kBQ - 1) / kBQ > 65535) return kInvalid;   // grid y, z limits
+  if (static_cast<int64_t>(B) * NH * T * kD >= (int64_t{1} << 40)) return kInvalid;
+  return kOk;
+}
+
 }  // namespace
 }  // namespace soupk
 
@@ -464,16 +565,15 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_fwd(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* key_valid,
     uint16_t* out, float* lse, int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D,
     float scale, void* stream) {
-  if (B < 0 || T < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
-  if (!(scale > 0.f)) return kInvalid;
+  const int rc = check_shape(B, T, NH, NKV, D, scale);
+  if (rc != kOk) return rc;
   if (B == 0 || T == 0) return kOk;
   if (!q || !k || !v || !out || !lse) return kInvalid;
   for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k),
                         static_cast<const void*>(v), static_cast<const void*>(out)})
     if (reinterpret_cast<uintptr_t>(p) & 15) return kInvalid;
-  if (static_cast<int64_t>(B) * NH * T * kD >= (int64_t{1} << 40)) return kInvalid;
-  const dim3 grid(static_cast<unsigned>((T + kBQ - 1) / kBQ), static_cast<unsigned>(NH),
-                  static_cast<unsigned>(B));
+  const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B),
+                  static_cast<unsigned>((T + kBQ - 1) / kBQ));
   return launch_kernel(attn_fwd_kernel, grid, dim3(kAttnThreads),
                        static_cast<hipStream_t>(stream), q, k, v, key_valid, out, lse, T, NH,
                        NKV, scale * kLog2e);
@@ -484,8 +584,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_bwd(
     const uint16_t* out, const uint16_t* dout, const float* lse, float* workspace,
     uint16_t* dq, uint16_t* dk, uint16_t* dv, int32_t B, int32_t T, int32_t NH, int32_t NKV,
     int32_t D, float scale, void* stream) {
-  if (B < 0 || T < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
-  if (!(scale > 0.f)) return kInvalid;
+  const int rc0 = check_shape(B, T, NH, NKV, D, scale);
+  if (rc0 != kOk) return rc0;
   if (B == 0 || T == 0) return kOk;
   if (!q || !k || !v || !out || !dout || !lse || !workspace || !dq || !dk || !dv)
     return kInvalid;
@@ -504,7 +604,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_bwd(
   float* dk_part = workspace + delta_n;
   float* dv_part = dk_part + part;
   const int nb = (T + kBQ - 1) / kBQ;
-  const dim3 grid(static_cast<unsigned>(nb), static_cast<unsigned>(NH), static_cast<unsigned>(B));
+  const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B), static_cast<unsigned>(nb));
   int rc = launch_kernel(attn_bwd_dq_kernel, grid, dim3(kAttnThreads), st, q, k, v, key_valid,
                          out, dout, lse, delta, dq, T, NH, NKV, scale, scale * kLog2e);
   if (rc != kOk) return rc;
