@@ -98,7 +98,9 @@ def test_frozen_linear_keep_modes_agree(monkeypatch, keep):
     grad = torch.randn(17, 192, generator=g).to(torch.float16).to(DEV)
     monkeypatch.setattr(nf4, "KEEP_UNPACKED_FOR_BACKWARD", keep)
     out = nf4.frozen_linear(x, (w,))
+    assert (out.grad_fn.unpacked is not None) == keep    # the forward's weight is held in ctx
     out.backward(grad, retain_graph=True)
+    assert out.grad_fn.unpacked is None                   # and released by the backward
     first = x.grad.clone()
     out.backward(grad)                 # a second backward unpacks again when nothing is kept
     assert torch.equal(x.grad, 2 * first)

@@ -33,8 +33,10 @@ KEEP_UNPACKED_FOR_BACKWARD = True
 
 
 def keep_for_backward(ctx, weight):
-    """Hold the forward's unpacked fp16 `weight` in ctx when a backward will read it."""
-    keep = KEEP_UNPACKED_FOR_BACKWARD and torch.is_grad_enabled() and any(ctx.needs_input_grad)
+    """Hold the forward's unpacked fp16 `weight` in ctx when a backward may read it (an input
+    needs a gradient; a forward outside autograd frees ctx, and the weight, with its outputs).
+    Grad mode is always off inside autograd.Function.forward, so it is not consulted."""
+    keep = KEEP_UNPACKED_FOR_BACKWARD and any(ctx.needs_input_grad)
     ctx.unpacked = weight if keep else None
 
 
