@@ -21,6 +21,7 @@ and the CPU baseline (the reference's eager PyTorch path on the host cores, orac
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -33,6 +34,7 @@ sys.path.insert(0, ROOT)
 from testt_amd import _ext, workloads  # noqa: E402
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (written by
 # `bench.py --summarize-pmc`); the roofline's "traffic" field is read from this table.
@@ -310,6 +312,46 @@ def time_layer(dev, steps, warmup):
     return out
 
 
+def time_attention(dev, steps, warmup):
+    """The causal GQA attention kernels (testt_amd/csrc/attention.hip) at the layer's shape,
+    B=4 x T=512, 12 query / 2 key-value heads of 128: forward and backward (dQ, dK/dV partials,
+    GQA reduce) per call, torch events on the stream they run on.  Algorithmic FLOPs: 4*D per
+    visible (query, key) pair forward (S and P.V), 10*D backward (recomputed S, dP, dV, dK, dQ),
+    T(T+1)/2 visible pairs per (row, head); MFMA-bound, against 2.5 PFLOP/s dense fp16."""
+    from testt_amd import attention
+
+    B, T, NH, NKV, D = workloads.BATCH, workloads.SEQ, workloads.N_HEADS, workloads.N_KV, 128
+    g = workloads.gen(13)
+    q = torch.randn(B, NH, T, D, generator=g).to(torch.float16).to(dev)
+    k = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
+    v = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
+    dout = torch.randn(B * T, NH * D, generator=g).to(torch.float16).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out, lse = attention.attention_fwd(q, k, v, None, scale)
+    pairs = B * NH * T * (T + 1) / 2
+    res = {}
+    for name, fn, flops in (
+            ("fwd", lambda: attention.attention_fwd(q, k, v, None, scale), 4 * D * pairs),
+            ("bwd", lambda: attention.attention_bwd(q, k, v, None, out, lse, dout, scale),
+             10 * D * pairs)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        tflops = flops / (us * 1e-6) / 1e12
+        res[name] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
+                     "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16_TFLOPS, 4)}
+    res.update(shape={"batch": B, "seq": T, "q_heads": NH, "kv_heads": NKV, "head_dim": D},
+               note="causal, no padding; bwd = dQ + dK/dV-partial + GQA-reduce launches")
+    return res
+
+
 def time_step(dev, steps, warmup, n_layers=28):
     """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model (testt_amd/model.py: 28
     decoder layers, final norm, the chunked fused head loss over the 151,936-token vocabulary)
@@ -480,6 +522,24 @@ def summarize_stats(stats_csv, bench_json, command):
     return "\n".join(out) + "\n"
 
 
+def summarize_kernels(stats_csv, title, command, top=30):
+    """Markdown table of every kernel of a rocprofv3 --kernel-trace --stats run, by total time
+    (hipBLASLt, torch and soupk kernels alike)."""
+    rows = sorted(_read_csv(stats_csv), key=lambda r: -float(r["TotalDurationNs"]))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    out = [f"# {title}", "", "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```",
+           command, "```", "", f"All kernels: {total / 1e6:.2f} ms in "
+           f"{sum(int(r['Calls']) for r in rows)} launches.", "",
+           "| kernel | calls | avg us | total ms | share |", "|---|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        name = r["Name"]
+        short = _kernel_base(name) if "soupk" in name else name.split("(")[0][:90]
+        out.append(f"| `{short}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.3f} | "
+                   f"{100 * float(r['TotalDurationNs']) / total:.1f}% |")
+    return "\n".join(out) + "\n"
+
+
 def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     """Markdown table of HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
     WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the 1 GiB device
@@ -539,12 +599,19 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer timing")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the whole-model training-step timing")
+    ap.add_argument("--heuristic-gemms", action="store_true",
+                    help="keep hipBLASLt's heuristic choice for every GEMM (no tuned table)")
     ap.add_argument("--summarize-stats", nargs=3, metavar=("STATS_CSV", "BENCH_JSON", "CMD"),
                     help="print a markdown summary of a rocprofv3 --stats run and exit (CPU)")
     ap.add_argument("--summarize-pmc", nargs=5,
                     metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "CMD1", "CMD2"),
                     help="print the HBM traffic table of two rocprofv3 --pmc runs and exit (CPU)")
+    ap.add_argument("--summarize-kernels", nargs=3, metavar=("STATS_CSV", "TITLE", "CMD"),
+                    help="print every kernel of a rocprofv3 --stats run by total time (CPU)")
     args = ap.parse_args()
+    if args.summarize_kernels:
+        sys.stdout.write(summarize_kernels(*args.summarize_kernels))
+        return
     if args.summarize_stats:
         sys.stdout.write(summarize_stats(*args.summarize_stats))
         return
@@ -563,6 +630,14 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _ext.lib()
+    gemm_table = None
+    if not args.heuristic_gemms:
+        from testt_amd import gemm_tuning
+
+        accepted = gemm_tuning.enable()
+        gemm_table = {"table": os.path.relpath(gemm_tuning.RESULTS, ROOT), "accepted": accepted}
+        log(f"tuned hipBLASLt solutions ({gemm_table['table']}): "
+            f"{'replayed' if accepted else 'rejected by TunableOp, heuristic choices'}")
     log("building inputs")
     cases = build_cases(dev)
     torch.cuda.synchronize(dev)
@@ -575,6 +650,11 @@ def main():
         log("timing one decoder layer fwd+bwd at 2048 tokens")
         layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
         log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us")
+    attn_t = None
+    if not args.no_layer:
+        log("timing the causal GQA attention kernels at the layer's shape")
+        attn_t = time_attention(dev, 50, 5)
+        log(f"attention fwd {attn_t['fwd']['us']} us, bwd {attn_t['bwd']['us']} us")
     step_t = None
     if not args.no_step:
         log("timing one training step of the 28-layer model at 2048 tokens")
@@ -625,6 +705,8 @@ def main():
                             "HIP-event durations",
         "kernels": kernels,
         "layer": layer_t,
+        "attention": attn_t,
+        "gemm_selection": gemm_table or "hipBLASLt heuristic (--heuristic-gemms)",
         "step": step_t,
         "copy_peak_GBps": copy_gbps,
         "copy_reference": "kernels[*].copy_us: a plain 16-byte non-temporal device copy "

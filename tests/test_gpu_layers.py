@@ -123,3 +123,23 @@ def test_frozen_linear_qkv_with_bias():
     out.backward(grad)
     ref.backward(grad.float())
     close(x.grad, xr.grad)
+
+
+def test_tuned_gemm_table_replays():
+    """The committed table of tuned hipBLASLt solutions (testt_amd/gemm_tuning.py) is accepted
+    on this system, and a tuned problem of the step (the o-projection, [2048 x 1536] @ W^T)
+    gives the heuristic's product up to fp32 summation order."""
+    from testt_amd import gemm_tuning
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2048, 1536, generator=g).to(torch.float16).to(DEV)
+    w = (0.02 * torch.randn(1536, 1536, generator=g)).to(torch.float16).to(DEV)
+    ref = x @ w.t()
+    try:
+        assert gemm_tuning.enable()
+        got = x @ w.t()
+        torch.cuda.synchronize()
+    finally:
+        gemm_tuning.disable()
+    exact = x.double() @ w.double().t()
+    assert (got.double() - exact).abs().max() <= 2 * (ref.double() - exact).abs().max() + 1e-3
