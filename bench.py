@@ -306,10 +306,58 @@ def time_layer(dev, steps, warmup):
         e1.record()
         torch.cuda.synchronize(dev)
         out[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 1)
+    out.update(graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps))
     out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
                note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs in fp16, "
-                    "every other op (attention included) a soupk kernel (testt_amd/layer.py)")
+                    "every other op (attention included) a soupk kernel (testt_amd/layer.py); "
+                    "fwd_bwd_us / fwd_us: eager loop, bounded by the host's enqueue rate; "
+                    "graph_*: the same step captured once in a HIP graph and replayed (the "
+                    "layer's GPU time; replays match the eager step bit for bit, "
+                    "tests/test_gpu_layer_graph.py)")
     return out
+
+
+def graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps):
+    """The layer's forward+backward (and forward alone) captured in a HIP graph
+    (torch.cuda.graph) and replayed `steps` times between torch events: the launches and their
+    work without the Python and dispatch time of the eager loop."""
+    from testt_amd import layer
+
+    B, T = workloads.BATCH, workloads.SEQ
+    s_in = s0.clone().requires_grad_(True)
+    d_in = d0.clone().requires_grad_(True)
+    leaves = (s_in, d_in, *w.lora_q, *w.lora_v)
+
+    def step(backward):
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, None)
+        if backward:
+            torch.autograd.backward([s, d], [gs, gd])
+        for t in leaves:
+            t.grad = None
+
+    res = {}
+    for name, bwd in (("graph_fwd_bwd_us", True), ("graph_fwd_us", False)):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step(bwd)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(bwd)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        res[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 1)
+        del graph
+    return res
 
 
 def time_attention(dev, steps, warmup):
@@ -649,7 +697,9 @@ def main():
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
         layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
-        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us")
+        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us (eager); "
+            f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
+            f"{layer_t['graph_fwd_bwd_us']} us")
     attn_t = None
     if not args.no_layer:
         log("timing the causal GQA attention kernels at the layer's shape")
