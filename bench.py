@@ -693,13 +693,6 @@ def main():
     host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
     copy_us = copy_reference(cases, dev)
-    layer_t = None
-    if not args.no_layer:
-        log("timing one decoder layer fwd+bwd at 2048 tokens")
-        layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
-        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us (eager); "
-            f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
-            f"{layer_t['graph_fwd_bwd_us']} us")
     attn_t = None
     if not args.no_layer:
         log("timing the causal GQA attention kernels at the layer's shape")
@@ -711,6 +704,15 @@ def main():
         step_t = time_step(dev, 5, 2)
         log(f"step fwd {step_t['fwd_ms']} ms, fwd+bwd {step_t['fwd_bwd_ms']} ms, "
             f"{step_t['tokens_per_s']} tokens/s")
+    # Last: the layer timing captures HIP graphs, and eager work of the same process measured
+    # after a capture ran slower (the 28-layer step: 36 ms against 25 ms before it).
+    layer_t = None
+    if not args.no_layer:
+        log("timing one decoder layer fwd+bwd at 2048 tokens")
+        layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
+        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us (eager); "
+            f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
+            f"{layer_t['graph_fwd_bwd_us']} us")
     kernels = {}
     total_us = 0.0
     total_bytes = 0

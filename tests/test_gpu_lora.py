@@ -1,0 +1,113 @@
+"""GPU: the rank-16 LoRA kernels (testt_amd/csrc/lora.hip) against float64 restatements of the
+rounding steps of the fp16 GEMMs they replace (peft's branch under fp16 autocast,
+solution/model.py:195-206).  Each fp16 result is one rounding of a sum of exact fp16 products
+accumulated in fp32, so it lies within n fp16 ulps of the exact sum (n = 1, or 2 where a
+scaling multiplies an already rounded value) plus the fp32 summation error, bounded by
+32 * 2^-24 * sum|terms| (the sums are at most ~16 additions deep: 32-product MFMA steps, then
+four partial sums); the second term matters only where the sum cancels to a small result.
+gs = fp16(g * scaling) is elementwise and exact.  The fused QKVLora is also checked against its
+separate-GEMM path."""
+
+import pytest
+import torch
+
+from testt_amd import layer, lora, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def within_ulps(got, exact, n, abs_terms):
+    """|got - exact| <= n fp16 ulps of exact + 32 * 2^-24 * abs_terms (float64 tensors)."""
+    h = exact.to(torch.float16)
+    inf = torch.tensor(float("inf"), dtype=torch.float16, device=h.device)
+    ulp = (torch.nextafter(h.abs(), inf) - h.abs()).double()
+    err = (got.double() - exact).abs()
+    bad = err > n * ulp + 32 * 2.0 ** -24 * abs_terms
+    assert not bool(bad.any()), (f"{int(bad.sum())} of {bad.numel()} beyond the bound, "
+                                 f"max err {float(err.max()):.3g}")
+
+
+def params(H, NQ, NV, seed):
+    g = torch.Generator().manual_seed(seed)
+    a_q = (torch.randn(16, H, generator=g) / H ** 0.5).to(DEV)
+    a_v = (torch.randn(16, H, generator=g) / H ** 0.5).to(DEV)
+    b_q = (0.05 * torch.randn(NQ, 16, generator=g)).to(DEV)
+    b_v = (0.05 * torch.randn(NV, 16, generator=g)).to(DEV)
+    return a_q, a_v, b_q, b_v
+
+
+def f64_16(t):
+    return t.to(torch.float16).double()
+
+
+@pytest.mark.parametrize("M,H,NQ,NV,scaling", [(2048, 1536, 1536, 256, 2.0), (37, 512, 512, 256, 0.7),
+                                               (1, 256, 256, 128, 2.0)])
+def test_lora_fwd(M, H, NQ, NV, scaling):
+    print(f"lora fwd M={M} H={H} NQ={NQ} NV={NV} s={scaling}", flush=True)
+    a_q, a_v, b_q, b_v = params(H, NQ, NV, M + H)
+    g = torch.Generator().manual_seed(1)
+    y = torch.randn(M, H, generator=g).to(torch.float16).to(DEV)
+    t, lq, lv = lora.lora_fwd(y, a_q, a_v, b_q, b_v, scaling)
+    a16 = f64_16(torch.cat([a_q, a_v]))
+    within_ulps(t, y.double() @ a16.t(), 1, y.double().abs() @ a16.abs().t())
+    for out, tt, b in ((lq, t[:, :16], b_q), (lv, t[:, 16:], b_v)):
+        b16 = f64_16(b)
+        inner = (tt.double() @ b16.t()).to(torch.float16).double()   # one GEMM rounding
+        within_ulps(out, inner * scaling, 2, scaling * (tt.double().abs() @ b16.abs().t()))
+
+
+@pytest.mark.parametrize("M,H,NQ,NV,scaling,strided", [(2048, 1536, 1536, 256, 2.0, True),
+                                                       (37, 512, 512, 256, 0.7, False),
+                                                       (1, 256, 256, 128, 2.0, True)])
+def test_lora_bwd_rows(M, H, NQ, NV, scaling, strided):
+    print(f"lora bwd rows M={M} H={H} NQ={NQ} NV={NV} s={scaling} strided={strided}", flush=True)
+    a_q, a_v, b_q, b_v = params(H, NQ, NV, M + NQ)
+    g = torch.Generator().manual_seed(2)
+    if strided:      # the layout RopePack's backward hands over: views of one [M, NQ+2NV+...]
+        wide = (1e-2 * torch.randn(M, NQ + 2 * NV, generator=g)).to(torch.float16).to(DEV)
+        g_q, g_v = wide[:, :NQ], wide[:, NQ + NV:]
+    else:
+        g_q = (1e-2 * torch.randn(M, NQ, generator=g)).to(torch.float16).to(DEV)
+        g_v = (1e-2 * torch.randn(M, NV, generator=g)).to(torch.float16).to(DEV)
+    gs_q, gs_v, dt, dy = lora.lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling)
+    assert torch.equal(gs_q, (g_q.float() * scaling).to(torch.float16))
+    assert torch.equal(gs_v, (g_v.float() * scaling).to(torch.float16))
+    bq16, bv16 = f64_16(b_q), f64_16(b_v)
+    exact_dt = torch.cat([gs_q.double() @ bq16, gs_v.double() @ bv16], dim=1)
+    terms_dt = torch.cat([gs_q.double().abs() @ bq16.abs(), gs_v.double().abs() @ bv16.abs()],
+                         dim=1)
+    within_ulps(dt, exact_dt, 1, terms_dt)
+    a16 = f64_16(torch.cat([a_q, a_v]))
+    within_ulps(dy, dt.double() @ a16, 1, dt.double().abs() @ a16.abs())
+
+
+def rel(a, b):
+    a, b = a.detach().double(), b.detach().double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def test_qkvlora_fused_matches_gemm_path(monkeypatch):
+    """The same QKVLora step through the kernels and through separate fp16 GEMMs: outputs and
+    every gradient agree to fp16 GEMM rounding (relative L2 < 2e-3)."""
+    w = layer.synthetic_layer(DEV, seed=9)
+    M = 300
+    g = torch.Generator().manual_seed(3)
+    y = torch.randn(M, workloads.HIDDEN, generator=g).to(torch.float16).to(DEV)
+    gq = (1e-2 * torch.randn(M, 2048, generator=g)).to(torch.float16).to(DEV)
+    glq = (1e-2 * torch.randn(M, 1536, generator=g)).to(torch.float16).to(DEV)
+    glv = (1e-2 * torch.randn(M, 256, generator=g)).to(torch.float16).to(DEV)
+    results = []
+    for fused in (True, False):
+        monkeypatch.setattr(layer, "USE_FUSED_LORA", fused)
+        yi = y.clone().requires_grad_(True)
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+        qkv, lq, lv = layer.QKVLora.apply(yi, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
+                                          (w.q, w.k, w.v))
+        torch.autograd.backward([qkv, lq, lv], [gq, glq, glv])
+        results.append([qkv, lq, lv, yi.grad] + [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+    assert torch.equal(results[0][0], results[1][0])          # the projection itself: one GEMM
+    for name, a, b in zip(("lq", "lv", "dy", "dA_q", "dB_q", "dA_v", "dB_v"), results[0][1:],
+                          results[1][1:]):
+        assert rel(a, b) < 2e-3, (name, rel(a, b))

@@ -31,6 +31,7 @@ from dataclasses import dataclass
 import torch
 
 from . import attention as _attention
+from . import lora as _lora
 from . import workloads
 from .mlp import fused_mlp
 from .nf4 import frozen_linear, keep_for_backward, unpack_concat, unpacked_for_backward
@@ -85,6 +86,10 @@ def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
         head_dim=head_dim, dropout=dropout, **nf4w)
 
 
+# Rank-16 LoRA through testt_amd/csrc/lora.hip (False: the separate fp16 GEMMs below).
+USE_FUSED_LORA = True
+
+
 class QKVLora(torch.autograd.Function):
     """(qkv, lora_q, lora_v) from the fp16 norm output y, for LoRA without dropout:
     qkv = y @ [Wq;Wk;Wv]^T + b (frozen NF4; the unpacked weight kept for backward, or unpacked
@@ -98,6 +103,13 @@ class QKVLora(torch.autograd.Function):
         qkv = torch.nn.functional.linear(y16, w, bias)
         keep_for_backward(ctx, w)
         del w
+        ctx.weights, ctx.scaling = weights, scaling
+        params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
+        ctx.fused = USE_FUSED_LORA and _lora.supported(y16, *params)
+        if ctx.fused:       # testt_amd/csrc/lora.hip: one launch for t, lq and lv
+            t, lq, lv = _lora.lora_fwd(y16, *params, scaling)
+            ctx.save_for_backward(y16, t, *params)
+            return qkv, lq, lv
         r = a_q.shape[0]
         a16 = torch.cat([a_q.detach(), a_v.detach()]).to(torch.float16)
         t = y16 @ a16.t()
@@ -109,11 +121,13 @@ class QKVLora(torch.autograd.Function):
             lq.mul_(scaling)
             lv.mul_(scaling)
         ctx.save_for_backward(y16, t, a16, bq16, bv16)
-        ctx.weights, ctx.scaling, ctx.rank = weights, scaling, r
+        ctx.rank = r
         return qkv, lq, lv
 
     @staticmethod
     def backward(ctx, g_qkv, g_lq, g_lv):
+        if ctx.fused:
+            return QKVLora._backward_fused(ctx, g_qkv, g_lq, g_lv)
         y16, t, a16, bq16, bv16 = ctx.saved_tensors
         s, r = ctx.scaling, ctx.rank
         m = y16.shape[0]
@@ -133,8 +147,25 @@ class QKVLora(torch.autograd.Function):
         dy = dt @ a16
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
-            dy = torch.addmm(dy, g_qkv.to(torch.float16), w)
+            dy.addmm_(g_qkv.to(torch.float16), w)
         return dy, None, grads[0], grads[1], grads[2], grads[3], None, None
+
+    @staticmethod
+    def _backward_fused(ctx, g_qkv, g_lq, g_lv):
+        y16, t, a_q, a_v, b_q, b_v = ctx.saved_tensors
+        r = _lora.RANK
+        if g_lq is None and g_lv is None:
+            g_lq = torch.zeros((y16.shape[0], b_q.shape[0]), dtype=torch.float16,
+                               device=y16.device)
+        gs_q, gs_v, dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling)
+        # fp16 products cast to the fp32 parameters, as autocast's backward gives them
+        d_bq = (gs_q.t() @ t[:, :r]).float()
+        d_bv = (gs_v.t() @ t[:, r:]).float()
+        da = (dt.t() @ y16).float()
+        if g_qkv is not None:
+            w = unpacked_for_backward(ctx, ctx.weights, y16.device)
+            dy.addmm_(g_qkv.to(torch.float16), w)
+        return dy, None, da[:r], d_bq, da[r:], d_bv, None, None
 
 
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):

@@ -1,0 +1,75 @@
+"""The LoRA branch of the q and v projections for rank 16 on gfx950 (testt_amd/csrc/lora.hip):
+peft's lora_B(lora_A(x)) * scaling under fp16 autocast (solution/model.py:195-206, dropout 0),
+in one launch forward and one backward, in place of the separate fp16 GEMMs, casts and
+scalings.  `layer.QKVLora` uses it when `supported` holds and keeps its GEMM path otherwise.
+
+    lora_fwd(y16, a_q, a_v, b_q, b_v, scaling)      -> t [M, 32], lq [M, NQ], lv [M, NV] fp16
+    lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s)   -> gs_q, gs_v, dt [M, 32], dy [M, H] fp16
+
+with t = fp16(y A^T), lq = fp16(fp16(t_q B_q^T) * s), gs = fp16(g * s),
+dt = fp16(gs_q B_q | gs_v B_v), dy = fp16(dt A): the rounding steps of the fp16 GEMMs they
+replace (fp32 sums in another order)."""
+
+import torch
+
+from . import _ext
+
+RANK = 16
+
+
+def supported(y16, a_q, a_v, b_q, b_v):
+    """Rank 16, fp16 y and fp32 parameters on one HIP device, H, NQ, NV multiples of 128."""
+    if not (y16.is_cuda and y16.dtype == torch.float16 and y16.dim() == 2):
+        return False
+    H = y16.shape[1]
+    for p in (a_q, a_v, b_q, b_v):
+        if p.dtype != torch.float32 or p.device != y16.device or not p.is_contiguous():
+            return False
+    return (tuple(a_q.shape) == (RANK, H) and tuple(a_v.shape) == (RANK, H)
+            and b_q.dim() == 2 and b_q.shape[1] == RANK and b_v.dim() == 2
+            and b_v.shape[1] == RANK and H % 128 == 0 and b_q.shape[0] % 128 == 0
+            and b_v.shape[0] % 128 == 0)
+
+
+def lora_fwd(y16, a_q, a_v, b_q, b_v, scaling):
+    _ext.require(y16, "y16", dtype=torch.float16, ndim=2)
+    M, H = y16.shape
+    NQ, NV = b_q.shape[0], b_v.shape[0]
+    dev = y16.device
+    t = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
+    lq = torch.empty((M, NQ), dtype=torch.float16, device=dev)
+    lv = torch.empty((M, NV), dtype=torch.float16, device=dev)
+    _ext.call("soupk_lora_fwd", _ext.ptr(y16), _ext.ptr(a_q), _ext.ptr(a_v), _ext.ptr(b_q),
+              _ext.ptr(b_v), float(scaling), _ext.ptr(t), _ext.ptr(lq), _ext.ptr(lv), M, H, NQ,
+              NV, RANK, _ext.stream_of(y16))
+    return t, lq, lv
+
+
+def _rows(g, n, m, dev):
+    """g as an fp16 [m, n] view with unit column stride (zeros for a missing gradient)."""
+    if g is None:
+        return torch.zeros((m, n), dtype=torch.float16, device=dev)
+    g = g.to(torch.float16)
+    if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
+        g = g.contiguous()
+    return g
+
+
+def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling):
+    M, H = None, a_q.shape[1]
+    NQ, NV = b_q.shape[0], b_v.shape[0]
+    ref = g_q if g_q is not None else g_v
+    M, dev = ref.shape[0], ref.device
+    g_q, g_v = _rows(g_q, NQ, M, dev), _rows(g_v, NV, M, dev)
+    if tuple(g_q.shape) != (M, NQ) or tuple(g_v.shape) != (M, NV):
+        raise ValueError(f"lora_bwd_rows: gradient shapes {tuple(g_q.shape)}, "
+                         f"{tuple(g_v.shape)} do not match ({M}, {NQ}), ({M}, {NV})")
+    gs_q = torch.empty((M, NQ), dtype=torch.float16, device=dev)
+    gs_v = torch.empty((M, NV), dtype=torch.float16, device=dev)
+    dt = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
+    dy = torch.empty((M, H), dtype=torch.float16, device=dev)
+    _ext.call("soupk_lora_bwd_rows", _ext.ptr(g_q), g_q.stride(0), _ext.ptr(g_v), g_v.stride(0),
+              _ext.ptr(a_q), _ext.ptr(a_v), _ext.ptr(b_q), _ext.ptr(b_v), float(scaling),
+              _ext.ptr(gs_q), _ext.ptr(gs_v), _ext.ptr(dt), _ext.ptr(dy), M, H, NQ, NV, RANK,
+              _ext.stream_of(dy))
+    return gs_q, gs_v, dt, dy
