@@ -223,6 +223,19 @@ int soupk_lora_bwd_rows(const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, 
                         uint16_t* dy, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
                         void* stream);
 
+/*
+ * Its backward, the parameter gradients (reductions over the M rows), each the fp16 GEMM result
+ * cast to fp32: d_aq = fp16(dt[:, :16]^T y), d_av = fp16(dt[:, 16:]^T y) [16, H];
+ * d_bq = fp16(gs_q^T t[:, :16]) [NQ, 16], d_bv = fp16(gs_v^T t[:, 16:]) [NV, 16].  workspace:
+ * fp32 device memory of ceil(M/128) * (32*H + 16*(NQ + NV)) floats (per-slice partial sums,
+ * added in slice order: deterministic).  Same shape rules (H, NQ, NV multiples of 128).
+ */
+int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
+                          const uint16_t* gs_q, const uint16_t* gs_v, float* workspace,
+                          int64_t workspace_floats, float* d_aq, float* d_av, float* d_bq,
+                          float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,3 +111,33 @@ def test_qkvlora_fused_matches_gemm_path(monkeypatch):
     for name, a, b in zip(("lq", "lv", "dy", "dA_q", "dB_q", "dA_v", "dB_v"), results[0][1:],
                           results[1][1:]):
         assert rel(a, b) < 2e-3, (name, rel(a, b))
+
+
+@pytest.mark.parametrize("M,H,NQ,NV", [(2048, 1536, 1536, 256), (300, 512, 512, 256),
+                                       (37, 256, 256, 128), (1, 256, 256, 128)])
+def test_lora_bwd_params(M, H, NQ, NV):
+    """The parameter gradients (reductions over the rows, per-128-row slices added in order):
+    fp16 roundings of the exact sums, as fp32."""
+    print(f"lora bwd params M={M} H={H} NQ={NQ} NV={NV}", flush=True)
+    g = torch.Generator().manual_seed(M + H)
+
+    def f16(*shape, sd):
+        return (sd * torch.randn(*shape, generator=g)).to(torch.float16).to(DEV)
+
+    y, t, dt = f16(M, H, sd=1.0), f16(M, 32, sd=0.5), f16(M, 32, sd=0.01)
+    gs_q, gs_v = f16(M, NQ, sd=0.01), f16(M, NV, sd=0.01)
+    d_aq, d_av, d_bq, d_bv = lora.lora_bwd_params(y, t, dt, gs_q, gs_v)
+    assert d_aq.dtype == torch.float32 and d_bq.shape == (NQ, 16) and d_bv.shape == (NV, 16)
+    yd, td, dtd = y.double(), t.double(), dt.double()
+    within_ulps(torch.cat([d_aq, d_av]), dtd.t() @ yd, 1, dtd.abs().t() @ yd.abs())
+    within_ulps(d_bq, gs_q.double().t() @ td[:, :16], 1, gs_q.double().abs().t() @ td[:, :16].abs())
+    within_ulps(d_bv, gs_v.double().t() @ td[:, 16:], 1, gs_v.double().abs().t() @ td[:, 16:].abs())
+
+
+def test_lora_bwd_params_no_rows():
+    e = torch.empty(0, 256, dtype=torch.float16, device=DEV)
+    e32 = torch.empty(0, 32, dtype=torch.float16, device=DEV)
+    out = lora.lora_bwd_params(e, e32, e32, e, torch.empty(0, 128, dtype=torch.float16,
+                                                          device=DEV))
+    for x in out:
+        assert torch.equal(x, torch.zeros_like(x))

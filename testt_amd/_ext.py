@@ -45,6 +45,8 @@ SIGNATURES = {
     "soupk_lora_fwd": [_p, _p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
     "soupk_lora_bwd_rows": [_p, _i64, _p, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _i64, _i32,
                             _i32, _i32, _i32, _p],
+    "soupk_lora_bwd_params": [_p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i32, _i32,
+                              _i32, _i32, _p],
 }
 
 

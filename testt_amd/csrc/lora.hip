@@ -45,9 +45,9 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
 
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(x)); }
 
-// Eight consecutive fp32 values rounded to fp16.
-__device__ __forceinline__ h8 cast8(const float* p) {
-  const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+__device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+__device__ __forceinline__ h8 to_h8(f4 a, f4 b) {
   h8 r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -57,7 +57,11 @@ __device__ __forceinline__ h8 cast8(const float* p) {
   return r;
 }
 
-__device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+// Loop steps and tiles are processed kBatch at a time: the loads of a batch (at clamped
+// indices, so unconditional) are all issued before its first MFMA, and the MFMAs and stores
+// past the end of the range are skipped (a wavefront-uniform test).  One step at a time, each
+// MFMA waited for its own loads.
+constexpr int kBatch = 4;
 
 __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
     const uint16_t* __restrict__ y, const float* __restrict__ aq, const float* __restrict__ av,
@@ -76,12 +80,28 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   f4 acc_q = {0.f, 0.f, 0.f, 0.f}, acc_v = {0.f, 0.f, 0.f, 0.f};
   const uint16_t* yrow = y + row * H;
 
-  for (int k0 = w * kw; k0 < (w + 1) * kw; k0 += 32) {
-    const h8 ya = *reinterpret_cast<const h8*>(yrow + k0 + 8 * gr);
-    const h8 qa = cast8(aq + static_cast<int64_t>(ql) * H + k0 + 8 * gr);
-    const h8 va = cast8(av + static_cast<int64_t>(ql) * H + k0 + 8 * gr);
-    acc_q = mfma32(ya, qa, acc_q);
-    acc_v = mfma32(ya, va, acc_v);
+  const int steps = kw / 32;
+  const float* aqrow = aq + static_cast<int64_t>(ql) * H + 8 * gr;
+  const float* avrow = av + static_cast<int64_t>(ql) * H + 8 * gr;
+  for (int s0 = 0; s0 < steps; s0 += kBatch) {
+    h8 ya[kBatch];
+    f4 qa[kBatch][2], va[kBatch][2];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k0 = w * kw + 32 * min(s0 + u, steps - 1);
+      ya[u] = *reinterpret_cast<const h8*>(yrow + k0 + 8 * gr);
+      qa[u][0] = *reinterpret_cast<const f4*>(aqrow + k0);
+      qa[u][1] = *reinterpret_cast<const f4*>(aqrow + k0 + 4);
+      va[u][0] = *reinterpret_cast<const f4*>(avrow + k0);
+      va[u][1] = *reinterpret_cast<const f4*>(avrow + k0 + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (s0 + u < steps) {
+        acc_q = mfma32(ya[u], to_h8(qa[u][0], qa[u][1]), acc_q);
+        acc_v = mfma32(ya[u], to_h8(va[u][0], va[u][1]), acc_v);
+      }
+    }
   }
   // C: column = feature ql, rows 4gr .. +3
 #pragma unroll
@@ -101,24 +121,40 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   // lq, lv: tile f0..f0+15 of the output columns, transposed: A = B16 rows (feature f0 + ql,
   // k = rank 4gr..+3), B = t rows (column = row ql of the workgroup, same k)
   const int nq16 = NQ / 16, n16 = nq16 + NV / 16;
-  for (int tile = w; tile < n16; tile += 4) {
-    const bool is_q = tile < nq16;
-    const int f0 = 16 * (is_q ? tile : tile - nq16);
-    const int N = is_q ? NQ : NV;
-    const f4 bw = *reinterpret_cast<const f4*>((is_q ? bq : bv) +
-                                               static_cast<int64_t>(f0 + ql) * kR + 4 * gr);
-    const h4 a = {static_cast<_Float16>(bw[0]), static_cast<_Float16>(bw[1]),
-                  static_cast<_Float16>(bw[2]), static_cast<_Float16>(bw[3])};
-    const float* trow = &tt[ql][(is_q ? 0 : kR) + 4 * gr];
-    const h4 b = {static_cast<_Float16>(trow[0]), static_cast<_Float16>(trow[1]),
-                  static_cast<_Float16>(trow[2]), static_cast<_Float16>(trow[3])};
-    const f4 c = mfma16(a, b, f4{0.f, 0.f, 0.f, 0.f});
-    // C: column = row ql, rows = features f0 + 4gr .. +3
-    if (m0 + ql < M) {
-      uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + ql) * N + f0 + 4 * gr;
-      *reinterpret_cast<u32x2*>(dst) =
-          u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
-                pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+  const float* tq = &tt[ql][4 * gr];
+  const float* tv = &tt[ql][kR + 4 * gr];
+  const h4 tq4 = {static_cast<_Float16>(tq[0]), static_cast<_Float16>(tq[1]),
+                  static_cast<_Float16>(tq[2]), static_cast<_Float16>(tq[3])};
+  const h4 tv4 = {static_cast<_Float16>(tv[0]), static_cast<_Float16>(tv[1]),
+                  static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
+  const bool row_ok = m0 + ql < M;
+  for (int t0 = w; t0 < n16; t0 += 4 * kBatch) {
+    f4 bw[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int tile = min(t0 + 4 * u, n16 - 1);
+      const bool is_q = tile < nq16;
+      const int f0 = 16 * (is_q ? tile : tile - nq16);
+      bw[u] = *reinterpret_cast<const f4*>((is_q ? bq : bv) +
+                                           static_cast<int64_t>(f0 + ql) * kR + 4 * gr);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int tile = t0 + 4 * u;
+      if (tile >= n16) break;
+      const bool is_q = tile < nq16;
+      const int f0 = 16 * (is_q ? tile : tile - nq16);
+      const int N = is_q ? NQ : NV;
+      const h4 a = {static_cast<_Float16>(bw[u][0]), static_cast<_Float16>(bw[u][1]),
+                    static_cast<_Float16>(bw[u][2]), static_cast<_Float16>(bw[u][3])};
+      const f4 c = mfma16(a, is_q ? tq4 : tv4, f4{0.f, 0.f, 0.f, 0.f});
+      // C: column = row ql, rows = features f0 + 4gr .. +3
+      if (row_ok) {
+        uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + ql) * N + f0 + 4 * gr;
+        *reinterpret_cast<u32x2*>(dst) =
+            u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
+                  pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+      }
     }
   }
 }
@@ -141,25 +177,40 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   // way; B operand = B16 (column = rank index ql, k = j rows: B is [N, r] row-major, so the
   // 8 k-values of a lane are 8 rows, each read by 16 consecutive lanes as 64 contiguous bytes)
   f4 acc_q = {0.f, 0.f, 0.f, 0.f}, acc_v = {0.f, 0.f, 0.f, 0.f};
-  auto step = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const float* b, int j0,
-                  f4& acc) {
-    const h8 graw = *reinterpret_cast<const h8*>(g + row * ldg + j0 + 8 * gr);
-    h8 ga;
+  // steps of 32 columns of g over this wavefront's quarter of N
+  auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const float* b,
+                 f4& acc) {
+    const int kn = N / 4, steps = kn / 32;
+    const uint16_t* grow = g + row * ldg + w * kn + 8 * gr;
+    const float* bcol = b + static_cast<int64_t>(w * kn + 8 * gr) * kR + ql;
+    for (int s0 = 0; s0 < steps; s0 += kBatch) {
+      h8 graw[kBatch];
+      float braw[kBatch][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      ga[i] = static_cast<_Float16>(static_cast<float>(graw[i]) * scaling);
-    if (row_ok) *reinterpret_cast<h8*>(gs + static_cast<int64_t>(mr) * N + j0 + 8 * gr) = ga;
-    h8 ba;
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = 32 * min(s0 + u, steps - 1);
+        graw[u] = *reinterpret_cast<const h8*>(grow + j);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      ba[i] = static_cast<_Float16>(b[static_cast<int64_t>(j0 + 8 * gr + i) * kR + ql]);
-    acc = mfma32(ga, ba, acc);
+        for (int i = 0; i < 8; ++i) braw[u][i] = bcol[static_cast<int64_t>(j + i) * kR];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (s0 + u >= steps) break;
+        h8 ga, ba;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ga[i] = static_cast<_Float16>(static_cast<float>(graw[u][i]) * scaling);
+          ba[i] = static_cast<_Float16>(braw[u][i]);
+        }
+        if (row_ok)
+          *reinterpret_cast<h8*>(gs + static_cast<int64_t>(mr) * N + w * kn + 32 * (s0 + u) +
+                                 8 * gr) = ga;
+        acc = mfma32(ga, ba, acc);
+      }
+    }
   };
-  const int kq = NQ / 4, kv = NV / 4;
-
-  for (int j0 = w * kq; j0 < (w + 1) * kq; j0 += 32) step(gq, ldq, gsq, NQ, bq, j0, acc_q);
-
-  for (int j0 = w * kv; j0 < (w + 1) * kv; j0 += 32) step(gv, ldv, gsv, NV, bv, j0, acc_v);
+  run(gq, ldq, gsq, NQ, bq, acc_q);
+  run(gv, ldv, gsv, NV, bv, acc_v);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     part[w][4 * gr + i][ql] = acc_q[i];
@@ -178,21 +229,143 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   // 16-column tile of H at a time, transposed: A operand = A16 columns (row h0 + ql, k = rank
   // 8gr..+7: 8 rows of A, each read by 16 consecutive lanes as 64 contiguous bytes), B = dt
   // rows (column = row ql)
-  for (int tile = w; tile < H / 16; tile += 4) {
-    const int h0 = 16 * tile;
-    const float* acol = (gr < 2 ? aq + static_cast<int64_t>(8 * gr) * H
-                                : av + static_cast<int64_t>(8 * (gr - 2)) * H) + h0 + ql;
-    h8 a, b;
+  h8 dtb;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a[i] = static_cast<_Float16>(acol[static_cast<int64_t>(i) * H]);
-      b[i] = static_cast<_Float16>(dts[ql][8 * gr + i]);
+  for (int i = 0; i < 8; ++i) dtb[i] = static_cast<_Float16>(dts[ql][8 * gr + i]);
+  const float* abase = (gr < 2 ? aq + static_cast<int64_t>(8 * gr) * H
+                               : av + static_cast<int64_t>(8 * (gr - 2)) * H) + ql;
+  const int n16 = H / 16;
+  for (int t0 = w; t0 < n16; t0 += 4 * kBatch) {
+    float araw[kBatch][8];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int h0 = 16 * min(t0 + 4 * u, n16 - 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) araw[u][i] = abase[static_cast<int64_t>(i) * H + h0];
     }
-    const f4 c = mfma32(a, b, f4{0.f, 0.f, 0.f, 0.f});
-    if (m0 + ql < M)
-      *reinterpret_cast<u32x2*>(dy + static_cast<int64_t>(m0 + ql) * H + h0 + 4 * gr) =
-          u32x2{pack_h2(c[0], c[1]), pack_h2(c[2], c[3])};
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int tile = t0 + 4 * u;
+      if (tile >= n16) break;
+      h8 a;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = static_cast<_Float16>(araw[u][i]);
+      const f4 c = mfma32(a, dtb, f4{0.f, 0.f, 0.f, 0.f});
+      if (row_ok)
+        *reinterpret_cast<u32x2*>(dy + static_cast<int64_t>(mr) * H + 16 * tile + 4 * gr) =
+            u32x2{pack_h2(c[0], c[1]), pack_h2(c[2], c[3])};
+    }
   }
+}
+
+// ---- parameter gradients: reductions over the rows ---------------------------------------
+//   dA[i][k]  = fp16(sum_m dt[m][i] y[m][k])          i < 2r, k < H  (A_q rows, then A_v rows)
+//   dBq[j][i] = fp16(sum_m gs_q[m][j] t[m][i])        j < NQ, i < r
+//   dBv[j][i] = fp16(sum_m gs_v[m][j] t[m][r + i])    j < NV, i < r
+// each cast to fp32 (the fp16 GEMM result cast to the fp32 parameter, as autocast's backward
+// gives it).  lora_params_partial_kernel: workgroup (column block of 64, slice of kSlice rows)
+// stages 64-row chunks of X (y, gs_q or gs_v: its 64 columns) and Z (dt or t) through LDS,
+// transposed so that each MFMA operand is 8 consecutive rows of one column, and writes fp32
+// partial sums per slice; lora_params_reduce_kernel adds the slices in order and rounds.
+constexpr int kSlice = 128;        // rows per slice
+constexpr int kChunk = 64;         // rows per LDS chunk
+constexpr int kPStride = kChunk + 8;   // transposed tile row (halves): 144 B, 16-B aligned
+
+// Rows (2rp, 2rp+1) x 8 columns, loaded at clamped rows and zeroed past `rows`, written
+// transposed into tr[col][row] (stride kPStride) as 4-byte pairs.
+__device__ __forceinline__ void stage_pair_t(_Float16* tr, const uint16_t* src, int64_t ld,
+                                             int r0, int rows, int rp, int c8) {
+  const int t0 = r0 + 2 * rp, t1 = t0 + 1;
+  u32x4 a = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t0, rows - 1)) * ld +
+                                            8 * c8);
+  u32x4 b = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t1, rows - 1)) * ld +
+                                            8 * c8);
+  if (t0 >= rows) a = u32x4{0u, 0u, 0u, 0u};
+  if (t1 >= rows) b = u32x4{0u, 0u, 0u, 0u};
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t* col = reinterpret_cast<uint32_t*>(tr + (8 * c8) * kPStride + 2 * rp);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    col[(2 * j) * (kPStride / 2)] = (aw[j] & 0xffffu) | (bw[j] << 16);
+    col[(2 * j + 1) * (kPStride / 2)] = (aw[j] >> 16) | (bw[j] & 0xffff0000u);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void lora_params_partial_kernel(
+    const uint16_t* __restrict__ y, const uint16_t* __restrict__ t,
+    const uint16_t* __restrict__ dt, const uint16_t* __restrict__ gsq,
+    const uint16_t* __restrict__ gsv, float* __restrict__ part, int M, int H, int NQ, int NV,
+    int64_t n_out) {
+  __shared__ __align__(16) _Float16 XT[64 * kPStride];       // [64 columns][64 rows]
+  __shared__ __align__(16) _Float16 ZT[2 * kR * kPStride];   // [32 columns][64 rows]
+  const int nba = H / 64, nbq = NQ / 64;
+  const int blk = blockIdx.x, slice = blockIdx.y;
+  // kind 0: dA (X = y, Z = dt, 32 Z columns), 1: dBq (X = gs_q, Z = t[:, :r]), 2: dBv
+  const int kind = blk < nba ? 0 : (blk < nba + nbq ? 1 : 2);
+  const int col0 = 64 * (kind == 0 ? blk : (kind == 1 ? blk - nba : blk - nba - nbq));
+  const uint16_t* X = kind == 0 ? y : (kind == 1 ? gsq : gsv);
+  const int64_t ldx = kind == 0 ? H : (kind == 1 ? NQ : NV);
+  const int zc = kind == 0 ? 2 * kR : kR;                   // Z columns
+  const uint16_t* Z = (kind == 0 ? dt : t) + (kind == 2 ? kR : 0);
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  const int ql = lane & 15, gr = lane >> 4;
+  const int r_begin = slice * kSlice, r_end = min(M, r_begin + kSlice);
+  // dA: C = X^T Z tiles (row = X column, column = Z column): wave w owns X columns 16w..+15
+  //     and both Z tiles; dB: C = Z^T X (row = Z column, column = X column): wave w owns X
+  //     columns 16w..+15.  Either way a lane's 4 results are 4 consecutive partial entries.
+  f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  for (int r0 = r_begin; r0 < r_end; r0 += kChunk) {
+    __syncthreads();
+    {
+      const int rp = threadIdx.x & 31, c8 = threadIdx.x >> 5;   // 32 row pairs x 8 chunks
+      stage_pair_t(XT, X + col0, ldx, r0, r_end, rp, c8);
+      if (c8 < zc / 8) stage_pair_t(ZT, Z, 2 * kR, r0, r_end, rp, c8);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kChunk / 32; ++s) {
+      const h8 xf = *reinterpret_cast<const h8*>(XT + (16 * w + ql) * kPStride + 32 * s + 8 * gr);
+      const h8 z0 = *reinterpret_cast<const h8*>(ZT + ql * kPStride + 32 * s + 8 * gr);
+      if (kind == 0) {
+        const h8 z1 =
+            *reinterpret_cast<const h8*>(ZT + (kR + ql) * kPStride + 32 * s + 8 * gr);
+        acc0 = mfma32(xf, z0, acc0);   // rows = X columns, column = Z column ql
+        acc1 = mfma32(xf, z1, acc1);
+      } else {
+        acc0 = mfma32(z0, xf, acc0);   // rows = Z columns, column = X column
+      }
+    }
+  }
+  float* out = part + static_cast<int64_t>(slice) * n_out;
+  if (kind == 0) {
+    // dA[i][k]: i = Z column (ql, or r + ql), k = col0 + 16w + 4gr .. +3
+    const int k = col0 + 16 * w + 4 * gr;
+    *reinterpret_cast<f4*>(out + static_cast<int64_t>(ql) * H + k) = acc0;
+    *reinterpret_cast<f4*>(out + static_cast<int64_t>(kR + ql) * H + k) = acc1;
+  } else {
+    // dB[j][i]: j = col0 + 16w + ql (X column), i = 4gr .. +3
+    const int64_t base = 2 * kR * static_cast<int64_t>(H) + (kind == 2 ? kR * NQ : 0);
+    *reinterpret_cast<f4*>(out + base + static_cast<int64_t>(col0 + 16 * w + ql) * kR + 4 * gr) =
+        acc0;
+  }
+}
+
+// Sum of the slices in slice order, one fp16 rounding, then fp32: dA_q, dA_v [r, H], dB_q
+// [NQ, r], dB_v [NV, r] (the partial layout: dA rows, then dB_q, then dB_v).
+__global__ __launch_bounds__(256) void lora_params_reduce_kernel(
+    const float* __restrict__ part, int slices, int64_t n_out, int H, int NQ,
+    float* __restrict__ daq, float* __restrict__ dav, float* __restrict__ dbq,
+    float* __restrict__ dbv) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (o >= n_out) return;
+  float s = 0.f;
+  for (int i = 0; i < slices; ++i) s += part[static_cast<int64_t>(i) * n_out + o];
+  const float v = r16(s);
+  const int64_t na = static_cast<int64_t>(kR) * H;
+  if (o < na) daq[o] = v;
+  else if (o < 2 * na) dav[o - na] = v;
+  else if (o < 2 * na + static_cast<int64_t>(kR) * NQ) dbq[o - 2 * na] = v;
+  else dbv[o - 2 * na - static_cast<int64_t>(kR) * NQ] = v;
 }
 
 int check_dims(int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r) {
@@ -249,4 +422,43 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_rows(
   return launch_kernel(lora_bwd_rows_kernel, dim3(grid), dim3(kThreads),
                        static_cast<hipStream_t>(stream), g_q, ld_q, g_v, ld_v, a_q, a_v, b_q, b_v,
                        scaling, gs_q, gs_v, dt, dy, static_cast<int>(M), H, NQ, NV);
+}
+
+// Workspace of soupk_lora_bwd_params, in floats: ceil(M / 128) slices of partial sums.
+static int64_t lora_params_workspace(int64_t M, int32_t H, int32_t NQ, int32_t NV) {
+  const int64_t slices = (M + kSlice - 1) / kSlice;
+  return slices * (2 * kR * static_cast<int64_t>(H) + kR * static_cast<int64_t>(NQ + NV));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params(
+    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
+    const uint16_t* gs_v, float* workspace, int64_t workspace_floats, float* d_aq, float* d_av,
+    float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
+    void* stream) {
+  const int rc = check_dims(M, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  if (H % 64 || NQ % 64 || NV % 64) return kInvalid;
+  const int64_t n_out = 2 * kR * static_cast<int64_t>(H) + kR * static_cast<int64_t>(NQ + NV);
+  if (workspace_floats < lora_params_workspace(M, H, NQ, NV)) return kInvalid;
+  if (!d_aq || !d_av || !d_bq || !d_bv) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned reduce_grid = static_cast<unsigned>((n_out + 255) / 256);
+  if (M == 0)   // no rows: zero gradients (the reduction over no slices)
+    return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st,
+                         static_cast<const float*>(nullptr), 0, n_out, H, NQ, d_aq, d_av,
+                         d_bq, d_bv);
+  if (!y || !t || !dt || !gs_q || !gs_v || !workspace) return kInvalid;
+  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(t),
+                        static_cast<const void*>(dt), static_cast<const void*>(gs_q),
+                        static_cast<const void*>(gs_v), static_cast<const void*>(workspace)})
+    if (misaligned(p)) return kInvalid;
+  const int slices = static_cast<int>((M + kSlice - 1) / kSlice);
+  if (slices > 65535) return kInvalid;
+  const dim3 grid(static_cast<unsigned>(H / 64 + NQ / 64 + NV / 64),
+                  static_cast<unsigned>(slices));
+  int rc2 = launch_kernel(lora_params_partial_kernel, grid, dim3(kThreads), st, y, t, dt, gs_q,
+                          gs_v, workspace, static_cast<int>(M), H, NQ, NV, n_out);
+  if (rc2 != kOk) return rc2;
+  return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st, workspace,
+                       slices, n_out, H, NQ, d_aq, d_av, d_bq, d_bv);
 }

@@ -153,19 +153,16 @@ class QKVLora(torch.autograd.Function):
     @staticmethod
     def _backward_fused(ctx, g_qkv, g_lq, g_lv):
         y16, t, a_q, a_v, b_q, b_v = ctx.saved_tensors
-        r = _lora.RANK
         if g_lq is None and g_lv is None:
             g_lq = torch.zeros((y16.shape[0], b_q.shape[0]), dtype=torch.float16,
                                device=y16.device)
         gs_q, gs_v, dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling)
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
-        d_bq = (gs_q.t() @ t[:, :r]).float()
-        d_bv = (gs_v.t() @ t[:, r:]).float()
-        da = (dt.t() @ y16).float()
+        d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, gs_q, gs_v)
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)
-        return dy, None, da[:r], d_bq, da[r:], d_bv, None, None
+        return dy, None, d_aq, d_bq, d_av, d_bv, None, None
 
 
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):

@@ -5,10 +5,12 @@ scalings.  `layer.QKVLora` uses it when `supported` holds and keeps its GEMM pat
 
     lora_fwd(y16, a_q, a_v, b_q, b_v, scaling)      -> t [M, 32], lq [M, NQ], lv [M, NV] fp16
     lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s)   -> gs_q, gs_v, dt [M, 32], dy [M, H] fp16
+    lora_bwd_params(y16, t, dt, gs_q, gs_v)          -> dA_q, dA_v [16, H], dB_q, dB_v fp32
 
 with t = fp16(y A^T), lq = fp16(fp16(t_q B_q^T) * s), gs = fp16(g * s),
-dt = fp16(gs_q B_q | gs_v B_v), dy = fp16(dt A): the rounding steps of the fp16 GEMMs they
-replace (fp32 sums in another order)."""
+dt = fp16(gs_q B_q | gs_v B_v), dy = fp16(dt A), dA = fp32(fp16(dt^T y)),
+dB_x = fp32(fp16(gs_x^T t_x)): the rounding steps of the fp16 GEMMs they replace (fp32 sums in
+another order)."""
 
 import torch
 
@@ -73,3 +75,28 @@ def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling):
               _ext.ptr(gs_q), _ext.ptr(gs_v), _ext.ptr(dt), _ext.ptr(dy), M, H, NQ, NV, RANK,
               _ext.stream_of(dy))
     return gs_q, gs_v, dt, dy
+
+
+SLICE_ROWS = 128   # rows per partial sum of soupk_lora_bwd_params
+
+
+def lora_bwd_params(y16, t, dt, gs_q, gs_v):
+    M, H = y16.shape
+    NQ, NV = gs_q.shape[1], gs_v.shape[1]
+    dev = y16.device
+    for x, name, cols in ((y16, "y16", H), (t, "t", 2 * RANK), (dt, "dt", 2 * RANK),
+                          (gs_q, "gs_q", NQ), (gs_v, "gs_v", NV)):
+        _ext.require(x, name, dtype=torch.float16, ndim=2, device=dev)
+        if tuple(x.shape) != (M, cols):
+            raise ValueError(f"{name} has shape {tuple(x.shape)}, expected {(M, cols)}")
+    slices = (M + SLICE_ROWS - 1) // SLICE_ROWS
+    n_ws = slices * (2 * RANK * H + RANK * (NQ + NV))
+    ws = torch.empty(max(n_ws, 4), dtype=torch.float32, device=dev)
+    d_aq = torch.empty((RANK, H), dtype=torch.float32, device=dev)
+    d_av = torch.empty((RANK, H), dtype=torch.float32, device=dev)
+    d_bq = torch.empty((NQ, RANK), dtype=torch.float32, device=dev)
+    d_bv = torch.empty((NV, RANK), dtype=torch.float32, device=dev)
+    _ext.call("soupk_lora_bwd_params", _ext.ptr(y16), _ext.ptr(t), _ext.ptr(dt), _ext.ptr(gs_q),
+              _ext.ptr(gs_v), _ext.ptr(ws), ws.numel(), _ext.ptr(d_aq), _ext.ptr(d_av),
+              _ext.ptr(d_bq), _ext.ptr(d_bv), M, H, NQ, NV, RANK, _ext.stream_of(y16))
+    return d_aq, d_av, d_bq, d_bv
