@@ -236,6 +236,30 @@ int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* 
                           float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
                           void* stream);
 
+/*
+ * y = x W^T (+ bias), fp16, on MFMA with 128 x 128 tiles (the GEMM core of soupk_gemm_tn_nf4;
+ * widening: the reference's torch.matmul).  x [M, K] (row stride ldx, a multiple of 8), W
+ * [N, K] row-major, bias nullable fp16 [N], y [M, N]; N a multiple of 128, K of 64.
+ */
+int soupk_gemm_tn(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
+                  uint16_t* y, int64_t M, int32_t N, int32_t K, void* stream);
+
+/*
+ * The fused NF4-dequant GEMM (the reference's stated next step, README.md:190-192, in place of
+ * nf4_unpack + torch.matmul in FrozenNF4Linear, solution/nf4.py:108-127): y = x W^T (+ bias)
+ * with W the row stack of n_parts (1..4) NF4 weights, part i given by host arrays of device
+ * pointers packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i], nf4[i] (the
+ * soupk_nf4_unpack operands) and part_rows[i] (a multiple of 128; the sum is N).  qblock must
+ * be 64 and qblock2 256.  The dequantised values are soupk_nf4_unpack's bit for bit.
+ */
+int soupk_gemm_tn_nf4(const uint16_t* x, int64_t ldx, int32_t n_parts,
+                      const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+                      const float* const* code2, const float* const* absmax2,
+                      const float* const* offset, const float* const* nf4,
+                      const int32_t* part_rows, int32_t qblock, int32_t qblock2,
+                      const uint16_t* bias, uint16_t* y, int64_t M, int32_t N, int32_t K,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

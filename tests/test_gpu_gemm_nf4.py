@@ -1,0 +1,90 @@
+"""GPU: the MFMA GEMM of testt_amd/csrc/gemm_nf4.hip.  The fp16 path against float64 sums of the
+same fp16 products (one fp16 rounding of an fp32 accumulation: within 1 ulp plus
+32 * 2^-24 * sum|terms|); the NF4 path bit-exact against unpack (the oracle-pinned unpack
+kernel) followed by the fp16 path, and against float64 on the oracle's dequantised weights."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.nf4 import dequant_state
+from testt_amd import nf4, nf4_gemm, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def within(got, exact, terms):
+    h = exact.to(torch.float16)
+    inf = torch.tensor(float("inf"), dtype=torch.float16, device=h.device)
+    ulp = (torch.nextafter(h.abs(), inf) - h.abs()).double()
+    err = (got.double() - exact).abs()
+    bad = err > ulp + 32 * 2.0 ** -24 * terms
+    assert not bool(bad.any()), f"{int(bad.sum())} of {bad.numel()} beyond, max err {float(err.max()):.3g}"
+
+
+@pytest.mark.parametrize("M,N,K,with_bias", [(2048, 2048, 1536, True), (300, 256, 128, False),
+                                             (1, 128, 64, True), (131, 384, 1536, False)])
+def test_gemm_tn_fp16(M, N, K, with_bias):
+    print(f"gemm_tn M={M} N={N} K={K} bias={with_bias}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.float16).to(DEV)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.float16).to(DEV)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.float16).to(DEV) if with_bias else None
+    y = nf4_gemm.gemm_tn(x, w, b)
+    exact = x.double() @ w.double().t()
+    terms = x.double().abs() @ w.double().abs().t()
+    if b is not None:
+        exact = exact + b.double()
+        terms = terms + b.double().abs()
+    within(y, exact, terms)
+
+
+@pytest.mark.parametrize("rows,K,M", [((256,), 1536, 2048), ((256, 128, 128), 512, 77),
+                                      ((128, 128), 64, 5)])
+def test_gemm_tn_nf4(rows, K, M):
+    print(f"gemm_tn_nf4 parts={rows} K={K} M={M}", flush=True)
+    ws = [workloads.nf4_weight(r, K, seed=50 + i, device=DEV, absmax2_range=(0.005, 0.02),
+                               offset=0.01) for i, r in enumerate(rows)]
+    assert nf4_gemm.supported(torch.empty(M, K, dtype=torch.float16, device=DEV), ws)
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(torch.float16).to(DEV)
+    b = (0.1 * torch.randn(sum(rows), generator=g)).to(torch.float16).to(DEV)
+    y = nf4_gemm.nf4_linear(x, ws, b)
+    w16 = nf4.unpack_concat(ws, DEV)
+    assert torch.equal(y, nf4_gemm.gemm_tn(x, w16, b))        # same values, same sums
+    wd = torch.from_numpy(np.concatenate([dequant_state(w) for w in ws]).astype(np.float64)).to(DEV)
+    within(y, x.double() @ wd.t() + b.double(), x.double().abs() @ wd.abs().t() + b.double().abs())
+
+
+def test_rejects_shapes():
+    x = torch.randn(8, 64, device=DEV).to(torch.float16)
+    with pytest.raises(Exception):
+        nf4_gemm.gemm_tn(x, torch.randn(100, 64, device=DEV).to(torch.float16))   # N % 128
+    with pytest.raises(Exception):
+        nf4_gemm.gemm_tn(torch.randn(8, 96, device=DEV).to(torch.float16),
+                         torch.randn(128, 96, device=DEV).to(torch.float16))       # K % 64
+    w = workloads.nf4_weight(192, 64, seed=3, device=DEV)                           # 192 rows
+    assert not nf4_gemm.supported(x, [w])
+
+
+def test_frozen_linear_fused_switch(monkeypatch):
+    """FrozenNF4Linear with the fused NF4 GEMM forward against its unpack + hipBLASLt forward:
+    the same fp16 weights, sums in another order (relative L2 < 1e-3); the backward is the same
+    path either way."""
+    ws = [workloads.nf4_weight(r, 512, seed=70 + i, device=DEV, absmax2_range=(0.005, 0.02),
+                               offset=0.01) for i, r in enumerate((256, 128))]
+    g = torch.Generator().manual_seed(6)
+    x0 = torch.randn(200, 512, generator=g).to(torch.float16).to(DEV)
+    b = (0.1 * torch.randn(384, generator=g)).to(torch.float16).to(DEV)
+    gout = (1e-2 * torch.randn(200, 384, generator=g)).to(torch.float16).to(DEV)
+    res = []
+    for fused in (False, True):
+        monkeypatch.setattr(nf4, "USE_FUSED_NF4_GEMM", fused)
+        x = x0.clone().requires_grad_(True)
+        out = nf4.frozen_linear(x, ws, b)
+        out.backward(gout)
+        res.append((out.detach(), x.grad))
+    rel = float((res[1][0].double() - res[0][0].double()).norm() / res[0][0].double().norm())
+    assert rel < 1e-3, rel
+    assert torch.equal(res[0][1], res[1][1])

@@ -47,6 +47,9 @@ SIGNATURES = {
                             _i32, _i32, _i32, _p],
     "soupk_lora_bwd_params": [_p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i32, _i32,
                               _i32, _i32, _p],
+    "soupk_gemm_tn": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _p],
+    "soupk_gemm_tn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _i64,
+                          _i32, _i32, _p],
 }
 
 

@@ -1,0 +1,259 @@
+// y = x W^T (+ bias) with the frozen weight W read in NF4 (bitsandbytes double quant) and
+// dequantised inside the GEMM, on gfx950 MFMA (v_mfma_f32_32x32x16_f16): the fused NF4-dequant
+// GEMM the reference names as its next step (README.md:190-192, SUBMISSION.md:54-58), in place
+// of unpacking W to fp16 in HBM (testt_amd/csrc/nf4_unpack.hip) and a hipBLASLt GEMM
+// (solution/nf4.py:108-127).  The same kernel also takes an fp16 W (the plain GEMM), which is
+// how its GEMM core is checked against hipBLASLt.
+//
+// Tiling: a workgroup computes a 128 x 128 tile of y (128 rows of x, 128 rows of W) with 4
+// wavefronts of 64 x 64 (2 x 2 MFMA tiles of 32 x 32, 16 fp32 accumulators each).  K advances
+// in tiles of 64: x and W tiles are staged in LDS ([128][72] halves each, double-buffered; the
+// 72-half row stride makes the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct
+// 4-bank groups), the next tile's global loads are issued before the current tile's MFMAs, and
+// one barrier per K tile separates the LDS writes from the reads.
+//
+// NF4 weights: a 64-wide K tile of one W row is exactly one 64-value quantisation block, so a
+// thread dequantises 32 codes of one row with one block scale:
+//   scale = fp32(fp32(code2[absmax_u8[b]] * absmax2[b / 256]) + offset)
+//   w     = fp16(nf4[code] * scale)          (the unpack kernel's arithmetic, bit for bit)
+// code2 and nf4 staged in LDS.  W may be up to 4 row parts with their own quantisation states
+// (q | k | v, gate | up), each a multiple of 128 rows.
+//
+// MFMA 32x32x16 layouts (checked on the device): A[32 x 16]: lane l holds row l%32,
+// k = 8(l/32)..+7; B[16 x 32]: lane l holds column l%32, same k; C: element i of lane l is row
+// 8(i/4) + 4(l/32) + i%4, column l%32.
+
+#include "soupk_common.hpp"
+
+namespace soupk {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kGThreads = 256;
+constexpr int kLds = kBK + 8;          // LDS row stride (halves)
+constexpr int kMaxParts = 4;
+
+struct Nf4Part {
+  const uint8_t* packed;     // [rows * K / 2] bytes, high nibble = even element
+  const uint8_t* absmax_u8;  // [rows * K / 64]
+  const float* code2;        // [256]
+  const float* absmax2;      // [ceil(rows * K / 64 / 256)]
+  const float* offset;       // [1]
+  const float* nf4;          // [16]
+  int rows;
+};
+
+struct Nf4Weights {
+  Nf4Part part[kMaxParts];
+  int n_parts;
+};
+
+__device__ __forceinline__ f16v mfma32x32(h8 a, h8 b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
+
+// Registers of one K tile for one thread: 4 x 16 bytes of x (rows tid/8 + 32j, chunk tid%8);
+// for W either 4 x 16 bytes of fp16 (same mapping) or 16 bytes of NF4 codes (row tid/2, codes
+// 32(tid%2) .. +31) and that row's block scale inputs.
+struct TileRegs {
+  u32x4 x[4];
+  u32x4 w[4];
+  uint32_t ablk;   // NF4: absmax_u8 of the block
+  float a2;        // NF4: absmax2 of the block's group
+};
+
+template <bool NF4>
+__global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* w16, Nf4Weights nw,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K) {
+  __shared__ __align__(16) _Float16 Xs[2][kBM * kLds];
+  __shared__ __align__(16) _Float16 Ws[2][kBN * kLds];
+  __shared__ float code2_s[256];
+  __shared__ float nf4_s[16];
+  const int tid = threadIdx.x;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+  const int lane = tid % kWave, wv = tid / kWave;
+  const int wm = wv >> 1, wn = wv & 1;
+
+  // the weight part holding rows n0 .. n0 + 127, and the row of that part
+  int part = 0, prow0 = n0;
+  if constexpr (NF4) {
+    while (part + 1 < nw.n_parts && prow0 >= nw.part[part].rows) {
+      prow0 -= nw.part[part].rows;
+      ++part;
+    }
+  }
+  const Nf4Part P = nw.part[part];
+  float offset = 0.f;
+  if constexpr (NF4) {
+    code2_s[tid] = P.code2[tid];
+    if (tid < 16) nf4_s[tid] = P.nf4[tid];
+    offset = P.offset[0];
+  }
+
+  const int KT = K / kBK;
+  auto load = [&](TileRegs& r, int kt) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = tid / 8 + 32 * j, ch = tid % 8;
+      const int64_t xr = min(m0 + row, M - 1);
+      r.x[j] = *reinterpret_cast<const u32x4*>(x + xr * ldx + k0 + 8 * ch);
+      if constexpr (!NF4)
+        r.w[j] = *reinterpret_cast<const u32x4*>(w16 + static_cast<int64_t>(n0 + row) * K + k0 +
+                                                 8 * ch);
+    }
+    if constexpr (NF4) {
+      const int row = tid / 2, half = tid % 2;
+      const int64_t e0 = static_cast<int64_t>(prow0 + row) * K + k0;   // first element
+      r.w[0] = *reinterpret_cast<const u32x4*>(P.packed + e0 / 2 + 16 * half);
+      const int64_t blk = e0 / 64;
+      r.ablk = P.absmax_u8[blk];
+      r.a2 = P.absmax2[blk / 256];
+    }
+  };
+  auto store = [&](const TileRegs& r, int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = tid / 8 + 32 * j, ch = tid % 8;
+      *reinterpret_cast<u32x4*>(&Xs[buf][row * kLds + 8 * ch]) = r.x[j];
+      if constexpr (!NF4) *reinterpret_cast<u32x4*>(&Ws[buf][row * kLds + 8 * ch]) = r.w[j];
+    }
+    if constexpr (NF4) {
+      const int row = tid / 2, half = tid % 2;
+      const float scale = code2_s[r.ablk] * r.a2 + offset;   // two roundings (no FMA)
+      const uint32_t words[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+      uint32_t out[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t byte = (words[q] >> (8 * b)) & 0xffu;
+          out[q * 4 + b] = pack_h2(nf4_s[byte >> 4] * scale, nf4_s[byte & 15u] * scale);
+        }
+      }
+      _Float16* dst = &Ws[buf][row * kLds + 32 * half];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<u32x4*>(dst + 8 * q) =
+            u32x4{out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]};
+    }
+  };
+
+  f16v acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  TileRegs regs;
+  load(regs, 0);
+  if constexpr (NF4) __syncthreads();   // code2_s / nf4_s written before the first store
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    store(regs, buf);
+    __syncthreads();
+    if (kt + 1 < KT) load(regs, kt + 1);
+    issue_here();
+    const _Float16* xa = &Xs[buf][(64 * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
+    const _Float16* wb = &Ws[buf][(64 * wn + (lane % 32)) * kLds + 8 * (lane / 32)];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      h8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = *reinterpret_cast<const h8*>(xa + 32 * i * kLds + 16 * ks);
+        b[i] = *reinterpret_cast<const h8*>(wb + 32 * i * kLds + 16 * ks);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32(a[i], b[j], acc[i][j]);
+    }
+  }
+
+  // epilogue: element e of acc[i][j] is row 64wm + 32i + 8(e/4) + 4(lane/32) + e%4,
+  // column 64wn + 32j + lane%32
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + 64 * wn + 32 * j + lane % 32;
+    const float bv = bias != nullptr ? h2f(bias[n]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+        if (m < M)
+          y[static_cast<int64_t>(m) * N + n] =
+              __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[i][j][e] + bv));
+      }
+    }
+  }
+}
+
+int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
+  if (M < 0 || N <= 0 || K <= 0 || N % kBN || K % kBK || ldx < K || ldx % 8) return kInvalid;
+  if ((M + kBM - 1) / kBM > 65535 || N / kBN > 0x7fffffff) return kInvalid;
+  if (M * static_cast<int64_t>(N) >= (int64_t{1} << 40)) return kInvalid;
+  return kOk;
+}
+
+bool bad_ptr(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15); }
+
+}  // namespace
+}  // namespace soupk
+
+using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
+    const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
+    int64_t M, int32_t N, int32_t K, void* stream) {
+  const int rc = check_gemm(M, N, K, ldx);
+  if (rc != kOk) return rc;
+  if (M == 0) return kOk;
+  if (bad_ptr(x) || bad_ptr(w) || bad_ptr(y)) return kInvalid;
+  Nf4Weights none{};
+  const dim3 grid(static_cast<unsigned>(N / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  return launch_kernel(gemm_tn_kernel<false>, grid, dim3(kGThreads),
+                       static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
+                       static_cast<int>(M), N, K);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
+    const uint16_t* x, int64_t ldx, int32_t n_parts, const uint8_t* const* packed,
+    const uint8_t* const* absmax_u8, const float* const* code2, const float* const* absmax2,
+    const float* const* offset, const float* const* nf4, const int32_t* part_rows,
+    int32_t qblock, int32_t qblock2, const uint16_t* bias, uint16_t* y, int64_t M, int32_t N,
+    int32_t K, void* stream) {
+  const int rc = check_gemm(M, N, K, ldx);
+  if (rc != kOk) return rc;
+  if (qblock != kBK || qblock2 != 256) return kInvalid;
+  if (n_parts < 1 || n_parts > kMaxParts || !packed || !absmax_u8 || !code2 || !absmax2 ||
+      !offset || !nf4 || !part_rows)
+    return kInvalid;
+  Nf4Weights nw{};
+  int64_t rows = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    if (part_rows[i] <= 0 || part_rows[i] % kBN || bad_ptr(packed[i]) || !absmax_u8[i] ||
+        !code2[i] || !absmax2[i] || !offset[i] || !nf4[i])
+      return kInvalid;
+    nw.part[i] = Nf4Part{packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i], nf4[i],
+                         part_rows[i]};
+    rows += part_rows[i];
+  }
+  nw.n_parts = n_parts;
+  if (rows != N) return kInvalid;
+  if (M == 0) return kOk;
+  if (bad_ptr(x) || bad_ptr(y)) return kInvalid;
+  const dim3 grid(static_cast<unsigned>(N / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  return launch_kernel(gemm_tn_kernel<true>, grid, dim3(kGThreads),
+                       static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
+                       static_cast<int>(M), N, K);
+}

@@ -31,6 +31,12 @@ BYTES_PER_PROGRAM = 16384
 # deterministic).  False restores the reference's memory profile.
 KEEP_UNPACKED_FOR_BACKWARD = True
 
+# FrozenNF4Linear's forward through the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py: W read
+# as NF4, dequantised in the GEMM's tile loads, no fp16 W in HBM) when the shapes allow it; its
+# backward then unpacks W.  Off by default: on MI355X that GEMM core is still slower than
+# hipBLASLt's tuned kernels (26 against 21 us on the 2048 x 2048 x 1536 q|k|v shape).
+USE_FUSED_NF4_GEMM = False
+
 
 def keep_for_backward(ctx, weight):
     """Hold the forward's unpacked fp16 `weight` in ctx when a backward may read it (an input
@@ -172,9 +178,17 @@ class FrozenNF4Linear(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, bias, weights):
+        ctx.weights = weights
+        if USE_FUSED_NF4_GEMM:
+            from . import nf4_gemm
+
+            x2 = x.reshape(-1, x.shape[-1])
+            if nf4_gemm.supported(x2, weights, bias):
+                ctx.unpacked = None
+                out = nf4_gemm.nf4_linear(x2, weights, bias)
+                return out.view(*x.shape[:-1], out.shape[-1])
         weight = unpack_concat(weights, x.device)
         out = torch.nn.functional.linear(x, weight, bias)
-        ctx.weights = weights
         keep_for_backward(ctx, weight)
         return out
 

@@ -1,0 +1,73 @@
+"""y = x W^T (+ bias) with the frozen NF4 weight dequantised inside the GEMM
+(testt_amd/csrc/gemm_nf4.hip), the fused NF4-dequant GEMM the reference names as its next step
+(README.md:190-192), in place of unpack_concat + torch.matmul (solution/nf4.py:108-127).
+
+    nf4_linear(x, weights, bias=None)   x fp16 [M, K]; weights: 1-4 Params4bit-like parts
+                                        stacked by rows (q|k|v, gate|up), each a multiple of
+                                        128 rows, blocksize 64, nested 256; -> fp16 [M, N]
+    gemm_tn(x, w16, bias=None)          the same GEMM on an fp16 W [N, K]
+
+The weight values are the unpack kernel's bit for bit (same arithmetic), so nf4_linear equals
+gemm_tn(x, unpack_concat(weights)) exactly."""
+
+import ctypes
+
+import torch
+
+from . import _ext
+from . import nf4 as _nf4
+
+MAX_PARTS = 4
+
+
+def supported(x, weights, bias=None):
+    if not (x.is_cuda and x.dtype == torch.float16 and x.dim() == 2):
+        return False
+    if not 1 <= len(weights) <= MAX_PARTS:
+        return False
+    K = x.shape[1]
+    for w in weights:
+        if not _nf4.supports_fast_unpack(w):
+            return False
+        st = w.quant_state
+        rows, cols = _nf4.weight_shape(w)
+        if cols != K or rows % 128 or st.blocksize != 64 or st.state2.blocksize != 256:
+            return False
+        if _nf4._plan(w, x.device) is None:
+            return False
+    if bias is not None and (bias.dtype != torch.float16 or not bias.is_cuda):
+        return False
+    return K % 64 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+
+
+def gemm_tn(x, w16, bias=None):
+    _ext.require(w16, "w16", dtype=torch.float16, ndim=2, device=x.device)
+    M, K = x.shape
+    N = w16.shape[0]
+    y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if bias is not None:
+        _ext.require(bias, "bias", dtype=torch.float16, ndim=1, device=x.device)
+    _ext.call("soupk_gemm_tn", x.data_ptr(), x.stride(0), w16.data_ptr(), _ext.ptr(bias),
+              y.data_ptr(), M, N, K, _ext.stream_of(x))
+    return y
+
+
+def nf4_linear(x, weights, bias=None):
+    """x @ W^T (+ bias) for W the row stack of `weights`, dequantised in the GEMM."""
+    M, K = x.shape
+    plans = [_nf4._plan(w, x.device) for w in weights]
+    rows = [_nf4.weight_shape(w)[0] for w in weights]
+    N = sum(rows)
+    if bias is not None:
+        _ext.require(bias, "bias", dtype=torch.float16, ndim=1, device=x.device)
+        if bias.numel() != N:
+            raise ValueError(f"bias has {bias.numel()} entries, the weights {N} rows")
+    n = len(weights)
+    arrays = [(ctypes.c_void_p * n)(*[p[0][i] for p in plans]) for i in range(6)]
+    part_rows = (ctypes.c_int32 * n)(*rows)
+    y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _ext.call("soupk_gemm_tn_nf4", x.data_ptr(), x.stride(0), n,
+              *[ctypes.addressof(a) for a in arrays], ctypes.addressof(part_rows),
+              plans[0][2], plans[0][3], _ext.ptr(bias), y.data_ptr(), M, N, K,
+              _ext.stream_of(x))
+    return y
