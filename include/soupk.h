@@ -67,6 +67,23 @@ int soupk_nf4_unpack(const uint8_t* packed, const uint8_t* absmax_u8, const floa
                      void* stream);
 
 /*
+ * soupk_nf4_unpack over up to 8 weights in one launch (the reference launches its unpack
+ * kernel once per weight, solution/nf4.py:72-89 called per projection from
+ * solution/nf4.py:125 and solution/mlp.py:105-108; here the projections of one decoder
+ * layer, or the q|k|v and gate|up stacks, share a launch).  Part i is the soupk_nf4_unpack
+ * call (packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i], nf4[i], out_f16[i],
+ * n_bytes[i]) with the common qblock, qblock2; results are bit-identical to those calls.
+ * Parts of zero bytes are skipped; a part the tiled kernel does not take (n_bytes % 4,
+ * alignment, qblock not a power of two) gets its own soupk_nf4_unpack launches.
+ */
+int soupk_nf4_unpack_multi(int32_t n_parts, const uint8_t* const* packed,
+                           const uint8_t* const* absmax_u8, const float* const* code2,
+                           const float* const* absmax2, const float* const* offset,
+                           const float* const* nf4, uint16_t* const* out_f16,
+                           const int64_t* n_bytes, int32_t qblock, int32_t qblock2,
+                           void* stream);
+
+/*
  * Inverse of a scatter index (no counterpart kernel in the reference: it lets the pad-layout
  * writers of rmsnorm_fwd and rope_pack_fwd zero the unused rows in the same launch instead of
  * a separate torch.zeros, solution/rmsnorm.py:82, solution/rope.py:141-143).

@@ -52,6 +52,9 @@ def test_version_and_status_strings(lib):
     ("soupk_swiglu_fwd", (None, None, -1, 8, None)),
     ("soupk_swiglu_bwd_inplace", (None, None, 4, 8, None)),
     ("soupk_nf4_unpack", (None,) * 7 + (64, 63, 256, None)),
+    ("soupk_nf4_unpack_multi", (9,) + (None,) * 8 + (64, 256, None)),      # more than 8 parts
+    ("soupk_nf4_unpack_multi", (1,) + (None,) * 8 + (63, 256, None)),
+    ("soupk_nf4_unpack_multi", (2,) + (None,) * 8 + (64, 256, None)),      # null arrays
     ("soupk_rmsnorm_fwd", (None,) * 9 + (4, 0, 0, 1e-6, None)),
     ("soupk_rmsnorm_bwd", (None,) * 9 + (-1, 0, 16, None)),
     ("soupk_rope_pack_fwd", (None,) * 3 + (7,) + (None,) * 7 + (1, 1, 1, 1, 1, 8, None)),
@@ -70,6 +73,7 @@ def test_invalid_arguments_rejected_before_launch(lib, name, args):
 @pytest.mark.parametrize("name,args", [
     ("soupk_swiglu_fwd", (None, None, 0, 8960, None)),
     ("soupk_nf4_unpack", (None,) * 7 + (0, 64, 256, None)),
+    ("soupk_nf4_unpack_multi", (0,) + (None,) * 8 + (64, 256, None)),
     ("soupk_head_stats_grad", (None,) * 6 + (1.0, 0, 151936, None)),
     ("soupk_index_inverse", (None, 0, None, 0, None)),
 ])

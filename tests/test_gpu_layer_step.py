@@ -12,7 +12,7 @@ import torch
 
 from oracle.nf4 import dequant_state
 from oracle.rope import apply_rotary
-from testt_amd import layer, workloads
+from testt_amd import layer, nf4, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -115,3 +115,39 @@ def test_decoder_layer_matches_fp32_eager(lengths, dropout):
     for name, a, b in zip(("d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"), fused, ref):
         assert a is not None and b is not None, name
         assert rel_err(a, b) < 2e-2, (name, rel_err(a, b))
+
+
+@pytest.mark.parametrize("keep", [True, False])
+def test_unpack_per_layer_is_bit_identical(monkeypatch, keep):
+    """All seven projections unpacked by one launch before the layer (UNPACK_PER_LAYER) or each
+    stack where it is used: the same fp16 weights, so the same outputs and gradients, bit for
+    bit, with the weights kept for backward or unpacked again there."""
+    batch, seq, lengths = 2, 64, (64, 37)
+    w = layer.synthetic_layer(DEV, seed=11)
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(5)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    monkeypatch.setattr(nf4, "KEEP_UNPACKED_FOR_BACKWARD", keep)
+    runs = []
+    for per_layer in (True, False):
+        monkeypatch.setattr(layer, "UNPACK_PER_LAYER", per_layer)
+        s_in = s0.clone().requires_grad_(True)
+        d_in = d0.clone().requires_grad_(True)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                                   layer.key_valid_of(amask))
+        torch.autograd.backward([s, d], [gs, gd])
+        runs.append([s.detach(), d.detach(), s_in.grad, d_in.grad] +
+                    [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+    for name, a, b in zip(("s", "d", "d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"),
+                          *runs):
+        assert torch.equal(a, b), name

@@ -109,3 +109,84 @@ def test_rejects_invalid_arguments():
     w = workloads.nf4_weight(16, 64, seed=5, device=DEV)
     with pytest.raises(ValueError):
         nf4.unpack_into(w, torch.empty((16, 64), dtype=torch.float16))   # CPU output
+
+
+def _raw_part(n_bytes, seed):
+    """A packed NF4 stream of n_bytes with random codes and scales (host tensors)."""
+    g = torch.Generator().manual_seed(seed)
+    packed = torch.randint(0, 256, (n_bytes,), generator=g, dtype=torch.int32).to(torch.uint8)
+    n_blocks = -(-n_bytes // 32)
+    absmax_u8 = torch.randint(0, 256, (max(n_blocks, 1),), generator=g,
+                              dtype=torch.int32).to(torch.uint8)
+    absmax2 = 0.01 + 0.09 * torch.rand(max(-(-n_blocks // 256), 1), generator=g)
+    offset = torch.tensor([0.01 * (seed % 7)], dtype=torch.float32)
+    return packed, absmax_u8, absmax2, offset
+
+
+def test_unpack_multi_through_abi():
+    """soupk_nf4_unpack_multi against the oracle, part by part: whole tiles, a part ending
+    mid-tile, a byte tail (n_bytes % 4), an output off the 16-byte grid (both on the per-part
+    fallback) and an empty part, in one call."""
+    import ctypes
+
+    specs = [(16384 * 3, 0), (5000 * 4, 0), (16 * 100 + 3, 0), (4096, 1), (0, 0), (64, 0)]
+    code2 = workloads.dynamic_code_signed().to(DEV)
+    nf4_t = torch.tensor(workloads.NF4_LEVELS, dtype=torch.float32, device=DEV)
+    parts, outs, refs = [], [], []
+    for i, (n_bytes, shift) in enumerate(specs):
+        packed, absmax_u8, absmax2, offset = _raw_part(n_bytes, 70 + i)
+        dev = [x.to(DEV) for x in (packed, absmax_u8, absmax2, offset)]
+        buf = torch.full((2 * n_bytes + shift + 8,), float("nan"), dtype=torch.float16,
+                         device=DEV)
+        parts.append(dev)
+        outs.append((buf, buf[shift:shift + 2 * n_bytes]))
+        refs.append(dequant_nf4(packed.numpy(), absmax_u8.numpy(), code2.cpu().numpy(),
+                                absmax2.numpy(), offset.numpy(), nf4_t.cpu().numpy())
+                    if n_bytes else np.zeros(0, np.float16))
+    n = len(specs)
+
+    def arr(values):
+        return (ctypes.c_void_p * n)(*values)
+
+    keep = [arr([p[0].data_ptr() for p in parts]), arr([p[1].data_ptr() for p in parts]),
+            arr([code2.data_ptr()] * n), arr([p[2].data_ptr() for p in parts]),
+            arr([p[3].data_ptr() for p in parts]), arr([nf4_t.data_ptr()] * n),
+            arr([o.data_ptr() for _, o in outs])]
+    sizes = (ctypes.c_int64 * n)(*[s for s, _ in specs])
+    _ext.call("soupk_nf4_unpack_multi", n, *[ctypes.addressof(a) for a in keep],
+              ctypes.addressof(sizes), 64, 256, _ext.stream_of(code2))
+    for (n_bytes, shift), (buf, out), ref in zip(specs, outs, refs):
+        assert np.array_equal(bits(out), ref.view(np.int16)), n_bytes
+        rest = torch.cat([buf[:shift], buf[shift + 2 * n_bytes:]])
+        assert bool(torch.isnan(rest).all()), "wrote outside its part"
+
+
+def test_unpack_groups_one_buffer():
+    """unpack_groups: the row stacks of a layer (here 11 weights in 4 groups, more than one
+    launch's 8 parts) bit-identical to the oracle, stacked and aligned as unpack_concat's."""
+    groups = (((96, 640), (32, 640), (32, 640)), ((640, 64),), ((128, 640), (128, 640)),
+              ((640, 128),), ((64, 640), (64, 640), (64, 640), (64, 640)))
+    weights = [tuple(workloads.nf4_weight(*shape, seed=80 + 10 * gi + wi, device=DEV)
+                     for wi, shape in enumerate(group)) for gi, group in enumerate(groups)]
+    stacks = nf4.unpack_groups(weights, DEV)
+    base = stacks[0].data_ptr()
+    for group, stack in zip(weights, stacks):
+        assert stack.is_contiguous() and (stack.data_ptr() - base) % 512 == 0
+        ref = np.concatenate([dequant_state(w) for w in group])
+        assert np.array_equal(bits(stack), ref.view(np.int16))
+        assert torch.equal(stack, nf4.unpack_concat(group, DEV))
+
+
+def test_unpack_multi_rejects_invalid_arguments():
+    import ctypes
+
+    one = (ctypes.c_void_p * 9)()
+    sizes = (ctypes.c_int64 * 9)()
+    for n_parts, qblock in ((9, 64), (-1, 64), (1, 63)):
+        with pytest.raises(_ext.SoupkError):
+            _ext.call("soupk_nf4_unpack_multi", n_parts, *[ctypes.addressof(one)] * 7,
+                      ctypes.addressof(sizes), qblock, 256, None)
+    sizes[0] = 64                      # a non-empty part with null pointers
+    with pytest.raises(_ext.SoupkError):
+        _ext.call("soupk_nf4_unpack_multi", 1, *[ctypes.addressof(one)] * 7,
+                  ctypes.addressof(sizes), 64, 256, None)

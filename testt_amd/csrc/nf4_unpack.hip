@@ -54,14 +54,13 @@ __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
 #endif
 constexpr bool kNf4NtLd = SOUPK_NF4_NT_LD != 0, kNf4NtSt = SOUPK_NF4_NT_ST != 0;
 
-__global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
+// One tile (256 threads x kNf4Dwords dwords, from dword d0) of one weight.
+__device__ __forceinline__ void nf4_unpack_tile(
     const uint32_t* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
     const float* __restrict__ code2, const float* __restrict__ absmax2,
     const float* __restrict__ offset, const float* __restrict__ nf4, u32x4* __restrict__ out,
-    int64_t n_dwords, int64_t n_blocks, int dword_block_shift, int block2_shift) {
-  __shared__ float2 pair[256];
-  __shared__ float scale[kNf4TileDwords];  // enough for qblock >= 8 (1 block per dword)
-  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kNf4TileDwords;
+    int64_t d0, int64_t n_dwords, int64_t n_blocks, int dword_block_shift, int block2_shift,
+    float2* pair, float* scale) {
   uint32_t w[kNf4Dwords];
 #pragma unroll
   for (int k = 0; k < kNf4Dwords; ++k) {
@@ -87,6 +86,51 @@ __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
     const u32x4 v = nf4_expand_dword(w[k], s, pair);
     if (d < n_dwords) st<kNf4NtSt>(out + d, v);
   }
+}
+
+__global__ __launch_bounds__(kNf4Threads) void nf4_unpack_vec_kernel(
+    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ absmax_u8,
+    const float* __restrict__ code2, const float* __restrict__ absmax2,
+    const float* __restrict__ offset, const float* __restrict__ nf4, u32x4* __restrict__ out,
+    int64_t n_dwords, int64_t n_blocks, int dword_block_shift, int block2_shift) {
+  __shared__ float2 pair[256];
+  __shared__ float scale[kNf4TileDwords];  // enough for qblock >= 8 (1 block per dword)
+  nf4_unpack_tile(packed, absmax_u8, code2, absmax2, offset, nf4, out,
+                  static_cast<int64_t>(blockIdx.x) * kNf4TileDwords, n_dwords, n_blocks,
+                  dword_block_shift, block2_shift, pair, scale);
+}
+
+// Several weights in one launch (the projections of a decoder layer): workgroup x unpacks tile
+// x - first_tile[p] of part p, first_tile[p] <= x < first_tile[p + 1].  The part table is a
+// kernel argument (read through the scalar unit); every part takes the vector path.
+constexpr int kNf4MaxParts = 8;
+struct Nf4Parts {
+  const uint32_t* packed[kNf4MaxParts];
+  const uint8_t* absmax_u8[kNf4MaxParts];
+  const float* code2[kNf4MaxParts];
+  const float* absmax2[kNf4MaxParts];
+  const float* offset[kNf4MaxParts];
+  const float* nf4[kNf4MaxParts];
+  u32x4* out[kNf4MaxParts];
+  int64_t n_dwords[kNf4MaxParts];
+  int64_t n_blocks[kNf4MaxParts];
+  int first_tile[kNf4MaxParts + 1];
+  int n_parts;
+};
+
+__global__ __launch_bounds__(kNf4Threads) void nf4_unpack_multi_kernel(Nf4Parts parts,
+                                                                       int dword_block_shift,
+                                                                       int block2_shift) {
+  __shared__ float2 pair[256];
+  __shared__ float scale[kNf4TileDwords];
+  const int x = static_cast<int>(blockIdx.x);
+  int p = 0;
+  while (p + 1 < parts.n_parts && x >= parts.first_tile[p + 1]) ++p;
+  nf4_unpack_tile(parts.packed[p], parts.absmax_u8[p], parts.code2[p], parts.absmax2[p],
+                  parts.offset[p], parts.nf4[p], parts.out[p],
+                  static_cast<int64_t>(x - parts.first_tile[p]) * kNf4TileDwords,
+                  parts.n_dwords[p], parts.n_blocks[p], dword_block_shift, block2_shift, pair,
+                  scale);
 }
 
 // One packed byte per thread; any even qblock, any qblock2, any alignment.  Also used for the
@@ -159,4 +203,56 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack(
                          static_cast<int64_t>(qblock2));
   }
   return kOk;
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi(
+    int32_t n_parts, const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+    const float* const* code2, const float* const* absmax2, const float* const* offset,
+    const float* const* nf4, uint16_t* const* out_f16, const int64_t* n_bytes, int32_t qblock,
+    int32_t qblock2, void* stream) {
+  if (n_parts < 0 || n_parts > kNf4MaxParts || qblock <= 0 || (qblock & 1) || qblock2 <= 0)
+    return kInvalid;
+  if (n_parts == 0) return kOk;
+  if (!packed || !absmax_u8 || !code2 || !absmax2 || !offset || !nf4 || !out_f16 || !n_bytes)
+    return kInvalid;
+  for (int i = 0; i < n_parts; ++i) {
+    if (n_bytes[i] < 0) return kInvalid;
+    if (n_bytes[i] > 0 && (!packed[i] || !absmax_u8[i] || !code2[i] || !absmax2[i] ||
+                           !offset[i] || !nf4[i] || !out_f16[i]))
+      return kInvalid;
+  }
+  const bool vec_layout = qblock >= 8 && qblock / 8 <= kNf4TileDwords && is_pow2(qblock) &&
+                          is_pow2(qblock2);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t bytes_per_block = qblock / 2;
+  Nf4Parts parts{};
+  int64_t tiles = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    if (n_bytes[i] == 0) continue;
+    const bool vec = vec_layout && n_bytes[i] % 4 == 0 && aligned(packed[i], 4) &&
+                     aligned(out_f16[i], 16);
+    if (!vec) {   // a layout the tiles do not take: its own launches, as soupk_nf4_unpack
+      const int st = soupk_nf4_unpack(packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i],
+                                      nf4[i], out_f16[i], n_bytes[i], qblock, qblock2, stream);
+      if (st != kOk) return st;
+      continue;
+    }
+    const int j = parts.n_parts++;
+    parts.packed[j] = reinterpret_cast<const uint32_t*>(packed[i]);
+    parts.absmax_u8[j] = absmax_u8[i];
+    parts.code2[j] = code2[i];
+    parts.absmax2[j] = absmax2[i];
+    parts.offset[j] = offset[i];
+    parts.nf4[j] = nf4[i];
+    parts.out[j] = reinterpret_cast<u32x4*>(out_f16[i]);
+    parts.n_dwords[j] = n_bytes[i] / 4;
+    parts.n_blocks[j] = (n_bytes[i] + bytes_per_block - 1) / bytes_per_block;
+    parts.first_tile[j] = static_cast<int>(tiles);
+    tiles += (parts.n_dwords[j] + kNf4TileDwords - 1) / kNf4TileDwords;
+    if (tiles > 0x7fffffff) return kInvalid;
+  }
+  if (parts.n_parts == 0) return kOk;
+  for (int j = parts.n_parts; j <= kNf4MaxParts; ++j) parts.first_tile[j] = static_cast<int>(tiles);
+  return launch_kernel(nf4_unpack_multi_kernel, dim3(static_cast<unsigned>(tiles)),
+                       dim3(kNf4Threads), s, parts, log2_exact(qblock / 8), log2_exact(qblock2));
 }

@@ -4,13 +4,14 @@ Mirrors the per-layer body of the reference's fused_forward (solution/model.py:2
 real (non-pad) tokens:
 
   s, y, y_pad = add_rmsnorm(s, d)               residual add + input RMSNorm (HIP)
-  qkv        = y @ [Wq;Wk;Wv]^T + b               NF4 unpack (HIP) + one hipBLASLt GEMM
-  lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v, PyTorch (fp16 GEMMs)
+  (all seven NF4 projections unpacked by one HIP launch: UNPACK_PER_LAYER)
+  qkv        = y @ [Wq;Wk;Wv]^T + b               one hipBLASLt GEMM
+  lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v (HIP, or fp16 GEMMs with dropout)
   q, k, v    = rope_pack(qkv, lq, lv)             LoRA add + RoPE + pack (HIP)
   a          = attention(q, k, v, causal + pad)   causal GQA flash attention (HIP), token-major
-  o          = a[real tokens] @ Wo^T              NF4 unpack (HIP) + hipBLASLt
+  o          = a[real tokens] @ Wo^T              hipBLASLt
   s, y2, _   = add_rmsnorm(s, o)                  residual add + post-attention RMSNorm (HIP)
-  d          = mlp(y2)                            NF4 unpack + GEMM + SwiGLU (HIP) + GEMM
+  d          = mlp(y2)                            GEMM + SwiGLU (HIP) + GEMM
 
 The reference takes these modules from a PEFT/bitsandbytes model; here they are plain tensors
 (`LayerWeights`), so one layer can be built from synthetic NF4 weights for measurement and
@@ -34,7 +35,8 @@ from . import attention as _attention
 from . import lora as _lora
 from . import workloads
 from .mlp import fused_mlp
-from .nf4 import frozen_linear, keep_for_backward, unpack_concat, unpacked_for_backward
+from .nf4 import (frozen_linear, keep_for_backward, unpack_concat, unpack_groups,
+                  unpacked_for_backward)
 from .rmsnorm import add_rmsnorm
 from .rope import rope_pack
 
@@ -89,6 +91,13 @@ def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
 # Rank-16 LoRA through testt_amd/csrc/lora.hip (False: the separate fp16 GEMMs below).
 USE_FUSED_LORA = True
 
+# The seven projections of a layer unpacked by one launch before its forward (one buffer, the
+# row stacks q|k|v, o, gate|up, down as views), instead of one launch per stack where each is
+# used (the reference's order, solution/nf4.py:125 and solution/mlp.py:105-108).  The fp16
+# values are the same; the whole buffer lives until the last stack is released (the backward
+# of q|k|v when the weights are kept for backward, the end of the layer's forward otherwise).
+UNPACK_PER_LAYER = True
+
 
 class QKVLora(torch.autograd.Function):
     """(qkv, lora_q, lora_v) from the fp16 norm output y, for LoRA without dropout:
@@ -98,8 +107,8 @@ class QKVLora(torch.autograd.Function):
     autocast (solution/model.py:195-206 with dropout p = 0)."""
 
     @staticmethod
-    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights):
-        w = unpack_concat(weights, y16.device)
+    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16=None):
+        w = w16 if w16 is not None else unpack_concat(weights, y16.device)
         qkv = torch.nn.functional.linear(y16, w, bias)
         keep_for_backward(ctx, w)
         del w
@@ -148,7 +157,7 @@ class QKVLora(torch.autograd.Function):
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)
-        return dy, None, grads[0], grads[1], grads[2], grads[3], None, None
+        return dy, None, grads[0], grads[1], grads[2], grads[3], None, None, None
 
     @staticmethod
     def _backward_fused(ctx, g_qkv, g_lq, g_lv):
@@ -162,7 +171,7 @@ class QKVLora(torch.autograd.Function):
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)
-        return dy, None, d_aq, d_bq, d_av, d_bv, None, None
+        return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None
 
 
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
@@ -223,24 +232,28 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     padded."""
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
+    w_qkv = w_o = w_gu = w_d = None
+    if UNPACK_PER_LAYER:
+        w_qkv, w_o, w_gu, w_d = unpack_groups(((w.q, w.k, w.v), (w.o,), (w.gate, w.up),
+                                               (w.down,)), s.device)
     if w.dropout == 0.0:
         s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         qkv, lq, lv = QKVLora.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
-                                    (w.q, w.k, w.v))
+                                    (w.q, w.k, w.v), w_qkv)
     else:
         s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
-        qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias)
+        qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias, w_qkv)
         lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
         lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
         del y_pad
     q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
-    del qkv, lq, lv
+    del qkv, lq, lv, w_qkv
     a = attention(q, k, v, key_valid)
     del q, k, v
     if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
         a = a.index_select(0, pos_idx)
-    o = frozen_linear(a, (w.o,), None)
-    del a
+    o = frozen_linear(a, (w.o,), None, w_o)
+    del a, w_o
     s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)
-    d = fused_mlp(y2, w.gate, w.up, w.down)
+    d = fused_mlp(y2, w.gate, w.up, w.down, w_gu, w_d)
     return s, d

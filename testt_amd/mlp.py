@@ -60,8 +60,8 @@ def gated_silu_backward_(dact, gu):
 
 class FusedNF4MLP(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, gate_w, up_w, down_w):
-        gate_up = unpack_concat((gate_w, up_w), x.device)
+    def forward(ctx, x, gate_w, up_w, down_w, gate_up16=None, down16=None):
+        gate_up = gate_up16 if gate_up16 is not None else unpack_concat((gate_w, up_w), x.device)
         gu = torch.matmul(x, gate_up.t())
         act = gated_silu(gu)
         ctx.recompute = RECOMPUTE_GATE_UP
@@ -71,7 +71,7 @@ class FusedNF4MLP(torch.autograd.Function):
             ctx.save_for_backward(x)
         else:
             ctx.save_for_backward(x, gu)
-        down = unpack_concat((down_w,), x.device)
+        down = down16 if down16 is not None else unpack_concat((down_w,), x.device)
         out = torch.matmul(act, down.t())
         ctx.weights = (gate_w, up_w, down_w)
         keep_for_backward(ctx, (gate_up, down))
@@ -80,7 +80,7 @@ class FusedNF4MLP(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         if not ctx.needs_input_grad[0]:
-            return None, None, None, None
+            return None, None, None, None, None, None
         gate_w, up_w, down_w = ctx.weights
         saved = ctx.saved_tensors
         x = saved[0]
@@ -106,10 +106,12 @@ class FusedNF4MLP(torch.autograd.Function):
         gated_silu_backward_(dact, gu)
         del dact
         grad_x = torch.matmul(gu, gate_up)
-        return grad_x, None, None, None
+        return grad_x, None, None, None, None, None
 
 
-def fused_mlp(x, gate_w, up_w, down_w):
+def fused_mlp(x, gate_w, up_w, down_w, gate_up16=None, down16=None):
+    """down(silu(gate(x)) * up(x)); gate_up16 / down16, when given, are the gate|up and down
+    stacks already unpacked (nf4.unpack_groups)."""
     if not kernels_ok(x):
         raise ValueError("fused_mlp: x must be a HIP device tensor (no CPU path)")
-    return FusedNF4MLP.apply(x.contiguous(), gate_w, up_w, down_w)
+    return FusedNF4MLP.apply(x.contiguous(), gate_w, up_w, down_w, gate_up16, down16)

@@ -14,6 +14,8 @@ bitsandbytes' dequantize_4bit.  Several projections are unpacked into one buffer
 or gate/up run as a single hipBLASLt GEMM (torch.matmul).
 """
 
+import ctypes
+
 import torch
 
 from . import _ext
@@ -158,28 +160,96 @@ def weight_shape(weight):
     return tuple(_quant_state(weight).shape)
 
 
+# Most weights soupk_nf4_unpack_multi takes in one launch.
+MAX_PARTS_PER_LAUNCH = 8
+
+
+def unpack_many(weights, outs):
+    """unpack_into(w, o) for every pair, as few launches as the kernel allows: the weights with
+    a kernel plan that share one (qblock, qblock2) go through soupk_nf4_unpack_multi, up to
+    MAX_PARTS_PER_LAUNCH per launch, the rest through unpack_into."""
+    if not outs:
+        return
+    if not all(kernels_ok(o) for o in outs):
+        raise ValueError("unpack_many: outputs must be HIP device tensors (no CPU path)")
+    groups = {}
+    for weight, out in zip(weights, outs, strict=True):
+        plan = _plan(weight, out.device)
+        if plan is None or out.device != outs[0].device:
+            unpack_into(weight, out)
+            continue
+        _ext.require(out, "out", dtype=torch.float16)
+        if out.numel() != 2 * plan[1] or not out.is_contiguous():
+            raise ValueError(f"out has {out.numel()} elements (contiguous: "
+                             f"{out.is_contiguous()}), the weight holds {2 * plan[1]}")
+        groups.setdefault((plan[2], plan[3]), []).append((plan, out))
+    for (qblock, qblock2), items in groups.items():
+        for c in range(0, len(items), MAX_PARTS_PER_LAUNCH):
+            chunk = items[c:c + MAX_PARTS_PER_LAUNCH]
+            n = len(chunk)
+            arrays = [(ctypes.c_void_p * n)(*[p[0][i] for p, _ in chunk]) for i in range(6)]
+            outs_a = (ctypes.c_void_p * n)(*[o.data_ptr() for _, o in chunk])
+            sizes = (ctypes.c_int64 * n)(*[p[1] for p, _ in chunk])
+            _ext.call("soupk_nf4_unpack_multi", n, *[ctypes.addressof(a) for a in arrays],
+                      ctypes.addressof(outs_a), ctypes.addressof(sizes), qblock, qblock2,
+                      _ext.stream_of(chunk[0][1]))
+
+
 def unpack_concat(weights, device):
-    """fp16 [sum N_i, K]: the weights stacked by rows, each unpacked in place."""
+    """fp16 [sum N_i, K]: the weights stacked by rows, unpacked in place (one launch)."""
     rows = [weight_shape(w)[0] for w in weights]
     cols = weight_shape(weights[0])[1]
     out = torch.empty((sum(rows), cols), dtype=torch.float16, device=device)
-    start = 0
-    for weight, n in zip(weights, rows):
-        unpack_into(weight, out[start:start + n])
+    views, start = [], 0
+    for n in rows:
+        views.append(out[start:start + n])
         start += n
+    unpack_many(weights, views)
     return out
+
+
+# Row stacks placed in one buffer by unpack_groups start at multiples of this many elements
+# (512 bytes), the alignment the GEMM kernels are given for separately allocated weights.
+_GROUP_ALIGN = 256
+
+
+def unpack_groups(groups, device):
+    """One fp16 [sum N_i, K] row stack per group of weights (unpack_concat of each group), all
+    unpacked by one launch into a single buffer: the projections of a decoder layer
+    (q|k|v, o, gate|up, down) before its forward.  Returns the stacks, views of the buffer."""
+    shapes, total = [], 0
+    for weights in groups:
+        rows = [weight_shape(w)[0] for w in weights]
+        cols = weight_shape(weights[0])[1]
+        if any(weight_shape(w)[1] != cols for w in weights):
+            raise ValueError("weights of one group must have the same number of columns")
+        shapes.append((total, rows, cols))
+        total += -(-sum(rows) * cols // _GROUP_ALIGN) * _GROUP_ALIGN
+    buf = torch.empty(total, dtype=torch.float16, device=device)
+    stacks, flat_w, flat_o = [], [], []
+    for weights, (start, rows, cols) in zip(groups, shapes):
+        stack = buf[start:start + sum(rows) * cols].view(sum(rows), cols)
+        stacks.append(stack)
+        r0 = 0
+        for w, n in zip(weights, rows):
+            flat_w.append(w)
+            flat_o.append(stack[r0:r0 + n])
+            r0 += n
+    unpack_many(flat_w, flat_o)
+    return stacks
 
 
 class FrozenNF4Linear(torch.autograd.Function):
     """y = x @ W^T (+ b) for frozen 4-bit weights stacked by rows, fp16 in and out.
 
     No input is kept because W does not train (solution/nf4.py:108-127); the unpacked weight
-    is kept for backward or unpacked again there (KEEP_UNPACKED_FOR_BACKWARD)."""
+    (`w16` when the caller unpacked it already) is kept for backward or unpacked again there
+    (KEEP_UNPACKED_FOR_BACKWARD)."""
 
     @staticmethod
-    def forward(ctx, x, bias, weights):
+    def forward(ctx, x, bias, weights, w16=None):
         ctx.weights = weights
-        if USE_FUSED_NF4_GEMM:
+        if w16 is None and USE_FUSED_NF4_GEMM:
             from . import nf4_gemm
 
             x2 = x.reshape(-1, x.shape[-1])
@@ -187,7 +257,7 @@ class FrozenNF4Linear(torch.autograd.Function):
                 ctx.unpacked = None
                 out = nf4_gemm.nf4_linear(x2, weights, bias)
                 return out.view(*x.shape[:-1], out.shape[-1])
-        weight = unpack_concat(weights, x.device)
+        weight = w16 if w16 is not None else unpack_concat(weights, x.device)
         out = torch.nn.functional.linear(x, weight, bias)
         keep_for_backward(ctx, weight)
         return out
@@ -198,8 +268,10 @@ class FrozenNF4Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
             grad_x = grad_out.to(torch.float16) @ weight
-        return grad_x, None, None
+        return grad_x, None, None, None
 
 
-def frozen_linear(x, weights, bias=None):
-    return FrozenNF4Linear.apply(x, bias, tuple(weights))
+def frozen_linear(x, weights, bias=None, w16=None):
+    """x @ W^T (+ bias), W the row stack of `weights`; `w16`, when given, is that stack already
+    unpacked (unpack_groups), used instead of unpacking again."""
+    return FrozenNF4Linear.apply(x, bias, tuple(weights), w16)
