@@ -94,6 +94,16 @@ int soupk_index_inverse(const int64_t* idx, int64_t n, int32_t* inv, int64_t n_s
                         void* stream);
 
 /*
+ * Split-K reduction (no counterpart kernel in the reference: the reference computes the MLP's
+ * gate|up input gradient as one fp16 GEMM, solution/mlp.py:105-113; here that GEMM runs as
+ * n_parts batched GEMMs over slices of K with fp32 outputs, and this sums them).
+ *   out_f16[i] = fp16_rn(((parts[i] + parts[stride + i]) + parts[2 stride + i]) + ...)
+ * for i < n, partials added in index order.  1 <= n_parts <= 16, part_stride >= n.
+ */
+int soupk_sum_partials(const float* parts, int32_t n_parts, int64_t part_stride, int64_t n,
+                       uint16_t* out_f16, void* stream);
+
+/*
  * Residual add + Qwen2RMSNorm forward (replaces rmsnorm_fwd_kernel, solution/rmsnorm.py:24-43,
  * launched from _launch_fwd, solution/rmsnorm.py:76-92).  Per row r of [rows, H]:
  *   s = x + fp32(delta)            (stored to s_out when delta != NULL)

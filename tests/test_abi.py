@@ -53,6 +53,10 @@ def test_version_and_status_strings(lib):
     ("soupk_swiglu_bwd_inplace", (None, None, 4, 8, None)),
     ("soupk_nf4_unpack", (None,) * 7 + (64, 63, 256, None)),
     ("soupk_nf4_unpack_multi", (9,) + (None,) * 8 + (64, 256, None)),      # more than 8 parts
+    ("soupk_sum_partials", (None, 0, 8, 8, None, None)),
+    ("soupk_sum_partials", (None, 17, 8, 8, None, None)),
+    ("soupk_sum_partials", (None, 2, 4, 8, None, None)),                    # stride < n
+    ("soupk_sum_partials", (None, 2, 8, 8, None, None)),                    # null pointers
     ("soupk_nf4_unpack_multi", (1,) + (None,) * 8 + (63, 256, None)),
     ("soupk_nf4_unpack_multi", (2,) + (None,) * 8 + (64, 256, None)),      # null arrays
     ("soupk_rmsnorm_fwd", (None,) * 9 + (4, 0, 0, 1e-6, None)),
@@ -74,6 +78,7 @@ def test_invalid_arguments_rejected_before_launch(lib, name, args):
     ("soupk_swiglu_fwd", (None, None, 0, 8960, None)),
     ("soupk_nf4_unpack", (None,) * 7 + (0, 64, 256, None)),
     ("soupk_nf4_unpack_multi", (0,) + (None,) * 8 + (64, 256, None)),
+    ("soupk_sum_partials", (None, 4, 0, 0, None, None)),
     ("soupk_head_stats_grad", (None,) * 6 + (1.0, 0, 151936, None)),
     ("soupk_index_inverse", (None, 0, None, 0, None)),
 ])

@@ -13,14 +13,20 @@
 // caller then adds the frozen projection's input gradient into dy in place and forms the
 // parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from gs, t and dt.
 //
-// A workgroup is 4 wavefronts and 16 rows.  The long contractions (over H for t, over NQ / NV
-// for dt) run on v_mfma_f32_16x16x32_f16 with the contraction split over the 4 wavefronts and
-// the partial sums added in wavefront order (deterministic).  The short ones (over r for lq/lv,
-// on v_mfma_f32_16x16x16f16; over 2r for dy, on 16x16x32) are computed transposed, one 16-column
-// tile at a time: (out tile)^T = W16 x^T, so that a lane's four results are four consecutive
-// columns of one row (one 8-byte store).  MFMA layouts: A lane l holds row l%16, B lane l
-// column l%16, each with k = 8(l/16)..+7 (16x16x32) or 4(l/16)..+3 (16x16x16); C lane l holds
-// column l%16, rows 4(l/16)..+3.
+// A workgroup is 4 wavefronts and 64 rows (four 16-row MFMA tiles, which share every A / B
+// fragment a wavefront loads: the fp32 LoRA parameters are read once per 64 rows), and the
+// workgroups of a row block split the wide output (lq|lv, or dy) by 16-column tiles (grid.y
+// parts), each recomputing the block's rank-2r product, so that the launch still has a few
+// hundred workgroups (the rank-2r product, t or dt, and gs are written by part 0).  The long contractions (over H for
+// t, over NQ / NV for dt) run on v_mfma_f32_16x16x32_f16 with the contraction split over the
+// 4 wavefronts and the partial sums added in wavefront order (deterministic).  The short ones
+// (over r for lq/lv, on v_mfma_f32_16x16x16f16; over 2r for dy, on 16x16x32) are computed
+// transposed, one 16-column tile at a time: (out tile)^T = W16 x^T, so that a lane's four
+// results are four consecutive columns of one row (one 8-byte store).  MFMA layouts: A lane l
+// holds row l%16, B lane l column l%16, each with k = 8(l/16)..+7 (16x16x32) or 4(l/16)..+3
+// (16x16x16); C lane l holds column l%16, rows 4(l/16)..+3.
+
+#include <algorithm>
 
 #include "soupk_common.hpp"
 
@@ -32,7 +38,11 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kR = 16;           // LoRA rank
-constexpr int kRows = 16;        // rows per workgroup
+#ifndef SOUPK_LORA_ROW_TILES
+#define SOUPK_LORA_ROW_TILES 4
+#endif
+constexpr int kRowTiles = SOUPK_LORA_ROW_TILES;   // 16-row MFMA tiles per workgroup
+constexpr int kRows = 16 * kRowTiles;              // rows per workgroup
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
@@ -43,7 +53,9 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(x)); }
+__device__ __forceinline__ float r16(float x) {
+  return static_cast<float>(static_cast<_Float16>(x));
+}
 
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
@@ -63,6 +75,13 @@ __device__ __forceinline__ h8 to_h8(f4 a, f4 b) {
 // MFMA waited for its own loads.
 constexpr int kBatch = 4;
 
+// Split of the output tiles over the workgroups of one row block (grid.y column parts): each
+// part recomputes the row block's rank-r product (cheap: 2r columns) and writes its share of
+// the wide output, so that a small M still fills the GPU.
+__device__ __forceinline__ int tile_part(int n_tiles, int part, int parts) {
+  return static_cast<int>((static_cast<int64_t>(n_tiles) * part) / parts);
+}
+
 __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
     const uint16_t* __restrict__ y, const float* __restrict__ aq, const float* __restrict__ av,
     const float* __restrict__ bq, const float* __restrict__ bv, float scaling,
@@ -73,23 +92,30 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   const int m0 = blockIdx.x * kRows;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
-  const int64_t row = min(m0 + ql, M - 1);
-  // t = y A^T: A operand = y rows (row ql, k = k0 + 8gr..+7); B operand = A_q / A_v rows
-  // (column = feature ql).  The contraction over H is split over the 4 wavefronts.
+  // t = y A^T: A operand = y rows (row 16rt + ql of row tile rt, k = k0 + 8gr..+7); B operand =
+  // A_q / A_v rows (column = feature ql), loaded once per step for the kRowTiles row tiles.
+  // The contraction over H is split over the 4 wavefronts.
   const int kw = H / 4;
-  f4 acc_q = {0.f, 0.f, 0.f, 0.f}, acc_v = {0.f, 0.f, 0.f, 0.f};
-  const uint16_t* yrow = y + row * H;
-
+  const uint16_t* yrow[kRowTiles];
+  f4 acc_q[kRowTiles], acc_v[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    yrow[rt] = y + static_cast<int64_t>(min(m0 + 16 * rt + ql, M - 1)) * H;
+    acc_q[rt] = f4{0.f, 0.f, 0.f, 0.f};
+    acc_v[rt] = f4{0.f, 0.f, 0.f, 0.f};
+  }
   const int steps = kw / 32;
   const float* aqrow = aq + static_cast<int64_t>(ql) * H + 8 * gr;
   const float* avrow = av + static_cast<int64_t>(ql) * H + 8 * gr;
   for (int s0 = 0; s0 < steps; s0 += kBatch) {
-    h8 ya[kBatch];
+    h8 ya[kBatch][kRowTiles];
     f4 qa[kBatch][2], va[kBatch][2];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int k0 = w * kw + 32 * min(s0 + u, steps - 1);
-      ya[u] = *reinterpret_cast<const h8*>(yrow + k0 + 8 * gr);
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt)
+        ya[u][rt] = *reinterpret_cast<const h8*>(yrow[rt] + k0 + 8 * gr);
       qa[u][0] = *reinterpret_cast<const f4*>(aqrow + k0);
       qa[u][1] = *reinterpret_cast<const f4*>(aqrow + k0 + 4);
       va[u][0] = *reinterpret_cast<const f4*>(avrow + k0);
@@ -98,16 +124,23 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (s0 + u < steps) {
-        acc_q = mfma32(ya[u], to_h8(qa[u][0], qa[u][1]), acc_q);
-        acc_v = mfma32(ya[u], to_h8(va[u][0], va[u][1]), acc_v);
+        const h8 bq8 = to_h8(qa[u][0], qa[u][1]), bv8 = to_h8(va[u][0], va[u][1]);
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          acc_q[rt] = mfma32(ya[u][rt], bq8, acc_q[rt]);
+          acc_v[rt] = mfma32(ya[u][rt], bv8, acc_v[rt]);
+        }
       }
     }
   }
-  // C: column = feature ql, rows 4gr .. +3
+  // C: column = feature ql, rows 16rt + 4gr .. +3
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    part[w][4 * gr + i][ql] = acc_q[i];
-    part[w][4 * gr + i][kR + ql] = acc_v[i];
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part[w][16 * rt + 4 * gr + i][ql] = acc_q[rt][i];
+      part[w][16 * rt + 4 * gr + i][kR + ql] = acc_v[rt][i];
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < kRows * 2 * kR; e += kThreads) {
@@ -115,20 +148,29 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
     const float s = ((part[0][m][f] + part[1][m][f]) + part[2][m][f]) + part[3][m][f];
     const _Float16 h = static_cast<_Float16>(s);
     tt[m][f] = static_cast<float>(h);
-    if (m0 + m < M) t_out[static_cast<int64_t>(m0 + m) * (2 * kR) + f] = h_bits(h);
+    if (blockIdx.y == 0 && m0 + m < M)
+      t_out[static_cast<int64_t>(m0 + m) * (2 * kR) + f] = h_bits(h);
   }
   __syncthreads();
   // lq, lv: tile f0..f0+15 of the output columns, transposed: A = B16 rows (feature f0 + ql,
-  // k = rank 4gr..+3), B = t rows (column = row ql of the workgroup, same k)
-  const int nq16 = NQ / 16, n16 = nq16 + NV / 16;
-  const float* tq = &tt[ql][4 * gr];
-  const float* tv = &tt[ql][kR + 4 * gr];
-  const h4 tq4 = {static_cast<_Float16>(tq[0]), static_cast<_Float16>(tq[1]),
-                  static_cast<_Float16>(tq[2]), static_cast<_Float16>(tq[3])};
-  const h4 tv4 = {static_cast<_Float16>(tv[0]), static_cast<_Float16>(tv[1]),
-                  static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
-  const bool row_ok = m0 + ql < M;
-  for (int t0 = w; t0 < n16; t0 += 4 * kBatch) {
+  // k = rank 4gr..+3), B = t rows (column = row ql of a row tile, same k).  Column part
+  // blockIdx.y of gridDim.y takes tiles [t_begin, t_end) of the NQ/16 + NV/16.
+  const int nq16 = NQ / 16;
+  const int t_begin = tile_part(NQ / 16 + NV / 16, blockIdx.y, gridDim.y);
+  const int n16 = tile_part(NQ / 16 + NV / 16, blockIdx.y + 1, gridDim.y);
+  h4 tq4[kRowTiles], tv4[kRowTiles];
+  bool row_ok[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    const float* tq = &tt[16 * rt + ql][4 * gr];
+    const float* tv = &tt[16 * rt + ql][kR + 4 * gr];
+    tq4[rt] = h4{static_cast<_Float16>(tq[0]), static_cast<_Float16>(tq[1]),
+                 static_cast<_Float16>(tq[2]), static_cast<_Float16>(tq[3])};
+    tv4[rt] = h4{static_cast<_Float16>(tv[0]), static_cast<_Float16>(tv[1]),
+                 static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
+    row_ok[rt] = m0 + 16 * rt + ql < M;
+  }
+  for (int t0 = t_begin + w; t0 < n16; t0 += 4 * kBatch) {
     f4 bw[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -147,13 +189,17 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
       const int N = is_q ? NQ : NV;
       const h4 a = {static_cast<_Float16>(bw[u][0]), static_cast<_Float16>(bw[u][1]),
                     static_cast<_Float16>(bw[u][2]), static_cast<_Float16>(bw[u][3])};
-      const f4 c = mfma16(a, is_q ? tq4 : tv4, f4{0.f, 0.f, 0.f, 0.f});
-      // C: column = row ql, rows = features f0 + 4gr .. +3
-      if (row_ok) {
-        uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + ql) * N + f0 + 4 * gr;
-        *reinterpret_cast<u32x2*>(dst) =
-            u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
-                  pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt) {
+        const f4 c = mfma16(a, is_q ? tq4[rt] : tv4[rt], f4{0.f, 0.f, 0.f, 0.f});
+        // C: column = row 16rt + ql, rows = features f0 + 4gr .. +3
+        if (row_ok[rt]) {
+          uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + 16 * rt + ql) * N + f0 +
+                          4 * gr;
+          *reinterpret_cast<u32x2*>(dst) =
+              u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
+                    pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+        }
       }
     }
   }
@@ -170,51 +216,70 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   const int m0 = blockIdx.x * kRows;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
-  const int mr = m0 + ql;
-  const int64_t row = min(mr, M - 1);
-  const bool row_ok = mr < M;
-  // dt_x = gs_x B16_x: A operand = gs rows (row ql, k = j0 + 8gr..+7), stored as gs on the
-  // way; B operand = B16 (column = rank index ql, k = j rows: B is [N, r] row-major, so the
-  // 8 k-values of a lane are 8 rows, each read by 16 consecutive lanes as 64 contiguous bytes)
-  f4 acc_q = {0.f, 0.f, 0.f, 0.f}, acc_v = {0.f, 0.f, 0.f, 0.f};
+  int64_t row[kRowTiles];
+  bool row_ok[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    row[rt] = min(m0 + 16 * rt + ql, M - 1);
+    row_ok[rt] = m0 + 16 * rt + ql < M;
+  }
+  const bool store_gs = blockIdx.y == 0;
+  // dt_x = gs_x B16_x: A operand = gs rows (row 16rt + ql, k = j0 + 8gr..+7), stored as gs on
+  // the way (by column part 0); B operand = B16 (column = rank index ql, k = j rows: B is
+  // [N, r] row-major, so the 8 k-values of a lane are 8 rows, each read by 16 consecutive
+  // lanes as 64 contiguous bytes), loaded once per step for the kRowTiles row tiles.
+  f4 acc_q[kRowTiles], acc_v[kRowTiles];
+#pragma unroll
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+    acc_q[rt] = f4{0.f, 0.f, 0.f, 0.f};
+    acc_v[rt] = f4{0.f, 0.f, 0.f, 0.f};
+  }
   // steps of 32 columns of g over this wavefront's quarter of N
   auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const float* b,
-                 f4& acc) {
+                 f4* acc) {
     const int kn = N / 4, steps = kn / 32;
-    const uint16_t* grow = g + row * ldg + w * kn + 8 * gr;
     const float* bcol = b + static_cast<int64_t>(w * kn + 8 * gr) * kR + ql;
     for (int s0 = 0; s0 < steps; s0 += kBatch) {
-      h8 graw[kBatch];
+      h8 graw[kBatch][kRowTiles];
       float braw[kBatch][8];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int j = 32 * min(s0 + u, steps - 1);
-        graw[u] = *reinterpret_cast<const h8*>(grow + j);
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt)
+          graw[u][rt] = *reinterpret_cast<const h8*>(g + row[rt] * ldg + w * kn + 8 * gr + j);
 #pragma unroll
         for (int i = 0; i < 8; ++i) braw[u][i] = bcol[static_cast<int64_t>(j + i) * kR];
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         if (s0 + u >= steps) break;
-        h8 ga, ba;
+        h8 ba;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          ga[i] = static_cast<_Float16>(static_cast<float>(graw[u][i]) * scaling);
-          ba[i] = static_cast<_Float16>(braw[u][i]);
+        for (int i = 0; i < 8; ++i) ba[i] = static_cast<_Float16>(braw[u][i]);
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          h8 ga;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            ga[i] = static_cast<_Float16>(static_cast<float>(graw[u][rt][i]) * scaling);
+          if (store_gs && row_ok[rt])
+            *reinterpret_cast<h8*>(gs + (m0 + 16 * rt + ql) * static_cast<int64_t>(N) +
+                                   w * kn + 32 * (s0 + u) + 8 * gr) = ga;
+          acc[rt] = mfma32(ga, ba, acc[rt]);
         }
-        if (row_ok)
-          *reinterpret_cast<h8*>(gs + static_cast<int64_t>(mr) * N + w * kn + 32 * (s0 + u) +
-                                 8 * gr) = ga;
-        acc = mfma32(ga, ba, acc);
       }
     }
   };
   run(gq, ldq, gsq, NQ, bq, acc_q);
   run(gv, ldv, gsv, NV, bv, acc_v);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    part[w][4 * gr + i][ql] = acc_q[i];
-    part[w][4 * gr + i][kR + ql] = acc_v[i];
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part[w][16 * rt + 4 * gr + i][ql] = acc_q[rt][i];
+      part[w][16 * rt + 4 * gr + i][kR + ql] = acc_v[rt][i];
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < kRows * 2 * kR; e += kThreads) {
@@ -222,20 +287,25 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     const float s = ((part[0][m][f] + part[1][m][f]) + part[2][m][f]) + part[3][m][f];
     const _Float16 h = static_cast<_Float16>(s);
     dts[m][f] = static_cast<float>(h);
-    if (m0 + m < M) dt_out[static_cast<int64_t>(m0 + m) * (2 * kR) + f] = h_bits(h);
+    if (blockIdx.y == 0 && m0 + m < M)
+      dt_out[static_cast<int64_t>(m0 + m) * (2 * kR) + f] = h_bits(h);
   }
   __syncthreads();
   // dy = dt A16 (contraction over the 2r rank indices; A = A_q rows then A_v rows), one
   // 16-column tile of H at a time, transposed: A operand = A16 columns (row h0 + ql, k = rank
   // 8gr..+7: 8 rows of A, each read by 16 consecutive lanes as 64 contiguous bytes), B = dt
-  // rows (column = row ql)
-  h8 dtb;
+  // rows (column = row ql of a row tile)
+  h8 dtb[kRowTiles];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dtb[i] = static_cast<_Float16>(dts[ql][8 * gr + i]);
+  for (int rt = 0; rt < kRowTiles; ++rt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dtb[rt][i] = static_cast<_Float16>(dts[16 * rt + ql][8 * gr + i]);
+  }
   const float* abase = (gr < 2 ? aq + static_cast<int64_t>(8 * gr) * H
                                : av + static_cast<int64_t>(8 * (gr - 2)) * H) + ql;
-  const int n16 = H / 16;
-  for (int t0 = w; t0 < n16; t0 += 4 * kBatch) {
+  const int t_begin = tile_part(H / 16, blockIdx.y, gridDim.y);
+  const int n16 = tile_part(H / 16, blockIdx.y + 1, gridDim.y);
+  for (int t0 = t_begin + w; t0 < n16; t0 += 4 * kBatch) {
     float araw[kBatch][8];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -250,10 +320,14 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
       h8 a;
 #pragma unroll
       for (int i = 0; i < 8; ++i) a[i] = static_cast<_Float16>(araw[u][i]);
-      const f4 c = mfma32(a, dtb, f4{0.f, 0.f, 0.f, 0.f});
-      if (row_ok)
-        *reinterpret_cast<u32x2*>(dy + static_cast<int64_t>(mr) * H + 16 * tile + 4 * gr) =
-            u32x2{pack_h2(c[0], c[1]), pack_h2(c[2], c[3])};
+#pragma unroll
+      for (int rt = 0; rt < kRowTiles; ++rt) {
+        const f4 c = mfma32(a, dtb[rt], f4{0.f, 0.f, 0.f, 0.f});
+        if (row_ok[rt])
+          *reinterpret_cast<u32x2*>(dy + (m0 + 16 * rt + ql) * static_cast<int64_t>(H) +
+                                    16 * tile + 4 * gr) =
+              u32x2{pack_h2(c[0], c[1]), pack_h2(c[2], c[3])};
+      }
     }
   }
 }
@@ -378,6 +452,19 @@ int check_dims(int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r) {
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
+// Column parts per row block: about kTargetGroups workgroups in all (2 per CU), each part at
+// least 4 * kBatch output tiles (one batch per wavefront).
+#ifndef SOUPK_LORA_TARGET_GROUPS
+#define SOUPK_LORA_TARGET_GROUPS 512
+#endif
+constexpr int64_t kTargetGroups = SOUPK_LORA_TARGET_GROUPS;
+unsigned column_parts(int64_t M, int n_tiles) {
+  const int64_t row_blocks = (M + kRows - 1) / kRows;
+  int64_t parts = (kTargetGroups + row_blocks - 1) / row_blocks;
+  parts = std::min<int64_t>(parts, std::max(1, n_tiles / (4 * kBatch)));
+  return static_cast<unsigned>(std::max<int64_t>(parts, 1));
+}
+
 }  // namespace
 }  // namespace soupk
 
@@ -397,7 +484,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_fwd(
                         static_cast<const void*>(lv)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
-  return launch_kernel(lora_fwd_kernel, dim3(grid), dim3(kThreads),
+  return launch_kernel(lora_fwd_kernel, dim3(grid, column_parts(M, NQ / 16 + NV / 16)),
+                       dim3(kThreads),
                        static_cast<hipStream_t>(stream), y, a_q, a_v, b_q, b_v, scaling, t, lq,
                        lv, static_cast<int>(M), H, NQ, NV);
 }
@@ -419,7 +507,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_rows(
                         static_cast<const void*>(dy)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
-  return launch_kernel(lora_bwd_rows_kernel, dim3(grid), dim3(kThreads),
+  return launch_kernel(lora_bwd_rows_kernel, dim3(grid, column_parts(M, H / 16)),
+                       dim3(kThreads),
                        static_cast<hipStream_t>(stream), g_q, ld_q, g_v, ld_v, a_q, a_v, b_q, b_v,
                        scaling, gs_q, gs_v, dt, dy, static_cast<int>(M), H, NQ, NV);
 }

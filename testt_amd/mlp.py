@@ -5,7 +5,8 @@ Drop-in for solution/mlp.py.
 - testt_amd/csrc/swiglu.hip reads the fp16 [tokens, 2I] result and writes silu(g) * u in fp16
   (computed in fp32, rounded once to fp16 where the down projection reads it);
 - backward turns the incoming gradient into the gate/up gradients in place, in the [tokens, 2I]
-  gate/up buffer, so the input gradient is again a single GEMM.
+  gate/up buffer, so the input gradient is again a single product (split along K over
+  batched GEMMs with fp32 partials, SPLIT_K_GATE_UP, and summed by a HIP kernel).
 
 RECOMPUTE_GATE_UP (solution/mlp.py:27) chooses where that buffer comes from.  The reference
 recomputes it in backward (one more [tokens, H] x [H, 2I] GEMM) to keep nothing of size
@@ -24,6 +25,12 @@ from ._common import kernels_ok
 from .nf4 import keep_for_backward, unpack_concat
 
 RECOMPUTE_GATE_UP = False  # True: keep only the [tokens, H] input, recompute gate/up
+
+# Split of the gate|up input-gradient GEMM (d(gate|up) [tokens, 2I] @ [W_gate; W_up] [2I, H])
+# along K into this many batched hipBLASLt GEMMs with fp32 outputs, summed in order and rounded
+# once to fp16 by soupk_sum_partials.  The [tokens, H] output of the 2048-token step is 192
+# tiles of 128 x 128 for 256 CUs; four K slices make 768.  1 = one fp16 GEMM (the reference's).
+SPLIT_K_GATE_UP = 4
 # Columns one workgroup step covers per row in the reference's tiling (solution/mlp.py:28);
 # the HIP kernels stream the flat [rows, I] space in 16-byte chunks instead.
 COLS_PER_PROGRAM = 1024
@@ -56,6 +63,25 @@ def gated_silu_backward_(dact, gu):
         _ext.call("soupk_swiglu_bwd_inplace", _ext.ptr(dact), _ext.ptr(gu), rows, inter,
                   _ext.stream_of(gu))
     return gu
+
+
+def matmul_split_k(a, b, parts):
+    """fp16 a [M, K] @ b [K, N] as `parts` GEMMs over equal slices of K (batched, fp32
+    outputs), summed in slice order and rounded once to fp16.  K % parts == 0; a and b must
+    have unit column stride."""
+    M, K = a.shape
+    N = b.shape[1]
+    if K % parts or a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError(f"matmul_split_k: K={K} must split into {parts} slices, unit strides")
+    c = K // parts
+    a3 = a.as_strided((parts, M, c), (c, a.stride(0), 1))
+    b3 = b.as_strided((parts, c, N), (c * b.stride(0), b.stride(0), 1))
+    partial = torch.ops.aten.bmm.dtype(a3, b3, torch.float32)      # [parts, M, N] fp32
+    out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    if M * N:
+        _ext.call("soupk_sum_partials", partial.data_ptr(), parts, M * N, M * N,
+                  out.data_ptr(), _ext.stream_of(out))
+    return out
 
 
 class FusedNF4MLP(torch.autograd.Function):
@@ -105,7 +131,11 @@ class FusedNF4MLP(torch.autograd.Function):
             gu = saved[1]
         gated_silu_backward_(dact, gu)
         del dact
-        grad_x = torch.matmul(gu, gate_up)
+        parts = SPLIT_K_GATE_UP
+        if parts > 1 and gu.shape[1] % parts == 0 and gu.shape[0] > 0:
+            grad_x = matmul_split_k(gu, gate_up, parts)
+        else:
+            grad_x = torch.matmul(gu, gate_up)
         return grad_x, None, None, None, None, None
 
 
