@@ -13,18 +13,19 @@
 // caller then adds the frozen projection's input gradient into dy in place and forms the
 // parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from gs, t and dt.
 //
-// A workgroup is 4 wavefronts and 64 rows (four 16-row MFMA tiles, which share every A / B
-// fragment a wavefront loads: the fp32 LoRA parameters are read once per 64 rows), and the
-// workgroups of a row block split the wide output (lq|lv, or dy) by 16-column tiles (grid.y
-// parts), each recomputing the block's rank-2r product, so that the launch still has a few
-// hundred workgroups (the rank-2r product, t or dt, and gs are written by part 0).  The long contractions (over H for
-// t, over NQ / NV for dt) run on v_mfma_f32_16x16x32_f16 with the contraction split over the
-// 4 wavefronts and the partial sums added in wavefront order (deterministic).  The short ones
-// (over r for lq/lv, on v_mfma_f32_16x16x16f16; over 2r for dy, on 16x16x32) are computed
-// transposed, one 16-column tile at a time: (out tile)^T = W16 x^T, so that a lane's four
-// results are four consecutive columns of one row (one 8-byte store).  MFMA layouts: A lane l
-// holds row l%16, B lane l column l%16, each with k = 8(l/16)..+7 (16x16x32) or 4(l/16)..+3
-// (16x16x16); C lane l holds column l%16, rows 4(l/16)..+3.
+// A workgroup is 4 wavefronts and kRowTiles 16-row MFMA tiles (which share every A / B fragment a
+// wavefront loads), and the workgroups of a row block split the wide output (lq|lv, or dy) by
+// 16-column tiles (grid.y parts), each recomputing the block's rank-2r product (the rank-2r
+// product, t or dt, and gs are written by part 0).  Measured on MI355X at 2048 rows: one row tile
+// and about 256 workgroups (two column parts) is fastest (13.3 / 11.2 us against 16.4 / 13.8 us
+// with one part; four row tiles, or more parts, are slower).  The long contractions (over H for t,
+// over NQ / NV for dt) run on v_mfma_f32_16x16x32_f16 with the contraction split over the 4
+// wavefronts and the partial sums added in wavefront order (deterministic).  The short ones (over r
+// for lq/lv, on v_mfma_f32_16x16x16f16; over 2r for dy, on 16x16x32) are computed transposed, one
+// 16-column tile at a time: (out tile)^T = W16 x^T, so that a lane's four results are four
+// consecutive columns of one row (one 8-byte store).  MFMA layouts: A lane l holds row l%16, B lane
+// l column l%16, each with k = 8(l/16)..+7 (16x16x32) or 4(l/16)..+3 (16x16x16); C lane l holds
+// column l%16, rows 4(l/16)..+3.
 
 #include <algorithm>
 
@@ -39,7 +40,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kR = 16;           // LoRA rank
 #ifndef SOUPK_LORA_ROW_TILES
-#define SOUPK_LORA_ROW_TILES 4
+#define SOUPK_LORA_ROW_TILES 1
 #endif
 constexpr int kRowTiles = SOUPK_LORA_ROW_TILES;   // 16-row MFMA tiles per workgroup
 constexpr int kRows = 16 * kRowTiles;              // rows per workgroup
@@ -452,10 +453,10 @@ int check_dims(int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r) {
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
-// Column parts per row block: about kTargetGroups workgroups in all (2 per CU), each part at
-// least 4 * kBatch output tiles (one batch per wavefront).
+// Column parts per row block: about kTargetGroups workgroups in all, each part at least
+// 4 * kBatch output tiles (one batch per wavefront).
 #ifndef SOUPK_LORA_TARGET_GROUPS
-#define SOUPK_LORA_TARGET_GROUPS 512
+#define SOUPK_LORA_TARGET_GROUPS 256
 #endif
 constexpr int64_t kTargetGroups = SOUPK_LORA_TARGET_GROUPS;
 unsigned column_parts(int64_t M, int n_tiles) {
