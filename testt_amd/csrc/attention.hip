@@ -298,29 +298,64 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
 // With P = softmax of the scaled scores (recomputed from the saved log-sum-exp), dO the output
 // gradient and D = rowsum(dO * O):  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,
 // dK = scale * dS^T Q,  dV = P^T dO.  Three launches:
-//   attn_bwd_dq_kernel   (b, head, 64 queries): D for its queries (written for the next kernel),
-//                        then over its key blocks S^T = K Q^T, dP^T = V dO^T (the forward's
-//                        orientation: query = lane column), dQ^T += K^T dS^T;
-//   attn_bwd_dkdv_kernel (b, head, 64 keys): over the query blocks that see them,
-//                        S = Q K^T, dP = dO V^T (key = lane column), dV^T += dO^T P,
-//                        dK^T += Q^T dS, into fp32 partials per query head;
+//   attn_bwd_delta_kernel (b, head, 64 queries): D;
+//   attn_bwd_kernel       two kinds of workgroup in one grid, so that they run side by side
+//                         (z even: dK/dV of 64 keys, z odd: dQ of 64 queries, the heaviest
+//                         causal blocks of both kinds dispatched first):
+//     dQ   (b, head, 64 queries): over its key blocks S^T = K Q^T, dP^T = V dO^T (the
+//          forward's orientation: query = lane column), dQ^T += K^T dS^T;
+//     dKdV (b, head, 64 keys): over the query blocks that see them, S = Q K^T, dP = dO V^T
+//          (key = lane column), dV^T += dO^T P, dK^T += Q^T dS, into fp32 partials per query
+//          head;
 //   attn_bwd_reduce_kernel: dK, dV of a key/value head = the sum of its query heads' partials
-//                        (a fixed order: deterministic), fp16.
+//                         (a fixed order: deterministic), fp16.
 // Operands contracted over the head dim are read from row-major tiles (16-byte reads);
 // operands contracted over keys or queries from transposed tiles, in the order of the C tiles
 // they meet (lds_runs).
 
-__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
+// D = rowsum(dO * O) of 64 queries: lane (row l%16 of wavefront w's 16, group l/16) sums dims
+// 32s + 8gr .. +7 (s = 0..3) in order, then the four groups are combined by column_sum.
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_delta_kernel(
+    const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, float* __restrict__ delta,
+    int T, int NH) {
+  const int qb = static_cast<int>(blockIdx.z);
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  const int ql = lane & 15, gr = lane >> 4;
+  const int q_abs = qb * kBQ + 16 * w + ql;
+  const int qc = min(q_abs, T - 1);
+  const int64_t HD = static_cast<int64_t>(NH) * kD;
+  const uint16_t* orow = out + (static_cast<int64_t>(b) * T + qc) * HD + h * kD;
+  const uint16_t* dorow = dout + (static_cast<int64_t>(b) * T + qc) * HD + h * kD;
+  h8 of[4], dof[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    of[s] = *reinterpret_cast<const h8*>(orow + 32 * s + 8 * gr);
+    dof[s] = *reinterpret_cast<const h8*>(dorow + 32 * s + 8 * gr);
+  }
+  float dsum = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dsum = dsum + static_cast<float>(dof[s][i]) * static_cast<float>(of[s][i]);
+  }
+  dsum = column_sum(dsum);
+  if (gr == 0 && q_abs < T) delta[(static_cast<int64_t>(b) * NH + h) * T + q_abs] = dsum;
+}
+
+// LDS of the backward workgroups (the larger of the two kinds: dKdV's Q, Q^T, dO, dO^T tiles).
+constexpr int kBwdLdsBytes = 2 * (kBQ * kRStride + kD * kTStride) * 2 + 2 * kBQ * 4;
+
+__device__ __forceinline__ void attn_bwd_dq(
     const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
-    const uint8_t* key_valid, const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, float* __restrict__ delta, uint16_t* __restrict__ dq, int T,
-    int NH, int NKV, float scale, float scale_log2) {
-  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
-  __shared__ __align__(16) _Float16 Vs[kBK * kRStride];
-  __shared__ __align__(16) _Float16 Kt[kD * kTStride];
-  __shared__ __align__(16) uint8_t kflag[kBK];
-  const int nqb = (T + kBQ - 1) / kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.z);
+    const uint8_t* key_valid, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ delta, uint16_t* __restrict__ dq, int T, int NH, int NKV,
+    float scale, float scale_log2, int qb, unsigned char* smem) {
+  _Float16* Ks = reinterpret_cast<_Float16*>(smem);
+  _Float16* Vs = Ks + kBK * kRStride;
+  _Float16* Kt = Vs + kBK * kRStride;
+  uint8_t* kflag = reinterpret_cast<uint8_t*>(Kt + kD * kTStride);
   const int h = blockIdx.x, b = blockIdx.y;
   const int g = h / (NH / NKV);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
@@ -329,7 +364,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
   const int qc = min(q_abs, T - 1);
   const int64_t HD = static_cast<int64_t>(NH) * kD;
   const uint16_t* qrow = q + ((static_cast<int64_t>(b) * NH + h) * T + qc) * kD;
-  const uint16_t* orow = out + (static_cast<int64_t>(b) * T + qc) * HD + h * kD;
   const uint16_t* dorow = dout + (static_cast<int64_t>(b) * T + qc) * HD + h * kD;
   const uint16_t* kbase = k + (static_cast<int64_t>(b) * NKV + g) * T * kD;
   const uint16_t* vbase = v + (static_cast<int64_t>(b) * NKV + g) * T * kD;
@@ -337,20 +371,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
   const bool has_valid = valid != nullptr;
 
   h8 qf[4], dof[4];
-  float dsum = 0.f;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     qf[s] = *reinterpret_cast<const h8*>(qrow + 32 * s + 8 * gr);
     dof[s] = *reinterpret_cast<const h8*>(dorow + 32 * s + 8 * gr);
-    const h8 of = *reinterpret_cast<const h8*>(orow + 32 * s + 8 * gr);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dsum = dsum + static_cast<float>(dof[s][i]) * static_cast<float>(of[i]);
   }
-  dsum = column_sum(dsum);
+  const float dsum = delta[(static_cast<int64_t>(b) * NH + h) * T + qc];
   const float lse_q = lse[(static_cast<int64_t>(b) * NH + h) * T + qc];
   const float lse2 = lse_q * kLog2e;  // +inf: no visible key, every p = 0
-  if (gr == 0 && q_abs < T) delta[(static_cast<int64_t>(b) * NH + h) * T + q_abs] = dsum;
 
   f4 acc[8];
 #pragma unroll
@@ -412,17 +440,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
   }
 }
 
-__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
+__device__ __forceinline__ void attn_bwd_dkdv(
     const uint16_t* q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ key_valid, const uint16_t* dout, const float* lse,
     const float* delta, float* __restrict__ dk_part, float* __restrict__ dv_part,
-    int T, int NH, int NKV, float scale, float scale_log2) {
-  __shared__ __align__(16) _Float16 Qs[kBQ * kRStride];
-  __shared__ __align__(16) _Float16 Qt[kD * kTStride];
-  __shared__ __align__(16) _Float16 Ds[kBQ * kRStride];   // dO row-major
-  __shared__ __align__(16) _Float16 Dt[kD * kTStride];    // dO transposed
-  __shared__ float lse2_s[kBQ], delta_s[kBQ];
-  const int kb = static_cast<int>(blockIdx.z);  // block 0 sees the most query blocks
+    int T, int NH, int NKV, float scale, float scale_log2, int kb, unsigned char* smem) {
+  _Float16* Qs = reinterpret_cast<_Float16*>(smem);
+  _Float16* Qt = Qs + kBQ * kRStride;
+  _Float16* Ds = Qt + kD * kTStride;    // dO row-major
+  _Float16* Dt = Ds + kBQ * kRStride;   // dO transposed
+  float* lse2_s = reinterpret_cast<float*>(Dt + kD * kTStride);
+  float* delta_s = lse2_s + kBQ;
   const int h = blockIdx.x, b = blockIdx.y;
   const int g = h / (NH / NKV);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
@@ -492,15 +520,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
         sc = mfma32(qa[s], kf[s], sc);
         dp = mfma32(da[s], vf[s], dp);
       }
-      // C: rows = queries 16n + 4gr + i, column = this lane's key
+      // C: rows = queries 16n + 4gr + i, column = this lane's key.  The per-query values are
+      // read and every exponential computed unconditionally, the mask applied as a select:
+      // a conditional LDS read would put each of them behind its own branch and wait.
+      const f4 l2 = *reinterpret_cast<const f4*>(lse2_s + 16 * n + 4 * gr);
+      const f4 dl = *reinterpret_cast<const f4*>(delta_s + 16 * n + 4 * gr);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int qi = 16 * n + 4 * gr + i;
-        const int q_abs = qb * kBQ + qi;
-        const bool vis = !masked || (key_vis && key_abs <= q_abs && q_abs < T);
-        const float p = vis ? __builtin_amdgcn_exp2f(sc[i] * scale_log2 - lse2_s[qi]) : 0.f;
+        const int q_abs = qb * kBQ + 16 * n + 4 * gr + i;
+        // (bitwise, not short-circuit: no per-lane branch)
+        const bool vis = !masked | (key_vis & (key_abs <= q_abs) & (q_abs < T));
+        const float e = __builtin_amdgcn_exp2f(sc[i] * scale_log2 - l2[i]);
+        const float p = vis ? e : 0.f;
         pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p);
-        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - delta_s[qi]));
+        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - dl[i]));
       }
     }
     // dV^T += dO^T P, dK^T += Q^T dS  (contraction over the block's queries)
@@ -524,6 +557,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
     *reinterpret_cast<f4*>(dkp + 16 * t + 4 * gr) = dk[t] * scale;
     *reinterpret_cast<f4*>(dvp + 16 * t + 4 * gr) = dv[t];
   }
+}
+
+// Grid z = 2 * blocks: z even -> dKdV of key block z/2 (block 0 sees the most query blocks),
+// z odd -> dQ of query block nb - 1 - z/2 (the last sees the most key blocks).
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_kernel(
+    const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* key_valid,
+    const uint16_t* dout, const float* lse, const float* delta, uint16_t* dq, float* dk_part,
+    float* dv_part, int T, int NH, int NKV, float scale, float scale_log2) {
+  __shared__ __align__(16) unsigned char smem[kBwdLdsBytes];
+  const int nb = (T + kBQ - 1) / kBQ;
+  const int z = static_cast<int>(blockIdx.z);
+  if ((z & 1) == 0)
+    attn_bwd_dkdv(q, k, v, key_valid, dout, lse, delta, dk_part, dv_part, T, NH, NKV, scale,
+                  scale_log2, z >> 1, smem);
+  else
+    attn_bwd_dq(q, k, v, key_valid, dout, lse, delta, dq, T, NH, NKV, scale, scale_log2,
+                nb - 1 - (z >> 1), smem);
 }
 
 // dK, dV of each key/value head: the sum of its NH/NKV query heads' partials, in head order.
@@ -551,7 +601,7 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
 int check_shape(int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D, float scale) {
   if (B < 0 || T < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
   if (!(scale > 0.f)) return kInvalid;
-  if (B > 65535 || (T + kBQ - 1) / kBQ > 65535) return kInvalid;   // grid y, z limits
+  if (B > 65535 || 2 * ((T + kBQ - 1) / kBQ) > 65535) return kInvalid;   // grid y, z limits
   if (static_cast<int64_t>(B) * NH * T * kD >= (int64_t{1} << 40)) return kInvalid;
   return kOk;
 }
@@ -605,11 +655,13 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_bwd(
   float* dv_part = dk_part + part;
   const int nb = (T + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B), static_cast<unsigned>(nb));
-  int rc = launch_kernel(attn_bwd_dq_kernel, grid, dim3(kAttnThreads), st, q, k, v, key_valid,
-                         out, dout, lse, delta, dq, T, NH, NKV, scale, scale * kLog2e);
+  int rc = launch_kernel(attn_bwd_delta_kernel, grid, dim3(kAttnThreads), st, out, dout, delta,
+                         T, NH);
   if (rc != kOk) return rc;
-  rc = launch_kernel(attn_bwd_dkdv_kernel, grid, dim3(kAttnThreads), st, q, k, v, key_valid,
-                     dout, lse, delta, dk_part, dv_part, T, NH, NKV, scale, scale * kLog2e);
+  const dim3 grid2(static_cast<unsigned>(NH), static_cast<unsigned>(B),
+                   static_cast<unsigned>(2 * nb));
+  rc = launch_kernel(attn_bwd_kernel, grid2, dim3(kAttnThreads), st, q, k, v, key_valid, dout,
+                     lse, delta, dq, dk_part, dv_part, T, NH, NKV, scale, scale * kLog2e);
   if (rc != kOk) return rc;
   const int64_t n4 = static_cast<int64_t>(B) * NKV * per_head / 4;
   return launch_kernel(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
