@@ -88,7 +88,7 @@ __device__ __forceinline__ float column_sum(float v) {
 }
 
 // A [64 x 128] fp16 tile (64 rows of one head) is staged through registers: thread item
-// it (0, 1) covers rows 2rp, 2rp+1 (rp = item % 32) at dims 8dc..8dc+7 (dc = item / 32), so
+// it (0, 1) covers rows 2rp, 2rp+1 at dims 8dc..8dc+7 (tile_item), so
 // one pair of 16-byte row loads gives both the row-major LDS copy and, packed two rows to a
 // 4-byte word, the transposed one.  The loads of block i+1 are issued before block i is
 // computed and written to LDS after the next barrier, so their latency overlaps the MFMAs.
@@ -100,12 +100,25 @@ struct TileRegs {
   u32x4 a[2], b[2];
 };
 
+// Which row pair rp (0..31) and 8-dim chunk dc (0..15) thread item `it` covers: a
+// wavefront's item covers 16 row pairs x 4 chunks, lane bits (dc0, rp0, rp1, rp2, dc1, rp3).
+// Each 16-lane group of a 16-byte row-major store then writes 8 row pairs x 2 chunks, and the
+// 64 lanes of a 4-byte transposed store 16 pairs x 4 chunks, both on distinct LDS banks (lane
+// l covering pair l % 32 gave 2-way conflicts on both), and the global loads read 64
+// contiguous bytes per row.  Measured on MI355X: forward 20.0 -> 18.3 us, backward 39.8 ->
+// 36.7 us at the 2048-token shape.
+__device__ __forceinline__ void tile_item(int it, int& rp, int& dc) {
+  const int lane = threadIdx.x & 63, wi = (threadIdx.x >> 6) + 4 * it;
+  rp = 16 * (wi & 1) + ((lane >> 1) & 7) + 8 * (lane >> 5);
+  dc = 4 * (wi >> 1) + (lane & 1) + 2 * ((lane >> 4) & 1);
+}
+
 __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* src, int64_t stride,
                                           int r0, int nrows) {
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
-    const int item = threadIdx.x + kAttnThreads * it;
-    const int rp = item & 31, dc = item >> 5;
+    int rp, dc;
+    tile_item(it, rp, dc);
     const int t0 = min(r0 + 2 * rp, nrows - 1), t1 = min(r0 + 2 * rp + 1, nrows - 1);
     r.a[it] = *reinterpret_cast<const u32x4*>(src + t0 * stride + 8 * dc);
     r.b[it] = *reinterpret_cast<const u32x4*>(src + t1 * stride + 8 * dc);
@@ -141,8 +154,9 @@ template <bool RM, bool TR>
 __device__ __forceinline__ void store_tile(_Float16* rm, _Float16* tr, const TileRegs& r) {
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
-    const int item = threadIdx.x + kAttnThreads * it;
-    stage_pair<RM, TR>(rm, tr, r.a[it], r.b[it], item & 31, item >> 5);
+    int rp, dc;
+    tile_item(it, rp, dc);
+    stage_pair<RM, TR>(rm, tr, r.a[it], r.b[it], rp, dc);
   }
 }
 
