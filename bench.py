@@ -396,7 +396,8 @@ def time_attention(dev, steps, warmup):
         res[name] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
                      "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16_TFLOPS, 4)}
     res.update(shape={"batch": B, "seq": T, "q_heads": NH, "kv_heads": NKV, "head_dim": D},
-               note="causal, no padding; bwd = dQ + dK/dV-partial + GQA-reduce launches")
+               note="causal, no padding; bwd = D + (dQ | dK/dV-partial, one grid) + GQA-reduce "
+                    "launches")
     return res
 
 
@@ -588,6 +589,40 @@ def summarize_kernels(stats_csv, title, command, top=30):
     return "\n".join(out) + "\n"
 
 
+def summarize_step(trace_csv, title, command, n_layers=28, top=32):
+    """Markdown breakdown of one training step from a rocprofv3 --kernel-trace run of bench.py:
+    the launches between the first attention forward of one step and that of the next (steps
+    with a backward: those holding attn_bwd launches), per kernel, for the step whose GPU busy
+    time is the median."""
+    rows = sorted(_read_csv(trace_csv), key=lambda r: int(r["Start_Timestamp"]))
+    names = [_kernel_base(r["Kernel_Name"]) if "soupk" in r["Kernel_Name"]
+             else r["Kernel_Name"].split("(")[0][:90] for r in rows]
+    dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
+    firsts = [i for i, n in enumerate(names) if n == "attn_fwd_kernel"][::n_layers]
+    steps = []
+    for a, b in zip(firsts, firsts[1:]):
+        if any(names[i].startswith("attn_bwd") for i in range(a, b)):
+            steps.append((sum(dur[a:b]), a, b))
+    if not steps:
+        raise ValueError("no forward+backward step in the trace")
+    steps.sort()
+    busy, a, b = steps[len(steps) // 2]
+    per, calls = {}, {}
+    for i in range(a, b):
+        per[names[i]] = per.get(names[i], 0) + dur[i]
+        calls[names[i]] = calls.get(names[i], 0) + 1
+    out = [f"# {title}", "", "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```",
+           command, "```", "",
+           f"One forward+backward step (the median of {len(steps)} by GPU busy time): "
+           f"{busy / 1e6:.2f} ms of kernel time in {b - a} launches "
+           f"({busy / 1e3 / n_layers:.0f} us per layer).", "",
+           "| kernel | calls | us per call | us per step | share |", "|---|---:|---:|---:|---:|"]
+    for name, t in sorted(per.items(), key=lambda kv: -kv[1])[:top]:
+        out.append(f"| `{name}` | {calls[name]} | {t / 1e3 / calls[name]:.1f} | {t / 1e3:.0f} | "
+                   f"{100 * t / busy:.1f}% |")
+    return "\n".join(out) + "\n"
+
+
 def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     """Markdown table of HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
     WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the 1 GiB device
@@ -656,7 +691,13 @@ def main():
                     help="print the HBM traffic table of two rocprofv3 --pmc runs and exit (CPU)")
     ap.add_argument("--summarize-kernels", nargs=3, metavar=("STATS_CSV", "TITLE", "CMD"),
                     help="print every kernel of a rocprofv3 --stats run by total time (CPU)")
+    ap.add_argument("--summarize-step", nargs=3, metavar=("TRACE_CSV", "TITLE", "CMD"),
+                    help="print the per-kernel breakdown of one training step of a rocprofv3 "
+                         "--kernel-trace run (CPU)")
     args = ap.parse_args()
+    if args.summarize_step:
+        sys.stdout.write(summarize_step(*args.summarize_step))
+        return
     if args.summarize_kernels:
         sys.stdout.write(summarize_kernels(*args.summarize_kernels))
         return
@@ -669,7 +710,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the kernel set has no cross-GPU exchange and this "
-              "build runs no multi-GPU configuration (see DESIGN.md, 'Sharding').",
+              "build runs no multi-GPU configuration (a data-parallel run would all-reduce the "
+              "LoRA gradients once per step; it is not implemented here).",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
