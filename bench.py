@@ -803,7 +803,8 @@ def main():
         "gemm_selection": gemm_table or "hipBLASLt heuristic (--heuristic-gemms)",
         "step": step_t,
         "copy_peak_GBps": copy_gbps,
-        "copy_reference": "kernels[*].copy_us: a plain 16-byte non-temporal device copy "
+        "copy_reference": "kernels[*].copy_us: a plain 16-byte streaming device copy "
+                          "(one chunk per thread, non-temporal load, nt|sc1 store) "
                           "(soupk_bench_copy) moving the kernel's algorithmic bytes, half read "
                           "and half written, timed the same way; copy_over_kernel = copy_us / "
                           "us_mean",

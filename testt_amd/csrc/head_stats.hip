@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
       const float F = __builtin_amdgcn_exp2f(__builtin_fmaf(mk, kLog2e, fbase));
       __builtin_amdgcn_raw_buffer_store_b128(grad_from_e(w[k], F, c == tc ? thit : -1, gt),
                                              rsrc, lane_off + k * kChunkStride, 0,
-                                             kAuxNonTemporal);
+                                             kAuxStream);
     }
     __builtin_amdgcn_sched_barrier(0);
   }

@@ -45,14 +45,12 @@ __device__ __forceinline__ u32x4 nf4_expand_dword(uint32_t w, float scale,
 // straddles two blocks, and a tile spans whole blocks).  One tile per workgroup; the packed loads are issued
 // unconditionally (indices past the end clamped to the last dword, results dropped), because a
 // predicated load makes the compiler wait on it before issuing the next.
-// Cache policy of the packed codes and the fp16 output (1 = non-temporal: each is touched once).
+// Cache policy of the packed codes (1 = non-temporal: touched once); the fp16 output is written
+// with streaming stores (StreamOut: nt | sc1).
 #ifndef SOUPK_NF4_NT_LD
 #define SOUPK_NF4_NT_LD 1
 #endif
-#ifndef SOUPK_NF4_NT_ST
-#define SOUPK_NF4_NT_ST 1
-#endif
-constexpr bool kNf4NtLd = SOUPK_NF4_NT_LD != 0, kNf4NtSt = SOUPK_NF4_NT_ST != 0;
+constexpr bool kNf4NtLd = SOUPK_NF4_NT_LD != 0;
 
 // One tile (256 threads x kNf4Dwords dwords, from dword d0) of one weight.
 __device__ __forceinline__ void nf4_unpack_tile(
@@ -79,12 +77,14 @@ __device__ __forceinline__ void nf4_unpack_tile(
     }
   }
   __syncthreads();
+  // The tile's stores: dword d at byte 16 (d - d0) of a descriptor from d0 to the end of the
+  // output (dwords past the end fall outside it and are dropped).
+  const StreamOut dst(out + d0, static_cast<uint64_t>(n_dwords - d0) * 16u);
 #pragma unroll
   for (int k = 0; k < kNf4Dwords; ++k) {
-    const int64_t d = d0 + k * kNf4Threads + threadIdx.x;
-    const float s = scale[(k * kNf4Threads + threadIdx.x) >> dword_block_shift];
-    const u32x4 v = nf4_expand_dword(w[k], s, pair);
-    if (d < n_dwords) st<kNf4NtSt>(out + d, v);
+    const int i = k * kNf4Threads + threadIdx.x;
+    const u32x4 v = nf4_expand_dword(w[k], scale[i >> dword_block_shift], pair);
+    dst.store(static_cast<uint32_t>(i) * 16u, v);
   }
 }
 

@@ -37,21 +37,26 @@ constexpr int kWprBwd = SOUPK_NORM_WPR_BWD;
 #ifndef SOUPK_NORM_NT_LD
 #define SOUPK_NORM_NT_LD 1
 #endif
-#ifndef SOUPK_NORM_NT_ST
-#define SOUPK_NORM_NT_ST 1
-#endif
 // Row streams (x, delta, s, dy, dypad, ds in; s, y, ypad, dx, ddelta out) are touched once per
-// launch: non-temporal (1).  The weight, read by every row, stays cached.  (Cached row loads
-// made the backward pass 2% faster on MI355X but the RoPE forward kernel that follows it in a
-// training step 10% slower.)
-constexpr bool kNormNtLd = SOUPK_NORM_NT_LD != 0, kNormNtSt = SOUPK_NORM_NT_ST != 0;
+// launch: non-temporal loads (1) and streaming stores (StreamOut: nt | sc1).  The weight, read
+// by every row, stays cached.  (Cached row loads made the backward pass 2% faster on MI355X but
+// the RoPE forward kernel that follows it in a training step 10% slower.)
+constexpr bool kNormNtLd = SOUPK_NORM_NT_LD != 0;
 
 __device__ __forceinline__ f32x4 load_h4(const uint16_t* p) {
   const u32x2 w = ld<kNormNtLd>(reinterpret_cast<const u32x2*>(p));
   return f32x4{lo_h(w.x), hi_h(w.x), lo_h(w.y), hi_h(w.y)};
 }
-__device__ __forceinline__ void store_h4(uint16_t* p, f32x4 v) {
-  st<kNormNtSt>(reinterpret_cast<u32x2*>(p), u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)});
+__device__ __forceinline__ u32x2 pack_h4(f32x4 v) {
+  return u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
+}
+// A value loaded at a wave-uniform address, moved to scalar registers (a buffer descriptor
+// built from it then needs no per-lane loop).
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 
@@ -79,8 +84,8 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
     const int64_t p =
         (static_cast<int64_t>(blockIdx.x) - row_blocks) * (kRowsPerBlock * WPR) + wave;
     if (p >= pad_rows || pad_inv[p] >= 0) return;
-    f32x4* dst = reinterpret_cast<f32x4*>(ypad + p * H);
-    for (int c = lane; c < nch; c += kWave) st<kNormNtSt>(dst + c, zero);
+    const StreamOut dst(ypad + p * H, static_cast<uint64_t>(H) * 4u);
+    for (int c = lane; c < nch; c += kWave) dst.store(16u * c, zero);
     return;
   }
   const int rib = wave / WPR, sub = wave % WPR;  // row in block, wave within the row
@@ -99,19 +104,20 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
   }
   int64_t dest = -1;
   if (ypad != nullptr) {
-    dest = pad_idx[row];
+    dest = uniform_i64(pad_idx[row]);  // (row is the wave's: the destination is wave-uniform)
     if (dest < 0 || dest >= pad_rows) dest = -1;
   }
 #pragma unroll
   for (int j = 0; j < CPL; ++j)
     if ((j * WPR + sub) * kWave + lane >= nch) v[j] = zero;
   if (delta != nullptr) {
-    f32x4* sr = reinterpret_cast<f32x4*>(s_out + row * H);
+    // (chunks past the row's end fall outside the row's descriptor: their stores are dropped)
+    const StreamOut sr(s_out + row * H, static_cast<uint64_t>(H) * 4u);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = (j * WPR + sub) * kWave + lane;
       v[j] = v[j] + d[j];
-      if (live && c < nch) st<kNormNtSt>(sr + c, v[j]);
+      if (live) sr.store(16u * c, v[j]);
     }
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -131,16 +137,14 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
   }
   if (!live) return;
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-  uint16_t* yr = y + row * H;
-  f32x4* pr = dest >= 0 ? reinterpret_cast<f32x4*>(ypad + dest * H) : nullptr;
+  const StreamOut yr(y + row * H, static_cast<uint64_t>(H) * 2u);
+  const StreamOut pr(ypad + (dest >= 0 ? dest : 0) * H, static_cast<uint64_t>(H) * 4u);
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = (j * WPR + sub) * kWave + lane;
-    if (c < nch) {
-      const f32x4 o = (v[j] * rstd) * wv[j];
-      store_h4(yr + 4 * c, o);
-      if (pr != nullptr) st<kNormNtSt>(pr + c, o);
-    }
+    const f32x4 o = (v[j] * rstd) * wv[j];
+    yr.store(8u * c, pack_h4(o));
+    if (dest >= 0) pr.store(16u * c, o);
   }
   if (sub == 0 && lane == 0) rstd_out[row] = rstd;
 }
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kerne
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   int64_t src = -1;
   if (dypad != nullptr) {
-    src = pad_idx[row];
+    src = uniform_i64(pad_idx[row]);  // (row is the wave's: the source is wave-uniform)
     if (src < 0 || src >= pad_rows) src = -1;
   }
   const f32x4* sr = reinterpret_cast<const f32x4*>(s + row * H);
@@ -198,17 +202,17 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kerne
   }
   if (!live) return;
   const float proj = dot / static_cast<float>(H);
-  f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * H);
-  uint16_t* ddr = ddelta != nullptr ? ddelta + row * H : nullptr;
+  // (chunks past the row's end fall outside the rows' descriptors: their stores are dropped)
+  const StreamOut dxr(dx + row * H, static_cast<uint64_t>(H) * 4u);
+  const StreamOut ddr(ddelta != nullptr ? static_cast<const void*>(ddelta + row * H) : dx,
+                      static_cast<uint64_t>(H) * 2u);
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = (j * WPR + sub) * kWave + lane;
-    if (c < nch) {
-      f32x4 o = (g[j] - n[j] * proj) * rstd;
-      if (dsr != nullptr) o = o + dd[j];
-      st<kNormNtSt>(dxr + c, o);
-      if (ddr != nullptr) store_h4(ddr + 4 * c, o);
-    }
+    f32x4 o = (g[j] - n[j] * proj) * rstd;
+    if (dsr != nullptr) o = o + dd[j];
+    dxr.store(16u * c, o);
+    if (ddelta != nullptr) ddr.store(8u * c, pack_h4(o));
   }
 }
 
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(kGenThreads) void rmsnorm_fwd_generic_kernel(
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
   int64_t dest = -1;
   if (ypad != nullptr) {
-    dest = pad_idx[row];
+    dest = uniform_i64(pad_idx[row]);  // (row is the wave's: the destination is wave-uniform)
     if (dest < 0 || dest >= pad_rows) dest = -1;
   }
   for (int c = threadIdx.x; c < H; c += kGenThreads) {
@@ -275,7 +279,7 @@ __global__ __launch_bounds__(kGenThreads) void rmsnorm_bwd_generic_kernel(
   if (row >= rows) return;
   int64_t src = -1;
   if (dypad != nullptr) {
-    src = pad_idx[row];
+    src = uniform_i64(pad_idx[row]);  // (row is the wave's: the source is wave-uniform)
     if (src < 0 || src >= pad_rows) src = -1;
   }
   const float rstd = rstd_in[row];

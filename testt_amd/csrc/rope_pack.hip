@@ -18,6 +18,8 @@
 // after the token workgroups write zeros at the padded positions that no token maps to
 // (pos_inv[p] < 0), replacing the three torch.zeros memsets of the reference.
 
+#include <type_traits>
+
 #include "soupk_common.hpp"
 #include "fastdiv.hpp"
 
@@ -25,25 +27,20 @@ namespace soupk {
 namespace {
 
 constexpr int kRopeThreads = 256;
-// Cache policy per direction and access (1 = non-temporal), chosen by measurement on MI355X
-// at 2048 tokens: the forward pass is fastest with cached loads and non-temporal stores (5.9 us
-// against 6.7 with both non-temporal and 6.4 with both cached, which also slows the backward
-// pass that follows), the backward pass with non-temporal ones.  The cos/sin tables, shared by
-// every token at a position, are always read cached.
+// Cache policy of the loads per direction (1 = non-temporal), chosen by measurement on MI355X
+// at 2048 tokens: the forward pass is fastest with cached loads (5.9 us against 6.7 with
+// non-temporal ones; cached stores were slower still and also slowed the backward pass that
+// follows), the backward pass with non-temporal ones.  Results are written with streaming
+// stores (StreamOut: nt | sc1).  The cos/sin tables, shared by every token at a position, are
+// always read cached.
 #ifndef SOUPK_ROPE_NT_FWD_LD
 #define SOUPK_ROPE_NT_FWD_LD 0
-#endif
-#ifndef SOUPK_ROPE_NT_FWD_ST
-#define SOUPK_ROPE_NT_FWD_ST 1
 #endif
 #ifndef SOUPK_ROPE_NT_BWD_LD
 #define SOUPK_ROPE_NT_BWD_LD 1
 #endif
-#ifndef SOUPK_ROPE_NT_BWD_ST
-#define SOUPK_ROPE_NT_BWD_ST 1
-#endif
-constexpr bool kFwdNtLd = SOUPK_ROPE_NT_FWD_LD != 0, kFwdNtSt = SOUPK_ROPE_NT_FWD_ST != 0;
-constexpr bool kBwdNtLd = SOUPK_ROPE_NT_BWD_LD != 0, kBwdNtSt = SOUPK_ROPE_NT_BWD_ST != 0;
+constexpr bool kFwdNtLd = SOUPK_ROPE_NT_FWD_LD != 0;
+constexpr bool kBwdNtLd = SOUPK_ROPE_NT_BWD_LD != 0;
 
 struct RopeDims {
   int B, T, NH, NKV;
@@ -73,12 +70,44 @@ __device__ __forceinline__ void load8_h(const uint16_t* p, float* v) {
   v[0] = lo_h(w.x); v[1] = hi_h(w.x); v[2] = lo_h(w.y); v[3] = hi_h(w.y);
   v[4] = lo_h(w.z); v[5] = hi_h(w.z); v[6] = lo_h(w.w); v[7] = hi_h(w.w);
 }
-template <bool NT>
-__device__ __forceinline__ void store8_h(uint16_t* p, const float* v) {
-  st<NT>(reinterpret_cast<u32x4*>(p),
-              u32x4{pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
-                    pack_h2(v[6], v[7])});
+__device__ __forceinline__ u32x4 pack8_h(const float* v) {
+  return u32x4{pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
+               pack_h2(v[6], v[7])};
 }
+// Streaming stores into q, k, v ([B, heads, T, D] fp16 each) through one descriptor per tensor
+// over the whole tensor (the host keeps each below 2^32 bytes).  A lane picks its tensor with a
+// branch, never a per-lane choice of descriptor (that would not be wave-uniform).
+struct PackedOut {
+  StreamOut q, k, v;
+  int NH, NKV, T;
+  template <int D>
+  __device__ __forceinline__ PackedOut(uint16_t* q_, uint16_t* k_, uint16_t* v_,
+                                       const RopeDims& dm, std::integral_constant<int, D>)
+      : q(q_, static_cast<uint64_t>(dm.B) * dm.NH * dm.T * D * 2u),
+        k(k_, static_cast<uint64_t>(dm.B) * dm.NKV * dm.T * D * 2u),
+        v(v_, static_cast<uint64_t>(dm.B) * dm.NKV * dm.T * D * 2u),
+        NH(dm.NH), NKV(dm.NKV), T(dm.T) {}
+  // Stores a (first half) and bh (second half) of the 8-dim slice c of head h at (b, t).
+  template <int D>
+  __device__ __forceinline__ void store(int h, int b, int t, int c, u32x4 a, u32x4 bh) const {
+    constexpr uint32_t kHalfBytes = D;  // D/2 fp16
+    if (h < NH) {
+      const uint32_t off = ((static_cast<uint32_t>(b) * NH + h) * T + t) * (2u * D) + 16u * c;
+      q.store(off, a);
+      q.store(off + kHalfBytes, bh);
+    } else if (h < NH + NKV) {
+      const uint32_t off =
+          ((static_cast<uint32_t>(b) * NKV + (h - NH)) * T + t) * (2u * D) + 16u * c;
+      k.store(off, a);
+      k.store(off + kHalfBytes, bh);
+    } else {
+      const uint32_t off =
+          ((static_cast<uint32_t>(b) * NKV + (h - NH - NKV)) * T + t) * (2u * D) + 16u * c;
+      v.store(off, a);
+      v.store(off + kHalfBytes, bh);
+    }
+  }
+};
 // The cos/sin rows of the tokens a workgroup touches are staged once in LDS (per token 2*D fp32:
 // cos then sin), instead of every thread reading its 4 x 32 bytes of them from L1/L2.  A
 // workgroup's 256 items span at most kRopeMaxTok tokens (the host checks items per token).
@@ -132,16 +161,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     const int h = it / CPH, c = it % CPH;
     int b, t;
     split_pos(p, dm, b, t);
-    uint16_t* base;
-    if (h < dm.NH)
-      base = q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D;
-    else if (h < dm.NH + dm.NKV)
-      base = k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
-    else
-      base = v + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH - dm.NKV)) * dm.T + t) * D;
     const u32x4 z = {0u, 0u, 0u, 0u};
-    st<kFwdNtSt>(reinterpret_cast<u32x4*>(base + 8 * c), z);
-    st<kFwdNtSt>(reinterpret_cast<u32x4*>(base + HALF + 8 * c), z);
+    PackedOut(q, k, v, dm, std::integral_constant<int, D>()).store<D>(h, b, t, c, z, z);
     return;
   }
   const uint32_t g0 = blockIdx.x * kRopeThreads;
@@ -197,22 +218,16 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     lds8(tr + HALF / 4 + 2 * c, c2);
     lds8(tr + D / 4 + 2 * c, s1);
     lds8(tr + D / 4 + HALF / 4 + 2 * c, s2);
-    float o1[8], o2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      o1[i] = x1[i] * c1[i] - x2[i] * s1[i];
-      o2[i] = x2[i] * c2[i] + x1[i] * s2[i];
+      const float r1 = x1[i] * c1[i] - x2[i] * s1[i];
+      const float r2 = x2[i] * c2[i] + x1[i] * s2[i];
+      x1[i] = r1;
+      x2[i] = r2;
     }
-    uint16_t* dst = is_q ? q + ((static_cast<int64_t>(b) * dm.NH + h) * dm.T + t) * D
-                         : k + ((static_cast<int64_t>(b) * dm.NKV + (h - dm.NH)) * dm.T + t) * D;
-    store8_h<kFwdNtSt>(dst + 8 * c, o1);
-    store8_h<kFwdNtSt>(dst + HALF + 8 * c, o2);
-  } else {
-    const int hv = h - dm.NH - dm.NKV;
-    uint16_t* dst = v + ((static_cast<int64_t>(b) * dm.NKV + hv) * dm.T + t) * D;
-    store8_h<kFwdNtSt>(dst + 8 * c, x1);
-    store8_h<kFwdNtSt>(dst + HALF + 8 * c, x2);
   }
+  PackedOut(q, k, v, dm, std::integral_constant<int, D>())
+      .store<D>(h, b, t, c, pack8_h(x1), pack8_h(x2));
 }
 
 template <int HALF>
@@ -257,7 +272,9 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
   const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
   __syncthreads();
   if (!active) return;
-  uint16_t* out = dqkv + static_cast<int64_t>(tok) * heads * D + h * D + 8 * c;
+  // Streaming stores through one descriptor over dqkv (the host keeps it below 2^32 bytes).
+  const StreamOut out(dqkv, static_cast<uint64_t>(rows) * heads * D * 2u);
+  const uint32_t off = (tok * static_cast<uint32_t>(heads) + h) * (2u * D) + 16u * c;
   if (!is_v) {
     const f32x4* tr = tab + (tok - tok0) * per;
     float c1[8], c2[8], s1[8], s2[8];
@@ -271,11 +288,11 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
       o1[i] = g1[i] * c1[i] + g2[i] * s2[i];
       o2[i] = g2[i] * c2[i] - g1[i] * s1[i];
     }
-    store8_h<kBwdNtSt>(out, o1);
-    store8_h<kBwdNtSt>(out + HALF, o2);
+    out.store(off, pack8_h(o1));
+    out.store(off + 2u * HALF, pack8_h(o2));
   } else {
-    store8_h<kBwdNtSt>(out, g1);
-    store8_h<kBwdNtSt>(out + HALF, g2);
+    out.store(off, pack8_h(g1));
+    out.store(off + 2u * HALF, pack8_h(g2));
   }
 }
 
@@ -417,7 +434,9 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
   const int heads = NH + 2 * NKV;
   const int lora_align = 16;
   // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens)
+  // (the stores address q, k and v with 32-bit byte offsets)
   const bool vec = half == 64 && heads * (half / 8) >= 18 && slots < (int64_t{1} << 31) &&
+                   slots * (NH > NKV ? NH : NKV) * D * 2 < (int64_t{1} << 32) &&
                    aligned(qkv, 16) &&
                    aligned(cos, 16) && aligned(sin, 16) && aligned(q, 16) && aligned(k, 16) &&
                    aligned(v, 16) && aligned(lora_q, lora_align) && aligned(lora_v, lora_align);
@@ -463,8 +482,10 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
   const int heads = NH + 2 * NKV;
   // (the vector kernel stages table row 0 for invalid positions, so it needs T >= 1)
   const int64_t slots = static_cast<int64_t>(B) * T;
+  // (the stores address dqkv with 32-bit byte offsets)
   const bool vec = half == 64 && heads * (half / 8) >= 18 && slots > 0 &&
-                   slots < (int64_t{1} << 31) && aligned(dq, 16) &&
+                   slots < (int64_t{1} << 31) && rows * heads * D * 2 < (int64_t{1} << 32) &&
+                   aligned(dq, 16) &&
                    aligned(dk, 16) && aligned(dv, 16) && aligned(cos, 16) && aligned(sin, 16) &&
                    aligned(dqkv, 16);
   if (vec) {

@@ -8,7 +8,8 @@
 // GEMM gives, with a different (still deterministic) summation order.
 //
 // Pure HBM streaming: each thread reads 4 consecutive floats of every partial (16-byte
-// non-temporal loads, all issued before the first add) and writes 4 fp16 (8 bytes).
+// non-temporal loads, all issued before the first add) and writes 4 fp16 (8 bytes, a streaming
+// store).
 
 #include "soupk_common.hpp"
 
@@ -21,7 +22,8 @@ constexpr int kMaxPartials = 16;
 template <int P>
 __global__ __launch_bounds__(kRedThreads) void sum_partials_kernel(
     const f32x4* __restrict__ parts, int64_t stride4, int64_t n4, u32x2* __restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kRedThreads + threadIdx.x;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kRedThreads;
+  const int64_t i = i0 + threadIdx.x;
   if (i >= n4) return;
   f32x4 v[P];
 #pragma unroll
@@ -29,7 +31,10 @@ __global__ __launch_bounds__(kRedThreads) void sum_partials_kernel(
   f32x4 s = v[0];
 #pragma unroll
   for (int p = 1; p < P; ++p) s = s + v[p];
-  st<true>(out + i, u32x2{pack_h2(s[0], s[1]), pack_h2(s[2], s[3])});
+  // Streaming store through a descriptor over the workgroup's slice of out.
+  const StreamOut dst(out + i0, static_cast<uint64_t>(n4 - i0) * 8u);
+  dst.store(static_cast<uint32_t>(threadIdx.x) * 8u,
+            u32x2{pack_h2(s[0], s[1]), pack_h2(s[2], s[3])});
 }
 
 // Any count of partials (up to kMaxPartials) and any n: one element per thread.

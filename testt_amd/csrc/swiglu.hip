@@ -50,15 +50,13 @@ __device__ __forceinline__ u32x2 silu_bwd_word(uint32_t dw, uint32_t gw, uint32_
   return u32x2{pack_h2(dg[0], dg[1]), pack_h2(du[0], du[1])};
 }
 
-// Cache policy of the streamed operands (1 = non-temporal: each is touched once per launch;
-// cached loads ran 15% slower on MI355X and slowed the kernels that follow).
+// Cache policy of the streamed loads (1 = non-temporal: each operand is touched once per
+// launch; cached loads ran 15% slower on MI355X and slowed the kernels that follow).  The
+// results are written with streaming stores (StreamOut: nt | sc1).
 #ifndef SOUPK_SWI_NT_LD
 #define SOUPK_SWI_NT_LD 1
 #endif
-#ifndef SOUPK_SWI_NT_ST
-#define SOUPK_SWI_NT_ST 1
-#endif
-constexpr bool kSwiNtLd = SOUPK_SWI_NT_LD != 0, kSwiNtSt = SOUPK_SWI_NT_ST != 0;
+constexpr bool kSwiNtLd = SOUPK_SWI_NT_LD != 0;
 
 // One workgroup = one tile of kSwiThreads * kSwiUnroll chunks; chunk k*kSwiThreads + tid of the
 // tile per thread, so each wave load/store instruction covers 1 KiB contiguous.  All loads are
@@ -67,7 +65,11 @@ constexpr bool kSwiNtLd = SOUPK_SWI_NT_LD != 0, kSwiNtSt = SOUPK_SWI_NT_ST != 0;
 __global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec_kernel(
     const u32x4* __restrict__ gu, u32x4* __restrict__ act, uint32_t n_chunks, FastDiv row_of,
     uint32_t I_chunks) {
-  const uint32_t base = blockIdx.x * (kSwiThreads * kSwiUnroll) + threadIdx.x;
+  const uint32_t c0 = blockIdx.x * (kSwiThreads * kSwiUnroll);
+  const uint32_t base = c0 + threadIdx.x;
+  // Stores of the tile: chunk c at byte 16 (c - c0) of a descriptor from chunk c0 to the end of
+  // act (chunks past the end fall outside it and are dropped).
+  const StreamOut out(act + c0, static_cast<uint64_t>(n_chunks - c0) * 16u);
   u32x4 g[kSwiUnroll], u[kSwiUnroll];
 #pragma unroll
   for (int k = 0; k < kSwiUnroll; ++k) {
@@ -82,14 +84,19 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec_kernel(
     const uint32_t c = base + k * kSwiThreads;
     const u32x4 r = {silu_mul_word(g[k].x, u[k].x), silu_mul_word(g[k].y, u[k].y),
                      silu_mul_word(g[k].z, u[k].z), silu_mul_word(g[k].w, u[k].w)};
-    if (c < n_chunks) st<kSwiNtSt>(act + c, r);
+    out.store((c - c0) * 16u, r);
   }
 }
 
 __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec_kernel(
     const u32x4* __restrict__ dact, u32x4* __restrict__ gu, uint32_t n_chunks, FastDiv row_of,
     uint32_t I_chunks) {
-  const uint32_t base = blockIdx.x * (kSwiThreads * kSwiUnroll) + threadIdx.x;
+  const uint32_t c0 = blockIdx.x * (kSwiThreads * kSwiUnroll);
+  const uint32_t base = c0 + threadIdx.x;
+  // Stores of the tile relative to the tile's first gate chunk g0 (the host keeps the tile's
+  // span, under two rows of gate|up plus a tile, below 2^32 bytes).
+  const uint64_t g0 = static_cast<uint64_t>(c0) + static_cast<uint64_t>(row_of.div(c0)) * I_chunks;
+  const StreamOut out(gu + g0, (2ull * n_chunks - g0) * 16u);
   u32x4 d[kSwiUnroll], g[kSwiUnroll], u[kSwiUnroll];
   uint64_t gi[kSwiUnroll];
 #pragma unroll
@@ -107,9 +114,12 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec_kernel(
     const u32x2 r1 = silu_bwd_word(d[k].y, g[k].y, u[k].y);
     const u32x2 r2 = silu_bwd_word(d[k].z, g[k].z, u[k].z);
     const u32x2 r3 = silu_bwd_word(d[k].w, g[k].w, u[k].w);
+    // (a thread past the end holds the last chunk's indices: its store would overwrite that
+    // chunk's result in place, so it stores nothing)
     if (c < n_chunks) {
-      st<kSwiNtSt>(gu + gi[k], u32x4{r0.x, r1.x, r2.x, r3.x});
-      st<kSwiNtSt>(gu + gi[k] + I_chunks, u32x4{r0.y, r1.y, r2.y, r3.y});
+      const uint32_t off = static_cast<uint32_t>(gi[k] - g0) * 16u;
+      out.store(off, u32x4{r0.x, r1.x, r2.x, r3.x});
+      out.store(off + I_chunks * 16u, u32x4{r0.y, r1.y, r2.y, r3.y});
     }
   }
 }
@@ -176,7 +186,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_swiglu_bwd_inplace(
   if (n == 0) return kOk;
   if (!gu || !dact) return kInvalid;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && aligned16(gu) && aligned16(dact)) {
+  if (I % 8 == 0 && n / 8 < (int64_t{1} << 31) && I / 8 < (int64_t{1} << 26) && aligned16(gu) &&
+      aligned16(dact)) {
     const uint32_t n_chunks = static_cast<uint32_t>(n / 8);
     const uint32_t I_chunks = static_cast<uint32_t>(I / 8);
     return launch_kernel(swiglu_bwd_vec_kernel, dim3(vec_grid(n_chunks)), dim3(kSwiThreads), s,
