@@ -447,7 +447,7 @@ def time_step(dev, steps, warmup, n_layers=28):
 
 
 def copy_reference(cases, dev, reps=60, pool_mib=768):
-    """Mean duration of a plain non-temporal device copy (soupk_bench_copy) moving each kernel's
+    """Mean duration of a plain streaming device copy (soupk_bench_copy) moving each kernel's
     algorithmic byte count (half read, half written), timed like the kernels.  Every launch
     copies a different slice of two pool_mib pools, so more than 600 MB of other traffic lies
     between two uses of one slice and the Infinity Cache cannot serve them.  Returns

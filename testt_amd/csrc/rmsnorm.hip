@@ -5,8 +5,8 @@
 // The normalisation is transformers' Qwen2RMSNorm (modeling_qwen2.py:247-252):
 // w * (s * rsqrt(mean(s^2) + eps)), with the product (s * rstd) rounded before the weight.
 //
-// Mapping (gfx950): a row of H fp32 is H/4 float4 chunks, split over WPR wavefronts (2 forward,
-// 1 backward) owning alternate 64-chunk slices, so every load or store instruction of a wave
+// Mapping (gfx950): a row of H fp32 is H/4 float4 chunks, split over WPR wavefronts (2 in both
+// directions) owning alternate 64-chunk slices, so every load or store instruction of a wave
 // touches 1 KiB (fp32) or 512 B (fp16) of contiguous memory.  The row's values stay in registers
 // between the load, the wave64 reduction (DPP steps; combined across the row's waves in LDS) and
 // the stores.  In the forward pass two waves per row give 16 waves per CU at 2048 rows, which
@@ -25,12 +25,12 @@ namespace {
 #endif
 constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // rows per workgroup
 // Wavefronts per row on the vector path (measured on MI355X at 2048 x 1536: the forward pass is
-// 17% faster with two, the backward pass 3% faster with one).
+// 17% faster with two than with one; the backward pass, with streaming stores, 2% faster).
 #ifndef SOUPK_NORM_WPR_FWD
 #define SOUPK_NORM_WPR_FWD 2
 #endif
 #ifndef SOUPK_NORM_WPR_BWD
-#define SOUPK_NORM_WPR_BWD 1
+#define SOUPK_NORM_WPR_BWD 2
 #endif
 constexpr int kWprFwd = SOUPK_NORM_WPR_FWD;
 constexpr int kWprBwd = SOUPK_NORM_WPR_BWD;
