@@ -31,6 +31,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+import testt_amd  # noqa: E402
 from testt_amd import _ext, workloads  # noqa: E402
 
 PEAK_HBM_GBPS = 8000.0
@@ -244,18 +245,48 @@ class HipEvents:
         self.events = []
 
 
+class DeviceHold:
+    """Keeps the current stream busy with a device-side wait (torch.cuda._sleep: a one-thread
+    kernel spinning on the clock counter for a given number of cycles, so it always ends) while
+    the host queues the launches to be timed behind it.  The GPU then runs them back to back, as
+    in a training step, instead of at the host's launch rate (a ctypes launch with its event
+    pair costs the host about as long as the shorter kernels run, so each of them would start
+    on an idle GPU and the means would depend on the host's speed)."""
+
+    def __init__(self, dev):
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cycles = 5_000_000
+        e0.record()
+        torch.cuda._sleep(cycles)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        self.cycles_per_us = cycles / max(e0.elapsed_time(e1) * 1e3, 1.0)
+
+    def hold(self, us):
+        torch.cuda._sleep(int(min(us, 2e5) * self.cycles_per_us))
+
+
 def time_gpu(cases, steps, warmup, dev, lib=None):
     """Per-launch kernel durations: soupk_time_next_launch() makes each launch record a HIP
-    event pair with its own dispatch (hipExtLaunchKernelGGL), on the stream it runs on."""
+    event pair with its own dispatch (hipExtLaunchKernelGGL), on the stream it runs on.  The
+    timed launches are queued behind a DeviceHold that outlasts their enqueueing, so they run
+    back to back."""
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     arm = (lib if lib is not None else _ext.lib()).soupk_time_next_launch
     hip = HipEvents()
+    holder = DeviceHold(dev)
+    t0 = time.perf_counter()
     for w in range(warmup):
         for c in cases:
             c.launch(w, sh)
+    warm_us = (time.perf_counter() - t0) * 1e6 / max(warmup, 1)
     ev = [[(hip.new(), hip.new()) for _ in cases] for _ in range(steps)]
     torch.cuda.synchronize(dev)
+    # (the timed loop also arms the events: twice the warm-up's host time per step, plus 2 ms)
+    holder.hold(2.0 * warm_us * steps + 2000.0)
     t0 = time.perf_counter()
     for s in range(steps):
         for j, c in enumerate(cases):
@@ -264,11 +295,12 @@ def time_gpu(cases, steps, warmup, dev, lib=None):
             c.launch(s, sh)
     host_enqueue = time.perf_counter() - t0
     torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
     for j, c in enumerate(cases):
         c.times = [hip.elapsed_us(*ev[s][j]) for s in range(steps)]
+    # GPU time from the first timed launch's start to the last one's end
+    span = hip.elapsed_us(ev[0][0][0], ev[-1][-1][1]) * 1e-6
     hip.close()
-    return host_enqueue, wall
+    return host_enqueue, span
 
 
 def time_layer(dev, steps, warmup):
@@ -310,7 +342,8 @@ def time_layer(dev, steps, warmup):
     out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
                note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs in fp16, "
                     "every other op (attention included) a soupk kernel (testt_amd/layer.py); "
-                    "fwd_bwd_us / fwd_us: eager loop, bounded by the host's enqueue rate; "
+                    "fwd_bwd_us / fwd_us: eager loop (backward on the calling thread, as "
+                    "testt_amd.apply() sets it); "
                     "graph_*: the same step captured once in a HIP graph and replayed (the "
                     "layer's GPU time; replays match the eager step bit for bit, "
                     "tests/test_gpu_layer_graph.py)")
@@ -441,14 +474,17 @@ def time_step(dev, steps, warmup, n_layers=28):
     out.update(tokens=B * T, batch=B, seq=T, layers=n_layers,
                tokens_per_s=round(B * T / (out["fwd_bwd_ms"] * 1e-3), 1),
                note="synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; "
-                    "hipBLASLt GEMMs in fp16, every other op (attention included) a soupk kernel")
+                    "hipBLASLt GEMMs in fp16, every other op (attention included) a soupk kernel; "
+                    "backward on the calling thread (testt_amd.configure_backward, as apply() "
+                    "sets it)")
     del m
     return out
 
 
 def copy_reference(cases, dev, reps=60, pool_mib=768):
     """Mean duration of a plain streaming device copy (soupk_bench_copy) moving each kernel's
-    algorithmic byte count (half read, half written), timed like the kernels.  Every launch
+    algorithmic byte count (half read, half written), timed like the kernels (back to back,
+    behind a DeviceHold).  Every launch
     copies a different slice of two pool_mib pools, so more than 600 MB of other traffic lies
     between two uses of one slice and the Infinity Cache cannot serve them.  Returns
     {case name: us}."""
@@ -458,11 +494,14 @@ def copy_reference(cases, dev, reps=60, pool_mib=768):
     dst = torch.empty(pool, dtype=torch.uint8, device=dev)
     sh = torch.cuda.current_stream(dev).cuda_stream
     hip = HipEvents()
+    holder = DeviceHold(dev)
     out = {}
     for c in cases:
         size = (c.nbytes // 2) // 4096 * 4096
         slots = max(1, pool // size)
         evs = [(hip.new(), hip.new()) for _ in range(reps)]
+        torch.cuda.synchronize(dev)
+        holder.hold(60.0 * (reps + 10) + 2000.0)   # (launches run back to back, as the kernels')
         for r in range(reps + 10):
             off = (r % slots) * size
             if r >= 10:
@@ -720,6 +759,8 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _ext.lib()
+    # Backward on this thread, as testt_amd.apply() sets it for the training thread.
+    testt_amd.configure_backward()
     gemm_table = None
     if not args.heuristic_gemms:
         from testt_amd import gemm_tuning
@@ -732,7 +773,7 @@ def main():
     cases = build_cases(dev)
     torch.cuda.synchronize(dev)
     log(f"timing {len(cases)} kernels: warmup {args.warmup}, steps {args.steps}")
-    host_enqueue, wall = time_gpu(cases, args.steps, args.warmup, dev)
+    host_enqueue, span = time_gpu(cases, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
     copy_us = copy_reference(cases, dev)
     attn_t = None
@@ -809,8 +850,9 @@ def main():
                           "and half written, timed the same way; copy_over_kernel = copy_us / "
                           "us_mean",
         "timing": "per-launch HIP events recorded by the kernel dispatch itself "
-                  "(soupk_time_next_launch / hipExtLaunchKernelGGL), mean over steps",
-        "step_wall_ms": round(wall * 1e3 / args.steps, 4),
+                  "(soupk_time_next_launch / hipExtLaunchKernelGGL), mean over steps; the "
+                  "launches run back to back, queued behind a device-side wait (DeviceHold)",
+        "step_gpu_span_ms": round(span * 1e3 / args.steps, 4),
         "host_enqueue_ms": round(host_enqueue * 1e3 / args.steps, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,

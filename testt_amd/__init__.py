@@ -16,7 +16,23 @@ include/soupk.h (`python -m testt_amd.build_ext`) and called through ctypes with
 current stream.  There is no CPU or Triton path.
 """
 
-__all__ = ["apply", "nf4", "rmsnorm", "rope", "attention", "mlp", "head", "warmup"]
+__all__ = ["apply", "configure_backward", "nf4", "rmsnorm", "rope", "attention", "mlp", "head",
+           "warmup"]
+
+# One process drives one GPU here, so autograd's per-device worker thread adds no parallelism,
+# and handing every backward to it costs host time: on the MI355X boxes one decoder layer's
+# eager forward + backward went from 823 to 682 us of wall time (host-bound to GPU-bound) with
+# backward run on the calling thread.  apply() makes that the calling thread's setting.
+SINGLE_THREADED_BACKWARD = True
+
+
+def configure_backward(single_threaded=SINGLE_THREADED_BACKWARD):
+    """Run autograd's backward passes started from this thread on this thread
+    (torch.autograd.set_multithreading_enabled, a thread-local setting) instead of on the
+    device's worker thread.  Results are the same either way."""
+    import torch
+
+    torch.autograd.set_multithreading_enabled(not single_threaded)
 
 
 def apply():
@@ -26,12 +42,14 @@ def apply():
     compute_loss, Soup rewind, Soup setup); that module and model.py stay the reference's own
     and import the kernel modules by name, so applying the reference's patches after placing
     these modules where solution/ keeps its kernels is the integration.  Here apply() loads the
-    kernel library (loudly, if it is missing) and then runs the trainer patches when a
+    kernel library (loudly, if it is missing), runs the calling thread's backward passes on
+    that thread (configure_backward) and then runs the trainer patches when a
     `trainer_patch` module sits beside this package, printing, as the reference does, any patch
     that cannot be installed."""
     from . import _ext
 
     _ext.lib()
+    configure_backward()
     try:
         from . import trainer_patch  # noqa: F401  (present only in an integrated tree)
     except ImportError as exc:
