@@ -614,10 +614,16 @@ def summarize_kernels(stats_csv, title, command, top=30):
     """Markdown table of every kernel of a rocprofv3 --kernel-trace --stats run, by total time
     (hipBLASLt, torch and soupk kernels alike)."""
     rows = sorted(_read_csv(stats_csv), key=lambda r: -float(r["TotalDurationNs"]))
+    # DeviceHold's waits (torch.cuda._sleep's spin kernel) are not work: listed apart
+    holds = [r for r in rows if "spin_kernel" in r["Name"]]
+    rows = [r for r in rows if "spin_kernel" not in r["Name"]]
     total = sum(float(r["TotalDurationNs"]) for r in rows)
     out = [f"# {title}", "", "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```",
            command, "```", "", f"All kernels: {total / 1e6:.2f} ms in "
-           f"{sum(int(r['Calls']) for r in rows)} launches.", "",
+           f"{sum(int(r['Calls']) for r in rows)} launches"
+           + (f", besides {sum(int(r['Calls']) for r in holds)} device-side waits "
+              f"(DeviceHold, {sum(float(r['TotalDurationNs']) for r in holds) / 1e6:.1f} ms)"
+              if holds else "") + ".", "",
            "| kernel | calls | avg us | total ms | share |", "|---|---:|---:|---:|---:|"]
     for r in rows[:top]:
         name = r["Name"]

@@ -57,3 +57,33 @@ def test_head_stats_row_losses():
     means, tokens = st.row_losses()
     assert tokens == [2, 0, 3]
     assert means == [1.5, 0.0, 1.5]
+
+
+def test_configure_backward_is_thread_local():
+    """configure_backward() (run by testt_amd.apply()) turns off autograd's device worker
+    thread for backward passes started from the calling thread only, and gradients are the
+    same either way."""
+    import threading
+
+    import testt_amd
+
+    seen = {}
+
+    def worker():
+        testt_amd.configure_backward()
+        seen["worker"] = torch._C._is_multithreading_enabled()
+        x = torch.randn(5, 3, generator=torch.Generator().manual_seed(1), requires_grad=True)
+        (x.sin() * x).sum().backward()
+        seen["grad"] = x.grad.clone()
+        testt_amd.configure_backward(single_threaded=False)
+        seen["restored"] = torch._C._is_multithreading_enabled()
+
+    before = torch._C._is_multithreading_enabled()
+    th = threading.Thread(target=worker)
+    th.start()
+    th.join()
+    assert seen["worker"] is False and seen["restored"] is True
+    assert torch._C._is_multithreading_enabled() == before     # this thread is untouched
+    x = torch.randn(5, 3, generator=torch.Generator().manual_seed(1), requires_grad=True)
+    (x.sin() * x).sum().backward()
+    assert torch.equal(x.grad, seen["grad"])
