@@ -73,8 +73,12 @@ __device__ __forceinline__ h8 to_h8(f4 a, f4 b) {
 // Loop steps and tiles are processed kBatch at a time: the loads of a batch (at clamped
 // indices, so unconditional) are all issued before its first MFMA, and the MFMAs and stores
 // past the end of the range are skipped (a wavefront-uniform test).  One step at a time, each
-// MFMA waited for its own loads.
-constexpr int kBatch = 4;
+// MFMA waited for its own loads; batches of 6 measured the same as 4 on MI355X at the step
+// shape, and of 8 slower (forward 16.9 against 15.3 us); 12 spills.
+#ifndef SOUPK_LORA_BATCH
+#define SOUPK_LORA_BATCH 4
+#endif
+constexpr int kBatch = SOUPK_LORA_BATCH;
 
 // Split of the output tiles over the workgroups of one row block (grid.y column parts): each
 // part recomputes the row block's rank-r product (cheap: 2r columns) and writes its share of
