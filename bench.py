@@ -717,6 +717,8 @@ def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     from collections import defaultdict
     bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
     algo = {v["kernel"]: v["bytes"] for v in bench["kernels"].values()}
+    algo.update({v["kernel"]: v["bytes"]
+                 for v in bench.get("kernels_beyond_set", {}).values()})
     fetch, write = _read_csv(fetch_csv), _read_csv(write_csv)
     gib_kib = float(1 << 20)
     copies = {r["Dispatch_Id"] for r in write if "copyBuffer" in r["Kernel_Name"]
