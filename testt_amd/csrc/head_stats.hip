@@ -245,8 +245,10 @@ constexpr float kLift = 15.f;
 // its inputs).  When it raises the running max, the sums are rescaled and the chunk's raw
 // logits are kept in `best` (with its number in kbest) for the argmax, which is resolved once at
 // the end; then the chunk's registers are overwritten with its lifted exponentials.
-__device__ __forceinline__ void absorb_keep(RowStats& st, int& kbest, u32x4& best, u32x4& w,
-                                            int k) {
+// `shift` (kLift - m * log2 e) and `m16` (m as fp16, exact: m is one of the logits) follow the
+// running max, updated only when a chunk raises it, not recomputed for every chunk.
+__device__ __forceinline__ void absorb_keep(RowStats& st, float& shift, f16& m16, int& kbest,
+                                            u32x4& best, u32x4& w, int k) {
   const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
   const f16x2 m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
                                                  __builtin_elementwise_maximum(c, d));
@@ -257,10 +259,11 @@ __device__ __forceinline__ void absorb_keep(RowStats& st, int& kbest, u32x4& bes
     st.se = st.se * f;
     st.sd = st.sd * f;
     st.m = bm;
+    shift = kLift - bm * kLog2e;
+    m16 = static_cast<f16>(bm);
     kbest = k;
     best = w;
   }
-  const float shift = kLift - st.m * kLog2e;
   const f16 h[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
   float e[8];
 #pragma unroll
@@ -333,6 +336,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   // per chunk on top of the row.
   const int32_t nvec = static_cast<int32_t>(sp.nvec), lead = static_cast<int32_t>(sp.lead);
   RowStats st = {-INFINITY, 0.f, 0.f, INT_MAX};
+  float run_shift = kLift - st.m * kLog2e;   // (+inf until a chunk sets the max)
+  f16 m16 = static_cast<f16>(-INFINITY);
   int kbest = -1;
   u32x4 best = {0u, 0u, 0u, 0u};
   // Load k + P is issued before chunk k is folded in, so each wave keeps P chunks in flight and
@@ -344,8 +349,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
       w[k + P] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + (k + P) * kChunkStride, 0,
                                                        kAuxNonTemporal);
     if (k * kHeadThreads + tid < nvec) {
-      absorb_keep(st, kbest, best, w[k], k);
-      chunk_max[k * kHeadThreads + tid] = static_cast<f16>(st.m);
+      absorb_keep(st, run_shift, m16, kbest, best, w[k], k);
+      chunk_max[k * kHeadThreads + tid] = m16;
     }
     __builtin_amdgcn_sched_barrier(0);
   }
