@@ -175,6 +175,16 @@ def test_unpack_groups_one_buffer():
         ref = np.concatenate([dequant_state(w) for w in group])
         assert np.array_equal(bits(stack), ref.view(np.int16))
         assert torch.equal(stack, nf4.unpack_concat(group, DEV))
+    # the second call runs the prepared launches; a replaced state must be seen by the next
+    again = nf4.unpack_groups(weights, DEV)
+    assert all(torch.equal(a, b) for a, b in zip(again, stacks))
+    st = weights[2][1].quant_state
+    st.absmax = torch.flip(st.absmax, [0]).contiguous()
+    st.offset = 0.25
+    third = nf4.unpack_groups(weights, DEV)
+    ref = np.concatenate([dequant_state(w) for w in weights[2]])
+    assert np.array_equal(bits(third[2]), ref.view(np.int16))
+    assert not torch.equal(third[2], stacks[2])
 
 
 def test_unpack_multi_rejects_invalid_arguments():

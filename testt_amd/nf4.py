@@ -93,17 +93,26 @@ def _f32(t):
     return t if t.dtype == torch.float32 and t.is_contiguous() else t.float().contiguous()
 
 
+def _plan_key(weight, device):
+    """What a cached plan of `weight` depends on: the addresses of its packed data and state
+    tensors and the offset object (None for an object that is not an NF4 weight)."""
+    state = _quant_state(weight)
+    try:
+        return (device, weight.data.data_ptr(), state.absmax.data_ptr(), state.code.data_ptr(),
+                state.state2.code.data_ptr(), state.state2.absmax.data_ptr(), id(state.offset))
+    except AttributeError:
+        return None
+
+
 def _plan(weight, device):
     """The kernel arguments of one weight on `device` (pointers into its quant state, converted
     tables kept alive), checked once and cached on the weight; None for a layout or device the
     kernel does not take.  The cache is keyed by the addresses of the state tensors, so a
     weight whose state is replaced is checked again."""
-    state = _quant_state(weight)
-    try:
-        key = (device, weight.data.data_ptr(), state.absmax.data_ptr(), state.code.data_ptr(),
-               state.state2.code.data_ptr(), state.state2.absmax.data_ptr(), id(state.offset))
-    except AttributeError:
+    key = _plan_key(weight, device)
+    if key is None:
         return None
+    state = _quant_state(weight)
     cached = getattr(weight, "_soupk_plan", None)
     if cached is not None and cached[0] == key:
         return cached[1]
@@ -213,10 +222,94 @@ def unpack_concat(weights, device):
 _GROUP_ALIGN = 256
 
 
+class _GroupPlan:
+    """unpack_groups' launches for one list of weight groups, prepared once: the buffer size,
+    each stack's place in it, and per launch the NF4 state pointer tables and sizes (ctypes
+    arrays) and the byte offsets of the outputs; a call allocates the buffer and adds its
+    address.  It is kept on the first weight and rebuilt when any weight's plan key (its packed
+    data and state tensors, _plan_key) has changed."""
+
+    def __init__(self, groups, device, flat_w, offsets, stacks, total):
+        plans = [_plan(w, device) for w in flat_w]
+        self.ok = all(pl is not None for pl in plans) and len({(pl[2], pl[3]) for pl in plans}) == 1
+        self.total, self.stacks = total, stacks
+        self.device = device
+        self.check = [(w, _plan_key(w, device)) for w in flat_w]
+        self.launches = []
+        if not self.ok:
+            return
+        self.qblock, self.qblock2 = plans[0][2], plans[0][3]
+        self.keep = plans
+        for c in range(0, len(plans), MAX_PARTS_PER_LAUNCH):
+            chunk = plans[c:c + MAX_PARTS_PER_LAUNCH]
+            n = len(chunk)
+            arrays = [(ctypes.c_void_p * n)(*[pl[0][i] for pl in chunk]) for i in range(6)]
+            sizes = (ctypes.c_int64 * n)(*[pl[1] for pl in chunk])
+            self.launches.append((n, arrays, sizes, [2 * o for o in offsets[c:c + n]]))
+
+    def valid(self):
+        return all(_plan_key(w, self.device) == key for w, key in self.check)
+
+    def run(self, device):
+        buf = torch.empty(self.total, dtype=torch.float16, device=device)
+        base = buf.data_ptr()
+        stream = _ext.stream_of(buf)
+        for n, arrays, sizes, out_offsets in self.launches:
+            outs = (ctypes.c_void_p * n)(*[base + o for o in out_offsets])
+            _ext.call("soupk_nf4_unpack_multi", n, *[ctypes.addressof(a) for a in arrays],
+                      ctypes.addressof(outs), ctypes.addressof(sizes), self.qblock,
+                      self.qblock2, stream)
+        return [buf[st:st + rows * cols].view(rows, cols) for st, rows, cols in self.stacks]
+
+
+def _group_plan(groups, device, flat_w, offsets, stacks, total):
+    key = (device.index, tuple(id(w) for w in flat_w))
+    cache = getattr(flat_w[0], "_soupk_groups", None)
+    if cache is None:
+        cache = {}
+        try:
+            flat_w[0]._soupk_groups = cache
+        except AttributeError:      # an object without a __dict__: planned on every call
+            pass
+    plan = cache.get(key)
+    if plan is None or not plan.valid():
+        plan = cache[key] = _GroupPlan(groups, device, flat_w, offsets, stacks, total)
+    return plan
+
+
 def unpack_groups(groups, device):
     """One fp16 [sum N_i, K] row stack per group of weights (unpack_concat of each group), all
     unpacked by one launch into a single buffer: the projections of a decoder layer
-    (q|k|v, o, gate|up, down) before its forward.  Returns the stacks, views of the buffer."""
+    (q|k|v, o, gate|up, down) before its forward.  Returns the stacks, views of the buffer.
+    The launch arguments are prepared once per list of weights (_GroupPlan) and checked on each
+    call with the same key as each weight's own plan."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("unpack_groups: the device must be a HIP device (no CPU path)")
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    flat_w, offsets, stacks, total = [], [], [], 0
+    for weights in groups:
+        rows = [weight_shape(w)[0] for w in weights]
+        cols = weight_shape(weights[0])[1]
+        if any(weight_shape(w)[1] != cols for w in weights):
+            raise ValueError("weights of one group must have the same number of columns")
+        stacks.append((total, sum(rows), cols))
+        r0 = 0
+        for w, n in zip(weights, rows):
+            flat_w.append(w)
+            offsets.append(total + r0 * cols)
+            r0 += n
+        total += -(-sum(rows) * cols // _GROUP_ALIGN) * _GROUP_ALIGN
+    if flat_w:
+        plan = _group_plan(groups, device, flat_w, offsets, stacks, total)
+        if plan.ok:
+            return plan.run(device)
+    return _unpack_groups_generic(groups, device)
+
+
+def _unpack_groups_generic(groups, device):
+    """unpack_groups through unpack_many (layouts or devices a prepared launch does not take)."""
     shapes, total = [], 0
     for weights in groups:
         rows = [weight_shape(w)[0] for w in weights]
