@@ -124,8 +124,13 @@ __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_multi_kernel(Nf4Parts 
   __shared__ float2 pair[256];
   __shared__ float scale[kNf4TileDwords];
   const int x = static_cast<int>(blockIdx.x);
+  // p = the number of parts 1..n_parts-1 whose first tile is <= x (first_tile is non-decreasing).
+  // Unrolled over constant offsets, the table arrives in one batch of scalar loads; a search
+  // loop waits on one scalar load per part passed before the tile's first packed load.
   int p = 0;
-  while (p + 1 < parts.n_parts && x >= parts.first_tile[p + 1]) ++p;
+#pragma unroll
+  for (int q = 1; q < kNf4MaxParts; ++q)
+    p += (q < parts.n_parts && x >= parts.first_tile[q]) ? 1 : 0;
   nf4_unpack_tile(parts.packed[p], parts.absmax_u8[p], parts.code2[p], parts.absmax2[p],
                   parts.offset[p], parts.nf4[p], parts.out[p],
                   static_cast<int64_t>(x - parts.first_tile[p]) * kNf4TileDwords,
