@@ -48,10 +48,10 @@ def attention_bwd(q, k, v, key_valid, out, lse, dout, scale):
     B, NH, T, D = q.shape
     NKV = k.shape[1]
     dev = q.device
+    dout = dout.to(torch.float16).contiguous()
     _ext.require(dout, "dout", dtype=torch.float16, ndim=2, device=dev)
     if tuple(dout.shape) != (B * T, NH * D):
         raise ValueError(f"dout has shape {tuple(dout.shape)}, expected {(B * T, NH * D)}")
-    dout = dout.contiguous()
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)

@@ -33,11 +33,28 @@ def supported(y16, a_q, a_v, b_q, b_v):
             and b_v.shape[0] % 128 == 0)
 
 
+def _check_params(a_q, a_v, b_q, b_v, H, dev):
+    """The four LoRA parameters must be contiguous fp32 tensors on `dev` of shapes (16, H),
+    (16, H), (NQ, 16), (NV, 16) with H, NQ and NV multiples of 128 (the kernels' tiling)."""
+    for p, name in ((a_q, "a_q"), (a_v, "a_v"), (b_q, "b_q"), (b_v, "b_v")):
+        _ext.require(p, name, dtype=torch.float32, ndim=2, device=dev)
+    if tuple(a_q.shape) != (RANK, H) or tuple(a_v.shape) != (RANK, H):
+        raise ValueError(f"a_q {tuple(a_q.shape)} and a_v {tuple(a_v.shape)} must be "
+                         f"({RANK}, {H})")
+    if b_q.shape[1] != RANK or b_v.shape[1] != RANK:
+        raise ValueError(f"b_q {tuple(b_q.shape)} and b_v {tuple(b_v.shape)} must have "
+                         f"{RANK} columns")
+    if H % 128 or b_q.shape[0] % 128 or b_v.shape[0] % 128:
+        raise ValueError(f"H ({H}), NQ ({b_q.shape[0]}) and NV ({b_v.shape[0]}) must be "
+                         "multiples of 128")
+    return b_q.shape[0], b_v.shape[0]
+
+
 def lora_fwd(y16, a_q, a_v, b_q, b_v, scaling):
     _ext.require(y16, "y16", dtype=torch.float16, ndim=2)
     M, H = y16.shape
-    NQ, NV = b_q.shape[0], b_v.shape[0]
     dev = y16.device
+    NQ, NV = _check_params(a_q, a_v, b_q, b_v, H, dev)
     t = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
     lq = torch.empty((M, NQ), dtype=torch.float16, device=dev)
     lv = torch.empty((M, NV), dtype=torch.float16, device=dev)
@@ -51,6 +68,9 @@ def _rows(g, n, m, dev):
     """g as an fp16 [m, n] view with unit column stride (zeros for a missing gradient)."""
     if g is None:
         return torch.zeros((m, n), dtype=torch.float16, device=dev)
+    if not g.is_cuda or g.device != dev or g.dim() != 2:
+        raise ValueError(f"a LoRA output gradient must be a 2-d tensor on {dev}, got "
+                         f"{tuple(g.shape)} on {g.device}")
     g = g.to(torch.float16)
     if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
         g = g.contiguous()
@@ -58,10 +78,12 @@ def _rows(g, n, m, dev):
 
 
 def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling):
-    M, H = None, a_q.shape[1]
-    NQ, NV = b_q.shape[0], b_v.shape[0]
     ref = g_q if g_q is not None else g_v
+    if ref is None:
+        raise ValueError("lora_bwd_rows needs at least one of g_q, g_v")
     M, dev = ref.shape[0], ref.device
+    NQ, NV = _check_params(a_q, a_v, b_q, b_v, a_q.shape[-1], dev)
+    H = a_q.shape[1]
     g_q, g_v = _rows(g_q, NQ, M, dev), _rows(g_v, NV, M, dev)
     if tuple(g_q.shape) != (M, NQ) or tuple(g_v.shape) != (M, NV):
         raise ValueError(f"lora_bwd_rows: gradient shapes {tuple(g_q.shape)}, "

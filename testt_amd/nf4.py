@@ -15,6 +15,7 @@ or gate/up run as a single hipBLASLt GEMM (torch.matmul).
 """
 
 import ctypes
+import weakref
 
 import torch
 
@@ -222,24 +223,38 @@ def unpack_concat(weights, device):
 _GROUP_ALIGN = 256
 
 
+def _weak(obj):
+    """A weak reference to `obj` (a callable giving it back), or a strong one for objects that
+    take no weak reference."""
+    try:
+        return weakref.ref(obj)
+    except TypeError:
+        return lambda: obj
+
+
 class _GroupPlan:
     """unpack_groups' launches for one list of weight groups, prepared once: the buffer size,
     each stack's place in it, and per launch the NF4 state pointer tables and sizes (ctypes
     arrays) and the byte offsets of the outputs; a call allocates the buffer and adds its
-    address.  It is kept on the first weight and rebuilt when any weight's plan key (its packed
-    data and state tensors, _plan_key) has changed."""
+    address.
 
-    def __init__(self, groups, device, flat_w, offsets, stacks, total):
+    One plan is kept on the first weight of the list (a later list that starts with the same
+    weight replaces it).  It holds the weights only weakly, so it keeps no replaced weight
+    alive and forms no reference cycle with the weight that carries it, and it is used only for
+    the same device, the same grouping and the same weights (by identity), each with an
+    unchanged plan key (its packed data and state tensors, _plan_key)."""
+
+    def __init__(self, device, sizes, flat_w, offsets, stacks, total):
         plans = [_plan(w, device) for w in flat_w]
         self.ok = all(pl is not None for pl in plans) and len({(pl[2], pl[3]) for pl in plans}) == 1
         self.total, self.stacks = total, stacks
-        self.device = device
-        self.check = [(w, _plan_key(w, device)) for w in flat_w]
+        self.device, self.sizes = device, sizes
+        self.check = [(_weak(w), _plan_key(w, device)) for w in flat_w]
         self.launches = []
         if not self.ok:
             return
         self.qblock, self.qblock2 = plans[0][2], plans[0][3]
-        self.keep = plans
+        self.keep = [pl[4] for pl in plans]
         for c in range(0, len(plans), MAX_PARTS_PER_LAUNCH):
             chunk = plans[c:c + MAX_PARTS_PER_LAUNCH]
             n = len(chunk)
@@ -247,8 +262,11 @@ class _GroupPlan:
             sizes = (ctypes.c_int64 * n)(*[pl[1] for pl in chunk])
             self.launches.append((n, arrays, sizes, [2 * o for o in offsets[c:c + n]]))
 
-    def valid(self):
-        return all(_plan_key(w, self.device) == key for w, key in self.check)
+    def matches(self, device, sizes, flat_w):
+        if device != self.device or sizes != self.sizes or len(flat_w) != len(self.check):
+            return False
+        return all(ref() is w and _plan_key(w, device) == key
+                   for (ref, key), w in zip(self.check, flat_w))
 
     def run(self, device):
         buf = torch.empty(self.total, dtype=torch.float16, device=device)
@@ -263,17 +281,14 @@ class _GroupPlan:
 
 
 def _group_plan(groups, device, flat_w, offsets, stacks, total):
-    key = (device.index, tuple(id(w) for w in flat_w))
-    cache = getattr(flat_w[0], "_soupk_groups", None)
-    if cache is None:
-        cache = {}
+    sizes = tuple(len(g) for g in groups)
+    plan = getattr(flat_w[0], "_soupk_groups", None)
+    if plan is None or not plan.matches(device, sizes, flat_w):
+        plan = _GroupPlan(device, sizes, flat_w, offsets, stacks, total)
         try:
-            flat_w[0]._soupk_groups = cache
+            flat_w[0]._soupk_groups = plan
         except AttributeError:      # an object without a __dict__: planned on every call
             pass
-    plan = cache.get(key)
-    if plan is None or not plan.valid():
-        plan = cache[key] = _GroupPlan(groups, device, flat_w, offsets, stacks, total)
     return plan
 
 
