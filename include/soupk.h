@@ -26,7 +26,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; soupk_abi_version() returns the library's. */
-#define SOUPK_ABI_VERSION 1
+#define SOUPK_ABI_VERSION 2
 
 int soupk_abi_version(void);
 
@@ -193,6 +193,21 @@ int soupk_swiglu_bwd_inplace(const uint16_t* dact, uint16_t* gu, int64_t rows, i
 int soupk_head_stats_grad(uint16_t* logits, const int64_t* target, float* entropy, float* loss,
                           int32_t* correct, float* lse_out, float grad_scale, int64_t rows,
                           int64_t V, void* stream);
+
+/*
+ * soupk_head_stats_grad with the gradient written away from the logits (the kernel of
+ * solution/head.py:34-76 as FusedHeadLoss.forward, solution/head.py:87-137, uses it; no
+ * counterpart entry in the reference).  Statistics as soupk_head_stats_grad, at row r of
+ * entropy / loss / correct / lse_out.  logits are only read.  The gradient of a labelled row r
+ * goes to row grad_row[r] of grad_out ([grad_rows, V] fp16), so the labelled rows of a chunk
+ * land packed in their own buffer for the dh GEMM; a row whose grad_row entry lies outside
+ * [0, grad_rows) gets none.  grad_row and grad_out are both NULL (statistics only, no gradient
+ * written) or both set; then (2V) % 16 == 0 and grad_out has logits' address modulo 16.
+ */
+int soupk_head_stats_grad_rows(const uint16_t* logits, const int64_t* target,
+                               const int32_t* grad_row, uint16_t* grad_out, int64_t grad_rows,
+                               float* entropy, float* loss, int32_t* correct, float* lse_out,
+                               float grad_scale, int64_t rows, int64_t V, void* stream);
 
 /*
  * Causal grouped-query attention, forward (widening beyond the reference's kernel set: it

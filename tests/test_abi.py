@@ -64,6 +64,11 @@ def test_version_and_status_strings(lib):
     ("soupk_rope_pack_fwd", (None,) * 3 + (7,) + (None,) * 7 + (1, 1, 1, 1, 1, 8, None)),
     ("soupk_rope_pack_bwd", (None,) * 7 + (1, 1, 1, 1, 1, 7, None)),
     ("soupk_head_stats_grad", (None,) * 6 + (1.0, 1, 0, None)),
+    # gradient rows: map without buffer, a pitch of part of a chunk, a misaligned buffer
+    ("soupk_head_stats_grad_rows", (32, 32, 16, None, 1, 32, 32, 32, None, 1.0, 1, 8, None)),
+    ("soupk_head_stats_grad_rows", (32, 32, 16, 64, 1, 32, 32, 32, None, 1.0, 1, 7, None)),
+    ("soupk_head_stats_grad_rows", (32, 32, 16, 40, 1, 32, 32, 32, None, 1.0, 1, 8, None)),
+    ("soupk_head_stats_grad_rows", (32, 32, 16, 64, -1, 32, 32, 32, None, 1.0, 1, 8, None)),
     ("soupk_index_inverse", (None, -1, None, 4, None)),
     ("soupk_bench_copy", (None, None, 4096, None)),
     ("soupk_bench_copy", (16, 32, 24, None)),        # not a multiple of 16 bytes
@@ -80,6 +85,7 @@ def test_invalid_arguments_rejected_before_launch(lib, name, args):
     ("soupk_nf4_unpack_multi", (0,) + (None,) * 8 + (64, 256, None)),
     ("soupk_sum_partials", (None, 4, 0, 0, None, None)),
     ("soupk_head_stats_grad", (None,) * 6 + (1.0, 0, 151936, None)),
+    ("soupk_head_stats_grad_rows", (None,) * 4 + (0,) + (None,) * 4 + (1.0, 0, 151936, None)),
     ("soupk_index_inverse", (None, 0, None, 0, None)),
 ])
 def test_empty_work_is_a_no_op(lib, name, args):

@@ -117,3 +117,45 @@ def test_fused_head_loss_end_to_end(rows, hidden, vocab, chunk, monkeypatch):
     assert torch.equal(cor.cpu(), r_cor)
     (loss * 1024.0).backward()
     torch.testing.assert_close(hg.grad.cpu().double(), r_dh, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("rows,vocab", [(256, 151936), (37, 5000), (5, 200000)])
+def test_rows_variant_matches_in_place(rows, vocab):
+    """soupk_head_stats_grad_rows (the form FusedHeadLoss uses): identical statistics, each
+    labelled row's gradient bit-identical to the in-place kernel's, written to the row its map
+    names (here a reversed order); a map entry out of range writes nothing, the logits stay
+    as they were, and with no gradient output only the statistics are written."""
+    print(f"head rows variant rows={rows} vocab={vocab}", flush=True)
+    z, targets = workloads.head_logits(rows, vocab, seed=rows * 7 + vocab, scale=1.0)
+    targets = targets.clamp(max=vocab - 1)
+    targets[::3] = -100
+    new, ent, loss, cor, lse = run_kernel(z, targets, 0.37)
+    lab = (targets != -100).nonzero()[:, 0]
+    n_out = lab.numel()
+    slot = torch.full((rows,), -1, dtype=torch.int32)
+    slot[lab] = torch.arange(n_out - 1, -1, -1, dtype=torch.int32)
+    skipped = int(lab[0])
+    slot[skipped] = n_out + 5                      # out of range: no gradient for this row
+    logits = z.to(DEV)
+    g = torch.full((n_out, vocab), float("nan"), dtype=torch.float16, device=DEV)
+    outs = [torch.empty(rows, dtype=dt, device=DEV)
+            for dt in (torch.float32, torch.float32, torch.int32, torch.float32)]
+    head.head_stats_grad_rows(logits, targets.to(DEV), slot.to(DEV), g, outs[0], outs[1],
+                              outs[2], 0.37, outs[3])
+    assert torch.equal(logits.cpu().view(torch.int16), z.view(torch.int16))
+    for got, want in zip(outs, (ent, loss, cor.int(), lse)):
+        assert torch.equal(got.cpu(), want)
+    g = g.cpu()
+    for r in lab.tolist():
+        if r == skipped:
+            continue
+        assert torch.equal(g[int(slot[r])].view(torch.int16), new[r].view(torch.int16)), r
+    unused = sorted(set(range(n_out)) - {int(slot[r]) for r in lab.tolist() if r != skipped})
+    assert all(bool(torch.isnan(g[u].float()).all()) for u in unused)
+    # statistics only
+    stats_only = [torch.empty_like(o) for o in outs]
+    head.head_stats_grad_rows(logits, targets.to(DEV), None, None, *stats_only[:3], 0.37,
+                              stats_only[3])
+    assert torch.equal(logits.cpu().view(torch.int16), z.view(torch.int16))
+    for got, want in zip(stats_only, outs):
+        assert torch.equal(got, want)

@@ -16,7 +16,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsoupk.s
 _lock = threading.Lock()
 _lib = None
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F16 = 0
 DTYPE_F32 = 1
 
@@ -39,6 +39,7 @@ SIGNATURES = {
     "soupk_swiglu_fwd": [_p, _p, _i64, _i64, _p],
     "soupk_swiglu_bwd_inplace": [_p, _p, _i64, _i64, _p],
     "soupk_head_stats_grad": [_p, _p, _p, _p, _p, _p, _f32, _i64, _i64, _p],
+    "soupk_head_stats_grad_rows": [_p, _p, _p, _p, _i64, _p, _p, _p, _p, _f32, _i64, _i64, _p],
     "soupk_time_next_launch": [_p, _p],
     "soupk_bench_copy": [_p, _p, _i64, _p],
     "soupk_attention_fwd": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p],

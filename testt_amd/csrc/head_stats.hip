@@ -222,11 +222,29 @@ __device__ __forceinline__ u32x4 grad_chunk(u32x4 w, float shift, float grad_sca
                pack_h2(z[6] * grad_scale, z[7] * grad_scale)};
 }
 
-__device__ __forceinline__ void grad_scalar(uint16_t* base, int64_t col, int64_t tgt,
-                                            float shift, float grad_scale) {
-  const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(h2f(base[col]), kLog2e, shift));
+__device__ __forceinline__ void grad_scalar(const uint16_t* src, uint16_t* dst, int64_t col,
+                                            int64_t tgt, float shift, float grad_scale) {
+  const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(h2f(src[col]), kLog2e, shift));
   const float g = (col == tgt ? p - 1.0f : p) * grad_scale;
-  base[col] = static_cast<uint16_t>(pack_h2(g, 0.f) & 0xffffu);
+  dst[col] = static_cast<uint16_t>(pack_h2(g, 0.f) & 0xffffu);
+}
+
+// Where the gradient of `row` goes: the row itself (grad_out NULL, in place), row
+// grad_row[row] of grad_out, or nowhere (a row map entry outside [0, grad_rows), or no
+// gradient output at all: grad_row NULL with grad_out NULL and in_place false).
+struct GradDest {
+  const int32_t* grad_row;  // nullable
+  uint16_t* grad_out;       // nullable
+  int64_t grad_rows;
+  bool in_place;
+};
+
+__device__ __forceinline__ uint16_t* grad_row_base(const GradDest& gd, uint16_t* base,
+                                                   int64_t row, int64_t V) {
+  if (gd.in_place) return base;
+  if (gd.grad_out == nullptr || gd.grad_row == nullptr) return nullptr;
+  const int64_t d = gd.grad_row[row];
+  return (d >= 0 && d < gd.grad_rows) ? gd.grad_out + d * V : nullptr;
 }
 
 // ---- register-resident form ------------------------------------------------------------------
@@ -299,7 +317,7 @@ template <int CPT>
 __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
     uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
     float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
-    float* __restrict__ lse_out, float grad_scale, int64_t V) {
+    float* __restrict__ lse_out, float grad_scale, int64_t V, GradDest gd) {
   constexpr int P = CPT < kHeadPrefetch ? CPT : kHeadPrefetch;  // loads kept ahead of compute
   __shared__ RowStats part[kHeadWaves];
   __shared__ f16 chunk_max[CPT * kHeadThreads];  // m_k of chunk k of thread t at [k*1024 + t]
@@ -371,7 +389,12 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
 
   const float lse = finish_row(st, part, zt, row, tgt, labelled, tgt_ok, entropy,
                                loss, correct, lse_out, kLift);
-  if (!labelled) return;
+  uint16_t* const gbase = grad_row_base(gd, base, row, V);
+  if (!labelled || gbase == nullptr) return;
+  // The gradient row has the logits row's alignment (the entry point checks it), so it splits
+  // into the same lead columns, whole chunks and tail columns.
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      buffer_rsrc(gbase + sp.lead, static_cast<uint32_t>(sp.nvec * 16));
   const float shift = -lse * kLog2e;
   // F_k = 2^(m_k*log2e + fbase) = exp(m_k - lse) * grad_scale * 2^-kLift.
   const float fbase = (log2f(grad_scale) - kLift) - lse * kLog2e;
@@ -382,7 +405,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   // The target column: (exp(z_t - lse) - 1) * grad_scale in fp32 (used by one lane only).
   const float gt =
       (__builtin_amdgcn_exp2f(__builtin_fmaf(zt, kLog2e, shift)) - 1.0f) * grad_scale;
-  if (has_lead) grad_scalar(base, tid, tgt, shift, grad_scale);
+  if (has_lead) grad_scalar(base, gbase, tid, tgt, shift, grad_scale);
   // Store offsets are recomputed from an opaque copy of tid*16 (one add per chunk) rather than
   // kept live from the load phase: CPT offset registers on top of the row would spill.
   uint32_t lane_off = off0;
@@ -394,19 +417,19 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
       const float mk = static_cast<float>(chunk_max[k * kHeadThreads + tid]);
       const float F = __builtin_amdgcn_exp2f(__builtin_fmaf(mk, kLog2e, fbase));
       __builtin_amdgcn_raw_buffer_store_b128(grad_from_e(w[k], F, c == tc ? thit : -1, gt),
-                                             rsrc, lane_off + k * kChunkStride, 0,
+                                             wrsrc, lane_off + k * kChunkStride, 0,
                                              kAuxStream);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (has_tail) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
+  if (has_tail) grad_scalar(base, gbase, sp.tail0 + tid, tgt, shift, grad_scale);
 }
 
 // ---- streaming form (two reads of the row) -----------------------------------------------------
 __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
     uint16_t* __restrict__ logits, const int64_t* __restrict__ target,
     float* __restrict__ entropy, float* __restrict__ loss, int32_t* __restrict__ correct,
-    float* __restrict__ lse_out, float grad_scale, int64_t V) {
+    float* __restrict__ lse_out, float grad_scale, int64_t V, GradDest gd) {
   __shared__ RowStats part[kHeadWaves];
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
@@ -444,11 +467,13 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
   }
   const float lse = finish_row(st, part, zt, row, tgt, labelled, tgt_ok, entropy,
                                loss, correct, lse_out, 0.f);
-  if (!labelled) return;
+  uint16_t* const gbase = grad_row_base(gd, base, row, V);
+  if (!labelled || gbase == nullptr) return;
+  u32x4* const gvb = reinterpret_cast<u32x4*>(gbase + sp.lead);
   const float shift = -lse * kLog2e;
   const int64_t tc = (tgt_ok && tgt >= sp.lead && tgt < sp.tail0) ? (tgt - sp.lead) >> 3 : -1;
   const int thit = static_cast<int>((tgt - sp.lead) & 7);
-  if (tid < sp.lead) grad_scalar(base, tid, tgt, shift, grad_scale);
+  if (tid < sp.lead) grad_scalar(base, gbase, tid, tgt, shift, grad_scale);
   for (int64_t s0 = 0; s0 < sp.nvec; s0 += kStep) {
     u32x4 w[kStreamUnroll];
 #pragma unroll
@@ -461,10 +486,10 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
       const int64_t c = s0 + u * kHeadThreads + tid;
       if (c < sp.nvec)
         __builtin_nontemporal_store(grad_chunk(w[u], shift, grad_scale, c == tc ? thit : -1),
-                                    vb + c);
+                                    gvb + c);
     }
   }
-  if (sp.tail0 + tid < V) grad_scalar(base, sp.tail0 + tid, tgt, shift, grad_scale);
+  if (sp.tail0 + tid < V) grad_scalar(base, gbase, sp.tail0 + tid, tgt, shift, grad_scale);
 }
 
 }  // namespace
@@ -472,9 +497,11 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_stream_kernel(
 
 using namespace soupk;
 
-extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
-    uint16_t* logits, const int64_t* target, float* entropy, float* loss, int32_t* correct,
-    float* lse_out, float grad_scale, int64_t rows, int64_t V, void* stream) {
+namespace {
+
+int head_launch(uint16_t* logits, const int64_t* target, float* entropy, float* loss,
+                int32_t* correct, float* lse_out, float grad_scale, int64_t rows, int64_t V,
+                const GradDest& gd, void* stream) {
   if (rows < 0 || V <= 0 || V >= (int64_t{1} << 31) - 16) return kInvalid;
   if (rows == 0) return kOk;
   if (rows > 0x7fffffff) return kInvalid;
@@ -488,7 +515,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
   auto run = [&](auto tag) {
     constexpr int C = decltype(tag)::value;
     return launch_kernel(head_stats_grad_kernel<C>, grid, block, s, logits, target, entropy,
-                         loss, correct, lse_out, grad_scale, V);
+                         loss, correct, lse_out, grad_scale, V, gd);
   };
   if (cpt <= 1) return run(std::integral_constant<int, 1>{});
   if (cpt <= 2) return run(std::integral_constant<int, 2>{});
@@ -499,5 +526,33 @@ extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
   if (cpt <= 19) return run(std::integral_constant<int, 19>{});
   if (cpt <= kMaxCpt) return run(std::integral_constant<int, kMaxCpt>{});
   return launch_kernel(head_stats_grad_stream_kernel, grid, block, s, logits, target, entropy,
-                       loss, correct, lse_out, grad_scale, V);
+                       loss, correct, lse_out, grad_scale, V, gd);
+}
+
+}  // namespace
+
+extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad(
+    uint16_t* logits, const int64_t* target, float* entropy, float* loss, int32_t* correct,
+    float* lse_out, float grad_scale, int64_t rows, int64_t V, void* stream) {
+  const GradDest gd{nullptr, nullptr, 0, true};
+  return head_launch(logits, target, entropy, loss, correct, lse_out, grad_scale, rows, V, gd,
+                     stream);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_head_stats_grad_rows(
+    const uint16_t* logits, const int64_t* target, const int32_t* grad_row, uint16_t* grad_out,
+    int64_t grad_rows, float* entropy, float* loss, int32_t* correct, float* lse_out,
+    float grad_scale, int64_t rows, int64_t V, void* stream) {
+  if ((grad_out == nullptr) != (grad_row == nullptr) || grad_rows < 0) return kInvalid;
+  if (grad_out != nullptr) {
+    // Every gradient row must split into the same lead columns, 16-byte chunks and tail
+    // columns as every logits row: the same address modulo 16 and a row pitch of whole chunks.
+    if ((V * 2) % 16 != 0) return kInvalid;
+    if ((reinterpret_cast<uintptr_t>(grad_out) - reinterpret_cast<uintptr_t>(logits)) & 15u)
+      return kInvalid;
+  }
+  const GradDest gd{grad_row, grad_out, grad_rows, false};
+  // The kernels only read the logits when the gradient goes elsewhere (or nowhere).
+  return head_launch(const_cast<uint16_t*>(logits), target, entropy, loss, correct, lse_out,
+                     grad_scale, rows, V, gd, stream);
 }
