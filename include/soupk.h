@@ -28,6 +28,9 @@ extern "C" {
 /* ABI version of this header; soupk_abi_version() returns the library's. */
 #define SOUPK_ABI_VERSION 2
 
+/* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
+#define SOUPK_STATUS_SCRATCH_LIMIT 20001
+
 int soupk_abi_version(void);
 
 /* Human-readable text of a status code returned by any soupk_* call. */
@@ -277,6 +280,25 @@ int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* 
                           int64_t workspace_floats, float* d_aq, float* d_av, float* d_bq,
                           float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
                           void* stream);
+
+/*
+ * soupk_lora_bwd_params without the workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments, results and rounding as
+ * soupk_lora_bwd_params (the same kernels), but the per-slice partial sums live in a static
+ * buffer of SOUPK_LORA_SCRATCH_FLOATS floats (16 MiB) that the library holds on each GPU it
+ * runs on until the process ends; it calls no allocator.  A problem needing more than that,
+ * ceil(M/128) * (32*H + 16*(NQ + NV)) > SOUPK_LORA_SCRATCH_FLOATS (M > 6784 rows at H = 1536,
+ * NQ = 1536, NV = 256), returns SOUPK_STATUS_SCRATCH_LIMIT before any launch.  Every call on one
+ * GPU shares that GPU's buffer: calls that overlap on one GPU (concurrent streams, threads)
+ * race and must be serialised by the caller.  The buffer needs no clearing between calls (every
+ * entry a call reads is written by that call first).
+ */
+#define SOUPK_LORA_SCRATCH_FLOATS (4 << 20)
+int soupk_lora_bwd_params_noalloc(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
+                                  const uint16_t* gs_q, const uint16_t* gs_v, float* d_aq,
+                                  float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H,
+                                  int32_t NQ, int32_t NV, int32_t r, void* stream);
 
 /*
  * y = x W^T (+ bias), fp16, on MFMA with 128 x 128 tiles (the GEMM core of soupk_gemm_tn_nf4;

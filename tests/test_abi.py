@@ -90,3 +90,14 @@ def test_invalid_arguments_rejected_before_launch(lib, name, args):
 ])
 def test_empty_work_is_a_no_op(lib, name, args):
     _ext.call(name, *args)
+
+
+def test_noalloc_rejects_problems_beyond_its_scratch(lib):
+    """soupk_lora_bwd_params_noalloc returns SOUPK_STATUS_SCRATCH_LIMIT, before any HIP call,
+    for a problem whose partial sums exceed its static scratch (6785 rows at the Qwen2.5-1.5B
+    shapes; 6784 fit)."""
+    H, NQ, NV = 1536, 1536, 256
+    need = -(-6785 // 128) * (32 * H + 16 * (NQ + NV))
+    assert need > _ext.LORA_SCRATCH_FLOATS >= -(-6784 // 128) * (32 * H + 16 * (NQ + NV))
+    with pytest.raises(_ext.SoupkError, match=f"status {_ext.STATUS_SCRATCH_LIMIT}: .*scratch"):
+        _ext.call("soupk_lora_bwd_params_noalloc", *(16,) * 9, 6785, H, NQ, NV, 16, None)

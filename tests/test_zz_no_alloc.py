@@ -1,0 +1,47 @@
+"""GPU: soupk_lora_bwd_params_noalloc, the allocation-free form of soupk_lora_bwd_params (its
+partial sums in the library's static per-GPU scratch instead of a caller workspace), called
+through the C ABI.  It runs the same kernels over the same partial layout, so its parameter
+gradients must equal the workspace entry point's bit for bit: checked on consecutive calls,
+each smaller than the one before (so a call that read a slice left over from the previous one
+would differ), down to no rows at all (zero gradients)."""
+
+import pytest
+import torch
+
+from testt_amd import _ext, lora
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+H, NQ, NV, R = 1536, 1536, 256, 16
+
+
+def _inputs(M, seed):
+    g = torch.Generator().manual_seed(seed)
+
+    def mk(cols, scale):
+        return (torch.randn(M, cols, generator=g) * scale).to(torch.float16).to(DEV)
+
+    return mk(H, 1.0), mk(2 * R, 0.5), mk(2 * R, 0.1), mk(NQ, 0.1), mk(NV, 0.1)
+
+
+def _noalloc(y, t, dt, gs_q, gs_v):
+    M = y.shape[0]
+    outs = [torch.full(shape, float("nan"), dtype=torch.float32, device=DEV)
+            for shape in ((R, H), (R, H), (NQ, R), (NV, R))]
+    _ext.call("soupk_lora_bwd_params_noalloc", *[_ext.ptr(x) for x in (y, t, dt, gs_q, gs_v)],
+              *[_ext.ptr(o) for o in outs], M, H, NQ, NV, R, _ext.stream_of(y))
+    return outs
+
+
+@pytest.mark.parametrize("sizes", [(2048, 333, 0), (6784, 129)])
+def test_noalloc_matches_workspace_entry(sizes):
+    for i, M in enumerate(sizes):
+        print(f"lora params no-alloc call {i}: M={M}", flush=True)
+        ins = _inputs(M, seed=100 + M)
+        got = _noalloc(*ins)
+        want = lora.lora_bwd_params(*ins)
+        for name, a, b in zip(("d_aq", "d_av", "d_bq", "d_bv"), got, want):
+            assert torch.equal(a, b), f"{name} differs at M={M}"
+        if M == 0:
+            assert all(bool((a == 0).all()) for a in got)
+    torch.cuda.synchronize()

@@ -17,6 +17,8 @@ _lock = threading.Lock()
 _lib = None
 
 ABI_VERSION = 2
+STATUS_SCRATCH_LIMIT = 20001          # SOUPK_STATUS_SCRATCH_LIMIT
+LORA_SCRATCH_FLOATS = 4 << 20         # SOUPK_LORA_SCRATCH_FLOATS
 DTYPE_F16 = 0
 DTYPE_F32 = 1
 
@@ -50,6 +52,8 @@ SIGNATURES = {
                             _i32, _i32, _i32, _p],
     "soupk_lora_bwd_params": [_p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i32, _i32,
                               _i32, _i32, _p],
+    "soupk_lora_bwd_params_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                      _i32, _p],
     "soupk_gemm_tn": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _p],
     "soupk_gemm_tn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _i64,
                           _i32, _i32, _p],

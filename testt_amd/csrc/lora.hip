@@ -28,6 +28,7 @@
 // column l%16, rows 4(l/16)..+3.
 
 #include <algorithm>
+#include <mutex>
 
 #include "soupk_common.hpp"
 
@@ -524,35 +525,108 @@ static int64_t lora_params_workspace(int64_t M, int32_t H, int32_t NQ, int32_t N
   return slices * (2 * kR * static_cast<int64_t>(H) + kR * static_cast<int64_t>(NQ + NV));
 }
 
-extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params(
-    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
-    const uint16_t* gs_v, float* workspace, int64_t workspace_floats, float* d_aq, float* d_av,
-    float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
-    void* stream) {
-  const int rc = check_dims(M, H, NQ, NV, r);
-  if (rc != kOk) return rc;
-  if (H % 64 || NQ % 64 || NV % 64) return kInvalid;
+namespace {
+
+// The two launches of the parameter gradients over a caller-given partial-sum buffer `part`
+// (at least lora_params_workspace(M, H, NQ, NV) floats).  The partial kernel writes every
+// entry of every slice, so `part` needs no clearing and its old contents never leak into a
+// result.
+int lora_params_launch(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
+                       const uint16_t* gs_q, const uint16_t* gs_v, float* part, float* d_aq,
+                       float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ,
+                       int32_t NV, hipStream_t st) {
   const int64_t n_out = 2 * kR * static_cast<int64_t>(H) + kR * static_cast<int64_t>(NQ + NV);
-  if (workspace_floats < lora_params_workspace(M, H, NQ, NV)) return kInvalid;
-  if (!d_aq || !d_av || !d_bq || !d_bv) return kInvalid;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned reduce_grid = static_cast<unsigned>((n_out + 255) / 256);
   if (M == 0)   // no rows: zero gradients (the reduction over no slices)
     return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st,
                          static_cast<const float*>(nullptr), 0, n_out, H, NQ, d_aq, d_av,
                          d_bq, d_bv);
-  if (!y || !t || !dt || !gs_q || !gs_v || !workspace) return kInvalid;
-  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(t),
-                        static_cast<const void*>(dt), static_cast<const void*>(gs_q),
-                        static_cast<const void*>(gs_v), static_cast<const void*>(workspace)})
-    if (misaligned(p)) return kInvalid;
   const int slices = static_cast<int>((M + kSlice - 1) / kSlice);
-  if (slices > 65535) return kInvalid;
   const dim3 grid(static_cast<unsigned>(H / 64 + NQ / 64 + NV / 64),
                   static_cast<unsigned>(slices));
   int rc2 = launch_kernel(lora_params_partial_kernel, grid, dim3(kThreads), st, y, t, dt, gs_q,
-                          gs_v, workspace, static_cast<int>(M), H, NQ, NV, n_out);
+                          gs_v, part, static_cast<int>(M), H, NQ, NV, n_out);
   if (rc2 != kOk) return rc2;
-  return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st, workspace,
+  return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st, part,
                        slices, n_out, H, NQ, d_aq, d_av, d_bq, d_bv);
+}
+
+// Argument checks shared by both entry points (before any HIP call).
+int lora_params_check(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
+                      const uint16_t* gs_q, const uint16_t* gs_v, float* d_aq, float* d_av,
+                      float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV,
+                      int32_t r) {
+  const int rc = check_dims(M, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  if (H % 64 || NQ % 64 || NV % 64) return kInvalid;
+  if (!d_aq || !d_av || !d_bq || !d_bv) return kInvalid;
+  if (M == 0) return kOk;
+  if (!y || !t || !dt || !gs_q || !gs_v) return kInvalid;
+  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(t),
+                        static_cast<const void*>(dt), static_cast<const void*>(gs_q),
+                        static_cast<const void*>(gs_v)})
+    if (misaligned(p)) return kInvalid;
+  if ((M + kSlice - 1) / kSlice > 65535) return kInvalid;
+  return kOk;
+}
+
+// ---- the allocation-free variant's scratch ----------------------------------------------------
+// One fixed partial-sum buffer per GPU, in the library's code object: it exists on every device
+// the library's kernels are loaded on, from module load to process exit.  Host code never
+// passes `lora_scratch` itself to a kernel (on the host the name is only a stand-in for the
+// symbol); each device's address is looked up once, with that device current, and kept.
+constexpr int64_t kLoraScratchFloats = SOUPK_LORA_SCRATCH_FLOATS;
+__device__ __align__(256) float lora_scratch[kLoraScratchFloats];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices];   // device address of lora_scratch per ordinal (or null)
+
+// The device address of the current device's lora_scratch (looked up on its first use).
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kScratchDevices) return kInvalid;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(lora_scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (p == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params(
+    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
+    const uint16_t* gs_v, float* workspace, int64_t workspace_floats, float* d_aq, float* d_av,
+    float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
+    void* stream) {
+  const int rc = lora_params_check(y, t, dt, gs_q, gs_v, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  if (workspace_floats < lora_params_workspace(M, H, NQ, NV)) return kInvalid;
+  if (M > 0 && (!workspace || misaligned(workspace))) return kInvalid;
+  return lora_params_launch(y, t, dt, gs_q, gs_v, workspace, d_aq, d_av, d_bq, d_bv, M, H, NQ,
+                            NV, static_cast<hipStream_t>(stream));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params_noalloc(
+    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
+    const uint16_t* gs_v, float* d_aq, float* d_av, float* d_bq, float* d_bv, int64_t M,
+    int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
+  const int rc = lora_params_check(y, t, dt, gs_q, gs_v, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  if (lora_params_workspace(M, H, NQ, NV) > kLoraScratchFloats) return SOUPK_STATUS_SCRATCH_LIMIT;
+  float* part = nullptr;
+  if (M > 0) {
+    const int rs = scratch_on_current_device(&part);
+    if (rs != kOk) return rs;
+  }
+  return lora_params_launch(y, t, dt, gs_q, gs_v, part, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV,
+                            static_cast<hipStream_t>(stream));
 }

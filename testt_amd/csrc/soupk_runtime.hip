@@ -104,6 +104,9 @@ extern "C" __attribute__((visibility("default"))) int soupk_abi_version(void) {
 extern "C" __attribute__((visibility("default"))) const char* soupk_status_string(int status) {
   if (status == kOk) return "success";
   if (status == kInvalid) return "invalid argument (rejected before launch)";
+  if (status == SOUPK_STATUS_SCRATCH_LIMIT)
+    return "the problem needs more partial-sum memory than the allocation-free entry point's "
+           "static scratch holds (SOUPK_LORA_SCRATCH_FLOATS floats); nothing was launched";
   return hipGetErrorString(static_cast<hipError_t>(status));
 }
 
