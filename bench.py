@@ -254,6 +254,85 @@ def build_extra_cases(dev, n_sets=3, lib=None):
     return cases
 
 
+def build_floor_cases(dev, n_sets=3, lib=None):
+    """The launch floor, timed exactly as the kernels are: an empty kernel of one workgroup and
+    of 1024 workgroups (soupk_bench_empty), and a 4 KiB device copy (soupk_bench_copy)."""
+    bufs = [(torch.empty(4096, dtype=torch.uint8, device=dev),
+             torch.empty(4096, dtype=torch.uint8, device=dev)) for _ in range(n_sets)]
+    return [Case("empty_kernel_1wg", "bench_empty_kernel", "soupk_bench_empty", 0,
+                 [((), (1,))], lib=lib),
+            Case("empty_kernel_1024wg", "bench_empty_kernel", "soupk_bench_empty", 0,
+                 [((), (1024,))], lib=lib),
+            Case("copy_4KiB", "bench_copy_kernel", "soupk_bench_copy", 8192,
+                 [((a, b), (p(a), p(b), 4096)) for a, b in bufs], lib=lib)]
+
+
+# The ragged batch of BASELINE.json's RoPE config: real lengths of the 4 rows of 512.
+RAGGED_LENGTHS = (512, 152, 128, 96)
+
+
+def build_shape_cases(dev, n_sets=3, lib=None):
+    """Kernels of the set at the other shapes the step runs them at (reported apart, not in
+    `value`): the RoPE pack forward / backward on the ragged batch RAGGED_LENGTHS (M = 888 real
+    tokens of 4 x 512; the forward also writes the zeros of the 1160 pad positions, in the same
+    launch, as the reference's padded layout needs), and the vocab-head kernel on a 2048-row
+    chunk (head.CHUNK_ROWS, the product's chunk) through soupk_head_stats_grad_rows, the entry
+    FusedHeadLoss uses (gradient rows packed into their own buffer), 90% of rows labelled."""
+    H, NH, NKV, D, B, T = (workloads.HIDDEN, workloads.N_HEADS, workloads.N_KV,
+                           workloads.HEAD_DIM, workloads.BATCH, workloads.SEQ)
+    W = (NH + 2 * NKV) * D
+    cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
+    M = sum(RAGGED_LENGTHS)
+    fsets, bsets = [], []
+    for i in range(n_sets):
+        qkv, lq, lv, pos = workloads.rope_inputs(RAGGED_LENGTHS, T, NH, NKV, D, torch.float32,
+                                                 seed=60 + 10 * i, device=dev)
+        inv = torch.full((B * T,), -1, dtype=torch.int32, device=dev)
+        inv[pos] = torch.arange(M, dtype=torch.int32, device=dev)
+        q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
+        k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+        v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+        fsets.append(((qkv, lq, lv, pos, inv, q, k, v),
+                      (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), p(inv),
+                       p(q), p(k), p(v), M, B, T, NH, NKV, D)))
+        dq, dk, dv = workloads.rope_grads(B, T, NH, NKV, D, seed=70 + 10 * i, device=dev)
+        dqkv = torch.empty((M, W), dtype=torch.float16, device=dev)
+        bsets.append(((dq, dk, dv, pos, dqkv),
+                      (p(dq), p(dk), p(dv), p(cos), p(sin), p(pos), p(dqkv), M, B, T, NH, NKV,
+                       D)))
+    # cos/sin rows of the positions used (all 512 rows, read by the longest sequence)
+    tab = 2 * T * D * 4
+    cases = [
+        Case("rope_pack_fwd_ragged888", "rope_pack_fwd_kernel", "soupk_rope_pack_fwd",
+             M * W * 2 + M * (NH + NKV) * D * 4 + tab + 8 * M + 4 * B * T + B * T * W * 2,
+             fsets, lib=lib),
+        Case("rope_pack_bwd_ragged888", "rope_pack_bwd_kernel", "soupk_rope_pack_bwd",
+             M * W * 2 + tab + 8 * M + M * W * 2, bsets, lib=lib)]
+    rows, V = 2048, workloads.VOCAB
+    sets, n_lab = [], 0
+    for i in range(n_sets):
+        g = torch.Generator(device=dev).manual_seed(80 + i)
+        z = (0.784 * torch.randn(rows, V, generator=g, device=dev)).to(torch.float16)
+        tgt = torch.randint(0, V, (rows,), generator=g, device=dev)
+        tgt[torch.rand(rows, generator=g, device=dev) < 0.1] = -100
+        lab = tgt != -100
+        slot = torch.where(lab, torch.cumsum(lab, 0, dtype=torch.int32) - 1, -1).to(torch.int32)
+        n = int(lab.sum())
+        gbuf = torch.empty((n, V), dtype=torch.float16, device=dev)
+        stats = [torch.empty(rows, dtype=dt, device=dev)
+                 for dt in (torch.float32, torch.float32, torch.int32)]
+        sets.append(((z, tgt, slot, gbuf, stats),
+                     (p(z), p(tgt), p(slot), p(gbuf), n, *[p(t) for t in stats], None,
+                      64.0 / 1843.0, rows, V)))
+        if i == 0:
+            n_lab = n
+    cases.append(Case("head_stats_grad_2048rows", "head_stats_grad_kernel",
+                      "soupk_head_stats_grad_rows",
+                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 4 * rows + 12 * rows, sets,
+                      lib=lib))
+    return cases
+
+
 class HipEvents:
     """hipEvent_t pairs from the HIP runtime torch already loaded (RTLD_NOLOAD: the same one)."""
 
@@ -345,11 +424,74 @@ def time_gpu(cases, steps, warmup, dev, lib=None):
     return host_enqueue, span
 
 
-def time_layer(dev, steps, warmup):
+class GcWatch:
+    """Counts Python garbage collections (and their wall time) while active: a collection
+    inside a timed loop of host-driven steps shows up as a step far above the median."""
+
+    def __init__(self):
+        import gc
+
+        self.gc = gc
+        self.count, self.ms, self._t = 0, 0.0, None
+
+    def _cb(self, phase, info):
+        if phase == "start":
+            self._t = time.perf_counter()
+        elif self._t is not None:
+            self.count += 1
+            self.ms += (time.perf_counter() - self._t) * 1e3
+            self._t = None
+
+    def __enter__(self):
+        self.gc.callbacks.append(self._cb)
+        return self
+
+    def __exit__(self, *exc):
+        self.gc.callbacks.remove(self._cb)
+
+
+def timed_steps(dev, step, steps, warmup):
+    """Run `step()` warmup times, then `steps` times with a torch event pair around each step
+    (the step's span on the GPU, host gaps included, as the training loop sees it).  Returns
+    per-step microseconds, the span of the whole loop, and the garbage collections seen."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize(dev)
+    # No synchronisation between the warm-up and the timed steps: the first timed step then
+    # starts behind queued work, as every step of a training loop does (after a synchronise
+    # it started on an idle GPU and ran 120-300 us long in a 700 us layer step).
+    for _ in range(warmup):
+        step()
+    with GcWatch() as gcw:
+        for a, b in evs:
+            a.record()
+            step()
+            b.record()
+        torch.cuda.synchronize(dev)
+    per = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    total = evs[0][0].elapsed_time(evs[-1][1]) * 1e3
+    return per, total, gcw
+
+
+def step_summary(per, total, gcw, unit_scale=1.0, digits=1):
+    """mean (the loop's span / steps), median, min, max of per-step times."""
+    n = len(per)
+    return {"mean": round(total / n * unit_scale, digits),
+            "median": round(median(per) * unit_scale, digits),
+            "min": round(min(per) * unit_scale, digits),
+            "max": round(max(per) * unit_scale, digits),
+            "slowest_step": int(max(range(n), key=lambda i: per[i])), "steps": n,
+            "gc_collections": gcw.count, "gc_ms": round(gcw.ms, 2)}
+
+
+def time_layer(dev, steps, warmup, reference_profile=False):
     """One Qwen2.5-1.5B decoder layer (testt_amd/layer.py) at B=4 x T=512 = 2048 real tokens:
-    mean forward and forward+backward wall time on the GPU (torch events around the whole
-    layer: every kernel, GEMM and the attention)."""
-    from testt_amd import layer
+    forward and forward+backward time per step on the GPU (a torch event pair around each
+    step: every kernel, GEMM and the attention).  With reference_profile, the layer runs with
+    the reference's memory profile: gate|up recomputed in backward (mlp.RECOMPUTE_GATE_UP) and
+    the NF4 weights unpacked again in backward (nf4.KEEP_UNPACKED_FOR_BACKWARD = False), the
+    work the reference's own layer does."""
+    from testt_amd import layer, mlp, nf4
 
     B, T, H = workloads.BATCH, workloads.SEQ, workloads.HIDDEN
     w = layer.synthetic_layer(dev)
@@ -368,27 +510,34 @@ def time_layer(dev, steps, warmup):
         if backward:
             torch.autograd.backward([s, d], [gs, gd])
 
+    saved = (mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD)
+    if reference_profile:
+        mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD = True, False
     out = {}
-    for name, bwd in (("fwd_bwd_us", True), ("fwd_us", False)):
-        for _ in range(warmup):         # (per mode, as in time_step)
-            step(bwd)
-        torch.cuda.synchronize(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            step(bwd)
-        e1.record()
-        torch.cuda.synchronize(dev)
-        out[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 1)
-    out.update(graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps))
-    out.update(tokens=B * T, batch=B, seq=T, lora_rank=16,
-               note="synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs in fp16, "
-                    "every other op (attention included) a soupk kernel (testt_amd/layer.py); "
-                    "fwd_bwd_us / fwd_us: eager loop (backward on the calling thread, as "
-                    "testt_amd.apply() sets it); "
-                    "graph_*: the same step captured once in a HIP graph and replayed (the "
-                    "layer's GPU time; replays match the eager step bit for bit, "
-                    "tests/test_gpu_layer_graph.py)")
+    try:
+        for name, bwd in (("fwd_bwd", True), ("fwd", False)):
+            per, total, gcw = timed_steps(dev, lambda: step(bwd), steps, warmup)
+            st = step_summary(per, total, gcw)
+            out[f"{name}_us"] = st["mean"]
+            out[f"{name}_us_median"] = st["median"]
+            out[f"{name}_steps"] = st
+        if not reference_profile:
+            out.update(graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps))
+    finally:
+        mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD = saved
+    out.update(tokens=B * T, batch=B, seq=T, lora_rank=16)
+    if reference_profile:
+        out["note"] = ("the reference's work profile: RECOMPUTE_GATE_UP = True (the gate|up GEMM "
+                       "again in backward), KEEP_UNPACKED_FOR_BACKWARD = False (every NF4 weight "
+                       "unpacked again in backward); otherwise as `layer`")
+    else:
+        out["note"] = ("synthetic NF4 weights, LoRA r=16 on q/v; hipBLASLt GEMMs in fp16, "
+                       "every other op (attention included) a soupk kernel (testt_amd/layer.py); "
+                       "*_us: mean per step of the eager loop (backward on the calling thread, "
+                       "as testt_amd.apply() sets it), *_us_median the median step, *_steps the "
+                       "distribution; graph_*: the same step captured once in a HIP graph and "
+                       "replayed (the layer's GPU time; replays match the eager step bit for "
+                       "bit, tests/test_gpu_layer_graph.py)")
     return out
 
 
@@ -476,12 +625,14 @@ def time_attention(dev, steps, warmup):
     return res
 
 
-def time_step(dev, steps, warmup, n_layers=28):
+def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
     """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model (testt_amd/model.py: 28
     decoder layers, final norm, the chunked fused head loss over the 151,936-token vocabulary)
-    at B=4 x T=512 = 2048 real tokens, prompt tokens unlabelled: mean forward and
-    forward+backward wall time on the GPU (torch events around the whole step)."""
-    from testt_amd import model
+    at B=4 x T=512 = 2048 real tokens, prompt tokens unlabelled: forward and forward+backward
+    time per step on the GPU (a torch event pair around each step).  With reference_profile,
+    the reference's work profile: gate|up recomputed and the NF4 weights unpacked again in
+    backward, and the head in the reference's 256-row chunks (head.CHUNK_ROWS = 256)."""
+    from testt_amd import head, mlp, model, nf4
 
     B, T = workloads.BATCH, workloads.SEQ
     m = model.synthetic_model(dev, n_layers=n_layers)
@@ -493,32 +644,36 @@ def time_step(dev, steps, warmup, n_layers=28):
     params = model.lora_parameters(m)
 
     def step(backward):
-        for p in params:
-            p.grad = None
+        for q in params:
+            q.grad = None
         loss, _ = model.fused_forward(m, ids, mask, labels)
         if backward:
             loss.backward()
 
+    saved = (mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD, head.CHUNK_ROWS)
+    if reference_profile:
+        mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD, head.CHUNK_ROWS = True, False, 256
     out = {}
-    # Each mode is warmed up before it is timed: the caching allocator's pool then fits that
-    # mode's allocation pattern, and no device allocation falls inside the timed steps.
-    for name, bwd in (("fwd_bwd_ms", True), ("fwd_ms", False)):
-        for _ in range(warmup):
-            step(bwd)
-        torch.cuda.synchronize(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            step(bwd)
-        e1.record()
-        torch.cuda.synchronize(dev)
-        out[name] = round(e0.elapsed_time(e1) / steps, 3)
+    try:
+        # Each mode is warmed up before it is timed: the caching allocator's pool then fits
+        # that mode's allocation pattern, and no device allocation falls inside the timed steps.
+        for name, bwd in (("fwd_bwd", True), ("fwd", False)):
+            per, total, gcw = timed_steps(dev, lambda: step(bwd), steps, warmup)
+            st = step_summary(per, total, gcw, 1e-3, 3)
+            out[f"{name}_ms"] = st["mean"]
+            out[f"{name}_ms_median"] = st["median"]
+            out[f"{name}_steps"] = st
+    finally:
+        mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD, head.CHUNK_ROWS = saved
     out.update(tokens=B * T, batch=B, seq=T, layers=n_layers,
                tokens_per_s=round(B * T / (out["fwd_bwd_ms"] * 1e-3), 1),
-               note="synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; "
-                    "hipBLASLt GEMMs in fp16, every other op (attention included) a soupk kernel; "
-                    "backward on the calling thread (testt_amd.configure_backward, as apply() "
-                    "sets it)")
+               tokens_per_s_median=round(B * T / (out["fwd_bwd_ms_median"] * 1e-3), 1))
+    out["note"] = ("synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; hipBLASLt "
+                   "GEMMs in fp16, every other op (attention included) a soupk kernel; backward "
+                   "on the calling thread (testt_amd.configure_backward, as apply() sets it)"
+                   + ("; the reference's work profile: RECOMPUTE_GATE_UP = True, "
+                      "KEEP_UNPACKED_FOR_BACKWARD = False, CHUNK_ROWS = 256"
+                      if reference_profile else ""))
     del m
     return out
 
@@ -581,7 +736,7 @@ def copy_peak(dev, mib=1024, reps=6):
 def cpu_baseline(cases, seconds):
     from oracle import baseline as ob     # the CPU leg is the only user of oracle/ here
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads = max(1, len(os.sched_getaffinity(0)))      # every core this process may run on
     torch.set_num_threads(threads)
     runs = [c.cpu(ob) for c in cases]
     for run in runs:                      # warm-up pass (page faults, thread pool)
@@ -603,7 +758,7 @@ def cpu_baseline(cases, seconds):
     except OSError:
         pass
     return {"value": round(total / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "cpu_model": model, "kind": "port",
             "sample": (f"{passes} full pass(es) of the kernel set at the step shape (all 8 "
                        f"kernels, BASELINE configs) through the reference's eager PyTorch path "
                        f"on the CPU (oracle/baseline.py), {elapsed:.1f} s, {model}")}
@@ -826,6 +981,11 @@ def main():
     host_enqueue, span = time_gpu(cases, args.steps, args.warmup, dev)
     extra = build_extra_cases(dev)
     time_gpu(extra, args.steps, args.warmup, dev)
+    shapes = build_shape_cases(dev)
+    log(f"timing {len(shapes)} kernels of the set at the ragged / product-chunk shapes")
+    time_gpu(shapes, args.steps, args.warmup, dev)
+    floor = build_floor_cases(dev)
+    time_gpu(floor, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
     copy_us = copy_reference(cases, dev)
     attn_t = None
@@ -833,19 +993,29 @@ def main():
         log("timing the causal GQA attention kernels at the layer's shape")
         attn_t = time_attention(dev, 50, 5)
         log(f"attention fwd {attn_t['fwd']['us']} us, bwd {attn_t['bwd']['us']} us")
-    step_t = None
+    step_t = step_ref = None
     if not args.no_step:
         log("timing one training step of the 28-layer model at 2048 tokens")
-        step_t = time_step(dev, 5, 2)
-        log(f"step fwd {step_t['fwd_ms']} ms, fwd+bwd {step_t['fwd_bwd_ms']} ms, "
+        step_t = time_step(dev, 10, 3)
+        log(f"step fwd {step_t['fwd_ms']} ms (median {step_t['fwd_ms_median']}), fwd+bwd "
+            f"{step_t['fwd_bwd_ms']} ms (median {step_t['fwd_bwd_ms_median']}), "
             f"{step_t['tokens_per_s']} tokens/s")
+        step_ref = time_step(dev, 5, 2, reference_profile=True)
+        log(f"step, reference work profile: fwd+bwd {step_ref['fwd_bwd_ms']} ms (median "
+            f"{step_ref['fwd_bwd_ms_median']})")
     # Last: the layer timing captures HIP graphs, and eager work of the same process measured
-    # after a capture ran slower (the 28-layer step: 36 ms against 25 ms before it).
-    layer_t = None
+    # after a capture ran slower (the 28-layer step: 36 ms against 25 ms before it); the
+    # reference-profile layer (no capture) runs before it.
+    layer_t = layer_ref = None
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
-        layer_t = time_layer(dev, min(20, max(3, args.steps // 3)), 2)
-        log(f"layer fwd {layer_t['fwd_us']} us, fwd+bwd {layer_t['fwd_bwd_us']} us (eager); "
+        n_layer_steps = max(20, min(100, args.steps // 3))
+        layer_ref = time_layer(dev, n_layer_steps, 3, reference_profile=True)
+        log(f"layer, reference work profile: fwd {layer_ref['fwd_us']} us, fwd+bwd "
+            f"{layer_ref['fwd_bwd_us']} us (median {layer_ref['fwd_bwd_us_median']})")
+        layer_t = time_layer(dev, n_layer_steps, 3)
+        log(f"layer fwd {layer_t['fwd_us']} us (median {layer_t['fwd_us_median']}), fwd+bwd "
+            f"{layer_t['fwd_bwd_us']} us (median {layer_t['fwd_bwd_us_median']}) (eager); "
             f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
             f"{layer_t['graph_fwd_bwd_us']} us")
     kernels = {}
@@ -874,6 +1044,24 @@ def main():
                           "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
         log(f"{c.name:16s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
             f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s  (beyond the set)")
+    other_shapes = {}
+    for c in shapes:
+        mean_us = sum(c.times) / len(c.times)
+        gbps = c.nbytes / (mean_us * 1e-6) / 1e9
+        other_shapes[c.name] = {"kernel": c.kernel, "entry": c.entry,
+                                "us_mean": round(mean_us, 3),
+                                "us_median": round(median(c.times), 3), "bytes": c.nbytes,
+                                "GBps": round(gbps, 1),
+                                "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+        log(f"{c.name:24s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
+            f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s")
+    launch_floor = {c.name: round(median(c.times), 3) for c in floor}
+    launch_floor["note"] = ("median duration of launches timed exactly as the kernels are "
+                            "(dispatch-recorded events, back to back): an empty kernel of 1 and "
+                            "of 1024 workgroups x 256 threads, and a 4 KiB device copy; the "
+                            "fixed cost of any launch on this GPU")
+    log(f"launch floor: empty 1 WG {launch_floor['empty_kernel_1wg']} us, 1024 WG "
+        f"{launch_floor['empty_kernel_1024wg']} us, 4 KiB copy {launch_floor['copy_4KiB']} us")
     dom = max(cases, key=lambda c: sum(c.times))
     dom_us = sum(dom.times) / len(dom.times)
     dom_gbps = dom.nbytes / (dom_us * 1e-6) / 1e9
@@ -901,10 +1089,14 @@ def main():
                             "HIP-event durations",
         "kernels": kernels,
         "kernels_beyond_set": beyond,
+        "kernels_other_shapes": other_shapes,
+        "launch_floor_us": launch_floor,
         "layer": layer_t,
+        "layer_reference_profile": layer_ref,
         "attention": attn_t,
         "gemm_selection": gemm_table or "hipBLASLt heuristic (--heuristic-gemms)",
         "step": step_t,
+        "step_reference_profile": step_ref,
         "copy_peak_GBps": copy_gbps,
         "copy_reference": "kernels[*].copy_us: a plain 16-byte streaming device copy "
                           "(one chunk per thread, non-temporal load, nt|sc1 store) "

@@ -55,6 +55,13 @@ int soupk_time_next_launch(void* start_event, void* stop_event);
 int soupk_bench_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /*
+ * Benchmark reference (no counterpart in the reference): `workgroups` workgroups of 256
+ * threads that do nothing.  bench.py times it like the kernels (the fixed cost of a launch:
+ * dispatch, wave launch and completion) beside a 4 KiB soupk_bench_copy.
+ */
+int soupk_bench_empty(int32_t workgroups, void* stream);
+
+/*
  * NF4 double-quant unpack (replaces the launch of nf4_unpack_kernel, solution/nf4.py:27-45,
  * launched from unpack_into, solution/nf4.py:72-89).
  *   absmax[b] = fp32(fp32(code2[absmax_u8[b]] * absmax2[b / qblock2]) + offset[0])

@@ -73,6 +73,7 @@ def test_version_and_status_strings(lib):
     ("soupk_bench_copy", (None, None, 4096, None)),
     ("soupk_bench_copy", (16, 32, 24, None)),        # not a multiple of 16 bytes
     ("soupk_bench_copy", (16, 32, 0, None)),
+    ("soupk_bench_empty", (0, None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

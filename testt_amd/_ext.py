@@ -44,6 +44,7 @@ SIGNATURES = {
     "soupk_head_stats_grad_rows": [_p, _p, _p, _p, _i64, _p, _p, _p, _p, _f32, _i64, _i64, _p],
     "soupk_time_next_launch": [_p, _p],
     "soupk_bench_copy": [_p, _p, _i64, _p],
+    "soupk_bench_empty": [_i32, _p],
     "soupk_attention_fwd": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p],
     "soupk_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
                             _i32, _f32, _p],

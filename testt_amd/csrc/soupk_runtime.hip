@@ -78,10 +78,21 @@ __global__ __launch_bounds__(kCopyThreads) void bench_copy_kernel(const u32x4* _
   out.store(static_cast<uint32_t>(threadIdx.x) * 16u, v);
 }
 
+// A kernel that does nothing: the benchmark's launch floor (dispatch + completion of a grid
+// with no work), timed like every kernel of the set.
+__global__ __launch_bounds__(256) void bench_empty_kernel() {}
+
 }  // namespace
 }  // namespace soupk
 
 using namespace soupk;
+
+extern "C" __attribute__((visibility("default"))) int soupk_bench_empty(int32_t workgroups,
+                                                                        void* stream) {
+  if (workgroups <= 0) return kInvalid;
+  return launch_kernel(bench_empty_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256),
+                       static_cast<hipStream_t>(stream));
+}
 
 extern "C" __attribute__((visibility("default"))) int soupk_bench_copy(const void* src, void* dst,
                                                                        int64_t bytes,
