@@ -484,7 +484,7 @@ def step_summary(per, total, gcw, unit_scale=1.0, digits=1):
             "gc_collections": gcw.count, "gc_ms": round(gcw.ms, 2)}
 
 
-def time_layer(dev, steps, warmup, reference_profile=False):
+def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
     """One Qwen2.5-1.5B decoder layer (testt_amd/layer.py) at B=4 x T=512 = 2048 real tokens:
     forward and forward+backward time per step on the GPU (a torch event pair around each
     step: every kernel, GEMM and the attention).  With reference_profile, the layer runs with
@@ -495,18 +495,25 @@ def time_layer(dev, steps, warmup, reference_profile=False):
 
     B, T, H = workloads.BATCH, workloads.SEQ, workloads.HIDDEN
     w = layer.synthetic_layer(dev)
-    pos = torch.arange(B * T, device=dev)
+    if lengths is None:
+        pos, key_valid = torch.arange(B * T, device=dev), None
+    else:
+        amask = torch.zeros(B, T, dtype=torch.int64, device=dev)
+        for b, n in enumerate(lengths):
+            amask[b, :n] = 1
+        pos, key_valid = amask.reshape(-1).nonzero().squeeze(1), layer.key_valid_of(amask)
+    M = pos.numel()
     cos, sin = (t.to(dev) for t in workloads.rope_tables(T))
     g = workloads.gen(10)
-    s0 = torch.randn(B * T, H, generator=g).to(dev)
-    d0 = (0.5 * torch.randn(B * T, H, generator=g)).to(torch.float16).to(dev)
-    gs = (1e-2 * torch.randn(B * T, H, generator=g)).to(dev)
-    gd = (1e-2 * torch.randn(B * T, H, generator=g)).to(torch.float16).to(dev)
+    s0 = torch.randn(M, H, generator=g).to(dev)
+    d0 = (0.5 * torch.randn(M, H, generator=g)).to(torch.float16).to(dev)
+    gs = (1e-2 * torch.randn(M, H, generator=g)).to(dev)
+    gd = (1e-2 * torch.randn(M, H, generator=g)).to(torch.float16).to(dev)
 
     def step(backward):
         s_in = s0.detach().requires_grad_(True)
         d_in = d0.detach().requires_grad_(True)
-        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, None)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, key_valid)
         if backward:
             torch.autograd.backward([s, d], [gs, gd])
 
@@ -521,11 +528,13 @@ def time_layer(dev, steps, warmup, reference_profile=False):
             out[f"{name}_us"] = st["mean"]
             out[f"{name}_us_median"] = st["median"]
             out[f"{name}_steps"] = st
-        if not reference_profile:
+        if not reference_profile and lengths is None:
             out.update(graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps))
     finally:
         mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD = saved
-    out.update(tokens=B * T, batch=B, seq=T, lora_rank=16)
+    out.update(tokens=M, batch=B, seq=T, lora_rank=16)
+    if lengths is not None:
+        out["lengths"] = list(lengths)
     if reference_profile:
         out["note"] = ("the reference's work profile: RECOMPUTE_GATE_UP = True (the gate|up GEMM "
                        "again in backward), KEEP_UNPACKED_FOR_BACKWARD = False (every NF4 weight "
@@ -586,26 +595,21 @@ def graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps):
 
 def time_attention(dev, steps, warmup):
     """The causal GQA attention kernels (testt_amd/csrc/attention.hip) at the layer's shape,
-    B=4 x T=512, 12 query / 2 key-value heads of 128: forward and backward (dQ, dK/dV partials,
-    GQA reduce) per call, torch events on the stream they run on.  Algorithmic FLOPs: 4*D per
-    visible (query, key) pair forward (S and P.V), 10*D backward (recomputed S, dP, dV, dK, dQ),
-    T(T+1)/2 visible pairs per (row, head); MFMA-bound, against 2.5 PFLOP/s dense fp16."""
+    B=4 x T=512, 12 query / 2 key-value heads of 128: forward and backward per call, torch
+    events on the stream they run on.  `fwd`/`bwd`: the padded-layout kernels (every position
+    real); `varlen_*`: the kernels the layer runs (token-major rows of the real tokens; the
+    backward with RoPE's backward fused in); `ragged_*`: both at the BASELINE ragged batch
+    (512, 152, 128, 96 real tokens), the padded ones with key flags.  Algorithmic FLOPs: 4*D
+    per visible (query, key) pair forward (S and P.V), 10*D backward (recomputed S, dP, dV, dK,
+    dQ), L(L+1)/2 visible pairs per real row of L tokens and head; MFMA-bound, against
+    2.5 PFLOP/s dense fp16."""
     from testt_amd import attention
 
     B, T, NH, NKV, D = workloads.BATCH, workloads.SEQ, workloads.N_HEADS, workloads.N_KV, 128
-    g = workloads.gen(13)
-    q = torch.randn(B, NH, T, D, generator=g).to(torch.float16).to(dev)
-    k = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
-    v = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
-    dout = torch.randn(B * T, NH * D, generator=g).to(torch.float16).to(dev)
     scale = 1.0 / math.sqrt(D)
-    out, lse = attention.attention_fwd(q, k, v, None, scale)
-    pairs = B * NH * T * (T + 1) / 2
-    res = {}
-    for name, fn, flops in (
-            ("fwd", lambda: attention.attention_fwd(q, k, v, None, scale), 4 * D * pairs),
-            ("bwd", lambda: attention.attention_bwd(q, k, v, None, out, lse, dout, scale),
-             10 * D * pairs)):
+    cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
+
+    def timed(fn):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize(dev)
@@ -615,13 +619,54 @@ def time_attention(dev, steps, warmup):
             fn()
         e1.record()
         torch.cuda.synchronize(dev)
-        us = e0.elapsed_time(e1) * 1e3 / steps
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    def rate(us, flops):
         tflops = flops / (us * 1e-6) / 1e12
-        res[name] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
-                     "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16_TFLOPS, 4)}
-    res.update(shape={"batch": B, "seq": T, "q_heads": NH, "kv_heads": NKV, "head_dim": D},
-               note="causal, no padding; bwd = D + (dQ | dK/dV-partial, one grid) + GQA-reduce "
-                    "launches")
+        return {"us": round(us, 2), "TFLOPs": round(tflops, 1),
+                "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16_TFLOPS, 4)}
+
+    res = {}
+    for tag, lengths in (("", (T,) * B), ("ragged_", (512, 152, 128, 96))):
+        g = workloads.gen(13)
+        pos = workloads.ragged_positions(lengths, T).to(dev)
+        M = pos.numel()
+        pairs = NH * sum(n * (n + 1) / 2 for n in lengths)
+        rows = torch.randn(M, (NH + 2 * NKV) * D, generator=g).to(torch.float16).to(dev)
+        dout = torch.randn(M, NH * D, generator=g).to(torch.float16).to(dev)
+        cu = attention.cu_seqlens_of(pos, B, T)
+        out, lse = attention.attention_varlen_fwd(rows, cu, NH, NKV, scale)
+        rope = (cos, sin, pos, B, T)
+        res[f"{tag}varlen_fwd"] = rate(
+            timed(lambda: attention.attention_varlen_fwd(rows, cu, NH, NKV, scale)),
+            4 * D * pairs)
+        res[f"{tag}varlen_bwd"] = rate(
+            timed(lambda: attention.attention_varlen_bwd(rows, cu, out, lse, dout, scale, NH, NKV,
+                                                         rope=rope)), 10 * D * pairs)
+        # the padded layout of the same tokens (key flags when rows are ragged)
+        q = torch.randn(B, NH, T, D, generator=g).to(torch.float16).to(dev)
+        k = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
+        v = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
+        pdout = torch.randn(B * T, NH * D, generator=g).to(torch.float16).to(dev)
+        valid = None
+        if M != B * T:
+            valid = torch.zeros(B, T, dtype=torch.uint8, device=dev)
+            for b, n in enumerate(lengths):
+                valid[b, :n] = 1
+        pout, plse = attention.attention_fwd(q, k, v, valid, scale)
+        res[f"{tag}fwd"] = rate(timed(lambda: attention.attention_fwd(q, k, v, valid, scale)),
+                                4 * D * pairs)
+        res[f"{tag}bwd"] = rate(
+            timed(lambda: attention.attention_bwd(q, k, v, valid, pout, plse, pdout, scale)),
+            10 * D * pairs)
+    res.update(shape={"batch": B, "seq": T, "q_heads": NH, "kv_heads": NKV, "head_dim": D,
+                      "ragged_lengths": [512, 152, 128, 96]},
+               note="causal; fwd/bwd: padded layout (bwd = D + (dQ | dK/dV-partial, one grid) + "
+                    "GQA-reduce launches); varlen_*: token-major rows of the real tokens, the "
+                    "layer's path (varlen_bwd writes the q|k|v GEMM output's gradient, RoPE's "
+                    "backward fused into its dQ epilogue and GQA reduce); FLOPs count visible "
+                    "pairs of real tokens only, so the padded kernels on the ragged batch are "
+                    "charged only for the real work")
     return res
 
 
@@ -992,7 +1037,11 @@ def main():
     if not args.no_layer:
         log("timing the causal GQA attention kernels at the layer's shape")
         attn_t = time_attention(dev, 50, 5)
-        log(f"attention fwd {attn_t['fwd']['us']} us, bwd {attn_t['bwd']['us']} us")
+        log(f"attention fwd {attn_t['fwd']['us']} us, bwd {attn_t['bwd']['us']} us (padded); "
+            f"varlen fwd {attn_t['varlen_fwd']['us']} us, bwd {attn_t['varlen_bwd']['us']} us; "
+            f"ragged varlen fwd {attn_t['ragged_varlen_fwd']['us']} / bwd "
+            f"{attn_t['ragged_varlen_bwd']['us']} us against padded "
+            f"{attn_t['ragged_fwd']['us']} / {attn_t['ragged_bwd']['us']} us")
     step_t = step_ref = None
     if not args.no_step:
         log("timing one training step of the 28-layer model at 2048 tokens")
@@ -1006,10 +1055,14 @@ def main():
     # Last: the layer timing captures HIP graphs, and eager work of the same process measured
     # after a capture ran slower (the 28-layer step: 36 ms against 25 ms before it); the
     # reference-profile layer (no capture) runs before it.
-    layer_t = layer_ref = None
+    layer_t = layer_ref = layer_ragged = None
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
         n_layer_steps = max(20, min(100, args.steps // 3))
+        layer_ragged = time_layer(dev, n_layer_steps, 3, lengths=(512, 152, 128, 96))
+        log(f"layer at the ragged batch (M = {layer_ragged['tokens']}): fwd "
+            f"{layer_ragged['fwd_us']} us, fwd+bwd {layer_ragged['fwd_bwd_us']} us (median "
+            f"{layer_ragged['fwd_bwd_us_median']})")
         layer_ref = time_layer(dev, n_layer_steps, 3, reference_profile=True)
         log(f"layer, reference work profile: fwd {layer_ref['fwd_us']} us, fwd+bwd "
             f"{layer_ref['fwd_bwd_us']} us (median {layer_ref['fwd_bwd_us_median']})")
@@ -1093,6 +1146,7 @@ def main():
         "launch_floor_us": launch_floor,
         "layer": layer_t,
         "layer_reference_profile": layer_ref,
+        "layer_ragged": layer_ragged,
         "attention": attn_t,
         "gemm_selection": gemm_table or "hipBLASLt heuristic (--heuristic-gemms)",
         "step": step_t,

@@ -249,6 +249,51 @@ int soupk_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         float scale, void* stream);
 
 /*
+ * The RoPE pack forward into the token-major layout (the varlen attention's input; the padded
+ * layout of soupk_rope_pack_fwd, solution/rope.py:24-75, is what it replaces in the layer):
+ * out [rows, (NH + 2*NKV) * 128] fp16 in qkv's layout holds q = rot(qkv_q + lora_q),
+ * k = rot(qkv_k), v = qkv_v + lora_v, bit-identical to what soupk_rope_pack_fwd writes at the
+ * token's padded position; no scatter, no zero rows.  A token whose pos lies outside
+ * [0, B*T) gets a row of zeros.  D must be 128; T >= 1; pointers 16-byte aligned.
+ */
+int soupk_rope_pack_tokens(const uint16_t* qkv, const void* lora_q, const void* lora_v,
+                           int32_t lora_dtype, const float* cos, const float* sin,
+                           const int64_t* pos, uint16_t* out, int64_t rows, int32_t B, int32_t T,
+                           int32_t NH, int32_t NKV, int32_t D, void* stream);
+
+/*
+ * Causal GQA attention over variable-length sequences of real tokens (the reference's stated
+ * next step, "flash-attention with GQA and varlen without padding", README.md:187-189; it
+ * replaces soupk_attention_fwd on the padded layout in the layer).  qkv: [M, (NH+2*NKV)*128]
+ * fp16 token-major rows (soupk_rope_pack_tokens' output).  Sequence b is tokens
+ * cu_seqlens[b] .. cu_seqlens[b+1]-1 (int32 [B+1], non-decreasing from 0 to M; a sequence
+ * whose bounds leave [0, M] is skipped); query i of a sequence attends to its keys j <= i.
+ * Writes out [M, NH*128] fp16 (token-major) and lse [NH, M] (natural log).  16-byte aligned
+ * qkv and out; M * (NH + 2*NKV) * 128 < 2^31.
+ */
+int soupk_attention_varlen_fwd(const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B,
+                               uint16_t* out, float* lse, int64_t M, int32_t NH, int32_t NKV,
+                               int32_t D, float scale, void* stream);
+
+/*
+ * Its backward, with RoPE's backward (solution/rope.py:78-128) fused in: writes dqkv
+ * [M, (NH+2*NKV)*128] fp16, the gradient of the token-major q|k|v rows.  With cos, sin
+ * ([T_rope, 128] fp32) and pos (int64 [M], padded positions; t = pos % T_rope) given, the q and
+ * k gradients are rounded to fp16 and rotated back, (g1*c1 + g2*s2, g2*c2 - g1*s1), exactly as
+ * soupk_attention_bwd followed by soupk_rope_pack_bwd would give them, so dqkv is the gradient
+ * of the rows before rotation (of the q|k|v GEMM output); a token with pos outside
+ * [0, pos_slots) gets zero q and k gradients.  cos, sin, pos all NULL: dqkv is the gradient of
+ * qkv itself.  dK and dV are summed over each key/value head's query heads in a fixed order
+ * (deterministic).  workspace: fp32, round_up(NH*M, 4) + 2*NH*M*128 floats, 16-byte aligned.
+ */
+int soupk_attention_varlen_bwd(const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B,
+                               const uint16_t* out, const uint16_t* dout, const float* lse,
+                               const float* cos, const float* sin, const int64_t* pos,
+                               int64_t pos_slots, int32_t T_rope, float* workspace,
+                               uint16_t* dqkv, int64_t M, int32_t NH, int32_t NKV, int32_t D,
+                               float scale, void* stream);
+
+/*
  * LoRA branch of the q and v projections for rank 16 (peft's lora_B(lora_A(x)) * scaling under
  * fp16 autocast, solution/model.py:195-206 with dropout 0; widening: the reference runs it as
  * separate fp16 GEMMs, casts and a scaling).  y [M, H] fp16; a_q, a_v [16, H] and b_q [NQ, 16],

@@ -151,3 +151,38 @@ def test_unpack_per_layer_is_bit_identical(monkeypatch, keep):
     for name, a, b in zip(("s", "d", "d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"),
                           *runs):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("lengths", [(64, 37), (64, 64), (0, 9)])
+def test_varlen_attention_path_is_bit_identical(monkeypatch, lengths):
+    """The layer's varlen path (RopeAttention over the real tokens) against its padded path
+    (RopePack, attention with key flags, gather): for right-padded rows the same arithmetic in
+    the same order, so the same outputs and gradients, bit for bit."""
+    batch, seq = len(lengths), 64
+    w = layer.synthetic_layer(DEV, seed=13)
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(6)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    runs = []
+    for varlen in (True, False):
+        monkeypatch.setattr(layer, "USE_VARLEN_ATTENTION", varlen)
+        s_in = s0.clone().requires_grad_(True)
+        d_in = d0.clone().requires_grad_(True)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                                   layer.key_valid_of(amask))
+        torch.autograd.backward([s, d], [gs, gd])
+        runs.append([s.detach(), d.detach(), s_in.grad, d_in.grad] +
+                    [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+    for name, a, b in zip(("s", "d", "d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"),
+                          *runs):
+        assert torch.equal(a, b), name

@@ -48,6 +48,11 @@ SIGNATURES = {
     "soupk_attention_fwd": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p],
     "soupk_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
                             _i32, _f32, _p],
+    "soupk_rope_pack_tokens": [_p, _p, _p, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32,
+                               _i32, _p],
+    "soupk_attention_varlen_fwd": [_p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _f32, _p],
+    "soupk_attention_varlen_bwd": [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p,
+                                   _i64, _i32, _i32, _i32, _f32, _p],
     "soupk_lora_fwd": [_p, _p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
     "soupk_lora_bwd_rows": [_p, _i64, _p, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _i64, _i32,
                             _i32, _i32, _i32, _p],

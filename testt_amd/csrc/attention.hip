@@ -33,6 +33,7 @@
 // 4-bank groups), transposed tiles [128][68] halves (8-byte reads of 16 lanes hit 16 distinct
 // 2-bank pairs).
 
+#include "fastdiv.hpp"
 #include "soupk_common.hpp"
 
 namespace soupk {
@@ -113,6 +114,12 @@ __device__ __forceinline__ void tile_item(int it, int& rp, int& dc) {
   dc = 4 * (wi >> 1) + (lane & 1) + 2 * ((lane >> 4) & 1);
 }
 
+// Row t of a tile source with row stride `ld` elements.  The entry points keep every row offset
+// of a sequence below 2^31 elements, so it is formed with one 32-bit multiply.
+__device__ __forceinline__ const uint16_t* row_at(const uint16_t* base, int t, int64_t ld) {
+  return base + static_cast<uint32_t>(t) * static_cast<uint32_t>(ld);
+}
+
 __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* src, int64_t stride,
                                           int r0, int nrows) {
 #pragma unroll
@@ -120,8 +127,8 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* src, int6
     int rp, dc;
     tile_item(it, rp, dc);
     const int t0 = min(r0 + 2 * rp, nrows - 1), t1 = min(r0 + 2 * rp + 1, nrows - 1);
-    r.a[it] = *reinterpret_cast<const u32x4*>(src + t0 * stride + 8 * dc);
-    r.b[it] = *reinterpret_cast<const u32x4*>(src + t1 * stride + 8 * dc);
+    r.a[it] = *reinterpret_cast<const u32x4*>(row_at(src, t0, stride) + 8 * dc);
+    r.b[it] = *reinterpret_cast<const u32x4*>(row_at(src, t1, stride) + 8 * dc);
   }
 }
 
@@ -179,27 +186,111 @@ __device__ __forceinline__ uint32_t flag_word(const uint8_t* kflag, int n, int g
   return *reinterpret_cast<const uint32_t*>(kflag + 16 * n + 4 * gr);
 }
 
-// Grid: x = head, y = batch row, z = block index from the heaviest (most key blocks) down, so
-// that the longest workgroups are dispatched first.
-__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
-    const uint8_t* key_valid, uint16_t* __restrict__ out, float* __restrict__ lse, int T, int NH,
-    int NKV, float scale_log2) {
-  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
-  __shared__ __align__(16) _Float16 Vt[kD * kTStride];
-  __shared__ __align__(16) uint8_t kflag[kBK];
-  const int nqb = (T + kBQ - 1) / kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.z);
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int g = h / (NH / NKV);
+// ---- the rows of one (sequence, head) ----------------------------------------------------------
+// Both layouts reduce to: a sequence of `len` rows; row t of Q at q + t*ld_q, of K / V at
+// k / v + t*ld_kv, of O and dO at out / dout + t*ld_o (token-major); its lse and D at lse[t],
+// delta[t]; its dK / dV partials at row `plane + t` of the partial buffers; key flags (padded
+// layout only) at valid[t].
+//   padded [B, heads, T, D]: a sequence is a batch row (len = T, flags from key_valid);
+//   varlen: a sequence is tokens [cu[b], cu[b+1]) of the token-major q|k|v rows [M, W] that
+//           soupk_rope_pack_tokens writes (every token real, no flags; lse, D and the
+//           partials are [NH, M] planes).
+struct AttnParams {
+  const uint16_t* q;        // padded q, or the varlen q|k|v rows
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint8_t* key_valid;
+  const int32_t* cu;        // varlen: [B + 1] sequence starts
+  uint16_t* out;
+  const uint16_t* dout;
+  float* lse;
+  float* delta;
+  uint16_t* dq;             // padded dq [B, NH, T, D]; varlen dq|dk|dv rows [M, W]
+  uint16_t* dk;             // padded dk, dv (the reduce kernel's outputs)
+  uint16_t* dv;
+  float* dk_part;
+  float* dv_part;
+  const float* cos;         // varlen backward: the RoPE tables [rope_T, D] (null: no rotation)
+  const float* sin;
+  const int64_t* pos;       // varlen backward: padded position of each token
+  int64_t pos_slots;        // positions at or past this have no table row
+  FastDiv rope_div;         // divides by rope_T
+  int T, NH, NKV;
+  int64_t M, W;             // varlen: tokens, q|k|v row stride
+  float scale, scale_log2;
+};
+
+struct SeqHead {
+  int len;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t ld_q, ld_kv, ld_o;
+  const uint8_t* valid;
+  uint16_t* out;
+  const uint16_t* dout;
+  float* lse;
+  const float* delta;
+  int64_t tok0;             // token index of row 0 (varlen)
+  int64_t plane;            // partial-buffer row of row 0
+};
+
+template <bool VARLEN>
+__device__ __forceinline__ SeqHead seq_head(const AttnParams& p, int b, int h) {
+  const int g = h / (p.NH / p.NKV);
+  const int64_t HD = static_cast<int64_t>(p.NH) * kD;
+  SeqHead s;
+  if constexpr (VARLEN) {
+    // Sequence bounds come from device memory: a bound outside [0, M], or an end before its
+    // start, makes the sequence empty (nothing read, nothing written).
+    const int64_t s0 = p.cu[b], s1 = p.cu[b + 1];
+    const bool ok = s0 >= 0 && s1 >= s0 && s1 <= p.M;
+    s.len = ok ? static_cast<int>(s1 - s0) : 0;
+    const int64_t base = ok ? s0 : 0;
+    s.q = p.q + base * p.W + h * kD;
+    s.k = p.q + base * p.W + (p.NH + g) * kD;
+    s.v = p.q + base * p.W + (p.NH + p.NKV + g) * kD;
+    s.ld_q = s.ld_kv = p.W;
+    s.valid = nullptr;
+    s.out = p.out + base * HD + h * kD;
+    s.dout = p.dout + base * HD + h * kD;
+    s.ld_o = HD;
+    s.lse = p.lse + h * p.M + base;
+    s.delta = p.delta + h * p.M + base;
+    s.tok0 = base;
+    s.plane = h * p.M + base;
+  } else {
+    const int64_t T = p.T;
+    s.len = p.T;
+    s.q = p.q + (static_cast<int64_t>(b) * p.NH + h) * T * kD;
+    s.k = p.k + (static_cast<int64_t>(b) * p.NKV + g) * T * kD;
+    s.v = p.v + (static_cast<int64_t>(b) * p.NKV + g) * T * kD;
+    s.ld_q = s.ld_kv = kD;
+    s.valid = p.key_valid != nullptr ? p.key_valid + b * T : nullptr;
+    s.out = p.out + b * T * HD + h * kD;
+    s.dout = p.dout + b * T * HD + h * kD;
+    s.ld_o = HD;
+    s.lse = p.lse + (static_cast<int64_t>(b) * p.NH + h) * T;
+    s.delta = p.delta + (static_cast<int64_t>(b) * p.NH + h) * T;
+    s.tok0 = b * T;
+    s.plane = (static_cast<int64_t>(b) * p.NH + h) * T;
+  }
+  return s;
+}
+
+// One query block of one (sequence, head): flash-attention forward.
+__device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHead& sh, int qb,
+                                               _Float16* Ks, _Float16* Vt, uint8_t* kflag) {
+  const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
   const int q_abs = qb * kBQ + 16 * w + ql;
-  const uint16_t* qrow = q + ((static_cast<int64_t>(b) * NH + h) * T + min(q_abs, T - 1)) * kD;
-  const uint16_t* kbase = k + (static_cast<int64_t>(b) * NKV + g) * T * kD;
-  const uint16_t* vbase = v + (static_cast<int64_t>(b) * NKV + g) * T * kD;
-  const uint8_t* valid = key_valid != nullptr ? key_valid + static_cast<int64_t>(b) * T : nullptr;
+  const uint16_t* qrow = row_at(sh.q, min(q_abs, T - 1), sh.ld_q);
+  const uint16_t* kbase = sh.k;
+  const uint16_t* vbase = sh.v;
+  const uint8_t* valid = sh.valid;
   const bool has_valid = valid != nullptr;
+  const float scale_log2 = p.scale_log2;
 
   // Q^T operand: 4 k-steps of 32 dims, lane holds Q[q][32s + 8gr .. +7]
   h8 qf[4];
@@ -211,8 +302,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   float m_ref = -INFINITY, lsum = 0.f;
 
   TileRegs kr, vr;
-  load_tile(kr, kbase, kD, 0, T);
-  load_tile(vr, vbase, kD, 0, T);
+  load_tile(kr, kbase, sh.ld_kv, 0, T);
+  load_tile(vr, vbase, sh.ld_kv, 0, T);
   uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
   for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
@@ -220,8 +311,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
     store_tile<false, true>(nullptr, Vt, vr);
     if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
-    load_tile(kr, kbase, kD, (kb + 1) * kBK, T);   // the next block (clamped past the end)
-    load_tile(vr, vbase, kD, (kb + 1) * kBK, T);
+    load_tile(kr, kbase, sh.ld_kv, (kb + 1) * kBK, T);   // the next block (clamped past the end)
+    load_tile(vr, vbase, sh.ld_kv, (kb + 1) * kBK, T);
     fl_raw = load_flag_raw(valid, kbase, (kb + 1) * kBK, T);
     issue_here();
     // S^T for the 4 key tiles
@@ -278,9 +369,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(x[n][i] - m_use);  // 2^-inf = 0
-        ps += p;
-        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p);
+        const float pr = __builtin_amdgcn_exp2f(x[n][i] - m_use);  // 2^-inf = 0
+        ps += pr;
+        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(pr);
       }
     }
     lsum += ps;
@@ -295,17 +386,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(
   const float l_tot = column_sum(lsum);
   if (q_abs >= T) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  uint16_t* orow = out + (static_cast<int64_t>(b) * T + q_abs) * (static_cast<int64_t>(NH) * kD) +
-                   h * kD;
+  uint16_t* orow = sh.out + static_cast<uint32_t>(q_abs) * static_cast<uint32_t>(sh.ld_o);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const f4 o = acc[t] * inv;
     *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
                                                                 pack_h2(o[2], o[3])};
   }
-  if (gr == 0)
-    lse[(static_cast<int64_t>(b) * NH + h) * T + q_abs] =
-        l_tot > 0.f ? (m_ref + log2f(l_tot)) * kLn2 : INFINITY;
+  if (gr == 0) sh.lse[q_abs] = l_tot > 0.f ? (m_ref + log2f(l_tot)) * kLn2 : INFINITY;
+}
+
+// Grid: x = head, y = sequence (batch row), z = query-block slot: slot z is query block
+// nqb-1-z of its sequence, so the heaviest blocks (the most key blocks) are dispatched first.
+// The host gives z at least as many slots as the longest possible sequence has blocks (T for
+// the padded layout, ceil(M/64) for varlen, since no sequence holds more than M tokens): slots
+// past a sequence's blocks exit at once.  (A loop over several blocks per workgroup cost
+// 0.5 us forward and backward at the step's shape; the idle workgroups measured nothing.)
+template <bool VARLEN>
+__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(AttnParams p) {
+  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
+  __shared__ __align__(16) _Float16 Vt[kD * kTStride];
+  __shared__ __align__(16) uint8_t kflag[kBK];
+  const SeqHead sh = seq_head<VARLEN>(p, blockIdx.y, blockIdx.x);
+  const int qb = (sh.len + kBQ - 1) / kBQ - 1 - static_cast<int>(blockIdx.z);
+  if (qb >= 0) attn_fwd_block(p, sh, qb, Ks, Vt, kflag);
 }
 
 // ---- backward ------------------------------------------------------------------------------
@@ -361,28 +465,57 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_delta_kernel(
 // LDS of the backward workgroups (the larger of the two kinds: dKdV's Q, Q^T, dO, dO^T tiles).
 constexpr int kBwdLdsBytes = 2 * (kBQ * kRStride + kD * kTStride) * 2 + 2 * kBQ * 4;
 
-__device__ __forceinline__ void attn_bwd_dq(
-    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
-    const uint8_t* key_valid, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, uint16_t* __restrict__ dq, int T, int NH, int NKV,
-    float scale, float scale_log2, int qb, unsigned char* smem) {
+// fp32 -> fp16 -> fp32: the value a kernel that stores fp16 hands to the next one.
+__device__ __forceinline__ float round_h(float x) { return lo_h(pack_h2(x, 0.f)); }
+
+// Table rows (cos, sin) of the token's position for the transposed rotation, or null when the
+// token has none (no tables, or a position outside [0, pos_slots)).
+__device__ __forceinline__ bool rope_rows(const AttnParams& p, int64_t tok, const float** c,
+                                          const float** sn) {
+  if (p.cos == nullptr) return false;
+  const int64_t ps = p.pos[tok];
+  if (ps < 0 || ps >= p.pos_slots) return false;
+  const uint32_t pu = static_cast<uint32_t>(ps);
+  const uint32_t t = pu - p.rope_div.div(pu) * p.rope_div.d;
+  *c = p.cos + static_cast<int64_t>(t) * kD;
+  *sn = p.sin + static_cast<int64_t>(t) * kD;
+  return true;
+}
+
+// The transposed rotation of RoPE's backward (solution/rope.py:78-128) on fp16-rounded
+// gradients g1 (dims d..d+3 of the first half) and g2 (the same dims of the second half):
+// (g1*c1 + g2*s2, g2*c2 - g1*s1), each product rounded.
+__device__ __forceinline__ void rope_bwd4(const float* c, const float* sn, int d, const f4& g1,
+                                          const f4& g2, f4& o1, f4& o2) {
+  const f4 c1 = *reinterpret_cast<const f4*>(c + d), c2 = *reinterpret_cast<const f4*>(c + d + 64);
+  const f4 s1 = *reinterpret_cast<const f4*>(sn + d);
+  const f4 s2 = *reinterpret_cast<const f4*>(sn + d + 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o1[i] = g1[i] * c1[i] + g2[i] * s2[i];
+    o2[i] = g2[i] * c2[i] - g1[i] * s1[i];
+  }
+}
+
+template <bool VARLEN>
+__device__ __forceinline__ void attn_bwd_dq(const AttnParams& p, const SeqHead& sh, int h, int b,
+                                            int qb, unsigned char* smem) {
   _Float16* Ks = reinterpret_cast<_Float16*>(smem);
   _Float16* Vs = Ks + kBK * kRStride;
   _Float16* Kt = Vs + kBK * kRStride;
   uint8_t* kflag = reinterpret_cast<uint8_t*>(Kt + kD * kTStride);
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int g = h / (NH / NKV);
+  const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
   const int q_abs = qb * kBQ + 16 * w + ql;
   const int qc = min(q_abs, T - 1);
-  const int64_t HD = static_cast<int64_t>(NH) * kD;
-  const uint16_t* qrow = q + ((static_cast<int64_t>(b) * NH + h) * T + qc) * kD;
-  const uint16_t* dorow = dout + (static_cast<int64_t>(b) * T + qc) * HD + h * kD;
-  const uint16_t* kbase = k + (static_cast<int64_t>(b) * NKV + g) * T * kD;
-  const uint16_t* vbase = v + (static_cast<int64_t>(b) * NKV + g) * T * kD;
-  const uint8_t* valid = key_valid != nullptr ? key_valid + static_cast<int64_t>(b) * T : nullptr;
+  const uint16_t* qrow = row_at(sh.q, qc, sh.ld_q);
+  const uint16_t* dorow = row_at(sh.dout, qc, sh.ld_o);
+  const uint16_t* kbase = sh.k;
+  const uint16_t* vbase = sh.v;
+  const uint8_t* valid = sh.valid;
   const bool has_valid = valid != nullptr;
+  const float scale_log2 = p.scale_log2;
 
   h8 qf[4], dof[4];
 #pragma unroll
@@ -390,16 +523,15 @@ __device__ __forceinline__ void attn_bwd_dq(
     qf[s] = *reinterpret_cast<const h8*>(qrow + 32 * s + 8 * gr);
     dof[s] = *reinterpret_cast<const h8*>(dorow + 32 * s + 8 * gr);
   }
-  const float dsum = delta[(static_cast<int64_t>(b) * NH + h) * T + qc];
-  const float lse_q = lse[(static_cast<int64_t>(b) * NH + h) * T + qc];
-  const float lse2 = lse_q * kLog2e;  // +inf: no visible key, every p = 0
+  const float dsum = sh.delta[qc];
+  const float lse2 = sh.lse[qc] * kLog2e;  // +inf: no visible key, every p = 0
 
   f4 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
   TileRegs kr, vr;
-  load_tile(kr, kbase, kD, 0, T);
-  load_tile(vr, vbase, kD, 0, T);
+  load_tile(kr, kbase, sh.ld_kv, 0, T);
+  load_tile(vr, vbase, sh.ld_kv, 0, T);
   uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
   for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
@@ -407,8 +539,8 @@ __device__ __forceinline__ void attn_bwd_dq(
     store_tile<true, false>(Vs, nullptr, vr);
     if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
-    load_tile(kr, kbase, kD, (kb + 1) * kBK, T);   // the next block (clamped past the end)
-    load_tile(vr, vbase, kD, (kb + 1) * kBK, T);
+    load_tile(kr, kbase, sh.ld_kv, (kb + 1) * kBK, T);   // the next block (clamped past the end)
+    load_tile(vr, vbase, sh.ld_kv, (kb + 1) * kBK, T);
     fl_raw = load_flag_raw(valid, kbase, (kb + 1) * kBK, T);
     issue_here();
     const bool masked = kb == qb || has_valid;
@@ -432,8 +564,8 @@ __device__ __forceinline__ void attn_bwd_dq(
       for (int i = 0; i < 4; ++i) {
         const int key = kb * kBK + 16 * n + 4 * gr + i;
         const bool vis = !masked || (key <= q_abs && ((fl >> (8 * i)) & 0xffu) != 0);
-        const float p = vis ? __builtin_amdgcn_exp2f(sc[i] * scale_log2 - lse2) : 0.f;
-        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - dsum));
+        const float pr = vis ? __builtin_amdgcn_exp2f(sc[i] * scale_log2 - lse2) : 0.f;
+        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(pr * (dp[i] - dsum));
       }
     }
     // dQ^T += K^T dS^T
@@ -445,42 +577,76 @@ __device__ __forceinline__ void attn_bwd_dq(
     }
   }
   if (q_abs >= T) return;
-  uint16_t* dqrow = dq + ((static_cast<int64_t>(b) * NH + h) * T + q_abs) * kD;
+  const float scale = p.scale;
+  if constexpr (VARLEN) {
+    // dq|dk|dv row of the token; with tables, dQ is rounded to fp16 (the value an attention
+    // backward would store) and rotated back (RoPE's backward) before its store.
+    const int64_t tok = sh.tok0 + q_abs;
+    uint16_t* dqrow = p.dq + tok * p.W + h * kD;
+    const float* c = nullptr;
+    const float* sn = nullptr;
+    if (rope_rows(p, tok, &c, &sn)) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const f4 o = acc[t] * scale;
-    *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
-                                                                 pack_h2(o[2], o[3])};
+      for (int t = 0; t < 4; ++t) {
+        f4 g1, g2, o1, o2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          g1[i] = round_h(acc[t][i] * scale);
+          g2[i] = round_h(acc[t + 4][i] * scale);
+        }
+        const int d = 16 * t + 4 * gr;
+        rope_bwd4(c, sn, d, g1, g2, o1, o2);
+        *reinterpret_cast<u32x2*>(dqrow + d) = u32x2{pack_h2(o1[0], o1[1]), pack_h2(o1[2], o1[3])};
+        *reinterpret_cast<u32x2*>(dqrow + d + 64) =
+            u32x2{pack_h2(o2[0], o2[1]), pack_h2(o2[2], o2[3])};
+      }
+      return;
+    }
+    if (p.cos != nullptr) {   // a token without a table row: no gradient reaches its input
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * gr) = u32x2{0u, 0u};
+      return;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const f4 o = acc[t] * scale;
+      *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
+                                                                   pack_h2(o[2], o[3])};
+    }
+  } else {
+    uint16_t* dqrow = p.dq + ((static_cast<int64_t>(b) * p.NH + h) * p.T + q_abs) * kD;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const f4 o = acc[t] * scale;
+      *reinterpret_cast<u32x2*>(dqrow + 16 * t + 4 * gr) = u32x2{pack_h2(o[0], o[1]),
+                                                                   pack_h2(o[2], o[3])};
+    }
   }
 }
 
-__device__ __forceinline__ void attn_bwd_dkdv(
-    const uint16_t* q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint8_t* __restrict__ key_valid, const uint16_t* dout, const float* lse,
-    const float* delta, float* __restrict__ dk_part, float* __restrict__ dv_part,
-    int T, int NH, int NKV, float scale, float scale_log2, int kb, unsigned char* smem) {
+__device__ __forceinline__ void attn_bwd_dkdv(const AttnParams& p, const SeqHead& sh, int kb,
+                                              unsigned char* smem) {
   _Float16* Qs = reinterpret_cast<_Float16*>(smem);
   _Float16* Qt = Qs + kBQ * kRStride;
   _Float16* Ds = Qt + kD * kTStride;    // dO row-major
   _Float16* Dt = Ds + kBQ * kRStride;   // dO transposed
   float* lse2_s = reinterpret_cast<float*>(Dt + kD * kTStride);
   float* delta_s = lse2_s + kBQ;
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int g = h / (NH / NKV);
+  const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int kl = lane & 15, gr = lane >> 4;
   const int key_abs = kb * kBK + 16 * w + kl;
   const int kc = min(key_abs, T - 1);
-  const bool key_vis = key_abs < T && (key_valid == nullptr ||
-                                       key_valid[static_cast<int64_t>(b) * T + key_abs] != 0);
-  const bool has_valid = key_valid != nullptr;
-  const int64_t HD = static_cast<int64_t>(NH) * kD;
-  const uint16_t* krow = k + ((static_cast<int64_t>(b) * NKV + g) * T + kc) * kD;
-  const uint16_t* vrow = v + ((static_cast<int64_t>(b) * NKV + g) * T + kc) * kD;
-  const uint16_t* qbase = q + (static_cast<int64_t>(b) * NH + h) * T * kD;
-  const uint16_t* dobase = dout + static_cast<int64_t>(b) * T * HD + h * kD;
-  const float* lse_bh = lse + (static_cast<int64_t>(b) * NH + h) * T;
-  const float* del_bh = delta + (static_cast<int64_t>(b) * NH + h) * T;
+  const bool key_vis = key_abs < T && (sh.valid == nullptr || sh.valid[key_abs] != 0);
+  const bool has_valid = sh.valid != nullptr;
+  const uint16_t* krow = row_at(sh.k, kc, sh.ld_kv);
+  const uint16_t* vrow = row_at(sh.v, kc, sh.ld_kv);
+  const uint16_t* qbase = sh.q;
+  const uint16_t* dobase = sh.dout;
+  const float* lse_bh = sh.lse;
+  const float* del_bh = sh.delta;
+  const float scale_log2 = p.scale_log2;
 
   // K^T and V^T operands (B of S = Q K^T and of dP = dO V^T): lane holds row key of K / V,
   // dims 32s + 8gr .. +7
@@ -497,9 +663,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(
   TileRegs qr, dr;
   float lse_raw, del_raw;   // tested against T only when stored (see load_flag_raw)
   auto load_block = [&](int q0) {
-    load_tile(qr, qbase, kD, q0, T);
-    load_tile(dr, dobase, HD, q0, T);
-    const int t = min(q0 + (threadIdx.x & (kBQ - 1)), T - 1);
+    load_tile(qr, qbase, sh.ld_q, q0, T);
+    load_tile(dr, dobase, sh.ld_o, q0, T);
+    const int t = min(q0 + (static_cast<int>(threadIdx.x) & (kBQ - 1)), T - 1);
     lse_raw = lse_bh[t];
     del_raw = del_bh[t];
   };
@@ -545,9 +711,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(
         // (bitwise, not short-circuit: no per-lane branch)
         const bool vis = !masked | (key_vis & (key_abs <= q_abs) & (q_abs < T));
         const float e = __builtin_amdgcn_exp2f(sc[i] * scale_log2 - l2[i]);
-        const float p = vis ? e : 0.f;
-        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p);
-        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(p * (dp[i] - dl[i]));
+        const float pr = vis ? e : 0.f;
+        pb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(pr);
+        dsb[n >> 1][4 * (n & 1) + i] = static_cast<_Float16>(pr * (dp[i] - dl[i]));
       }
     }
     // dV^T += dO^T P, dK^T += Q^T dS  (contraction over the block's queries)
@@ -564,8 +730,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(
   }
   if (key_abs >= T) return;
   // C: rows = dims 16t + 4gr + i, column = this lane's key
-  float* dkp = dk_part + ((static_cast<int64_t>(b) * NH + h) * T + key_abs) * kD;
-  float* dvp = dv_part + ((static_cast<int64_t>(b) * NH + h) * T + key_abs) * kD;
+  float* dkp = p.dk_part + (sh.plane + key_abs) * kD;
+  float* dvp = p.dv_part + (sh.plane + key_abs) * kD;
+  const float scale = p.scale;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     *reinterpret_cast<f4*>(dkp + 16 * t + 4 * gr) = dk[t] * scale;
@@ -573,21 +740,20 @@ __device__ __forceinline__ void attn_bwd_dkdv(
   }
 }
 
-// Grid z = 2 * blocks: z even -> dKdV of key block z/2 (block 0 sees the most query blocks),
-// z odd -> dQ of query block nb - 1 - z/2 (the last sees the most key blocks).
-__global__ __launch_bounds__(kAttnThreads) void attn_bwd_kernel(
-    const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* key_valid,
-    const uint16_t* dout, const float* lse, const float* delta, uint16_t* dq, float* dk_part,
-    float* dv_part, int T, int NH, int NKV, float scale, float scale_log2) {
+// Grid z = 2 * slots (as the forward's): z even -> dKdV of key block z/2 (block 0 sees the
+// most query blocks), z odd -> dQ of query block nqb-1-z/2 (the last sees the most key blocks).
+template <bool VARLEN>
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_kernel(AttnParams p) {
   __shared__ __align__(16) unsigned char smem[kBwdLdsBytes];
-  const int nb = (T + kBQ - 1) / kBQ;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const SeqHead sh = seq_head<VARLEN>(p, b, h);
+  const int nb = (sh.len + kBQ - 1) / kBQ;
   const int z = static_cast<int>(blockIdx.z);
-  if ((z & 1) == 0)
-    attn_bwd_dkdv(q, k, v, key_valid, dout, lse, delta, dk_part, dv_part, T, NH, NKV, scale,
-                  scale_log2, z >> 1, smem);
-  else
-    attn_bwd_dq(q, k, v, key_valid, dout, lse, delta, dq, T, NH, NKV, scale, scale_log2,
-                nb - 1 - (z >> 1), smem);
+  if ((z & 1) == 0) {
+    if ((z >> 1) < nb) attn_bwd_dkdv(p, sh, z >> 1, smem);
+  } else if (nb - 1 - (z >> 1) >= 0) {
+    attn_bwd_dq<VARLEN>(p, sh, h, b, nb - 1 - (z >> 1), smem);
+  }
 }
 
 // dK, dV of each key/value head: the sum of its NH/NKV query heads' partials, in head order.
@@ -611,13 +777,80 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
   reinterpret_cast<u32x2*>(dv)[i] = u32x2{pack_h2(sv[0], sv[1]), pack_h2(sv[2], sv[3])};
 }
 
-// Shape checks shared by both entry points.
+// The varlen form of the reduce: item (token, key/value head g, 4-dim slice j of the first half)
+// sums dims 4j..4j+3 and 4j+64..+67 of the dK and dV partials of the group's query heads (head
+// order, as above), rounds to fp16 and writes them into the token's dq|dk|dv row, dK rotated
+// back (RoPE's backward) when tables are given.
+__global__ __launch_bounds__(256) void attn_bwd_reduce_varlen_kernel(AttnParams p,
+                                                                      int64_t items) {
+  const int64_t it = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (it >= items) return;
+  const int j = static_cast<int>(it & 15);
+  const int64_t tg = it >> 4;
+  const int64_t tok = tg / p.NKV;
+  const int g = static_cast<int>(tg - tok * p.NKV);
+  const int rep = p.NH / p.NKV;
+  const int d = 4 * j;
+  f4 k1 = {0.f, 0.f, 0.f, 0.f}, k2 = k1, v1 = k1, v2 = k1;
+  for (int r = 0; r < rep; ++r) {
+    const int64_t row = (static_cast<int64_t>(g * rep + r) * p.M + tok) * kD;
+    k1 = k1 + *reinterpret_cast<const f4*>(p.dk_part + row + d);
+    k2 = k2 + *reinterpret_cast<const f4*>(p.dk_part + row + d + 64);
+    v1 = v1 + *reinterpret_cast<const f4*>(p.dv_part + row + d);
+    v2 = v2 + *reinterpret_cast<const f4*>(p.dv_part + row + d + 64);
+  }
+  uint16_t* krow = p.dq + tok * p.W + (p.NH + g) * kD;
+  uint16_t* vrow = p.dq + tok * p.W + (p.NH + p.NKV + g) * kD;
+  if (p.cos != nullptr) {
+    const float* c = nullptr;
+    const float* sn = nullptr;
+    if (rope_rows(p, tok, &c, &sn)) {
+      f4 g1, g2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g1[i] = round_h(k1[i]);
+        g2[i] = round_h(k2[i]);
+      }
+      rope_bwd4(c, sn, d, g1, g2, k1, k2);
+    } else {
+      k1 = k2 = f4{0.f, 0.f, 0.f, 0.f};   // no table row: no gradient reaches the input
+    }
+  }
+  *reinterpret_cast<u32x2*>(krow + d) = u32x2{pack_h2(k1[0], k1[1]), pack_h2(k1[2], k1[3])};
+  *reinterpret_cast<u32x2*>(krow + d + 64) = u32x2{pack_h2(k2[0], k2[1]), pack_h2(k2[2], k2[3])};
+  *reinterpret_cast<u32x2*>(vrow + d) = u32x2{pack_h2(v1[0], v1[1]), pack_h2(v1[2], v1[3])};
+  *reinterpret_cast<u32x2*>(vrow + d + 64) = u32x2{pack_h2(v2[0], v2[1]), pack_h2(v2[2], v2[3])};
+}
+
+// Shape checks shared by the padded entry points.
 int check_shape(int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D, float scale) {
   if (B < 0 || T < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
   if (!(scale > 0.f)) return kInvalid;
   if (B > 65535 || 2 * ((T + kBQ - 1) / kBQ) > 65535) return kInvalid;   // grid y, z limits
   if (static_cast<int64_t>(B) * NH * T * kD >= (int64_t{1} << 40)) return kInvalid;
+  if (static_cast<int64_t>(T) * NH * kD >= (int64_t{1} << 31)) return kInvalid;  // row offsets
   return kOk;
+}
+
+// ... and by the varlen ones (the grid's z covers ceil(M/64) block slots, twice backward).
+int check_varlen(int32_t B, int64_t M, int32_t NH, int32_t NKV, int32_t D, float scale) {
+  if (B < 0 || M < 0 || NH <= 0 || NKV <= 0 || NH % NKV != 0 || D != kD) return kInvalid;
+  if (!(scale > 0.f)) return kInvalid;
+  if (B > 65535 || 2 * ((M + kBQ - 1) / kBQ) > 65535) return kInvalid;
+  if (M * (NH + 2 * NKV) * kD >= (int64_t{1} << 31)) return kInvalid;   // 32-bit row offsets
+  return kOk;
+}
+
+bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+
+AttnParams base_params(int32_t NH, int32_t NKV, float scale) {
+  AttnParams p = {};
+  p.NH = NH;
+  p.NKV = NKV;
+  p.scale = scale;
+  p.scale_log2 = scale * kLog2e;
+  p.rope_div = FastDiv(1);
+  return p;
 }
 
 }  // namespace
@@ -633,14 +866,21 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_fwd(
   if (rc != kOk) return rc;
   if (B == 0 || T == 0) return kOk;
   if (!q || !k || !v || !out || !lse) return kInvalid;
-  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k),
-                        static_cast<const void*>(v), static_cast<const void*>(out)})
-    if (reinterpret_cast<uintptr_t>(p) & 15) return kInvalid;
+  for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k),
+                          static_cast<const void*>(v), static_cast<const void*>(out)})
+    if (misaligned16(ptr)) return kInvalid;
+  AttnParams p = base_params(NH, NKV, scale);
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.key_valid = key_valid;
+  p.out = out;
+  p.lse = lse;
+  p.T = T;
   const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B),
                   static_cast<unsigned>((T + kBQ - 1) / kBQ));
-  return launch_kernel(attn_fwd_kernel, grid, dim3(kAttnThreads),
-                       static_cast<hipStream_t>(stream), q, k, v, key_valid, out, lse, T, NH,
-                       NKV, scale * kLog2e);
+  return launch_kernel(attn_fwd_kernel<false>, grid, dim3(kAttnThreads),
+                       static_cast<hipStream_t>(stream), p);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_attention_bwd(
@@ -653,31 +893,123 @@ extern "C" __attribute__((visibility("default"))) int soupk_attention_bwd(
   if (B == 0 || T == 0) return kOk;
   if (!q || !k || !v || !out || !dout || !lse || !workspace || !dq || !dk || !dv)
     return kInvalid;
-  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k),
-                        static_cast<const void*>(v), static_cast<const void*>(out),
-                        static_cast<const void*>(dout), static_cast<const void*>(workspace),
-                        static_cast<const void*>(dq), static_cast<const void*>(dk),
-                        static_cast<const void*>(dv)})
-    if (reinterpret_cast<uintptr_t>(p) & 15) return kInvalid;
+  for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k),
+                          static_cast<const void*>(v), static_cast<const void*>(out),
+                          static_cast<const void*>(dout), static_cast<const void*>(workspace),
+                          static_cast<const void*>(dq), static_cast<const void*>(dk),
+                          static_cast<const void*>(dv)})
+    if (misaligned16(ptr)) return kInvalid;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t per_head = static_cast<int64_t>(T) * kD;
   const int64_t part = static_cast<int64_t>(B) * NH * per_head;  // floats per partial
   // workspace: delta [B*NH*T] (padded to 4 floats), then the dK and dV partials
   const int64_t delta_n = (static_cast<int64_t>(B) * NH * T + 3) / 4 * 4;
-  float* delta = workspace;
-  float* dk_part = workspace + delta_n;
-  float* dv_part = dk_part + part;
+  AttnParams p = base_params(NH, NKV, scale);
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.key_valid = key_valid;
+  p.out = const_cast<uint16_t*>(out);
+  p.dout = dout;
+  p.lse = const_cast<float*>(lse);
+  p.delta = workspace;
+  p.dk_part = workspace + delta_n;
+  p.dv_part = p.dk_part + part;
+  p.dq = dq;
+  p.T = T;
   const int nb = (T + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B), static_cast<unsigned>(nb));
-  int rc = launch_kernel(attn_bwd_delta_kernel, grid, dim3(kAttnThreads), st, out, dout, delta,
-                         T, NH);
+  int rc = launch_kernel(attn_bwd_delta_kernel, grid, dim3(kAttnThreads), st, out, dout,
+                         p.delta, T, NH);
   if (rc != kOk) return rc;
   const dim3 grid2(static_cast<unsigned>(NH), static_cast<unsigned>(B),
                    static_cast<unsigned>(2 * nb));
-  rc = launch_kernel(attn_bwd_kernel, grid2, dim3(kAttnThreads), st, q, k, v, key_valid, dout,
-                     lse, delta, dq, dk_part, dv_part, T, NH, NKV, scale, scale * kLog2e);
+  rc = launch_kernel(attn_bwd_kernel<false>, grid2, dim3(kAttnThreads), st, p);
   if (rc != kOk) return rc;
   const int64_t n4 = static_cast<int64_t>(B) * NKV * per_head / 4;
   return launch_kernel(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
-                       dim3(256), st, dk_part, dv_part, dk, dv, per_head, NH, NKV, n4);
+                       dim3(256), st, p.dk_part, p.dv_part, dk, dv, per_head, NH, NKV, n4);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_attention_varlen_fwd(
+    const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B, uint16_t* out, float* lse,
+    int64_t M, int32_t NH, int32_t NKV, int32_t D, float scale, void* stream) {
+  const int rc = check_varlen(B, M, NH, NKV, D, scale);
+  if (rc != kOk) return rc;
+  if (B == 0 || M == 0) return kOk;
+  if (!qkv || !cu_seqlens || !out || !lse) return kInvalid;
+  if (misaligned16(qkv) || misaligned16(out)) return kInvalid;
+  AttnParams p = base_params(NH, NKV, scale);
+  p.q = qkv;
+  p.cu = cu_seqlens;
+  p.out = out;
+  p.lse = lse;
+  p.M = M;
+  p.W = static_cast<int64_t>(NH + 2 * NKV) * kD;
+  const int slots = static_cast<int>((M + kBQ - 1) / kBQ);
+  const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B),
+                  static_cast<unsigned>(slots));
+  return launch_kernel(attn_fwd_kernel<true>, grid, dim3(kAttnThreads),
+                       static_cast<hipStream_t>(stream), p);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_attention_varlen_bwd(
+    const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B, const uint16_t* out,
+    const uint16_t* dout, const float* lse, const float* cos, const float* sin,
+    const int64_t* pos, int64_t pos_slots, int32_t T_rope, float* workspace, uint16_t* dqkv,
+    int64_t M, int32_t NH, int32_t NKV, int32_t D, float scale, void* stream) {
+  const int rc0 = check_varlen(B, M, NH, NKV, D, scale);
+  if (rc0 != kOk) return rc0;
+  const bool rope = cos != nullptr || sin != nullptr || pos != nullptr;
+  if (rope && (!cos || !sin || !pos || T_rope <= 0 || pos_slots < 0 ||
+               pos_slots >= (int64_t{1} << 31) || misaligned16(cos) || misaligned16(sin)))
+    return kInvalid;
+  if (M == 0) return kOk;
+  if (!qkv || !cu_seqlens || !out || !dout || !lse || !workspace || !dqkv) return kInvalid;
+  for (const void* ptr : {static_cast<const void*>(qkv), static_cast<const void*>(out),
+                          static_cast<const void*>(dout), static_cast<const void*>(workspace),
+                          static_cast<const void*>(dqkv)})
+    if (misaligned16(ptr)) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t part = M * NH * kD;
+  const int64_t delta_n = (M * NH + 3) / 4 * 4;
+  AttnParams p = base_params(NH, NKV, scale);
+  p.q = qkv;
+  p.cu = cu_seqlens;
+  p.out = const_cast<uint16_t*>(out);
+  p.dout = dout;
+  p.lse = const_cast<float*>(lse);
+  p.delta = workspace;
+  p.dk_part = workspace + delta_n;
+  p.dv_part = p.dk_part + part;
+  p.dq = dqkv;
+  p.M = M;
+  p.W = static_cast<int64_t>(NH + 2 * NKV) * kD;
+  if (rope) {
+    p.cos = cos;
+    p.sin = sin;
+    p.pos = pos;
+    p.pos_slots = pos_slots;
+    p.rope_div = FastDiv(static_cast<uint32_t>(T_rope));
+  }
+  // With cu_seqlens running from 0 to M, every token row of dq|dk|dv is written: dQ by the dQ
+  // workgroups of its sequence, dK and dV by the reduce over all M tokens.  (A token outside
+  // every sequence gets an unspecified row; every access stays inside the buffers.)
+  // D = rowsum(dO * O) over all M tokens: the padded delta kernel over one row of M "positions"
+  // (its lse / D plane index (b*NH + h)*T + t is h*M + t for b = 0, T = M).
+  const int nbm = static_cast<int>((M + kBQ - 1) / kBQ);   // (check_varlen: 2 * nbm <= 65535)
+  int rc = launch_kernel(attn_bwd_delta_kernel,
+                         dim3(static_cast<unsigned>(NH), 1u, static_cast<unsigned>(nbm)),
+                         dim3(kAttnThreads), st, out, dout, p.delta, static_cast<int>(M), NH);
+  if (rc != kOk) return rc;
+  if (B > 0) {
+    const int slots = nbm;
+    const dim3 grid(static_cast<unsigned>(NH), static_cast<unsigned>(B),
+                    static_cast<unsigned>(2 * slots));
+    rc = launch_kernel(attn_bwd_kernel<true>, grid, dim3(kAttnThreads), st, p);
+    if (rc != kOk) return rc;
+  }
+  const int64_t items = M * NKV * 16;
+  return launch_kernel(attn_bwd_reduce_varlen_kernel,
+                       dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), st, p, items);
 }

@@ -139,7 +139,12 @@ __device__ __forceinline__ void lds8(const f32x4* p, float* v) {
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-template <int HALF>
+// TOKENS = false: q, k, v in the padded [B, heads, T, D] layout (the reference's), pad
+// positions zeroed by the workgroups after the token ones.  TOKENS = true: one token-major
+// output, q = [rows, (NH + 2*NKV) * D] in qkv's own layout (rotated q, rotated k, v + LoRA),
+// the form the varlen attention reads; k and v are unused and a token whose position has no
+// place (outside [0, B*T)) gets a row of zeros.
+template <int HALF, bool TOKENS>
 __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     const uint16_t* __restrict__ qkv, const void* __restrict__ lora_q,
     const void* __restrict__ lora_v, int lora_f32, const float* __restrict__ cos_t,
@@ -151,7 +156,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
   __shared__ f32x4 tab[kRopeMaxTok * D / 2];
   const int heads = dm.NH + 2 * dm.NKV;
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
-  if (static_cast<int64_t>(blockIdx.x) >= tok_blocks) {
+  if (!TOKENS && static_cast<int64_t>(blockIdx.x) >= tok_blocks) {
     // Zero the padded positions with no token.
     const uint32_t g = (blockIdx.x - static_cast<uint32_t>(tok_blocks)) * kRopeThreads +
                        threadIdx.x;
@@ -201,7 +206,17 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
   const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
   __syncthreads();
   if (!active) return;
-  if (p < 0 || p >= slots) return;
+  // (token-major rows: one descriptor over the whole output; the host keeps it < 2^32 bytes)
+  const uint32_t tok_off = (tok * static_cast<uint32_t>(heads) + h) * (2u * D) + 16u * c;
+  if (p < 0 || p >= slots) {
+    if constexpr (TOKENS) {
+      const StreamOut out(q, static_cast<uint64_t>(rows) * heads * D * 2u);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      out.store(tok_off, z);
+      out.store(tok_off + 2u * HALF, z);
+    }
+    return;
+  }
   int b, t;
   split_pos(p, dm, b, t);
   if (has_lora) {
@@ -226,8 +241,14 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
       x2[i] = r2;
     }
   }
-  PackedOut(q, k, v, dm, std::integral_constant<int, D>())
-      .store<D>(h, b, t, c, pack8_h(x1), pack8_h(x2));
+  if constexpr (TOKENS) {
+    const StreamOut out(q, static_cast<uint64_t>(rows) * heads * D * 2u);
+    out.store(tok_off, pack8_h(x1));
+    out.store(tok_off + 2u * HALF, pack8_h(x2));
+  } else {
+    PackedOut(q, k, v, dm, std::integral_constant<int, D>())
+        .store<D>(h, b, t, c, pack8_h(x1), pack8_h(x2));
+  }
 }
 
 template <int HALF>
@@ -451,7 +472,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
     if (tok_items + zero_items >= (int64_t{1} << 31)) return kInvalid;
     const int64_t tok_blocks = (tok_items + kRopeThreads - 1) / kRopeThreads;
     const int64_t blocks = tok_blocks + (zero_items + kRopeThreads - 1) / kRopeThreads;
-    return launch_kernel(rope_pack_fwd_kernel<64>, dim3(static_cast<unsigned>(blocks)),
+    return launch_kernel(rope_pack_fwd_kernel<64, false>, dim3(static_cast<unsigned>(blocks)),
                          dim3(kRopeThreads), st, qkv, lora_q, lora_v,
                          static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos, pos_inv,
                          q, k, v, rows, dm, tok_blocks);
@@ -506,4 +527,36 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_bwd(
   return launch_kernel(rope_pack_bwd_generic_kernel, dim3(static_cast<unsigned>(blocks)),
                        dim3(kRopeThreads), st, dq, dk, dv, cos, sin, pos, dqkv, rows, B, T, NH,
                        NKV, D);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_tokens(
+    const uint16_t* qkv, const void* lora_q, const void* lora_v, int32_t lora_dtype,
+    const float* cos, const float* sin, const int64_t* pos, uint16_t* out, int64_t rows,
+    int32_t B, int32_t T, int32_t NH, int32_t NKV, int32_t D, void* stream) {
+  if (rows < 0 || B < 0 || T < 0 || NH < 0 || NKV < 0 || D != 128) return kInvalid;
+  if (lora_dtype != SOUPK_DTYPE_F16 && lora_dtype != SOUPK_DTYPE_F32) return kInvalid;
+  const int heads = NH + 2 * NKV;
+  if (rows == 0 || heads == 0) return kOk;
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  if (!qkv || !pos || !out || !cos || !sin || T < 1) return kInvalid;
+  // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens; the
+  // stores address `out` with 32-bit byte offsets)
+  if (heads * 8 < 18 || slots >= (int64_t{1} << 31) || rows * heads * D * 2 >= (int64_t{1} << 32))
+    return kInvalid;
+  if (!aligned(qkv, 16) || !aligned(cos, 16) || !aligned(sin, 16) || !aligned(out, 16) ||
+      !aligned(lora_q, 16) || !aligned(lora_v, 16))
+    return kInvalid;
+  RopeDims dm;
+  dm.B = B; dm.T = T; dm.NH = NH; dm.NKV = NKV;
+  dm.items = static_cast<uint32_t>(heads * 8);
+  dm.per_tok = FastDiv(dm.items);
+  dm.per_seq = FastDiv(static_cast<uint32_t>(T));
+  const int64_t items = rows * dm.items;
+  if (items >= (int64_t{1} << 31)) return kInvalid;
+  const int64_t blocks = (items + kRopeThreads - 1) / kRopeThreads;
+  return launch_kernel(rope_pack_fwd_kernel<64, true>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kRopeThreads), static_cast<hipStream_t>(stream), qkv, lora_q, lora_v,
+                       static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos,
+                       static_cast<const int32_t*>(nullptr), out, static_cast<uint16_t*>(nullptr),
+                       static_cast<uint16_t*>(nullptr), rows, dm, blocks);
 }

@@ -7,9 +7,10 @@ real (non-pad) tokens:
   (all seven NF4 projections unpacked by one HIP launch: UNPACK_PER_LAYER)
   qkv        = y @ [Wq;Wk;Wv]^T + b               one hipBLASLt GEMM
   lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v (HIP, or fp16 GEMMs with dropout)
-  q, k, v    = rope_pack(qkv, lq, lv)             LoRA add + RoPE + pack (HIP)
-  a          = attention(q, k, v, causal + pad)   causal GQA flash attention (HIP), token-major
-  o          = a[real tokens] @ Wo^T              hipBLASLt
+  a          = rope_attention(qkv, lq, lv)        LoRA add + RoPE into token-major rows, then
+                                                  causal GQA flash attention over each row's
+                                                  real tokens (HIP; varlen, no padding)
+  o          = a @ Wo^T                           hipBLASLt
   s, y2, _   = add_rmsnorm(s, o)                  residual add + post-attention RMSNorm (HIP)
   d          = mlp(y2)                            GEMM + SwiGLU (HIP) + GEMM
 
@@ -90,6 +91,12 @@ def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
 
 # Rank-16 LoRA through testt_amd/csrc/lora.hip (False: the separate fp16 GEMMs below).
 USE_FUSED_LORA = True
+
+# Attention over each sequence's real tokens (attention.RopeAttention: token-major RoPE pack,
+# varlen attention, RoPE's backward inside the attention backward) for head dim 128; False
+# keeps the padded path (RopePack into [B, heads, T, D], attention with key flags, a gather of
+# the real rows), which gives bit-identical results for right-padded batches.
+USE_VARLEN_ATTENTION = True
 
 # The seven projections of a layer unpacked by one launch before its forward (one buffer, the
 # row stacks q|k|v, o, gate|up, down as views), instead of one launch per stack where each is
@@ -246,12 +253,18 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
         lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
         lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
         del y_pad
-    q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
-    del qkv, lq, lv, w_qkv
-    a = attention(q, k, v, key_valid)
-    del q, k, v
-    if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
-        a = a.index_select(0, pos_idx)
+    if USE_VARLEN_ATTENTION and _attention.varlen_supported(qkv, hd, nh, nkv):
+        # the real tokens only: rows of batch row b are cu[b] .. cu[b+1] of the sorted pos_idx
+        cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
+        a = _attention.rope_attention(qkv, lq, lv, cos, sin, pos_idx, cu, batch, seq, nh, nkv)
+        del qkv, lq, lv, w_qkv
+    else:
+        q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
+        del qkv, lq, lv, w_qkv
+        a = attention(q, k, v, key_valid)
+        del q, k, v
+        if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
+            a = a.index_select(0, pos_idx)
     o = frozen_linear(a, (w.o,), None, w_o)
     del a, w_o
     s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)

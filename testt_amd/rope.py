@@ -112,3 +112,37 @@ def rope_pack(qkv, lora_q, lora_v, cos, sin, pos_idx, batch, seq, n_heads, n_kv,
                           lora_v.contiguous() if lora_v is not None else None,
                           cos.contiguous(), sin.contiguous(), pos_idx, batch, seq,
                           n_heads, n_kv, head_dim)
+
+
+def rope_pack_tokens(qkv, lora_q, lora_v, cos, sin, pos_idx, batch, seq, n_heads, n_kv,
+                     head_dim):
+    """The RoPE pack forward without the scatter: fp16 [rows, (n_heads + 2*n_kv) * head_dim] in
+    qkv's own token-major layout -- q + lora_q rotated, k rotated, v + lora_v -- with the same
+    arithmetic as RopePack (bit-identical values), for the varlen attention, which reads the
+    real tokens where they are (no padded layout, no zero rows).  head_dim 128.  A token whose
+    position lies outside [0, batch*seq) gets a row of zeros.  Not differentiable by itself:
+    attention.RopeAttention carries its backward (fused into the attention backward)."""
+    _ext.require(qkv, "qkv", dtype=torch.float16, ndim=2)
+    rows = qkv.shape[0]
+    dev = qkv.device
+    width = (n_heads + 2 * n_kv) * head_dim
+    if qkv.shape[1] != width:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (n_heads + 2*n_kv) * head_dim = {width}")
+    if head_dim != 128:
+        raise ValueError("rope_pack_tokens handles head_dim 128 (use RopePack otherwise)")
+    pos = as_index(pos_idx)
+    if pos.numel() != rows:
+        raise ValueError(f"pos_idx has {pos.numel()} entries for {rows} rows")
+    lq, lv, code = _lora_pair(lora_q, lora_v)
+    if lq is not None and tuple(lq.shape) != (rows, n_heads * head_dim):
+        raise ValueError(f"lora_q shape {tuple(lq.shape)} != {(rows, n_heads * head_dim)}")
+    if lv is not None and tuple(lv.shape) != (rows, n_kv * head_dim):
+        raise ValueError(f"lora_v shape {tuple(lv.shape)} != {(rows, n_kv * head_dim)}")
+    cos32 = _table(cos, seq, head_dim, "cos", dev)
+    sin32 = _table(sin, seq, head_dim, "sin", dev)
+    out = torch.empty((rows, width), dtype=torch.float16, device=dev)
+    if rows:
+        _ext.call("soupk_rope_pack_tokens", _ext.ptr(qkv), _ext.ptr(lq),
+                  _ext.ptr(lv), code, _ext.ptr(cos32), _ext.ptr(sin32), _ext.ptr(pos),
+                  _ext.ptr(out), rows, batch, seq, n_heads, n_kv, head_dim, _ext.stream_of(out))
+    return out, cos32, sin32, pos
