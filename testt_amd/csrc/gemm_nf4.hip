@@ -67,16 +67,36 @@ struct TileRegs {
   float a2;        // NF4: absmax2 of the block's group
 };
 
+// Workgroups are dispatched to the 8 XCDs of the chip in turn (workgroup i to XCD i % 8), and
+// each XCD has its own L2.  Tile order: XCD j takes the j-th eighth of the tiles in row-major
+// (m-block, n-block) order, so the workgroups sharing an L2 work on few m-blocks -- their rows
+// of x stay in that L2 while the XCD walks the n-blocks -- instead of every XCD reading all of
+// x.  (With a tile count not divisible by 8 the plain order is kept.)
+constexpr int kXcds = 8;
+__device__ __forceinline__ void tile_of(int wg, int n_blocks, int m_blocks, int& nb, int& mb) {
+  const int tiles = n_blocks * m_blocks;
+  int t = wg;
+  if (tiles % kXcds == 0) t = (wg % kXcds) * (tiles / kXcds) + wg / kXcds;
+  mb = t / n_blocks;
+  nb = t - mb * n_blocks;
+}
+
 template <bool NF4>
 __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* w16, Nf4Weights nw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K) {
-  __shared__ __align__(16) _Float16 Xs[2][kBM * kLds];
-  __shared__ __align__(16) _Float16 Ws[2][kBN * kLds];
+  // Two LDS stages as separate arrays, so that the compiler sees the staging of one and the
+  // MFMA reads of the other as independent and interleaves them.
+  __shared__ __align__(16) _Float16 Xs0[kBM * kLds];
+  __shared__ __align__(16) _Float16 Ws0[kBN * kLds];
+  __shared__ __align__(16) _Float16 Xs1[kBM * kLds];
+  __shared__ __align__(16) _Float16 Ws1[kBN * kLds];
   __shared__ float code2_s[256];
-  __shared__ float nf4_s[16];
+  __shared__ float2 pair_s[256];   // NF4: (nf4[b >> 4], nf4[b & 15]) of byte value b
   const int tid = threadIdx.x;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+  int nb, mb;
+  tile_of(blockIdx.x, N / kBN, (M + kBM - 1) / kBM, nb, mb);
+  const int n0 = nb * kBN, m0 = mb * kBM;
   const int lane = tid % kWave, wv = tid / kWave;
   const int wm = wv >> 1, wn = wv & 1;
 
@@ -92,7 +112,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
   float offset = 0.f;
   if constexpr (NF4) {
     code2_s[tid] = P.code2[tid];
-    if (tid < 16) nf4_s[tid] = P.nf4[tid];
+    pair_s[tid] = float2{P.nf4[tid >> 4], P.nf4[tid & 15]};
     offset = P.offset[0];
   }
 
@@ -117,12 +137,12 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
       r.a2 = P.absmax2[blk / 256];
     }
   };
-  auto store = [&](const TileRegs& r, int buf) {
+  auto store = [&](const TileRegs& r, _Float16* Xs, _Float16* Ws) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = tid / 8 + 32 * j, ch = tid % 8;
-      *reinterpret_cast<u32x4*>(&Xs[buf][row * kLds + 8 * ch]) = r.x[j];
-      if constexpr (!NF4) *reinterpret_cast<u32x4*>(&Ws[buf][row * kLds + 8 * ch]) = r.w[j];
+      *reinterpret_cast<u32x4*>(&Xs[row * kLds + 8 * ch]) = r.x[j];
+      if constexpr (!NF4) *reinterpret_cast<u32x4*>(&Ws[row * kLds + 8 * ch]) = r.w[j];
     }
     if constexpr (NF4) {
       const int row = tid / 2, half = tid % 2;
@@ -133,11 +153,11 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const uint32_t byte = (words[q] >> (8 * b)) & 0xffu;
-          out[q * 4 + b] = pack_h2(nf4_s[byte >> 4] * scale, nf4_s[byte & 15u] * scale);
+          const float2 v = pair_s[(words[q] >> (8 * b)) & 0xffu];
+          out[q * 4 + b] = pack_h2(v.x * scale, v.y * scale);
         }
       }
-      _Float16* dst = &Ws[buf][row * kLds + 32 * half];
+      _Float16* dst = &Ws[row * kLds + 32 * half];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<u32x4*>(dst + 8 * q) =
@@ -153,17 +173,9 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  TileRegs regs;
-  load(regs, 0);
-  if constexpr (NF4) __syncthreads();   // code2_s / nf4_s written before the first store
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    store(regs, buf);
-    __syncthreads();
-    if (kt + 1 < KT) load(regs, kt + 1);
-    issue_here();
-    const _Float16* xa = &Xs[buf][(64 * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
-    const _Float16* wb = &Ws[buf][(64 * wn + (lane % 32)) * kLds + 8 * (lane / 32)];
+  auto compute = [&](const _Float16* Xs, const _Float16* Ws) {
+    const _Float16* xa = &Xs[(64 * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
+    const _Float16* wb = &Ws[(64 * wn + (lane % 32)) * kLds + 8 * (lane / 32)];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       h8 a[2], b[2];
@@ -177,6 +189,27 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32(a[i], b[j], acc[i][j]);
     }
+  };
+
+  // Software pipeline: at step kt the MFMAs read stage kt % 2 while the registers of tile
+  // kt + 1 (loaded a step earlier) are dequantised / written into the other stage and the
+  // global loads of tile kt + 2 are issued; one barrier per step.
+  TileRegs ra, rb;
+  load(ra, 0);
+  if constexpr (NF4) __syncthreads();   // code2_s / pair_s written before the first store
+  store(ra, Xs0, Ws0);
+  if (KT > 1) load(ra, 1);
+  auto step = [&](int kt, TileRegs& staged, TileRegs& next, const _Float16* cx,
+                  const _Float16* cw, _Float16* sx, _Float16* sw) {
+    __syncthreads();
+    if (kt + 2 < KT) load(next, kt + 2);
+    issue_here();
+    compute(cx, cw);
+    if (kt + 1 < KT) store(staged, sx, sw);
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    step(kt, ra, rb, Xs0, Ws0, Xs1, Ws1);
+    if (kt + 1 < KT) step(kt + 1, rb, ra, Xs1, Ws1, Xs0, Ws0);
   }
 
   // epilogue: element e of acc[i][j] is row 64wm + 32i + 8(e/4) + 4(lane/32) + e%4,
@@ -200,7 +233,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
 
 int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
   if (M < 0 || N <= 0 || K <= 0 || N % kBN || K % kBK || ldx < K || ldx % 8) return kInvalid;
-  if ((M + kBM - 1) / kBM > 65535 || N / kBN > 0x7fffffff) return kInvalid;
+  if ((M + kBM - 1) / kBM * static_cast<int64_t>(N / kBN) > 0x7fffffff) return kInvalid;
   if (M * static_cast<int64_t>(N) >= (int64_t{1} << 40)) return kInvalid;
   return kOk;
 }
@@ -220,7 +253,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(w) || bad_ptr(y)) return kInvalid;
   Nf4Weights none{};
-  const dim3 grid(static_cast<unsigned>(N / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<false>, grid, dim3(kGThreads),
                        static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
                        static_cast<int>(M), N, K);
@@ -252,7 +285,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
   if (rows != N) return kInvalid;
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(y)) return kInvalid;
-  const dim3 grid(static_cast<unsigned>(N / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<true>, grid, dim3(kGThreads),
                        static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
                        static_cast<int>(M), N, K);

@@ -270,15 +270,17 @@ __device__ __forceinline__ void absorb_keep(RowStats& st, float& shift, f16& m16
   const f16x2 a = as_h2(w.x), b = as_h2(w.y), c = as_h2(w.z), d = as_h2(w.w);
   const f16x2 m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
                                                  __builtin_elementwise_maximum(c, d));
-  const float bm = __builtin_elementwise_maximum(static_cast<float>(m2[0]),
-                                                 static_cast<float>(m2[1]));
-  if (bm > st.m) {
+  // Compared in fp16 with m16 (which equals st.m exactly): the widening to fp32 is needed only
+  // when the chunk raises the max.
+  const f16 bm16 = __builtin_elementwise_maximum(m2[0], m2[1]);
+  if (bm16 > m16) {
+    const float bm = static_cast<float>(bm16);
     const float f = scale_to(st.m, bm);
     st.se = st.se * f;
     st.sd = st.sd * f;
     st.m = bm;
     shift = kLift - bm * kLog2e;
-    m16 = static_cast<f16>(bm);
+    m16 = bm16;
     kbest = k;
     best = w;
   }
@@ -345,10 +347,13 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   const float zt_raw = h2f(base[tgt_ok ? tgt : 0]);
   const float zt = tgt_ok ? zt_raw : 0.f;
   u32x4 w[CPT];
-#pragma unroll
-  for (int k = 0; k < P; ++k)
-    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + k * kChunkStride, 0,
+  // Chunk column k of this thread (at byte offset off0 + k*kChunkStride of the row's chunks).
+  auto load_col = [&](int k) -> u32x4 {
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + k * kChunkStride, 0,
                                                  kAuxNonTemporal);
+  };
+#pragma unroll
+  for (int k = 0; k < P; ++k) w[k] = load_col(k);
 
   // 32-bit chunk indices (a row has < 2^28 chunks): 64-bit ones would cost a register pair
   // per chunk on top of the row.
@@ -363,9 +368,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   // temporaries live at a time (the row already occupies 4*CPT VGPRs).
 #pragma unroll
   for (int k = 0; k < CPT; ++k) {
-    if (k + P < CPT)
-      w[k + P] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off0 + (k + P) * kChunkStride, 0,
-                                                       kAuxNonTemporal);
+    if (k + P < CPT) w[k + P] = load_col(k + P);
     if (k * kHeadThreads + tid < nvec) {
       absorb_keep(st, run_shift, m16, kbest, best, w[k], k);
       chunk_max[k * kHeadThreads + tid] = m16;

@@ -36,10 +36,14 @@ constexpr int kRopeThreads = 256;
 #ifndef SOUPK_ROPE_NT_FWD_LD
 #define SOUPK_ROPE_NT_FWD_LD 0
 #endif
+#ifndef SOUPK_ROPE_NT_FWD_LORA_LD
+#define SOUPK_ROPE_NT_FWD_LORA_LD SOUPK_ROPE_NT_FWD_LD
+#endif
 #ifndef SOUPK_ROPE_NT_BWD_LD
 #define SOUPK_ROPE_NT_BWD_LD 1
 #endif
-constexpr bool kFwdNtLd = SOUPK_ROPE_NT_FWD_LD != 0;
+constexpr bool kFwdNtLd = SOUPK_ROPE_NT_FWD_LD != 0;          // the qkv rows
+constexpr bool kFwdLoraNtLd = SOUPK_ROPE_NT_FWD_LORA_LD != 0;  // the LoRA deltas
 constexpr bool kBwdNtLd = SOUPK_ROPE_NT_BWD_LD != 0;
 
 struct RopeDims {
@@ -196,11 +200,11 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
                              : static_cast<int64_t>(tok) * dm.NKV * D +
                                    (h - dm.NH - dm.NKV) * D + 8 * c;
     if (lora_f32) {
-      load8_f32<kFwdNtLd>(static_cast<const float*>(lora) + off, l1);
-      load8_f32<kFwdNtLd>(static_cast<const float*>(lora) + off + HALF, l2);
+      load8_f32<kFwdLoraNtLd>(static_cast<const float*>(lora) + off, l1);
+      load8_f32<kFwdLoraNtLd>(static_cast<const float*>(lora) + off + HALF, l2);
     } else {
-      load8_h<kFwdNtLd>(static_cast<const uint16_t*>(lora) + off, l1);
-      load8_h<kFwdNtLd>(static_cast<const uint16_t*>(lora) + off + HALF, l2);
+      load8_h<kFwdLoraNtLd>(static_cast<const uint16_t*>(lora) + off, l1);
+      load8_h<kFwdLoraNtLd>(static_cast<const uint16_t*>(lora) + off + HALF, l2);
     }
   }
   const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
