@@ -88,19 +88,43 @@ __device__ __forceinline__ int tile_part(int n_tiles, int part, int parts) {
   return static_cast<int>((static_cast<int64_t>(n_tiles) * part) / parts);
 }
 
+// A compiler-only barrier (no instruction): the prefetch loads issued above it stay above it
+// instead of being moved down to their first use.
+__device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
+
+// The parameter and activation pointers of the row kernels are not __restrict__: loads through
+// restrict pointers are taken as invariant and moved to their use, which would undo the
+// prefetch of the next batch.
 __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
-    const uint16_t* __restrict__ y, const float* __restrict__ aq, const float* __restrict__ av,
-    const float* __restrict__ bq, const float* __restrict__ bv, float scaling,
-    uint16_t* __restrict__ t_out, uint16_t* __restrict__ lq, uint16_t* __restrict__ lv, int M,
-    int H, int NQ, int NV) {
+    const uint16_t* y, const float* aq, const float* av, const float* bq, const float* bv,
+    float scaling, uint16_t* __restrict__ t_out, uint16_t* __restrict__ lq,
+    uint16_t* __restrict__ lv, int M, int H, int NQ, int NV) {
   __shared__ float part[4][kRows][2 * kR + 1];
   __shared__ float tt[kRows][2 * kR];
   const int m0 = blockIdx.x * kRows;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
+  // Output tiles of this wavefront (phase 2): their B16 fragments do not depend on t, so the
+  // first batch is loaded now and arrives while t is computed.
+  const int nq16 = NQ / 16;
+  const int t_begin = tile_part(NQ / 16 + NV / 16, blockIdx.y, gridDim.y);
+  const int n16 = tile_part(NQ / 16 + NV / 16, blockIdx.y + 1, gridDim.y);
+  auto load_b = [&](f4* bw, int t0) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int tile = min(t0 + 4 * u, max(n16 - 1, 0));
+      const bool is_q = tile < nq16;
+      const int f0 = 16 * (is_q ? tile : tile - nq16);
+      bw[u] = *reinterpret_cast<const f4*>((is_q ? bq : bv) +
+                                           static_cast<int64_t>(f0 + ql) * kR + 4 * gr);
+    }
+  };
+  f4 bw_next[kBatch];
+  if (t_begin + w < n16) load_b(bw_next, t_begin + w);
   // t = y A^T: A operand = y rows (row 16rt + ql of row tile rt, k = k0 + 8gr..+7); B operand =
   // A_q / A_v rows (column = feature ql), loaded once per step for the kRowTiles row tiles.
-  // The contraction over H is split over the 4 wavefronts.
+  // The contraction over H is split over the 4 wavefronts; batches of kBatch steps, the next
+  // batch's loads issued before the current batch's MFMAs.
   const int kw = H / 4;
   const uint16_t* yrow[kRowTiles];
   f4 acc_q[kRowTiles], acc_v[kRowTiles];
@@ -113,29 +137,47 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   const int steps = kw / 32;
   const float* aqrow = aq + static_cast<int64_t>(ql) * H + 8 * gr;
   const float* avrow = av + static_cast<int64_t>(ql) * H + 8 * gr;
-  for (int s0 = 0; s0 < steps; s0 += kBatch) {
+  struct Batch {
     h8 ya[kBatch][kRowTiles];
     f4 qa[kBatch][2], va[kBatch][2];
+  };
+  auto load_t = [&](Batch& r, int s0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int k0 = w * kw + 32 * min(s0 + u, steps - 1);
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt)
-        ya[u][rt] = *reinterpret_cast<const h8*>(yrow[rt] + k0 + 8 * gr);
-      qa[u][0] = *reinterpret_cast<const f4*>(aqrow + k0);
-      qa[u][1] = *reinterpret_cast<const f4*>(aqrow + k0 + 4);
-      va[u][0] = *reinterpret_cast<const f4*>(avrow + k0);
-      va[u][1] = *reinterpret_cast<const f4*>(avrow + k0 + 4);
+        r.ya[u][rt] = *reinterpret_cast<const h8*>(yrow[rt] + k0 + 8 * gr);
+      r.qa[u][0] = *reinterpret_cast<const f4*>(aqrow + k0);
+      r.qa[u][1] = *reinterpret_cast<const f4*>(aqrow + k0 + 4);
+      r.va[u][0] = *reinterpret_cast<const f4*>(avrow + k0);
+      r.va[u][1] = *reinterpret_cast<const f4*>(avrow + k0 + 4);
     }
+  };
+  auto mma_t = [&](const Batch& r, int s0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (s0 + u < steps) {
-        const h8 bq8 = to_h8(qa[u][0], qa[u][1]), bv8 = to_h8(va[u][0], va[u][1]);
+        const h8 bq8 = to_h8(r.qa[u][0], r.qa[u][1]), bv8 = to_h8(r.va[u][0], r.va[u][1]);
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
-          acc_q[rt] = mfma32(ya[u][rt], bq8, acc_q[rt]);
-          acc_v[rt] = mfma32(ya[u][rt], bv8, acc_v[rt]);
+          acc_q[rt] = mfma32(r.ya[u][rt], bq8, acc_q[rt]);
+          acc_v[rt] = mfma32(r.ya[u][rt], bv8, acc_v[rt]);
         }
+      }
+    }
+  };
+  {
+    Batch r0, r1;
+    load_t(r0, 0);
+    for (int s0 = 0; s0 < steps; s0 += 2 * kBatch) {
+      if (s0 + kBatch < steps) load_t(r1, s0 + kBatch);
+      issue_here();
+      mma_t(r0, s0);
+      if (s0 + kBatch < steps) {
+        if (s0 + 2 * kBatch < steps) load_t(r0, s0 + 2 * kBatch);
+        issue_here();
+        mma_t(r1, s0 + kBatch);
       }
     }
   }
@@ -160,10 +202,8 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   __syncthreads();
   // lq, lv: tile f0..f0+15 of the output columns, transposed: A = B16 rows (feature f0 + ql,
   // k = rank 4gr..+3), B = t rows (column = row ql of a row tile, same k).  Column part
-  // blockIdx.y of gridDim.y takes tiles [t_begin, t_end) of the NQ/16 + NV/16.
-  const int nq16 = NQ / 16;
-  const int t_begin = tile_part(NQ / 16 + NV / 16, blockIdx.y, gridDim.y);
-  const int n16 = tile_part(NQ / 16 + NV / 16, blockIdx.y + 1, gridDim.y);
+  // blockIdx.y of gridDim.y takes tiles [t_begin, t_end) of the NQ/16 + NV/16; each batch's
+  // B16 fragments were loaded a batch ahead (the first before the t phase).
   h4 tq4[kRowTiles], tv4[kRowTiles];
   bool row_ok[kRowTiles];
 #pragma unroll
@@ -176,16 +216,7 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
                  static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
     row_ok[rt] = m0 + 16 * rt + ql < M;
   }
-  for (int t0 = t_begin + w; t0 < n16; t0 += 4 * kBatch) {
-    f4 bw[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int tile = min(t0 + 4 * u, n16 - 1);
-      const bool is_q = tile < nq16;
-      const int f0 = 16 * (is_q ? tile : tile - nq16);
-      bw[u] = *reinterpret_cast<const f4*>((is_q ? bq : bv) +
-                                           static_cast<int64_t>(f0 + ql) * kR + 4 * gr);
-    }
+  auto out_tiles = [&](const f4* bw, int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int tile = t0 + 4 * u;
@@ -208,13 +239,27 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
         }
       }
     }
+  };
+  f4 bw_cur[kBatch];
+  for (int t0 = t_begin + w; t0 < n16; t0 += 8 * kBatch) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) bw_cur[u] = bw_next[u];
+    if (t0 + 4 * kBatch < n16) load_b(bw_next, t0 + 4 * kBatch);
+    issue_here();
+    out_tiles(bw_cur, t0);
+    if (t0 + 4 * kBatch < n16) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) bw_cur[u] = bw_next[u];
+      if (t0 + 8 * kBatch < n16) load_b(bw_next, t0 + 8 * kBatch);
+      issue_here();
+      out_tiles(bw_cur, t0 + 4 * kBatch);
+    }
   }
 }
 
 __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
-    const uint16_t* __restrict__ gq, int64_t ldq, const uint16_t* __restrict__ gv, int64_t ldv,
-    const float* __restrict__ aq, const float* __restrict__ av, const float* __restrict__ bq,
-    const float* __restrict__ bv, float scaling, uint16_t* __restrict__ gsq,
+    const uint16_t* gq, int64_t ldq, const uint16_t* gv, int64_t ldv, const float* aq,
+    const float* av, const float* bq, const float* bv, float scaling, uint16_t* __restrict__ gsq,
     uint16_t* __restrict__ gsv, uint16_t* __restrict__ dt_out, uint16_t* __restrict__ dy, int M,
     int H, int NQ, int NV) {
   __shared__ float part[4][kRows][2 * kR + 1];
@@ -240,40 +285,58 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     acc_q[rt] = f4{0.f, 0.f, 0.f, 0.f};
     acc_v[rt] = f4{0.f, 0.f, 0.f, 0.f};
   }
-  // steps of 32 columns of g over this wavefront's quarter of N
+  // steps of 32 columns of g over this wavefront's quarter of N, in batches of kBatch steps,
+  // the next batch's loads issued before the current batch's MFMAs
+  struct Batch {
+    h8 graw[kBatch][kRowTiles];
+    float braw[kBatch][8];
+  };
   auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const float* b,
                  f4* acc) {
     const int kn = N / 4, steps = kn / 32;
     const float* bcol = b + static_cast<int64_t>(w * kn + 8 * gr) * kR + ql;
-    for (int s0 = 0; s0 < steps; s0 += kBatch) {
-      h8 graw[kBatch][kRowTiles];
-      float braw[kBatch][8];
+    auto load = [&](Batch& r, int s0) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int j = 32 * min(s0 + u, steps - 1);
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt)
-          graw[u][rt] = *reinterpret_cast<const h8*>(g + row[rt] * ldg + w * kn + 8 * gr + j);
+          r.graw[u][rt] = *reinterpret_cast<const h8*>(g + row[rt] * ldg + w * kn + 8 * gr + j);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) braw[u][i] = bcol[static_cast<int64_t>(j + i) * kR];
+        for (int i = 0; i < 8; ++i) r.braw[u][i] = bcol[static_cast<int64_t>(j + i) * kR];
       }
+    };
+    auto mma = [&](const Batch& r, int s0) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         if (s0 + u >= steps) break;
         h8 ba;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ba[i] = static_cast<_Float16>(braw[u][i]);
+        for (int i = 0; i < 8; ++i) ba[i] = static_cast<_Float16>(r.braw[u][i]);
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
           h8 ga;
 #pragma unroll
           for (int i = 0; i < 8; ++i)
-            ga[i] = static_cast<_Float16>(static_cast<float>(graw[u][rt][i]) * scaling);
+            ga[i] = static_cast<_Float16>(static_cast<float>(r.graw[u][rt][i]) * scaling);
           if (store_gs && row_ok[rt])
             *reinterpret_cast<h8*>(gs + (m0 + 16 * rt + ql) * static_cast<int64_t>(N) +
                                    w * kn + 32 * (s0 + u) + 8 * gr) = ga;
           acc[rt] = mfma32(ga, ba, acc[rt]);
         }
+      }
+    };
+    if (steps <= 0) return;
+    Batch r0, r1;
+    load(r0, 0);
+    for (int s0 = 0; s0 < steps; s0 += 2 * kBatch) {
+      if (s0 + kBatch < steps) load(r1, s0 + kBatch);
+      issue_here();
+      mma(r0, s0);
+      if (s0 + kBatch < steps) {
+        if (s0 + 2 * kBatch < steps) load(r0, s0 + 2 * kBatch);
+        issue_here();
+        mma(r1, s0 + kBatch);
       }
     }
   };
@@ -311,14 +374,15 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
                                : av + static_cast<int64_t>(8 * (gr - 2)) * H) + ql;
   const int t_begin = tile_part(H / 16, blockIdx.y, gridDim.y);
   const int n16 = tile_part(H / 16, blockIdx.y + 1, gridDim.y);
-  for (int t0 = t_begin + w; t0 < n16; t0 += 4 * kBatch) {
-    float araw[kBatch][8];
+  auto load_a = [&](float (*araw)[8], int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int h0 = 16 * min(t0 + 4 * u, n16 - 1);
 #pragma unroll
       for (int i = 0; i < 8; ++i) araw[u][i] = abase[static_cast<int64_t>(i) * H + h0];
     }
+  };
+  auto out_tiles = [&](const float (*araw)[8], int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int tile = t0 + 4 * u;
@@ -333,6 +397,20 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
           *reinterpret_cast<u32x2*>(dy + (m0 + 16 * rt + ql) * static_cast<int64_t>(H) +
                                     16 * tile + 4 * gr) =
               u32x2{pack_h2(c[0], c[1]), pack_h2(c[2], c[3])};
+      }
+    }
+  };
+  if (t_begin + w < n16) {
+    float a0[kBatch][8], a1[kBatch][8];
+    load_a(a0, t_begin + w);
+    for (int t0 = t_begin + w; t0 < n16; t0 += 8 * kBatch) {
+      if (t0 + 4 * kBatch < n16) load_a(a1, t0 + 4 * kBatch);
+      issue_here();
+      out_tiles(a0, t0);
+      if (t0 + 4 * kBatch < n16) {
+        if (t0 + 8 * kBatch < n16) load_a(a0, t0 + 8 * kBatch);
+        issue_here();
+        out_tiles(a1, t0 + 4 * kBatch);
       }
     }
   }
