@@ -809,14 +809,15 @@ def cpu_baseline(cases, seconds):
                        f"on the CPU (oracle/baseline.py), {elapsed:.1f} s, {model}")}
 
 
-def pmc_traffic(kernel, path=TRAFFIC_TABLE):
-    """Measured HBM bytes per launch of `kernel` from the committed PMC table, or None."""
+def pmc_traffic(entry, path=TRAFFIC_TABLE):
+    """Measured HBM bytes per launch of bench entry `entry` (e.g. "swiglu_bwd") from the
+    committed PMC table, or None."""
     try:
         with open(path) as f:
             for ln in f:
                 cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
-                if len(cells) >= 6 and cells[0].split("<")[0] == kernel:
-                    return int(cells[5])
+                if len(cells) >= 10 and cells[0] == entry:
+                    return int(cells[7])
     except (OSError, ValueError):
         pass
     return None
@@ -832,23 +833,71 @@ def _read_csv(path):
         return list(csv.DictReader(f))
 
 
-def summarize_stats(stats_csv, bench_json, command):
-    """Markdown summary of a rocprofv3 --kernel-trace --stats run beside bench.py's own timing."""
+def _launch_groups(rows, name_col="Kernel_Name"):
+    """soupk launches of a rocprofv3 CSV grouped by (kernel, grid, workgroup), in the order of
+    each group's first dispatch: {key: [rows]}."""
+    groups = {}
+    for r in rows:
+        if "soupk" not in r[name_col]:
+            continue
+        grid = r.get("Grid_Size_X", r.get("Grid_Size"))
+        wg = r.get("Workgroup_Size_X", r.get("Workgroup_Size"))
+        key = (_kernel_base(r[name_col]), int(grid), int(wg))
+        groups.setdefault(key, []).append(r)
+    return dict(sorted(groups.items(), key=lambda kv: int(kv[1][0]["Dispatch_Id"])))
+
+
+def _bench_entries(bench, keys):
+    """{group key: (bench entry name, entry)}: bench.py times the set, then the kernels beyond
+    it, then the other shapes, then the launch floor, so each entry takes the earliest unused
+    group of its kernel; the floor's groups are matched by grid."""
+    out, used = {}, set()
+    for sect in ("kernels", "kernels_beyond_set", "kernels_other_shapes"):
+        for name, v in bench.get(sect, {}).items():
+            key = next((k for k in keys if k[0].split("<")[0] == v["kernel"] and k not in used),
+                       None)
+            if key is not None:
+                used.add(key)
+                out[key] = (name, v)
+    for name, kern, grid in (("empty_kernel_1wg", "bench_empty_kernel", 256),
+                             ("empty_kernel_1024wg", "bench_empty_kernel", 1024 * 256),
+                             ("copy_4KiB", "bench_copy_kernel", 4096 // 16)):
+        key = next((k for k in keys if k[0] == kern and k[1] == grid and k not in used), None)
+        if key is not None and name in bench.get("launch_floor_us", {}):
+            used.add(key)
+            out[key] = ("launch floor: " + name, {"us_median": bench["launch_floor_us"][name]})
+    return out
+
+
+def summarize_stats(trace_csv, bench_json, command):
+    """Markdown summary of a rocprofv3 --kernel-trace run of bench.py, launches grouped by
+    kernel and grid, beside bench.py's own timing of the same launches (an unprofiled run)."""
     bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
-    out = ["# rocprofv3 kernel statistics: kernel set at the 2048-token step (bench.py)", "",
+    groups = _launch_groups(_read_csv(trace_csv))
+    ns = {k: [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rs]
+          for k, rs in groups.items()}
+    names = _bench_entries(bench, list(groups))
+    out = ["# rocprofv3 kernel trace: kernel set at the 2048-token step (bench.py)", "",
            "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```", command, "```",
-           "", "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
-    for r in _read_csv(stats_csv):
-        if "soupk" in r["Name"]:
-            out.append(f"| `{_kernel_base(r['Name'])}` | {r['Calls']} | "
-                       f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
-                       f"{float(r['MaxNs']) / 1e3:.2f} |")
-    out += ["", "The same kernels timed by `python bench.py` (unprofiled run, dispatch-recorded "
-            "HIP events, mean us):", "", "| kernel | bench us | GB/s | % of 8 TB/s |",
-            "|---|---:|---:|---:|"]
-    for k, v in bench["kernels"].items():
-        out.append(f"| {k} (`{v['kernel']}`) | {v['us_mean']:.2f} | {v['GBps']:.0f} | "
-                   f"{100 * v['frac_of_peak']:.1f} |")
+           "", "Every soupk launch of the run by kernel and grid (threads / workgroup size), "
+           "beside `python bench.py`'s timing of the same launches in an unprofiled run "
+           "(dispatch-recorded HIP events; the mean, the median for the launch floor):", "",
+           "| bench entry | kernel | grid / WG | calls | rocprof avg us | rocprof median us | "
+           "min us | max us | bench us | rocprof / bench | bench GB/s | % of 8 TB/s |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for key, d in ns.items():
+        entry, v = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel"
+                                   else "-", None))
+        avg, med = sum(d) / len(d) / 1e3, median(d) / 1e3
+        if v is None:
+            tail = "- | - | - | -"
+        elif "us_mean" in v:
+            tail = (f"{v['us_mean']:.2f} | {avg / v['us_mean']:.3f} | {v['GBps']:.0f} | "
+                    f"{100 * v['frac_of_peak']:.1f}")
+        else:
+            tail = f"{v['us_median']:.2f} | {med / v['us_median']:.3f} (median) | - | -"
+        out.append(f"| {entry} | `{key[0]}` | {key[1]} / {key[2]} | {len(d)} | {avg:.2f} | "
+                   f"{med:.2f} | {min(d) / 1e3:.2f} | {max(d) / 1e3:.2f} | {tail} |")
     return "\n".join(out) + "\n"
 
 
@@ -880,19 +929,25 @@ def summarize_step(trace_csv, title, command, n_layers=28, top=32):
     """Markdown breakdown of one training step from a rocprofv3 --kernel-trace run of bench.py:
     the launches between the first attention forward of one step and that of the next (steps
     with a backward: those holding attn_bwd launches), per kernel, for the step whose GPU busy
-    time is the median."""
+    time is the median among the steps of the first work profile timed (bench.py's
+    reference-profile steps, which follow, launch more kernels)."""
     rows = sorted(_read_csv(trace_csv), key=lambda r: int(r["Start_Timestamp"]))
     names = [_kernel_base(r["Kernel_Name"]) if "soupk" in r["Kernel_Name"]
              else r["Kernel_Name"].split("(")[0][:90] for r in rows]
     dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
-    firsts = [i for i, n in enumerate(names) if n == "attn_fwd_kernel"][::n_layers]
+    firsts = [i for i, n in enumerate(names)
+              if n.split("<")[0] == "attn_fwd_kernel"][::n_layers]
     steps = []
     for a, b in zip(firsts, firsts[1:]):
         if any(names[i].startswith("attn_bwd") for i in range(a, b)):
             steps.append((sum(dur[a:b]), a, b))
     if not steps:
         raise ValueError("no forward+backward step in the trace")
-    steps.sort()
+    # the work profile: the earliest launch count shared by 3 or more steps (a first step
+    # launches a few one-time kernels more)
+    counts = [s[2] - s[1] for s in steps]
+    launches = next((n for n in counts if counts.count(n) >= 3), counts[0])
+    steps = sorted(s for s in steps if s[2] - s[1] == launches)
     busy, a, b = steps[len(steps) // 2]
     per, calls = {}, {}
     for i in range(a, b):
@@ -913,12 +968,9 @@ def summarize_step(trace_csv, title, command, n_layers=28, top=32):
 def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     """Markdown table of HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
     WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the 1 GiB device
-    copy that bench.py's copy_peak() makes (torch's copy_ -> __amd_rocclr_copyBuffer)."""
-    from collections import defaultdict
+    copy that bench.py's copy_peak() makes (torch's copy_ -> __amd_rocclr_copyBuffer).  Launches
+    are grouped by kernel and grid and named by the bench entry they belong to."""
     bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
-    algo = {v["kernel"]: v["bytes"] for v in bench["kernels"].values()}
-    algo.update({v["kernel"]: v["bytes"]
-                 for v in bench.get("kernels_beyond_set", {}).values()})
     fetch, write = _read_csv(fetch_csv), _read_csv(write_csv)
     gib_kib = float(1 << 20)
     copies = {r["Dispatch_Id"] for r in write if "copyBuffer" in r["Kernel_Name"]
@@ -929,11 +981,8 @@ def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     f_copy = mean([float(r["Counter_Value"]) for r in fetch if r["Dispatch_Id"] in copies])
     w_copy = mean([float(r["Counter_Value"]) for r in write if r["Dispatch_Id"] in copies])
     f_scale, w_scale = gib_kib / f_copy, gib_kib / w_copy
-    per = defaultdict(lambda: [[], []])
-    for i, rows in enumerate((fetch, write)):
-        for r in rows:
-            if "soupk" in r["Kernel_Name"]:
-                per[_kernel_base(r["Kernel_Name"])][i].append(float(r["Counter_Value"]))
+    fg, wg = _launch_groups(fetch), _launch_groups(write)
+    names = _bench_entries(bench, list(fg))
     out = ["# HBM traffic per launch (rocprofv3 PMC): kernel set at the 2048-token step", "",
            "Commands (run from /tmp on the MI355X box, TMPDIR=/tmp), one counter per pass:", "",
            "```", *commands, "```", "",
@@ -942,16 +991,64 @@ def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
            f"{f_copy:.0f} KiB for 1048576 KiB read -> x{f_scale:.4f}; WRITE_SIZE reads "
            f"{w_copy:.0f} KiB for 1048576 KiB written -> x{w_scale:.4f}.", "",
            "traffic = (FETCH_SIZE x fetch scale + WRITE_SIZE x write scale) x 1024 bytes, mean "
-           "over dispatches; algorithmic = the compulsory bytes bench.py prices the kernel at.",
-           "", "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB | traffic "
-           "bytes | algorithmic bytes | traffic / algorithmic |",
-           "|---|---:|---:|---:|---:|---:|---:|---:|"]
-    for name, (f, w) in per.items():
+           "over dispatches; algorithmic = the compulsory bytes bench.py prices the launch at.  "
+           "Launches grouped by kernel and grid (threads / workgroup size).", "",
+           "| bench entry | kernel | grid / WG | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | "
+           "scaled MB | traffic bytes | algorithmic bytes | traffic / algorithmic |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for key, rows in fg.items():
+        f = [float(r["Counter_Value"]) for r in rows]
+        w = [float(r["Counter_Value"]) for r in wg.get(key, [])]
+        if not w:
+            continue
         t = int(round((mean(f) * f_scale + mean(w) * w_scale) * 1024))
-        a = algo.get(name.split("<")[0])
+        entry, v = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel"
+                                   else "-", None))
+        a = v.get("bytes") if v else None
         ratio = f"{t / a:.3f}" if a else "-"
-        out.append(f"| `{name}` | {len(f)} | {mean(f):.1f} | {mean(w):.1f} | {t / 1e6:.2f} | "
-                   f"{t} | {a if a else '-'} | {ratio} |")
+        out.append(f"| {entry} | `{key[0]}` | {key[1]} / {key[2]} | {len(f)} | {mean(f):.1f} | "
+                   f"{mean(w):.1f} | {t / 1e6:.2f} | {t} | {a if a else '-'} | {ratio} |")
+    return "\n".join(out) + "\n"
+
+
+VALU_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_WAVE_CYCLES", "SQ_ACTIVE_INST_VALU",
+                 "SQ_ACTIVE_INST_ANY", "SQ_WAIT_INST_ANY", "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+
+
+def summarize_valu(raw_csv, busy_csv, bench_json, commands):
+    """Markdown table of VALU activity per soupk launch group (kernel, grid) from two rocprofv3
+    --pmc runs: the raw SQ counters of VALU_COUNTERS (one pass) and the derived VALUBusy (its
+    own pass).  The wave counters are wave-cycle sums (quad-cycles), so their ratios are the
+    share of the waves' lifetime spent issuing VALU work, issuing anything, or waiting."""
+    bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
+    raw, busy = _launch_groups(_read_csv(raw_csv)), _launch_groups(_read_csv(busy_csv))
+    names = _bench_entries(bench, list(raw))
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    out = ["# VALU activity per launch (rocprofv3 PMC): kernel set at the 2048-token step", "",
+           "Commands (run from /tmp on the MI355X box, TMPDIR=/tmp), raw counters and the "
+           "derived VALUBusy in passes of their own:", "", "```", *commands, "```", "",
+           "VALUBusy = 100 x SQ_ACTIVE_INST_VALU / CU_NUM / GRBM_GUI_ACTIVE (rocprofv3's gfx950 "
+           "definition).  VALU insts / wave = SQ_INSTS_VALU / SQ_WAVES.  VALU share, issue share "
+           "and wait share = SQ_ACTIVE_INST_VALU, SQ_ACTIVE_INST_ANY and SQ_WAIT_INST_ANY over "
+           "SQ_WAVE_CYCLES.  Launches grouped by kernel and grid (threads / workgroup size).", "",
+           "| bench entry | kernel | grid / WG | dispatches | waves | VALU insts / wave | "
+           "VALUBusy % | VALU share of wave cycles | issue share | wait share |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for key, rows in raw.items():
+        c = {}
+        for r in rows:
+            c.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        vb = [float(r["Counter_Value"]) for r in busy.get(key, [])
+              if r["Counter_Name"] == "VALUBusy"]
+        waves, cyc = mean(c.get("SQ_WAVES")), mean(c.get("SQ_WAVE_CYCLES"))
+        share = lambda k: f"{mean(c.get(k)) / cyc:.3f}" if cyc else "-"
+        entry = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel" else "-",
+                                None))[0]
+        out.append(f"| {entry} | `{key[0]}` | {key[1]} / {key[2]} | "
+                   f"{len(c.get('SQ_WAVES', []))} | {waves:.0f} | "
+                   f"{mean(c.get('SQ_INSTS_VALU')) / waves:.0f} | {mean(vb):.1f} | "
+                   f"{share('SQ_ACTIVE_INST_VALU')} | {share('SQ_ACTIVE_INST_ANY')} | "
+                   f"{share('SQ_WAIT_INST_ANY')} |")
     return "\n".join(out) + "\n"
 
 
@@ -973,17 +1070,26 @@ def main():
                     help="skip the whole-model training-step timing")
     ap.add_argument("--heuristic-gemms", action="store_true",
                     help="keep hipBLASLt's heuristic choice for every GEMM (no tuned table)")
-    ap.add_argument("--summarize-stats", nargs=3, metavar=("STATS_CSV", "BENCH_JSON", "CMD"),
-                    help="print a markdown summary of a rocprofv3 --stats run and exit (CPU)")
+    ap.add_argument("--summarize-stats", nargs=3, metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
+                    help="print a markdown summary of a rocprofv3 --kernel-trace run beside "
+                         "bench.py's timing and exit (CPU)")
     ap.add_argument("--summarize-pmc", nargs=5,
                     metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "CMD1", "CMD2"),
                     help="print the HBM traffic table of two rocprofv3 --pmc runs and exit (CPU)")
+    ap.add_argument("--summarize-valu", nargs=5,
+                    metavar=("RAW_CSV", "BUSY_CSV", "BENCH_JSON", "CMD1", "CMD2"),
+                    help="print the VALU activity table of two rocprofv3 --pmc runs and exit "
+                         "(CPU)")
     ap.add_argument("--summarize-kernels", nargs=3, metavar=("STATS_CSV", "TITLE", "CMD"),
                     help="print every kernel of a rocprofv3 --stats run by total time (CPU)")
     ap.add_argument("--summarize-step", nargs=3, metavar=("TRACE_CSV", "TITLE", "CMD"),
                     help="print the per-kernel breakdown of one training step of a rocprofv3 "
                          "--kernel-trace run (CPU)")
     args = ap.parse_args()
+    if args.summarize_valu:
+        a = args.summarize_valu
+        sys.stdout.write(summarize_valu(a[0], a[1], a[2], a[3:]))
+        return
     if args.summarize_step:
         sys.stdout.write(summarize_step(*args.summarize_step))
         return
@@ -1120,7 +1226,7 @@ def main():
     dom_gbps = dom.nbytes / (dom_us * 1e-6) / 1e9
     roofline = {"kernel": dom.kernel, "bound": "hbm", "achieved": round(dom_gbps, 1),
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(dom_gbps / PEAK_HBM_GBPS, 4),
-                "traffic": pmc_traffic(dom.kernel), "algorithmic_bytes": dom.nbytes,
+                "traffic": pmc_traffic(dom.name), "algorithmic_bytes": dom.nbytes,
                 "traffic_source": os.path.relpath(TRAFFIC_TABLE, ROOT)}
     cpu = None
     if not args.no_cpu:

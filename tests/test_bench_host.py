@@ -1,0 +1,68 @@
+"""CPU: bench.py's rocprofv3 summarizers on small synthetic CSVs -- launches grouped by kernel
+and grid, each bench entry matched to its own group, the PMC traffic scaled by the 1 GiB copy
+and read back by the roofline's lookup."""
+
+import csv
+import json
+
+import bench
+
+K = "void soupk::(anonymous namespace)::{}(int)"
+
+
+def _write(path, header, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+    return str(path)
+
+
+def _bench_json(tmp_path):
+    line = {"kernels": {"rope_pack_fwd": {"kernel": "rope_pack_fwd_kernel", "us_mean": 5.0,
+                                          "GBps": 6000.0, "frac_of_peak": 0.75, "bytes": 3000}},
+            "kernels_other_shapes": {"rope_pack_fwd_ragged": {
+                "kernel": "rope_pack_fwd_kernel", "us_mean": 4.0, "GBps": 4000.0,
+                "frac_of_peak": 0.5, "bytes": 1000}},
+            "launch_floor_us": {"empty_kernel_1wg": 4.0}}
+    p = tmp_path / "bench.json"
+    p.write_text("log line\n" + json.dumps(line) + "\n")
+    return str(p)
+
+
+def test_trace_groups_match_bench_entries(tmp_path):
+    hdr = ["Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp",
+           "End_Timestamp"]
+    rows = []
+    for i in range(4):      # the set's launches first, then the ragged shape's, then the floor
+        rows.append([1 + i, K.format("rope_pack_fwd_kernel<64, false>"), 4096, 256, 0, 5000])
+    for i in range(4):
+        rows.append([10 + i, K.format("rope_pack_fwd_kernel<64, false>"), 2048, 256, 0, 4400])
+    rows.append([20, K.format("bench_empty_kernel"), 256, 256, 0, 3900])
+    out = bench.summarize_stats(_write(tmp_path / "t.csv", hdr, rows), _bench_json(tmp_path),
+                                "cmd")
+    lines = {ln.split("|")[1].strip(): ln for ln in out.splitlines() if ln.startswith("| ")}
+    assert "| 4096 / 256 | 4 | 5.00 |" in lines["rope_pack_fwd"]
+    assert "| 2048 / 256 | 4 | 4.40 |" in lines["rope_pack_fwd_ragged"]
+    assert "1.100" in lines["rope_pack_fwd_ragged"]             # 4.40 / 4.00
+    assert "0.975 (median)" in lines["launch floor: empty_kernel_1wg"]
+
+
+def test_pmc_traffic_scaled_and_read_back(tmp_path):
+    hdr = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Workgroup_Size", "Counter_Name",
+           "Counter_Value"]
+    gib = 1 << 20
+    fetch = [[1, "__amd_rocclr_copyBuffer", 1, 1, "FETCH_SIZE", gib / 2],
+             [2, K.format("rope_pack_fwd_kernel<64, false>"), 4096, 256, "FETCH_SIZE", 1.0],
+             [3, K.format("rope_pack_fwd_kernel<64, false>"), 2048, 256, "FETCH_SIZE", 0.25]]
+    write = [[1, "__amd_rocclr_copyBuffer", 1, 1, "WRITE_SIZE", gib],
+             [2, K.format("rope_pack_fwd_kernel<64, false>"), 4096, 256, "WRITE_SIZE", 0.5],
+             [3, K.format("rope_pack_fwd_kernel<64, false>"), 2048, 256, "WRITE_SIZE", 0.5]]
+    table = bench.summarize_pmc(_write(tmp_path / "f.csv", hdr, fetch),
+                                _write(tmp_path / "w.csv", hdr, write), _bench_json(tmp_path),
+                                ["c1", "c2"])
+    path = tmp_path / "traffic.md"
+    path.write_text(table)
+    assert bench.pmc_traffic("rope_pack_fwd", path) == 2560           # (1 x 2 + 0.5) KiB
+    assert bench.pmc_traffic("rope_pack_fwd_ragged", path) == 1024    # (0.25 x 2 + 0.5) KiB
+    assert bench.pmc_traffic("swiglu_bwd", path) is None
