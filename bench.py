@@ -367,26 +367,22 @@ class HipEvents:
 
 
 class DeviceHold:
-    """Keeps the current stream busy with a device-side wait (torch.cuda._sleep: a one-thread
-    kernel spinning on the clock counter for a given number of cycles, so it always ends) while
-    the host queues the launches to be timed behind it.  The GPU then runs them back to back, as
-    in a training step, instead of at the host's launch rate (a ctypes launch with its event
-    pair costs the host about as long as the shorter kernels run, so each of them would start
-    on an idle GPU and the means would depend on the host's speed)."""
+    """Keeps the current stream busy with a device-side wait (soupk_bench_hold: one wave that
+    sleeps until the device's constant-rate wall clock has advanced the given time, so it
+    always ends) while the host queues the launches to be timed behind it.  The GPU then runs
+    them back to back, as in a training step, instead of at the host's launch rate (a ctypes
+    launch with its event pair costs the host about as long as the shorter kernels run, so each
+    of them would start on an idle GPU and the means would depend on the host's speed)."""
 
-    def __init__(self, dev):
-        torch.cuda._sleep(1000)
-        torch.cuda.synchronize(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        cycles = 5_000_000
-        e0.record()
-        torch.cuda._sleep(cycles)
-        e1.record()
-        torch.cuda.synchronize(dev)
-        self.cycles_per_us = cycles / max(e0.elapsed_time(e1) * 1e3, 1.0)
+    def __init__(self, dev, lib=None):
+        self.dev = dev
+        self.lib = lib if lib is not None else _ext.lib()
 
     def hold(self, us):
-        torch.cuda._sleep(int(min(us, 2e5) * self.cycles_per_us))
+        status = self.lib.soupk_bench_hold(float(min(us, 2e5)),
+                                           torch.cuda.current_stream(self.dev).cuda_stream)
+        if status != 0:
+            raise RuntimeError(f"soupk_bench_hold failed with status {status}")
 
 
 def time_gpu(cases, steps, warmup, dev, lib=None):
@@ -847,6 +843,12 @@ def _launch_groups(rows, name_col="Kernel_Name"):
     return dict(sorted(groups.items(), key=lambda kv: int(kv[1][0]["Dispatch_Id"])))
 
 
+def _unnamed(kernel):
+    """Label of a launch group that no bench entry claims."""
+    return {"bench_copy_kernel": "(copy reference)",
+            "bench_hold_kernel": "(device-side wait)"}.get(kernel, "-")
+
+
 def _bench_entries(bench, keys):
     """{group key: (bench entry name, entry)}: bench.py times the set, then the kernels beyond
     it, then the other shapes, then the launch floor, so each entry takes the earliest unused
@@ -886,8 +888,7 @@ def summarize_stats(trace_csv, bench_json, command):
            "min us | max us | bench us | rocprof / bench | bench GB/s | % of 8 TB/s |",
            "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     for key, d in ns.items():
-        entry, v = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel"
-                                   else "-", None))
+        entry, v = names.get(key, (_unnamed(key[0]), None))
         avg, med = sum(d) / len(d) / 1e3, median(d) / 1e3
         if v is None:
             tail = "- | - | - | -"
@@ -905,9 +906,9 @@ def summarize_kernels(stats_csv, title, command, top=30):
     """Markdown table of every kernel of a rocprofv3 --kernel-trace --stats run, by total time
     (hipBLASLt, torch and soupk kernels alike)."""
     rows = sorted(_read_csv(stats_csv), key=lambda r: -float(r["TotalDurationNs"]))
-    # DeviceHold's waits (torch.cuda._sleep's spin kernel) are not work: listed apart
-    holds = [r for r in rows if "spin_kernel" in r["Name"]]
-    rows = [r for r in rows if "spin_kernel" not in r["Name"]]
+    # DeviceHold's waits (bench_hold_kernel) are not work: listed apart
+    holds = [r for r in rows if "bench_hold_kernel" in r["Name"]]
+    rows = [r for r in rows if "bench_hold_kernel" not in r["Name"]]
     total = sum(float(r["TotalDurationNs"]) for r in rows)
     out = [f"# {title}", "", "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```",
            command, "```", "", f"All kernels: {total / 1e6:.2f} ms in "
@@ -1002,8 +1003,7 @@ def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
         if not w:
             continue
         t = int(round((mean(f) * f_scale + mean(w) * w_scale) * 1024))
-        entry, v = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel"
-                                   else "-", None))
+        entry, v = names.get(key, (_unnamed(key[0]), None))
         a = v.get("bytes") if v else None
         ratio = f"{t / a:.3f}" if a else "-"
         out.append(f"| {entry} | `{key[0]}` | {key[1]} / {key[2]} | {len(f)} | {mean(f):.1f} | "
@@ -1042,8 +1042,7 @@ def summarize_valu(raw_csv, busy_csv, bench_json, commands):
               if r["Counter_Name"] == "VALUBusy"]
         waves, cyc = mean(c.get("SQ_WAVES")), mean(c.get("SQ_WAVE_CYCLES"))
         share = lambda k: f"{mean(c.get(k)) / cyc:.3f}" if cyc else "-"
-        entry = names.get(key, ("(copy reference)" if key[0] == "bench_copy_kernel" else "-",
-                                None))[0]
+        entry = names.get(key, (_unnamed(key[0]), None))[0]
         out.append(f"| {entry} | `{key[0]}` | {key[1]} / {key[2]} | "
                    f"{len(c.get('SQ_WAVES', []))} | {waves:.0f} | "
                    f"{mean(c.get('SQ_INSTS_VALU')) / waves:.0f} | {mean(vb):.1f} | "

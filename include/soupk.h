@@ -62,6 +62,14 @@ int soupk_bench_copy(const void* src, void* dst, int64_t bytes, void* stream);
 int soupk_bench_empty(int32_t workgroups, void* stream);
 
 /*
+ * Benchmark utility (no counterpart in the reference): one wave that keeps `stream` busy for
+ * `microseconds` (0 to 2e6) of the device's constant-rate wall clock, then ends.  bench.py
+ * queues its timed launches behind it, so they run back to back however long the host takes
+ * to enqueue them.
+ */
+int soupk_bench_hold(double microseconds, void* stream);
+
+/*
  * NF4 double-quant unpack (replaces the launch of nf4_unpack_kernel, solution/nf4.py:27-45,
  * launched from unpack_into, solution/nf4.py:72-89).
  *   absmax[b] = fp32(fp32(code2[absmax_u8[b]] * absmax2[b / qblock2]) + offset[0])

@@ -74,6 +74,9 @@ def test_version_and_status_strings(lib):
     ("soupk_bench_copy", (16, 32, 24, None)),        # not a multiple of 16 bytes
     ("soupk_bench_copy", (16, 32, 0, None)),
     ("soupk_bench_empty", (0, None)),
+    ("soupk_bench_hold", (-1.0, None)),
+    ("soupk_bench_hold", (2.5e6, None)),               # beyond the 2 s cap
+    ("soupk_bench_hold", (float("nan"), None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

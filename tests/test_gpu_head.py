@@ -159,3 +159,58 @@ def test_rows_variant_matches_in_place(rows, vocab):
     assert torch.equal(logits.cpu().view(torch.int16), z.view(torch.int16))
     for got, want in zip(stats_only, outs):
         assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows,vocab,mode", [(2048, 151936, "rows"), (520, 151936, "in_place"),
+                                             (777, 5003, "in_place"), (1000, 32000, "rows")])
+def test_more_rows_than_cus(rows, vocab, mode):
+    """More rows than CUs (the product's 2048-row chunk among them): several workgroups per CU
+    in turn.  Ignored rows come in runs and alone; sampled rows -- the first and last rows of
+    every pass over the CUs, and every 13th -- are checked against the float64 oracle, which is
+    computed per row; rows spread over the chunk must match a one-row launch of that row."""
+    print(f"head multi-row rows={rows} vocab={vocab} mode={mode}", flush=True)
+    z, targets = workloads.head_logits(rows, vocab, seed=rows * 3 + vocab, scale=1.0)
+    targets = targets.clamp(max=vocab - 1)
+    targets[5:9] = -100                                  # a run of ignored rows
+    targets[::17] = -100
+    scale = 0.21
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    sample = sorted({r for r in range(rows)
+                     if r % 13 == 0 or r % cus in (0, 1, cus - 1) or r >= rows - 3})
+    ent = torch.empty(rows, dtype=torch.float32, device=DEV)
+    loss, lse = torch.empty_like(ent), torch.empty_like(ent)
+    cor = torch.empty(rows, dtype=torch.int32, device=DEV)
+    logits = z.to(DEV)
+    lab = targets != -100
+    if mode == "rows":
+        slot = torch.where(lab, torch.cumsum(lab, 0) - 1, -1).to(torch.int32)
+        g = torch.empty((int(lab.sum()), vocab), dtype=torch.float16, device=DEV)
+        head.head_stats_grad_rows(logits, targets.to(DEV), slot.to(DEV), g, ent, loss, cor,
+                                  scale, lse)
+        assert torch.equal(logits.cpu().view(torch.int16), z.view(torch.int16))
+        g = g.cpu()
+    else:
+        head.head_stats_grad(logits, targets.to(DEV), ent, loss, cor, scale, lse)
+        new = logits.cpu()
+    idx = torch.tensor(sample)
+    r_ent, r_loss, r_cor, r_lse, r_new = ohead.head_stats_grad(z[idx], targets[idx], scale)
+    assert_rel(lse.cpu()[idx], r_lse, 1e-4, what="lse")
+    assert_rel(ent.cpu()[idx], r_ent, 1e-4, what="entropy")
+    assert_rel(loss.cpu()[idx], r_loss, 1e-4, what="loss")
+    assert torch.equal(cor.cpu().bool()[idx], r_cor)
+    for i, r in enumerate(sample):
+        if mode == "rows":
+            if lab[r]:
+                assert_f16_ulp(g[int(slot[r])], r_new[i], 1, f"grad row {r}")
+        else:
+            assert_f16_ulp(new[r], r_new[i], 1, f"row {r}")
+    # every row's statistics equal a one-row launch of that row at the same address (the
+    # row's alignment fixes how its columns split into chunks, hence the summation order):
+    # a walk must not leak state from one row into the next; rows spread over all passes
+    fresh = z.to(DEV)
+    for r in range(0, rows, max(1, rows // 40)):
+        one = [torch.empty(1, dtype=t.dtype, device=DEV) for t in (ent, loss, cor, lse)]
+        head.head_stats_grad_rows(fresh[r:r + 1], targets[r:r + 1].to(DEV), None, None,
+                                  one[0], one[1], one[2], scale, one[3])
+        for got, want in zip(one, (ent, loss, cor, lse)):
+            assert torch.equal(got.cpu()[0], want.cpu()[r]), r

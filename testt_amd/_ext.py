@@ -45,6 +45,7 @@ SIGNATURES = {
     "soupk_time_next_launch": [_p, _p],
     "soupk_bench_copy": [_p, _p, _i64, _p],
     "soupk_bench_empty": [_i32, _p],
+    "soupk_bench_hold": [ctypes.c_double, _p],
     "soupk_attention_fwd": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p],
     "soupk_attention_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
                             _i32, _f32, _p],
@@ -121,11 +122,23 @@ def ptr(tensor):
     return None if tensor is None else tensor.data_ptr()
 
 
+# torch's raw current-stream query: the handle torch.cuda.current_stream(device).cuda_stream
+# returns, without building a Stream object on every kernel call (about 1 us of host time).
+# It is not public API, so the public form stands in wherever it is absent;
+# tests/test_gpu_streams.py checks that both give the same handle.
+_RAW_STREAM = getattr(getattr(torch, "_C", None), "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(tensor):
-    """The current HIP stream of the tensor's device, as a raw handle (torch's raw-stream query:
-    the same handle as torch.cuda.current_stream(device).cuda_stream, without building a
-    Stream object on every kernel call)."""
-    return torch._C._cuda_getCurrentRawStream(tensor.device.index)
+    """The current HIP stream of the tensor's device, as a raw handle."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(tensor.device.index)
+    return public_stream_of(tensor)
+
+
+def public_stream_of(tensor):
+    """stream_of through torch's public API."""
+    return torch.cuda.current_stream(tensor.device).cuda_stream
 
 
 def require(tensor, name, dtype=None, ndim=None, device=None):

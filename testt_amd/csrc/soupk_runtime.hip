@@ -10,6 +10,7 @@ namespace soupk {
 namespace {
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];  // 0 = not queried yet (zero-initialised static)
+std::atomic<int> g_wall_khz[kMaxDevices];  // device wall-clock rate in kHz, 0 = not queried yet
 thread_local hipEvent_t t_timing_start = nullptr;
 thread_local hipEvent_t t_timing_stop = nullptr;
 }  // namespace
@@ -82,6 +83,24 @@ __global__ __launch_bounds__(kCopyThreads) void bench_copy_kernel(const u32x4* _
 // with no work), timed like every kernel of the set.
 __global__ __launch_bounds__(256) void bench_empty_kernel() {}
 
+// One wave that holds its stream for `ticks` of the device's constant-rate wall clock
+// (s_memrealtime), sleeping between reads; it always ends once the clock has advanced that far.
+__global__ __launch_bounds__(64) void bench_hold_kernel(uint64_t ticks) {
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(16);
+}
+
+int device_wall_khz() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = g_wall_khz[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeWallClockRate, dev) != hipSuccess || n <= 0)
+    return 0;
+  g_wall_khz[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 }  // namespace
 }  // namespace soupk
 
@@ -92,6 +111,16 @@ extern "C" __attribute__((visibility("default"))) int soupk_bench_empty(int32_t 
   if (workgroups <= 0) return kInvalid;
   return launch_kernel(bench_empty_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256),
                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_bench_hold(double microseconds,
+                                                                       void* stream) {
+  if (!(microseconds >= 0.0) || microseconds > 2.0e6) return kInvalid;  // (NaN too)
+  const int khz = device_wall_khz();
+  if (khz <= 0) return static_cast<int>(hipErrorNotSupported);
+  const uint64_t ticks = static_cast<uint64_t>(microseconds * khz / 1000.0);
+  return launch_kernel(bench_hold_kernel, dim3(1), dim3(64), static_cast<hipStream_t>(stream),
+                       ticks);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_bench_copy(const void* src, void* dst,
