@@ -208,3 +208,29 @@ def test_rope_attention_autograd_matches_padded_path(lengths, T):
     assert torch.equal(_bits(out_a), _bits(out_b))
     for name, a, b in zip(("qkv", "lora_q", "lora_v"), leaves_a, leaves_b):
         assert torch.equal(_bits(a.grad), _bits(b.grad)), name
+
+
+def test_varlen_backward_rejects_mismatched_inputs():
+    """attention_varlen_bwd checks every tensor it hands the kernels (shapes, dtypes, the RoPE
+    tables' rows) before launching: a short lse or table would be read past its end."""
+    M, NH, NKV, D = 40, 4, 2, 128
+    W = (NH + 2 * NKV) * D
+    qkv = torch.zeros(M, W, dtype=torch.float16, device=DEV)
+    cu = torch.tensor([0, 25, 40], dtype=torch.int32, device=DEV)
+    out = torch.zeros(M, NH * D, dtype=torch.float16, device=DEV)
+    lse = torch.zeros(NH, M, dtype=torch.float32, device=DEV)
+    dout = torch.zeros_like(out)
+    cos = torch.ones(32, D, device=DEV)
+    sin = torch.zeros(32, D, device=DEV)
+    pos = torch.arange(M, device=DEV)
+    good = dict(qkv_r=qkv, cu_seqlens=cu, out=out, lse=lse, dout=dout, scale=0.1, n_heads=NH,
+                n_kv=NKV, rope=(cos, sin, pos, 2, 32))
+    attention.attention_varlen_bwd(**good)
+    torch.cuda.synchronize()
+    bad = [dict(lse=lse[:, :M - 1].contiguous()), dict(lse=lse.t().contiguous()),
+           dict(out=out[:M - 1]), dict(cu_seqlens=cu.long()),
+           dict(rope=(cos[:20].contiguous(), sin, pos, 2, 32)),
+           dict(rope=(cos, sin, pos[:M - 1], 2, 32)), dict(qkv_r=qkv[:, :W - 8].contiguous())]
+    for change in bad:
+        with pytest.raises((ValueError, TypeError)):
+            attention.attention_varlen_bwd(**{**good, **change})

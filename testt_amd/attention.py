@@ -72,8 +72,18 @@ def attention_varlen_bwd(qkv_r, cu_seqlens, out, lse, dout, scale, n_heads, n_kv
     """dqkv [M, W] fp16: the gradient of qkv_r's rows, or -- with rope = (cos, sin, pos, batch,
     seq) (fp32 tables [>= seq, 128], int64 padded positions b*seq + t) -- of the q|k|v rows
     before the rotation, RoPE's backward applied inside the kernels."""
+    _ext.require(qkv_r, "qkv_r", dtype=torch.float16, ndim=2)
     M = qkv_r.shape[0]
     dev = qkv_r.device
+    if qkv_r.shape[1] != (n_heads + 2 * n_kv) * HEAD_DIM:
+        raise ValueError(f"qkv_r width {qkv_r.shape[1]} != {(n_heads + 2 * n_kv) * HEAD_DIM}")
+    _ext.require(cu_seqlens, "cu_seqlens", dtype=torch.int32, ndim=1, device=dev)
+    _ext.require(out, "out", dtype=torch.float16, ndim=2, device=dev)
+    if tuple(out.shape) != (M, n_heads * HEAD_DIM):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {(M, n_heads * HEAD_DIM)}")
+    _ext.require(lse, "lse", dtype=torch.float32, ndim=2, device=dev)
+    if tuple(lse.shape) != (n_heads, M):
+        raise ValueError(f"lse has shape {tuple(lse.shape)}, expected {(n_heads, M)}")
     dout = dout.to(torch.float16).contiguous()
     _ext.require(dout, "dout", dtype=torch.float16, ndim=2, device=dev)
     if tuple(dout.shape) != tuple(out.shape):
@@ -87,6 +97,13 @@ def attention_varlen_bwd(qkv_r, cu_seqlens, out, lse, dout, scale, n_heads, n_kv
     slots, t_rope = 0, 0
     if rope is not None:
         cos, sin, pos, batch, seq = rope
+        for name, t in (("cos", cos), ("sin", sin)):
+            _ext.require(t, name, dtype=torch.float32, ndim=2, device=dev)
+            if t.shape[0] < seq or t.shape[1] != HEAD_DIM:
+                raise ValueError(f"{name} must be [>= {seq}, {HEAD_DIM}], got {tuple(t.shape)}")
+        _ext.require(pos, "pos", dtype=torch.int64, ndim=1, device=dev)
+        if pos.numel() != M:
+            raise ValueError(f"pos has {pos.numel()} entries for {M} rows")
         slots, t_rope = batch * seq, seq
     _ext.call("soupk_attention_varlen_bwd", _ext.ptr(qkv_r), _ext.ptr(cu_seqlens), B,
               _ext.ptr(out), _ext.ptr(dout), _ext.ptr(lse), _ext.ptr(cos),
