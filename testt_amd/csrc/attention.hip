@@ -13,14 +13,14 @@
 //
 // Forward (flash attention, online softmax): a workgroup is 4 wavefronts and 64 queries of one
 // (batch, head); wavefront w owns queries 16w..16w+15.  Key blocks of 64 rows are staged in LDS
-// -- K row-major, V transposed (key-contiguous) -- and each wavefront computes
+// -- K and V row-major -- and each wavefront computes
 //   S^T (64 keys x 16 queries) = K Q^T        (A = K rows from LDS, B = Q^T from registers)
 // so that, in the C layout, lane l holds the scores of query l%16 for keys 16n + 4(l/16) + i
 // of key tile n.  Two C tiles (n = 2m, 2m+1) together are the B operand of
 //   O^T (128 x 16) += V^T P^T                  (A = V^T from LDS, B = P^T from registers)
 // when the contraction index j of group gr stands for key 32m + 4gr + j (j < 4) or
-// 32m + 16 + 4gr + (j - 4): the A operand is read in the same order, as two 8-byte runs of a
-// V^T row.  The online-softmax state of a query is local to its four lanes (l%16 + 16r), which
+// 32m + 16 + 4gr + (j - 4): the A operand is read in the same order, with LDS transpose reads
+// of the row-major V tile (lds_runs_tr).  The online-softmax state of a query is local to its four lanes (l%16 + 16r), which
 // combine block maxima and final sums with v_permlane16_swap / v_permlane32_swap (no LDS).
 // Scores are kept in base 2: x = s * scale * log2(e), p = 2^(x - m).  The reference value m of
 // a query is raised only when a block maximum exceeds it by more than 8 (p <= 2^8 otherwise,
@@ -29,9 +29,8 @@
 // per-query log-sum-exp (natural log) for the backward pass; a query with no visible key gets
 // output 0 and lse = +inf (so its backward probabilities are 0).
 //
-// LDS strides: row-major tiles [64][136] halves (16-byte reads of 8 lanes hit 8 distinct
-// 4-bank groups), transposed tiles [128][68] halves (8-byte reads of 16 lanes hit 16 distinct
-// 2-bank pairs).
+// LDS: row-major tiles [64][136] halves (16-byte reads of 8 lanes hit 8 distinct 4-bank
+// groups).
 
 #include "fastdiv.hpp"
 #include "soupk_common.hpp"
@@ -48,7 +47,6 @@ constexpr int kBQ = 64;               // queries per workgroup (4 wavefronts x 1
 constexpr int kBK = 64;               // keys per block
 constexpr int kAttnThreads = 256;
 constexpr int kRStride = kD + 8;      // row-major tile row stride (halves), 272 B
-constexpr int kTStride = kBK + 4;     // transposed tile row stride (halves), 136 B
 constexpr float kRescaleMargin = 8.f;  // log2 of the largest unnormalised probability kept
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
@@ -59,12 +57,25 @@ __device__ __forceinline__ h8 lds_h8(const _Float16* p) {
   return *reinterpret_cast<const h8*>(p);
 }
 
-// The A operand of a product contracted over keys (or queries) from a transposed tile row:
-// elements 32m + 4gr .. +3, then 32m + 16 + 4gr .. +3 (the order of two C tiles 2m, 2m+1).
-__device__ __forceinline__ h8 lds_runs(const _Float16* row, int m, int gr) {
-  const h4 lo = *reinterpret_cast<const h4*>(row + 32 * m + 4 * gr);
-  const h4 hi = *reinterpret_cast<const h4*>(row + 32 * m + 16 + 4 * gr);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+// The A operand of a product contracted over keys (or queries), read transposed from a
+// row-major tile rm (row stride ld halves): lane l gets column col0 + l%16 at rows
+// 32m + 4gr .. +3, then 32m + 16 + 4gr .. +3 (the order of the two C tiles 2m, 2m+1 it meets).
+// Two ds_read_b64_tr_b16: within each 16-lane group, result lane i element j is element i%4
+// of the 8-byte read of lane 4j + i/4, so lane k of group gr reads row r0 + k/4 at columns
+// col0 + 4(k%4) (r0 = 32m + 4gr, then + 16); result lane i then holds rows r0..r0+3 of column
+// col0 + i.  (Layout checked on the device.)  Against a transposed copy of the tile built
+// with 4-byte LDS stores: forward 16.1 -> 15.5 us, backward 47.5 -> 45.3 us, identical bits.
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
+typedef __attribute__((address_space(3))) _Float16 lds_h;
+__device__ __forceinline__ h8 lds_runs_tr(const _Float16* rm, int ld, int col0, int m, int gr) {
+  const int k = threadIdx.x & 15;
+  const int row = 32 * m + 4 * gr + (k >> 2), col = col0 + 4 * (k & 3);
+  const lds_h* base = (const lds_h*)(rm);   // (an address-space cast: rm points into LDS)
+  const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + row * ld + col));
+  const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + (row + 16) * ld + col));
+  const h4 l4 = __builtin_bit_cast(h4, lo), h4v = __builtin_bit_cast(h4, hi);
+  return __builtin_shufflevector(l4, h4v, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // Max / sum over the four lanes of a column (l%16 + 16r, r = 0..3): rows 0<->1 and 2<->3 are
@@ -89,9 +100,8 @@ __device__ __forceinline__ float column_sum(float v) {
 }
 
 // A [64 x 128] fp16 tile (64 rows of one head) is staged through registers: thread item
-// it (0, 1) covers rows 2rp, 2rp+1 at dims 8dc..8dc+7 (tile_item), so
-// one pair of 16-byte row loads gives both the row-major LDS copy and, packed two rows to a
-// 4-byte word, the transposed one.  The loads of block i+1 are issued before block i is
+// it (0, 1) covers rows 2rp, 2rp+1 at dims 8dc..8dc+7 (tile_item), one pair of 16-byte row
+// loads and two 16-byte LDS stores.  The loads of block i+1 are issued before block i is
 // computed and written to LDS after the next barrier, so their latency overlaps the MFMAs.
 // Row indices past the end clamp to the last row (a finite value): the callers give such rows
 // zero weight (key flags, query bounds), so no branch guards the loads.  The pointers these
@@ -103,11 +113,10 @@ struct TileRegs {
 
 // Which row pair rp (0..31) and 8-dim chunk dc (0..15) thread item `it` covers: a
 // wavefront's item covers 16 row pairs x 4 chunks, lane bits (dc0, rp0, rp1, rp2, dc1, rp3).
-// Each 16-lane group of a 16-byte row-major store then writes 8 row pairs x 2 chunks, and the
-// 64 lanes of a 4-byte transposed store 16 pairs x 4 chunks, both on distinct LDS banks (lane
-// l covering pair l % 32 gave 2-way conflicts on both), and the global loads read 64
-// contiguous bytes per row.  Measured on MI355X: forward 20.0 -> 18.3 us, backward 39.8 ->
-// 36.7 us at the 2048-token shape.
+// Each 16-lane group of a 16-byte row-major store then writes 8 row pairs x 2 chunks on
+// distinct LDS banks, and the global loads read 64 contiguous bytes per row.  (With the
+// transposed tile copies this layout replaced, it took the forward from 20.0 to 18.3 us and
+// the backward from 39.8 to 36.7 us at the 2048-token shape.)
 __device__ __forceinline__ void tile_item(int it, int& rp, int& dc) {
   const int lane = threadIdx.x & 63, wi = (threadIdx.x >> 6) + 4 * it;
   rp = 16 * (wi & 1) + ((lane >> 1) & 7) + 8 * (lane >> 5);
@@ -136,36 +145,18 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* src, int6
 // instead of being moved down to their use in the next iteration.
 __device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
 
-// Rows (2rp, 2rp+1) x 8 dims: row-major into `rm` ([64][kRStride]) and/or transposed into
-// `tr` ([128][kTStride]).
-template <bool RM, bool TR>
-__device__ __forceinline__ void stage_pair(_Float16* rm, _Float16* tr, u32x4 a, u32x4 b, int rp,
-                                           int dc) {
-  if constexpr (RM) {
-    *reinterpret_cast<u32x4*>(rm + (2 * rp) * kRStride + 8 * dc) = a;
-    *reinterpret_cast<u32x4*>(rm + (2 * rp + 1) * kRStride + 8 * dc) = b;
-  }
-  if constexpr (TR) {
-    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    uint32_t* col = reinterpret_cast<uint32_t*>(tr + (8 * dc) * kTStride + 2 * rp);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // d = 8dc + 2j (low halves) and 8dc + 2j + 1 (high halves)
-      // one v_perm_b32 per word: byte k of the result is byte sel[k] of {bw (bytes 4-7), aw
-      // (bytes 0-3)} (against an and / shift / or pair: 1.6% off the forward, identical bits)
-      col[(2 * j) * (kTStride / 2)] = __builtin_amdgcn_perm(bw[j], aw[j], 0x05040100u);
-      col[(2 * j + 1) * (kTStride / 2)] = __builtin_amdgcn_perm(bw[j], aw[j], 0x07060302u);
-    }
-  }
+// Rows (2rp, 2rp+1) x 8 dims, row-major into `rm` ([64][kRStride]).
+__device__ __forceinline__ void stage_pair(_Float16* rm, u32x4 a, u32x4 b, int rp, int dc) {
+  *reinterpret_cast<u32x4*>(rm + (2 * rp) * kRStride + 8 * dc) = a;
+  *reinterpret_cast<u32x4*>(rm + (2 * rp + 1) * kRStride + 8 * dc) = b;
 }
 
-template <bool RM, bool TR>
-__device__ __forceinline__ void store_tile(_Float16* rm, _Float16* tr, const TileRegs& r) {
+__device__ __forceinline__ void store_tile(_Float16* rm, const TileRegs& r) {
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     int rp, dc;
     tile_item(it, rp, dc);
-    stage_pair<RM, TR>(rm, tr, r.a[it], r.b[it], rp, dc);
+    stage_pair(rm, r.a[it], r.b[it], rp, dc);
   }
 }
 
@@ -282,7 +273,7 @@ __device__ __forceinline__ SeqHead seq_head(const AttnParams& p, int b, int h) {
 
 // One query block of one (sequence, head): flash-attention forward.
 __device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHead& sh, int qb,
-                                               _Float16* Ks, _Float16* Vt, uint8_t* kflag) {
+                                               _Float16* Ks, _Float16* Vs, uint8_t* kflag) {
   const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
@@ -309,8 +300,8 @@ __device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHea
   uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
   for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
-    store_tile<true, false>(Ks, nullptr, kr);
-    store_tile<false, true>(nullptr, Vt, vr);
+    store_tile(Ks, kr);
+    store_tile(Vs, vr);   // V row-major too: its V^T fragments are read transposed
     if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
     load_tile(kr, kbase, sh.ld_kv, (kb + 1) * kBK, T);   // the next block (clamped past the end)
@@ -380,9 +371,9 @@ __device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHea
     // O^T += V^T P^T
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const _Float16* vrow = Vt + (16 * t + ql) * kTStride;
 #pragma unroll
-      for (int m = 0; m < 2; ++m) acc[t] = mfma32(lds_runs(vrow, m, gr), pb[m], acc[t]);
+      for (int m = 0; m < 2; ++m)
+        acc[t] = mfma32(lds_runs_tr(Vs, kRStride, 16 * t, m, gr), pb[m], acc[t]);
     }
   }
   const float l_tot = column_sum(lsum);
@@ -407,11 +398,11 @@ __device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHea
 template <bool VARLEN>
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(AttnParams p) {
   __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
-  __shared__ __align__(16) _Float16 Vt[kD * kTStride];
+  __shared__ __align__(16) _Float16 Vs[kBK * kRStride];
   __shared__ __align__(16) uint8_t kflag[kBK];
   const SeqHead sh = seq_head<VARLEN>(p, blockIdx.y, blockIdx.x);
   const int qb = (sh.len + kBQ - 1) / kBQ - 1 - static_cast<int>(blockIdx.z);
-  if (qb >= 0) attn_fwd_block(p, sh, qb, Ks, Vt, kflag);
+  if (qb >= 0) attn_fwd_block(p, sh, qb, Ks, Vs, kflag);
 }
 
 // ---- backward ------------------------------------------------------------------------------
@@ -429,9 +420,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(AttnParams p) {
 //          head;
 //   attn_bwd_reduce_kernel: dK, dV of a key/value head = the sum of its query heads' partials
 //                         (a fixed order: deterministic), fp16.
-// Operands contracted over the head dim are read from row-major tiles (16-byte reads);
-// operands contracted over keys or queries from transposed tiles, in the order of the C tiles
-// they meet (lds_runs).
+// Every tile is staged row-major.  Operands contracted over the head dim are read with
+// 16-byte LDS reads; operands contracted over keys or queries with LDS transpose reads of
+// the same tiles, in the order of the C tiles they meet (lds_runs_tr).
 
 // D = rowsum(dO * O) of 64 queries: lane (row l%16 of wavefront w's 16, group l/16) sums dims
 // 32s + 8gr .. +7 (s = 0..3) in order, then the four groups are combined by column_sum.
@@ -464,8 +455,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_delta_kernel(
   if (gr == 0 && q_abs < T) delta[(static_cast<int64_t>(b) * NH + h) * T + q_abs] = dsum;
 }
 
-// LDS of the backward workgroups (the larger of the two kinds: dKdV's Q, Q^T, dO, dO^T tiles).
-constexpr int kBwdLdsBytes = 2 * (kBQ * kRStride + kD * kTStride) * 2 + 2 * kBQ * 4;
+// LDS of the backward workgroups (the larger of the two kinds: dKdV's Q and dO tiles and the
+// block's lse / D values).
+constexpr int kBwdLdsBytes = 2 * kBQ * kRStride * 2 + 2 * kBQ * 4;
 
 // fp32 -> fp16 -> fp32: the value a kernel that stores fp16 hands to the next one.
 __device__ __forceinline__ float round_h(float x) { return lo_h(pack_h2(x, 0.f)); }
@@ -504,8 +496,7 @@ __device__ __forceinline__ void attn_bwd_dq(const AttnParams& p, const SeqHead& 
                                             int qb, unsigned char* smem) {
   _Float16* Ks = reinterpret_cast<_Float16*>(smem);
   _Float16* Vs = Ks + kBK * kRStride;
-  _Float16* Kt = Vs + kBK * kRStride;
-  uint8_t* kflag = reinterpret_cast<uint8_t*>(Kt + kD * kTStride);
+  uint8_t* kflag = reinterpret_cast<uint8_t*>(Vs + kBK * kRStride);
   const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int ql = lane & 15, gr = lane >> 4;
@@ -537,8 +528,8 @@ __device__ __forceinline__ void attn_bwd_dq(const AttnParams& p, const SeqHead& 
   uint8_t fl_raw = load_flag_raw(valid, kbase, 0, T);
   for (int kb = 0; kb <= qb; ++kb) {
     __syncthreads();
-    store_tile<true, true>(Ks, Kt, kr);
-    store_tile<true, false>(Vs, nullptr, vr);
+    store_tile(Ks, kr);   // K^T fragments read transposed from Ks
+    store_tile(Vs, vr);
     if (threadIdx.x < kBK) kflag[threadIdx.x] = key_flag(fl_raw, has_valid, kb * kBK, T);
     __syncthreads();
     load_tile(kr, kbase, sh.ld_kv, (kb + 1) * kBK, T);   // the next block (clamped past the end)
@@ -573,9 +564,9 @@ __device__ __forceinline__ void attn_bwd_dq(const AttnParams& p, const SeqHead& 
     // dQ^T += K^T dS^T
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const _Float16* krow = Kt + (16 * t + ql) * kTStride;
 #pragma unroll
-      for (int m = 0; m < 2; ++m) acc[t] = mfma32(lds_runs(krow, m, gr), dsb[m], acc[t]);
+      for (int m = 0; m < 2; ++m)
+        acc[t] = mfma32(lds_runs_tr(Ks, kRStride, 16 * t, m, gr), dsb[m], acc[t]);
     }
   }
   if (q_abs >= T) return;
@@ -630,10 +621,8 @@ __device__ __forceinline__ void attn_bwd_dq(const AttnParams& p, const SeqHead& 
 __device__ __forceinline__ void attn_bwd_dkdv(const AttnParams& p, const SeqHead& sh, int kb,
                                               unsigned char* smem) {
   _Float16* Qs = reinterpret_cast<_Float16*>(smem);
-  _Float16* Qt = Qs + kBQ * kRStride;
-  _Float16* Ds = Qt + kD * kTStride;    // dO row-major
-  _Float16* Dt = Ds + kBQ * kRStride;   // dO transposed
-  float* lse2_s = reinterpret_cast<float*>(Dt + kD * kTStride);
+  _Float16* Ds = Qs + kBQ * kRStride;   // dO row-major
+  float* lse2_s = reinterpret_cast<float*>(Ds + kBQ * kRStride);
   float* delta_s = lse2_s + kBQ;
   const int T = sh.len;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
@@ -674,8 +663,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const AttnParams& p, const SeqHead
   load_block(kb * kBQ);
   for (int qb = kb; qb < nqb; ++qb) {
     __syncthreads();
-    store_tile<true, true>(Qs, Qt, qr);
-    store_tile<true, true>(Ds, Dt, dr);
+    store_tile(Qs, qr);   // Q^T, dO^T fragments read transposed
+    store_tile(Ds, dr);
     if (threadIdx.x < kBQ) {
       const bool in = qb * kBQ + static_cast<int>(threadIdx.x) < T;
       lse2_s[threadIdx.x] = in ? lse_raw * kLog2e : INFINITY;
@@ -721,12 +710,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const AttnParams& p, const SeqHead
     // dV^T += dO^T P, dK^T += Q^T dS  (contraction over the block's queries)
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const _Float16* drow = Dt + (16 * t + kl) * kTStride;
-      const _Float16* qtrow = Qt + (16 * t + kl) * kTStride;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        dv[t] = mfma32(lds_runs(drow, m, gr), pb[m], dv[t]);
-        dk[t] = mfma32(lds_runs(qtrow, m, gr), dsb[m], dk[t]);
+        dv[t] = mfma32(lds_runs_tr(Ds, kRStride, 16 * t, m, gr), pb[m], dv[t]);
+        dk[t] = mfma32(lds_runs_tr(Qs, kRStride, 16 * t, m, gr), dsb[m], dk[t]);
       }
     }
   }
