@@ -64,7 +64,7 @@ __device__ __forceinline__ h8 lds_h8(const _Float16* p) {
 // of the 8-byte read of lane 4j + i/4, so lane k of group gr reads row r0 + k/4 at columns
 // col0 + 4(k%4) (r0 = 32m + 4gr, then + 16); result lane i then holds rows r0..r0+3 of column
 // col0 + i.  (Layout checked on the device.)  Against a transposed copy of the tile built
-// with 4-byte LDS stores: forward 16.1 -> 15.5 us, backward 47.5 -> 45.3 us, identical bits.
+// with 4-byte LDS stores: forward 16.1 -> 15.4 us, backward 47.5 -> 46.0 us, identical bits.
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4 lds_s4;
 typedef __attribute__((address_space(3))) _Float16 lds_h;
@@ -395,9 +395,17 @@ __device__ __forceinline__ void attn_fwd_block(const AttnParams& p, const SeqHea
 // the padded layout, ceil(M/64) for varlen, since no sequence holds more than M tokens): slots
 // past a sequence's blocks exit at once.  (A loop over several blocks per workgroup cost
 // 0.5 us forward and backward at the step's shape; the idle workgroups measured nothing.)
+// One forward workgroup per CU: the K tile array is padded so that a workgroup's LDS exceeds
+// half of a CU's 160 KB.  The dispatcher then never places a second workgroup beside one that
+// walks a long causal key range (the heaviest are dispatched first), and the lighter ones start
+// on whichever CU frees first.  At 2048 tokens (4 x 512) 15.24 -> 15.04 us, on rows of 512,
+// 512, 256 and 128 tokens 14.48 -> 13.04 us, no case slower.
+constexpr int kFwdLdsPad = 24576;   // halves
+static_assert((2 * kBK * kRStride + kFwdLdsPad) * 2 > 80 * 1024, "one workgroup per CU");
+
 template <bool VARLEN>
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(AttnParams p) {
-  __shared__ __align__(16) _Float16 Ks[kBK * kRStride];
+  __shared__ __align__(16) _Float16 Ks[kBK * kRStride + kFwdLdsPad];
   __shared__ __align__(16) _Float16 Vs[kBK * kRStride];
   __shared__ __align__(16) uint8_t kflag[kBK];
   const SeqHead sh = seq_head<VARLEN>(p, blockIdx.y, blockIdx.x);
