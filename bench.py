@@ -666,6 +666,57 @@ def time_attention(dev, steps, warmup):
     return res
 
 
+def time_nf4_gemm(dev, calls=40):
+    """GPU time per call (microseconds) of the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py,
+    csrc/gemm_nf4.hip) against hipBLASLt on the unpacked weight, at M = 2048 for the four
+    projections of a layer (q|k|v and gate|up as stacked parts): the fused kernel on fp16 and
+    on NF4 weights, hipBLASLt (torch.matmul) on fp16 weights, the standalone unpack
+    (nf4.unpack_concat) and unpack + hipBLASLt.  Each variant: 5 untimed calls, then `calls`
+    calls queued behind a DeviceHold and timed as one span (torch events), so host overhead is
+    not in the figure.  Synthetic NF4 weights (workloads.nf4_weight), x ~ N(0, 1)."""
+    from testt_amd import nf4, nf4_gemm
+
+    hold = DeviceHold(dev)
+
+    def span_us(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        hold.hold(calls * 250 + 3000)
+        e0.record()
+        for _ in range(calls):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return round(e0.elapsed_time(e1) * 1e3 / calls, 2)
+
+    M = 2048
+    shapes = {"qkv": ((workloads.N_HEADS * workloads.HEAD_DIM, workloads.N_KV * workloads.HEAD_DIM,
+                       workloads.N_KV * workloads.HEAD_DIM), workloads.HIDDEN),
+              "o": ((workloads.HIDDEN,), workloads.N_HEADS * workloads.HEAD_DIM),
+              "gate_up": ((workloads.INTER, workloads.INTER), workloads.HIDDEN),
+              "down": ((workloads.HIDDEN,), workloads.INTER)}
+    out = {}
+    for name, (rows, K) in shapes.items():
+        log(f"nf4 gemm: {name} ({sum(rows)} x {K}, M = {M})")
+        ws = [workloads.nf4_weight(r, K, seed=50 + i, device=dev) for i, r in enumerate(rows)]
+        g = workloads.gen(K)
+        x = torch.randn(M, K, generator=g).to(torch.float16).to(dev)
+        w16 = nf4.unpack_concat(ws, dev)
+        out[name] = {
+            "N": sum(rows), "K": K, "M": M,
+            "fused_fp16_w_us": span_us(lambda: nf4_gemm.gemm_tn(x, w16)),
+            "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(x, ws)),
+            "hipblaslt_fp16_w_us": span_us(lambda: torch.matmul(x, w16.t())),
+            "unpack_us": span_us(lambda: nf4.unpack_concat(ws, dev)),
+            "unpack_then_hipblaslt_us": span_us(
+                lambda: torch.matmul(x, nf4.unpack_concat(ws, dev).t())),
+        }
+        del ws, x, w16
+    return out
+
+
 def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
     """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model (testt_amd/model.py: 28
     decoder layers, final norm, the chunked fused head loss over the 151,936-token vocabulary)
@@ -926,6 +977,34 @@ def summarize_kernels(stats_csv, title, command, top=30):
     return "\n".join(out) + "\n"
 
 
+def summarize_trace(trace_csv, title, command):
+    """Markdown table of every launch group of a rocprofv3 --kernel-trace run, in the order of
+    each group's first dispatch: calls, mean and median duration (hipBLASLt, torch and soupk
+    kernels alike).  A group is one (kernel, grid, workgroup) between two DeviceHold waits, so
+    launches of equal grids timed apart (two GEMMs with one output shape) stay apart; the
+    waits themselves are left out."""
+    groups, span = {}, 0
+    for r in sorted(_read_csv(trace_csv), key=lambda r: int(r["Dispatch_Id"])):
+        name = r["Kernel_Name"]
+        if "bench_hold_kernel" in name:
+            span += 1
+            continue
+        short = _kernel_base(name) if "soupk" in name else name.split("(")[0][:90]
+        grid = r.get("Grid_Size_X", r.get("Grid_Size"))
+        wg = r.get("Workgroup_Size_X", r.get("Workgroup_Size"))
+        groups.setdefault((short, int(grid), int(wg), span), []).append(r)
+    order = sorted(groups.items(), key=lambda kv: int(kv[1][0]["Dispatch_Id"]))
+    out = [f"# {title}", "", "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```",
+           command, "```", "", "Launches grouped by kernel and grid (threads / workgroup size) "
+           "between two device-side waits, in the order of their first dispatch:", "",
+           "| kernel | grid / WG | calls | avg us | median us |", "|---|---:|---:|---:|---:|"]
+    for (short, grid, wg, _), rs in order:
+        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rs]
+        out.append(f"| `{short}` | {grid} / {wg} | {len(d)} | {sum(d) / len(d):.2f} | "
+                   f"{median(d):.2f} |")
+    return "\n".join(out) + "\n"
+
+
 def summarize_step(trace_csv, title, command, n_layers=28, top=32):
     """Markdown breakdown of one training step from a rocprofv3 --kernel-trace run of bench.py:
     the launches between the first attention forward of one step and that of the next (steps
@@ -1081,6 +1160,12 @@ def main():
                          "(CPU)")
     ap.add_argument("--summarize-kernels", nargs=3, metavar=("STATS_CSV", "TITLE", "CMD"),
                     help="print every kernel of a rocprofv3 --stats run by total time (CPU)")
+    ap.add_argument("--nf4-gemm", action="store_true",
+                    help="time the fused NF4-dequant GEMM against hipBLASLt and unpack + "
+                         "hipBLASLt at M = 2048, print one JSON line and exit")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "TITLE", "CMD"),
+                    help="print every launch group (kernel, grid) of a rocprofv3 "
+                         "--kernel-trace run (CPU)")
     ap.add_argument("--summarize-step", nargs=3, metavar=("TRACE_CSV", "TITLE", "CMD"),
                     help="print the per-kernel breakdown of one training step of a rocprofv3 "
                          "--kernel-trace run (CPU)")
@@ -1091,6 +1176,9 @@ def main():
         return
     if args.summarize_step:
         sys.stdout.write(summarize_step(*args.summarize_step))
+        return
+    if args.summarize_trace:
+        sys.stdout.write(summarize_trace(*args.summarize_trace))
         return
     if args.summarize_kernels:
         sys.stdout.write(summarize_kernels(*args.summarize_kernels))
@@ -1124,6 +1212,11 @@ def main():
         gemm_table = {"table": os.path.relpath(gemm_tuning.RESULTS, ROOT), "accepted": accepted}
         log(f"tuned hipBLASLt solutions ({gemm_table['table']}): "
             f"{'replayed' if accepted else 'rejected by TunableOp, heuristic choices'}")
+    if args.nf4_gemm:
+        print(json.dumps({"nf4_gemm": time_nf4_gemm(dev), "gemm_selection": gemm_table,
+                          "timing": "GPU time per call: calls queued behind a device-side "
+                                    "wait and timed as one span"}), flush=True)
+        return
     log("building inputs")
     cases = build_cases(dev)
     torch.cuda.synchronize(dev)

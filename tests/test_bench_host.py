@@ -66,3 +66,25 @@ def test_pmc_traffic_scaled_and_read_back(tmp_path):
     assert bench.pmc_traffic("rope_pack_fwd", path) == 2560           # (1 x 2 + 0.5) KiB
     assert bench.pmc_traffic("rope_pack_fwd_ragged", path) == 1024    # (0.25 x 2 + 0.5) KiB
     assert bench.pmc_traffic("swiglu_bwd", path) is None
+
+
+def test_trace_summary_groups_every_kernel(tmp_path):
+    """summarize_trace: soupk and library kernels alike, grouped by (kernel, grid), in the order
+    of first dispatch, device-side waits left out."""
+    hdr = ["Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp",
+           "End_Timestamp"]
+    rows = [[1, K.format("bench_hold_kernel"), 64, 64, 0, 900000]]
+    for i in range(3):
+        rows.append([2 + i, K.format("gemm_tn_kernel<false>"), 65536, 256, 0, 20000 + 1000 * i])
+    rows.append([5, "Cijk_Ailk_Bljk_HHS_BH_MT256x256x64(args)", 1024, 256, 0, 18000])
+    rows.append([6, K.format("gemm_tn_kernel<false>"), 1024, 256, 0, 7000])
+    rows.append([7, K.format("bench_hold_kernel"), 64, 64, 0, 900000])   # the next span:
+    rows.append([8, K.format("gemm_tn_kernel<false>"), 65536, 256, 0, 9000])  # same grid
+    trace = _write(tmp_path / "trace.csv", hdr, rows)
+    text = bench.summarize_trace(trace, "title", "cmd")
+    lines = [ln for ln in text.splitlines() if ln.startswith("| `")]
+    assert len(lines) == 4 and "bench_hold" not in text
+    assert lines[0].startswith("| `gemm_tn_kernel<false>` | 65536 / 256 | 3 | 21.00 | 21.00 |")
+    assert lines[1].startswith("| `Cijk_Ailk_Bljk_HHS_BH_MT256x256x64` | 1024 / 256 | 1 | 18.00")
+    assert lines[2].startswith("| `gemm_tn_kernel<false>` | 1024 / 256 | 1 | 7.00")
+    assert lines[3].startswith("| `gemm_tn_kernel<false>` | 65536 / 256 | 1 | 9.00")

@@ -36,8 +36,9 @@ KEEP_UNPACKED_FOR_BACKWARD = True
 
 # FrozenNF4Linear's forward through the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py: W read
 # as NF4, dequantised in the GEMM's tile loads, no fp16 W in HBM) when the shapes allow it; its
-# backward then unpacks W.  Off by default: on MI355X that GEMM core is still slower than
-# hipBLASLt's tuned kernels (26 against 21 us on the 2048 x 2048 x 1536 q|k|v shape).
+# backward then unpacks W.  Off by default: on MI355X that GEMM core is slower than hipBLASLt's
+# tuned kernels (device time at M = 2048: q|k|v 22.8 against 18.4 us on fp16 W), and with the
+# dequantisation in its loop it is behind unpack + hipBLASLt (30.8 against 7.6 + 20.2 us).
 USE_FUSED_NF4_GEMM = False
 
 
