@@ -598,18 +598,21 @@ def time_attention(dev, steps, warmup):
     (512, 152, 128, 96 real tokens), the padded ones with key flags.  Algorithmic FLOPs: 4*D
     per visible (query, key) pair forward (S and P.V), 10*D backward (recomputed S, dP, dV, dK,
     dQ), L(L+1)/2 visible pairs per real row of L tokens and head; MFMA-bound, against
-    2.5 PFLOP/s dense fp16."""
+    2.5 PFLOP/s dense fp16.  The timed calls are queued behind a DeviceHold, so the span
+    holds the kernels' time, not the host's per-call overhead."""
     from testt_amd import attention
 
     B, T, NH, NKV, D = workloads.BATCH, workloads.SEQ, workloads.N_HEADS, workloads.N_KV, 128
     scale = 1.0 / math.sqrt(D)
     cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
+    hold = DeviceHold(dev)
 
     def timed(fn):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        hold.hold(steps * 150 + 3000)
         e0.record()
         for _ in range(steps):
             fn()

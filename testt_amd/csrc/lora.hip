@@ -425,21 +425,26 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
 // stages 64-row chunks of X (y, gs_q or gs_v: its 64 columns) and Z (dt or t) through LDS,
 // transposed so that each MFMA operand is 8 consecutive rows of one column, and writes fp32
 // partial sums per slice; lora_params_reduce_kernel adds the slices in order and rounds.
+// With the next chunk's loads issued before the current chunk's MFMAs and the reduce's loads
+// issued eight slices at a time, the pair took 10.5 us against 13.2 us at 2048 rows on
+// MI355X (identical bits); 256-row slices were faster at 2048 rows (9.4 us) but slower at 888
+// (8.0 against 7.3 us), 64-row slices slower at both.
 constexpr int kSlice = 128;        // rows per slice
 constexpr int kChunk = 64;         // rows per LDS chunk
 constexpr int kPStride = kChunk + 8;   // transposed tile row (halves): 144 B, 16-B aligned
 
-// Rows (2rp, 2rp+1) x 8 columns, loaded at clamped rows and zeroed past `rows`, written
-// transposed into tr[col][row] (stride kPStride) as 4-byte pairs.
-__device__ __forceinline__ void stage_pair_t(_Float16* tr, const uint16_t* src, int64_t ld,
-                                             int r0, int rows, int rp, int c8) {
+// Rows (2rp, 2rp+1) x 8 columns, loaded at clamped rows and zeroed past `rows` ...
+__device__ __forceinline__ void load_pair(const uint16_t* src, int64_t ld, int r0, int rows,
+                                          int rp, int c8, u32x4& a, u32x4& b) {
   const int t0 = r0 + 2 * rp, t1 = t0 + 1;
-  u32x4 a = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t0, rows - 1)) * ld +
-                                            8 * c8);
-  u32x4 b = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t1, rows - 1)) * ld +
-                                            8 * c8);
+  a = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t0, rows - 1)) * ld + 8 * c8);
+  b = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(min(t1, rows - 1)) * ld + 8 * c8);
   if (t0 >= rows) a = u32x4{0u, 0u, 0u, 0u};
   if (t1 >= rows) b = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ... and written transposed into tr[col][row] (stride kPStride) as 4-byte pairs.
+__device__ __forceinline__ void store_pair_t(_Float16* tr, u32x4 a, u32x4 b, int rp, int c8) {
   const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
   uint32_t* col = reinterpret_cast<uint32_t*>(tr + (8 * c8) * kPStride + 2 * rp);
 #pragma unroll
@@ -472,14 +477,23 @@ __global__ __launch_bounds__(kThreads) void lora_params_partial_kernel(
   //     and both Z tiles; dB: C = Z^T X (row = Z column, column = X column): wave w owns X
   //     columns 16w..+15.  Either way a lane's 4 results are 4 consecutive partial entries.
   f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  // Staging: 32 row pairs x 8 column chunks of X, and of Z for the first zc / 8 chunks (whole
+  // wavefronts).  The next chunk's loads are issued before the current chunk's MFMAs.
+  const int rp = threadIdx.x & 31, c8 = threadIdx.x >> 5;
+  const bool has_z = c8 < zc / 8;
+  u32x4 xa, xb, za = {0u, 0u, 0u, 0u}, zb = za;
+  load_pair(X + col0, ldx, r_begin, r_end, rp, c8, xa, xb);
+  if (has_z) load_pair(Z, 2 * kR, r_begin, r_end, rp, c8, za, zb);
   for (int r0 = r_begin; r0 < r_end; r0 += kChunk) {
     __syncthreads();
-    {
-      const int rp = threadIdx.x & 31, c8 = threadIdx.x >> 5;   // 32 row pairs x 8 chunks
-      stage_pair_t(XT, X + col0, ldx, r0, r_end, rp, c8);
-      if (c8 < zc / 8) stage_pair_t(ZT, Z, 2 * kR, r0, r_end, rp, c8);
-    }
+    store_pair_t(XT, xa, xb, rp, c8);
+    if (has_z) store_pair_t(ZT, za, zb, rp, c8);
     __syncthreads();
+    if (r0 + kChunk < r_end) {
+      load_pair(X + col0, ldx, r0 + kChunk, r_end, rp, c8, xa, xb);
+      if (has_z) load_pair(Z, 2 * kR, r0 + kChunk, r_end, rp, c8, za, zb);
+    }
+    __asm__ volatile("" ::: "memory");   // keep the prefetch above the MFMAs
 #pragma unroll
     for (int s = 0; s < kChunk / 32; ++s) {
       const h8 xf = *reinterpret_cast<const h8*>(XT + (16 * w + ql) * kPStride + 32 * s + 8 * gr);
@@ -516,8 +530,17 @@ __global__ __launch_bounds__(256) void lora_params_reduce_kernel(
     float* __restrict__ dbv) {
   const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (o >= n_out) return;
+  // Eight slices' loads issued together (clamped, so unconditional), then added in slice order.
   float s = 0.f;
-  for (int i = 0; i < slices; ++i) s += part[static_cast<int64_t>(i) * n_out + o];
+  for (int i0 = 0; i0 < slices; i0 += 8) {
+    float v8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v8[j] = part[static_cast<int64_t>(min(i0 + j, slices - 1)) * n_out + o];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + j < slices) s += v8[j];
+  }
   const float v = r16(s);
   const int64_t na = static_cast<int64_t>(kR) * H;
   if (o < na) daq[o] = v;
