@@ -26,7 +26,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; soupk_abi_version() returns the library's. */
-#define SOUPK_ABI_VERSION 2
+#define SOUPK_ABI_VERSION 3
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
 #define SOUPK_STATUS_SCRATCH_LIMIT 20001
@@ -304,29 +304,40 @@ int soupk_attention_varlen_bwd(const uint16_t* qkv, const int32_t* cu_seqlens, i
 /*
  * LoRA branch of the q and v projections for rank 16 (peft's lora_B(lora_A(x)) * scaling under
  * fp16 autocast, solution/model.py:195-206 with dropout 0; widening: the reference runs it as
- * separate fp16 GEMMs, casts and a scaling).  y [M, H] fp16; a_q, a_v [16, H] and b_q [NQ, 16],
- * b_v [NV, 16] the fp32 LoRA parameters (cast to fp16 inside, as .to(float16) rounds).
- * Writes t = fp16(y [a_q; a_v]^T) [M, 32] fp16 (kept for the backward),
+ * separate fp16 GEMMs, casts and a scaling).
+ *
+ * soupk_lora_stage casts the fp32 LoRA parameters a_q, a_v [16, H] and b_q [NQ, 16],
+ * b_v [NV, 16] to fp16 (as .to(float16) rounds) into `staged`, once per forward, in the layouts
+ * soupk_lora_fwd and soupk_lora_bwd_rows read: [a_q; a_v] [32, H], its transpose [H, 32],
+ * [b_q; b_v] [NQ + NV, 16], b_q^T [16, NQ], b_v^T [16, NV], in that order:
+ * staged_elems >= 128*H + 32*(NQ + NV) halves, 16-byte aligned.
+ */
+int soupk_lora_stage(const float* a_q, const float* a_v, const float* b_q, const float* b_v,
+                     uint16_t* staged, int64_t staged_elems, int32_t H, int32_t NQ, int32_t NV,
+                     int32_t r, void* stream);
+
+/*
+ * The forward: y [M, H] fp16, `staged` from soupk_lora_stage.  Writes
+ * t = fp16(y [a_q; a_v]^T) [M, 32] fp16 (kept for the backward),
  * lq = fp16(fp16(t[:, :16] b_q^T) * scaling) [M, NQ], lv likewise from t[:, 16:] and b_v.
  * H, NQ, NV multiples of 128; r must be 16; pointers 16-byte aligned (t: 2-byte).
  */
-int soupk_lora_fwd(const uint16_t* y, const float* a_q, const float* a_v, const float* b_q,
-                   const float* b_v, float scaling, uint16_t* t, uint16_t* lq, uint16_t* lv,
-                   int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream);
+int soupk_lora_fwd(const uint16_t* y, const uint16_t* staged, float scaling, uint16_t* t,
+                   uint16_t* lq, uint16_t* lv, int64_t M, int32_t H, int32_t NQ, int32_t NV,
+                   int32_t r, void* stream);
 
 /*
  * Its backward, the row-local part: with g_q [M, NQ] (row stride ld_q) and g_v [M, NV] (ld_v)
- * the fp16 gradients of lq and lv, writes gs_q = fp16(g_q * scaling) [M, NQ], gs_v [M, NV],
- * dt = fp16([gs_q b_q16 | gs_v b_v16]) [M, 32] and dy = fp16(dt [a_q16; a_v16]) [M, H] (the
- * LoRA part of the gradient of y; the caller adds the frozen projection's part in place).  The
- * parameter gradients are gs_q^T t[:, :16], gs_v^T t[:, 16:] and dt^T y.  Same shape rules;
- * ld_q, ld_v multiples of 8.
+ * the fp16 gradients of lq and lv, and the forward's `staged` parameters, writes
+ * gs_q = fp16(g_q * scaling) [M, NQ], gs_v [M, NV], dt = fp16([gs_q b_q16 | gs_v b_v16])
+ * [M, 32] and dy = fp16(dt [a_q16; a_v16]) [M, H] (the LoRA part of the gradient of y; the
+ * caller adds the frozen projection's part in place).  The parameter gradients are
+ * gs_q^T t[:, :16], gs_v^T t[:, 16:] and dt^T y.  Same shape rules; ld_q, ld_v multiples of 8.
  */
 int soupk_lora_bwd_rows(const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
-                        const float* a_q, const float* a_v, const float* b_q, const float* b_v,
-                        float scaling, uint16_t* gs_q, uint16_t* gs_v, uint16_t* dt,
-                        uint16_t* dy, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
-                        void* stream);
+                        const uint16_t* staged, float scaling, uint16_t* gs_q, uint16_t* gs_v,
+                        uint16_t* dt, uint16_t* dy, int64_t M, int32_t H, int32_t NQ,
+                        int32_t NV, int32_t r, void* stream);
 
 /*
  * Its backward, the parameter gradients (reductions over the M rows), each the fp16 GEMM result

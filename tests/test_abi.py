@@ -77,6 +77,10 @@ def test_version_and_status_strings(lib):
     ("soupk_bench_hold", (-1.0, None)),
     ("soupk_bench_hold", (2.5e6, None)),               # beyond the 2 s cap
     ("soupk_bench_hold", (float("nan"), None)),
+    # LoRA staging: a buffer short of 128*H + 32*(NQ + NV) halves, a rank other than 16
+    ("soupk_lora_stage", (16, 32, 48, 64, 128, 128 * 256 + 32 * 256 - 1, 256, 128, 128, 16,
+                          None)),
+    ("soupk_lora_stage", (16, 32, 48, 64, 128, 1 << 20, 256, 128, 128, 8, None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

@@ -41,6 +41,21 @@ def f64_16(t):
     return t.to(torch.float16).double()
 
 
+@pytest.mark.parametrize("H,NQ,NV", [(1536, 1536, 256), (256, 384, 128)])
+def test_stage_layouts(H, NQ, NV):
+    """soupk_lora_stage: the fp16 casts of the parameters (torch's rounding), in the four
+    layouts, in order: [A_q; A_v], its transpose, [B_q; B_v], B_q^T, B_v^T."""
+    print(f"lora stage H={H} NQ={NQ} NV={NV}", flush=True)
+    a_q, a_v, b_q, b_v = params(H, NQ, NV, H + NQ)
+    st = lora.stage(a_q, a_v, b_q, b_v)
+    assert st.numel() == lora.staged_elems(H, NQ, NV)
+    a16 = torch.cat([a_q, a_v]).to(torch.float16)
+    b16 = torch.cat([b_q, b_v]).to(torch.float16)
+    want = torch.cat([a16.flatten(), a16.t().flatten(), b16.flatten(),
+                      b_q.to(torch.float16).t().flatten(), b_v.to(torch.float16).t().flatten()])
+    assert torch.equal(st, want)
+
+
 @pytest.mark.parametrize("M,H,NQ,NV,scaling", [(2048, 1536, 1536, 256, 2.0), (37, 512, 512, 256, 0.7),
                                                (1, 256, 256, 128, 2.0)])
 def test_lora_fwd(M, H, NQ, NV, scaling):

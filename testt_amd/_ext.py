@@ -16,7 +16,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsoupk.s
 _lock = threading.Lock()
 _lib = None
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 STATUS_SCRATCH_LIMIT = 20001          # SOUPK_STATUS_SCRATCH_LIMIT
 LORA_SCRATCH_FLOATS = 4 << 20         # SOUPK_LORA_SCRATCH_FLOATS
 DTYPE_F16 = 0
@@ -54,9 +54,10 @@ SIGNATURES = {
     "soupk_attention_varlen_fwd": [_p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "soupk_attention_varlen_bwd": [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p,
                                    _i64, _i32, _i32, _i32, _f32, _p],
-    "soupk_lora_fwd": [_p, _p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
-    "soupk_lora_bwd_rows": [_p, _i64, _p, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _i64, _i32,
-                            _i32, _i32, _i32, _p],
+    "soupk_lora_stage": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
+    "soupk_lora_fwd": [_p, _p, _f32, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
+    "soupk_lora_bwd_rows": [_p, _i64, _p, _i64, _p, _f32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                            _i32, _p],
     "soupk_lora_bwd_params": [_p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i32, _i32,
                               _i32, _i32, _p],
     "soupk_lora_bwd_params_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,

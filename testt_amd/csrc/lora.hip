@@ -9,9 +9,18 @@
 //                         dt   = fp16(gs_q B_q | gs_v B_v)        [M, 2r]
 //                         dy   = fp16(dt A16)                     [M, H]
 // with fp16(.) the rounding of an fp16 GEMM (fp32 sums, one rounding) and A16, B16 the fp16
-// casts of the fp32 LoRA parameters, rounded here as .to(torch.float16) rounds them.  The
-// caller then adds the frozen projection's input gradient into dy in place and forms the
-// parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from gs, t and dt.
+// casts of the fp32 LoRA parameters, rounded as .to(torch.float16) rounds them.  The casts are
+// made once per forward by soupk_lora_stage, into one buffer that holds each in the layouts the
+// kernels read with 8- and 16-byte loads:
+//   A16  [2r, H]   (A_q rows, then A_v rows)   t's contraction over H
+//   A16T [H, 2r]                               dy's contraction over the ranks
+//   B16  [NQ + NV, r]                          lq / lv's contraction over the ranks
+//   B16T [r, NQ], then [r, NV]                 dt's contraction over NQ / NV
+// (with the fp32 parameters read and cast in the kernels themselves, every workgroup of the
+// forward reads 196 KB of A: the forward took 13.3 us at 2048 rows against 10.0 us with the
+// staged fp16 A, identical bits; the row backward takes 11.1 us either way, and the staging
+// launch 2.2 us).  The caller then adds the frozen projection's input gradient into dy in
+// place and forms the parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from gs, t and dt.
 //
 // A workgroup is 4 wavefronts and kRowTiles 16-row MFMA tiles (which share every A / B fragment a
 // wavefront loads), and the workgroups of a row block split the wide output (lq|lv, or dy) by
@@ -61,16 +70,6 @@ __device__ __forceinline__ float r16(float x) {
 
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
-__device__ __forceinline__ h8 to_h8(f4 a, f4 b) {
-  h8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[i] = static_cast<_Float16>(a[i]);
-    r[4 + i] = static_cast<_Float16>(b[i]);
-  }
-  return r;
-}
-
 // Loop steps and tiles are processed kBatch at a time: the loads of a batch (at clamped
 // indices, so unconditional) are all issued before its first MFMA, and the MFMAs and stores
 // past the end of the range are skipped (a wavefront-uniform test).  One step at a time, each
@@ -92,13 +91,53 @@ __device__ __forceinline__ int tile_part(int n_tiles, int part, int parts) {
 // instead of being moved down to their first use.
 __device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
 
+// Offsets (halves) of the sections of the staged parameter buffer (r = kR).
+struct StagedLayout {
+  int64_t a16, a16t, b16, b16t_q, b16t_v, total;
+};
+__host__ __device__ inline StagedLayout staged_layout(int64_t H, int64_t NQ, int64_t NV) {
+  StagedLayout L;
+  L.a16 = 0;
+  L.a16t = 2 * kR * H;
+  L.b16 = 4 * kR * H;
+  L.b16t_q = L.b16 + (NQ + NV) * kR;
+  L.b16t_v = L.b16t_q + kR * NQ;
+  L.total = L.b16t_v + kR * NV;
+  return L;
+}
+
+// One thread per parameter value: the fp16 cast written in both layouts of its section.
+__global__ __launch_bounds__(256) void lora_stage_kernel(
+    const float* __restrict__ aq, const float* __restrict__ av, const float* __restrict__ bq,
+    const float* __restrict__ bv, _Float16* __restrict__ st, int H, int NQ, int NV) {
+  const StagedLayout L = staged_layout(H, NQ, NV);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t na = 2 * kR * static_cast<int64_t>(H);
+  if (e < na) {
+    const int i = static_cast<int>(e / H), k = static_cast<int>(e % H);
+    const _Float16 v = static_cast<_Float16>(i < kR ? aq[e] : av[e - kR * static_cast<int64_t>(H)]);
+    st[L.a16 + e] = v;
+    st[L.a16t + static_cast<int64_t>(k) * (2 * kR) + i] = v;
+  } else if (e < na + static_cast<int64_t>(NQ + NV) * kR) {
+    const int64_t e2 = e - na;
+    const int j = static_cast<int>(e2 / kR), i = static_cast<int>(e2 % kR);
+    const bool q = j < NQ;
+    const _Float16 v = static_cast<_Float16>(q ? bq[e2] : bv[e2 - static_cast<int64_t>(NQ) * kR]);
+    st[L.b16 + e2] = v;
+    if (q) st[L.b16t_q + static_cast<int64_t>(i) * NQ + j] = v;
+    else st[L.b16t_v + static_cast<int64_t>(i) * NV + (j - NQ)] = v;
+  }
+}
+
 // The parameter and activation pointers of the row kernels are not __restrict__: loads through
 // restrict pointers are taken as invariant and moved to their use, which would undo the
 // prefetch of the next batch.
 __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
-    const uint16_t* y, const float* aq, const float* av, const float* bq, const float* bv,
-    float scaling, uint16_t* __restrict__ t_out, uint16_t* __restrict__ lq,
-    uint16_t* __restrict__ lv, int M, int H, int NQ, int NV) {
+    const uint16_t* y, const _Float16* staged, float scaling, uint16_t* __restrict__ t_out,
+    uint16_t* __restrict__ lq, uint16_t* __restrict__ lv, int M, int H, int NQ, int NV) {
+  const StagedLayout L = staged_layout(H, NQ, NV);
+  const _Float16* a16 = staged + L.a16;
+  const _Float16* b16 = staged + L.b16;
   __shared__ float part[4][kRows][2 * kR + 1];
   __shared__ float tt[kRows][2 * kR];
   const int m0 = blockIdx.x * kRows;
@@ -109,17 +148,16 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   const int nq16 = NQ / 16;
   const int t_begin = tile_part(NQ / 16 + NV / 16, blockIdx.y, gridDim.y);
   const int n16 = tile_part(NQ / 16 + NV / 16, blockIdx.y + 1, gridDim.y);
-  auto load_b = [&](f4* bw, int t0) {
+  auto load_b = [&](h4* bw, int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
+      // B16 row of output tile column ql (the v rows follow the q rows)
       const int tile = min(t0 + 4 * u, max(n16 - 1, 0));
-      const bool is_q = tile < nq16;
-      const int f0 = 16 * (is_q ? tile : tile - nq16);
-      bw[u] = *reinterpret_cast<const f4*>((is_q ? bq : bv) +
-                                           static_cast<int64_t>(f0 + ql) * kR + 4 * gr);
+      bw[u] = *reinterpret_cast<const h4*>(b16 + static_cast<int64_t>(16 * tile + ql) * kR +
+                                           4 * gr);
     }
   };
-  f4 bw_next[kBatch];
+  h4 bw_next[kBatch];
   if (t_begin + w < n16) load_b(bw_next, t_begin + w);
   // t = y A^T: A operand = y rows (row 16rt + ql of row tile rt, k = k0 + 8gr..+7); B operand =
   // A_q / A_v rows (column = feature ql), loaded once per step for the kRowTiles row tiles.
@@ -135,11 +173,11 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
     acc_v[rt] = f4{0.f, 0.f, 0.f, 0.f};
   }
   const int steps = kw / 32;
-  const float* aqrow = aq + static_cast<int64_t>(ql) * H + 8 * gr;
-  const float* avrow = av + static_cast<int64_t>(ql) * H + 8 * gr;
+  const _Float16* aqrow = a16 + static_cast<int64_t>(ql) * H + 8 * gr;
+  const _Float16* avrow = a16 + static_cast<int64_t>(kR + ql) * H + 8 * gr;
   struct Batch {
     h8 ya[kBatch][kRowTiles];
-    f4 qa[kBatch][2], va[kBatch][2];
+    h8 qa[kBatch], va[kBatch];
   };
   auto load_t = [&](Batch& r, int s0) {
 #pragma unroll
@@ -148,17 +186,15 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt)
         r.ya[u][rt] = *reinterpret_cast<const h8*>(yrow[rt] + k0 + 8 * gr);
-      r.qa[u][0] = *reinterpret_cast<const f4*>(aqrow + k0);
-      r.qa[u][1] = *reinterpret_cast<const f4*>(aqrow + k0 + 4);
-      r.va[u][0] = *reinterpret_cast<const f4*>(avrow + k0);
-      r.va[u][1] = *reinterpret_cast<const f4*>(avrow + k0 + 4);
+      r.qa[u] = *reinterpret_cast<const h8*>(aqrow + k0);
+      r.va[u] = *reinterpret_cast<const h8*>(avrow + k0);
     }
   };
   auto mma_t = [&](const Batch& r, int s0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (s0 + u < steps) {
-        const h8 bq8 = to_h8(r.qa[u][0], r.qa[u][1]), bv8 = to_h8(r.va[u][0], r.va[u][1]);
+        const h8 bq8 = r.qa[u], bv8 = r.va[u];
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
           acc_q[rt] = mfma32(r.ya[u][rt], bq8, acc_q[rt]);
@@ -216,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
                  static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
     row_ok[rt] = m0 + 16 * rt + ql < M;
   }
-  auto out_tiles = [&](const f4* bw, int t0) {
+  auto out_tiles = [&](const h4* bw, int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int tile = t0 + 4 * u;
@@ -224,8 +260,7 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
       const bool is_q = tile < nq16;
       const int f0 = 16 * (is_q ? tile : tile - nq16);
       const int N = is_q ? NQ : NV;
-      const h4 a = {static_cast<_Float16>(bw[u][0]), static_cast<_Float16>(bw[u][1]),
-                    static_cast<_Float16>(bw[u][2]), static_cast<_Float16>(bw[u][3])};
+      const h4 a = bw[u];
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt) {
         const f4 c = mfma16(a, is_q ? tq4[rt] : tv4[rt], f4{0.f, 0.f, 0.f, 0.f});
@@ -240,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
       }
     }
   };
-  f4 bw_cur[kBatch];
+  h4 bw_cur[kBatch];
   for (int t0 = t_begin + w; t0 < n16; t0 += 8 * kBatch) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) bw_cur[u] = bw_next[u];
@@ -258,10 +293,10 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
 }
 
 __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
-    const uint16_t* gq, int64_t ldq, const uint16_t* gv, int64_t ldv, const float* aq,
-    const float* av, const float* bq, const float* bv, float scaling, uint16_t* __restrict__ gsq,
-    uint16_t* __restrict__ gsv, uint16_t* __restrict__ dt_out, uint16_t* __restrict__ dy, int M,
-    int H, int NQ, int NV) {
+    const uint16_t* gq, int64_t ldq, const uint16_t* gv, int64_t ldv, const _Float16* staged,
+    float scaling, uint16_t* __restrict__ gsq, uint16_t* __restrict__ gsv,
+    uint16_t* __restrict__ dt_out, uint16_t* __restrict__ dy, int M, int H, int NQ, int NV) {
+  const StagedLayout L = staged_layout(H, NQ, NV);
   __shared__ float part[4][kRows][2 * kR + 1];
   __shared__ float dts[kRows][2 * kR];
   const int m0 = blockIdx.x * kRows;
@@ -276,9 +311,9 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   }
   const bool store_gs = blockIdx.y == 0;
   // dt_x = gs_x B16_x: A operand = gs rows (row 16rt + ql, k = j0 + 8gr..+7), stored as gs on
-  // the way (by column part 0); B operand = B16 (column = rank index ql, k = j rows: B is
-  // [N, r] row-major, so the 8 k-values of a lane are 8 rows, each read by 16 consecutive
-  // lanes as 64 contiguous bytes), loaded once per step for the kRowTiles row tiles.
+  // the way (by column part 0); B operand = B16_x (column = rank index ql, k = j: 8
+  // consecutive entries of row ql of B16T_x, one 16-byte load), loaded once per step for the
+  // kRowTiles row tiles.
   f4 acc_q[kRowTiles], acc_v[kRowTiles];
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
@@ -289,12 +324,12 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   // the next batch's loads issued before the current batch's MFMAs
   struct Batch {
     h8 graw[kBatch][kRowTiles];
-    float braw[kBatch][8];
+    h8 b[kBatch];
   };
-  auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const float* b,
+  auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const _Float16* bt,
                  f4* acc) {
     const int kn = N / 4, steps = kn / 32;
-    const float* bcol = b + static_cast<int64_t>(w * kn + 8 * gr) * kR + ql;
+    const _Float16* brow = bt + static_cast<int64_t>(ql) * N + w * kn + 8 * gr;
     auto load = [&](Batch& r, int s0) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
@@ -302,17 +337,14 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt)
           r.graw[u][rt] = *reinterpret_cast<const h8*>(g + row[rt] * ldg + w * kn + 8 * gr + j);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r.braw[u][i] = bcol[static_cast<int64_t>(j + i) * kR];
+        r.b[u] = *reinterpret_cast<const h8*>(brow + j);
       }
     };
     auto mma = [&](const Batch& r, int s0) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         if (s0 + u >= steps) break;
-        h8 ba;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ba[i] = static_cast<_Float16>(r.braw[u][i]);
+        const h8 ba = r.b[u];
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) {
           h8 ga;
@@ -340,8 +372,8 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
       }
     }
   };
-  run(gq, ldq, gsq, NQ, bq, acc_q);
-  run(gv, ldv, gsv, NV, bv, acc_v);
+  run(gq, ldq, gsq, NQ, staged + L.b16t_q, acc_q);
+  run(gv, ldv, gsv, NV, staged + L.b16t_v, acc_v);
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
 #pragma unroll
@@ -362,34 +394,30 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
   __syncthreads();
   // dy = dt A16 (contraction over the 2r rank indices; A = A_q rows then A_v rows), one
   // 16-column tile of H at a time, transposed: A operand = A16 columns (row h0 + ql, k = rank
-  // 8gr..+7: 8 rows of A, each read by 16 consecutive lanes as 64 contiguous bytes), B = dt
-  // rows (column = row ql of a row tile)
+  // 8gr..+7: 8 consecutive entries of row h0 + ql of A16T, one 16-byte load), B = dt rows
+  // (column = row ql of a row tile)
   h8 dtb[kRowTiles];
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) dtb[rt][i] = static_cast<_Float16>(dts[16 * rt + ql][8 * gr + i]);
   }
-  const float* abase = (gr < 2 ? aq + static_cast<int64_t>(8 * gr) * H
-                               : av + static_cast<int64_t>(8 * (gr - 2)) * H) + ql;
+  const _Float16* abase = staged + L.a16t + static_cast<int64_t>(ql) * (2 * kR) + 8 * gr;
   const int t_begin = tile_part(H / 16, blockIdx.y, gridDim.y);
   const int n16 = tile_part(H / 16, blockIdx.y + 1, gridDim.y);
-  auto load_a = [&](float (*araw)[8], int t0) {
+  auto load_a = [&](h8* araw, int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int h0 = 16 * min(t0 + 4 * u, n16 - 1);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) araw[u][i] = abase[static_cast<int64_t>(i) * H + h0];
+      araw[u] = *reinterpret_cast<const h8*>(abase + static_cast<int64_t>(h0) * (2 * kR));
     }
   };
-  auto out_tiles = [&](const float (*araw)[8], int t0) {
+  auto out_tiles = [&](const h8* araw, int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int tile = t0 + 4 * u;
       if (tile >= n16) break;
-      h8 a;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = static_cast<_Float16>(araw[u][i]);
+      const h8 a = araw[u];
 #pragma unroll
       for (int rt = 0; rt < kRowTiles; ++rt) {
         const f4 c = mfma32(a, dtb[rt], f4{0.f, 0.f, 0.f, 0.f});
@@ -401,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     }
   };
   if (t_begin + w < n16) {
-    float a0[kBatch][8], a1[kBatch][8];
+    h8 a0[kBatch], a1[kBatch];
     load_a(a0, t_begin + w);
     for (int t0 = t_begin + w; t0 < n16; t0 += 8 * kBatch) {
       if (t0 + 4 * kBatch < n16) load_a(a1, t0 + 4 * kBatch);
@@ -577,47 +605,55 @@ unsigned column_parts(int64_t M, int n_tiles) {
 
 using namespace soupk;
 
+extern "C" __attribute__((visibility("default"))) int soupk_lora_stage(
+    const float* a_q, const float* a_v, const float* b_q, const float* b_v, uint16_t* staged,
+    int64_t staged_elems, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
+  const int rc = check_dims(0, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  if (!a_q || !a_v || !b_q || !b_v || !staged) return kInvalid;
+  if (misaligned(staged)) return kInvalid;
+  if (staged_elems < staged_layout(H, NQ, NV).total) return kInvalid;
+  const int64_t n = 2 * kR * static_cast<int64_t>(H) + static_cast<int64_t>(NQ + NV) * kR;
+  return launch_kernel(lora_stage_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
+                       dim3(256), static_cast<hipStream_t>(stream), a_q, a_v, b_q, b_v,
+                       reinterpret_cast<_Float16*>(staged), H, NQ, NV);
+}
+
 extern "C" __attribute__((visibility("default"))) int soupk_lora_fwd(
-    const uint16_t* y, const float* a_q, const float* a_v, const float* b_q, const float* b_v,
-    float scaling, uint16_t* t, uint16_t* lq, uint16_t* lv, int64_t M, int32_t H, int32_t NQ,
-    int32_t NV, int32_t r, void* stream) {
+    const uint16_t* y, const uint16_t* staged, float scaling, uint16_t* t, uint16_t* lq,
+    uint16_t* lv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
   const int rc = check_dims(M, H, NQ, NV, r);
   if (rc != kOk) return rc;
   if (M == 0) return kOk;
-  if (!y || !a_q || !a_v || !b_q || !b_v || !t || !lq || !lv) return kInvalid;
-  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(a_q),
-                        static_cast<const void*>(a_v), static_cast<const void*>(b_q),
-                        static_cast<const void*>(b_v), static_cast<const void*>(lq),
-                        static_cast<const void*>(lv)})
+  if (!y || !staged || !t || !lq || !lv) return kInvalid;
+  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(staged),
+                        static_cast<const void*>(lq), static_cast<const void*>(lv)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
   return launch_kernel(lora_fwd_kernel, dim3(grid, column_parts(M, NQ / 16 + NV / 16)),
-                       dim3(kThreads),
-                       static_cast<hipStream_t>(stream), y, a_q, a_v, b_q, b_v, scaling, t, lq,
-                       lv, static_cast<int>(M), H, NQ, NV);
+                       dim3(kThreads), static_cast<hipStream_t>(stream), y,
+                       reinterpret_cast<const _Float16*>(staged), scaling, t, lq, lv,
+                       static_cast<int>(M), H, NQ, NV);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_rows(
-    const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v, const float* a_q,
-    const float* a_v, const float* b_q, const float* b_v, float scaling, uint16_t* gs_q,
-    uint16_t* gs_v, uint16_t* dt, uint16_t* dy, int64_t M, int32_t H, int32_t NQ, int32_t NV,
-    int32_t r, void* stream) {
+    const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
+    const uint16_t* staged, float scaling, uint16_t* gs_q, uint16_t* gs_v, uint16_t* dt,
+    uint16_t* dy, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
   const int rc = check_dims(M, H, NQ, NV, r);
   if (rc != kOk) return rc;
   if (ld_q < NQ || ld_v < NV || ld_q % 8 || ld_v % 8) return kInvalid;
   if (M == 0) return kOk;
-  if (!g_q || !g_v || !a_q || !a_v || !b_q || !b_v || !gs_q || !gs_v || !dt || !dy)
-    return kInvalid;
+  if (!g_q || !g_v || !staged || !gs_q || !gs_v || !dt || !dy) return kInvalid;
   for (const void* p : {static_cast<const void*>(g_q), static_cast<const void*>(g_v),
-                        static_cast<const void*>(a_q), static_cast<const void*>(a_v),
-                        static_cast<const void*>(gs_q), static_cast<const void*>(gs_v),
-                        static_cast<const void*>(dy)})
+                        static_cast<const void*>(staged), static_cast<const void*>(gs_q),
+                        static_cast<const void*>(gs_v), static_cast<const void*>(dy)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
   return launch_kernel(lora_bwd_rows_kernel, dim3(grid, column_parts(M, H / 16)),
-                       dim3(kThreads),
-                       static_cast<hipStream_t>(stream), g_q, ld_q, g_v, ld_v, a_q, a_v, b_q, b_v,
-                       scaling, gs_q, gs_v, dt, dy, static_cast<int>(M), H, NQ, NV);
+                       dim3(kThreads), static_cast<hipStream_t>(stream), g_q, ld_q, g_v, ld_v,
+                       reinterpret_cast<const _Float16*>(staged), scaling, gs_q, gs_v, dt, dy,
+                       static_cast<int>(M), H, NQ, NV);
 }
 
 // Workspace of soupk_lora_bwd_params, in floats: ceil(M / 128) slices of partial sums.

@@ -122,9 +122,10 @@ class QKVLora(torch.autograd.Function):
         ctx.weights, ctx.scaling = weights, scaling
         params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
         ctx.fused = USE_FUSED_LORA and _lora.supported(y16, *params)
-        if ctx.fused:       # testt_amd/csrc/lora.hip: one launch for t, lq and lv
-            t, lq, lv = _lora.lora_fwd(y16, *params, scaling)
-            ctx.save_for_backward(y16, t, *params)
+        if ctx.fused:       # testt_amd/csrc/lora.hip: the parameters' fp16 casts, then t, lq, lv
+            staged = _lora.stage(*params)
+            t, lq, lv = _lora.lora_fwd(y16, *params, scaling, staged=staged)
+            ctx.save_for_backward(y16, t, *params, staged)
             return qkv, lq, lv
         r = a_q.shape[0]
         a16 = torch.cat([a_q.detach(), a_v.detach()]).to(torch.float16)
@@ -168,11 +169,12 @@ class QKVLora(torch.autograd.Function):
 
     @staticmethod
     def _backward_fused(ctx, g_qkv, g_lq, g_lv):
-        y16, t, a_q, a_v, b_q, b_v = ctx.saved_tensors
+        y16, t, a_q, a_v, b_q, b_v, staged = ctx.saved_tensors
         if g_lq is None and g_lv is None:
             g_lq = torch.zeros((y16.shape[0], b_q.shape[0]), dtype=torch.float16,
                                device=y16.device)
-        gs_q, gs_v, dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling)
+        gs_q, gs_v, dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling,
+                                                 staged=staged)
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
         d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, gs_q, gs_v)
         if g_qkv is not None:

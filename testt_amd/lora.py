@@ -3,14 +3,18 @@ peft's lora_B(lora_A(x)) * scaling under fp16 autocast (solution/model.py:195-20
 in one launch forward and one backward, in place of the separate fp16 GEMMs, casts and
 scalings.  `layer.QKVLora` uses it when `supported` holds and keeps its GEMM path otherwise.
 
-    lora_fwd(y16, a_q, a_v, b_q, b_v, scaling)      -> t [M, 32], lq [M, NQ], lv [M, NV] fp16
-    lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s)   -> gs_q, gs_v, dt [M, 32], dy [M, H] fp16
-    lora_bwd_params(y16, t, dt, gs_q, gs_v)          -> dA_q, dA_v [16, H], dB_q, dB_v fp32
+    stage(a_q, a_v, b_q, b_v)                         -> the fp16 casts of the parameters
+    lora_fwd(y16, a_q, a_v, b_q, b_v, scaling, st)    -> t [M, 32], lq [M, NQ], lv [M, NV] fp16
+    lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s, st) -> gs_q, gs_v, dt [M, 32], dy [M, H] fp16
+    lora_bwd_params(y16, t, dt, gs_q, gs_v)           -> dA_q, dA_v [16, H], dB_q, dB_v fp32
 
 with t = fp16(y A^T), lq = fp16(fp16(t_q B_q^T) * s), gs = fp16(g * s),
 dt = fp16(gs_q B_q | gs_v B_v), dy = fp16(dt A), dA = fp32(fp16(dt^T y)),
 dB_x = fp32(fp16(gs_x^T t_x)): the rounding steps of the fp16 GEMMs they replace (fp32 sums in
-another order)."""
+another order).  A and B enter the products as their fp16 casts (autocast's), which `stage`
+makes in one launch, in the layouts the kernels read; the forward's staged buffer serves its
+backward too (the parameters do not change in between).  Without `st` the functions stage
+the parameters themselves."""
 
 import torch
 
@@ -50,17 +54,43 @@ def _check_params(a_q, a_v, b_q, b_v, H, dev):
     return b_q.shape[0], b_v.shape[0]
 
 
-def lora_fwd(y16, a_q, a_v, b_q, b_v, scaling):
+def staged_elems(H, NQ, NV):
+    """Halves of the staged parameter buffer: [A_q; A_v] and its transpose, [B_q; B_v], and
+    B_q^T, B_v^T."""
+    return 4 * RANK * H + 2 * RANK * (NQ + NV)
+
+
+def stage(a_q, a_v, b_q, b_v):
+    """fp16 [staged_elems] device tensor: the parameters' fp16 casts in the kernels' layouts."""
+    H = a_q.shape[-1] if a_q.dim() == 2 else 0
+    dev = a_q.device
+    NQ, NV = _check_params(a_q, a_v, b_q, b_v, H, dev)
+    st = torch.empty(staged_elems(H, NQ, NV), dtype=torch.float16, device=dev)
+    _ext.call("soupk_lora_stage", _ext.ptr(a_q), _ext.ptr(a_v), _ext.ptr(b_q), _ext.ptr(b_v),
+              _ext.ptr(st), st.numel(), H, NQ, NV, RANK, _ext.stream_of(st))
+    return st
+
+
+def _staged(st, a_q, a_v, b_q, b_v, H, NQ, NV, dev):
+    if st is None:
+        return stage(a_q, a_v, b_q, b_v)
+    _ext.require(st, "staged", dtype=torch.float16, ndim=1, device=dev)
+    if st.numel() < staged_elems(H, NQ, NV):
+        raise ValueError(f"staged holds {st.numel()} values, {staged_elems(H, NQ, NV)} needed")
+    return st
+
+
+def lora_fwd(y16, a_q, a_v, b_q, b_v, scaling, staged=None):
     _ext.require(y16, "y16", dtype=torch.float16, ndim=2)
     M, H = y16.shape
     dev = y16.device
     NQ, NV = _check_params(a_q, a_v, b_q, b_v, H, dev)
+    st = _staged(staged, a_q, a_v, b_q, b_v, H, NQ, NV, dev)
     t = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
     lq = torch.empty((M, NQ), dtype=torch.float16, device=dev)
     lv = torch.empty((M, NV), dtype=torch.float16, device=dev)
-    _ext.call("soupk_lora_fwd", _ext.ptr(y16), _ext.ptr(a_q), _ext.ptr(a_v), _ext.ptr(b_q),
-              _ext.ptr(b_v), float(scaling), _ext.ptr(t), _ext.ptr(lq), _ext.ptr(lv), M, H, NQ,
-              NV, RANK, _ext.stream_of(y16))
+    _ext.call("soupk_lora_fwd", _ext.ptr(y16), _ext.ptr(st), float(scaling), _ext.ptr(t),
+              _ext.ptr(lq), _ext.ptr(lv), M, H, NQ, NV, RANK, _ext.stream_of(y16))
     return t, lq, lv
 
 
@@ -77,13 +107,14 @@ def _rows(g, n, m, dev):
     return g
 
 
-def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling):
+def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling, staged=None):
     ref = g_q if g_q is not None else g_v
     if ref is None:
         raise ValueError("lora_bwd_rows needs at least one of g_q, g_v")
     M, dev = ref.shape[0], ref.device
     NQ, NV = _check_params(a_q, a_v, b_q, b_v, a_q.shape[-1], dev)
     H = a_q.shape[1]
+    st = _staged(staged, a_q, a_v, b_q, b_v, H, NQ, NV, dev)
     g_q, g_v = _rows(g_q, NQ, M, dev), _rows(g_v, NV, M, dev)
     if tuple(g_q.shape) != (M, NQ) or tuple(g_v.shape) != (M, NV):
         raise ValueError(f"lora_bwd_rows: gradient shapes {tuple(g_q.shape)}, "
@@ -93,9 +124,8 @@ def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling):
     dt = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
     dy = torch.empty((M, H), dtype=torch.float16, device=dev)
     _ext.call("soupk_lora_bwd_rows", _ext.ptr(g_q), g_q.stride(0), _ext.ptr(g_v), g_v.stride(0),
-              _ext.ptr(a_q), _ext.ptr(a_v), _ext.ptr(b_q), _ext.ptr(b_v), float(scaling),
-              _ext.ptr(gs_q), _ext.ptr(gs_v), _ext.ptr(dt), _ext.ptr(dy), M, H, NQ, NV, RANK,
-              _ext.stream_of(dy))
+              _ext.ptr(st), float(scaling), _ext.ptr(gs_q), _ext.ptr(gs_v), _ext.ptr(dt),
+              _ext.ptr(dy), M, H, NQ, NV, RANK, _ext.stream_of(dy))
     return gs_q, gs_v, dt, dy
 
 
