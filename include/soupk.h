@@ -329,28 +329,29 @@ int soupk_lora_fwd(const uint16_t* y, const uint16_t* staged, float scaling, uin
 /*
  * Its backward, the row-local part: with g_q [M, NQ] (row stride ld_q) and g_v [M, NV] (ld_v)
  * the fp16 gradients of lq and lv, and the forward's `staged` parameters, writes
- * gs_q = fp16(g_q * scaling) [M, NQ], gs_v [M, NV], dt = fp16([gs_q b_q16 | gs_v b_v16])
- * [M, 32] and dy = fp16(dt [a_q16; a_v16]) [M, H] (the LoRA part of the gradient of y; the
- * caller adds the frozen projection's part in place).  The parameter gradients are
- * gs_q^T t[:, :16], gs_v^T t[:, 16:] and dt^T y.  Same shape rules; ld_q, ld_v multiples of 8.
+ * dt = fp16([gs_q b_q16 | gs_v b_v16]) [M, 32], gs_x = fp16(g_x * scaling) (formed in
+ * registers, not stored), and dy = fp16(dt [a_q16; a_v16]) [M, H] (the LoRA part of the
+ * gradient of y; the caller adds the frozen projection's part in place).  Same shape rules;
+ * ld_q, ld_v multiples of 8.
  */
 int soupk_lora_bwd_rows(const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
-                        const uint16_t* staged, float scaling, uint16_t* gs_q, uint16_t* gs_v,
-                        uint16_t* dt, uint16_t* dy, int64_t M, int32_t H, int32_t NQ,
-                        int32_t NV, int32_t r, void* stream);
+                        const uint16_t* staged, float scaling, uint16_t* dt, uint16_t* dy,
+                        int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream);
 
 /*
  * Its backward, the parameter gradients (reductions over the M rows), each the fp16 GEMM result
  * cast to fp32: d_aq = fp16(dt[:, :16]^T y), d_av = fp16(dt[:, 16:]^T y) [16, H];
- * d_bq = fp16(gs_q^T t[:, :16]) [NQ, 16], d_bv = fp16(gs_v^T t[:, 16:]) [NV, 16].  workspace:
- * fp32 device memory of ceil(M/128) * (32*H + 16*(NQ + NV)) floats (per-slice partial sums,
- * added in slice order: deterministic).  Same shape rules (H, NQ, NV multiples of 128).
+ * d_bq = fp16(gs_q^T t[:, :16]) [NQ, 16], d_bv = fp16(gs_v^T t[:, 16:]) [NV, 16], with
+ * gs_x = fp16(g_x * scaling) formed from g_q (row stride ld_q) and g_v (ld_v) as they are read.
+ * workspace: fp32 device memory of ceil(M/128) * (32*H + 16*(NQ + NV)) floats (per-slice
+ * partial sums, added in slice order: deterministic).  Same shape rules (H, NQ, NV multiples
+ * of 128; ld_q, ld_v multiples of 8).
  */
 int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
-                          const uint16_t* gs_q, const uint16_t* gs_v, float* workspace,
-                          int64_t workspace_floats, float* d_aq, float* d_av, float* d_bq,
-                          float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
-                          void* stream);
+                          const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
+                          float scaling, float* workspace, int64_t workspace_floats, float* d_aq,
+                          float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H,
+                          int32_t NQ, int32_t NV, int32_t r, void* stream);
 
 /*
  * soupk_lora_bwd_params without the workspace argument, for callers that cannot allocate
@@ -367,9 +368,10 @@ int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* 
  */
 #define SOUPK_LORA_SCRATCH_FLOATS (4 << 20)
 int soupk_lora_bwd_params_noalloc(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
-                                  const uint16_t* gs_q, const uint16_t* gs_v, float* d_aq,
-                                  float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H,
-                                  int32_t NQ, int32_t NV, int32_t r, void* stream);
+                                  const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v,
+                                  int64_t ld_v, float scaling, float* d_aq, float* d_av,
+                                  float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ,
+                                  int32_t NV, int32_t r, void* stream);
 
 /*
  * y = x W^T (+ bias), fp16, on MFMA with 128 x 128 tiles (the GEMM core of soupk_gemm_tn_nf4;

@@ -108,4 +108,5 @@ def test_noalloc_rejects_problems_beyond_its_scratch(lib):
     need = -(-6785 // 128) * (32 * H + 16 * (NQ + NV))
     assert need > _ext.LORA_SCRATCH_FLOATS >= -(-6784 // 128) * (32 * H + 16 * (NQ + NV))
     with pytest.raises(_ext.SoupkError, match=f"status {_ext.STATUS_SCRATCH_LIMIT}: .*scratch"):
-        _ext.call("soupk_lora_bwd_params_noalloc", *(16,) * 9, 6785, H, NQ, NV, 16, None)
+        _ext.call("soupk_lora_bwd_params_noalloc", 16, 16, 16, 16, NQ, 16, NV, 2.0,
+                  *(16,) * 4, 6785, H, NQ, NV, 16, None)

@@ -85,9 +85,9 @@ def test_lora_bwd_rows(M, H, NQ, NV, scaling, strided):
     else:
         g_q = (1e-2 * torch.randn(M, NQ, generator=g)).to(torch.float16).to(DEV)
         g_v = (1e-2 * torch.randn(M, NV, generator=g)).to(torch.float16).to(DEV)
-    gs_q, gs_v, dt, dy = lora.lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling)
-    assert torch.equal(gs_q, (g_q.float() * scaling).to(torch.float16))
-    assert torch.equal(gs_v, (g_v.float() * scaling).to(torch.float16))
+    dt, dy = lora.lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling)
+    gs_q = (g_q.float() * scaling).to(torch.float16)   # formed in the kernel, not stored
+    gs_v = (g_v.float() * scaling).to(torch.float16)
     bq16, bv16 = f64_16(b_q), f64_16(b_v)
     exact_dt = torch.cat([gs_q.double() @ bq16, gs_v.double() @ bv16], dim=1)
     terms_dt = torch.cat([gs_q.double().abs() @ bq16.abs(), gs_v.double().abs() @ bv16.abs()],
@@ -128,20 +128,30 @@ def test_qkvlora_fused_matches_gemm_path(monkeypatch):
         assert rel(a, b) < 2e-3, (name, rel(a, b))
 
 
-@pytest.mark.parametrize("M,H,NQ,NV", [(2048, 1536, 1536, 256), (300, 512, 512, 256),
-                                       (37, 256, 256, 128), (1, 256, 256, 128)])
-def test_lora_bwd_params(M, H, NQ, NV):
+@pytest.mark.parametrize("M,H,NQ,NV,scaling,strided", [(2048, 1536, 1536, 256, 2.0, True),
+                                                       (300, 512, 512, 256, 0.7, False),
+                                                       (37, 256, 256, 128, 2.0, True),
+                                                       (1, 256, 256, 128, 1.0, False)])
+def test_lora_bwd_params(M, H, NQ, NV, scaling, strided):
     """The parameter gradients (reductions over the rows, per-128-row slices added in order):
-    fp16 roundings of the exact sums, as fp32."""
-    print(f"lora bwd params M={M} H={H} NQ={NQ} NV={NV}", flush=True)
+    fp16 roundings of the exact sums, as fp32, with gs = fp16(g * scaling) formed from g (rows
+    of a wider buffer, as the attention backward hands them over, or contiguous)."""
+    print(f"lora bwd params M={M} H={H} NQ={NQ} NV={NV} s={scaling} strided={strided}",
+          flush=True)
     g = torch.Generator().manual_seed(M + H)
 
     def f16(*shape, sd):
         return (sd * torch.randn(*shape, generator=g)).to(torch.float16).to(DEV)
 
     y, t, dt = f16(M, H, sd=1.0), f16(M, 32, sd=0.5), f16(M, 32, sd=0.01)
-    gs_q, gs_v = f16(M, NQ, sd=0.01), f16(M, NV, sd=0.01)
-    d_aq, d_av, d_bq, d_bv = lora.lora_bwd_params(y, t, dt, gs_q, gs_v)
+    if strided:
+        wide = f16(M, NQ + 2 * NV, sd=0.01)
+        g_q, g_v = wide[:, :NQ], wide[:, NQ + NV:]
+    else:
+        g_q, g_v = f16(M, NQ, sd=0.01), f16(M, NV, sd=0.01)
+    d_aq, d_av, d_bq, d_bv = lora.lora_bwd_params(y, t, dt, g_q, g_v, scaling)
+    gs_q = (g_q.float() * scaling).to(torch.float16)
+    gs_v = (g_v.float() * scaling).to(torch.float16)
     assert d_aq.dtype == torch.float32 and d_bq.shape == (NQ, 16) and d_bv.shape == (NV, 16)
     yd, td, dtd = y.double(), t.double(), dt.double()
     within_ulps(torch.cat([d_aq, d_av]), dtd.t() @ yd, 1, dtd.abs().t() @ yd.abs())
@@ -153,6 +163,6 @@ def test_lora_bwd_params_no_rows():
     e = torch.empty(0, 256, dtype=torch.float16, device=DEV)
     e32 = torch.empty(0, 32, dtype=torch.float16, device=DEV)
     out = lora.lora_bwd_params(e, e32, e32, e, torch.empty(0, 128, dtype=torch.float16,
-                                                          device=DEV))
+                                                          device=DEV), 2.0)
     for x in out:
         assert torch.equal(x, torch.zeros_like(x))

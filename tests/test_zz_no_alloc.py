@@ -24,11 +24,12 @@ def _inputs(M, seed):
     return mk(H, 1.0), mk(2 * R, 0.5), mk(2 * R, 0.1), mk(NQ, 0.1), mk(NV, 0.1)
 
 
-def _noalloc(y, t, dt, gs_q, gs_v):
+def _noalloc(y, t, dt, g_q, g_v, scaling):
     M = y.shape[0]
     outs = [torch.full(shape, float("nan"), dtype=torch.float32, device=DEV)
             for shape in ((R, H), (R, H), (NQ, R), (NV, R))]
-    _ext.call("soupk_lora_bwd_params_noalloc", *[_ext.ptr(x) for x in (y, t, dt, gs_q, gs_v)],
+    _ext.call("soupk_lora_bwd_params_noalloc", *[_ext.ptr(x) for x in (y, t, dt)],
+              _ext.ptr(g_q), g_q.stride(0), _ext.ptr(g_v), g_v.stride(0), float(scaling),
               *[_ext.ptr(o) for o in outs], M, H, NQ, NV, R, _ext.stream_of(y))
     return outs
 
@@ -37,7 +38,7 @@ def _noalloc(y, t, dt, gs_q, gs_v):
 def test_noalloc_matches_workspace_entry(sizes):
     for i, M in enumerate(sizes):
         print(f"lora params no-alloc call {i}: M={M}", flush=True)
-        ins = _inputs(M, seed=100 + M)
+        ins = (*_inputs(M, seed=100 + M), 2.0)
         got = _noalloc(*ins)
         want = lora.lora_bwd_params(*ins)
         for name, a, b in zip(("d_aq", "d_av", "d_bq", "d_bv"), got, want):

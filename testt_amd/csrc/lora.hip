@@ -5,7 +5,8 @@
 //   soupk_lora_fwd:       t  = fp16(y A^T)                        [M, 2r]  (A = A_q | A_v)
 //                         lq = fp16(fp16(t_q B_q^T) * scaling)    [M, NQ]
 //                         lv = fp16(fp16(t_v B_v^T) * scaling)    [M, NV]
-//   soupk_lora_bwd_rows:  gs_x = fp16(g_x * scaling)              (g_x: the gradients of lq, lv)
+//   soupk_lora_bwd_rows:  gs_x = fp16(g_x * scaling)              (g_x: the gradients of lq, lv;
+//                                                                 in registers, not stored)
 //                         dt   = fp16(gs_q B_q | gs_v B_v)        [M, 2r]
 //                         dy   = fp16(dt A16)                     [M, H]
 // with fp16(.) the rounding of an fp16 GEMM (fp32 sums, one rounding) and A16, B16 the fp16
@@ -20,7 +21,9 @@
 // forward reads 196 KB of A: the forward took 13.3 us at 2048 rows against 10.0 us with the
 // staged fp16 A, identical bits; the row backward takes 11.1 us either way, and the staging
 // launch 2.2 us).  The caller then adds the frozen projection's input gradient into dy in
-// place and forms the parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from gs, t and dt.
+// place and forms the parameter gradients (B_x: gs_x^T t_x, A: dt^T y) from g, t and dt: the
+// parameter kernel forms gs from g again as it stages g's rows, so gs never goes to memory (its
+// stores took 2.1 of the row kernel's 11.2 us at 2048 rows).
 //
 // A workgroup is 4 wavefronts and kRowTiles 16-row MFMA tiles (which share every A / B fragment a
 // wavefront loads), and the workgroups of a row block split the wide output (lq|lv, or dy) by
@@ -294,8 +297,8 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
 
 __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     const uint16_t* gq, int64_t ldq, const uint16_t* gv, int64_t ldv, const _Float16* staged,
-    float scaling, uint16_t* __restrict__ gsq, uint16_t* __restrict__ gsv,
-    uint16_t* __restrict__ dt_out, uint16_t* __restrict__ dy, int M, int H, int NQ, int NV) {
+    float scaling, uint16_t* __restrict__ dt_out, uint16_t* __restrict__ dy, int M, int H,
+    int NQ, int NV) {
   const StagedLayout L = staged_layout(H, NQ, NV);
   __shared__ float part[4][kRows][2 * kR + 1];
   __shared__ float dts[kRows][2 * kR];
@@ -309,9 +312,8 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     row[rt] = min(m0 + 16 * rt + ql, M - 1);
     row_ok[rt] = m0 + 16 * rt + ql < M;
   }
-  const bool store_gs = blockIdx.y == 0;
-  // dt_x = gs_x B16_x: A operand = gs rows (row 16rt + ql, k = j0 + 8gr..+7), stored as gs on
-  // the way (by column part 0); B operand = B16_x (column = rank index ql, k = j: 8
+  // dt_x = gs_x B16_x: A operand = gs rows (row 16rt + ql, k = j0 + 8gr..+7); B operand =
+  // B16_x (column = rank index ql, k = j: 8
   // consecutive entries of row ql of B16T_x, one 16-byte load), loaded once per step for the
   // kRowTiles row tiles.
   f4 acc_q[kRowTiles], acc_v[kRowTiles];
@@ -326,8 +328,7 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
     h8 graw[kBatch][kRowTiles];
     h8 b[kBatch];
   };
-  auto run = [&](const uint16_t* g, int64_t ldg, uint16_t* gs, int N, const _Float16* bt,
-                 f4* acc) {
+  auto run = [&](const uint16_t* g, int64_t ldg, int N, const _Float16* bt, f4* acc) {
     const int kn = N / 4, steps = kn / 32;
     const _Float16* brow = bt + static_cast<int64_t>(ql) * N + w * kn + 8 * gr;
     auto load = [&](Batch& r, int s0) {
@@ -351,9 +352,6 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
 #pragma unroll
           for (int i = 0; i < 8; ++i)
             ga[i] = static_cast<_Float16>(static_cast<float>(r.graw[u][rt][i]) * scaling);
-          if (store_gs && row_ok[rt])
-            *reinterpret_cast<h8*>(gs + (m0 + 16 * rt + ql) * static_cast<int64_t>(N) +
-                                   w * kn + 32 * (s0 + u) + 8 * gr) = ga;
           acc[rt] = mfma32(ga, ba, acc[rt]);
         }
       }
@@ -372,8 +370,8 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
       }
     }
   };
-  run(gq, ldq, gsq, NQ, staged + L.b16t_q, acc_q);
-  run(gv, ldv, gsv, NV, staged + L.b16t_v, acc_v);
+  run(gq, ldq, NQ, staged + L.b16t_q, acc_q);
+  run(gv, ldv, NV, staged + L.b16t_v, acc_v);
 #pragma unroll
   for (int rt = 0; rt < kRowTiles; ++rt) {
 #pragma unroll
@@ -446,11 +444,12 @@ __global__ __launch_bounds__(kThreads) void lora_bwd_rows_kernel(
 
 // ---- parameter gradients: reductions over the rows ---------------------------------------
 //   dA[i][k]  = fp16(sum_m dt[m][i] y[m][k])          i < 2r, k < H  (A_q rows, then A_v rows)
-//   dBq[j][i] = fp16(sum_m gs_q[m][j] t[m][i])        j < NQ, i < r
+//   dBq[j][i] = fp16(sum_m gs_q[m][j] t[m][i])        j < NQ, i < r,  gs_x = fp16(g_x * s)
 //   dBv[j][i] = fp16(sum_m gs_v[m][j] t[m][r + i])    j < NV, i < r
 // each cast to fp32 (the fp16 GEMM result cast to the fp32 parameter, as autocast's backward
 // gives it).  lora_params_partial_kernel: workgroup (column block of 64, slice of kSlice rows)
-// stages 64-row chunks of X (y, gs_q or gs_v: its 64 columns) and Z (dt or t) through LDS,
+// stages 64-row chunks of X (y, or g_q / g_v scaled and rounded to gs as they are staged: its
+// 64 columns) and Z (dt or t) through LDS,
 // transposed so that each MFMA operand is 8 consecutive rows of one column, and writes fp32
 // partial sums per slice; lora_params_reduce_kernel adds the slices in order and rounds.
 // With the next chunk's loads issued before the current chunk's MFMAs and the reduce's loads
@@ -471,6 +470,12 @@ __device__ __forceinline__ void load_pair(const uint16_t* src, int64_t ld, int r
   if (t1 >= rows) b = u32x4{0u, 0u, 0u, 0u};
 }
 
+// Eight fp16 values times s, each rounded to fp16.
+__device__ __forceinline__ u32x4 scale_h8(u32x4 v, float s) {
+  return u32x4{pack_h2(lo_h(v.x) * s, hi_h(v.x) * s), pack_h2(lo_h(v.y) * s, hi_h(v.y) * s),
+               pack_h2(lo_h(v.z) * s, hi_h(v.z) * s), pack_h2(lo_h(v.w) * s, hi_h(v.w) * s)};
+}
+
 // ... and written transposed into tr[col][row] (stride kPStride) as 4-byte pairs.
 __device__ __forceinline__ void store_pair_t(_Float16* tr, u32x4 a, u32x4 b, int rp, int c8) {
   const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
@@ -484,9 +489,9 @@ __device__ __forceinline__ void store_pair_t(_Float16* tr, u32x4 a, u32x4 b, int
 
 __global__ __launch_bounds__(kThreads) void lora_params_partial_kernel(
     const uint16_t* __restrict__ y, const uint16_t* __restrict__ t,
-    const uint16_t* __restrict__ dt, const uint16_t* __restrict__ gsq,
-    const uint16_t* __restrict__ gsv, float* __restrict__ part, int M, int H, int NQ, int NV,
-    int64_t n_out) {
+    const uint16_t* __restrict__ dt, const uint16_t* __restrict__ gq, int64_t ldq,
+    const uint16_t* __restrict__ gv, int64_t ldv, float scaling, float* __restrict__ part, int M,
+    int H, int NQ, int NV, int64_t n_out) {
   __shared__ __align__(16) _Float16 XT[64 * kPStride];       // [64 columns][64 rows]
   __shared__ __align__(16) _Float16 ZT[2 * kR * kPStride];   // [32 columns][64 rows]
   const int nba = H / 64, nbq = NQ / 64;
@@ -494,8 +499,8 @@ __global__ __launch_bounds__(kThreads) void lora_params_partial_kernel(
   // kind 0: dA (X = y, Z = dt, 32 Z columns), 1: dBq (X = gs_q, Z = t[:, :r]), 2: dBv
   const int kind = blk < nba ? 0 : (blk < nba + nbq ? 1 : 2);
   const int col0 = 64 * (kind == 0 ? blk : (kind == 1 ? blk - nba : blk - nba - nbq));
-  const uint16_t* X = kind == 0 ? y : (kind == 1 ? gsq : gsv);
-  const int64_t ldx = kind == 0 ? H : (kind == 1 ? NQ : NV);
+  const uint16_t* X = kind == 0 ? y : (kind == 1 ? gq : gv);
+  const int64_t ldx = kind == 0 ? H : (kind == 1 ? ldq : ldv);
   const int zc = kind == 0 ? 2 * kR : kR;                   // Z columns
   const uint16_t* Z = (kind == 0 ? dt : t) + (kind == 2 ? kR : 0);
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
@@ -514,6 +519,10 @@ __global__ __launch_bounds__(kThreads) void lora_params_partial_kernel(
   if (has_z) load_pair(Z, 2 * kR, r_begin, r_end, rp, c8, za, zb);
   for (int r0 = r_begin; r0 < r_end; r0 += kChunk) {
     __syncthreads();
+    if (kind != 0) {   // gs = fp16(g * scaling), the value the fp16 GEMM it replaces reads
+      xa = scale_h8(xa, scaling);
+      xb = scale_h8(xb, scaling);
+    }
     store_pair_t(XT, xa, xb, rp, c8);
     if (has_z) store_pair_t(ZT, za, zb, rp, c8);
     __syncthreads();
@@ -638,21 +647,20 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_fwd(
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_rows(
     const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
-    const uint16_t* staged, float scaling, uint16_t* gs_q, uint16_t* gs_v, uint16_t* dt,
-    uint16_t* dy, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
+    const uint16_t* staged, float scaling, uint16_t* dt, uint16_t* dy, int64_t M, int32_t H,
+    int32_t NQ, int32_t NV, int32_t r, void* stream) {
   const int rc = check_dims(M, H, NQ, NV, r);
   if (rc != kOk) return rc;
   if (ld_q < NQ || ld_v < NV || ld_q % 8 || ld_v % 8) return kInvalid;
   if (M == 0) return kOk;
-  if (!g_q || !g_v || !staged || !gs_q || !gs_v || !dt || !dy) return kInvalid;
+  if (!g_q || !g_v || !staged || !dt || !dy) return kInvalid;
   for (const void* p : {static_cast<const void*>(g_q), static_cast<const void*>(g_v),
-                        static_cast<const void*>(staged), static_cast<const void*>(gs_q),
-                        static_cast<const void*>(gs_v), static_cast<const void*>(dy)})
+                        static_cast<const void*>(staged), static_cast<const void*>(dy)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
   return launch_kernel(lora_bwd_rows_kernel, dim3(grid, column_parts(M, H / 16)),
                        dim3(kThreads), static_cast<hipStream_t>(stream), g_q, ld_q, g_v, ld_v,
-                       reinterpret_cast<const _Float16*>(staged), scaling, gs_q, gs_v, dt, dy,
+                       reinterpret_cast<const _Float16*>(staged), scaling, dt, dy,
                        static_cast<int>(M), H, NQ, NV);
 }
 
@@ -669,9 +677,10 @@ namespace {
 // entry of every slice, so `part` needs no clearing and its old contents never leak into a
 // result.
 int lora_params_launch(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
-                       const uint16_t* gs_q, const uint16_t* gs_v, float* part, float* d_aq,
-                       float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ,
-                       int32_t NV, hipStream_t st) {
+                       const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
+                       float scaling, float* part, float* d_aq, float* d_av, float* d_bq,
+                       float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV,
+                       hipStream_t st) {
   const int64_t n_out = 2 * kR * static_cast<int64_t>(H) + kR * static_cast<int64_t>(NQ + NV);
   const unsigned reduce_grid = static_cast<unsigned>((n_out + 255) / 256);
   if (M == 0)   // no rows: zero gradients (the reduction over no slices)
@@ -681,8 +690,8 @@ int lora_params_launch(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
   const int slices = static_cast<int>((M + kSlice - 1) / kSlice);
   const dim3 grid(static_cast<unsigned>(H / 64 + NQ / 64 + NV / 64),
                   static_cast<unsigned>(slices));
-  int rc2 = launch_kernel(lora_params_partial_kernel, grid, dim3(kThreads), st, y, t, dt, gs_q,
-                          gs_v, part, static_cast<int>(M), H, NQ, NV, n_out);
+  int rc2 = launch_kernel(lora_params_partial_kernel, grid, dim3(kThreads), st, y, t, dt, g_q,
+                          ld_q, g_v, ld_v, scaling, part, static_cast<int>(M), H, NQ, NV, n_out);
   if (rc2 != kOk) return rc2;
   return launch_kernel(lora_params_reduce_kernel, dim3(reduce_grid), dim3(256), st, part,
                        slices, n_out, H, NQ, d_aq, d_av, d_bq, d_bv);
@@ -690,18 +699,19 @@ int lora_params_launch(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
 
 // Argument checks shared by both entry points (before any HIP call).
 int lora_params_check(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
-                      const uint16_t* gs_q, const uint16_t* gs_v, float* d_aq, float* d_av,
-                      float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV,
-                      int32_t r) {
+                      const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v, int64_t ld_v,
+                      float* d_aq, float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H,
+                      int32_t NQ, int32_t NV, int32_t r) {
   const int rc = check_dims(M, H, NQ, NV, r);
   if (rc != kOk) return rc;
   if (H % 64 || NQ % 64 || NV % 64) return kInvalid;
+  if (ld_q < NQ || ld_v < NV || ld_q % 8 || ld_v % 8) return kInvalid;
   if (!d_aq || !d_av || !d_bq || !d_bv) return kInvalid;
   if (M == 0) return kOk;
-  if (!y || !t || !dt || !gs_q || !gs_v) return kInvalid;
+  if (!y || !t || !dt || !g_q || !g_v) return kInvalid;
   for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(t),
-                        static_cast<const void*>(dt), static_cast<const void*>(gs_q),
-                        static_cast<const void*>(gs_v)})
+                        static_cast<const void*>(dt), static_cast<const void*>(g_q),
+                        static_cast<const void*>(g_v)})
     if (misaligned(p)) return kInvalid;
   if ((M + kSlice - 1) / kSlice > 65535) return kInvalid;
   return kOk;
@@ -740,23 +750,25 @@ int scratch_on_current_device(float** out) {
 }  // namespace
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params(
-    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
-    const uint16_t* gs_v, float* workspace, int64_t workspace_floats, float* d_aq, float* d_av,
-    float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r,
-    void* stream) {
-  const int rc = lora_params_check(y, t, dt, gs_q, gs_v, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV, r);
+    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* g_q, int64_t ld_q,
+    const uint16_t* g_v, int64_t ld_v, float scaling, float* workspace, int64_t workspace_floats,
+    float* d_aq, float* d_av, float* d_bq, float* d_bv, int64_t M, int32_t H, int32_t NQ,
+    int32_t NV, int32_t r, void* stream) {
+  const int rc = lora_params_check(y, t, dt, g_q, ld_q, g_v, ld_v, d_aq, d_av, d_bq, d_bv, M, H,
+                                   NQ, NV, r);
   if (rc != kOk) return rc;
   if (workspace_floats < lora_params_workspace(M, H, NQ, NV)) return kInvalid;
   if (M > 0 && (!workspace || misaligned(workspace))) return kInvalid;
-  return lora_params_launch(y, t, dt, gs_q, gs_v, workspace, d_aq, d_av, d_bq, d_bv, M, H, NQ,
-                            NV, static_cast<hipStream_t>(stream));
+  return lora_params_launch(y, t, dt, g_q, ld_q, g_v, ld_v, scaling, workspace, d_aq, d_av, d_bq,
+                            d_bv, M, H, NQ, NV, static_cast<hipStream_t>(stream));
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params_noalloc(
-    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* gs_q,
-    const uint16_t* gs_v, float* d_aq, float* d_av, float* d_bq, float* d_bv, int64_t M,
-    int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
-  const int rc = lora_params_check(y, t, dt, gs_q, gs_v, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV, r);
+    const uint16_t* y, const uint16_t* t, const uint16_t* dt, const uint16_t* g_q, int64_t ld_q,
+    const uint16_t* g_v, int64_t ld_v, float scaling, float* d_aq, float* d_av, float* d_bq,
+    float* d_bv, int64_t M, int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream) {
+  const int rc = lora_params_check(y, t, dt, g_q, ld_q, g_v, ld_v, d_aq, d_av, d_bq, d_bv, M, H,
+                                   NQ, NV, r);
   if (rc != kOk) return rc;
   if (lora_params_workspace(M, H, NQ, NV) > kLoraScratchFloats) return SOUPK_STATUS_SCRATCH_LIMIT;
   float* part = nullptr;
@@ -764,6 +776,6 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params_noal
     const int rs = scratch_on_current_device(&part);
     if (rs != kOk) return rs;
   }
-  return lora_params_launch(y, t, dt, gs_q, gs_v, part, d_aq, d_av, d_bq, d_bv, M, H, NQ, NV,
-                            static_cast<hipStream_t>(stream));
+  return lora_params_launch(y, t, dt, g_q, ld_q, g_v, ld_v, scaling, part, d_aq, d_av, d_bq,
+                            d_bv, M, H, NQ, NV, static_cast<hipStream_t>(stream));
 }

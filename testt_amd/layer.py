@@ -170,13 +170,12 @@ class QKVLora(torch.autograd.Function):
     @staticmethod
     def _backward_fused(ctx, g_qkv, g_lq, g_lv):
         y16, t, a_q, a_v, b_q, b_v, staged = ctx.saved_tensors
-        if g_lq is None and g_lv is None:
-            g_lq = torch.zeros((y16.shape[0], b_q.shape[0]), dtype=torch.float16,
-                               device=y16.device)
-        gs_q, gs_v, dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling,
-                                                 staged=staged)
+        m, dev = y16.shape[0], y16.device
+        g_lq = _lora.rows_view(g_lq, b_q.shape[0], m, dev)
+        g_lv = _lora.rows_view(g_lv, b_v.shape[0], m, dev)
+        dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling, staged=staged)
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
-        d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, gs_q, gs_v)
+        d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)

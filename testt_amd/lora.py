@@ -5,13 +5,14 @@ scalings.  `layer.QKVLora` uses it when `supported` holds and keeps its GEMM pat
 
     stage(a_q, a_v, b_q, b_v)                         -> the fp16 casts of the parameters
     lora_fwd(y16, a_q, a_v, b_q, b_v, scaling, st)    -> t [M, 32], lq [M, NQ], lv [M, NV] fp16
-    lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s, st) -> gs_q, gs_v, dt [M, 32], dy [M, H] fp16
-    lora_bwd_params(y16, t, dt, gs_q, gs_v)           -> dA_q, dA_v [16, H], dB_q, dB_v fp32
+    lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, s, st) -> dt [M, 32], dy [M, H] fp16
+    lora_bwd_params(y16, t, dt, g_q, g_v, s)          -> dA_q, dA_v [16, H], dB_q, dB_v fp32
 
 with t = fp16(y A^T), lq = fp16(fp16(t_q B_q^T) * s), gs = fp16(g * s),
 dt = fp16(gs_q B_q | gs_v B_v), dy = fp16(dt A), dA = fp32(fp16(dt^T y)),
 dB_x = fp32(fp16(gs_x^T t_x)): the rounding steps of the fp16 GEMMs they replace (fp32 sums in
-another order).  A and B enter the products as their fp16 casts (autocast's), which `stage`
+another order).  gs is never stored: both backward kernels form it from g as they read it.
+A and B enter the products as their fp16 casts (autocast's), which `stage`
 makes in one launch, in the layouts the kernels read; the forward's staged buffer serves its
 backward too (the parameters do not change in between).  Without `st` the functions stage
 the parameters themselves."""
@@ -115,32 +116,41 @@ def lora_bwd_rows(g_q, g_v, a_q, a_v, b_q, b_v, scaling, staged=None):
     NQ, NV = _check_params(a_q, a_v, b_q, b_v, a_q.shape[-1], dev)
     H = a_q.shape[1]
     st = _staged(staged, a_q, a_v, b_q, b_v, H, NQ, NV, dev)
-    g_q, g_v = _rows(g_q, NQ, M, dev), _rows(g_v, NV, M, dev)
-    if tuple(g_q.shape) != (M, NQ) or tuple(g_v.shape) != (M, NV):
-        raise ValueError(f"lora_bwd_rows: gradient shapes {tuple(g_q.shape)}, "
-                         f"{tuple(g_v.shape)} do not match ({M}, {NQ}), ({M}, {NV})")
-    gs_q = torch.empty((M, NQ), dtype=torch.float16, device=dev)
-    gs_v = torch.empty((M, NV), dtype=torch.float16, device=dev)
+    g_q, g_v = rows_view(g_q, NQ, M, dev), rows_view(g_v, NV, M, dev)
     dt = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
     dy = torch.empty((M, H), dtype=torch.float16, device=dev)
     _ext.call("soupk_lora_bwd_rows", _ext.ptr(g_q), g_q.stride(0), _ext.ptr(g_v), g_v.stride(0),
-              _ext.ptr(st), float(scaling), _ext.ptr(gs_q), _ext.ptr(gs_v), _ext.ptr(dt),
-              _ext.ptr(dy), M, H, NQ, NV, RANK, _ext.stream_of(dy))
-    return gs_q, gs_v, dt, dy
+              _ext.ptr(st), float(scaling), _ext.ptr(dt), _ext.ptr(dy), M, H, NQ, NV, RANK,
+              _ext.stream_of(dy))
+    return dt, dy
 
 
 SLICE_ROWS = 128   # rows per partial sum of soupk_lora_bwd_params
 
 
-def lora_bwd_params(y16, t, dt, gs_q, gs_v):
+def rows_view(g, n, m, dev):
+    """g_q / g_v as the backward kernels read them: fp16 [m, n] with unit column stride and a
+    16-byte aligned row stride (a view of the attention backward's q|k|v gradient stays one;
+    a missing gradient becomes zeros)."""
+    g = _rows(g, n, m, dev)
+    if tuple(g.shape) != (m, n):
+        raise ValueError(f"a LoRA output gradient has shape {tuple(g.shape)}, expected {(m, n)}")
+    return g
+
+
+def lora_bwd_params(y16, t, dt, g_q, g_v, scaling):
+    """dA_q, dA_v, dB_q, dB_v from the forward's y16 and t, the row backward's dt and the
+    gradients g_q, g_v of lq, lv (gs = fp16(g * scaling) formed as they are read)."""
     M, H = y16.shape
-    NQ, NV = gs_q.shape[1], gs_v.shape[1]
     dev = y16.device
-    for x, name, cols in ((y16, "y16", H), (t, "t", 2 * RANK), (dt, "dt", 2 * RANK),
-                          (gs_q, "gs_q", NQ), (gs_v, "gs_v", NV)):
+    for x, name, cols in ((y16, "y16", H), (t, "t", 2 * RANK), (dt, "dt", 2 * RANK)):
         _ext.require(x, name, dtype=torch.float16, ndim=2, device=dev)
         if tuple(x.shape) != (M, cols):
             raise ValueError(f"{name} has shape {tuple(x.shape)}, expected {(M, cols)}")
+    if g_q is None or g_v is None:
+        raise ValueError("lora_bwd_params needs g_q and g_v (pass zeros for a missing one)")
+    NQ, NV = g_q.shape[1], g_v.shape[1]
+    g_q, g_v = rows_view(g_q, NQ, M, dev), rows_view(g_v, NV, M, dev)
     slices = (M + SLICE_ROWS - 1) // SLICE_ROWS
     n_ws = slices * (2 * RANK * H + RANK * (NQ + NV))
     ws = torch.empty(max(n_ws, 4), dtype=torch.float32, device=dev)
@@ -148,7 +158,8 @@ def lora_bwd_params(y16, t, dt, gs_q, gs_v):
     d_av = torch.empty((RANK, H), dtype=torch.float32, device=dev)
     d_bq = torch.empty((NQ, RANK), dtype=torch.float32, device=dev)
     d_bv = torch.empty((NV, RANK), dtype=torch.float32, device=dev)
-    _ext.call("soupk_lora_bwd_params", _ext.ptr(y16), _ext.ptr(t), _ext.ptr(dt), _ext.ptr(gs_q),
-              _ext.ptr(gs_v), _ext.ptr(ws), ws.numel(), _ext.ptr(d_aq), _ext.ptr(d_av),
-              _ext.ptr(d_bq), _ext.ptr(d_bv), M, H, NQ, NV, RANK, _ext.stream_of(y16))
+    _ext.call("soupk_lora_bwd_params", _ext.ptr(y16), _ext.ptr(t), _ext.ptr(dt), _ext.ptr(g_q),
+              g_q.stride(0), _ext.ptr(g_v), g_v.stride(0), float(scaling), _ext.ptr(ws),
+              ws.numel(), _ext.ptr(d_aq), _ext.ptr(d_av), _ext.ptr(d_bq), _ext.ptr(d_bv), M, H,
+              NQ, NV, RANK, _ext.stream_of(y16))
     return d_aq, d_av, d_bq, d_bv
