@@ -23,6 +23,7 @@ import ctypes
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -874,6 +875,11 @@ def pmc_traffic(entry, path=TRAFFIC_TABLE):
 
 
 def _kernel_base(name):
+    # A name the profiler left mangled (it does not demangle _Float16 parameters): the
+    # length-prefixed function name after the namespaces.
+    m = re.match(r"_ZN5soupk12_GLOBAL__N_1(\d+)", name)
+    if m:
+        return name[m.end():m.end() + int(m.group(1))]
     return name.replace("soupk::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
 
 
