@@ -108,12 +108,17 @@ def lib():
     return _lib
 
 
+_entry = {}   # name -> the bound ctypes function of the package's library
+
+
 def call(name, *args):
     """Invoke entry point `name`; raise SoupkError on a non-zero status."""
-    handle = lib()
-    status = getattr(handle, name)(*args)
+    fn = _entry.get(name)
+    if fn is None:
+        fn = _entry[name] = getattr(lib(), name)
+    status = fn(*args)
     if status != 0:
-        text = handle.soupk_status_string(status)
+        text = lib().soupk_status_string(status)
         text = text.decode() if text else "?"
         raise SoupkError(f"{name} failed with status {status}: {text}")
 
@@ -144,14 +149,14 @@ def public_stream_of(tensor):
 
 def require(tensor, name, dtype=None, ndim=None, device=None):
     """Kernel inputs must be contiguous HIP device tensors of the stated dtype."""
-    if not torch.is_tensor(tensor):
+    if not isinstance(tensor, torch.Tensor):
         raise TypeError(f"{name} must be a tensor, got {type(tensor).__name__}")
     if not tensor.is_cuda:
         raise ValueError(f"{name} must be a HIP device tensor (got device {tensor.device}); "
                          "the soupk kernels have no CPU path")
     if device is not None and tensor.device != device:
         raise ValueError(f"{name} is on {tensor.device}, expected {device}")
-    if dtype is not None and tensor.dtype != dtype:
+    if dtype is not None and tensor.dtype is not dtype:
         raise TypeError(f"{name} must be {dtype}, got {tensor.dtype}")
     if ndim is not None and tensor.dim() != ndim:
         raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(tensor.shape)}")

@@ -65,6 +65,12 @@ def gated_silu_backward_(dact, gu):
     return gu
 
 
+def _mm(a, b):
+    """a @ b: torch.mm for the 2-d operands of the layer (the same hipBLASLt GEMM as
+    torch.matmul, without its shape dispatch on the host), torch.matmul otherwise."""
+    return torch.mm(a, b) if a.dim() == 2 else torch.matmul(a, b)
+
+
 def matmul_split_k(a, b, parts):
     """fp16 a [M, K] @ b [K, N] as `parts` GEMMs over equal slices of K (batched, fp32
     outputs), summed in slice order and rounded once to fp16.  K % parts == 0; a and b must
@@ -88,7 +94,7 @@ class FusedNF4MLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, gate_up16=None, down16=None):
         gate_up = gate_up16 if gate_up16 is not None else unpack_concat((gate_w, up_w), x.device)
-        gu = torch.matmul(x, gate_up.t())
+        gu = _mm(x, gate_up.t())
         act = gated_silu(gu)
         ctx.recompute = RECOMPUTE_GATE_UP
         ctx.consumed = False
@@ -98,7 +104,7 @@ class FusedNF4MLP(torch.autograd.Function):
         else:
             ctx.save_for_backward(x, gu)
         down = down16 if down16 is not None else unpack_concat((down_w,), x.device)
-        out = torch.matmul(act, down.t())
+        out = _mm(act, down.t())
         ctx.weights = (gate_w, up_w, down_w)
         keep_for_backward(ctx, (gate_up, down))
         return out
@@ -116,12 +122,12 @@ class FusedNF4MLP(torch.autograd.Function):
         gate_up, down = kept if kept is not None else (None, None)
         if down is None:
             down = unpack_concat((down_w,), grad_out.device)
-        dact = torch.matmul(grad_out, down)
+        dact = _mm(grad_out, down)
         del down
         if gate_up is None:
             gate_up = unpack_concat((gate_w, up_w), grad_out.device)
         if ctx.recompute:
-            gu = torch.matmul(x, gate_up.t())
+            gu = _mm(x, gate_up.t())
         else:
             if ctx.consumed:
                 raise RuntimeError("FusedNF4MLP: backward ran twice through a graph whose kept "
@@ -135,7 +141,7 @@ class FusedNF4MLP(torch.autograd.Function):
         if parts > 1 and gu.shape[1] % parts == 0 and gu.shape[0] > 0:
             grad_x = matmul_split_k(gu, gate_up, parts)
         else:
-            grad_x = torch.matmul(gu, gate_up)
+            grad_x = _mm(gu, gate_up)
         return grad_x, None, None, None, None, None
 
 

@@ -376,7 +376,8 @@ class FrozenNF4Linear(torch.autograd.Function):
         grad_x = None
         if ctx.needs_input_grad[0]:
             weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
-            grad_x = grad_out.to(torch.float16) @ weight
+            g = grad_out.to(torch.float16)
+            grad_x = torch.mm(g, weight) if g.dim() == 2 else g @ weight
         return grad_x, None, None, None
 
 
