@@ -102,6 +102,22 @@ int soupk_nf4_unpack_multi(int32_t n_parts, const uint8_t* const* packed,
                            void* stream);
 
 /*
+ * soupk_nf4_unpack_multi and soupk_lora_stage in one launch: the NF4 parts as there, and the
+ * rank-16 LoRA parameters a_q, a_v, b_q, b_v of the same layer cast to fp16 into `staged` by
+ * extra workgroups (the same values and layout as soupk_lora_stage).  A decoder layer then
+ * prepares all of its weights, frozen and trainable, with one launch before its forward.  The
+ * LoRA arguments follow soupk_lora_stage's rules and are checked before anything is launched.
+ */
+int soupk_nf4_unpack_multi_lora(int32_t n_parts, const uint8_t* const* packed,
+                                const uint8_t* const* absmax_u8, const float* const* code2,
+                                const float* const* absmax2, const float* const* offset,
+                                const float* const* nf4, uint16_t* const* out_f16,
+                                const int64_t* n_bytes, int32_t qblock, int32_t qblock2,
+                                const float* a_q, const float* a_v, const float* b_q,
+                                const float* b_v, uint16_t* staged, int64_t staged_elems,
+                                int32_t H, int32_t NQ, int32_t NV, int32_t r, void* stream);
+
+/*
  * Inverse of a scatter index (no counterpart kernel in the reference: it lets the pad-layout
  * writers of rmsnorm_fwd and rope_pack_fwd zero the unused rows in the same launch instead of
  * a separate torch.zeros, solution/rmsnorm.py:82, solution/rope.py:141-143).

@@ -81,6 +81,13 @@ def test_version_and_status_strings(lib):
     ("soupk_lora_stage", (16, 32, 48, 64, 128, 128 * 256 + 32 * 256 - 1, 256, 128, 128, 16,
                           None)),
     ("soupk_lora_stage", (16, 32, 48, 64, 128, 1 << 20, 256, 128, 128, 8, None)),
+    # the unpack with the LoRA staging: the same LoRA rules, checked before the NF4 parts
+    ("soupk_nf4_unpack_multi_lora", (0,) + (None,) * 8 + (64, 256) +
+     (16, 32, 48, 64, 128, 1 << 20, 256, 128, 128, 8, None)),
+    ("soupk_nf4_unpack_multi_lora", (0,) + (None,) * 8 + (64, 256) +
+     (16, 32, 48, 64, 128, 100, 256, 128, 128, 16, None)),
+    ("soupk_nf4_unpack_multi_lora", (0,) + (None,) * 8 + (64, 256) +
+     (16, 32, 48, 64, 136, 1 << 20, 256, 128, 128, 16, None)),            # misaligned staged
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

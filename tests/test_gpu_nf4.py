@@ -187,6 +187,31 @@ def test_unpack_groups_one_buffer():
     assert not torch.equal(third[2], stacks[2])
 
 
+def test_unpack_groups_lora_stages_in_the_same_launch():
+    """unpack_groups_lora: the stacks bit-identical to unpack_groups', and the LoRA staging
+    (extra workgroups of the last launch) bit-identical to lora.stage; over more than one
+    launch (11 weights) and over one."""
+    from testt_amd import lora
+
+    H, NQ, NV = 640, 384, 128
+    g = torch.Generator().manual_seed(5)
+    params = ((torch.randn(16, H, generator=g) / 25).to(DEV),
+              (torch.randn(16, H, generator=g) / 25).to(DEV),
+              (torch.randn(NQ, 16, generator=g) / 20).to(DEV),
+              (torch.randn(NV, 16, generator=g) / 20).to(DEV))
+    for groups in ((((96, 640), (32, 640), (32, 640)), ((640, 64),), ((128, 640), (128, 640)),
+                    ((640, 128),), ((64, 640), (64, 640), (64, 640), (64, 640))),
+                   (((128, 640), (64, 640)), ((640, 128),))):
+        weights = [tuple(workloads.nf4_weight(*shape, seed=90 + 10 * gi + wi, device=DEV)
+                         for wi, shape in enumerate(group)) for gi, group in enumerate(groups)]
+        print(f"unpack_groups_lora: {sum(len(gr) for gr in groups)} weights", flush=True)
+        stacks, staged = nf4.unpack_groups_lora(weights, DEV, params)
+        want = nf4.unpack_groups(weights, DEV)
+        assert all(torch.equal(a, b) for a, b in zip(stacks, want))
+        assert staged.data_ptr() % 16 == 0
+        assert torch.equal(staged, lora.stage(*params))
+
+
 def test_unpack_multi_rejects_invalid_arguments():
     import ctypes
 

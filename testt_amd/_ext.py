@@ -31,6 +31,8 @@ _f32 = ctypes.c_float
 SIGNATURES = {
     "soupk_nf4_unpack": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
     "soupk_nf4_unpack_multi": [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p],
+    "soupk_nf4_unpack_multi_lora": [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _p,
+                                    _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
     "soupk_index_inverse": [_p, _i64, _p, _i64, _p],
     "soupk_sum_partials": [_p, _i32, _i64, _i64, _p, _p],
     "soupk_rmsnorm_fwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _f32, _p],

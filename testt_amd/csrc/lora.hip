@@ -42,6 +42,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "lora_stage.hpp"
 #include "soupk_common.hpp"
 
 namespace soupk {
@@ -51,7 +52,7 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kR = 16;           // LoRA rank
+constexpr int kR = kLoraRank;    // LoRA rank
 #ifndef SOUPK_LORA_ROW_TILES
 #define SOUPK_LORA_ROW_TILES 1
 #endif
@@ -94,42 +95,9 @@ __device__ __forceinline__ int tile_part(int n_tiles, int part, int parts) {
 // instead of being moved down to their first use.
 __device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
 
-// Offsets (halves) of the sections of the staged parameter buffer (r = kR).
-struct StagedLayout {
-  int64_t a16, a16t, b16, b16t_q, b16t_v, total;
-};
-__host__ __device__ inline StagedLayout staged_layout(int64_t H, int64_t NQ, int64_t NV) {
-  StagedLayout L;
-  L.a16 = 0;
-  L.a16t = 2 * kR * H;
-  L.b16 = 4 * kR * H;
-  L.b16t_q = L.b16 + (NQ + NV) * kR;
-  L.b16t_v = L.b16t_q + kR * NQ;
-  L.total = L.b16t_v + kR * NV;
-  return L;
-}
-
 // One thread per parameter value: the fp16 cast written in both layouts of its section.
-__global__ __launch_bounds__(256) void lora_stage_kernel(
-    const float* __restrict__ aq, const float* __restrict__ av, const float* __restrict__ bq,
-    const float* __restrict__ bv, _Float16* __restrict__ st, int H, int NQ, int NV) {
-  const StagedLayout L = staged_layout(H, NQ, NV);
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t na = 2 * kR * static_cast<int64_t>(H);
-  if (e < na) {
-    const int i = static_cast<int>(e / H), k = static_cast<int>(e % H);
-    const _Float16 v = static_cast<_Float16>(i < kR ? aq[e] : av[e - kR * static_cast<int64_t>(H)]);
-    st[L.a16 + e] = v;
-    st[L.a16t + static_cast<int64_t>(k) * (2 * kR) + i] = v;
-  } else if (e < na + static_cast<int64_t>(NQ + NV) * kR) {
-    const int64_t e2 = e - na;
-    const int j = static_cast<int>(e2 / kR), i = static_cast<int>(e2 % kR);
-    const bool q = j < NQ;
-    const _Float16 v = static_cast<_Float16>(q ? bq[e2] : bv[e2 - static_cast<int64_t>(NQ) * kR]);
-    st[L.b16 + e2] = v;
-    if (q) st[L.b16t_q + static_cast<int64_t>(i) * NQ + j] = v;
-    else st[L.b16t_v + static_cast<int64_t>(i) * NV + (j - NQ)] = v;
-  }
+__global__ __launch_bounds__(256) void lora_stage_kernel(LoraStageArgs a) {
+  lora_stage_value(a, static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x);
 }
 
 // The parameter and activation pointers of the row kernels are not __restrict__: loads through
@@ -622,10 +590,10 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_stage(
   if (!a_q || !a_v || !b_q || !b_v || !staged) return kInvalid;
   if (misaligned(staged)) return kInvalid;
   if (staged_elems < staged_layout(H, NQ, NV).total) return kInvalid;
-  const int64_t n = 2 * kR * static_cast<int64_t>(H) + static_cast<int64_t>(NQ + NV) * kR;
+  const int64_t n = staged_values(H, NQ, NV);
+  const LoraStageArgs a{a_q, a_v, b_q, b_v, reinterpret_cast<_Float16*>(staged), H, NQ, NV};
   return launch_kernel(lora_stage_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-                       dim3(256), static_cast<hipStream_t>(stream), a_q, a_v, b_q, b_v,
-                       reinterpret_cast<_Float16*>(staged), H, NQ, NV);
+                       dim3(256), static_cast<hipStream_t>(stream), a);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_fwd(

@@ -17,6 +17,7 @@
 // Other layouts (qblock or qblock2 not a power of two, qblock < 8, unaligned pointers) take a
 // one-byte-per-thread kernel with the same arithmetic, which also handles the last n_bytes % 4.
 
+#include "lora_stage.hpp"
 #include "soupk_common.hpp"
 
 namespace soupk {
@@ -138,6 +139,28 @@ __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_multi_kernel(Nf4Parts 
                   scale);
 }
 
+// The same launch with extra workgroups after the NF4 tiles that stage a decoder layer's LoRA
+// parameters in fp16 (lora_stage.hpp), so that preparing the layer's weights takes one launch.
+__global__ __launch_bounds__(kNf4Threads) void nf4_unpack_multi_lora_kernel(
+    Nf4Parts parts, int dword_block_shift, int block2_shift, LoraStageArgs lora, int nf4_tiles) {
+  __shared__ float2 pair[256];
+  __shared__ float scale[kNf4TileDwords];
+  const int x = static_cast<int>(blockIdx.x);
+  if (x >= nf4_tiles) {   // a whole workgroup: no barrier below is reached by part of one
+    lora_stage_value(lora, static_cast<int64_t>(x - nf4_tiles) * kNf4Threads + threadIdx.x);
+    return;
+  }
+  int p = 0;
+#pragma unroll
+  for (int q = 1; q < kNf4MaxParts; ++q)
+    p += (q < parts.n_parts && x >= parts.first_tile[q]) ? 1 : 0;
+  nf4_unpack_tile(parts.packed[p], parts.absmax_u8[p], parts.code2[p], parts.absmax2[p],
+                  parts.offset[p], parts.nf4[p], parts.out[p],
+                  static_cast<int64_t>(x - parts.first_tile[p]) * kNf4TileDwords,
+                  parts.n_dwords[p], parts.n_blocks[p], dword_block_shift, block2_shift, pair,
+                  scale);
+}
+
 // One packed byte per thread; any even qblock, any qblock2, any alignment.  Also used for the
 // bytes after the last whole dword of the vector kernel.
 __global__ __launch_bounds__(kNf4Threads) void nf4_unpack_byte_kernel(
@@ -210,13 +233,20 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack(
   return kOk;
 }
 
-extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi(
-    int32_t n_parts, const uint8_t* const* packed, const uint8_t* const* absmax_u8,
-    const float* const* code2, const float* const* absmax2, const float* const* offset,
-    const float* const* nf4, uint16_t* const* out_f16, const int64_t* n_bytes, int32_t qblock,
-    int32_t qblock2, void* stream) {
+namespace soupk {
+namespace {
+
+// The vector-path parts of a multi-part unpack as one tile table; parts the tiles do not take
+// are unpacked at once by their own launches (soupk_nf4_unpack).
+int nf4_multi_parts(int32_t n_parts, const uint8_t* const* packed,
+                    const uint8_t* const* absmax_u8, const float* const* code2,
+                    const float* const* absmax2, const float* const* offset,
+                    const float* const* nf4, uint16_t* const* out_f16, const int64_t* n_bytes,
+                    int32_t qblock, int32_t qblock2, void* stream, Nf4Parts* parts,
+                    int64_t* tiles_out) {
   if (n_parts < 0 || n_parts > kNf4MaxParts || qblock <= 0 || (qblock & 1) || qblock2 <= 0)
     return kInvalid;
+  *tiles_out = 0;
   if (n_parts == 0) return kOk;
   if (!packed || !absmax_u8 || !code2 || !absmax2 || !offset || !nf4 || !out_f16 || !n_bytes)
     return kInvalid;
@@ -228,9 +258,8 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi(
   }
   const bool vec_layout = qblock >= 8 && qblock / 8 <= kNf4TileDwords && is_pow2(qblock) &&
                           is_pow2(qblock2);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t bytes_per_block = qblock / 2;
-  Nf4Parts parts{};
+  *parts = Nf4Parts{};
   int64_t tiles = 0;
   for (int i = 0; i < n_parts; ++i) {
     if (n_bytes[i] == 0) continue;
@@ -242,22 +271,69 @@ extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi(
       if (st != kOk) return st;
       continue;
     }
-    const int j = parts.n_parts++;
-    parts.packed[j] = reinterpret_cast<const uint32_t*>(packed[i]);
-    parts.absmax_u8[j] = absmax_u8[i];
-    parts.code2[j] = code2[i];
-    parts.absmax2[j] = absmax2[i];
-    parts.offset[j] = offset[i];
-    parts.nf4[j] = nf4[i];
-    parts.out[j] = reinterpret_cast<u32x4*>(out_f16[i]);
-    parts.n_dwords[j] = n_bytes[i] / 4;
-    parts.n_blocks[j] = (n_bytes[i] + bytes_per_block - 1) / bytes_per_block;
-    parts.first_tile[j] = static_cast<int>(tiles);
-    tiles += (parts.n_dwords[j] + kNf4TileDwords - 1) / kNf4TileDwords;
+    const int j = parts->n_parts++;
+    parts->packed[j] = reinterpret_cast<const uint32_t*>(packed[i]);
+    parts->absmax_u8[j] = absmax_u8[i];
+    parts->code2[j] = code2[i];
+    parts->absmax2[j] = absmax2[i];
+    parts->offset[j] = offset[i];
+    parts->nf4[j] = nf4[i];
+    parts->out[j] = reinterpret_cast<u32x4*>(out_f16[i]);
+    parts->n_dwords[j] = n_bytes[i] / 4;
+    parts->n_blocks[j] = (n_bytes[i] + bytes_per_block - 1) / bytes_per_block;
+    parts->first_tile[j] = static_cast<int>(tiles);
+    tiles += (parts->n_dwords[j] + kNf4TileDwords - 1) / kNf4TileDwords;
     if (tiles > 0x7fffffff) return kInvalid;
   }
-  if (parts.n_parts == 0) return kOk;
-  for (int j = parts.n_parts; j <= kNf4MaxParts; ++j) parts.first_tile[j] = static_cast<int>(tiles);
+  for (int j = parts->n_parts; j <= kNf4MaxParts; ++j)
+    parts->first_tile[j] = static_cast<int>(tiles);
+  *tiles_out = tiles;
+  return kOk;
+}
+
+}  // namespace
+}  // namespace soupk
+
+extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi(
+    int32_t n_parts, const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+    const float* const* code2, const float* const* absmax2, const float* const* offset,
+    const float* const* nf4, uint16_t* const* out_f16, const int64_t* n_bytes, int32_t qblock,
+    int32_t qblock2, void* stream) {
+  Nf4Parts parts;
+  int64_t tiles = 0;
+  const int rc = nf4_multi_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4,
+                                 out_f16, n_bytes, qblock, qblock2, stream, &parts, &tiles);
+  if (rc != kOk || tiles == 0) return rc;
   return launch_kernel(nf4_unpack_multi_kernel, dim3(static_cast<unsigned>(tiles)),
-                       dim3(kNf4Threads), s, parts, log2_exact(qblock / 8), log2_exact(qblock2));
+                       dim3(kNf4Threads), static_cast<hipStream_t>(stream), parts,
+                       log2_exact(qblock / 8), log2_exact(qblock2));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_nf4_unpack_multi_lora(
+    int32_t n_parts, const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+    const float* const* code2, const float* const* absmax2, const float* const* offset,
+    const float* const* nf4, uint16_t* const* out_f16, const int64_t* n_bytes, int32_t qblock,
+    int32_t qblock2, const float* a_q, const float* a_v, const float* b_q, const float* b_v,
+    uint16_t* staged, int64_t staged_elems, int32_t H, int32_t NQ, int32_t NV, int32_t r,
+    void* stream) {
+  // The LoRA arguments first (nothing launched if they are rejected): soupk_lora_stage's rules.
+  if (r != kLoraRank || H <= 0 || NQ <= 0 || NV <= 0 || H % 128 || NQ % 128 || NV % 128)
+    return kInvalid;
+  if (!a_q || !a_v || !b_q || !b_v || !staged || !aligned(staged, 16)) return kInvalid;
+  if (staged_elems < staged_layout(H, NQ, NV).total) return kInvalid;
+  if (n_parts < 0 || n_parts > kNf4MaxParts) return kInvalid;
+  Nf4Parts parts;
+  int64_t tiles = 0;
+  const int rc = nf4_multi_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4,
+                                 out_f16, n_bytes, qblock, qblock2, stream, &parts, &tiles);
+  if (rc != kOk) return rc;
+  const int64_t stage_groups = (staged_values(H, NQ, NV) + kNf4Threads - 1) / kNf4Threads;
+  if (tiles + stage_groups > 0x7fffffff) return kInvalid;
+  const LoraStageArgs lora{a_q, a_v, b_q, b_v, reinterpret_cast<_Float16*>(staged), H, NQ, NV};
+  const int qshift = tiles > 0 ? log2_exact(qblock / 8) : 0;
+  const int q2shift = tiles > 0 ? log2_exact(qblock2) : 0;
+  return launch_kernel(nf4_unpack_multi_lora_kernel,
+                       dim3(static_cast<unsigned>(tiles + stage_groups)), dim3(kNf4Threads),
+                       static_cast<hipStream_t>(stream), parts, qshift, q2shift, lora,
+                       static_cast<int>(tiles));
 }

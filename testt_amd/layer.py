@@ -37,7 +37,7 @@ from . import lora as _lora
 from . import workloads
 from .mlp import fused_mlp
 from .nf4 import (frozen_linear, keep_for_backward, unpack_concat, unpack_groups,
-                  unpacked_for_backward)
+                  unpack_groups_lora, unpacked_for_backward)
 from .rmsnorm import add_rmsnorm
 from .rope import rope_pack
 
@@ -114,7 +114,7 @@ class QKVLora(torch.autograd.Function):
     autocast (solution/model.py:195-206 with dropout p = 0)."""
 
     @staticmethod
-    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16=None):
+    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16=None, staged=None):
         w = w16 if w16 is not None else unpack_concat(weights, y16.device)
         qkv = torch.nn.functional.linear(y16, w, bias)
         keep_for_backward(ctx, w)
@@ -123,7 +123,8 @@ class QKVLora(torch.autograd.Function):
         params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
         ctx.fused = USE_FUSED_LORA and _lora.supported(y16, *params)
         if ctx.fused:       # testt_amd/csrc/lora.hip: the parameters' fp16 casts, then t, lq, lv
-            staged = _lora.stage(*params)
+            if staged is None:   # (else staged by the layer's weight launch, unpack_groups_lora)
+                staged = _lora.stage(*params)
             t, lq, lv = _lora.lora_fwd(y16, *params, scaling, staged=staged)
             ctx.save_for_backward(y16, t, *params, staged)
             return qkv, lq, lv
@@ -165,7 +166,7 @@ class QKVLora(torch.autograd.Function):
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)
-        return dy, None, grads[0], grads[1], grads[2], grads[3], None, None, None
+        return dy, None, grads[0], grads[1], grads[2], grads[3], None, None, None, None
 
     @staticmethod
     def _backward_fused(ctx, g_qkv, g_lq, g_lv):
@@ -179,7 +180,7 @@ class QKVLora(torch.autograd.Function):
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
             dy.addmm_(g_qkv.to(torch.float16), w)
-        return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None
+        return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None, None
 
 
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
@@ -240,14 +241,22 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     padded."""
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
-    w_qkv = w_o = w_gu = w_d = None
+    w_qkv = w_o = w_gu = w_d = staged = None
     if UNPACK_PER_LAYER:
-        w_qkv, w_o, w_gu, w_d = unpack_groups(((w.q, w.k, w.v), (w.o,), (w.gate, w.up),
-                                               (w.down,)), s.device)
+        groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
+        a_q, b_q = w.lora_q
+        a_v, b_v = w.lora_v
+        if w.dropout == 0.0 and USE_FUSED_LORA and \
+                _lora.params_supported(a_q, a_v, b_q, b_v, s.device):
+            # the LoRA parameters' fp16 staging rides on the same launch as the unpack
+            (w_qkv, w_o, w_gu, w_d), staged = unpack_groups_lora(
+                groups, s.device, tuple(p.detach() for p in (a_q, a_v, b_q, b_v)))
+        else:
+            w_qkv, w_o, w_gu, w_d = unpack_groups(groups, s.device)
     if w.dropout == 0.0:
         s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         qkv, lq, lv = QKVLora.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
-                                    (w.q, w.k, w.v), w_qkv)
+                                    (w.q, w.k, w.v), w_qkv, staged)
     else:
         s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
         qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias, w_qkv)

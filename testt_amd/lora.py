@@ -24,18 +24,23 @@ from . import _ext
 RANK = 16
 
 
+def params_supported(a_q, a_v, b_q, b_v, device):
+    """Rank 16 fp32 contiguous parameters on `device`, H, NQ, NV multiples of 128."""
+    for p in (a_q, a_v, b_q, b_v):
+        if p.dtype != torch.float32 or p.device != device or not p.is_contiguous() or \
+                p.dim() != 2:
+            return False
+    H = a_q.shape[1]
+    return (tuple(a_q.shape) == (RANK, H) and tuple(a_v.shape) == (RANK, H)
+            and b_q.shape[1] == RANK and b_v.shape[1] == RANK and H % 128 == 0
+            and b_q.shape[0] % 128 == 0 and b_v.shape[0] % 128 == 0)
+
+
 def supported(y16, a_q, a_v, b_q, b_v):
     """Rank 16, fp16 y and fp32 parameters on one HIP device, H, NQ, NV multiples of 128."""
     if not (y16.is_cuda and y16.dtype == torch.float16 and y16.dim() == 2):
         return False
-    H = y16.shape[1]
-    for p in (a_q, a_v, b_q, b_v):
-        if p.dtype != torch.float32 or p.device != y16.device or not p.is_contiguous():
-            return False
-    return (tuple(a_q.shape) == (RANK, H) and tuple(a_v.shape) == (RANK, H)
-            and b_q.dim() == 2 and b_q.shape[1] == RANK and b_v.dim() == 2
-            and b_v.shape[1] == RANK and H % 128 == 0 and b_q.shape[0] % 128 == 0
-            and b_v.shape[0] % 128 == 0)
+    return params_supported(a_q, a_v, b_q, b_v, y16.device) and a_q.shape[1] == y16.shape[1]
 
 
 def _check_params(a_q, a_v, b_q, b_v, H, dev):

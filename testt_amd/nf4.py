@@ -269,16 +269,35 @@ class _GroupPlan:
         return all(ref() is w and _plan_key(w, device) == key
                    for (ref, key), w in zip(self.check, flat_w))
 
-    def run(self, device):
-        buf = torch.empty(self.total, dtype=torch.float16, device=device)
+    def run(self, device, lora_params=None):
+        """The stacks; with lora_params (a_q, a_v, b_q, b_v), also their fp16 staging
+        (lora.stage) by the same launch, placed after the stacks: (stacks, staged)."""
+        extra = 0
+        if lora_params is not None:
+            from . import lora as _lora
+
+            a_q = lora_params[0]
+            H = a_q.shape[1]
+            NQ, NV = _lora._check_params(*lora_params, H, device)
+            extra = _lora.staged_elems(H, NQ, NV)
+        buf = torch.empty(self.total + extra, dtype=torch.float16, device=device)
         base = buf.data_ptr()
         stream = _ext.stream_of(buf)
-        for n, arrays, sizes, out_offsets in self.launches:
+        last = len(self.launches) - 1
+        for c, (n, arrays, sizes, out_offsets) in enumerate(self.launches):
             outs = (ctypes.c_void_p * n)(*[base + o for o in out_offsets])
-            _ext.call("soupk_nf4_unpack_multi", n, *[ctypes.addressof(a) for a in arrays],
-                      ctypes.addressof(outs), ctypes.addressof(sizes), self.qblock,
-                      self.qblock2, stream)
-        return [buf[st:st + rows * cols].view(rows, cols) for st, rows, cols in self.stacks]
+            args = (n, *[ctypes.addressof(a) for a in arrays], ctypes.addressof(outs),
+                    ctypes.addressof(sizes), self.qblock, self.qblock2)
+            if extra and c == last:
+                _ext.call("soupk_nf4_unpack_multi_lora", *args,
+                          *[p.data_ptr() for p in lora_params], base + 2 * self.total, extra,
+                          H, NQ, NV, _lora.RANK, stream)
+            else:
+                _ext.call("soupk_nf4_unpack_multi", *args, stream)
+        stacks = [buf[st:st + rows * cols].view(rows, cols) for st, rows, cols in self.stacks]
+        if lora_params is None:
+            return stacks
+        return stacks, buf[self.total:]
 
 
 def _group_plan(groups, device, flat_w, offsets, stacks, total):
@@ -293,17 +312,48 @@ def _group_plan(groups, device, flat_w, offsets, stacks, total):
     return plan
 
 
+def unpack_groups_lora(groups, device, lora_params):
+    """unpack_groups plus the fp16 staging of a decoder layer's LoRA parameters
+    lora_params = (a_q, a_v, b_q, b_v) (testt_amd.lora.stage's buffer) in the same launch:
+    (stacks, staged)."""
+    device = _hip_device(device)
+    flat_w, offsets, stacks, total = _group_layout(groups)
+    if flat_w:
+        plan = _group_plan(groups, device, flat_w, offsets, stacks, total)
+        if plan.ok and plan.launches:
+            return plan.run(device, lora_params)
+    from . import lora as _lora
+
+    return _unpack_groups_generic(groups, device), _lora.stage(*lora_params)
+
+
 def unpack_groups(groups, device):
     """One fp16 [sum N_i, K] row stack per group of weights (unpack_concat of each group), all
     unpacked by one launch into a single buffer: the projections of a decoder layer
     (q|k|v, o, gate|up, down) before its forward.  Returns the stacks, views of the buffer.
     The launch arguments are prepared once per list of weights (_GroupPlan) and checked on each
     call with the same key as each weight's own plan."""
+    device = _hip_device(device)
+    flat_w, offsets, stacks, total = _group_layout(groups)
+    if flat_w:
+        plan = _group_plan(groups, device, flat_w, offsets, stacks, total)
+        if plan.ok:
+            return plan.run(device)
+    return _unpack_groups_generic(groups, device)
+
+
+def _hip_device(device):
     device = torch.device(device)
     if device.type != "cuda":
         raise ValueError("unpack_groups: the device must be a HIP device (no CPU path)")
     if device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())
+    return device
+
+
+def _group_layout(groups):
+    """The weights in order, each one's element offset in the buffer, each stack's
+    (offset, rows, cols), and the buffer's size (stacks at multiples of _GROUP_ALIGN)."""
     flat_w, offsets, stacks, total = [], [], [], 0
     for weights in groups:
         rows = [weight_shape(w)[0] for w in weights]
@@ -317,11 +367,7 @@ def unpack_groups(groups, device):
             offsets.append(total + r0 * cols)
             r0 += n
         total += -(-sum(rows) * cols // _GROUP_ALIGN) * _GROUP_ALIGN
-    if flat_w:
-        plan = _group_plan(groups, device, flat_w, offsets, stacks, total)
-        if plan.ok:
-            return plan.run(device)
-    return _unpack_groups_generic(groups, device)
+    return flat_w, offsets, stacks, total
 
 
 def _unpack_groups_generic(groups, device):
