@@ -94,21 +94,24 @@ constexpr int kAuxNonTemporal = 2;  // cache-policy bits of buffer ops: streamin
 // from a wave-uniform base (kernel arguments, blockIdx, readfirstlane values) and covers `bytes`
 // from it: the hardware drops stores at byte offsets >= bytes.
 constexpr int kAuxStream = 2 | 16;  // nt | sc1
-struct StreamOut {
+// (A kernel may take nt alone, Aux = kAuxNonTemporal, where that measured faster.)
+template <int Aux>
+struct StreamOutT {
   __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ StreamOut(const void* base, uint64_t bytes)
+  __device__ __forceinline__ StreamOutT(const void* base, uint64_t bytes)
       : r(buffer_rsrc(base, bytes > 0xffffffffull ? 0xffffffffu
                                                   : static_cast<uint32_t>(bytes))) {}
   __device__ __forceinline__ void store(uint32_t off, u32x4 v) const {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, kAuxStream);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, Aux);
   }
   __device__ __forceinline__ void store(uint32_t off, f32x4 v) const {
     store(off, __builtin_bit_cast(u32x4, v));
   }
   __device__ __forceinline__ void store(uint32_t off, u32x2 v) const {
-    __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(off), 0, kAuxStream);
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(off), 0, Aux);
   }
 };
+using StreamOut = StreamOutT<kAuxStream>;
 
 // ---- streaming (non-temporal) or cached global access, chosen at compile time ---------------
 // Data read or written exactly once per launch streams past the caches when NT is true.
