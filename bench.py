@@ -9,9 +9,9 @@ shape).  Inputs are resident in HBM before the timed region; 20 warm-up steps, 2
 Each launch carries a pair of HIP events on the stream it runs on (torch's current stream),
 recorded by the kernel dispatch itself (soupk_time_next_launch -> hipExtLaunchKernelGGL), so
 they time the kernel exactly as rocprofv3's kernel trace does; launches go straight through
-the C ABI with preallocated buffers.  Three input sets per kernel rotate, and the other
-kernels of the step move > 600 MB between two launches of one kernel, so the 256 MB Infinity
-Cache does not serve its inputs.
+the C ABI with preallocated buffers.  Each kernel rotates through enough input sets that one
+rotation's inputs exceed twice the 256 MB Infinity Cache (rotation_sets), so no launch finds its
+inputs there: they come from HBM, as the roofline assumes.
 
 Prints ONE JSON line: value = the set's aggregate compulsory HBM bytes / summed kernel time
 (GB/s), per-kernel us / GB/s / fraction of the 8 TB/s peak, the roofline of the dominant kernel,
@@ -68,7 +68,21 @@ def p(t):
     return t.data_ptr() if t is not None else None
 
 
-def build_cases(dev, n_sets=3, lib=None):
+# Input bytes one rotation of a kernel's input sets spans: twice the 256 MB Infinity Cache
+# (MALL).  With a fixed three sets, the RoPE forward (whose loads allocate in the MALL) found
+# its 23 MB of inputs there and ran 5.6 us against 6.45 us from HBM.
+ROTATION_BYTES = 512 << 20
+
+
+def rotation_sets(in_bytes, n_sets=None):
+    """Number of input sets a kernel with `in_bytes` of input per launch rotates through:
+    `n_sets` if given (quick probes), else enough to span ROTATION_BYTES, at least 3."""
+    if n_sets is not None:
+        return n_sets
+    return max(3, -(-ROTATION_BYTES // in_bytes))
+
+
+def build_cases(dev, n_sets=None, lib=None):
     """The eight kernels at the step shape; `lib` selects the soupk library (default: the
     package's)."""
     cases = []
@@ -78,7 +92,7 @@ def build_cases(dev, n_sets=3, lib=None):
 
     # nf4_unpack: gate|up [17920, 1536]
     sets = []
-    for i in range(n_sets):
+    for i in range(rotation_sets(2 * I * H // 2 + 2 * I * H // 64, n_sets)):
         w = workloads.nf4_weight(2 * I, H, seed=1 + i, device=dev)
         st = w.quant_state
         out = torch.empty((2 * I, H), dtype=torch.float16, device=dev)
@@ -97,16 +111,20 @@ def build_cases(dev, n_sets=3, lib=None):
 
     # add + RMSNorm forward (delta, pad output) and backward at [2048, 1536]
     fsets, bsets = [], []
-    for i in range(n_sets):
+    n_f, n_b = rotation_sets(6 * M * H, n_sets), rotation_sets(14 * M * H, n_sets)
+    for i in range(max(n_f, n_b)):
         x, delta, w, pad_idx, padded = workloads.rmsnorm_inputs(M, H, M, seed=2 + 10 * i,
                                                                 device=dev)
         s = torch.empty_like(x)
         y = torch.empty((M, H), dtype=torch.float16, device=dev)
         ypad = torch.empty((M, H), dtype=torch.float32, device=dev)
         rstd = torch.empty(M, dtype=torch.float32, device=dev)
-        fsets.append(((x, delta, w, pad_idx, s, y, ypad, rstd),
-                      (p(x), p(delta), p(w), p(s), p(y), p(ypad), p(pad_idx), None, p(rstd), M, M,
-                       H, 1e-6)))
+        if i < n_f:
+            fsets.append(((x, delta, w, pad_idx, s, y, ypad, rstd),
+                          (p(x), p(delta), p(w), p(s), p(y), p(ypad), p(pad_idx), None, p(rstd),
+                           M, M, H, 1e-6)))
+        if i >= n_b:
+            continue
         dy, dypad, ds = workloads.rmsnorm_grads(M, H, M, seed=3 + 10 * i, device=dev)
         s_b = x + delta.float()
         rstd_b = torch.rsqrt(s_b.pow(2).mean(-1) + 1e-6)
@@ -135,15 +153,21 @@ def build_cases(dev, n_sets=3, lib=None):
     fsets, bsets = [], []
     cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
     W = (NH + 2 * NKV) * D
-    for i in range(n_sets):
+    # forward: qkv fp16 + fp32 LoRA deltas; backward: dq, dk, dv fp16
+    n_f = rotation_sets(M * W * 2 + M * (NH + NKV) * D * 4, n_sets)
+    n_b = rotation_sets(M * W * 2, n_sets)
+    for i in range(max(n_f, n_b)):
         qkv, lq, lv, pos = workloads.rope_inputs((T,) * B, T, NH, NKV, D, torch.float32,
                                                  seed=6 + 10 * i, device=dev)
-        q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
-        k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
-        v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
-        fsets.append(((qkv, lq, lv, pos, q, k, v),
-                      (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), None, p(q),
-                       p(k), p(v), M, B, T, NH, NKV, D)))
+        if i < n_f:
+            q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
+            k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+            v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+            fsets.append(((qkv, lq, lv, pos, q, k, v),
+                          (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), None,
+                           p(q), p(k), p(v), M, B, T, NH, NKV, D)))
+        if i >= n_b:
+            continue
         dq, dk, dv = workloads.rope_grads(B, T, NH, NKV, D, seed=7 + 10 * i, device=dev)
         dqkv = torch.empty((M, W), dtype=torch.float16, device=dev)
         bsets.append(((dq, dk, dv, pos, dqkv),
@@ -169,10 +193,11 @@ def build_cases(dev, n_sets=3, lib=None):
 
     # SwiGLU forward and in-place backward at [2048, 2 x 8960]
     fsets, bsets = [], []
-    for i in range(n_sets):
+    for i in range(rotation_sets(M * 2 * I * 2, n_sets)):
         gu = workloads.swiglu_inputs(M, I, seed=4 + 10 * i, device=dev)
         act = torch.empty((M, I), dtype=torch.float16, device=dev)
         fsets.append(((gu, act), (p(gu), p(act), M, I)))
+    for i in range(rotation_sets(M * 3 * I * 2, n_sets)):
         gu2 = workloads.swiglu_inputs(M, I, seed=5 + 10 * i, device=dev)
         dact = workloads.swiglu_grad(M, I, seed=5 + 10 * i, device=dev)
         bsets.append(((gu2, dact), (p(dact), p(gu2), M, I)))
@@ -194,7 +219,7 @@ def build_cases(dev, n_sets=3, lib=None):
     sets = []
     rows, V = 256, workloads.VOCAB
     n_lab = 0
-    for i in range(n_sets):
+    for i in range(rotation_sets(rows * V * 2, n_sets)):
         z, tgt = workloads.head_logits(rows, V, seed=8 + 10 * i, device=dev)
         ent = torch.empty(rows, dtype=torch.float32, device=dev)
         loss = torch.empty(rows, dtype=torch.float32, device=dev)
@@ -213,7 +238,7 @@ def build_cases(dev, n_sets=3, lib=None):
     return cases
 
 
-def build_extra_cases(dev, n_sets=3, lib=None):
+def build_extra_cases(dev, n_sets=None, lib=None):
     """HBM-bound kernels of the layer beyond the BASELINE set (reported apart, not in `value`):
     the one-launch NF4 unpack of a decoder layer's seven projections (soupk_nf4_unpack_multi,
     testt_amd.nf4.unpack_groups) and the split-K sum of the MLP's gate|up input gradient
@@ -224,7 +249,8 @@ def build_extra_cases(dev, n_sets=3, lib=None):
                         workloads.HEAD_DIM)
     shapes = [(NH * D, H), (NKV * D, H), (NKV * D, H), (H, NH * D), (I, H), (I, H), (H, I)]
     sets, nbytes = [], 0
-    for i in range(n_sets):
+    elems = sum(n * k for n, k in shapes)
+    for i in range(rotation_sets(elems // 2 + elems // 64, n_sets)):
         ws = [workloads.nf4_weight(n, k, seed=100 + 10 * i + j, device=dev)
               for j, (n, k) in enumerate(shapes)]
         plans = [nf4._plan(w, dev) for w in ws]
@@ -246,7 +272,7 @@ def build_extra_cases(dev, n_sets=3, lib=None):
     M, n_parts = workloads.BATCH * workloads.SEQ, 4
     n = M * H
     sets = []
-    for i in range(n_sets):
+    for i in range(rotation_sets(4 * n_parts * n, n_sets)):
         parts = torch.randn(n_parts, n, generator=workloads.gen(200 + i)).to(dev)
         out = torch.empty(n, dtype=torch.float16, device=dev)
         sets.append(((parts, out), (parts.data_ptr(), n_parts, n, n, out.data_ptr())))
@@ -272,11 +298,13 @@ def build_floor_cases(dev, n_sets=3, lib=None):
 RAGGED_LENGTHS = (512, 152, 128, 96)
 
 
-def build_shape_cases(dev, n_sets=3, lib=None):
+def build_shape_cases(dev, n_sets=None, lib=None):
     """Kernels of the set at the other shapes the step runs them at (reported apart, not in
     `value`): the RoPE pack forward / backward on the ragged batch RAGGED_LENGTHS (M = 888 real
     tokens of 4 x 512; the forward also writes the zeros of the 1160 pad positions, in the same
-    launch, as the reference's padded layout needs), and the vocab-head kernel on a 2048-row
+    launch, as the reference's padded layout needs); the token-major RoPE forward the layer
+    runs (soupk_rope_pack_tokens: rotated q, k and v + LoRA in qkv's own row layout, no pad
+    rows) on all 2048 tokens and on the ragged batch; and the vocab-head kernel on a 2048-row
     chunk (head.CHUNK_ROWS, the product's chunk) through soupk_head_stats_grad_rows, the entry
     FusedHeadLoss uses (gradient rows packed into their own buffer), 90% of rows labelled."""
     H, NH, NKV, D, B, T = (workloads.HIDDEN, workloads.N_HEADS, workloads.N_KV,
@@ -285,17 +313,23 @@ def build_shape_cases(dev, n_sets=3, lib=None):
     cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=dev)
     M = sum(RAGGED_LENGTHS)
     fsets, bsets = [], []
-    for i in range(n_sets):
+    # (the bytes read: the real positions' rows)
+    n_f = rotation_sets(M * W * 2 + M * (NH + NKV) * D * 4, n_sets)
+    n_b = rotation_sets(M * W * 2, n_sets)
+    for i in range(max(n_f, n_b)):
         qkv, lq, lv, pos = workloads.rope_inputs(RAGGED_LENGTHS, T, NH, NKV, D, torch.float32,
                                                  seed=60 + 10 * i, device=dev)
-        inv = torch.full((B * T,), -1, dtype=torch.int32, device=dev)
-        inv[pos] = torch.arange(M, dtype=torch.int32, device=dev)
-        q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
-        k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
-        v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
-        fsets.append(((qkv, lq, lv, pos, inv, q, k, v),
-                      (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), p(inv),
-                       p(q), p(k), p(v), M, B, T, NH, NKV, D)))
+        if i < n_f:
+            inv = torch.full((B * T,), -1, dtype=torch.int32, device=dev)
+            inv[pos] = torch.arange(M, dtype=torch.int32, device=dev)
+            q = torch.empty((B, NH, T, D), dtype=torch.float16, device=dev)
+            k = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+            v = torch.empty((B, NKV, T, D), dtype=torch.float16, device=dev)
+            fsets.append(((qkv, lq, lv, pos, inv, q, k, v),
+                          (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), p(inv),
+                           p(q), p(k), p(v), M, B, T, NH, NKV, D)))
+        if i >= n_b:
+            continue
         dq, dk, dv = workloads.rope_grads(B, T, NH, NKV, D, seed=70 + 10 * i, device=dev)
         dqkv = torch.empty((M, W), dtype=torch.float16, device=dev)
         bsets.append(((dq, dk, dv, pos, dqkv),
@@ -309,9 +343,23 @@ def build_shape_cases(dev, n_sets=3, lib=None):
              fsets, lib=lib),
         Case("rope_pack_bwd_ragged888", "rope_pack_bwd_kernel", "soupk_rope_pack_bwd",
              M * W * 2 + tab + 8 * M + M * W * 2, bsets, lib=lib)]
+    for lengths, name in (((T,) * B, "rope_pack_tokens"),
+                          (RAGGED_LENGTHS, "rope_pack_tokens_ragged888")):
+        rows = sum(lengths)
+        tsets = []
+        for i in range(rotation_sets(rows * W * 2 + rows * (NH + NKV) * D * 4, n_sets)):
+            qkv, lq, lv, pos = workloads.rope_inputs(lengths, T, NH, NKV, D, torch.float32,
+                                                     seed=90 + 10 * i, device=dev)
+            out = torch.empty((rows, W), dtype=torch.float16, device=dev)
+            tsets.append(((qkv, lq, lv, pos, out),
+                          (p(qkv), p(lq), p(lv), _ext.DTYPE_F32, p(cos), p(sin), p(pos), p(out),
+                           rows, B, T, NH, NKV, D)))
+        cases.append(Case(name, "rope_pack_fwd_kernel", "soupk_rope_pack_tokens",
+                          rows * W * 2 + rows * (NH + NKV) * D * 4 + tab + 8 * rows
+                          + rows * W * 2, tsets, lib=lib))
     rows, V = 2048, workloads.VOCAB
     sets, n_lab = [], 0
-    for i in range(n_sets):
+    for i in range(rotation_sets(rows * V * 2, n_sets)):
         g = torch.Generator(device=dev).manual_seed(80 + i)
         z = (0.784 * torch.randn(rows, V, generator=g, device=dev)).to(torch.float16)
         tgt = torch.randint(0, V, (rows,), generator=g, device=dev)
@@ -1289,6 +1337,7 @@ def main():
         kernels[c.name] = {"kernel": c.kernel, "us_mean": round(mean_us, 3),
                            "us_median": round(median(c.times), 3),
                            "us_min": round(min(c.times), 3), "bytes": c.nbytes,
+                           "input_sets": len(c.sets),
                            "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
                            "copy_us": round(copy_us[c.name], 3),
                            "copy_over_kernel": round(copy_us[c.name] / mean_us, 3)}
@@ -1301,6 +1350,7 @@ def main():
         gbps = c.nbytes / (mean_us * 1e-6) / 1e9
         beyond[c.name] = {"kernel": c.kernel, "us_mean": round(mean_us, 3),
                           "us_median": round(median(c.times), 3), "bytes": c.nbytes,
+                          "input_sets": len(c.sets),
                           "GBps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
         log(f"{c.name:16s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
             f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s  (beyond the set)")
@@ -1311,7 +1361,7 @@ def main():
         other_shapes[c.name] = {"kernel": c.kernel, "entry": c.entry,
                                 "us_mean": round(mean_us, 3),
                                 "us_median": round(median(c.times), 3), "bytes": c.nbytes,
-                                "GBps": round(gbps, 1),
+                                "input_sets": len(c.sets), "GBps": round(gbps, 1),
                                 "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
         log(f"{c.name:24s} {mean_us:8.2f} us  {gbps:8.1f} GB/s  "
             f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% of 8 TB/s")

@@ -28,13 +28,15 @@ namespace {
 
 constexpr int kRopeThreads = 256;
 // Cache policy of the loads per direction (1 = non-temporal), chosen by measurement on MI355X
-// at 2048 tokens: the forward pass is fastest with cached loads (5.9 us against 6.7 with
-// non-temporal ones; cached stores were slower still and also slowed the backward pass that
-// follows), the backward pass with non-temporal ones.  Results are written with streaming
-// stores (StreamOut: nt | sc1).  The cos/sin tables, shared by every token at a position, are
-// always read cached.
+// at 2048 tokens: every input is read once, and non-temporal loads are used both ways.  With
+// inputs read from HBM, the forward pass takes as long with cached loads (6.62 us against 6.65),
+// and the 23 MB they leave in the caches slowed the kernels launched after it (the NF4 unpack
+// 11.7 us against 11.2, the add+RMSNorm forward 8.6 against 8.2); cached loads only looked
+// faster (5.6 us) when the same inputs were re-read out of the Infinity Cache.  Results are
+// written with streaming stores (StreamOut: nt | sc1).  The cos/sin tables, shared by every
+// token at a position, are always read cached.
 #ifndef SOUPK_ROPE_NT_FWD_LD
-#define SOUPK_ROPE_NT_FWD_LD 0
+#define SOUPK_ROPE_NT_FWD_LD 1
 #endif
 #ifndef SOUPK_ROPE_NT_FWD_LORA_LD
 #define SOUPK_ROPE_NT_FWD_LORA_LD SOUPK_ROPE_NT_FWD_LD
