@@ -1,6 +1,6 @@
 """CPU: bench.py's rocprofv3 summarizers on small synthetic CSVs -- launches grouped by kernel
 and grid, each bench entry matched to its own group, the PMC traffic scaled by the 1 GiB copy
-and read back by the roofline's lookup."""
+and read back by the roofline's lookup -- and the input-set rotation rule of its timing."""
 
 import csv
 import json
@@ -88,3 +88,13 @@ def test_trace_summary_groups_every_kernel(tmp_path):
     assert lines[1].startswith("| `Cijk_Ailk_Bljk_HHS_BH_MT256x256x64` | 1024 / 256 | 1 | 18.00")
     assert lines[2].startswith("| `gemm_tn_kernel<false>` | 1024 / 256 | 1 | 7.00")
     assert lines[3].startswith("| `gemm_tn_kernel<false>` | 65536 / 256 | 1 | 9.00")
+
+
+def test_rotation_sets_span_twice_the_infinity_cache():
+    """Every timed kernel rotates through input sets whose inputs add up to at least 512 MB
+    (twice the 256 MB Infinity Cache), and through at least 3; an explicit count overrides."""
+    for in_bytes in (3_637_248, 8_388_608, 23_068_672, 77_791_232, 110_100_480, 622_329_856):
+        n = bench.rotation_sets(in_bytes)
+        assert n >= 3 and n * in_bytes >= bench.ROTATION_BYTES == 512 << 20
+        assert n == 3 or (n - 1) * in_bytes < bench.ROTATION_BYTES      # no more than needed
+    assert bench.rotation_sets(8_388_608, n_sets=2) == 2
