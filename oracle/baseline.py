@@ -3,9 +3,9 @@ baseline.  TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): timed beside the G
 never shipped.
 
 Each function computes what the corresponding kernel produces, the way base Soup's eager path
-does: bitsandbytes-style dequant (numpy fp32, oracle.nf4), Qwen2RMSNorm
-+ autograd, index_copy + apply_rotary_pos_emb + autograd, silu * up + autograd, and
-log_softmax / argmax / softmax - onehot over fp32-cast logits.
+does: bitsandbytes-style dequant (numpy fp32, oracle.nf4), Qwen2RMSNorm + autograd,
+index_copy + apply_rotary_pos_emb + autograd, silu * up + autograd, and log_softmax / argmax /
+softmax - onehot over fp32-cast logits.
 """
 
 import torch
