@@ -1,21 +1,23 @@
 """CPU regression test: the RoPE pack kernels' per-thread index arithmetic stays in bounds.
 
-testt_amd/csrc/rope_pack.hip maps 256-thread workgroups onto (token, head, 8-dim chunk) items.
-When the item count is not a multiple of 256, the last workgroup holds threads past the last
-item; they must form only in-bounds addresses (they take the last item's indices).  This test
-replays that arithmetic for every thread of the launch grid with numpy and checks each global
-and LDS index against its buffer, for the GPU tests' shapes (including 53 tokens = 26.5
-workgroups) and head counts other than Qwen2.5-1.5B's.  No GPU is needed.
+testt_amd/csrc/rope_pack.hip maps workgroups of 512 (forward) and 256 (backward) threads onto
+(token, head, 8-dim chunk) items.  When the item count is not a multiple of the workgroup size,
+the last workgroup holds threads past the last item; they must form only in-bounds addresses
+(they take the last item's indices).  This test replays that arithmetic for every thread of the
+launch grid with numpy, at both workgroup sizes, and checks each global and LDS index against
+its buffer, for the GPU tests' shapes (including 53 tokens, a fraction of a workgroup) and head
+counts other than Qwen2.5-1.5B's.  No GPU is needed.
 """
 
 import numpy as np
 import pytest
 
-THREADS = 256
-MAX_TOK = 16          # kRopeMaxTok: tokens whose cos/sin rows one workgroup stages in LDS
+def max_tok(threads):
+    """rope_max_tok<THREADS>(): tokens whose cos/sin rows one workgroup stages in LDS."""
+    return threads // 18 + 2
 
 
-def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
+def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv, THREADS):
     """Largest index each buffer is touched at, for the forward and backward vector kernels."""
     HALF = D // 2
     heads = NH + 2 * NKV
@@ -46,7 +48,7 @@ def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
         if v.any():
             lv = tok * NKV * D + (h - NH - NKV) * D + 8 * c + HALF + 7
             worst["lv"] = max(worst["lv"], int(lv[v].max()))
-        # table staging: i = tid, tid + 256, ... < ntok * D/2 float4; entry i is float4
+        # table staging: i = tid, tid + THREADS, ... < ntok * D/2 float4; entry i is float4
         # i % (D/2) of token tok0 + i // (D/2)'s row (cos, then sin), at t = pos % T
         stage = np.arange(0, ntok * (D // 2))
         worst["pos"] = max(worst["pos"], int(tok0 + stage.max() // (D // 2)), int(tok.max()))
@@ -89,16 +91,18 @@ def _fwd_bwd_addresses(rows, B, T, NH, NKV, D, with_inv):
     return worst
 
 
+@pytest.mark.parametrize("threads", [512, 256])
 @pytest.mark.parametrize("heads", [(12, 2), (1, 1), (3, 0), (28, 4)])
 @pytest.mark.parametrize("lengths,seq", [((512,) * 4, 512), ((512, 152, 128, 96), 512),
                                          ((77, 75), 77), ((40, 0, 13), 64), ((30, 20), 32),
                                          ((1,), 1), ((3, 0, 0), 4)])
-def test_rope_vector_kernels_stay_in_bounds(lengths, seq, heads):
+def test_rope_vector_kernels_stay_in_bounds(lengths, seq, heads, threads):
     NH, NKV = heads
     D = 128
     B = len(lengths)
     rows = sum(lengths)
-    w = _fwd_bwd_addresses(rows, B, seq, NH, NKV, D, with_inv=rows != B * seq)
+    w = _fwd_bwd_addresses(rows, B, seq, NH, NKV, D, rows != B * seq, threads)
+    MAX_TOK = max_tok(threads)
     assert w["ntok"] <= MAX_TOK
     assert w["qkv"] < rows * (NH + 2 * NKV) * D
     assert w["lq"] < rows * NH * D and w["lv"] < rows * NKV * D

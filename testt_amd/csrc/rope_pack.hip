@@ -26,7 +26,14 @@
 namespace soupk {
 namespace {
 
+// Workgroup sizes: the vector forward kernels take 512 items (4 tokens of Qwen2.5-1.5B's 16
+// heads x 8 chunks) per workgroup, the backward and generic kernels 256.  Measured on MI355X
+// with HBM-resident inputs at 2048 tokens / the ragged 888: the padded forward 6.58 -> 6.45 us,
+// ragged 5.84 -> 5.65 us, the token-major forward 6.4-6.6 -> 6.34 us, ragged 4.2 -> 4.06 us;
+// 256 or 1024 were slower (1024 badly so on the ragged batch: 7.05 us), and the backward kept
+// 256 (4.25 against 4.28 us with 512).
 constexpr int kRopeThreads = 256;
+constexpr int kRopeFwdThreads = 512;
 // Cache policy of the loads per direction (1 = non-temporal), chosen by measurement on MI355X
 // at 2048 tokens: every input is read once, and non-temporal loads are used both ways.  With
 // inputs read from HBM, the forward pass takes as long with cached loads (6.62 us against 6.65),
@@ -115,11 +122,15 @@ struct PackedOut {
   }
 };
 // The cos/sin rows of the tokens a workgroup touches are staged once in LDS (per token 2*D fp32:
-// cos then sin), instead of every thread reading its 4 x 32 bytes of them from L1/L2.  A
-// workgroup's 256 items span at most kRopeMaxTok tokens (the host checks items per token).
-constexpr int kRopeMaxTok = 16;
+// cos then sin), instead of every thread reading its 4 x 32 bytes of them from L1/L2.  With at
+// least 18 items per token (the host's condition) a workgroup of THREADS consecutive items
+// spans at most ceil((THREADS - 1) / 18) + 1 <= THREADS / 18 + 2 tokens.
+template <int THREADS>
+constexpr int rope_max_tok() {
+  return THREADS / 18 + 2;
+}
 
-template <int HALF>
+template <int HALF, int THREADS>
 __device__ __forceinline__ int stage_tables(f32x4* tab, const float* __restrict__ cos_t,
                                             const float* __restrict__ sin_t,
                                             const int64_t* __restrict__ pos, uint32_t tok0,
@@ -127,7 +138,7 @@ __device__ __forceinline__ int stage_tables(f32x4* tab, const float* __restrict_
   constexpr int D = 2 * HALF;
   constexpr int Q = D / 4;  // float4 per table row
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
-  for (int i = threadIdx.x; i < static_cast<int>(ntok) * 2 * Q; i += kRopeThreads) {
+  for (int i = threadIdx.x; i < static_cast<int>(ntok) * 2 * Q; i += THREADS) {
     const int j = i / (2 * Q), q = i % (2 * Q);
     const int64_t p = pos[tok0 + j];
     int b = 0, t = 0;  // (row 0 for an invalid position: the host guarantees T >= 1)
@@ -151,7 +162,7 @@ __device__ __forceinline__ void lds8(const f32x4* p, float* v) {
 // the form the varlen attention reads; k and v are unused and a token whose position has no
 // place (outside [0, B*T)) gets a row of zeros.
 template <int HALF, bool TOKENS>
-__global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
+__global__ __launch_bounds__(kRopeFwdThreads) void rope_pack_fwd_kernel(
     const uint16_t* __restrict__ qkv, const void* __restrict__ lora_q,
     const void* __restrict__ lora_v, int lora_f32, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
@@ -159,12 +170,12 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     uint16_t* __restrict__ v, int64_t rows, RopeDims dm, int64_t tok_blocks) {
   constexpr int D = 2 * HALF;
   constexpr int CPH = HALF / 8;  // items per head
-  __shared__ f32x4 tab[kRopeMaxTok * D / 2];
+  __shared__ f32x4 tab[rope_max_tok<kRopeFwdThreads>() * D / 2];
   const int heads = dm.NH + 2 * dm.NKV;
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
   if (!TOKENS && static_cast<int64_t>(blockIdx.x) >= tok_blocks) {
     // Zero the padded positions with no token.
-    const uint32_t g = (blockIdx.x - static_cast<uint32_t>(tok_blocks)) * kRopeThreads +
+    const uint32_t g = (blockIdx.x - static_cast<uint32_t>(tok_blocks)) * kRopeFwdThreads +
                        threadIdx.x;
     const uint32_t p = dm.per_tok.div(g);
     if (p >= slots || pos_inv[p] >= 0) return;
@@ -176,10 +187,10 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
     PackedOut(q, k, v, dm, std::integral_constant<int, D>()).store<D>(h, b, t, c, z, z);
     return;
   }
-  const uint32_t g0 = blockIdx.x * kRopeThreads;
+  const uint32_t g0 = blockIdx.x * kRopeFwdThreads;
   const uint32_t total = static_cast<uint32_t>(rows) * dm.items;
   const uint32_t tok0 = dm.per_tok.div(g0);
-  const uint32_t ntok = dm.per_tok.div(min(g0 + kRopeThreads, total) - 1) - tok0 + 1;
+  const uint32_t ntok = dm.per_tok.div(min(g0 + kRopeFwdThreads, total) - 1) - tok0 + 1;
   // Threads past the last item take the last item's indices (so every address they form is in
   // bounds), help stage the tables, and leave after the barrier.
   const bool active = g0 + threadIdx.x < total;
@@ -209,7 +220,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_fwd_kernel(
       load8_h<kFwdLoraNtLd>(static_cast<const uint16_t*>(lora) + off + HALF, l2);
     }
   }
-  const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
+  const int per = stage_tables<HALF, kRopeFwdThreads>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
   __syncthreads();
   if (!active) return;
   // (token-major rows: one descriptor over the whole output; the host keeps it < 2^32 bytes)
@@ -265,7 +276,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
     uint16_t* __restrict__ dqkv, int64_t rows, RopeDims dm) {
   constexpr int D = 2 * HALF;
   constexpr int CPH = HALF / 8;
-  __shared__ f32x4 tab[kRopeMaxTok * D / 2];
+  __shared__ f32x4 tab[rope_max_tok<kRopeThreads>() * D / 2];
   const int heads = dm.NH + 2 * dm.NKV;
   const int64_t slots = static_cast<int64_t>(dm.B) * dm.T;
   const uint32_t g0 = blockIdx.x * kRopeThreads;
@@ -296,7 +307,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_pack_bwd_kernel(
     load8_h<kBwdNtLd>(src + base + 8 * c, g1);
     load8_h<kBwdNtLd>(src + base + HALF + 8 * c, g2);
   }
-  const int per = stage_tables<HALF>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
+  const int per = stage_tables<HALF, kRopeThreads>(tab, cos_t, sin_t, pos, tok0, ntok, dm);
   __syncthreads();
   if (!active) return;
   // Streaming stores through one descriptor over dqkv (the host keeps it below 2^32 bytes).
@@ -460,7 +471,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
   const int half = D / 2;
   const int heads = NH + 2 * NKV;
   const int lora_align = 16;
-  // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens)
+  // (items per token >= 18: a workgroup's items span at most rope_max_tok() tokens)
   // (the stores address q, k and v with 32-bit byte offsets)
   const bool vec = half == 64 && heads * (half / 8) >= 18 && slots < (int64_t{1} << 31) &&
                    slots * (NH > NKV ? NH : NKV) * D * 2 < (int64_t{1} << 32) &&
@@ -476,10 +487,10 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_fwd(
     const int64_t tok_items = rows * dm.items;
     const int64_t zero_items = zero_slots * dm.items;
     if (tok_items + zero_items >= (int64_t{1} << 31)) return kInvalid;
-    const int64_t tok_blocks = (tok_items + kRopeThreads - 1) / kRopeThreads;
-    const int64_t blocks = tok_blocks + (zero_items + kRopeThreads - 1) / kRopeThreads;
+    const int64_t tok_blocks = (tok_items + kRopeFwdThreads - 1) / kRopeFwdThreads;
+    const int64_t blocks = tok_blocks + (zero_items + kRopeFwdThreads - 1) / kRopeFwdThreads;
     return launch_kernel(rope_pack_fwd_kernel<64, false>, dim3(static_cast<unsigned>(blocks)),
-                         dim3(kRopeThreads), st, qkv, lora_q, lora_v,
+                         dim3(kRopeFwdThreads), st, qkv, lora_q, lora_v,
                          static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos, pos_inv,
                          q, k, v, rows, dm, tok_blocks);
   }
@@ -545,7 +556,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_tokens(
   if (rows == 0 || heads == 0) return kOk;
   const int64_t slots = static_cast<int64_t>(B) * T;
   if (!qkv || !pos || !out || !cos || !sin || T < 1) return kInvalid;
-  // (items per token >= 18: a workgroup's 256 items span at most kRopeMaxTok tokens; the
+  // (items per token >= 18: a workgroup's items span at most rope_max_tok() tokens; the
   // stores address `out` with 32-bit byte offsets)
   if (heads * 8 < 18 || slots >= (int64_t{1} << 31) || rows * heads * D * 2 >= (int64_t{1} << 32))
     return kInvalid;
@@ -559,9 +570,9 @@ extern "C" __attribute__((visibility("default"))) int soupk_rope_pack_tokens(
   dm.per_seq = FastDiv(static_cast<uint32_t>(T));
   const int64_t items = rows * dm.items;
   if (items >= (int64_t{1} << 31)) return kInvalid;
-  const int64_t blocks = (items + kRopeThreads - 1) / kRopeThreads;
+  const int64_t blocks = (items + kRopeFwdThreads - 1) / kRopeFwdThreads;
   return launch_kernel(rope_pack_fwd_kernel<64, true>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kRopeThreads), static_cast<hipStream_t>(stream), qkv, lora_q, lora_v,
+                       dim3(kRopeFwdThreads), static_cast<hipStream_t>(stream), qkv, lora_q, lora_v,
                        static_cast<int>(lora_dtype == SOUPK_DTYPE_F32), cos, sin, pos,
                        static_cast<const int32_t*>(nullptr), out, static_cast<uint16_t*>(nullptr),
                        static_cast<uint16_t*>(nullptr), rows, dm, blocks);
