@@ -23,6 +23,8 @@ CASES = [  # lengths, seq, nh, nkv, d, theta, lora dtype (None: no LoRA)
     ((512, 152, 128, 96), 512, 12, 2, 128, 1e6, torch.float16),
     ((77, 75), 77, 12, 2, 128, 1e4, torch.float16),          # the reference's test shape
     ((40, 0, 13), 64, 12, 2, 128, 1e6, None),
+    ((37, 20), 40, 1, 1, 128, 1e4, torch.float32),            # 24 items/token: ~21 tokens per
+    ((53,), 64, 2, 1, 128, 1e6, torch.float16),               # forward workgroup, partial tail
     ((5, 3), 5, 3, 1, 8, 1e4, torch.float16),                 # head_dim 8: generic kernel
     ((6, 2), 7, 2, 1, 6, 1e4, torch.float32),                 # head_dim 6: generic kernel
 ]
