@@ -778,27 +778,35 @@ def time_nf4_gemm(dev, calls=40):
 
 
 def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
-    """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model (testt_amd/model.py: 28
-    decoder layers, final norm, the chunked fused head loss over the 151,936-token vocabulary)
-    at B=4 x T=512 = 2048 real tokens, prompt tokens unlabelled: forward and forward+backward
-    time per step on the GPU (a torch event pair around each step).  With reference_profile,
-    the reference's work profile: gate|up recomputed and the NF4 weights unpacked again in
-    backward, and the head in the reference's 256-row chunks (head.CHUNK_ROWS = 256)."""
+    """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model at B=4 x T=512 = 2048
+    real tokens, prompt tokens unlabelled, through the model-level drop-in the reference's
+    trainer patch calls (solution/trainer_patch.py:57-63): a transformers Qwen2ForCausalLM with
+    4-bit projections and LoRA r=16 on q/v (workloads.qwen2_qlora), `can_run` and then
+    `fused_forward(model, input_ids, attention_mask, labels, num_items_in_batch)` under fp16
+    autocast (28 decoder layers, final norm, the chunked fused head loss over the
+    151,936-token vocabulary): forward and forward+backward time per step on the GPU (a torch
+    event pair around each step).  With reference_profile, the reference's work profile:
+    gate|up recomputed and the NF4 weights unpacked again in backward, and the head in the
+    reference's 256-row chunks (head.CHUNK_ROWS = 256)."""
     from testt_amd import head, mlp, model, nf4
 
     B, T = workloads.BATCH, workloads.SEQ
-    m = model.synthetic_model(dev, n_layers=n_layers)
+    hf = workloads.qwen2_qlora(dev, n_layers=n_layers)
     g = workloads.gen(12)
     ids = torch.randint(0, workloads.VOCAB, (B, T), generator=g).to(dev)
     mask = torch.ones(B, T, dtype=torch.int64, device=dev)
     labels = ids.clone()
     labels[:, :T // 4] = -100                        # prompt tokens carry no label
-    params = model.lora_parameters(m)
+    params = workloads.lora_parameters(hf)
+    with torch.autocast("cuda", dtype=torch.float16):
+        if not model.can_run(hf, ids, mask, labels, {"num_items_in_batch": None}):
+            raise RuntimeError("the fused path does not take the benchmark model")
 
     def step(backward):
         for q in params:
             q.grad = None
-        loss, _ = model.fused_forward(m, ids, mask, labels)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = model.fused_forward(hf, ids, mask, labels, None).loss
         if backward:
             loss.backward()
 
@@ -820,13 +828,15 @@ def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
     out.update(tokens=B * T, batch=B, seq=T, layers=n_layers,
                tokens_per_s=round(B * T / (out["fwd_bwd_ms"] * 1e-3), 1),
                tokens_per_s_median=round(B * T / (out["fwd_bwd_ms_median"] * 1e-3), 1))
-    out["note"] = ("synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v; hipBLASLt "
-                   "GEMMs in fp16, every other op (attention included) a soupk kernel; backward "
+    out["note"] = ("model.fused_forward on a transformers Qwen2ForCausalLM under fp16 autocast "
+                   "(synthetic NF4 weights and fp16 tied embedding, LoRA r=16 on q/v); "
+                   "hipBLASLt GEMMs in fp16, every other op (attention included) a soupk "
+                   "kernel; backward "
                    "on the calling thread (testt_amd.configure_backward, as apply() sets it)"
                    + ("; the reference's work profile: RECOMPUTE_GATE_UP = True, "
                       "KEEP_UNPACKED_FOR_BACKWARD = False, CHUNK_ROWS = 256"
                       if reference_profile else ""))
-    del m
+    del hf
     return out
 
 

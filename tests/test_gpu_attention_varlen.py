@@ -234,3 +234,104 @@ def test_varlen_backward_rejects_mismatched_inputs():
     for change in bad:
         with pytest.raises((ValueError, TypeError)):
             attention.attention_varlen_bwd(**{**good, **change})
+
+
+def _rope32(x, cos_t, sin_t, heads):
+    """float32 rotation of [M, heads*D] rows by per-token tables [M, D] (rotate_half form)."""
+    M = x.shape[0]
+    h = x.view(M, heads, D)
+    rot = torch.cat([-h[..., D // 2:], h[..., :D // 2]], dim=-1)
+    return (h * cos_t[:, None] + rot * sin_t[:, None]).reshape(M, heads * D)
+
+
+def _reference_rope_attention(qkv, lq, lv, cos, sin, pos, mask, NH, NKV, dout, scale):
+    """float32 (CPU) RoPE + causal GQA attention over the padded layout with the key-padding
+    mask of `mask`, gathered at the real tokens, and its gradients for qkv, lq, lv."""
+    B, T = mask.shape
+    M = pos.numel()
+    leaves = [t.detach().cpu().float().requires_grad_(True) for t in (qkv, lq, lv)]
+    x, lq32, lv32 = leaves
+    pos = pos.cpu()
+    tt = pos % T
+    c, s = cos.cpu()[tt], sin.cpu()[tt]
+    q = _rope32(x[:, :NH * D] + lq32, c, s, NH)
+    k = _rope32(x[:, NH * D:(NH + NKV) * D], c, s, NKV)
+    v = x[:, (NH + NKV) * D:] + lv32
+
+    def padded(rows, heads):
+        flat = torch.zeros(B * T, heads * D).index_copy(0, pos, rows)
+        return flat.view(B, T, heads, D).transpose(1, 2)
+
+    qp, kp, vp = padded(q, NH), padded(k, NKV), padded(v, NKV)
+    rep = NH // NKV
+    kp, vp = kp.repeat_interleave(rep, 1), vp.repeat_interleave(rep, 1)
+    allowed = torch.ones(T, T, dtype=torch.bool).tril()[None, None] & \
+        mask.cpu().bool()[:, None, None, :]
+    allowed = allowed | torch.eye(T, dtype=torch.bool)[None, None]   # pad queries: finite rows
+    sc = (qp @ kp.transpose(-1, -2)) * scale
+    p = torch.softmax(sc.masked_fill(~allowed, float("-inf")), -1)
+    out = (p @ vp).transpose(1, 2).reshape(B * T, NH * D)[pos]
+    out.backward(dout.detach().cpu().float())
+    return out.detach(), [t.grad for t in leaves]
+
+
+def _mask(kind, B, T):
+    m = torch.zeros(B, T, dtype=torch.int64)
+    if kind == "left":          # the BASELINE ragged lengths, left-aligned (prompt padding)
+        for b, n in enumerate((512, 152, 128, 96)[:B]):
+            m[b, T - n:] = 1
+    else:                       # pads inside rows, at both ends and in runs of several lengths
+        m[0, 20:] = 1
+        m[1, :10] = 1
+        m[1, 30:61] = 1
+        m[2] = (torch.arange(T) % 3 != 1).long()
+        m[3, 5:6] = 1
+    return m.to(DEV)
+
+
+@pytest.mark.parametrize("kind,T", [("left", 512), ("gaps", 77)])
+def test_rope_attention_left_padding_and_gaps(kind, T):
+    """Masks whose real tokens are not a prefix of each row: left padding (TRL's padded
+    prompts) and pads between real tokens.  The varlen path attends within each row's real
+    tokens in index order (= position order); RoPE uses the tokens' true positions.  Against
+    the padded path (RopePack -> causal attention with the key flags -> gather) and the float32
+    reference: outputs within 2e-3 absolute, the qkv / LoRA gradients within 1e-2 relative
+    (L2 norm)."""
+    NH, NKV, B = 12, 2, 4
+    mask = _mask(kind, B, T)
+    pos = mask.reshape(-1).nonzero().squeeze(1)
+    M = pos.numel()
+    print(f"rope attention {kind} mask T={T} M={M}", flush=True)
+    g = torch.Generator().manual_seed(17 + T)
+    width = (NH + 2 * NKV) * D
+    qkv = torch.randn(M, width, generator=g).to(torch.float16).to(DEV)
+    lq = (1e-2 * torch.randn(M, NH * D, generator=g)).to(torch.float16).to(DEV)
+    lv = (1e-2 * torch.randn(M, NKV * D, generator=g)).to(torch.float16).to(DEV)
+    dout = torch.randn(M, NH * D, generator=g).to(torch.float16).to(DEV)
+    cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=DEV)
+    cu = attention.cu_seqlens_of(pos, B, T)
+    assert cu.tolist() == [0] + mask.sum(1).cumsum(0).tolist()
+    scale = 1.0 / math.sqrt(D)
+
+    leaves_a = [t.clone().requires_grad_(True) for t in (qkv, lq, lv)]
+    out_a = attention.rope_attention(*leaves_a, cos, sin, pos, cu, B, T, NH, NKV)
+    out_a.backward(dout)
+
+    leaves_b = [t.clone().requires_grad_(True) for t in (qkv, lq, lv)]
+    q, k, v = rope.rope_pack(*leaves_b, cos, sin, pos, B, T, NH, NKV, D)
+    key_valid = (mask != 0).to(torch.uint8).contiguous()
+    out_b = attention.causal_attention(q, k, v, key_valid).index_select(0, pos)
+    out_b.backward(dout)
+
+    r_out, r_grads = _reference_rope_attention(qkv, lq, lv, cos, sin, pos, mask, NH, NKV,
+                                               dout, scale)
+    err_ref = (out_a.detach().cpu().float() - r_out).abs().max().item()
+    err_pad = (out_a.detach().float() - out_b.detach().float()).abs().max().item()
+    print(f"  max |out - fp32| = {err_ref:.2e}, |varlen - padded| = {err_pad:.2e}", flush=True)
+    assert err_ref < 2e-3 and err_pad < 2e-3
+    for name, a, b, r in zip(("qkv", "lora_q", "lora_v"), leaves_a, leaves_b, r_grads):
+        ga = a.grad.cpu().float()
+        rel_ref = float((ga - r).norm() / r.norm())
+        rel_pad = float((ga - b.grad.cpu().float()).norm() / b.grad.cpu().float().norm())
+        print(f"  grad {name}: rel to fp32 {rel_ref:.1e}, to padded {rel_pad:.1e}", flush=True)
+        assert rel_ref < 1e-2 and rel_pad < 1e-2, name

@@ -1,16 +1,25 @@
-"""GPU: the fused training step (testt_amd/model.py, solution/model.py:209-279) against the
-unpatched transformers Qwen2ForCausalLM on a small random 4-bit Qwen2 + LoRA: loss, every LoRA
-gradient, TRL's entropy and accuracy, and Soup's per-row rewind losses, with the tolerances of
-the reference's own step test (solution/test_model.py:115-127).
+"""GPU: the model-level drop-in (testt_amd/model.py: model_plan, can_run, fused_forward on the
+causal LM itself, solution/model.py:152-279) against the unpatched transformers
+Qwen2ForCausalLM on a small random 4-bit Qwen2 + LoRA: loss, every LoRA gradient, TRL's entropy
+and accuracy, and Soup's per-row rewind losses, with the tolerances of the reference's own step
+test (solution/test_model.py:115-127).
+
+The fused side is reached exactly as the reference's trainer patch reaches it
+(solution/trainer_patch.py:57-63): `can_run(model, input_ids, attention_mask, labels, kwargs)`
+and then `fused_forward(model, input_ids, attention_mask, labels,
+kwargs.get("num_items_in_batch"))`, whose output's `logits` is the HeadStats.
 
 The reference builds the model with bitsandbytes + peft (solution/test_model.py:23-57); neither
-is installed here, so the setup reproduces what they do: the fp16 checkpoint's projections are
-quantized to NF4 double-quant (the oracle's bitsandbytes restatement), the unpatched model runs
-with exactly the dequantized fp16 weights (what Linear4bit computes with under fp16 autocast),
-every other parameter in fp32 (prepare_model_for_kbit_training), and LoRA r=16 on q_proj/v_proj
-is a wrapper computing peft's `base(x) + B(A(dropout(x))) * scaling`, dropout drawn on the same
-[batch, seq, hidden] fp32 input in the same order.  The unpatched side's metrics are computed
-from its logits as TRL's entropy_from_logits and Soup's rewind row_losses define them."""
+is installed here, so the setup reproduces what they leave: every projection a 4-bit module
+(workloads.Linear4bit: the NF4 double-quant weight with its quant_state, quantized by the
+oracle's bitsandbytes restatement from the fp16 checkpoint, and the dequantized fp16 values its
+own forward computes with, as Linear4bit does under fp16 autocast), every other parameter in
+fp32 (prepare_model_for_kbit_training), and peft's LoRA Linear on q_proj/v_proj
+(workloads.LoraLinear: lora_A / lora_B / lora_dropout ModuleDicts, `base(x) +
+B(A(dropout(x))) * scaling`), dropout drawn on the same [batch, seq, hidden] fp32 input in the
+same order.  The unpatched side's metrics are computed from its logits as TRL's
+entropy_from_logits and Soup's rewind row_losses define them.  Attention masks: right padding
+(the reference's test), and left padding with a gap inside a row."""
 
 import math
 
@@ -28,23 +37,6 @@ DEV = torch.device("cuda")
 RANK, ALPHA = 16, 32
 
 
-class LoraWrap(torch.nn.Module):
-    """peft's LoRA Linear forward: base_layer(x) + lora_B(lora_A(dropout(x))) * scaling."""
-
-    def __init__(self, base, a, b, scaling, p):
-        super().__init__()
-        self.base_layer, self.a, self.b, self.scaling, self.p = base, a, b, scaling, p
-
-    def get_base_layer(self):
-        return self.base_layer
-
-    def forward(self, x):
-        out = self.base_layer(x)
-        d = torch.nn.functional.dropout(x.to(self.a.dtype), self.p, training=self.training)
-        return out + torch.nn.functional.linear(torch.nn.functional.linear(d, self.a),
-                                                self.b) * self.scaling
-
-
 def nf4_of(w16, seed):
     """Params4bit-like NF4 double-quant weight of an fp16 [n_out, n_in] array, and its dequantized
     fp16 values."""
@@ -60,13 +52,13 @@ def nf4_of(w16, seed):
 
 
 def build(dropout, hidden=256):
-    from transformers import Qwen2Config, Qwen2ForCausalLM
+    """A 2-layer Qwen2ForCausalLM (4 heads, 2 KV heads: head dim 64 at hidden 256, which runs
+    torch SDPA; 128 at hidden 512, the HIP attention) with 4-bit projections and LoRA r=16 on
+    q/v; returns the model and its LoRA modules."""
+    from transformers import Qwen2ForCausalLM
 
-    # 4 heads: hidden 256 gives head dim 64 (torch SDPA), 512 head dim 128 (the HIP attention)
-    cfg = Qwen2Config(vocab_size=1000, hidden_size=hidden, intermediate_size=512,
-                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
-                      max_position_embeddings=256, tie_word_embeddings=True)
-    cfg._attn_implementation = "sdpa"
+    cfg = workloads.qwen2_config(n_layers=2, vocab=1000, hidden=hidden, inter=512, n_heads=4,
+                                 n_kv=2, max_positions=256)
     torch.manual_seed(0)
     hf = Qwen2ForCausalLM(cfg)
     with torch.no_grad():
@@ -76,67 +68,74 @@ def build(dropout, hidden=256):
             lyr.input_layernorm.weight.uniform_(0.5, 1.5)
             lyr.post_attention_layernorm.weight.uniform_(0.5, 1.5)
     hf = hf.to(torch.float16).float()          # the fp16 checkpoint, non-4-bit params in fp32
-    nf4 = []
-    for i, lyr in enumerate(hf.model.layers):
-        attn, mlp = lyr.self_attn, lyr.mlp
-        mods = {"q": attn.q_proj, "k": attn.k_proj, "v": attn.v_proj, "o": attn.o_proj,
-                "gate": mlp.gate_proj, "up": mlp.up_proj, "down": mlp.down_proj}
-        weights = {}
-        for j, (name, mod) in enumerate(mods.items()):
-            p, deq = nf4_of(mod.weight.detach().to(torch.float16).numpy(), seed=100 * i + j)
-            weights[name] = p
-            mod.weight = torch.nn.Parameter(deq, requires_grad=False)   # Linear4bit's fp16 view
-        nf4.append(weights)
     for p in hf.parameters():
         p.requires_grad_(False)
     hf.to(DEV)
-    # LoRA tensors (plain leaf tensors shared by both sides; A as peft's kaiming-uniform range,
-    # B ~ N(0, 0.05) as the reference's test sets it)
     g = torch.Generator().manual_seed(5)
-    scaling = ALPHA / RANK
-    lora = []
-    for lyr in hf.model.layers:
-        attn = lyr.self_attn
-        pair = []
-        for mod in (attn.q_proj, attn.v_proj):
-            a = (torch.rand(RANK, mod.in_features, generator=g) - 0.5) * \
-                (2 / math.sqrt(mod.in_features))
-            b = 0.05 * torch.randn(mod.out_features, RANK, generator=g)
-            pair.append((a.to(DEV).requires_grad_(True), b.to(DEV).requires_grad_(True)))
-        lora.append(pair)
-        attn.q_proj = LoraWrap(attn.q_proj, *pair[0], scaling, dropout)
-        attn.v_proj = LoraWrap(attn.v_proj, *pair[1], scaling, dropout)
+    loras = []
+    for i, lyr in enumerate(hf.model.layers):
+        attn, mlp = lyr.self_attn, lyr.mlp
+        owners = [(attn, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj")] + \
+                 [(mlp, n) for n in ("gate_proj", "up_proj", "down_proj")]
+        for j, (owner, name) in enumerate(owners):
+            mod = getattr(owner, name)
+            p, deq = nf4_of(mod.weight.detach().cpu().to(torch.float16).numpy(), seed=100 * i + j)
+            bias = None if mod.bias is None else mod.bias.detach().clone()
+            setattr(owner, name, workloads.Linear4bit(p, bias, deq.to(DEV)))
+        # A in peft's kaiming-uniform range, B ~ N(0, 0.05) as the reference's test sets it
+        for name in ("q_proj", "v_proj"):
+            base = getattr(attn, name)
+            a = (torch.rand(RANK, base.in_features, generator=g) - 0.5) * \
+                (2 / math.sqrt(base.in_features))
+            b = 0.05 * torch.randn(base.out_features, RANK, generator=g)
+            wrap = workloads.LoraLinear(base, RANK, ALPHA, dropout, a.to(DEV), b.to(DEV))
+            setattr(attn, name, wrap)
+            loras.append((f"{i}.{name}", wrap))
     hf.train()
-    fused = fused_model.from_qwen2(hf, nf4, lora, scaling, dropout)
-    return hf, fused, lora
+    return hf, loras
 
 
-def batch(vocab=1000):
+def batch(layout, vocab=1000):
+    """input_ids, attention_mask, labels of 3 rows.  "right": real tokens first (lengths 24, 15,
+    6); "mixed": row 0 left-padded (6 pads, then 18 tokens), row 1 with pads at positions 2..4
+    between real tokens, row 2 right-padded (6 tokens).  The first third of each row's real
+    tokens is prompt (label -100).
+
+    The fused path scores the real tokens only (solution/model.py:262); the unpatched model also
+    scores a pad position whose next position is labelled.  The gap of row 1 therefore lies in
+    the prompt, as padding does in TRL's batches (left-padded prompts, right-padded rows), so
+    that both score the same positions."""
     torch.manual_seed(1)
-    lengths = [24, 15, 6]
-    seq = max(lengths)
-    ids = torch.randint(0, vocab, (len(lengths), seq))
+    seq = 24
+    ids = torch.randint(0, vocab, (3, seq))
     mask = torch.zeros_like(ids)
+    if layout == "right":
+        for row, n in enumerate((24, 15, 6)):
+            mask[row, :n] = 1
+    else:
+        mask[0, 6:] = 1
+        mask[1, :17] = 1
+        mask[1, 2:5] = 0
+        mask[2, :6] = 1
     labels = torch.full_like(ids, -100)
-    for row, n in enumerate(lengths):
-        mask[row, :n] = 1
-        prompt = n // 3
-        labels[row, prompt:n] = ids[row, prompt:n]
+    for row in range(3):
+        real = mask[row].nonzero().squeeze(1)
+        lab = real[len(real) // 3:]
+        labels[row, lab] = ids[row, lab]
     ids[mask == 0] = 0
     return ids.to(DEV), mask.to(DEV), labels.to(DEV)
 
 
-def grads_of(lora):
+def grads_of(loras):
     out = {}
-    for i, pair in enumerate(lora):
-        for name, (a, b) in zip(("q", "v"), pair):
-            out[f"{i}.{name}.A"] = a.grad.detach().float().clone()
-            out[f"{i}.{name}.B"] = b.grad.detach().float().clone()
-            a.grad = b.grad = None
+    for name, mod in loras:
+        for part, lin in (("A", mod.lora_A["default"]), ("B", mod.lora_B["default"])):
+            out[f"{name}.{part}"] = lin.weight.grad.detach().float().clone()
+            lin.weight.grad = None
     return out
 
 
-def run_unpatched(hf, lora, ids, mask, labels, n_items):
+def run_unpatched(hf, loras, ids, mask, labels, n_items):
     torch.manual_seed(123)
     with torch.autocast("cuda", dtype=torch.float16):
         out = hf(input_ids=ids, attention_mask=mask, labels=labels, num_items_in_batch=n_items)
@@ -157,31 +156,25 @@ def run_unpatched(hf, lora, ids, mask, labels, n_items):
     rows = ([float(x) for x in (ce.sum(1) / tokens.clamp(min=1)).tolist()],
             [int(t) for t in tokens.tolist()])
     run_unpatched.pred = pred
-    return loss, grads_of(lora), entropy, accuracy, rows
+    return loss, grads_of(loras), entropy, accuracy, rows
 
 
-def run_fused(fused, lora, ids, mask, labels, n_items):
+def run_fused(hf, loras, ids, mask, labels, n_items):
     torch.manual_seed(123)
+    kwargs = {"num_items_in_batch": n_items, "return_dict": True}
     with torch.autocast("cuda", dtype=torch.float16):
-        loss, stats = fused_model.fused_forward(fused, ids, mask, labels, n_items)
-    (loss * 1024).backward()
-    loss = loss.detach()
+        assert fused_model.can_run(hf, ids, mask, labels, kwargs)
+        out = fused_model.fused_forward(hf, ids, mask, labels, kwargs.get("num_items_in_batch"))
+    (out.loss * 1024).backward()
+    stats = out.logits
     assert isinstance(stats, fused_model.HeadStats)
     m = metrics.trl_metrics(stats, mask)          # the trainer glue's reduction of HeadStats
     assert m["num_tokens_in_batch"] == int(mask.sum())
-    return float(loss), grads_of(lora), m["entropy"], m["mean_token_accuracy"], \
+    return float(out.loss.detach()), grads_of(loras), m["entropy"], m["mean_token_accuracy"], \
         stats.row_losses()
 
 
-@pytest.mark.parametrize("dropout,hidden", [(0.0, 256), (0.05, 256), (0.0, 512), (0.05, 512)])
-def test_fused_step_matches_unpatched_model(dropout, hidden):
-    print(f"model step: tiny Qwen2 (hidden {hidden}) + NF4 + LoRA r=16, lora dropout {dropout}",
-          flush=True)
-    hf, fused, lora = build(dropout, hidden)
-    ids, mask, labels = batch()
-    n_items = (labels[:, 1:] != -100).sum()
-    ref = run_unpatched(hf, lora, ids, mask, labels, n_items)
-    got = run_fused(fused, lora, ids, mask, labels, n_items)
+def compare(got, ref):
     worst = max(float((got[1][n] - g).norm() / g.norm().clamp(min=1e-12))
                 for n, g in ref[1].items())
     print(f"  loss {got[0]:.6f} vs {ref[0]:.6f} (rel {abs(got[0] - ref[0]) / ref[0]:.1e}); "
@@ -198,6 +191,21 @@ def test_fused_step_matches_unpatched_model(dropout, hidden):
     for a, b in zip(got[4][0], ref[4][0]):
         assert abs(a - b) / b < 2e-3, (got[4][0], ref[4][0])
 
+
+@pytest.mark.parametrize("dropout,hidden,layout", [
+    (0.0, 256, "right"), (0.05, 256, "right"), (0.0, 512, "right"), (0.05, 512, "right"),
+    (0.0, 512, "mixed"), (0.05, 512, "mixed")])
+def test_fused_step_matches_unpatched_model(dropout, hidden, layout):
+    print(f"model step: tiny Qwen2 (hidden {hidden}) + NF4 + LoRA r=16, lora dropout {dropout}, "
+          f"{layout} padding", flush=True)
+    hf, loras = build(dropout, hidden)
+    assert fused_model.model_plan(hf) is not None
+    ids, mask, labels = batch(layout)
+    n_items = (labels[:, 1:] != -100).sum()
+    ref = run_unpatched(hf, loras, ids, mask, labels, n_items)
+    got = run_fused(hf, loras, ids, mask, labels, n_items)
+    compare(got, ref)
+
     # A random model never predicts its label (accuracy 0 on both sides), so score the step
     # again against labels that take the unpatched model's own prediction at every other
     # labelled position: the argmax-hit counts must then agree on a non-trivial accuracy.
@@ -206,19 +214,50 @@ def test_fused_step_matches_unpatched_model(dropout, hidden):
     lab = (tgt != -100).nonzero()
     pick = lab[::2]
     tgt[pick[:, 0], pick[:, 1]] = run_unpatched.pred[pick[:, 0], pick[:, 1]]
-    ref2 = run_unpatched(hf, lora, ids, mask, hit, n_items)
-    got2 = run_fused(fused, lora, ids, mask, hit, n_items)
+    ref2 = run_unpatched(hf, loras, ids, mask, hit, n_items)
+    got2 = run_fused(hf, loras, ids, mask, hit, n_items)
     print(f"  argmax labels: accuracy {got2[3]:.4f} vs {ref2[3]:.4f}", flush=True)
     assert ref2[3] > 0.4
     assert abs(got2[3] - ref2[3]) < 1e-6 + 0.02, (got2[3], ref2[3])
     assert abs(got2[0] - ref2[0]) / ref2[0] < 2e-3, (got2[0], ref2[0])
 
 
+def test_can_run_gates_on_device_mode_and_autocast():
+    """The conditions of solution/model.py:165-192 on a model the plan takes: the fused path
+    runs only for a labelled training forward under fp16 autocast, with the allowed keywords."""
+    hf, _ = build(0.0, 512)
+    ids, mask, labels = batch("right")
+    with torch.autocast("cuda", dtype=torch.float16):
+        assert fused_model.can_run(hf, ids, mask, labels, {})
+        assert fused_model.can_run(hf, ids, mask, labels, {"output_attentions": False})
+        assert not fused_model.can_run(hf, ids, mask, labels, {"output_attentions": True})
+        assert not fused_model.can_run(hf, ids, mask, labels, {"position_ids": None})
+        assert not fused_model.can_run(hf, ids, mask, None, {})
+        assert not fused_model.can_run(hf, ids, mask[:, :-1], labels, {})
+        with torch.no_grad():
+            assert not fused_model.can_run(hf, ids, mask, labels, {})
+        hf.eval()
+        assert not fused_model.can_run(hf, ids, mask, labels, {})
+        hf.train()
+    assert not fused_model.can_run(hf, ids, mask, labels, {})          # no autocast
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        assert not fused_model.can_run(hf, ids, mask, labels, {})
+    # a second active adapter is not a form the path reproduces
+    q = hf.model.layers[0].self_attn.q_proj
+    q.active_adapters = ["default", "other"]
+    q.lora_A["other"] = torch.nn.Linear(512, RANK, bias=False, device=DEV)
+    with torch.autocast("cuda", dtype=torch.float16):
+        assert not fused_model.can_run(hf, ids, mask, labels, {})
+    q.active_adapters = ["default"]
+    with torch.autocast("cuda", dtype=torch.float16):
+        assert fused_model.can_run(hf, ids, mask, labels, {})
+
+
 def test_synthetic_model_full_width_step():
-    """Two Qwen2.5-1.5B-width layers and the full 151,936-token vocabulary on a ragged batch:
-    the step runs, its loss is that of near-uniform logits, every LoRA gradient is finite and
-    the statistics count what the batch holds."""
-    m = fused_model.synthetic_model(DEV, n_layers=2)
+    """Two Qwen2.5-1.5B-width layers and the full 151,936-token vocabulary on a ragged batch,
+    through can_run / fused_forward: the step runs, its loss is that of near-uniform logits,
+    every LoRA gradient is finite and the statistics count what the batch holds."""
+    hf = workloads.qwen2_qlora(DEV, n_layers=2)
     lengths, seq = (64, 40, 9), 64
     g = torch.Generator().manual_seed(3)
     ids = torch.randint(0, workloads.VOCAB, (3, seq), generator=g)
@@ -228,12 +267,17 @@ def test_synthetic_model_full_width_step():
         mask[r, :n] = 1
         labels[r, n // 4:n] = ids[r, n // 4:n]
     ids, mask, labels = ids.to(DEV), mask.to(DEV), labels.to(DEV)
-    loss, stats = fused_model.fused_forward(m, ids, mask, labels)
-    loss.backward()
-    assert abs(float(loss.detach()) - math.log(workloads.VOCAB)) < 1.0
+    with torch.autocast("cuda", dtype=torch.float16):
+        assert fused_model.can_run(hf, ids, mask, labels, {})
+        out = fused_model.fused_forward(hf, ids, mask, labels, None)
+    out.loss.backward()
+    stats = out.logits
+    assert abs(float(out.loss.detach()) - math.log(workloads.VOCAB)) < 1.0
     n_lab = int((torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:][mask.bool()]
                  != -100).sum())
     assert int(stats.labelled) == n_lab
     assert sum(stats.row_losses()[1]) == n_lab
-    for p in fused_model.lora_parameters(m):
+    params = workloads.lora_parameters(hf)
+    assert len(params) == 8
+    for p in params:
         assert p.grad is not None and bool(torch.isfinite(p.grad).all())

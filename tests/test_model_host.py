@@ -87,3 +87,113 @@ def test_configure_backward_is_thread_local():
     x = torch.randn(5, 3, generator=torch.Generator().manual_seed(1), requires_grad=True)
     (x.sin() * x).sum().backward()
     assert torch.equal(x.grad, seen["grad"])
+
+
+# ---- the model-level entry: plan and gate (solution/model.py:54-192), no kernel calls ----
+
+def _tiny(**kw):
+    from testt_amd import workloads
+
+    args = dict(n_layers=2, vocab=1000, hidden=256, inter=512, n_heads=2, n_kv=1)
+    args.update(kw)
+    return workloads.qwen2_qlora("cpu", **args)
+
+
+def test_model_plan_of_a_4bit_lora_model():
+    hf = _tiny()
+    plan = model.model_plan(hf)
+    assert plan is not None and len(plan.layers) == 2
+    assert (plan.n_heads, plan.n_kv, plan.head_dim, plan.hidden) == (2, 1, 128, 256)
+    assert model.model_plan(hf) is plan                       # built once, kept on the model
+    lw = plan.layer_weights(plan.layers[1])
+    lyr = hf.model.layers[1]
+    assert lw.q is lyr.self_attn.q_proj.base_layer.weight
+    assert lw.lora_q[0] is lyr.self_attn.q_proj.lora_A["default"].weight
+    assert lw.lora_v[1] is lyr.self_attn.v_proj.lora_B["default"].weight
+    assert lw.scaling == 2.0 and lw.scaling_v == 2.0 and lw.dropout == 0.0
+    assert lw.qkv_bias.dtype == torch.float16 and lw.qkv_bias.numel() == (2 + 2) * 128
+    assert lw.o_bias is None
+    assert lw.attn_scale == lyr.self_attn.scaling
+    from testt_amd import layer
+
+    assert layer.lora_without_dropout(lw)
+
+
+def test_model_plan_reads_the_adapters_dropout_each_time():
+    from testt_amd import layer
+
+    hf = _tiny(dropout=0.1)
+    plan = model.model_plan(hf)
+    lw = plan.layer_weights(plan.layers[0])
+    assert lw.dropout == 0.1 and isinstance(lw.lora_dropout[0], torch.nn.Dropout)
+    assert not layer.lora_without_dropout(lw)
+    hf.eval()                                  # a dropout module in eval mode draws nothing
+    lw = plan.layer_weights(plan.layers[0])
+    assert lw.dropout == 0.0 and layer.lora_without_dropout(lw)
+
+
+def test_model_plan_refuses_other_models(capsys):
+    from transformers import Qwen2ForCausalLM
+
+    from testt_amd import workloads
+
+    plain = Qwen2ForCausalLM(workloads.qwen2_config(1, 1000, 256, 512, 2, 1, 256))
+    assert model.model_plan(plain) is None                    # projections not 4-bit
+    assert "not a bitsandbytes 4-bit layer" in capsys.readouterr().out
+
+    hf = _tiny()
+    hf.config._attn_implementation = "eager"
+    assert model.model_plan(hf) is None
+
+    hf = _tiny()
+    k = hf.model.layers[0].self_attn.k_proj
+    hf.model.layers[0].self_attn.k_proj = workloads.LoraLinear(k, 16, 32)
+    assert model.model_plan(hf) is None                       # LoRA outside q/v
+
+    hf = _tiny()
+    hf.model.embed_tokens.weight.requires_grad_(True)
+    assert model.model_plan(hf) is None                       # trainable embedding / head
+
+    hf = _tiny()
+    hf.model.layers[1].mlp.up_proj.bias = torch.nn.Parameter(torch.zeros(512))
+    assert model.model_plan(hf) is None                       # MLP bias
+
+
+def test_lora_parts_rules():
+    from testt_amd import workloads
+
+    hf = _tiny()
+    q = hf.model.layers[0].self_attn.q_proj
+    parts = model._lora_parts(q)
+    assert parts and parts.scaling == 2.0 and isinstance(parts.dropout, torch.nn.Identity)
+    assert model._lora_parts(hf.model.layers[0].self_attn.k_proj) is None   # no LoRA
+    q.active_adapters = []
+    assert model._lora_parts(q) is None                                      # none active
+    q.active_adapters = ["default"]
+    q.merged = True
+    assert model._lora_parts(q) is False
+    q.merged = False
+    q.use_dora = {"default": True}
+    assert model._lora_parts(q) is False
+    q.use_dora = {"default": False}
+    q.lora_bias = {"default": True}
+    assert model._lora_parts(q) is False
+    q.lora_bias = {"default": False}
+    q.lora_dropout["default"] = torch.nn.ReLU()
+    assert model._lora_parts(q) is False
+    q.lora_dropout["default"] = torch.nn.Identity()
+    q.lora_variant = {"default": object()}
+    assert model._lora_parts(q) is False
+    q.lora_variant = {}
+    assert model._lora_parts(q)
+    base = workloads.Linear4bit(workloads.nf4_weight(128, 256, seed=1))
+    assert model._is_4bit(base) and not model._is_4bit(torch.nn.Linear(256, 128))
+
+
+def test_can_run_refuses_cpu_tensors():
+    """The kernels run on HIP device tensors only (solution/model.py:173)."""
+    hf = _tiny()
+    ids = torch.randint(0, 1000, (2, 8))
+    mask = torch.ones_like(ids)
+    with torch.autocast("cpu", dtype=torch.float16):
+        assert not model.can_run(hf, ids, mask, ids.clone(), {})

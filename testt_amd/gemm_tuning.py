@@ -68,7 +68,7 @@ def main(argv=None):
     torch.cuda.tunable.tuning_enable(True)
     torch.cuda.tunable.set_filename(os.devnull)      # the table is written below, not at exit
     dev = torch.device("cuda", 0)
-    m = model.synthetic_model(dev, n_layers=args.layers)
+    hf = workloads.qwen2_qlora(dev, n_layers=args.layers)
     B, T = workloads.BATCH, workloads.SEQ
     g = workloads.gen(12)
     ids = torch.randint(0, workloads.VOCAB, (B, T), generator=g).to(dev)
@@ -76,7 +76,8 @@ def main(argv=None):
     labels = ids.clone()
     labels[:, :T // 4] = -100
     for i in range(2):
-        loss, _ = model.fused_forward(m, ids, mask, labels)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = model.fused_forward(hf, ids, mask, labels, None).loss
         loss.backward()
         torch.cuda.synchronize(dev)
         print(f"tuning step {i} done", flush=True)

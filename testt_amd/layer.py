@@ -53,15 +53,19 @@ class LayerWeights:
     gate: object
     up: object
     down: object
-    qkv_bias: torch.Tensor          # fp16 [(NH + 2*NKV) * D]
-    lora_q: tuple                   # (A fp32 [r, H], B fp32 [NH*D, r]) trainable
-    lora_v: tuple                   # (A fp32 [r, H], B fp32 [NKV*D, r]) trainable
-    scaling: float
+    qkv_bias: torch.Tensor          # fp16 [(NH + 2*NKV) * D], or None
+    lora_q: tuple                   # (A fp32 [r, H], B fp32 [NH*D, r]) trainable, or None
+    lora_v: tuple                   # (A fp32 [r, H], B fp32 [NKV*D, r]) trainable, or None
+    scaling: float                  # LoRA scaling of q (and of v unless scaling_v is given)
     n_heads: int
     n_kv: int
     head_dim: int
     eps: float = 1e-6
-    dropout: float = 0.0
+    dropout: float = 0.0            # LoRA dropout probability (when lora_dropout is None)
+    o_bias: torch.Tensor = None     # fp16 [H], or None
+    scaling_v: float = None         # LoRA scaling of v when it differs from q's
+    lora_dropout: tuple = None      # (q, v) dropout modules to call (peft's), instead of dropout
+    attn_scale: float = None        # attention softmax scale (None: 1/sqrt(head_dim))
 
 
 def synthetic_layer(device, hidden=workloads.HIDDEN, inter=workloads.INTER,
@@ -185,16 +189,22 @@ class QKVLora(torch.autograd.Function):
 
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
     """peft's B(A(dropout(x))) * scaling for the real tokens, fp16 matmuls (solution/model.py:
-    195-206): the dropout runs on the padded fp32 norm output, A and B on the real rows."""
+    195-206): the dropout runs on the padded fp32 norm output, A and B on the real rows.
+    `dropout` is a probability or a dropout module to call (peft's own, so that its training
+    flag and the random draws are the unpatched model's)."""
     a, b = ab
     hidden = y_pad.shape[-1]
-    dropped = torch.nn.functional.dropout(y_pad.view(batch, seq, hidden), dropout,
-                                          training=dropout > 0).view(batch * seq, hidden)
+    x = y_pad.view(batch, seq, hidden)
+    if callable(dropout):
+        dropped = dropout(x)
+    else:
+        dropped = torch.nn.functional.dropout(x, dropout, training=dropout > 0)
+    dropped = dropped.view(batch * seq, hidden)
     rows = dropped.index_select(0, pos_idx).to(torch.float16)
     return (rows @ a.to(torch.float16).t()) @ b.to(torch.float16).t() * scaling
 
 
-def attention(q, k, v, key_valid):
+def attention(q, k, v, key_valid, scale=None):
     """Causal GQA attention of the padded [B, heads, T, D] layout -> token-major [B*T, NH*D].
 
     Query i of row b sees key j iff j <= i and the key is real (key_valid[b, j] != 0; every key
@@ -203,9 +213,9 @@ def attention(q, k, v, key_valid):
     same mask, as the reference runs every shape (solution/model.py:246-247)."""
     B, NH, T, D = q.shape
     if _attention.supported(q, k, v):
-        return _attention.causal_attention(q, k, v, key_valid)
+        return _attention.causal_attention(q, k, v, key_valid, scale)
     mask = None if key_valid is None else causal_pad_mask(key_valid)
-    scale = 1.0 / math.sqrt(D)
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     if mask is None:
         a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
                                                              scale=scale, enable_gqa=True)
@@ -235,47 +245,75 @@ def causal_pad_mask(attention_mask):
     return mask | (eye & ~attention_mask.bool()[:, None, :, None])
 
 
+def _dropout_p(module):
+    if isinstance(module, torch.nn.Dropout) and module.training:
+        return float(module.p)
+    return 0.0
+
+
+def lora_without_dropout(w):
+    """True when the layer's LoRA runs as QKVLora: adapters on both q and v with one rank and
+    one scaling, and no dropout drawn (p = 0, Identity, or a dropout module in eval mode)."""
+    if w.lora_q is None or w.lora_v is None:
+        return False
+    if w.scaling_v is not None and w.scaling_v != w.scaling:
+        return False
+    if w.lora_q[0].shape[0] != w.lora_v[0].shape[0]:
+        return False
+    if w.lora_dropout is not None:
+        return all(m is None or _dropout_p(m) == 0.0 for m in w.lora_dropout)
+    return w.dropout == 0.0
+
+
 def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     """(s, d): the residual stream and the MLP output of one layer (the next layer's delta).
     key_valid: uint8 [batch, seq] (key_valid_of(attention_mask)), or None when nothing is
     padded."""
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
+    plain = lora_without_dropout(w)
     w_qkv = w_o = w_gu = w_d = staged = None
     if UNPACK_PER_LAYER:
         groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
-        a_q, b_q = w.lora_q
-        a_v, b_v = w.lora_v
-        if w.dropout == 0.0 and USE_FUSED_LORA and \
-                _lora.params_supported(a_q, a_v, b_q, b_v, s.device):
+        params = (w.lora_q[0], w.lora_v[0], w.lora_q[1], w.lora_v[1]) if plain else None
+        if plain and USE_FUSED_LORA and _lora.params_supported(*params, s.device):
             # the LoRA parameters' fp16 staging rides on the same launch as the unpack
             (w_qkv, w_o, w_gu, w_d), staged = unpack_groups_lora(
-                groups, s.device, tuple(p.detach() for p in (a_q, a_v, b_q, b_v)))
+                groups, s.device, tuple(p.detach() for p in params))
         else:
             w_qkv, w_o, w_gu, w_d = unpack_groups(groups, s.device)
-    if w.dropout == 0.0:
+    if plain:
         s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         qkv, lq, lv = QKVLora.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
                                     (w.q, w.k, w.v), w_qkv, staged)
     else:
-        s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
+        any_lora = w.lora_q is not None or w.lora_v is not None
+        if any_lora:
+            s, y, y_pad = add_rmsnorm(s, delta, w.input_norm, w.eps, pos_idx, padded)
+        else:
+            s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         qkv = frozen_linear(y, (w.q, w.k, w.v), w.qkv_bias, w_qkv)
-        lq = lora_branch(y_pad, w.lora_q, w.scaling, w.dropout, batch, seq, pos_idx)
-        lv = lora_branch(y_pad, w.lora_v, w.scaling, w.dropout, batch, seq, pos_idx)
-        del y_pad
+        drops = w.lora_dropout if w.lora_dropout is not None else (w.dropout, w.dropout)
+        scales = (w.scaling, w.scaling if w.scaling_v is None else w.scaling_v)
+        lq, lv = (None if ab is None else
+                  lora_branch(y_pad, ab, sc, dr, batch, seq, pos_idx)
+                  for ab, sc, dr in zip((w.lora_q, w.lora_v), scales, drops))
+        if any_lora:
+            del y_pad
     if USE_VARLEN_ATTENTION and _attention.varlen_supported(qkv, hd, nh, nkv):
         # the real tokens only: rows of batch row b are cu[b] .. cu[b+1] of the sorted pos_idx
         cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
-        a = _attention.rope_attention(qkv, lq, lv, cos, sin, pos_idx, cu, batch, seq, nh, nkv)
+        a = _attention.rope_attention(qkv, lq, lv, cos, sin, pos_idx, cu, batch, seq, nh, nkv,
+                                      w.attn_scale)
         del qkv, lq, lv, w_qkv
     else:
         q, k, v = rope_pack(qkv, lq, lv, cos, sin, pos_idx, batch, seq, nh, nkv, hd)
         del qkv, lq, lv, w_qkv
-        a = attention(q, k, v, key_valid)
+        a = attention(q, k, v, key_valid, w.attn_scale)
         del q, k, v
         if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
             a = a.index_select(0, pos_idx)
-    o = frozen_linear(a, (w.o,), None, w_o)
+    o = frozen_linear(a, (w.o,), w.o_bias, w_o)
     del a, w_o
     s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)
     d = fused_mlp(y2, w.gate, w.up, w.down, w_gu, w_d)

@@ -1,26 +1,41 @@
-"""The training forward of Qwen2ForCausalLM + LoRA on the real tokens, built from the drop-in ops.
+"""The training forward of a 4-bit Qwen2ForCausalLM + LoRA on the real tokens, built from the
+drop-in ops: the model-level entry the reference's trainer patch binds
+(`from .model import HeadStats, can_run, fused_forward, model_plan`,
+solution/trainer_patch.py:23, called at solution/trainer_patch.py:57-63).
 
-Mirrors the reference's fused_forward (solution/model.py:209-279) and HeadStats
-(solution/model.py:36-51).  With s the fp32 residual stream of the M real tokens (pad-free:
-pos_idx = attention_mask.nonzero(), solution/model.py:220):
+    model_plan(causal_lm)                      the checked layout of the model (cached on it),
+                                               None when the fused path does not take the model
+    can_run(causal_lm, input_ids, attention_mask, labels, extra)
+                                               True for a labelled training step under fp16
+                                               autocast on a HIP device that the plan covers
+    fused_forward(causal_lm, input_ids, attention_mask, labels, num_items_in_batch)
+                                               CausalLMOutputWithPast(loss, logits=HeadStats)
 
-  s          = embedding(input_ids[real])             fp16 table -> fp32 rows
-  per layer  : testt_amd.layer.decoder_layer          norm, QKV + LoRA, RoPE pack, attention, o-proj,
-                                                       norm, NF4 MLP (the reference's loop body,
-                                                       solution/model.py:235-255)
+Same names, arguments, conditions and results as solution/model.py:36-51,152-279.  With s the
+fp32 residual stream of the M real tokens (pos_idx = attention_mask.nonzero(), the pad-free
+layout of solution/model.py:220):
+
+  s          = embedding(input_ids[real])             (the table as the model holds it) -> fp32
+  per layer  : testt_amd.layer.decoder_layer          norm, q|k|v GEMM + LoRA (HIP kernels),
+                                                       RoPE + varlen causal GQA attention over
+                                                       each row's real tokens (HIP), o GEMM,
+                                                       norm, NF4 MLP (solution/model.py:235-255)
   y          = add_rmsnorm(s, d, final norm)           (solution/model.py:257)
-  targets    = labels shifted by one, real rows        (ForCausalLMLoss's shift,
-                                                        solution/model.py:261-263)
-  loss, ...  = fused_head_loss(y, W16, targets, denom) chunked vocab head (solution/model.py:268)
+  targets    = labels shifted by one, real rows        (solution/model.py:260-263)
+  loss, ...  = fused_head_loss(y, W16, targets, denom) (solution/model.py:264-268)
 
-and returns (loss, HeadStats) in place of the [batch, seq, vocab] logits: the statistics TRL's
-metrics (entropy over attention_mask == 1, accuracy over labelled targets) and Soup's rewind
-log (per-row mean token loss) read from them.
+Where the reference runs torch SDPA on the padded layout, peft's LoRA modules and one unpack per
+projection, this runs the layer's own path: one NF4 unpack launch per layer (the LoRA
+parameters' fp16 staging in the same launch), the rank-16 LoRA kernels, and attention over the
+real tokens only with RoPE's backward inside the attention backward.  LoRA with dropout, other
+ranks, or a LoRA adapter on only one of q/v run the reference's LoRA formulation
+(layer.lora_branch: peft's own dropout modules on the padded fp32 norm output, so the dropout
+draws are the unpatched model's); head dims other than 128 run torch SDPA on the padded layout.
 
-The reference takes its weights from a PEFT/bitsandbytes model; here they are plain tensors
-(`ModelWeights`: the fp16 embedding, `layer.LayerWeights` per decoder layer, the final norm),
-so the whole model runs without transformers, peft or bitsandbytes.  `from_qwen2` builds them
-from a transformers Qwen2ForCausalLM whose projection weights the caller supplies in NF4.
+The 4-bit projections are recognised by their weight's `quant_state` (bitsandbytes' Params4bit
+carries it; bitsandbytes itself is not needed to run the kernels), the LoRA adapters by peft's
+LoraLayer attributes (lora_A / lora_B / lora_dropout ModuleDicts, scaling, active_adapters).
+`ModelWeights` + `forward_weights` run the same path on plain tensors.
 """
 
 from dataclasses import dataclass, field
@@ -28,14 +43,24 @@ from dataclasses import dataclass, field
 import torch
 
 from . import layer as _layer
-from . import workloads
+from ._common import kernels_ok
 from .head import IGNORE_INDEX, fused_head_loss
 from .rmsnorm import add_rmsnorm
+
+# Keyword arguments of Qwen2ForCausalLM.forward that the fused path accepts
+# (solution/model.py:32-33): num_items_in_batch and return_dict with any value, the two output
+# flags only when false.
+_ALLOWED_KWARGS = frozenset(("num_items_in_batch", "output_attentions", "output_hidden_states",
+                             "return_dict"))
+_ANY_VALUE_KWARGS = frozenset(("num_items_in_batch", "return_dict"))
+
+# Where model_plan keeps its result on the model (solution/model.py:154 uses the same key).
+_PLAN_KEY = "_soup_kernel_plan"
 
 
 class HeadStats:
     """What TRL's metrics and Soup's rewind log need from one labelled forward, in place of the
-    logits (solution/model.py:36-51)."""
+    [batch, seq, vocab] logits (solution/model.py:36-51).  Lives in `outputs.logits`."""
 
     def __init__(self, entropy_sum, correct, labelled, row_loss_sum, row_tokens):
         self.entropy_sum = entropy_sum      # sum of token entropies over attention_mask == 1
@@ -52,14 +77,264 @@ class HeadStats:
         return [float(m) for m in means.tolist()], [int(t) for t in tokens.tolist()]
 
 
+# --------------------------------------------------------------------------------------------
+# Recognising the model's modules
+
+
+def _base_layer(module):
+    """The projection under a LoRA wrapper (peft's get_base_layer), else the module itself
+    (solution/model.py:54-56)."""
+    get = getattr(module, "get_base_layer", None)
+    return get() if callable(get) else module
+
+
+def _is_4bit(module):
+    """A 4-bit linear: its weight carries a bitsandbytes quant state (Linear4bit's Params4bit;
+    solution/model.py:59-65 asks the same of a bitsandbytes.nn.Linear4bit)."""
+    return getattr(getattr(module, "weight", None), "quant_state", None) is not None
+
+
+class LoraParts:
+    """The one active vanilla LoRA adapter of a peft LoraLayer: its dropout module, A and B
+    linears and scaling (what solution/model.py:68-91 returns as a tuple)."""
+
+    __slots__ = ("dropout", "lora_a", "lora_b", "scaling")
+
+    def __init__(self, dropout, lora_a, lora_b, scaling):
+        self.dropout, self.lora_a, self.lora_b, self.scaling = dropout, lora_a, lora_b, scaling
+
+    def __iter__(self):
+        return iter((self.dropout, self.lora_a, self.lora_b, self.scaling))
+
+
+def _adapter_flag(module, attr, name):
+    table = getattr(module, attr, None)
+    return bool(table.get(name, False)) if isinstance(table, dict) else False
+
+
+def _lora_parts(module):
+    """None: no LoRA on `module` (or no active adapter of it); LoraParts: exactly one active
+    vanilla adapter; False: any other LoRA state the fused path does not reproduce (merged or
+    disabled adapters, several active adapters, DoRA, LoRA bias, a variant, a dropout that is
+    neither Dropout nor Identity).  The rules of solution/model.py:68-91."""
+    if not hasattr(module, "lora_A"):
+        return None
+    try:
+        if getattr(module, "merged", False) or getattr(module, "disable_adapters", False):
+            return False
+        names = [n for n in module.active_adapters if n in module.lora_A.keys()]
+        if not names:
+            return None
+        if len(names) > 1:
+            return False
+        name = names[0]
+        variants = getattr(module, "lora_variant", None) or {}
+        if name in variants or _adapter_flag(module, "use_dora", name) or \
+                _adapter_flag(module, "lora_bias", name):
+            return False
+        dropout = module.lora_dropout[name]
+        if not isinstance(dropout, (torch.nn.Dropout, torch.nn.Identity)):
+            return False
+        return LoraParts(dropout, module.lora_A[name], module.lora_B[name],
+                         float(module.scaling[name]))
+    except Exception:  # noqa: BLE001 - a peft layout this path does not know: not ours to run
+        return False
+
+
+def _norm_weight(weight):
+    """A norm's weight as the RMSNorm kernels take it: fp32 (prepare_model_for_kbit_training
+    leaves the norms in fp32; a model with fp16 norms gets an fp32 copy per forward)."""
+    w = weight.detach()
+    return w if w.dtype == torch.float32 else w.float()
+
+
+def _dropout_p(dropout):
+    """The probability the dropout module applies now (0 for Identity or in eval mode)."""
+    if isinstance(dropout, torch.nn.Dropout) and dropout.training:
+        return float(dropout.p)
+    return 0.0
+
+
+# --------------------------------------------------------------------------------------------
+# The plan
+
+
+class LayerPlan:
+    """One decoder layer's frozen parts, checked once (solution/model.py:94-122): the seven
+    4-bit projections, the q|k|v and o biases in fp16, the two norms, and the q/v modules whose
+    LoRA state is read on every forward."""
+
+    __slots__ = ("layer", "attn", "q", "k", "v", "o", "gate", "up", "down", "qkv_bias",
+                 "o_bias", "lora_modules")
+
+    def __init__(self, layer):
+        self.layer = layer
+        attn, mlp = layer.self_attn, layer.mlp
+        self.attn = attn
+        self.lora_modules = (attn.q_proj, attn.v_proj)
+        mods = (attn.q_proj, attn.k_proj, attn.v_proj, attn.o_proj, mlp.gate_proj, mlp.up_proj,
+                mlp.down_proj)
+        bases = [_base_layer(m) for m in mods]
+        if not all(_is_4bit(b) for b in bases):
+            raise ValueError("not a bitsandbytes 4-bit layer")
+        q, k, v, o, gate, up, down = bases
+        self.q, self.k, self.v, self.o = q.weight, k.weight, v.weight, o.weight
+        self.gate, self.up, self.down = gate.weight, up.weight, down.weight
+        if any(getattr(b, "bias", None) is not None for b in (gate, up, down)):
+            raise ValueError("MLP bias")
+        qkv_b = [getattr(b, "bias", None) for b in (q, k, v)]
+        present = sum(b is not None for b in qkv_b)
+        if present not in (0, 3):
+            raise ValueError("mixed q/k/v bias")
+        self.qkv_bias = torch.cat([b.detach().to(torch.float16) for b in qkv_b]) \
+            if present else None
+        o_b = getattr(o, "bias", None)
+        self.o_bias = o_b.detach().to(torch.float16) if o_b is not None else None
+        for m in (attn.k_proj, attn.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj):
+            if _lora_parts(m) is not None:
+                raise ValueError("LoRA outside q_proj/v_proj")
+
+
+class ModelPlan:
+    """The model-level checks and parts (solution/model.py:125-149): SDPA attention, full
+    attention in every layer, SiLU, an even head dim, a frozen unbiased embedding and head with
+    one row per vocabulary entry, and a LayerPlan per decoder layer."""
+
+    def __init__(self, causal_lm):
+        cfg = causal_lm.config
+        inner = causal_lm.model
+        if getattr(cfg, "_attn_implementation", None) != "sdpa":
+            raise ValueError("attention is not sdpa")
+        if getattr(inner, "has_sliding_layers", False) or \
+                any(t != "full_attention" for t in (getattr(cfg, "layer_types", None) or [])):
+            raise ValueError("sliding-window layers")
+        if getattr(cfg, "hidden_act", "silu") != "silu":
+            raise ValueError("activation is not silu")
+        self.n_heads = cfg.num_attention_heads
+        self.n_kv = cfg.num_key_value_heads
+        self.hidden = cfg.hidden_size
+        self.head_dim = getattr(cfg, "head_dim", None) or self.hidden // self.n_heads
+        if self.head_dim % 2:
+            raise ValueError("odd head_dim")
+        self.layers = [LayerPlan(lyr) for lyr in inner.layers[:cfg.num_hidden_layers]]
+        self.embed = inner.embed_tokens
+        self.head = causal_lm.lm_head
+        self.norm = inner.norm
+        self.rotary = inner.rotary_emb
+        if self.embed.weight.requires_grad or self.head.weight.requires_grad or \
+                getattr(self.head, "bias", None) is not None:
+            raise ValueError("trainable or biased embedding/head")
+        if self.head.weight.shape[0] != cfg.vocab_size:
+            raise ValueError("vocab size")
+
+    def layer_weights(self, lp):
+        """layer.LayerWeights of one layer with its LoRA state as it is now (adapters can be
+        switched between steps, as peft allows)."""
+        lyr = lp.layer
+        parts = [_lora_parts(m) for m in lp.lora_modules]
+        lora = [None if p is None else (p.lora_a.weight, p.lora_b.weight) for p in parts]
+        scal = [None if p is None else p.scaling for p in parts]
+        drop = [None if p is None else p.dropout for p in parts]
+        eps_in = lyr.input_layernorm.variance_epsilon
+        if lyr.post_attention_layernorm.variance_epsilon != eps_in:
+            raise ValueError("the two norms of a layer have different eps")
+        return _layer.LayerWeights(
+            input_norm=_norm_weight(lyr.input_layernorm.weight),
+            post_norm=_norm_weight(lyr.post_attention_layernorm.weight),
+            q=lp.q, k=lp.k, v=lp.v, o=lp.o, gate=lp.gate, up=lp.up, down=lp.down,
+            qkv_bias=lp.qkv_bias, o_bias=lp.o_bias, lora_q=lora[0], lora_v=lora[1],
+            scaling=scal[0] if scal[0] is not None else 1.0, scaling_v=scal[1],
+            n_heads=self.n_heads, n_kv=self.n_kv, head_dim=self.head_dim, eps=eps_in,
+            dropout=max(_dropout_p(d) for d in drop if d is not None) if any(
+                d is not None for d in drop) else 0.0,
+            lora_dropout=tuple(drop), attn_scale=getattr(lp.attn, "scaling", None))
+
+
+def model_plan(causal_lm):
+    """The checked plan of this model, built once and kept on it; None when the fused path does
+    not take the model (the reason printed once, as solution/model.py:152-162 does)."""
+    plan = causal_lm.__dict__.get(_PLAN_KEY)
+    if plan is None:
+        try:
+            plan = ModelPlan(causal_lm)
+        except Exception as exc:  # noqa: BLE001 - any unexpected layout: not ours to run
+            plan = False
+            print(f"[testt_amd] fused path off for this model: {exc}", flush=True)
+        causal_lm.__dict__[_PLAN_KEY] = plan
+    return plan or None
+
+
+def can_run(causal_lm, input_ids, attention_mask, labels, extra):
+    """Whether fused_forward takes this call (solution/model.py:165-192): a labelled training
+    forward with grad enabled, [batch, seq] input_ids / attention_mask / labels on a HIP device,
+    only the allowed keyword arguments, fp16 autocast, a model the plan covers, and LoRA only
+    on q/v in a form the plan reproduces."""
+    if not (causal_lm.training and torch.is_grad_enabled() and labels is not None):
+        return False
+    if input_ids is None or attention_mask is None or input_ids.dim() != 2:
+        return False
+    if attention_mask.shape != input_ids.shape or labels.shape != input_ids.shape:
+        return False
+    if not kernels_ok(input_ids):
+        return False
+    for key, value in extra.items():
+        if key not in _ALLOWED_KWARGS or (key not in _ANY_VALUE_KWARGS and value):
+            return False
+    dev = input_ids.device.type
+    if not torch.is_autocast_enabled(dev) or torch.get_autocast_dtype(dev) != torch.float16:
+        return False
+    plan = model_plan(causal_lm)
+    if plan is None:
+        return False
+    for lp in plan.layers:
+        if _lora_parts(lp.attn.k_proj) is not None:
+            return False
+        if any(_lora_parts(m) is False for m in lp.lora_modules):
+            return False
+    return True
+
+
+def fused_forward(causal_lm, input_ids, attention_mask, labels, num_items_in_batch):
+    """CausalLMOutputWithPast(loss=loss, logits=HeadStats) of one labelled training forward of
+    `causal_lm` (solution/model.py:209-279); call it where can_run holds.  The loss is
+    differentiable with respect to the LoRA parameters."""
+    from transformers.modeling_outputs import CausalLMOutputWithPast
+
+    plan = model_plan(causal_lm)
+    if plan is None:
+        raise ValueError("fused_forward: the fused path does not take this model")
+    batch, seq = input_ids.shape
+    # The model's own rotary embedding at positions 0 .. seq-1 (any rope scaling it has),
+    # fp32 [seq, head_dim], as the reference takes them (solution/model.py:227-232).
+    shape_ref = torch.empty((1, 1, 1), dtype=torch.float32, device=input_ids.device).expand(
+        batch, seq, plan.hidden)
+    position_ids = torch.arange(seq, device=input_ids.device).unsqueeze(0)
+    cos, sin = plan.rotary(shape_ref, position_ids)
+    cos, sin = cos[0].float(), sin[0].float()
+    layers = [plan.layer_weights(lp) for lp in plan.layers]
+    head = plan.head.weight
+    tied = head is plan.embed.weight
+    weights = ModelWeights(embed=plan.embed.weight, layers=layers,
+                           final_norm=_norm_weight(plan.norm.weight),
+                           inv_freq=None, eps=plan.norm.variance_epsilon,
+                           head=None if tied else head)
+    loss, stats = _forward(weights, cos, sin, input_ids, attention_mask, labels,
+                           num_items_in_batch)
+    return CausalLMOutputWithPast(loss=loss, logits=stats)
+
+
+# --------------------------------------------------------------------------------------------
+# The path on plain tensors
+
+
 @dataclass
 class ModelWeights:
-    embed: torch.Tensor                         # fp16 [V, H] (the tied head reads it too)
+    embed: torch.Tensor                         # [V, H], fp16 or fp32 (the tied head reads it)
     layers: list                                # layer.LayerWeights per decoder layer
     final_norm: torch.Tensor                    # fp32 [H]
-    inv_freq: torch.Tensor                      # fp32 [head_dim / 2], the rotary frequencies
+    inv_freq: torch.Tensor                      # fp32 [head_dim / 2] rotary frequencies, or None
     eps: float = 1e-6
-    head: torch.Tensor = field(default=None)    # fp16 [V, H]; None: tied to `embed`
+    head: torch.Tensor = field(default=None)    # [V, H]; None: tied to `embed`
 
 
 def rotary_tables(inv_freq, seq):
@@ -84,21 +359,23 @@ def shifted_targets(labels, pos_idx):
     return targets.reshape(-1).index_select(0, pos_idx)
 
 
-def fused_forward(model, input_ids, attention_mask, labels, num_items_in_batch=None):
-    """(loss, HeadStats) of one labelled training forward (solution/model.py:209-279).
-
-    `loss` is differentiable with respect to the LoRA parameters of `model.layers` (and
-    nothing else: the embedding, norms and NF4 projections are frozen, as in QLoRA)."""
+def forward_weights(model, input_ids, attention_mask, labels, num_items_in_batch=None):
+    """(loss, HeadStats) of one labelled training forward of the plain-tensor `model`
+    (ModelWeights with `inv_freq`): the path of fused_forward without a transformers model."""
     if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape or \
             labels.shape != input_ids.shape:
         raise ValueError("input_ids, attention_mask and labels must share one [batch, seq] shape")
+    cos, sin = rotary_tables(model.inv_freq, input_ids.shape[1])
+    return _forward(model, cos, sin, input_ids, attention_mask, labels, num_items_in_batch)
+
+
+def _forward(model, cos, sin, input_ids, attention_mask, labels, num_items_in_batch):
     batch, seq = input_ids.shape
     dev = input_ids.device
     pos_idx = attention_mask.reshape(-1).nonzero().squeeze(1)
 
     ids = input_ids.reshape(-1).index_select(0, pos_idx)
     s = torch.nn.functional.embedding(ids, model.embed).float()
-    cos, sin = rotary_tables(model.inv_freq, seq)
     key_valid = _layer.key_valid_of(attention_mask)
 
     delta = None
@@ -128,81 +405,10 @@ def fused_forward(model, input_ids, attention_mask, labels, num_items_in_batch=N
 
 
 def lora_parameters(model):
-    """The trainable tensors of `model`: (A_q, B_q, A_v, B_v) per layer."""
+    """The trainable tensors of a ModelWeights: (A_q, B_q, A_v, B_v) per layer."""
     out = []
     for w in model.layers:
-        out += [*w.lora_q, *w.lora_v]
+        for pair in (w.lora_q, w.lora_v):
+            if pair is not None:
+                out += list(pair)
     return out
-
-
-def synthetic_model(device, n_layers=28, vocab=workloads.VOCAB, hidden=workloads.HIDDEN,
-                    inter=workloads.INTER, n_heads=workloads.N_HEADS, n_kv=workloads.N_KV,
-                    head_dim=workloads.HEAD_DIM, rank=16, alpha=32, dropout=0.0, seed=11):
-    """A Qwen2.5-1.5B-shaped model (28 layers, tied 151,936 x 1536 embedding) with synthetic
-    NF4 projections (distinct per layer) and LoRA r=16 on q/v, for measurement."""
-    layers = [_layer.synthetic_layer(device, hidden, inter, n_heads, n_kv, head_dim, rank, alpha,
-                                     dropout, seed=seed * 1000 + i) for i in range(n_layers)]
-    g = workloads.gen(seed)
-    embed = (0.02 * torch.randn(vocab, hidden, generator=g)).to(torch.float16).to(device)
-    final = (1 + 0.02 * torch.randn(hidden, generator=g)).to(device)
-    return ModelWeights(embed=embed, layers=layers, final_norm=final,
-                        inv_freq=default_inv_freq(head_dim, workloads.ROPE_THETA, device))
-
-
-def _base_layer(module):
-    """The projection under a LoRA wrapper (peft's get_base_layer), else the module itself
-    (solution/model.py:54-56)."""
-    get = getattr(module, "get_base_layer", None)
-    return get() if callable(get) else module
-
-
-def from_qwen2(causal_lm, nf4_weights, lora, scaling, dropout=0.0):
-    """ModelWeights of a transformers Qwen2ForCausalLM (the unquantized parts: embedding, norms,
-    q/k/v biases, rotary frequencies), with the projections of layer i given in NF4 by
-    `nf4_weights[i]` (dict q, k, v, o, gate, up, down of Params4bit-like weights) and its LoRA
-    tensors by `lora[i]` ((A_q, B_q), (A_v, B_v)).  Checks the model is one the fused path runs
-    (the conditions of solution/model.py:125-149: full attention, silu, no MLP bias, q/k/v
-    biases all present or all absent, an untied or tied head without bias)."""
-    cfg = causal_lm.config
-    inner = causal_lm.model
-    if getattr(cfg, "hidden_act", "silu") != "silu":
-        raise ValueError("activation is not silu")
-    if any(t != "full_attention" for t in (getattr(cfg, "layer_types", None) or [])):
-        raise ValueError("sliding-window layers")
-    n_heads, n_kv = cfg.num_attention_heads, cfg.num_key_value_heads
-    head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // n_heads
-    layers = []
-    for i, lyr in enumerate(inner.layers[:cfg.num_hidden_layers]):
-        attn, mlp = lyr.self_attn, lyr.mlp
-        q, k, v, o, gate, up, down = (_base_layer(m) for m in (
-            attn.q_proj, attn.k_proj, attn.v_proj, attn.o_proj, mlp.gate_proj, mlp.up_proj,
-            mlp.down_proj))
-        if any(getattr(m, "bias", None) is not None for m in (gate, up, down)):
-            raise ValueError("MLP bias")
-        biases = [q.bias, k.bias, v.bias]
-        if all(b is not None for b in biases):
-            qkv_bias = torch.cat([b.detach().to(torch.float16) for b in biases])
-        elif all(b is None for b in biases):
-            qkv_bias = None
-        else:
-            raise ValueError("mixed q/k/v bias")
-        if o.bias is not None:
-            raise ValueError("o_proj bias")
-        nw = nf4_weights[i]
-        layers.append(_layer.LayerWeights(
-            input_norm=lyr.input_layernorm.weight.detach().float(),
-            post_norm=lyr.post_attention_layernorm.weight.detach().float(),
-            q=nw["q"], k=nw["k"], v=nw["v"], o=nw["o"], gate=nw["gate"], up=nw["up"],
-            down=nw["down"], qkv_bias=qkv_bias, lora_q=tuple(lora[i][0]),
-            lora_v=tuple(lora[i][1]), scaling=scaling, n_heads=n_heads, n_kv=n_kv,
-            head_dim=head_dim, eps=lyr.input_layernorm.variance_epsilon, dropout=dropout))
-    head = causal_lm.lm_head.weight
-    embed = inner.embed_tokens.weight.detach().to(torch.float16)
-    tied = head.data_ptr() == inner.embed_tokens.weight.data_ptr()
-    rot = getattr(inner, "rotary_emb", None)
-    inv_freq = rot.inv_freq.detach().float() if rot is not None else \
-        default_inv_freq(head_dim, getattr(cfg, "rope_theta", 10000.0), embed.device)
-    return ModelWeights(embed=embed, layers=layers,
-                        final_norm=inner.norm.weight.detach().float(), inv_freq=inv_freq,
-                        eps=inner.norm.variance_epsilon,
-                        head=None if tied else head.detach().to(torch.float16))

@@ -280,10 +280,11 @@ class _GroupPlan:
             H = a_q.shape[1]
             NQ, NV = _lora._check_params(*lora_params, H, device)
             extra = _lora.staged_elems(H, NQ, NV)
-        # (the staged parameters start on a 16-byte boundary, as the kernel requires)
-        st_off = (self.total + 7) // 8 * 8
-        buf = torch.empty(st_off + extra if extra else self.total, dtype=torch.float16,
-                          device=device)
+        buf = torch.empty(self.total, dtype=torch.float16, device=device)
+        # The staged parameters get an allocation of their own (304 KB at Qwen2.5-1.5B's
+        # shapes): the LoRA backward keeps them, and a view into `buf` would keep all seven
+        # fp16 projections (94 MB per layer) alive with them until that layer's backward.
+        staged = torch.empty(extra, dtype=torch.float16, device=device) if extra else None
         base = buf.data_ptr()
         stream = _ext.stream_of(buf)
         last = len(self.launches) - 1
@@ -293,14 +294,14 @@ class _GroupPlan:
                     ctypes.addressof(sizes), self.qblock, self.qblock2)
             if extra and c == last:
                 _ext.call("soupk_nf4_unpack_multi_lora", *args,
-                          *[p.data_ptr() for p in lora_params], base + 2 * st_off, extra,
+                          *[p.data_ptr() for p in lora_params], staged.data_ptr(), extra,
                           H, NQ, NV, _lora.RANK, stream)
             else:
                 _ext.call("soupk_nf4_unpack_multi", *args, stream)
         stacks = [buf[st:st + rows * cols].view(rows, cols) for st, rows, cols in self.stacks]
         if lora_params is None:
             return stacks
-        return stacks, buf[st_off:]
+        return stacks, staged
 
 
 def _group_plan(groups, device, flat_w, offsets, stacks, total):
