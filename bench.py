@@ -215,26 +215,34 @@ def build_cases(dev, n_sets=None, lib=None):
                       M * I * 2 + 2 * (M * 2 * I * 2), bsets, cpu=lambda ob: swi_cpu(ob, True),
                       lib=lib))
 
-    # vocab head: one 256-row chunk of logits [256, 151936]
+    # vocab head: one 256-row chunk of logits [256, 151936].  Timed through
+    # soupk_head_stats_grad_rows (the form FusedHeadLoss calls) with the identity row map into
+    # a gradient buffer of its own: the same kernel and the same bytes as the in-place
+    # soupk_head_stats_grad (each labelled row read once and its gradient written once), but
+    # the logits stay logits from one use of a set to the next (in place, every launch after a
+    # set's first would run on the previous launch's gradient values, which are ~1e-7).
     sets = []
     rows, V = 256, workloads.VOCAB
     n_lab = 0
     for i in range(rotation_sets(rows * V * 2, n_sets)):
         z, tgt = workloads.head_logits(rows, V, seed=8 + 10 * i, device=dev)
+        slot = torch.where(tgt != -100, torch.arange(rows, device=dev), -1).to(torch.int32)
+        gbuf = torch.empty((rows, V), dtype=torch.float16, device=dev)
         ent = torch.empty(rows, dtype=torch.float32, device=dev)
         loss = torch.empty(rows, dtype=torch.float32, device=dev)
         cor = torch.empty(rows, dtype=torch.int32, device=dev)
-        sets.append(((z, tgt, ent, loss, cor),
-                     (p(z), p(tgt), p(ent), p(loss), p(cor), None, 64.0 / 1843.0, rows, V)))
+        sets.append(((z, tgt, slot, gbuf, ent, loss, cor),
+                     (p(z), p(tgt), p(slot), p(gbuf), rows, p(ent), p(loss), p(cor), None,
+                      64.0 / 1843.0, rows, V)))
         if i == 0:
             n_lab = int((tgt != -100).sum())
     def head_cpu(ob):
         zc, tc = workloads.head_logits(rows, V, seed=8)
         return lambda: ob.head_stats_grad(zc, tc, 64.0 / 1843.0)
 
-    cases.append(Case("head_stats_grad", "head_stats_grad_kernel", "soupk_head_stats_grad",
-                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 12 * rows, sets, cpu=head_cpu,
-                      lib=lib))
+    cases.append(Case("head_stats_grad", "head_stats_grad_kernel", "soupk_head_stats_grad_rows",
+                      rows * V * 2 + n_lab * V * 2 + 8 * rows + 4 * rows + 12 * rows, sets,
+                      cpu=head_cpu, lib=lib))
     return cases
 
 
@@ -876,8 +884,39 @@ def copy_reference(cases, dev, reps=60, pool_mib=768):
     return out
 
 
-def copy_peak(dev, mib=1024, reps=6):
-    """Read+write GB/s of torch's device copy of `mib` MiB (the box's plain-copy reference)."""
+def copy_peak(dev, mib=1024, reps=12):
+    """Read+write GB/s of the fastest plain streaming copy measured on this GPU
+    (soupk_bench_copy: one 16-byte chunk per thread, non-temporal load, nt sc1 store) moving
+    `mib` MiB, timed like the kernels (dispatch-recorded events, back to back behind a device
+    wait); the median of `reps` launches."""
+    lib = _ext.lib()
+    size = mib << 20
+    src = torch.empty(size, dtype=torch.uint8, device=dev)
+    dst = torch.empty(size, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    hip = HipEvents()
+    holder = DeviceHold(dev)
+    evs = [(hip.new(), hip.new()) for _ in range(reps)]
+    for _ in range(2):
+        lib.soupk_bench_copy(src.data_ptr(), dst.data_ptr(), size, sh)
+    torch.cuda.synchronize(dev)
+    holder.hold(500.0 * reps + 2000.0)
+    for a, b in evs:
+        lib.soupk_time_next_launch(a, b)
+        st = lib.soupk_bench_copy(src.data_ptr(), dst.data_ptr(), size, sh)
+        if st:
+            raise _ext.SoupkError(f"soupk_bench_copy failed with status {st}")
+    torch.cuda.synchronize(dev)
+    us = median([hip.elapsed_us(a, b) for a, b in evs])
+    hip.close()
+    del src, dst
+    return round(2 * size / (us * 1e-6) / 1e9, 1)
+
+
+def torch_copy_GBps(dev, mib=1024, reps=6):
+    """Read+write GB/s of torch's device copy (copy_, __amd_rocclr_copyBuffer) of `mib` MiB;
+    the 1 GiB copy whose PMC counters scale the traffic table (summarize_pmc)."""
     n = mib * (1 << 20) // 4
     a = torch.ones(n, device=dev)
     b = torch.empty(n, device=dev)
@@ -1123,7 +1162,7 @@ def summarize_step(trace_csv, title, command, n_layers=28, top=32):
 def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     """Markdown table of HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then
     WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the 1 GiB device
-    copy that bench.py's copy_peak() makes (torch's copy_ -> __amd_rocclr_copyBuffer).  Launches
+    copy that bench.py's torch_copy_GBps() makes (torch's copy_ -> __amd_rocclr_copyBuffer).  Launches
     are grouped by kernel and grid and named by the bench entry they belong to."""
     bench = json.loads(open(bench_json).read().strip().splitlines()[-1])
     fetch, write = _read_csv(fetch_csv), _read_csv(write_csv)
@@ -1141,7 +1180,7 @@ def summarize_pmc(fetch_csv, write_csv, bench_json, commands):
     out = ["# HBM traffic per launch (rocprofv3 PMC): kernel set at the 2048-token step", "",
            "Commands (run from /tmp on the MI355X box, TMPDIR=/tmp), one counter per pass:", "",
            "```", *commands, "```", "",
-           f"Scale factors from the 1 GiB device copy of `bench.py` (`copy_peak`, "
+           f"Scale factors from the 1 GiB device copy of `bench.py` (`torch_copy_GBps`, "
            f"`__amd_rocclr_copyBuffer`, {len(copies)} dispatches): FETCH_SIZE reads "
            f"{f_copy:.0f} KiB for 1048576 KiB read -> x{f_scale:.4f}; WRITE_SIZE reads "
            f"{w_copy:.0f} KiB for 1048576 KiB written -> x{w_scale:.4f}.", "",
@@ -1305,6 +1344,7 @@ def main():
     floor = build_floor_cases(dev)
     time_gpu(floor, args.steps, args.warmup, dev)
     copy_gbps = copy_peak(dev)
+    torch_copy_gbps = torch_copy_GBps(dev)
     copy_us = copy_reference(cases, dev)
     attn_t = None
     if not args.no_layer:
@@ -1427,6 +1467,7 @@ def main():
         "step": step_t,
         "step_reference_profile": step_ref,
         "copy_peak_GBps": copy_gbps,
+        "torch_copy_GBps": torch_copy_gbps,
         "copy_reference": "kernels[*].copy_us: a plain 16-byte streaming device copy "
                           "(one chunk per thread, non-temporal load, nt|sc1 store) "
                           "(soupk_bench_copy) moving the kernel's algorithmic bytes, half read "
