@@ -343,6 +343,24 @@ int soupk_lora_fwd(const uint16_t* y, const uint16_t* staged, float scaling, uin
                    int32_t r, void* stream);
 
 /*
+ * The forward fused with the RoPE pack of the varlen attention (replaces soupk_lora_fwd followed
+ * by soupk_rope_pack_tokens on the layer's path; the reference's rope_pack_fwd_kernel,
+ * solution/rope.py:24-75, in the token-major layout of soupk_rope_pack_tokens).  qkv
+ * [M, (NH + 2*NKV)*128] fp16 is the q|k|v GEMM output, cos/sin [>= T, 128] fp32, pos int64 [M]
+ * (padded positions b*T + t).  Writes t as soupk_lora_fwd does and
+ * out [M, (NH + 2*NKV)*128] fp16 = rotated(q + lq) | rotated(k) | v + lv, with lq, lv the deltas
+ * soupk_lora_fwd would write (NQ = NH*128, NV = NKV*128) and the rotation of
+ * soupk_rope_pack_tokens: the same bits as that pair of launches, without lq / lv in memory.  A
+ * row whose position lies outside [0, B*T) gets zeros.  D must be 128, r 16, H a multiple of 128;
+ * pointers 16-byte aligned (t, pos: element-aligned); M*(NH + 2*NKV)*256 < 2^32 bytes.
+ */
+int soupk_lora_rope_fwd(const uint16_t* y, const uint16_t* staged, float scaling,
+                        const uint16_t* qkv, const float* cos, const float* sin,
+                        const int64_t* pos, uint16_t* t, uint16_t* out, int64_t M, int32_t H,
+                        int32_t NH, int32_t NKV, int32_t D, int32_t r, int32_t B, int32_t T,
+                        void* stream);
+
+/*
  * Its backward, the row-local part: with g_q [M, NQ] (row stride ld_q) and g_v [M, NV] (ld_v)
  * the fp16 gradients of lq and lv, and the forward's `staged` parameters, writes
  * dt = fp16([gs_q b_q16 | gs_v b_v16]) [M, 32], gs_x = fp16(g_x * scaling) (formed in

@@ -88,6 +88,18 @@ def test_version_and_status_strings(lib):
      (16, 32, 48, 64, 128, 100, 256, 128, 128, 16, None)),
     ("soupk_nf4_unpack_multi_lora", (0,) + (None,) * 8 + (64, 256) +
      (16, 32, 48, 64, 136, 1 << 20, 256, 128, 128, 16, None)),            # misaligned staged
+    # the LoRA forward fused with the RoPE pack: head dim other than 128, no position rows, a
+    # rank other than 16, null pointers, a misaligned output
+    ("soupk_lora_rope_fwd", (16, 32, 2.0, 48, 64, 80, 96, 112, 128, 4, 256, 2, 1, 64, 16, 1, 4,
+                             None)),
+    ("soupk_lora_rope_fwd", (16, 32, 2.0, 48, 64, 80, 96, 112, 128, 4, 256, 2, 1, 128, 16, 1, 0,
+                             None)),
+    ("soupk_lora_rope_fwd", (16, 32, 2.0, 48, 64, 80, 96, 112, 128, 4, 256, 2, 1, 128, 8, 1, 4,
+                             None)),
+    ("soupk_lora_rope_fwd", (None, 32, 2.0, 48, 64, 80, 96, 112, 128, 4, 256, 2, 1, 128, 16, 1,
+                             4, None)),
+    ("soupk_lora_rope_fwd", (16, 32, 2.0, 48, 64, 80, 96, 112, 136, 4, 256, 2, 1, 128, 16, 1, 4,
+                             None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

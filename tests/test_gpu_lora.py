@@ -166,3 +166,72 @@ def test_lora_bwd_params_no_rows():
                                                           device=DEV), 2.0)
     for x in out:
         assert torch.equal(x, torch.zeros_like(x))
+
+
+def _bits(t):
+    return t.detach().contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("lengths,T,NH,NKV,scaling", [
+    ((512, 512, 512, 512), 512, 12, 2, 2.0),      # the step shape (M = 2048)
+    ((512, 152, 128, 96), 512, 12, 2, 2.0),       # the BASELINE ragged batch (M = 888)
+    ((17,), 40, 4, 2, 0.7),                        # one partial row block, a second part
+    ((33, 0, 20), 64, 2, 1, 1.0)])                 # an empty row, one head pair per part
+def test_lora_rope_fwd_matches_lora_then_rope(lengths, T, NH, NKV, scaling):
+    """soupk_lora_rope_fwd writes t as soupk_lora_fwd does and the rows
+    soupk_rope_pack_tokens writes from lora_fwd's lq / lv: both bit for bit.  One position is
+    made invalid: its row is zeros in both."""
+    print(f"lora+rope fwd lengths={lengths} T={T} NH={NH} NKV={NKV} s={scaling}", flush=True)
+    from testt_amd import rope
+
+    D, H = 128, 512 if NH < 12 else 1536
+    NQ, NV = NH * D, NKV * D
+    a_q, a_v, b_q, b_v = params(H, NQ, NV, sum(lengths) + NH)
+    qkv, _, _, pos = workloads.rope_inputs(lengths, T, NH, NKV, D, seed=T + NH, device=DEV)
+    M = pos.numel()
+    if M > 3:
+        pos[3] = -1
+    g = torch.Generator().manual_seed(M)
+    y = torch.randn(M, H, generator=g).to(torch.float16).to(DEV)
+    cos, sin = workloads.rope_tables(T, D, workloads.ROPE_THETA, device=DEV)
+    B = len(lengths)
+    st = lora.stage(a_q, a_v, b_q, b_v)
+    t_ref, lq, lv = lora.lora_fwd(y, a_q, a_v, b_q, b_v, scaling, staged=st)
+    rows_ref, _, _, _ = rope.rope_pack_tokens(qkv, lq, lv, cos, sin, pos, B, T, NH, NKV, D)
+    t, rows, _, _, _ = lora.lora_rope_fwd(y, a_q, a_v, b_q, b_v, scaling, qkv, cos, sin, pos, B,
+                                          T, NH, NKV, staged=st)
+    assert torch.equal(_bits(t), _bits(t_ref))
+    assert torch.equal(_bits(rows), _bits(rows_ref))
+    if M > 3:
+        assert not bool(rows[3].any())
+
+
+@pytest.mark.parametrize("lengths", [(512, 512, 512, 512), (512, 152, 128, 96), (40, 0, 7)])
+def test_fused_lora_rope_layer_matches_unfused(monkeypatch, lengths):
+    """decoder_layer with the q|k|v GEMM, LoRA + RoPE and attention in one node
+    (QKVLoraRopeAttention) against QKVLora followed by RopeAttention: the layer's outputs and
+    the gradients of the input and of every LoRA parameter are bit-identical."""
+    print(f"fused LoRA+RoPE layer lengths={lengths}", flush=True)
+    w = layer.synthetic_layer(DEV, seed=9)
+    B, T = len(lengths), max(max(lengths), 1)
+    pos = workloads.ragged_positions(lengths, T).to(DEV)
+    M = pos.numel()
+    g = torch.Generator().manual_seed(M)
+    s0 = torch.randn(M, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(M, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(M, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(M, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    cos, sin = workloads.rope_tables(T, workloads.HEAD_DIM, workloads.ROPE_THETA, device=DEV)
+    results = []
+    for fused in (True, False):
+        monkeypatch.setattr(layer, "FUSE_LORA_ROPE", fused)
+        s = s0.clone().requires_grad_(True)
+        d = d0.clone().requires_grad_(True)
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+        so, do = layer.decoder_layer(s, d, w, pos, B, T, cos, sin, None)
+        torch.autograd.backward([so, do], [gs, gd])
+        results.append([so, do, s.grad, d.grad] + [p.grad.clone() for p in (*w.lora_q,
+                                                                              *w.lora_v)])
+    for name, a, b in zip(("s", "d", "ds", "dd", "dA_q", "dB_q", "dA_v", "dB_v"), *results):
+        assert torch.equal(a.detach(), b.detach()), name

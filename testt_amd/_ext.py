@@ -58,6 +58,8 @@ SIGNATURES = {
                                    _i64, _i32, _i32, _i32, _f32, _p],
     "soupk_lora_stage": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
     "soupk_lora_fwd": [_p, _p, _f32, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _p],
+    "soupk_lora_rope_fwd": [_p, _p, _f32, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32,
+                            _i32, _i32, _i32, _p],
     "soupk_lora_bwd_rows": [_p, _i64, _p, _i64, _p, _f32, _p, _p, _i64, _i32, _i32, _i32, _i32,
                             _p],
     "soupk_lora_bwd_params": [_p, _p, _p, _p, _i64, _p, _i64, _f32, _p, _i64, _p, _p, _p, _p,

@@ -42,6 +42,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "fastdiv.hpp"
 #include "lora_stage.hpp"
 #include "soupk_common.hpp"
 
@@ -103,9 +104,32 @@ __global__ __launch_bounds__(256) void lora_stage_kernel(LoraStageArgs a) {
 // The parameter and activation pointers of the row kernels are not __restrict__: loads through
 // restrict pointers are taken as invariant and moved to their use, which would undo the
 // prefetch of the next batch.
+// The fused LoRA + RoPE form of the forward (ROPE = true): instead of lq and lv it writes the
+// rows the varlen attention reads, out = [rotated q + lq | rotated k | v + lv] in the q|k|v
+// GEMM's own layout [M, NQ + NK + NV] (head dim 128), with the arithmetic of
+// soupk_rope_pack_tokens: x = fp32(qkv) + fp32(fp16 LoRA delta), then
+// (x1*c1 - x2*s1, x2*c2 + x1*s2) with each product rounded, then fp16.  The LoRA tiles of a
+// head's dims d..d+15 and d+64..d+79 (the rotation partners) are tiles j and j + 4 of the head's
+// eight, which the same wavefront computes as items u and u + 1 of a batch (a wavefront takes
+// every fourth tile, and the column parts split the tiles at whole heads), so a lane holds
+// both partners of its four dims.  The k columns are extra tiles with no LoRA product.
+struct LoraRope {
+  const uint16_t* qkv;   // [M, W] q|k|v GEMM output, W = NQ + NK + NV
+  uint16_t* out;         // [M, W]
+  const float* cos_t;    // [T, 128]
+  const float* sin_t;    // [T, 128]
+  const int64_t* pos;    // [M] padded position of each row, b * T + t
+  int NK;                // key columns (NKV * 128): rotation only
+  int T;
+  int64_t slots;         // B * T (< 2^31)
+  FastDiv per_seq;       // divides by T
+};
+
+template <bool ROPE>
 __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
     const uint16_t* y, const _Float16* staged, float scaling, uint16_t* __restrict__ t_out,
-    uint16_t* __restrict__ lq, uint16_t* __restrict__ lv, int M, int H, int NQ, int NV) {
+    uint16_t* __restrict__ lq, uint16_t* __restrict__ lv, int M, int H, int NQ, int NV,
+    LoraRope ra) {
   const StagedLayout L = staged_layout(H, NQ, NV);
   const _Float16* a16 = staged + L.a16;
   const _Float16* b16 = staged + L.b16;
@@ -117,19 +141,43 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
   // Output tiles of this wavefront (phase 2): their B16 fragments do not depend on t, so the
   // first batch is loaded now and arrives while t is computed.
   const int nq16 = NQ / 16;
-  const int t_begin = tile_part(NQ / 16 + NV / 16, blockIdx.y, gridDim.y);
-  const int n16 = tile_part(NQ / 16 + NV / 16, blockIdx.y + 1, gridDim.y);
-  auto load_b = [&](h4* bw, int t0) {
+  const int nlora = NQ / 16 + NV / 16;
+  int t_begin, n16;
+  if constexpr (ROPE) {   // whole heads (8 tiles) per column part
+    const int heads = (nlora + ra.NK / 16) / 8;
+    t_begin = 8 * tile_part(heads, blockIdx.y, gridDim.y);
+    n16 = 8 * tile_part(heads, blockIdx.y + 1, gridDim.y);
+  } else {
+    t_begin = tile_part(nlora, blockIdx.y, gridDim.y);
+    n16 = tile_part(nlora, blockIdx.y + 1, gridDim.y);
+  }
+  const int W = NQ + ra.NK + NV;
+  // (ROPE) the output column of tile `tile`: q tiles, then v tiles, then k tiles
+  auto tile_col = [&](int tile) {
+    return tile < nq16 ? 16 * tile
+                       : (tile < nlora ? NQ + ra.NK + 16 * (tile - nq16) : NQ + 16 * (tile - nlora));
+  };
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  auto load_b = [&](h4* bw, u32x2v (*xq)[kRowTiles], int t0) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       // B16 row of output tile column ql (the v rows follow the q rows)
       const int tile = min(t0 + 4 * u, max(n16 - 1, 0));
-      bw[u] = *reinterpret_cast<const h4*>(b16 + static_cast<int64_t>(16 * tile + ql) * kR +
+      const int bt = ROPE ? min(tile, nlora - 1) : tile;
+      bw[u] = *reinterpret_cast<const h4*>(b16 + static_cast<int64_t>(16 * bt + ql) * kR +
                                            4 * gr);
+      if constexpr (ROPE) {   // this lane's four columns of the GEMM output
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          const int64_t m = min(m0 + 16 * rt + ql, M - 1);
+          xq[u][rt] = *reinterpret_cast<const u32x2v*>(ra.qkv + m * W + tile_col(tile) + 4 * gr);
+        }
+      }
     }
   };
   h4 bw_next[kBatch];
-  if (t_begin + w < n16) load_b(bw_next, t_begin + w);
+  u32x2v xq_next[kBatch][kRowTiles];
+  if (t_begin + w < n16) load_b(bw_next, xq_next, t_begin + w);
   // t = y A^T: A operand = y rows (row 16rt + ql of row tile rt, k = k0 + 8gr..+7); B operand =
   // A_q / A_v rows (column = feature ql), loaded once per step for the kRowTiles row tiles.
   // The contraction over H is split over the 4 wavefronts; batches of kBatch steps, the next
@@ -223,42 +271,122 @@ __global__ __launch_bounds__(kThreads) void lora_fwd_kernel(
                  static_cast<_Float16>(tv[2]), static_cast<_Float16>(tv[3])};
     row_ok[rt] = m0 + 16 * rt + ql < M;
   }
-  auto out_tiles = [&](const h4* bw, int t0) {
+  // (ROPE) per lane: the position of its rows and the table entries of its dims d .. d+3 and
+  // d+64 .. d+67, d = 16w + 4gr (every tile pair this wavefront takes is j = w, j + 4 of a head)
+  f4 cs1[kRowTiles], cs2[kRowTiles], sn1[kRowTiles], sn2[kRowTiles];
+  bool pos_ok[kRowTiles];
+  if constexpr (ROPE) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int tile = t0 + 4 * u;
-      if (tile >= n16) break;
-      const bool is_q = tile < nq16;
-      const int f0 = 16 * (is_q ? tile : tile - nq16);
-      const int N = is_q ? NQ : NV;
-      const h4 a = bw[u];
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      const int64_t p = ra.pos[min(m0 + 16 * rt + ql, M - 1)];
+      pos_ok[rt] = p >= 0 && p < ra.slots;
+      const uint32_t pu = pos_ok[rt] ? static_cast<uint32_t>(p) : 0u;
+      const uint32_t t = pu - ra.per_seq.div(pu) * static_cast<uint32_t>(ra.T);
+      const int64_t e = static_cast<int64_t>(t) * 128 + 16 * w + 4 * gr;
+      cs1[rt] = *reinterpret_cast<const f4*>(ra.cos_t + e);
+      cs2[rt] = *reinterpret_cast<const f4*>(ra.cos_t + e + 64);
+      sn1[rt] = *reinterpret_cast<const f4*>(ra.sin_t + e);
+      sn2[rt] = *reinterpret_cast<const f4*>(ra.sin_t + e + 64);
+    }
+  }
+  // fp16(fp16(c) * scaling), the LoRA delta as peft's fp16 matmul and scaling round it (the
+  // empty asm keeps the multiply and the fp16 conversion from fusing into one rounding)
+  auto delta = [&](float c) {
+    float v = r16(c) * scaling;
+    asm("" : "+v"(v));
+    return r16(v);
+  };
+  auto out_tiles = [&](const h4* bw, u32x2v (*xq)[kRowTiles], int t0) {
+    if constexpr (ROPE) {
+      const StreamOut out(ra.out, static_cast<uint64_t>(M) * W * 2u);
 #pragma unroll
-      for (int rt = 0; rt < kRowTiles; ++rt) {
-        const f4 c = mfma16(a, is_q ? tq4[rt] : tv4[rt], f4{0.f, 0.f, 0.f, 0.f});
-        // C: column = row 16rt + ql, rows = features f0 + 4gr .. +3
-        if (row_ok[rt]) {
-          uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + 16 * rt + ql) * N + f0 +
-                          4 * gr;
-          *reinterpret_cast<u32x2*>(dst) =
-              u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
-                    pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+      for (int pr = 0; pr < kBatch / 2; ++pr) {
+        const int tile = t0 + 8 * pr;          // dims d of a head; tile + 4: dims d + 64
+        if (tile >= n16) break;
+        const bool is_q = tile < nq16, is_k = tile >= nlora;
+        const int col = tile_col(tile);
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          const u32x2v a2 = xq[2 * pr][rt], b2 = xq[2 * pr + 1][rt];
+          float x1[4] = {lo_h(a2.x), hi_h(a2.x), lo_h(a2.y), hi_h(a2.y)};
+          float x2[4] = {lo_h(b2.x), hi_h(b2.x), lo_h(b2.y), hi_h(b2.y)};
+          if (!is_k) {
+            const h4 tr = is_q ? tq4[rt] : tv4[rt];
+            const f4 c1 = mfma16(bw[2 * pr], tr, f4{0.f, 0.f, 0.f, 0.f});
+            const f4 c2 = mfma16(bw[2 * pr + 1], tr, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              x1[i] = x1[i] + delta(c1[i]);
+              x2[i] = x2[i] + delta(c2[i]);
+            }
+          }
+          if (is_q || is_k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float r1 = x1[i] * cs1[rt][i] - x2[i] * sn1[rt][i];
+              const float r2 = x2[i] * cs2[rt][i] + x1[i] * sn2[rt][i];
+              x1[i] = r1;
+              x2[i] = r2;
+            }
+          }
+          if (!pos_ok[rt]) {     // a row with no place: zeros, as soupk_rope_pack_tokens
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x1[i] = x2[i] = 0.f;
+          }
+          if (row_ok[rt]) {
+            const uint32_t off =
+                (static_cast<uint32_t>(m0 + 16 * rt + ql) * W + col + 4 * gr) * 2u;
+            out.store(off, u32x2{pack_h2(x1[0], x1[1]), pack_h2(x1[2], x1[3])});
+            out.store(off + 128u, u32x2{pack_h2(x2[0], x2[1]), pack_h2(x2[2], x2[3])});
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int tile = t0 + 4 * u;
+        if (tile >= n16) break;
+        const bool is_q = tile < nq16;
+        const int f0 = 16 * (is_q ? tile : tile - nq16);
+        const int N = is_q ? NQ : NV;
+        const h4 a = bw[u];
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
+          const f4 c = mfma16(a, is_q ? tq4[rt] : tv4[rt], f4{0.f, 0.f, 0.f, 0.f});
+          // C: column = row 16rt + ql, rows = features f0 + 4gr .. +3
+          if (row_ok[rt]) {
+            uint16_t* dst = (is_q ? lq : lv) + static_cast<int64_t>(m0 + 16 * rt + ql) * N +
+                            f0 + 4 * gr;
+            *reinterpret_cast<u32x2*>(dst) =
+                u32x2{pack_h2(r16(c[0]) * scaling, r16(c[1]) * scaling),
+                      pack_h2(r16(c[2]) * scaling, r16(c[3]) * scaling)};
+          }
         }
       }
     }
   };
   h4 bw_cur[kBatch];
+  u32x2v xq_cur[kBatch][kRowTiles];
+  auto take = [&]() {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      bw_cur[u] = bw_next[u];
+      if constexpr (ROPE) {
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) xq_cur[u][rt] = xq_next[u][rt];
+      }
+    }
+  };
   for (int t0 = t_begin + w; t0 < n16; t0 += 8 * kBatch) {
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) bw_cur[u] = bw_next[u];
-    if (t0 + 4 * kBatch < n16) load_b(bw_next, t0 + 4 * kBatch);
+    take();
+    if (t0 + 4 * kBatch < n16) load_b(bw_next, xq_next, t0 + 4 * kBatch);
     issue_here();
-    out_tiles(bw_cur, t0);
+    out_tiles(bw_cur, xq_cur, t0);
     if (t0 + 4 * kBatch < n16) {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) bw_cur[u] = bw_next[u];
-      if (t0 + 8 * kBatch < n16) load_b(bw_next, t0 + 8 * kBatch);
+      take();
+      if (t0 + 8 * kBatch < n16) load_b(bw_next, xq_next, t0 + 8 * kBatch);
       issue_here();
-      out_tiles(bw_cur, t0 + 4 * kBatch);
+      out_tiles(bw_cur, xq_cur, t0 + 4 * kBatch);
     }
   }
 }
@@ -607,10 +735,42 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_fwd(
                         static_cast<const void*>(lq), static_cast<const void*>(lv)})
     if (misaligned(p)) return kInvalid;
   const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
-  return launch_kernel(lora_fwd_kernel, dim3(grid, column_parts(M, NQ / 16 + NV / 16)),
+  return launch_kernel(lora_fwd_kernel<false>, dim3(grid, column_parts(M, NQ / 16 + NV / 16)),
                        dim3(kThreads), static_cast<hipStream_t>(stream), y,
                        reinterpret_cast<const _Float16*>(staged), scaling, t, lq, lv,
-                       static_cast<int>(M), H, NQ, NV);
+                       static_cast<int>(M), H, NQ, NV, LoraRope{});
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_lora_rope_fwd(
+    const uint16_t* y, const uint16_t* staged, float scaling, const uint16_t* qkv,
+    const float* cos, const float* sin, const int64_t* pos, uint16_t* t, uint16_t* out,
+    int64_t M, int32_t H, int32_t NH, int32_t NKV, int32_t D, int32_t r, int32_t B, int32_t T,
+    void* stream) {
+  if (D != 128 || NH <= 0 || NKV <= 0 || B < 0 || T < 1) return kInvalid;
+  const int32_t NQ = NH * D, NV = NKV * D;
+  const int rc = check_dims(M, H, NQ, NV, r);
+  if (rc != kOk) return rc;
+  const int64_t W = static_cast<int64_t>(NQ) + 2 * NV;
+  const int64_t slots = static_cast<int64_t>(B) * T;
+  // (32-bit store offsets into `out`; positions split with a 31-bit divider)
+  if (M * W * 2 >= (int64_t{1} << 32) || slots >= (int64_t{1} << 31)) return kInvalid;
+  if (M == 0) return kOk;
+  if (!y || !staged || !qkv || !cos || !sin || !pos || !t || !out) return kInvalid;
+  for (const void* p : {static_cast<const void*>(y), static_cast<const void*>(staged),
+                        static_cast<const void*>(qkv), static_cast<const void*>(cos),
+                        static_cast<const void*>(sin), static_cast<const void*>(out)})
+    if (misaligned(p)) return kInvalid;
+  LoraRope ra{qkv, out, cos, sin, pos, NV, T, slots, FastDiv(static_cast<uint32_t>(T))};
+  // whole heads per column part (one part per head at most)
+  const int heads = static_cast<int>((W / 128));
+  const unsigned parts = std::min<unsigned>(column_parts(M, NQ / 16 + NV / 16),
+                                            static_cast<unsigned>(heads));
+  const unsigned grid = static_cast<unsigned>((M + kRows - 1) / kRows);
+  return launch_kernel(lora_fwd_kernel<true>, dim3(grid, parts), dim3(kThreads),
+                       static_cast<hipStream_t>(stream), y,
+                       reinterpret_cast<const _Float16*>(staged), scaling, t,
+                       static_cast<uint16_t*>(nullptr), static_cast<uint16_t*>(nullptr),
+                       static_cast<int>(M), H, NQ, NV, ra);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_rows(

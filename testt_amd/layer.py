@@ -187,6 +187,63 @@ class QKVLora(torch.autograd.Function):
         return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None, None
 
 
+# The rank-16 LoRA forward and the RoPE pack of the varlen attention in one launch
+# (soupk_lora_rope_fwd: the rotated q|k|v rows written directly, no lq / lv in memory and no
+# rope_pack_tokens launch), with the q|k|v GEMM, the LoRA and the attention in one autograd node
+# (QKVLoraRopeAttention).  False: QKVLora then attention.RopeAttention, bit-identical values.
+FUSE_LORA_ROPE = True
+
+
+class QKVLoraRopeAttention(torch.autograd.Function):
+    """out [M, NH*128] = varlen causal GQA attention of rotate(y @ [Wq;Wk;Wv]^T + b + LoRA), the
+    forward of QKVLora followed by attention.RopeAttention in one node, for rank-16 LoRA without
+    dropout and head dim 128: the q|k|v GEMM (hipBLASLt), soupk_lora_rope_fwd (t, and the
+    rotated rows with the LoRA deltas added), the varlen attention.  The backward is theirs:
+    the attention backward with RoPE's backward fused in gives the gradient of the q|k|v GEMM
+    output, whose q and v columns are the LoRA deltas' gradients (views, as RopePack's backward
+    returns them); then the LoRA backward and the frozen projection's input gradient."""
+
+    @staticmethod
+    def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16, staged, cos, sin,
+                pos_idx, cu_seqlens, batch, seq, n_heads, n_kv, scale):
+        w = w16 if w16 is not None else unpack_concat(weights, y16.device)
+        qkv = torch.nn.functional.linear(y16, w, bias)
+        keep_for_backward(ctx, w)
+        del w
+        params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
+        if staged is None:
+            staged = _lora.stage(*params)
+        t, qkv_r, cos32, sin32, pos = _lora.lora_rope_fwd(y16, *params, scaling, qkv, cos, sin,
+                                                          pos_idx, batch, seq, n_heads, n_kv,
+                                                          staged=staged)
+        del qkv
+        out, lse = _attention.attention_varlen_fwd(qkv_r, cu_seqlens, n_heads, n_kv, scale)
+        ctx.save_for_backward(y16, t, *params, staged, qkv_r, out, lse, cos32, sin32, pos,
+                              cu_seqlens)
+        ctx.weights, ctx.scaling = weights, scaling
+        ctx.dims = (batch, seq, n_heads, n_kv, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (y16, t, a_q, a_v, b_q, b_v, staged, qkv_r, out, lse, cos, sin, pos,
+         cu) = ctx.saved_tensors
+        batch, seq, n_heads, n_kv, scale = ctx.dims
+        dqkv = _attention.attention_varlen_bwd(qkv_r, cu, out, lse, dout, scale, n_heads, n_kv,
+                                               rope=(cos, sin, pos, batch, seq))
+        del qkv_r, out, lse
+        m, dev = y16.shape[0], y16.device
+        NQ, NV = b_q.shape[0], b_v.shape[0]
+        g_lq = _lora.rows_view(dqkv[:, :NQ], NQ, m, dev)
+        g_lv = _lora.rows_view(dqkv[:, NQ + NV:], NV, m, dev)
+        dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling, staged=staged)
+        # fp16 products cast to the fp32 parameters, as autocast's backward gives them
+        d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
+        w = unpacked_for_backward(ctx, ctx.weights, dev)
+        dy.addmm_(dqkv, w)
+        return (dy, None, d_aq, d_bq, d_av, d_bv) + (None,) * 13
+
+
 def lora_branch(y_pad, ab, scaling, dropout, batch, seq, pos_idx):
     """peft's B(A(dropout(x))) * scaling for the real tokens, fp16 matmuls (solution/model.py:
     195-206): the dropout runs on the padded fp32 norm output, A and B on the real rows.
@@ -272,16 +329,28 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     padded = batch * seq
     nh, nkv, hd = w.n_heads, w.n_kv, w.head_dim
     plain = lora_without_dropout(w)
+    params = (w.lora_q[0], w.lora_v[0], w.lora_q[1], w.lora_v[1]) if plain else None
     w_qkv = w_o = w_gu = w_d = staged = None
     if UNPACK_PER_LAYER:
         groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
-        params = (w.lora_q[0], w.lora_v[0], w.lora_q[1], w.lora_v[1]) if plain else None
         if plain and USE_FUSED_LORA and _lora.params_supported(*params, s.device):
             # the LoRA parameters' fp16 staging rides on the same launch as the unpack
             (w_qkv, w_o, w_gu, w_d), staged = unpack_groups_lora(
                 groups, s.device, tuple(p.detach() for p in params))
         else:
             w_qkv, w_o, w_gu, w_d = unpack_groups(groups, s.device)
+    if plain and FUSE_LORA_ROPE and USE_FUSED_LORA and USE_VARLEN_ATTENTION and \
+            hd == _attention.HEAD_DIM and nkv > 0 and nh % nkv == 0 and \
+            w.lora_q[1].shape[0] == nh * hd and w.lora_v[1].shape[0] == nkv * hd and \
+            _lora.params_supported(*params, s.device):
+        s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
+        cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
+        scale = 1.0 / math.sqrt(hd) if w.attn_scale is None else float(w.attn_scale)
+        a = QKVLoraRopeAttention.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
+                                       (w.q, w.k, w.v), w_qkv, staged, cos, sin, pos_idx, cu,
+                                       batch, seq, nh, nkv, scale)
+        del w_qkv, staged
+        return _layer_tail(s, a, w, w_o, w_gu, w_d)
     if plain:
         s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         qkv, lq, lv = QKVLora.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
@@ -313,6 +382,11 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
         del q, k, v
         if pos_idx.numel() != padded:       # nonzero() indices are sorted: all slots = identity
             a = a.index_select(0, pos_idx)
+    return _layer_tail(s, a, w, w_o, w_gu, w_d)
+
+
+def _layer_tail(s, a, w, w_o, w_gu, w_d):
+    """o-projection, residual add + post-attention RMSNorm, MLP: (s, d)."""
     o = frozen_linear(a, (w.o,), w.o_bias, w_o)
     del a, w_o
     s, y2, _ = add_rmsnorm(s, o, w.post_norm, w.eps)

@@ -100,6 +100,41 @@ def lora_fwd(y16, a_q, a_v, b_q, b_v, scaling, staged=None):
     return t, lq, lv
 
 
+def lora_rope_fwd(y16, a_q, a_v, b_q, b_v, scaling, qkv, cos, sin, pos_idx, batch, seq,
+                  n_heads, n_kv, staged=None):
+    """The LoRA forward fused with the RoPE pack of the varlen attention's rows
+    (soupk_lora_rope_fwd): t [M, 32] and out [M, (n_heads + 2 n_kv) * 128] fp16 = rotated
+    (q + lq) | rotated k | v + lv, where lq, lv are lora_fwd's deltas and qkv the q|k|v GEMM
+    output; the values of rope.rope_pack_tokens(qkv, lq, lv, ...) bit for bit, without lq and lv
+    in memory.  Returns (t, out, cos32, sin32, pos) (the tables and positions as the attention
+    backward takes them)."""
+    from . import rope as _rope
+
+    _ext.require(y16, "y16", dtype=torch.float16, ndim=2)
+    M, H = y16.shape
+    dev = y16.device
+    NQ, NV = _check_params(a_q, a_v, b_q, b_v, H, dev)
+    D = 128
+    if NQ != n_heads * D or NV != n_kv * D:
+        raise ValueError(f"B_q / B_v rows ({NQ}, {NV}) != heads x 128 ({n_heads * D}, {n_kv * D})")
+    width = NQ + 2 * NV
+    _ext.require(qkv, "qkv", dtype=torch.float16, ndim=2, device=dev)
+    if tuple(qkv.shape) != (M, width):
+        raise ValueError(f"qkv shape {tuple(qkv.shape)} != {(M, width)}")
+    pos = _rope.as_index(pos_idx)
+    if pos.numel() != M or pos.device != dev:
+        raise ValueError(f"pos_idx has {pos.numel()} entries on {pos.device} for {M} rows")
+    cos32 = _rope._table(cos, seq, D, "cos", dev)
+    sin32 = _rope._table(sin, seq, D, "sin", dev)
+    st = _staged(staged, a_q, a_v, b_q, b_v, H, NQ, NV, dev)
+    t = torch.empty((M, 2 * RANK), dtype=torch.float16, device=dev)
+    out = torch.empty((M, width), dtype=torch.float16, device=dev)
+    _ext.call("soupk_lora_rope_fwd", _ext.ptr(y16), _ext.ptr(st), float(scaling), _ext.ptr(qkv),
+              _ext.ptr(cos32), _ext.ptr(sin32), _ext.ptr(pos), _ext.ptr(t), _ext.ptr(out), M, H,
+              n_heads, n_kv, D, RANK, batch, seq, _ext.stream_of(y16))
+    return t, out, cos32, sin32, pos
+
+
 def _rows(g, n, m, dev):
     """g as an fp16 [m, n] view with unit column stride (zeros for a missing gradient)."""
     if g is None:
