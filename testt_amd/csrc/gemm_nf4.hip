@@ -31,8 +31,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kGThreads = 256;
+constexpr int kBK = 64;
 constexpr int kLds = kBK + 8;          // LDS row stride (halves)
 constexpr int kMaxParts = 4;
 
@@ -57,16 +56,6 @@ __device__ __forceinline__ f16v mfma32x32(h8 a, h8 b, f16v c) {
 
 __device__ __forceinline__ void issue_here() { __asm__ volatile("" ::: "memory"); }
 
-// Registers of one K tile for one thread: 4 x 16 bytes of x (rows tid/8 + 32j, chunk tid%8);
-// for W either 4 x 16 bytes of fp16 (same mapping) or 16 bytes of NF4 codes (row tid/2, codes
-// 32(tid%2) .. +31) and that row's block scale inputs.
-struct TileRegs {
-  u32x4 x[4];
-  u32x4 w[4];
-  uint32_t ablk;   // NF4: absmax_u8 of the block
-  float a2;        // NF4: absmax2 of the block's group
-};
-
 // Workgroups are dispatched to the 8 XCDs of the chip in turn (workgroup i to XCD i % 8), and
 // each XCD has its own L2.  Tile order: XCD j takes the j-th eighth of the tiles in row-major
 // (m-block, n-block) order, so the workgroups sharing an L2 work on few m-blocks -- their rows
@@ -81,26 +70,55 @@ __device__ __forceinline__ void tile_of(int wg, int n_blocks, int m_blocks, int&
   nb = t - mb * n_blocks;
 }
 
-template <bool NF4>
-__global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
+// Tile shape of one launch: a BM x BN block of y per workgroup, WM x WN wavefronts, each a
+// (BM/WM) x (BN/WN) tile of 32 x 32 MFMA tiles.
+template <int BM_, int BN_, int WM_, int WN_>
+struct GemmShape {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
+  static constexpr int FM = TM / 32, FN = TN / 32;   // 32 x 32 MFMA tiles per wave
+  static constexpr int XC = BM * 8 / kThreads;       // 16-byte x chunks per thread per K tile
+  static constexpr int WC = BN * 8 / kThreads;       // fp16 W chunks
+  static constexpr int NI = (BN * 4 + kThreads - 1) / kThreads;   // NF4: 16-code items
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tiles are whole 32 x 32 MFMA tiles");
+  static_assert(XC * kThreads == BM * 8 && WC * kThreads == BN * 8, "whole chunks per thread");
+};
+
+// Registers of one K tile for one thread: XC x 16 bytes of x (chunk c = tid + threads*j: row
+// c / 8, 8 halves at 8 * (c % 8)); for W either WC x 16 bytes of fp16 (same mapping) or NI items
+// of 16 NF4 codes (8 bytes; item i: row i / 4, codes 16 (i % 4) .. +15 of the row's 64-code
+// block) with the block's scale inputs.
+template <class S>
+struct TileRegs {
+  u32x4 x[S::XC];
+  u32x4 w[S::WC];
+  u32x2 c[S::NI];
+  uint32_t ablk[S::NI];   // NF4: absmax_u8 of the block
+  float a2[S::NI];        // NF4: absmax2 of the block's group
+};
+
+template <class S, bool NF4>
+__global__ __launch_bounds__(S::kThreads) void gemm_tn_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* w16, Nf4Weights nw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K) {
+  constexpr int BM = S::BM, BN = S::BN, T = S::kThreads;
   // Two LDS stages as separate arrays, so that the compiler sees the staging of one and the
   // MFMA reads of the other as independent and interleaves them.
-  __shared__ __align__(16) _Float16 Xs0[kBM * kLds];
-  __shared__ __align__(16) _Float16 Ws0[kBN * kLds];
-  __shared__ __align__(16) _Float16 Xs1[kBM * kLds];
-  __shared__ __align__(16) _Float16 Ws1[kBN * kLds];
+  __shared__ __align__(16) _Float16 Xs0[BM * kLds];
+  __shared__ __align__(16) _Float16 Ws0[BN * kLds];
+  __shared__ __align__(16) _Float16 Xs1[BM * kLds];
+  __shared__ __align__(16) _Float16 Ws1[BN * kLds];
   __shared__ float code2_s[256];
   __shared__ float2 pair_s[256];   // NF4: (nf4[b >> 4], nf4[b & 15]) of byte value b
   const int tid = threadIdx.x;
   int nb, mb;
-  tile_of(blockIdx.x, N / kBN, (M + kBM - 1) / kBM, nb, mb);
-  const int n0 = nb * kBN, m0 = mb * kBM;
+  tile_of(blockIdx.x, N / BN, (M + BM - 1) / BM, nb, mb);
+  const int n0 = nb * BN, m0 = mb * BM;
   const int lane = tid % kWave, wv = tid / kWave;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv / S::WN, wn = wv % S::WN;
 
-  // the weight part holding rows n0 .. n0 + 127, and the row of that part
+  // the weight part holding rows n0 .. n0 + BN - 1, and the row of that part
   int part = 0, prow0 = n0;
   if constexpr (NF4) {
     while (part + 1 < nw.n_parts && prow0 >= nw.part[part].rows) {
@@ -111,95 +129,117 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
   const Nf4Part P = nw.part[part];
   float offset = 0.f;
   if constexpr (NF4) {
-    code2_s[tid] = P.code2[tid];
-    pair_s[tid] = float2{P.nf4[tid >> 4], P.nf4[tid & 15]};
+    for (int i = tid; i < 256; i += T) {
+      code2_s[i] = P.code2[i];
+      pair_s[i] = float2{P.nf4[i >> 4], P.nf4[i & 15]};
+    }
     offset = P.offset[0];
   }
 
   const int KT = K / kBK;
-  auto load = [&](TileRegs& r, int kt) {
+  auto load = [&](TileRegs<S>& r, int kt) {
     const int k0 = kt * kBK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = tid / 8 + 32 * j, ch = tid % 8;
+    for (int j = 0; j < S::XC; ++j) {
+      const int c = tid + T * j, row = c / 8, ch = c % 8;
       const int64_t xr = min(m0 + row, M - 1);
       r.x[j] = *reinterpret_cast<const u32x4*>(x + xr * ldx + k0 + 8 * ch);
-      if constexpr (!NF4)
+    }
+    if constexpr (!NF4) {
+#pragma unroll
+      for (int j = 0; j < S::WC; ++j) {
+        const int c = tid + T * j, row = c / 8, ch = c % 8;
         r.w[j] = *reinterpret_cast<const u32x4*>(w16 + static_cast<int64_t>(n0 + row) * K + k0 +
                                                  8 * ch);
-    }
-    if constexpr (NF4) {
-      const int row = tid / 2, half = tid % 2;
-      const int64_t e0 = static_cast<int64_t>(prow0 + row) * K + k0;   // first element
-      r.w[0] = *reinterpret_cast<const u32x4*>(P.packed + e0 / 2 + 16 * half);
-      const int64_t blk = e0 / 64;
-      r.ablk = P.absmax_u8[blk];
-      r.a2 = P.absmax2[blk / 256];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < S::NI; ++j) {
+        const int it = min(tid + T * j, BN * 4 - 1), row = it / 4, q = it % 4;
+        const int64_t e0 = static_cast<int64_t>(prow0 + row) * K + k0;   // first element
+        r.c[j] = *reinterpret_cast<const u32x2*>(P.packed + e0 / 2 + 8 * q);
+        const int64_t blk = e0 / 64;
+        r.ablk[j] = P.absmax_u8[blk];
+        r.a2[j] = P.absmax2[blk / 256];
+      }
     }
   };
-  auto store = [&](const TileRegs& r, _Float16* Xs, _Float16* Ws) {
+  auto store = [&](const TileRegs<S>& r, _Float16* Xs, _Float16* Ws) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = tid / 8 + 32 * j, ch = tid % 8;
+    for (int j = 0; j < S::XC; ++j) {
+      const int c = tid + T * j, row = c / 8, ch = c % 8;
       *reinterpret_cast<u32x4*>(&Xs[row * kLds + 8 * ch]) = r.x[j];
-      if constexpr (!NF4) *reinterpret_cast<u32x4*>(&Ws[row * kLds + 8 * ch]) = r.w[j];
     }
-    if constexpr (NF4) {
-      const int row = tid / 2, half = tid % 2;
-      const float scale = code2_s[r.ablk] * r.a2 + offset;   // two roundings (no FMA)
-      const uint32_t words[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
-      uint32_t out[16];
+    if constexpr (!NF4) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const float2 v = pair_s[(words[q] >> (8 * b)) & 0xffu];
-          out[q * 4 + b] = pack_h2(v.x * scale, v.y * scale);
-        }
+      for (int j = 0; j < S::WC; ++j) {
+        const int c = tid + T * j, row = c / 8, ch = c % 8;
+        *reinterpret_cast<u32x4*>(&Ws[row * kLds + 8 * ch]) = r.w[j];
       }
-      _Float16* dst = &Ws[row * kLds + 32 * half];
+    } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<u32x4*>(dst + 8 * q) =
-            u32x4{out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]};
+      for (int j = 0; j < S::NI; ++j) {
+        const int it = tid + T * j;
+        if (S::NI * T > BN * 4 && it >= BN * 4) break;
+        const int row = it / 4, q = it % 4;
+        const uint32_t words[2] = {r.c[j].x, r.c[j].y};
+        // All eight (nf4[hi], nf4[lo]) lookups and the scale's code2 lookup are issued before
+        // any is used: left to itself the compiler issued them one at a time, each waiting for
+        // its own LDS round trip.
+        float2 v[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) v[h * 4 + b] = pair_s[(words[h] >> (8 * b)) & 0xffu];
+        const float c2 = code2_s[r.ablk[j]];
+        __builtin_amdgcn_sched_barrier(0);
+        const float scale = c2 * r.a2[j] + offset;   // two roundings (no FMA)
+        uint32_t out[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = pack_h2(v[k].x * scale, v[k].y * scale);
+        _Float16* dst = &Ws[row * kLds + 16 * q];
+        *reinterpret_cast<u32x4*>(dst) = u32x4{out[0], out[1], out[2], out[3]};
+        *reinterpret_cast<u32x4*>(dst + 8) = u32x4{out[4], out[5], out[6], out[7]};
+      }
     }
   };
 
-  f16v acc[2][2];
+  f16v acc[S::FM][S::FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < S::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < S::FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   auto compute = [&](const _Float16* Xs, const _Float16* Ws) {
-    const _Float16* xa = &Xs[(64 * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
-    const _Float16* wb = &Ws[(64 * wn + (lane % 32)) * kLds + 8 * (lane / 32)];
+    const _Float16* xa = &Xs[(S::TM * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
+    const _Float16* wb = &Ws[(S::TN * wn + (lane % 32)) * kLds + 8 * (lane / 32)];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      h8 a[2], b[2];
+      h8 a[S::FM], b[S::FN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < S::FM; ++i)
         a[i] = *reinterpret_cast<const h8*>(xa + 32 * i * kLds + 16 * ks);
-        b[i] = *reinterpret_cast<const h8*>(wb + 32 * i * kLds + 16 * ks);
-      }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < S::FN; ++j)
+        b[j] = *reinterpret_cast<const h8*>(wb + 32 * j * kLds + 16 * ks);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32(a[i], b[j], acc[i][j]);
+      for (int i = 0; i < S::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma32x32(a[i], b[j], acc[i][j]);
     }
   };
 
   // Software pipeline: at step kt the MFMAs read stage kt % 2 while the registers of tile
   // kt + 1 (loaded a step earlier) are dequantised / written into the other stage and the
   // global loads of tile kt + 2 are issued; one barrier per step.
-  TileRegs ra, rb;
+  TileRegs<S> ra, rb;
   load(ra, 0);
   if constexpr (NF4) __syncthreads();   // code2_s / pair_s written before the first store
   store(ra, Xs0, Ws0);
   if (KT > 1) load(ra, 1);
-  auto step = [&](int kt, TileRegs& staged, TileRegs& next, const _Float16* cx,
+  auto step = [&](int kt, TileRegs<S>& staged, TileRegs<S>& next, const _Float16* cx,
                   const _Float16* cw, _Float16* sx, _Float16* sw) {
     __syncthreads();
     if (kt + 2 < KT) load(next, kt + 2);
@@ -207,22 +247,38 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
     compute(cx, cw);
     if (kt + 1 < KT) store(staged, sx, sw);
   };
-  for (int kt = 0; kt < KT; kt += 2) {
+  // Steady state with every load and store unconditional: with the loads and stores under
+  // tests inside the loop, the compiler's wait-count analysis merged the paths and waited for
+  // all outstanding loads before issuing the next tile's (one tile of prefetch instead of two).
+  int kt = 0;
+  for (; kt + 3 < KT; kt += 2) {
+    __syncthreads();
+    load(rb, kt + 2);
+    issue_here();
+    compute(Xs0, Ws0);
+    store(ra, Xs1, Ws1);
+    __syncthreads();
+    load(ra, kt + 3);
+    issue_here();
+    compute(Xs1, Ws1);
+    store(rb, Xs0, Ws0);
+  }
+  for (; kt < KT; kt += 2) {      // the last (up to three) steps
     step(kt, ra, rb, Xs0, Ws0, Xs1, Ws1);
     if (kt + 1 < KT) step(kt + 1, rb, ra, Xs1, Ws1, Xs0, Ws0);
   }
 
-  // epilogue: element e of acc[i][j] is row 64wm + 32i + 8(e/4) + 4(lane/32) + e%4,
-  // column 64wn + 32j + lane%32
+  // epilogue: element e of acc[i][j] is row TM wm + 32i + 8(e/4) + 4(lane/32) + e%4,
+  // column TN wn + 32j + lane%32
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + 64 * wn + 32 * j + lane % 32;
+  for (int j = 0; j < S::FN; ++j) {
+    const int n = n0 + S::TN * wn + 32 * j + lane % 32;
     const float bv = bias != nullptr ? h2f(bias[n]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < S::FM; ++i) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+        const int m = m0 + S::TM * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
         if (m < M)
           y[static_cast<int64_t>(m) * N + n] =
               __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[i][j][e] + bv));
@@ -230,6 +286,28 @@ __global__ __launch_bounds__(kGThreads) void gemm_tn_kernel(
     }
   }
 }
+
+// The tile shape of both entry points (SOUPK_GEMM_SHAPE selects another for measurement):
+//   0: 128 x 128, 2 x 2 waves of 64 x 64      1: 128 x 128, 4 x 2 waves of 32 x 64
+//   2: 128 x 128, 2 x 4 waves of 64 x 32      3: 128 x 64, 2 x 2 waves of 64 x 32
+//   4: 64 x 128, 2 x 2 waves of 32 x 64       5: 256 x 128, 4 x 2 waves of 64 x 64
+#ifndef SOUPK_GEMM_SHAPE
+#define SOUPK_GEMM_SHAPE 1
+#endif
+#if SOUPK_GEMM_SHAPE == 0
+using Shape = GemmShape<128, 128, 2, 2>;
+#elif SOUPK_GEMM_SHAPE == 1
+using Shape = GemmShape<128, 128, 4, 2>;
+#elif SOUPK_GEMM_SHAPE == 2
+using Shape = GemmShape<128, 128, 2, 4>;
+#elif SOUPK_GEMM_SHAPE == 3
+using Shape = GemmShape<128, 64, 2, 2>;
+#elif SOUPK_GEMM_SHAPE == 4
+using Shape = GemmShape<64, 128, 2, 2>;
+#else
+using Shape = GemmShape<256, 128, 4, 2>;
+#endif
+constexpr int kBM = Shape::BM, kBN = Shape::BN;
 
 int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
   if (M < 0 || N <= 0 || K <= 0 || N % kBN || K % kBK || ldx < K || ldx % 8) return kInvalid;
@@ -254,7 +332,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
   if (bad_ptr(x) || bad_ptr(w) || bad_ptr(y)) return kInvalid;
   Nf4Weights none{};
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
-  return launch_kernel(gemm_tn_kernel<false>, grid, dim3(kGThreads),
+  return launch_kernel(gemm_tn_kernel<Shape, false>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
                        static_cast<int>(M), N, K);
 }
@@ -286,7 +364,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(y)) return kInvalid;
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
-  return launch_kernel(gemm_tn_kernel<true>, grid, dim3(kGThreads),
+  return launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
                        static_cast<int>(M), N, K);
 }
