@@ -739,7 +739,9 @@ def time_nf4_gemm(dev, calls=40):
     csrc/gemm_nf4.hip) against hipBLASLt on the unpacked weight, at M = 2048 for the four
     projections of a layer (q|k|v and gate|up as stacked parts): the fused kernel on fp16 and
     on NF4 weights, hipBLASLt (torch.matmul) on fp16 weights, the standalone unpack
-    (nf4.unpack_concat) and unpack + hipBLASLt.  Each variant: 5 untimed calls, then `calls`
+    (nf4.unpack_concat) and unpack + hipBLASLt; and the input gradient dx = dy W fused
+    (nf4_gemm.nf4_grad_input), on hipBLASLt and unpack + hipBLASLt.  Each variant: 5 untimed
+    calls, then `calls`
     calls queued behind a DeviceHold and timed as one span (torch events), so host overhead is
     not in the figure.  Synthetic NF4 weights (workloads.nf4_weight), x ~ N(0, 1)."""
     from testt_amd import nf4, nf4_gemm
@@ -751,7 +753,7 @@ def time_nf4_gemm(dev, calls=40):
             fn()
         torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        hold.hold(calls * 250 + 3000)
+        hold.hold(calls * 600 + 3000)
         e0.record()
         for _ in range(calls):
             fn()
@@ -771,6 +773,7 @@ def time_nf4_gemm(dev, calls=40):
         ws = [workloads.nf4_weight(r, K, seed=50 + i, device=dev) for i, r in enumerate(rows)]
         g = workloads.gen(K)
         x = torch.randn(M, K, generator=g).to(torch.float16).to(dev)
+        dy = (0.1 * torch.randn(M, sum(rows), generator=g)).to(torch.float16).to(dev)
         w16 = nf4.unpack_concat(ws, dev)
         out[name] = {
             "N": sum(rows), "K": K, "M": M,
@@ -780,8 +783,14 @@ def time_nf4_gemm(dev, calls=40):
             "unpack_us": span_us(lambda: nf4.unpack_concat(ws, dev)),
             "unpack_then_hipblaslt_us": span_us(
                 lambda: torch.matmul(x, nf4.unpack_concat(ws, dev).t())),
+            # the input gradient dx = dy W: fused (W dequantised in the GEMM) against
+            # hipBLASLt on the fp16 weight and unpack + hipBLASLt
+            "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dy, ws)),
+            "bwd_hipblaslt_fp16_w_us": span_us(lambda: torch.matmul(dy, w16)),
+            "bwd_unpack_then_hipblaslt_us": span_us(
+                lambda: torch.matmul(dy, nf4.unpack_concat(ws, dev))),
         }
-        del ws, x, w16
+        del ws, x, w16, dy
     return out
 
 

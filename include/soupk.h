@@ -431,6 +431,22 @@ int soupk_gemm_tn_nf4(const uint16_t* x, int64_t ldx, int32_t n_parts,
                       const uint16_t* bias, uint16_t* y, int64_t M, int32_t N, int32_t K,
                       void* stream);
 
+/*
+ * Its input gradient (the backward of the same projection): dx = dy W, dy [M, K] fp16 (row
+ * pitch lddy), W [K, N] the NF4 row stack (n_parts parts of part_rows[i] rows, K in all, each a
+ * multiple of 128; N, W's columns, a multiple of 128; K a multiple of 64) dequantised as it is
+ * staged (the same values as soupk_nf4_unpack), dx [M, N] fp16.  One fp16 rounding of fp32 MFMA
+ * sums.  No counterpart kernel in the reference, which unpacks W again and calls cuBLAS
+ * (solution/nf4.py:122-127); the fused form its README names as the next step
+ * (README.md:190-192).
+ */
+int soupk_gemm_nn_nf4(const uint16_t* dy, int64_t lddy, int32_t n_parts,
+                      const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+                      const float* const* code2, const float* const* absmax2,
+                      const float* const* offset, const float* const* nf4,
+                      const int32_t* part_rows, int32_t qblock, int32_t qblock2, uint16_t* dx,
+                      int64_t M, int32_t N, int32_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

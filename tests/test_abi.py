@@ -100,6 +100,12 @@ def test_version_and_status_strings(lib):
                              4, None)),
     ("soupk_lora_rope_fwd", (16, 32, 2.0, 48, 64, 80, 96, 112, 136, 4, 256, 2, 1, 128, 16, 1, 4,
                              None)),
+    # the NF4 input-gradient GEMM: W columns not a multiple of 128, a contraction not a
+    # multiple of 64, no parts, a blocksize other than 64
+    ("soupk_gemm_nn_nf4", (16, 256, 1) + (16,) * 7 + (64, 256, 16, 4, 100, 256, None)),
+    ("soupk_gemm_nn_nf4", (16, 256, 1) + (16,) * 7 + (64, 256, 16, 4, 128, 100, None)),
+    ("soupk_gemm_nn_nf4", (16, 256, 0) + (16,) * 7 + (64, 256, 16, 4, 128, 256, None)),
+    ("soupk_gemm_nn_nf4", (16, 256, 1) + (16,) * 7 + (32, 256, 16, 4, 128, 256, None)),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, name, args):
     with pytest.raises(_ext.SoupkError, match="status 1"):

@@ -57,6 +57,27 @@ def test_gemm_tn_nf4(rows, K, M):
     within(y, x.double() @ wd.t() + b.double(), x.double().abs() @ wd.abs().t() + b.double().abs())
 
 
+@pytest.mark.parametrize("rows,K,M", [((1536, 256, 256), 1536, 2048), ((1536,), 1536, 2048),
+                                      ((256, 128, 128), 512, 77), ((128,), 128, 1)])
+def test_gemm_nn_nf4_grad_input(rows, K, M):
+    """dx = dy @ W with W dequantised in the GEMM (the backward of nf4_linear): against float64
+    sums over the oracle's dequantised weights (one fp16 rounding of fp32 sums: within 1 ulp
+    plus 32 * 2^-24 * sum|terms|), and a contraction spanning the parts (q|k|v)."""
+    print(f"gemm_nn_nf4 parts={rows} K={K} M={M}", flush=True)
+    ws = [workloads.nf4_weight(r, K, seed=90 + i, device=DEV, absmax2_range=(0.005, 0.02),
+                               offset=0.01) for i, r in enumerate(rows)]
+    g = torch.Generator().manual_seed(M + K + len(rows))
+    dy = (0.1 * torch.randn(M, sum(rows), generator=g)).to(torch.float16).to(DEV)
+    assert nf4_gemm.grad_input_supported(dy, ws)
+    dx = nf4_gemm.nf4_grad_input(dy, ws)
+    wd = torch.from_numpy(np.concatenate([dequant_state(w) for w in ws]).astype(np.float64)).to(DEV)
+    within(dx, dy.double() @ wd, dy.double().abs() @ wd.abs())
+    # a strided dy (rows of a wider buffer) gives the same result
+    wide = torch.zeros(M, sum(rows) + 64, dtype=torch.float16, device=DEV)
+    wide[:, :sum(rows)] = dy
+    assert torch.equal(nf4_gemm.nf4_grad_input(wide[:, :sum(rows)], ws), dx)
+
+
 def test_rejects_shapes():
     x = torch.randn(8, 64, device=DEV).to(torch.float16)
     with pytest.raises(Exception):

@@ -67,6 +67,8 @@ SIGNATURES = {
     "soupk_lora_bwd_params_noalloc": [_p, _p, _p, _p, _i64, _p, _i64, _f32, _p, _p, _p, _p, _i64,
                                       _i32, _i32, _i32, _i32, _p],
     "soupk_gemm_tn": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _p],
+    "soupk_gemm_nn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64,
+                          _i32, _i32, _p],
     "soupk_gemm_tn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _i64,
                           _i32, _i32, _p],
 }

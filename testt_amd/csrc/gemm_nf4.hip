@@ -31,8 +31,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 64;
-constexpr int kLds = kBK + 8;          // LDS row stride (halves)
+constexpr int kQBlock = 64;            // NF4 quantisation block (values)
 constexpr int kMaxParts = 4;
 
 struct Nf4Part {
@@ -72,17 +71,21 @@ __device__ __forceinline__ void tile_of(int wg, int n_blocks, int m_blocks, int&
 
 // Tile shape of one launch: a BM x BN block of y per workgroup, WM x WN wavefronts, each a
 // (BM/WM) x (BN/WN) tile of 32 x 32 MFMA tiles.
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int WM_, int WN_, int BK_ = 64>
 struct GemmShape {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_;
   static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kLds = BK + 8;                // LDS row stride (halves)
+  static constexpr int CPR = BK / 8;                 // 16-byte chunks per row of a K tile
+  static constexpr int IPR = BK / 16;                // NF4 16-code items per row of a K tile
   static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;   // 32 x 32 MFMA tiles per wave
-  static constexpr int XC = BM * 8 / kThreads;       // 16-byte x chunks per thread per K tile
-  static constexpr int WC = BN * 8 / kThreads;       // fp16 W chunks
-  static constexpr int NI = (BN * 4 + kThreads - 1) / kThreads;   // NF4: 16-code items
+  static constexpr int XC = BM * CPR / kThreads;     // 16-byte x chunks per thread per K tile
+  static constexpr int WC = BN * CPR / kThreads;     // fp16 W chunks
+  static constexpr int NI = (BN * IPR + kThreads - 1) / kThreads;   // NF4: 16-code items
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tiles are whole 32 x 32 MFMA tiles");
-  static_assert(XC * kThreads == BM * 8 && WC * kThreads == BN * 8, "whole chunks per thread");
+  static_assert(XC * kThreads == BM * CPR && WC * kThreads == BN * CPR, "whole chunks");
+  static_assert(BK % kQBlock == 0, "a K tile holds whole quantisation blocks");
 };
 
 // Registers of one K tile for one thread: XC x 16 bytes of x (chunk c = tid + threads*j: row
@@ -98,11 +101,19 @@ struct TileRegs {
   float a2[S::NI];        // NF4: absmax2 of the block's group
 };
 
+#ifndef SOUPK_GEMM_WPE
+#define SOUPK_GEMM_WPE 0
+#endif
 template <class S, bool NF4>
-__global__ __launch_bounds__(S::kThreads) void gemm_tn_kernel(
+__global__ __launch_bounds__(S::kThreads)
+#if SOUPK_GEMM_WPE
+__attribute__((amdgpu_waves_per_eu(SOUPK_GEMM_WPE, SOUPK_GEMM_WPE)))
+#endif
+void gemm_tn_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* w16, Nf4Weights nw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K) {
-  constexpr int BM = S::BM, BN = S::BN, T = S::kThreads;
+  constexpr int BM = S::BM, BN = S::BN, T = S::kThreads, kBK = S::BK, kLds = S::kLds;
+  constexpr int CPR = S::CPR, IPR = S::IPR;
   // Two LDS stages as separate arrays, so that the compiler sees the staging of one and the
   // MFMA reads of the other as independent and interleaves them.
   __shared__ __align__(16) _Float16 Xs0[BM * kLds];
@@ -141,24 +152,25 @@ __global__ __launch_bounds__(S::kThreads) void gemm_tn_kernel(
     const int k0 = kt * kBK;
 #pragma unroll
     for (int j = 0; j < S::XC; ++j) {
-      const int c = tid + T * j, row = c / 8, ch = c % 8;
+      const int c = tid + T * j, row = c / CPR, ch = c % CPR;
       const int64_t xr = min(m0 + row, M - 1);
       r.x[j] = *reinterpret_cast<const u32x4*>(x + xr * ldx + k0 + 8 * ch);
     }
     if constexpr (!NF4) {
 #pragma unroll
       for (int j = 0; j < S::WC; ++j) {
-        const int c = tid + T * j, row = c / 8, ch = c % 8;
+        const int c = tid + T * j, row = c / CPR, ch = c % CPR;
         r.w[j] = *reinterpret_cast<const u32x4*>(w16 + static_cast<int64_t>(n0 + row) * K + k0 +
                                                  8 * ch);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < S::NI; ++j) {
-        const int it = min(tid + T * j, BN * 4 - 1), row = it / 4, q = it % 4;
-        const int64_t e0 = static_cast<int64_t>(prow0 + row) * K + k0;   // first element
-        r.c[j] = *reinterpret_cast<const u32x2*>(P.packed + e0 / 2 + 8 * q);
-        const int64_t blk = e0 / 64;
+        const int it = min(tid + T * j, BN * IPR - 1), row = it / IPR, q = it % IPR;
+        // first element of the item
+        const int64_t e0 = static_cast<int64_t>(prow0 + row) * K + k0 + 16 * q;
+        r.c[j] = *reinterpret_cast<const u32x2*>(P.packed + e0 / 2);
+        const int64_t blk = e0 / kQBlock;
         r.ablk[j] = P.absmax_u8[blk];
         r.a2[j] = P.absmax2[blk / 256];
       }
@@ -167,21 +179,21 @@ __global__ __launch_bounds__(S::kThreads) void gemm_tn_kernel(
   auto store = [&](const TileRegs<S>& r, _Float16* Xs, _Float16* Ws) {
 #pragma unroll
     for (int j = 0; j < S::XC; ++j) {
-      const int c = tid + T * j, row = c / 8, ch = c % 8;
+      const int c = tid + T * j, row = c / CPR, ch = c % CPR;
       *reinterpret_cast<u32x4*>(&Xs[row * kLds + 8 * ch]) = r.x[j];
     }
     if constexpr (!NF4) {
 #pragma unroll
       for (int j = 0; j < S::WC; ++j) {
-        const int c = tid + T * j, row = c / 8, ch = c % 8;
+        const int c = tid + T * j, row = c / CPR, ch = c % CPR;
         *reinterpret_cast<u32x4*>(&Ws[row * kLds + 8 * ch]) = r.w[j];
       }
     } else {
 #pragma unroll
       for (int j = 0; j < S::NI; ++j) {
         const int it = tid + T * j;
-        if (S::NI * T > BN * 4 && it >= BN * 4) break;
-        const int row = it / 4, q = it % 4;
+        if (S::NI * T > BN * IPR && it >= BN * IPR) break;
+        const int row = it / IPR, q = it % IPR;
         const uint32_t words[2] = {r.c[j].x, r.c[j].y};
         // All eight (nf4[hi], nf4[lo]) lookups and the scale's code2 lookup are issued before
         // any is used: left to itself the compiler issued them one at a time, each waiting for
@@ -287,10 +299,209 @@ __global__ __launch_bounds__(S::kThreads) void gemm_tn_kernel(
   }
 }
 
+// ---- the input gradient: dX = dY W with W read as NF4 --------------------------------------
+// dX [M, Kw] = dY [M, Nw] W [Nw, Kw] for y = x W^T: the contraction runs over W's rows (Nw).  A
+// contraction step stages 64 rows of W x BN output columns in LDS in W's own layout (row n,
+// columns contiguous), dequantised as in the forward -- a thread's item is 16 consecutive
+// columns of one row (8 code bytes, 8 lanes reading a row's 64 contiguous bytes; one 64-value
+// block), written as two 16-byte stores -- and the MFMA B fragments (column c, 8 consecutive
+// rows) are read with two ds_read_b64_tr_b16 each: in a 16-lane group, lane k reads 4 columns
+// of row r0 + k/4 and receives column c0 + k of rows r0 .. r0 + 3.  (Staged transposed with
+// 4-byte stores instead, the dequantised tile took 8-way LDS bank conflicts: 60.8 us against
+// 34.3 us for unpack + hipBLASLt at the q|k|v shape.)  W may be up to 4 row parts (q|k|v); a
+// 64-row step lies in one part, whose tables (code2, nf4 pairs) are all staged at the start.
+template <class S>
+struct TileRegsNN {
+  static constexpr int IPR = S::BN / 16;   // 16-column items per W row of a step
+  static constexpr int NI = (64 * IPR + S::kThreads - 1) / S::kThreads;
+  u32x4 x[S::XC];
+  u32x2 c[NI];
+  uint32_t ablk[NI];
+  float a2[NI];
+};
+
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
+typedef __attribute__((address_space(3))) _Float16 lds_h;
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+template <class S>
+__global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
+    const uint16_t* __restrict__ dy, int64_t lddy, Nf4Weights nw, uint16_t* __restrict__ dx,
+    int M, int N /* W columns: dx columns */, int K /* W rows: the contraction */) {
+  constexpr int BM = S::BM, BN = S::BN, T = S::kThreads, kBK = 64, kLds = kBK + 8;
+  constexpr int kLdw = BN + 8;                   // W tile row stride (halves)
+  constexpr int CPR = kBK / 8;
+  constexpr int IPR = TileRegsNN<S>::IPR;
+  constexpr int NI = TileRegsNN<S>::NI;
+  static_assert(S::BK == 64, "64-row contraction steps");
+  __shared__ __align__(16) _Float16 Xs0[BM * kLds];
+  __shared__ __align__(16) _Float16 Ws0[kBK * kLdw];
+  __shared__ __align__(16) _Float16 Xs1[BM * kLds];
+  __shared__ __align__(16) _Float16 Ws1[kBK * kLdw];
+  __shared__ float code2_s[kMaxParts][256];
+  __shared__ float2 pair_s[kMaxParts][256];
+  const int tid = threadIdx.x;
+  int nb, mb;
+  tile_of(blockIdx.x, N / BN, (M + BM - 1) / BM, nb, mb);
+  const int n0 = nb * BN, m0 = mb * BM;
+  const int lane = tid % kWave, wv = tid / kWave;
+  const int wm = wv / S::WN, wn = wv % S::WN;
+  for (int p = 0; p < nw.n_parts; ++p)
+    for (int i = tid; i < 256; i += T) {
+      code2_s[p][i] = nw.part[p].code2[i];
+      pair_s[p][i] = float2{nw.part[p].nf4[i >> 4], nw.part[p].nf4[i & 15]};
+    }
+
+  const int KT = K / kBK;
+  // the part holding W rows k0 .. k0 + 63, and the row of that part (wave-uniform)
+  auto part_of = [&](int k0, int& prow) {
+    int part = 0;
+    prow = k0;
+    while (part + 1 < nw.n_parts && prow >= nw.part[part].rows) {
+      prow -= nw.part[part].rows;
+      ++part;
+    }
+    return part;
+  };
+  auto load = [&](TileRegsNN<S>& r, int kt) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int j = 0; j < S::XC; ++j) {
+      const int c = tid + T * j, row = c / CPR, ch = c % CPR;
+      const int64_t xr = min(m0 + row, M - 1);
+      r.x[j] = *reinterpret_cast<const u32x4*>(dy + xr * lddy + k0 + 8 * ch);
+    }
+    int prow0;
+    const Nf4Part P = nw.part[part_of(k0, prow0)];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int it = min(tid + T * j, 64 * IPR - 1), row = it / IPR, q = it % IPR;
+      const int64_t e0 = static_cast<int64_t>(prow0 + row) * N + n0 + 16 * q;
+      r.c[j] = *reinterpret_cast<const u32x2*>(P.packed + e0 / 2);
+      const int64_t blk = e0 / kQBlock;
+      r.ablk[j] = P.absmax_u8[blk];
+      r.a2[j] = P.absmax2[blk / 256];
+    }
+  };
+  auto store = [&](const TileRegsNN<S>& r, int kt, _Float16* Xs, _Float16* Ws) {
+#pragma unroll
+    for (int j = 0; j < S::XC; ++j) {
+      const int c = tid + T * j, row = c / CPR, ch = c % CPR;
+      *reinterpret_cast<u32x4*>(&Xs[row * kLds + 8 * ch]) = r.x[j];
+    }
+    int prow0;
+    const int part = part_of(kt * kBK, prow0);
+    const float offset = nw.part[part].offset[0];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int it = tid + T * j;
+      if (NI * T > 64 * IPR && it >= 64 * IPR) break;
+      const int row = it / IPR, q = it % IPR;
+      const uint32_t words[2] = {r.c[j].x, r.c[j].y};
+      float2 v[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[h * 4 + b] = pair_s[part][(words[h] >> (8 * b)) & 0xffu];
+      const float c2 = code2_s[part][r.ablk[j]];
+      __builtin_amdgcn_sched_barrier(0);
+      const float scale = c2 * r.a2[j] + offset;   // two roundings (no FMA)
+      uint32_t out[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) out[k] = pack_h2(v[k].x * scale, v[k].y * scale);
+      _Float16* dst = &Ws[row * kLdw + 16 * q];
+      *reinterpret_cast<u32x4*>(dst) = u32x4{out[0], out[1], out[2], out[3]};
+      *reinterpret_cast<u32x4*>(dst + 8) = u32x4{out[4], out[5], out[6], out[7]};
+    }
+  };
+
+  f16v acc[S::FM][S::FN];
+#pragma unroll
+  for (int i = 0; i < S::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  // B fragment of output columns c0 + lane%32 at contraction rows 16ks + 8(lane/32) .. +7
+  const int gk = lane & 15, grp = lane >> 4;
+  auto compute = [&](const _Float16* Xs, const _Float16* Ws) {
+    const _Float16* xa = &Xs[(S::TM * wm + (lane % 32)) * kLds + 8 * (lane / 32)];
+    const lds_h* wbase = (const lds_h*)(Ws);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      h8 a[S::FM], b[S::FN];
+#pragma unroll
+      for (int i = 0; i < S::FM; ++i)
+        a[i] = *reinterpret_cast<const h8*>(xa + 32 * i * kLds + 16 * ks);
+#pragma unroll
+      for (int j = 0; j < S::FN; ++j) {
+        const int row = 16 * ks + 8 * (grp >> 1) + (gk >> 2);
+        const int col = S::TN * wn + 32 * j + 16 * (grp & 1) + 4 * (gk & 3);
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)(wbase + row * kLdw + col));
+        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)(wbase + (row + 4) * kLdw + col));
+        b[j] = __builtin_shufflevector(__builtin_bit_cast(h4, lo), __builtin_bit_cast(h4, hi),
+                                       0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int i = 0; i < S::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma32x32(a[i], b[j], acc[i][j]);
+    }
+  };
+  TileRegsNN<S> ra, rb;
+  load(ra, 0);
+  __syncthreads();   // the tables written before the first store
+  store(ra, 0, Xs0, Ws0);
+  if (KT > 1) load(ra, 1);
+  auto step = [&](int kt, TileRegsNN<S>& staged, TileRegsNN<S>& next, const _Float16* cx,
+                  const _Float16* cw, _Float16* sx, _Float16* sw) {
+    __syncthreads();
+    if (kt + 2 < KT) load(next, kt + 2);
+    issue_here();
+    compute(cx, cw);
+    if (kt + 1 < KT) store(staged, kt + 1, sx, sw);
+  };
+  int kt = 0;
+  for (; kt + 3 < KT; kt += 2) {   // steady state: every load and store unconditional
+    __syncthreads();
+    load(rb, kt + 2);
+    issue_here();
+    compute(Xs0, Ws0);
+    store(ra, kt + 1, Xs1, Ws1);
+    __syncthreads();
+    load(ra, kt + 3);
+    issue_here();
+    compute(Xs1, Ws1);
+    store(rb, kt + 2, Xs0, Ws0);
+  }
+  for (; kt < KT; kt += 2) {
+    step(kt, ra, rb, Xs0, Ws0, Xs1, Ws1);
+    if (kt + 1 < KT) step(kt + 1, rb, ra, Xs1, Ws1, Xs0, Ws0);
+  }
+#pragma unroll
+  for (int j = 0; j < S::FN; ++j) {
+    const int n = n0 + S::TN * wn + 32 * j + lane % 32;
+#pragma unroll
+    for (int i = 0; i < S::FM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + S::TM * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+        if (m < M)
+          dx[static_cast<int64_t>(m) * N + n] =
+              __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[i][j][e]));
+      }
+    }
+  }
+}
+
 // The tile shape of both entry points (SOUPK_GEMM_SHAPE selects another for measurement):
 //   0: 128 x 128, 2 x 2 waves of 64 x 64      1: 128 x 128, 4 x 2 waves of 32 x 64
 //   2: 128 x 128, 2 x 4 waves of 64 x 32      3: 128 x 64, 2 x 2 waves of 64 x 32
 //   4: 64 x 128, 2 x 2 waves of 32 x 64       5: 256 x 128, 4 x 2 waves of 64 x 64
+//   6: as 1 with K tiles of 128
 #ifndef SOUPK_GEMM_SHAPE
 #define SOUPK_GEMM_SHAPE 1
 #endif
@@ -304,9 +515,12 @@ using Shape = GemmShape<128, 128, 2, 4>;
 using Shape = GemmShape<128, 64, 2, 2>;
 #elif SOUPK_GEMM_SHAPE == 4
 using Shape = GemmShape<64, 128, 2, 2>;
-#else
+#elif SOUPK_GEMM_SHAPE == 5
 using Shape = GemmShape<256, 128, 4, 2>;
+#else
+using Shape = GemmShape<128, 128, 4, 2, 128>;
 #endif
+constexpr int kBK = Shape::BK;
 constexpr int kBM = Shape::BM, kBN = Shape::BN;
 
 int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
@@ -317,6 +531,29 @@ int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
 }
 
 bool bad_ptr(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15); }
+
+// The NF4 parts of W (up to kMaxParts stacked by rows, each a multiple of 128 rows), checked.
+int nf4_parts(int32_t n_parts, const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+              const float* const* code2, const float* const* absmax2,
+              const float* const* offset, const float* const* nf4, const int32_t* part_rows,
+              int32_t qblock, int32_t qblock2, int64_t total_rows, Nf4Weights& nw) {
+  if (qblock != kQBlock || qblock2 != 256) return kInvalid;
+  if (n_parts < 1 || n_parts > kMaxParts || !packed || !absmax_u8 || !code2 || !absmax2 ||
+      !offset || !nf4 || !part_rows)
+    return kInvalid;
+  nw = Nf4Weights{};
+  int64_t rows = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    if (part_rows[i] <= 0 || part_rows[i] % 128 || bad_ptr(packed[i]) || !absmax_u8[i] ||
+        !code2[i] || !absmax2[i] || !offset[i] || !nf4[i])
+      return kInvalid;
+    nw.part[i] = Nf4Part{packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i], nf4[i],
+                         part_rows[i]};
+    rows += part_rows[i];
+  }
+  nw.n_parts = n_parts;
+  return rows == total_rows ? kOk : kInvalid;
+}
 
 }  // namespace
 }  // namespace soupk
@@ -345,26 +582,53 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
     int32_t K, void* stream) {
   const int rc = check_gemm(M, N, K, ldx);
   if (rc != kOk) return rc;
-  if (qblock != kBK || qblock2 != 256) return kInvalid;
-  if (n_parts < 1 || n_parts > kMaxParts || !packed || !absmax_u8 || !code2 || !absmax2 ||
-      !offset || !nf4 || !part_rows)
-    return kInvalid;
-  Nf4Weights nw{};
-  int64_t rows = 0;
-  for (int i = 0; i < n_parts; ++i) {
-    if (part_rows[i] <= 0 || part_rows[i] % kBN || bad_ptr(packed[i]) || !absmax_u8[i] ||
-        !code2[i] || !absmax2[i] || !offset[i] || !nf4[i])
-      return kInvalid;
-    nw.part[i] = Nf4Part{packed[i], absmax_u8[i], code2[i], absmax2[i], offset[i], nf4[i],
-                         part_rows[i]};
-    rows += part_rows[i];
-  }
-  nw.n_parts = n_parts;
-  if (rows != N) return kInvalid;
+  Nf4Weights nw;
+  const int rp = nf4_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4, part_rows,
+                           qblock, qblock2, N, nw);
+  if (rp != kOk) return rp;
+  for (int i = 0; i < n_parts; ++i)
+    if (part_rows[i] % kBN) return kInvalid;
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(y)) return kInvalid;
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
                        static_cast<int>(M), N, K);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4(
+    const uint16_t* dy, int64_t lddy, int32_t n_parts, const uint8_t* const* packed,
+    const uint8_t* const* absmax_u8, const float* const* code2, const float* const* absmax2,
+    const float* const* offset, const float* const* nf4, const int32_t* part_rows,
+    int32_t qblock, int32_t qblock2, uint16_t* dx, int64_t M, int32_t N, int32_t K,
+    void* stream) {
+// Tile shape of the input gradient (measured at M = 2048 on MI355X: 128 x 64 on 4 wavefronts
+// 40.9 / 28.8 us at the q|k|v / o shapes; 128 x 128 on 8, 44.9 / 32.2 us, fills only 192 of the
+// 256 CUs there; 64 x 128, 54.1 / 39.6 us).
+#ifndef SOUPK_GEMM_NN_SHAPE
+#define SOUPK_GEMM_NN_SHAPE 1
+#endif
+#if SOUPK_GEMM_NN_SHAPE == 0
+  using NS = GemmShape<128, 128, 4, 2>;
+#elif SOUPK_GEMM_NN_SHAPE == 1
+  using NS = GemmShape<128, 64, 2, 2>;
+#elif SOUPK_GEMM_NN_SHAPE == 2
+  using NS = GemmShape<64, 128, 2, 2>;
+#else
+  using NS = GemmShape<128, 64, 4, 2>;
+#endif
+  // N: W's columns (dx's), K: W's rows (the contraction, dy's columns)
+  if (M < 0 || N <= 0 || K <= 0 || N % NS::BN || K % 64 || lddy < K || lddy % 8) return kInvalid;
+  if ((M + NS::BM - 1) / NS::BM * static_cast<int64_t>(N / NS::BN) > 0x7fffffff) return kInvalid;
+  if (M * static_cast<int64_t>(N) >= (int64_t{1} << 40)) return kInvalid;
+  Nf4Weights nw;
+  const int rp = nf4_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4, part_rows,
+                           qblock, qblock2, K, nw);
+  if (rp != kOk) return rp;
+  if (M == 0) return kOk;
+  if (bad_ptr(dy) || bad_ptr(dx)) return kInvalid;
+  const dim3 grid(static_cast<unsigned>((N / NS::BN) * ((M + NS::BM - 1) / NS::BM)));
+  return launch_kernel(gemm_nn_nf4_kernel<NS>, grid, dim3(NS::kThreads),
+                       static_cast<hipStream_t>(stream), dy, lddy, nw, dx, static_cast<int>(M),
+                       N, K);
 }

@@ -35,11 +35,16 @@ BYTES_PER_PROGRAM = 16384
 KEEP_UNPACKED_FOR_BACKWARD = True
 
 # FrozenNF4Linear's forward through the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py: W read
-# as NF4, dequantised in the GEMM's tile loads, no fp16 W in HBM) when the shapes allow it; its
-# backward then unpacks W.  Off by default: on MI355X that GEMM core is slower than hipBLASLt's
-# tuned kernels (device time at M = 2048: q|k|v 22.8 against 18.4 us on fp16 W), and with the
-# dequantisation in its loop it is behind unpack + hipBLASLt (30.8 against 7.6 + 20.2 us).
-USE_FUSED_NF4_GEMM = False
+# as NF4, dequantised in the GEMM's tile loads, no fp16 W in HBM) where it measured ahead of
+# unpack + hipBLASLt on MI355X (nf4_gemm.prefer_fused: the q|k|v and o projections of
+# Qwen2.5-1.5B with at most one wave of 128 x 128 tiles, M <= 2048: q|k|v 27.1 against 28.0 us
+# at M = 2048, 2-3% ahead from M = 768 on; o level); elsewhere (gate|up, down, larger M) it is
+# behind and the unpack + hipBLASLt path runs.  Only a forward that unpacks W itself uses it: a
+# caller that passes the unpacked weight (the decoder layer's one-launch unpack of all seven
+# projections) keeps hipBLASLt.  The backward unpacks W and runs hipBLASLt, as the reference
+# does: the fused input-gradient GEMM (nf4_gemm.nf4_grad_input) measured behind it
+# (40.9 / 28.8 against 34.0 / 28.3 us at the q|k|v / o shapes).
+USE_FUSED_NF4_GEMM = True
 
 
 def keep_for_backward(ctx, weight):
@@ -412,7 +417,7 @@ class FrozenNF4Linear(torch.autograd.Function):
             from . import nf4_gemm
 
             x2 = x.reshape(-1, x.shape[-1])
-            if nf4_gemm.supported(x2, weights, bias):
+            if nf4_gemm.supported(x2, weights, bias) and nf4_gemm.prefer_fused(x2, weights):
                 ctx.unpacked = None
                 out = nf4_gemm.nf4_linear(x2, weights, bias)
                 return out.view(*x.shape[:-1], out.shape[-1])

@@ -40,6 +40,33 @@ def supported(x, weights, bias=None):
     return K % 64 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
 
 
+# Where the fused forward measured ahead of unpack + hipBLASLt on MI355X: weights of at most
+# this many elements (Qwen2.5-1.5B's q|k|v, 3.1 M, and o, 2.4 M; not gate|up, 27.5 M, or down,
+# 13.8 M) and at most one 128 x 128 tile per compute unit (M <= 2048 at those shapes; with a
+# second round of tiles it fell 26-34% behind).
+FUSED_MAX_WEIGHT_ELEMS = 4 << 20
+
+
+def _cu_count(device):
+    cached = _cu_count.cache.get(device)
+    if cached is None:
+        cached = _cu_count.cache[device] = torch.cuda.get_device_properties(device)\
+            .multi_processor_count
+    return cached
+
+
+_cu_count.cache = {}
+
+
+def prefer_fused(x, weights):
+    """True where the fused NF4 forward is the faster path (FUSED_MAX_WEIGHT_ELEMS, one wave of
+    tiles)."""
+    M, K = x.shape
+    N = sum(_nf4.weight_shape(w)[0] for w in weights)
+    tiles = -(-M // 128) * (N // 128)
+    return N * K <= FUSED_MAX_WEIGHT_ELEMS and tiles <= _cu_count(x.device)
+
+
 def gemm_tn(x, w16, bias=None):
     _ext.require(w16, "w16", dtype=torch.float16, ndim=2, device=x.device)
     M, K = x.shape
@@ -50,6 +77,55 @@ def gemm_tn(x, w16, bias=None):
     _ext.call("soupk_gemm_tn", x.data_ptr(), x.stride(0), w16.data_ptr(), _ext.ptr(bias),
               y.data_ptr(), M, N, K, _ext.stream_of(x))
     return y
+
+
+def _nf4_args(weights, device):
+    plans = [_nf4._plan(w, device) for w in weights]
+    rows = [_nf4.weight_shape(w)[0] for w in weights]
+    n = len(weights)
+    arrays = [(ctypes.c_void_p * n)(*[p[0][i] for p in plans]) for i in range(6)]
+    part_rows = (ctypes.c_int32 * n)(*rows)
+    return plans, rows, arrays, part_rows
+
+
+def grad_input_supported(dy, weights):
+    """nf4_grad_input takes these: fp16 dy [M, N] with unit column stride and 16-byte aligned
+    rows, 1-4 NF4 parts (blocksize 64, nested 256) of one column count, each a multiple of 128
+    rows, W's columns a multiple of 128."""
+    if not (dy.is_cuda and dy.dtype == torch.float16 and dy.dim() == 2):
+        return False
+    if not 1 <= len(weights) <= MAX_PARTS:
+        return False
+    cols = None
+    total = 0
+    for w in weights:
+        if not _nf4.supports_fast_unpack(w):
+            return False
+        st = w.quant_state
+        r, c = _nf4.weight_shape(w)
+        if r % 128 or st.blocksize != 64 or st.state2.blocksize != 256 or \
+                (cols is not None and c != cols):
+            return False
+        if _nf4._plan(w, dy.device) is None:
+            return False
+        cols, total = c, total + r
+    return (cols % 128 == 0 and dy.shape[1] == total and dy.stride(1) == 1 and
+            dy.stride(0) % 8 == 0 and dy.data_ptr() % 16 == 0)
+
+
+def nf4_grad_input(dy, weights):
+    """dx = dy @ W (fp16 [M, K]) for W the row stack of `weights` ([N, K]), dequantised in the
+    GEMM (soupk_gemm_nn_nf4): the input gradient of nf4_linear without an fp16 W in memory."""
+    M, N = dy.shape
+    plans, rows, arrays, part_rows = _nf4_args(weights, dy.device)
+    if sum(rows) != N:
+        raise ValueError(f"dy has {N} columns, the weights {sum(rows)} rows")
+    K = _nf4.weight_shape(weights[0])[1]
+    dx = torch.empty((M, K), dtype=torch.float16, device=dy.device)
+    _ext.call("soupk_gemm_nn_nf4", dy.data_ptr(), dy.stride(0), len(weights),
+              *[ctypes.addressof(a) for a in arrays], ctypes.addressof(part_rows),
+              plans[0][2], plans[0][3], dx.data_ptr(), M, K, N, _ext.stream_of(dy))
+    return dx
 
 
 def nf4_linear(x, weights, bias=None):
