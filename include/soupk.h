@@ -401,6 +401,15 @@ int soupk_lora_bwd_params(const uint16_t* y, const uint16_t* t, const uint16_t* 
  * entry a call reads is written by that call first).
  */
 #define SOUPK_LORA_SCRATCH_FLOATS (4 << 20)
+/*
+ * Per-device set-up of the library (no counterpart in the reference): looks up, with the
+ * calling thread's current device, the device address of that device's no-alloc scratch
+ * buffer and keeps it.  The Python binding calls it when it loads the library.  A caller that
+ * captures soupk_lora_bwd_params_noalloc into a HIP graph calls it once per device before the
+ * capture: under capture, that entry point does not make the lookup itself and returns
+ * hipErrorStreamCaptureUnsupported if it has not been made.  Returns 0 or a hipError_t value.
+ */
+int soupk_init_device(void);
 int soupk_lora_bwd_params_noalloc(const uint16_t* y, const uint16_t* t, const uint16_t* dt,
                                   const uint16_t* g_q, int64_t ld_q, const uint16_t* g_v,
                                   int64_t ld_v, float scaling, float* d_aq, float* d_av,

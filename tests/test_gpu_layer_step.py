@@ -186,3 +186,40 @@ def test_varlen_attention_path_is_bit_identical(monkeypatch, lengths):
     for name, a, b in zip(("s", "d", "d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"),
                           *runs):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("keep", [False, True])
+def test_unpacked_weights_freed_after_forward_without_keep(monkeypatch, keep):
+    """With nf4.KEEP_UNPACKED_FOR_BACKWARD = False (the reference's memory profile), no fp16
+    projection outlives its layer's forward: four layer forwards with grad (each keeping what
+    its backward needs) grow the allocated memory by far less than one layer's unpacked weights
+    (94 MB at Qwen2.5-1.5B's shapes) per layer.  The LoRA parameters' fp16 staging, which the
+    backward keeps, is its own small allocation, not a view that holds the unpack buffer.  With
+    True the weights are kept for the backward, one buffer per layer."""
+    monkeypatch.setattr(nf4, "KEEP_UNPACKED_FOR_BACKWARD", keep)
+    w = layer.synthetic_layer(DEV, seed=21)
+    unpacked = sum(int(np.prod(nf4.weight_shape(p))) * 2
+                   for p in (w.q, w.k, w.v, w.o, w.gate, w.up, w.down))
+    B, T = 4, 128
+    pos = workloads.ragged_positions((T,) * B, T).to(DEV)
+    M = pos.numel()
+    g = torch.Generator().manual_seed(4)
+    s = torch.randn(M, workloads.HIDDEN, generator=g).to(DEV).requires_grad_(True)
+    cos, sin = workloads.rope_tables(T, workloads.HEAD_DIM, workloads.ROPE_THETA, device=DEV)
+    d = None
+    outs = []
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(DEV)
+    for _ in range(4):
+        s, d = layer.decoder_layer(s, d, w, pos, B, T, cos, sin, None)
+        outs.append((s, d))
+    torch.cuda.synchronize()
+    per_layer = (torch.cuda.memory_allocated(DEV) - before) / 4
+    print(f"keep={keep}: {per_layer / 1e6:.1f} MB per layer (unpacked weights "
+          f"{unpacked / 1e6:.1f} MB)", flush=True)
+    if keep:
+        assert per_layer > unpacked
+    else:
+        assert per_layer < 0.5 * unpacked
+    (s.float().sum() + d.float().sum()).backward()
+    assert w.lora_q[0].grad is not None

@@ -67,6 +67,7 @@ SIGNATURES = {
     "soupk_lora_bwd_params_noalloc": [_p, _p, _p, _p, _i64, _p, _i64, _f32, _p, _p, _p, _p, _i64,
                                       _i32, _i32, _i32, _i32, _p],
     "soupk_gemm_tn": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _p],
+    "soupk_init_device": [],
     "soupk_gemm_nn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64,
                           _i32, _i32, _p],
     "soupk_gemm_tn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _i64,
@@ -104,13 +105,18 @@ def load_library(path):
 
 
 def lib():
-    """The package's library, loaded once (raises if it has not been built)."""
+    """The package's library, loaded once (raises if it has not been built).  On a machine
+    with a HIP device, the current device's per-device state is set up right away
+    (soupk_init_device), so that no later call has to do it under graph capture."""
     global _lib
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is None:
-            _lib = load_library(_LIB_PATH)
+            handle = load_library(_LIB_PATH)
+            if torch.cuda.is_available():
+                handle.soupk_init_device()   # (a failure here resurfaces at the call)
+            _lib = handle
     return _lib
 
 

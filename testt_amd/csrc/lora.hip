@@ -901,9 +901,31 @@ extern "C" __attribute__((visibility("default"))) int soupk_lora_bwd_params_noal
   if (lora_params_workspace(M, H, NQ, NV) > kLoraScratchFloats) return SOUPK_STATUS_SCRATCH_LIMIT;
   float* part = nullptr;
   if (M > 0) {
+    // Under stream capture the address must already be known (soupk_init_device, which the
+    // Python binding calls when it loads the library): the lookup is not a call to make while
+    // a graph is being captured.
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return kInvalid;
+    float* known = nullptr;
+    {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      known = g_scratch_ptr[dev];
+    }
+    if (known == nullptr) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) != hipSuccess)
+        return kInvalid;
+      if (cs != hipStreamCaptureStatusNone)
+        return static_cast<int>(hipErrorStreamCaptureUnsupported);
+    }
     const int rs = scratch_on_current_device(&part);
     if (rs != kOk) return rs;
   }
   return lora_params_launch(y, t, dt, g_q, ld_q, g_v, ld_v, scaling, part, d_aq, d_av, d_bq,
                             d_bv, M, H, NQ, NV, static_cast<hipStream_t>(stream));
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_init_device(void) {
+  float* part = nullptr;
+  return scratch_on_current_device(&part);
 }
