@@ -514,9 +514,12 @@ class GcWatch:
 def timed_steps(dev, step, steps, warmup):
     """Run `step()` warmup times, then `steps` times with a torch event pair around each step
     (the step's span on the GPU, host gaps included, as the training loop sees it).  Returns
-    per-step microseconds, the span of the whole loop, and the garbage collections seen."""
+    per-step microseconds, the span of the whole loop, and the garbage collections seen; the
+    host's time to issue each step (its Python and dispatch time, microseconds) is attached to
+    the GcWatch as `host_us`, so a slow step can be told apart as host- or device-side."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
+    host = [0.0] * steps
     torch.cuda.synchronize(dev)
     # No synchronisation between the warm-up and the timed steps: the first timed step then
     # starts behind queued work, as every step of a training loop does (after a synchronise
@@ -524,25 +527,37 @@ def timed_steps(dev, step, steps, warmup):
     for _ in range(warmup):
         step()
     with GcWatch() as gcw:
-        for a, b in evs:
+        for i, (a, b) in enumerate(evs):
+            t0 = time.perf_counter()
             a.record()
             step()
             b.record()
+            host[i] = (time.perf_counter() - t0) * 1e6
         torch.cuda.synchronize(dev)
     per = [a.elapsed_time(b) * 1e3 for a, b in evs]
     total = evs[0][0].elapsed_time(evs[-1][1]) * 1e3
+    gcw.host_us = host
     return per, total, gcw
 
 
 def step_summary(per, total, gcw, unit_scale=1.0, digits=1):
-    """mean (the loop's span / steps), median, min, max of per-step times."""
+    """mean (the loop's span / steps), median, min, max of per-step times; with the host's
+    issue time of the median step and of the slowest one (a slowest step whose host time
+    exceeds the median host time by about its excess over the median step was held up on the
+    host, not on the GPU)."""
     n = len(per)
-    return {"mean": round(total / n * unit_scale, digits),
-            "median": round(median(per) * unit_scale, digits),
-            "min": round(min(per) * unit_scale, digits),
-            "max": round(max(per) * unit_scale, digits),
-            "slowest_step": int(max(range(n), key=lambda i: per[i])), "steps": n,
-            "gc_collections": gcw.count, "gc_ms": round(gcw.ms, 2)}
+    slowest = int(max(range(n), key=lambda i: per[i]))
+    out = {"mean": round(total / n * unit_scale, digits),
+           "median": round(median(per) * unit_scale, digits),
+           "min": round(min(per) * unit_scale, digits),
+           "max": round(max(per) * unit_scale, digits),
+           "slowest_step": slowest, "steps": n,
+           "gc_collections": gcw.count, "gc_ms": round(gcw.ms, 2)}
+    host = getattr(gcw, "host_us", None)
+    if host:
+        out["host_issue_median"] = round(median(host) * unit_scale, digits)
+        out["host_issue_slowest_step"] = round(host[slowest] * unit_scale, digits)
+    return out
 
 
 def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):

@@ -25,8 +25,9 @@
 extern "C" {
 #endif
 
-/* ABI version of this header; soupk_abi_version() returns the library's. */
-#define SOUPK_ABI_VERSION 3
+/* ABI version of this header; soupk_abi_version() returns the library's.  4 adds
+   soupk_lora_rope_fwd, soupk_gemm_nn_nf4 and soupk_init_device to version 3's entry points. */
+#define SOUPK_ABI_VERSION 4
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
 #define SOUPK_STATUS_SCRATCH_LIMIT 20001

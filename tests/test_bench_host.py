@@ -98,3 +98,18 @@ def test_rotation_sets_span_twice_the_infinity_cache():
         assert n >= 3 and n * in_bytes >= bench.ROTATION_BYTES == 512 << 20
         assert n == 3 or (n - 1) * in_bytes < bench.ROTATION_BYTES      # no more than needed
     assert bench.rotation_sets(8_388_608, n_sets=2) == 2
+
+
+def test_step_summary_reports_host_issue_time_of_the_slowest_step():
+    """The per-step record names the slowest step and the host's issue time of it beside the
+    median's, so an outlier can be attributed to the host (issue time up by about the step's
+    excess) or to the device (issue time as usual)."""
+    watch = bench.GcWatch()
+    per = [600.0, 610.0, 1100.0, 605.0, 598.0]
+    watch.host_us = [500.0, 505.0, 1010.0, 498.0, 502.0]
+    st = bench.step_summary(per, sum(per), watch)
+    assert st["slowest_step"] == 2 and st["max"] == 1100.0 and st["median"] == 605.0
+    assert st["host_issue_slowest_step"] == 1010.0 and st["host_issue_median"] == 502.0
+    assert st["mean"] == round(sum(per) / 5, 1) and st["gc_collections"] == 0
+    plain = bench.step_summary(per, sum(per), bench.GcWatch())    # no host times recorded
+    assert "host_issue_median" not in plain and plain["slowest_step"] == 2

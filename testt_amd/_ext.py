@@ -16,7 +16,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsoupk.s
 _lock = threading.Lock()
 _lib = None
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 STATUS_SCRATCH_LIMIT = 20001          # SOUPK_STATUS_SCRATCH_LIMIT
 LORA_SCRATCH_FLOATS = 4 << 20         # SOUPK_LORA_SCRATCH_FLOATS
 DTYPE_F16 = 0

@@ -5,12 +5,13 @@
 // (solution/nf4.py:108-127).  The same kernel also takes an fp16 W (the plain GEMM), which is
 // how its GEMM core is checked against hipBLASLt.
 //
-// Tiling: a workgroup computes a 128 x 128 tile of y (128 rows of x, 128 rows of W) with 4
-// wavefronts of 64 x 64 (2 x 2 MFMA tiles of 32 x 32, 16 fp32 accumulators each).  K advances
-// in tiles of 64: x and W tiles are staged in LDS ([128][72] halves each, double-buffered; the
-// 72-half row stride makes the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct
-// 4-bank groups), the next tile's global loads are issued before the current tile's MFMAs, and
-// one barrier per K tile separates the LDS writes from the reads.
+// Tiling: a workgroup computes a BM x BN tile of y (BM rows of x, BN rows of W) with WM x WN
+// wavefronts, each a grid of 32 x 32 MFMA tiles (16 fp32 accumulators each); the shipped shape is
+// 128 x 128 on 8 wavefronts (4 x 2, two per SIMD) of 32 x 64.  K advances in tiles of 64: x and
+// W tiles are staged in LDS ([BM][72] / [BN][72] halves, double-buffered; the 72-half row stride
+// makes the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct 4-bank groups), the
+// global loads run two tiles ahead of the MFMAs, and one barrier per K tile separates the LDS
+// writes from the reads.
 //
 // NF4 weights: a 64-wide K tile of one W row is exactly one 64-value quantisation block, so a
 // thread dequantises 32 codes of one row with one block scale:
