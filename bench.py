@@ -669,7 +669,7 @@ def graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps):
     return res
 
 
-def time_attention(dev, steps, warmup):
+def time_attention(dev, steps, warmup, varlen_only=False):
     """The causal GQA attention kernels (testt_amd/csrc/attention.hip) at the layer's shape,
     B=4 x T=512, 12 query / 2 key-value heads of 128: forward and backward per call, torch
     events on the stream they run on.  `fwd`/`bwd`: the padded-layout kernels (every position
@@ -722,6 +722,8 @@ def time_attention(dev, steps, warmup):
         res[f"{tag}varlen_bwd"] = rate(
             timed(lambda: attention.attention_varlen_bwd(rows, cu, out, lse, dout, scale, NH, NKV,
                                                          rope=rope)), 10 * D * pairs)
+        if varlen_only:
+            continue
         # the padded layout of the same tokens (key flags when rows are ragged)
         q = torch.randn(B, NH, T, D, generator=g).to(torch.float16).to(dev)
         k = torch.randn(B, NKV, T, D, generator=g).to(torch.float16).to(dev)
@@ -1268,6 +1270,96 @@ def summarize_valu(raw_csv, busy_csv, bench_json, commands):
     return "\n".join(out) + "\n"
 
 
+# Counter passes of the attention profile (each within one pass's hardware limits: at most 8
+# SQ counters, derived counters counted by the raw counters they read).
+ATTN_PMC_PASSES = (
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_SALU "
+    "SQ_INSTS_VMEM SQ_INSTS_VALU_TRANS_F32",
+    "MfmaUtil LdsUtil LdsBankConflict VALUBusy SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS "
+    "SQ_ACTIVE_INST_ANY SQ_WAIT_INST_ANY",
+    "MeanOccupancyPerActiveCU OccupancyPercent SQ_VALU_MFMA_COEXEC_CYCLES "
+    "SQ_INSTS_LDS_LOAD_BANDWIDTH SQ_INSTS_LDS_STORE_BANDWIDTH",
+)
+
+
+def attn_block_steps(lengths, n_heads, block=64):
+    """(forward, backward) key-block steps of the varlen attention over sequences of the given
+    lengths: a forward workgroup of query block i walks key blocks 0..i, so a sequence of nb
+    blocks takes nb(nb+1)/2 per head; the backward's dQ workgroups walk the same pairs and its
+    dK/dV workgroups (key block j over query blocks j..nb-1) as many again."""
+    per_head = sum((n + block - 1) // block * ((n + block - 1) // block + 1) // 2
+                   for n in lengths)
+    return n_heads * per_head, 2 * n_heads * per_head
+
+
+def summarize_attn_pmc(a_csv, b_csv, c_csv, bench_json, commands):
+    """Markdown table of the varlen attention kernels' counters (three rocprofv3 --pmc runs of
+    `bench.py --attention`): per launch group (kernel, grid), the instruction mix per key-block
+    step of a wavefront, the pipes' utilisation and the occupancy.  A kernel's groups are taken
+    in dispatch order: the 2048-token case, then the ragged batch (bench.py times them so)."""
+    bench = json.loads(open(bench_json).read().strip().splitlines()[-1])["attention"]
+    shape = bench["shape"]
+    NH, B, T = shape["q_heads"], shape["batch"], shape["seq"]
+    cases = (("2048 tokens", [T] * B, ""), ("ragged", shape["ragged_lengths"], "ragged_"))
+    passes = [_launch_groups(_read_csv(f)) for f in (a_csv, b_csv, c_csv)]
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    seen = {}
+    out = ["# Varlen attention counters (rocprofv3 PMC): the layer's kernels at 2048 tokens and "
+           "the ragged batch", "",
+           "Commands (run from /tmp on the MI355X box, TMPDIR=/tmp), one pass each:", "", "```",
+           *commands, "```", "",
+           "Per launch group (kernel, grid = threads / workgroup size), means over dispatches.  "
+           "Per-step figures divide a wave counter by 4 wavefronts x the key-block steps the "
+           "launch performs (forward: a query block of nb blocks walks its causal key blocks, "
+           "nb(nb+1)/2 per sequence and head; backward: as many dQ steps again as dK/dV steps); "
+           "they include each workgroup's set-up and epilogue and the idle slots of the grid.  "
+           "MfmaUtil = MFMA busy cycles / (GPU cycles x SIMDs); LdsUtil = LDS indexed-active "
+           "cycles / (GPU cycles x CUs); LdsBankConflict = conflict cycles per active cycle; "
+           "VALUBusy as rocprofv3 defines it; LDS issue / wait share = SQ_ACTIVE_INST_LDS / "
+           "SQ_WAIT_INST_LDS over SQ_ACTIVE_INST_ANY + SQ_WAIT_INST_ANY; occupancy: "
+           "MeanOccupancyPerActiveCU (waves per busy CU) and OccupancyPercent; LDS KB per step: "
+           "SQ_INSTS_LDS_LOAD_BANDWIDTH / _STORE_BANDWIDTH (64-byte units).", "",
+           "| case | kernel | grid / WG | µs (bench) | waves | key-block steps | VALU / step | "
+           "MFMA / step | LDS instr / step | LDS KB read / step | LDS KB written / step | "
+           "exp / step | VALUBusy % | MfmaUtil % | LdsUtil % | LdsBankConflict | "
+           "LDS issue / wait share | waves per busy CU | occupancy % |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"
+           "---:|---:|"]
+    for key, rows in passes[0].items():
+        kern = key[0].split("<")[0]
+        i = seen.get(kern, 0)
+        seen[kern] = i + 1
+        if i >= len(cases) or not kern.startswith("attn_"):
+            continue
+        label, lengths, tag = cases[i]
+        fwd_steps, bwd_steps = attn_block_steps(lengths, NH)
+        steps = fwd_steps if kern == "attn_fwd_kernel" else bwd_steps
+        us = (bench.get(f"{tag}varlen_fwd", {}).get("us") if kern == "attn_fwd_kernel" else
+              bench.get(f"{tag}varlen_bwd", {}).get("us") if kern == "attn_bwd_kernel" else None)
+        c = {}
+        for p_ in passes:
+            for r in p_.get(key, []):
+                c.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        m = {k: mean(v) for k, v in c.items()}
+        per = lambda k: f"{m[k] / (4 * steps):.0f}" if k in m and kern != "attn_bwd_delta_kernel" \
+            and kern != "attn_bwd_reduce_varlen_kernel" else "-"
+        kb = lambda k: (f"{m[k] * 64 / 1024 / (4 * steps):.1f}" if k in m and per(k) != "-"
+                        else "-")
+        busy = m.get("SQ_ACTIVE_INST_ANY", 0) + m.get("SQ_WAIT_INST_ANY", 0)
+        share = (f"{m.get('SQ_ACTIVE_INST_LDS', 0) / busy:.3f} / "
+                 f"{m.get('SQ_WAIT_INST_LDS', 0) / busy:.3f}") if busy else "-"
+        f = lambda k, d=1: f"{m[k]:.{d}f}" if k in m else "-"
+        out.append(
+            f"| {label} | `{key[0]}` | {key[1]} / {key[2]} | {us if us is not None else '-'} | "
+            f"{f('SQ_WAVES', 0)} | {steps if per('SQ_INSTS_VALU') != '-' else '-'} | "
+            f"{per('SQ_INSTS_VALU')} | {per('SQ_INSTS_MFMA')} | {per('SQ_INSTS_LDS')} | "
+            f"{kb('SQ_INSTS_LDS_LOAD_BANDWIDTH')} | {kb('SQ_INSTS_LDS_STORE_BANDWIDTH')} | "
+            f"{per('SQ_INSTS_VALU_TRANS_F32')} | {f('VALUBusy')} | {f('MfmaUtil')} | "
+            f"{f('LdsUtil')} | {f('LdsBankConflict', 3)} | {share} | "
+            f"{f('MeanOccupancyPerActiveCU', 2)} | {f('OccupancyPercent')} |")
+    return "\n".join(out) + "\n"
+
+
 def median(xs):
     s = sorted(xs)
     n = len(s)
@@ -1298,6 +1390,13 @@ def main():
                          "(CPU)")
     ap.add_argument("--summarize-kernels", nargs=3, metavar=("STATS_CSV", "TITLE", "CMD"),
                     help="print every kernel of a rocprofv3 --stats run by total time (CPU)")
+    ap.add_argument("--attention", action="store_true",
+                    help="time only the layer's varlen attention kernels (forward, backward; "
+                         "2048 real tokens and the ragged batch), print one JSON line and exit")
+    ap.add_argument("--summarize-attn-pmc", nargs=7,
+                    metavar=("A_CSV", "B_CSV", "C_CSV", "BENCH_JSON", "CMD1", "CMD2", "CMD3"),
+                    help="print the attention counter table of three rocprofv3 --pmc runs of "
+                         "bench.py --attention and exit (CPU)")
     ap.add_argument("--nf4-gemm", action="store_true",
                     help="time the fused NF4-dequant GEMM against hipBLASLt and unpack + "
                          "hipBLASLt at M = 2048, print one JSON line and exit")
@@ -1308,6 +1407,10 @@ def main():
                     help="print the per-kernel breakdown of one training step of a rocprofv3 "
                          "--kernel-trace run (CPU)")
     args = ap.parse_args()
+    if args.summarize_attn_pmc:
+        a = args.summarize_attn_pmc
+        sys.stdout.write(summarize_attn_pmc(a[0], a[1], a[2], a[3], a[4:]))
+        return
     if args.summarize_valu:
         a = args.summarize_valu
         sys.stdout.write(summarize_valu(a[0], a[1], a[2], a[3:]))
@@ -1350,6 +1453,12 @@ def main():
         gemm_table = {"table": os.path.relpath(gemm_tuning.RESULTS, ROOT), "accepted": accepted}
         log(f"tuned hipBLASLt solutions ({gemm_table['table']}): "
             f"{'replayed' if accepted else 'rejected by TunableOp, heuristic choices'}")
+    if args.attention:
+        print(json.dumps({"attention": time_attention(dev, args.steps, args.warmup,
+                                                      varlen_only=True),
+                          "timing": "GPU time per call: calls queued behind a device-side "
+                                    "wait and timed as one span"}), flush=True)
+        return
     if args.nf4_gemm:
         print(json.dumps({"nf4_gemm": time_nf4_gemm(dev), "gemm_selection": gemm_table,
                           "timing": "GPU time per call: calls queued behind a device-side "
