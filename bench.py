@@ -312,7 +312,9 @@ def build_shape_cases(dev, n_sets=None, lib=None):
     tokens of 4 x 512; the forward also writes the zeros of the 1160 pad positions, in the same
     launch, as the reference's padded layout needs); the token-major RoPE forward the layer
     runs (soupk_rope_pack_tokens: rotated q, k and v + LoRA in qkv's own row layout, no pad
-    rows) on all 2048 tokens and on the ragged batch; and the vocab-head kernel on a 2048-row
+    rows) on all 2048 tokens and on the ragged batch; the add + RMSNorm forward and backward on
+    the ragged batch (888 rows; the forward's padded output over all 2048 positions); and the
+    vocab-head kernel on a 2048-row
     chunk (head.CHUNK_ROWS, the product's chunk) through soupk_head_stats_grad_rows, the entry
     FusedHeadLoss uses (gradient rows packed into their own buffer), 90% of rows labelled."""
     H, NH, NKV, D, B, T = (workloads.HIDDEN, workloads.N_HEADS, workloads.N_KV,
@@ -365,6 +367,33 @@ def build_shape_cases(dev, n_sets=None, lib=None):
         cases.append(Case(name, "rope_pack_fwd_kernel", "soupk_rope_pack_tokens",
                           rows * W * 2 + rows * (NH + NKV) * D * 4 + tab + 8 * rows
                           + rows * W * 2, tsets, lib=lib))
+    # add + RMSNorm forward / backward on the ragged batch: M real rows, the forward's padded
+    # output over all B * T positions (the 1160 unmapped rows zeroed in the same launch), the
+    # backward's padded gradient gathered at the M mapped positions
+    PT = B * T
+    rfsets, rbsets = [], []
+    for i in range(rotation_sets(14 * M * H, n_sets)):
+        x, delta, w, pad_idx, padded = workloads.rmsnorm_inputs(M, H, PT, seed=52 + 10 * i,
+                                                                device=dev)
+        s_o = torch.empty_like(x)
+        y = torch.empty((M, H), dtype=torch.float16, device=dev)
+        ypad = torch.empty((PT, H), dtype=torch.float32, device=dev)
+        rstd = torch.empty(M, dtype=torch.float32, device=dev)
+        rfsets.append(((x, delta, w, pad_idx, s_o, y, ypad, rstd),
+                       (p(x), p(delta), p(w), p(s_o), p(y), p(ypad), p(pad_idx), None, p(rstd),
+                        M, PT, H, 1e-6)))
+        dy, dypad, ds = workloads.rmsnorm_grads(M, H, PT, seed=53 + 10 * i, device=dev)
+        s_b = x + delta.float()
+        rstd_b = torch.rsqrt(s_b.pow(2).mean(-1) + 1e-6)
+        dx = torch.empty_like(x)
+        dd = torch.empty((M, H), dtype=torch.float16, device=dev)
+        rbsets.append(((s_b, rstd_b, w, dy, dypad, pad_idx, ds, dx, dd),
+                       (p(s_b), p(rstd_b), p(w), p(dy), p(dypad), p(pad_idx), p(ds), p(dx),
+                        p(dd), M, PT, H)))
+    cases.append(Case("rmsnorm_fwd_ragged888", "rmsnorm_fwd_kernel", "soupk_rmsnorm_fwd",
+                      16 * M * H + 4 * (PT - M) * H + 4 * H + 4 * M + 8 * M, rfsets, lib=lib))
+    cases.append(Case("rmsnorm_bwd_ragged888", "rmsnorm_bwd_kernel", "soupk_rmsnorm_bwd",
+                      20 * M * H + 4 * H + 4 * M + 8 * M, rbsets, lib=lib))
     rows, V = 2048, workloads.VOCAB
     sets, n_lab = [], 0
     for i in range(rotation_sets(rows * V * 2, n_sets)):

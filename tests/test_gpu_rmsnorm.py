@@ -23,6 +23,8 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "rmsnorm_qwen2.npz")
 CASES = [  # rows, hidden, padded, with_delta, with_pad
     (2048, 1536, 2048, True, True),     # the step's shape: every padded row holds a token
     (888, 1536, 2048, True, True),      # ragged batch: pad rows zeroed by the same launch
+    (1500, 1536, 2048, True, True),     # 4 rows per workgroup (2048 and up: 8; under 1024: 2)
+    (2051, 1536, 2051, True, True),     # 8 rows per workgroup with a partial last workgroup
     (300, 1536, 512, True, False),
     (300, 1536, 512, False, True),
     (7, 96, 10, True, True),

@@ -11,19 +11,17 @@
 // between the load, the wave64 reduction (DPP steps; combined across the row's waves in LDS) and
 // the stores.  In the forward pass two waves per row give 16 waves per CU at 2048 rows, which
 // hides HBM latency better than one (and 2 rows per wave, 4 waves per CU, ran 40% slower).  A
-// workgroup holds four rows.  In the forward pass extra workgroups after the row workgroups
-// zero the rows of the padded fp32 output that no token maps to (the pad rows), so the padded
-// tensor needs no separate memset.
+// workgroup holds 2, 4 or 8 rows, by the row count.  In the forward pass extra workgroups after
+// the row workgroups zero the rows of the padded fp32 output that no token maps to (the pad
+// rows), so the padded tensor needs no separate memset.
 
 #include "soupk_common.hpp"
 
 namespace soupk {
 namespace {
 
-#ifndef SOUPK_NORM_ROWS
-#define SOUPK_NORM_ROWS 4
-#endif
-constexpr int kRowsPerBlock = SOUPK_NORM_ROWS;  // rows per workgroup
+// Rows per workgroup, chosen at launch from the row count (fwd_rows_per_block,
+// bwd_rows_per_block below).
 // Wavefronts per row on the vector path (measured on MI355X at 2048 x 1536: the forward pass is
 // 17% faster with two than with one; the backward pass, with streaming stores, 2% faster).
 #ifndef SOUPK_NORM_WPR_FWD
@@ -84,14 +82,14 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v) {
 // loads are issued before any arithmetic: in the backward through the rows' buffer descriptors
 // (chunks past a row's end read zeros), in the forward at clamped chunk indices (lanes past the
 // row's end zero their values with a select).
-template <int CPL, int WPR>
-__global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kernel(
+template <int CPL, int WPR, int ROWS>
+__global__ __launch_bounds__(kWave * ROWS * WPR) void rmsnorm_fwd_kernel(
     const float* __restrict__ x, const uint16_t* __restrict__ delta, const float* __restrict__ w,
     float* __restrict__ s_out, uint16_t* __restrict__ y, float* __restrict__ ypad,
     const int64_t* __restrict__ pad_idx, const int32_t* __restrict__ pad_inv,
     float* __restrict__ rstd_out, int64_t rows, int64_t pad_rows, int H, float eps,
     int64_t row_blocks) {
-  __shared__ float part[kRowsPerBlock][WPR];
+  __shared__ float part[ROWS][WPR];
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -99,14 +97,14 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
   if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
     // Zero the padded rows that no token row is scattered to (one row per wavefront).
     const int64_t p =
-        (static_cast<int64_t>(blockIdx.x) - row_blocks) * (kRowsPerBlock * WPR) + wave;
+        (static_cast<int64_t>(blockIdx.x) - row_blocks) * (ROWS * WPR) + wave;
     if (p >= pad_rows || pad_inv[p] >= 0) return;
     const FwdOut dst(ypad + p * H, static_cast<uint64_t>(H) * 4u);
     for (int c = lane; c < nch; c += kWave) dst.store(16u * c, zero);
     return;
   }
   const int rib = wave / WPR, sub = wave % WPR;  // row in block, wave within the row
-  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rib;
+  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * ROWS + rib;
   const bool live = row_raw < rows;  // (all waves reach the barrier below)
   const int64_t row = live ? row_raw : rows - 1;
   // (The forward keeps global loads at clamped chunk indices, with the delta loads under their
@@ -172,18 +170,18 @@ __global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_fwd_kerne
   if (sub == 0 && lane == 0) rstd_out[row] = rstd;
 }
 
-template <int CPL, int WPR>
-__global__ __launch_bounds__(kWave * kRowsPerBlock * WPR) void rmsnorm_bwd_kernel(
+template <int CPL, int WPR, int ROWS>
+__global__ __launch_bounds__(kWave * ROWS * WPR) void rmsnorm_bwd_kernel(
     const float* __restrict__ s, const float* __restrict__ rstd_in, const float* __restrict__ w,
     const uint16_t* __restrict__ dy, const float* __restrict__ dypad,
     const int64_t* __restrict__ pad_idx, const float* __restrict__ ds, float* __restrict__ dx,
     uint16_t* __restrict__ ddelta, int64_t rows, int64_t pad_rows, int H) {
-  __shared__ float part[kRowsPerBlock][WPR];
+  __shared__ float part[ROWS][WPR];
   const int lane = threadIdx.x % kWave;
   const int nch = H / 4;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int rib = wave / WPR, sub = wave % WPR;
-  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + rib;
+  const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * ROWS + rib;
   const bool live = row_raw < rows;  // (all waves reach the barrier below)
   const int64_t row = live ? row_raw : rows - 1;
   // The padded gradient row is a gather through pad_idx.  Its index is loaded first, and the
@@ -363,26 +361,47 @@ int with_cpl(int cpl, Args... args) {
 }
 constexpr int kMaxCpl = 16;  // H <= 4 * 64 * WPR * 16 on the register-resident path
 
+// Rows per workgroup (measured on MI355X, 256 CUs, H = 1536, medians of 5 rounds in one
+// process): the backward at 2048 rows takes 10.35 us with 8 rows per workgroup (one
+// 1024-thread workgroup per CU), 11.23 with 4, 12.03 with 2; at the ragged batch's 888 rows 8
+// rows leave most CUs idle (7.16 us) and 4 is best (5.49; 2: 6.28).  The forward: 8.20 / 8.28
+// / 8.42 us at 2048 rows with 8 / 4 / 2 rows per workgroup, and 5.80 / 5.42 / 5.21 us at 888.
+constexpr int64_t kFullWaveRows = 8 * 256;   // 8 rows per workgroup fill the 256 CUs once
+int fwd_rows_per_block(int64_t rows) {
+  return rows >= kFullWaveRows ? 8 : rows >= kFullWaveRows / 2 ? 4 : 2;
+}
+int bwd_rows_per_block(int64_t rows) { return rows >= kFullWaveRows ? 8 : 4; }
+
 template <int CPL>
 struct FwdLaunch {
-  static int run(dim3 grid, hipStream_t st, const float* x, const uint16_t* delta, const float* w,
-                 float* s_out, uint16_t* y, float* ypad, const int64_t* pad_idx,
-                 const int32_t* pad_inv, float* rstd, int64_t rows, int64_t pad_rows, int H,
-                 float eps, int64_t row_blocks) {
-    return launch_kernel(rmsnorm_fwd_kernel<CPL, kWprFwd>, grid,
-                         dim3(kWave * kRowsPerBlock * kWprFwd), st, x, delta, w, s_out, y, ypad,
-                         pad_idx, pad_inv, rstd, rows, pad_rows, H, eps, row_blocks);
+  template <int ROWS>
+  static int go(dim3 grid, hipStream_t st, const float* x, const uint16_t* delta, const float* w,
+                float* s_out, uint16_t* y, float* ypad, const int64_t* pad_idx,
+                const int32_t* pad_inv, float* rstd, int64_t rows, int64_t pad_rows, int H,
+                float eps, int64_t row_blocks) {
+    return launch_kernel(rmsnorm_fwd_kernel<CPL, kWprFwd, ROWS>, grid,
+                         dim3(kWave * ROWS * kWprFwd), st, x, delta, w, s_out, y, ypad, pad_idx,
+                         pad_inv, rstd, rows, pad_rows, H, eps, row_blocks);
+  }
+  template <typename... Args>
+  static int run(int rpb, Args... args) {
+    return rpb == 8 ? go<8>(args...) : rpb == 4 ? go<4>(args...) : go<2>(args...);
   }
 };
 
 template <int CPL>
 struct BwdLaunch {
-  static int run(dim3 grid, hipStream_t st, const float* s, const float* rstd, const float* w,
-                 const uint16_t* dy, const float* dypad, const int64_t* pad_idx, const float* ds,
-                 float* dx, uint16_t* ddelta, int64_t rows, int64_t pad_rows, int H) {
-    return launch_kernel(rmsnorm_bwd_kernel<CPL, kWprBwd>, grid,
-                         dim3(kWave * kRowsPerBlock * kWprBwd), st, s, rstd, w, dy, dypad,
-                         pad_idx, ds, dx, ddelta, rows, pad_rows, H);
+  template <int ROWS>
+  static int go(dim3 grid, hipStream_t st, const float* s, const float* rstd, const float* w,
+                const uint16_t* dy, const float* dypad, const int64_t* pad_idx, const float* ds,
+                float* dx, uint16_t* ddelta, int64_t rows, int64_t pad_rows, int H) {
+    return launch_kernel(rmsnorm_bwd_kernel<CPL, kWprBwd, ROWS>, grid,
+                         dim3(kWave * ROWS * kWprBwd), st, s, rstd, w, dy, dypad, pad_idx, ds,
+                         dx, ddelta, rows, pad_rows, H);
+  }
+  template <typename... Args>
+  static int run(int rpb, Args... args) {
+    return rpb == 8 ? go<8>(args...) : go<4>(args...);
   }
 };
 
@@ -410,12 +429,13 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_fwd(
   const bool vec = H % 4 == 0 && cpl <= kMaxCpl && aligned(x, 16) && aligned(w, 16) &&
                    aligned(s_out, 16) && aligned(ypad, 16) && aligned(delta, 8) && aligned(y, 8);
   if (vec) {
-    const int64_t row_blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    const int64_t zero_per_block = kRowsPerBlock * kWprFwd;  // one pad row per wavefront
+    const int rpb = fwd_rows_per_block(rows);
+    const int64_t row_blocks = (rows + rpb - 1) / rpb;
+    const int64_t zero_per_block = rpb * kWprFwd;  // one pad row per wavefront
     const int64_t blocks = row_blocks + (zero_rows + zero_per_block - 1) / zero_per_block;
     if (blocks > 0x7fffffff) return kInvalid;
-    return with_cpl<FwdLaunch>(cpl, dim3(static_cast<unsigned>(blocks)), st, x, delta, w, s_out,
-                               y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows,
+    return with_cpl<FwdLaunch>(cpl, rpb, dim3(static_cast<unsigned>(blocks)), st, x, delta, w,
+                               s_out, y, ypad, pad_idx, pad_inv, rstd, rows, pad_rows,
                                static_cast<int>(H), eps, row_blocks);
   }
   const int64_t blocks = rows + zero_rows;
@@ -439,10 +459,11 @@ extern "C" __attribute__((visibility("default"))) int soupk_rmsnorm_bwd(
                    aligned(dypad, 16) && aligned(ds, 16) && aligned(dx, 16) && aligned(dy, 8) &&
                    aligned(ddelta, 8);
   if (vec) {
-    const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int rpb = bwd_rows_per_block(rows);
+    const int64_t blocks = (rows + rpb - 1) / rpb;
     if (blocks > 0x7fffffff) return kInvalid;
-    return with_cpl<BwdLaunch>(cpl, dim3(static_cast<unsigned>(blocks)), st, s, rstd, w, dy,
-                               dypad, pad_idx, ds, dx, ddelta, rows, pad_rows,
+    return with_cpl<BwdLaunch>(cpl, rpb, dim3(static_cast<unsigned>(blocks)), st, s, rstd, w,
+                               dy, dypad, pad_idx, ds, dx, ddelta, rows, pad_rows,
                                static_cast<int>(H));
   }
   if (rows > 0x7fffffff) return kInvalid;
