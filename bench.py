@@ -379,9 +379,11 @@ def build_shape_cases(dev, n_sets=None, lib=None):
         y = torch.empty((M, H), dtype=torch.float16, device=dev)
         ypad = torch.empty((PT, H), dtype=torch.float32, device=dev)
         rstd = torch.empty(M, dtype=torch.float32, device=dev)
-        rfsets.append(((x, delta, w, pad_idx, s_o, y, ypad, rstd),
-                       (p(x), p(delta), p(w), p(s_o), p(y), p(ypad), p(pad_idx), None, p(rstd),
-                        M, PT, H, 1e-6)))
+        inv = torch.full((PT,), -1, dtype=torch.int32, device=dev)
+        inv[pad_idx] = torch.arange(M, dtype=torch.int32, device=dev)
+        rfsets.append(((x, delta, w, pad_idx, inv, s_o, y, ypad, rstd),
+                       (p(x), p(delta), p(w), p(s_o), p(y), p(ypad), p(pad_idx), p(inv),
+                        p(rstd), M, PT, H, 1e-6)))
         dy, dypad, ds = workloads.rmsnorm_grads(M, H, PT, seed=53 + 10 * i, device=dev)
         s_b = x + delta.float()
         rstd_b = torch.rsqrt(s_b.pow(2).mean(-1) + 1e-6)
@@ -391,7 +393,8 @@ def build_shape_cases(dev, n_sets=None, lib=None):
                        (p(s_b), p(rstd_b), p(w), p(dy), p(dypad), p(pad_idx), p(ds), p(dx),
                         p(dd), M, PT, H)))
     cases.append(Case("rmsnorm_fwd_ragged888", "rmsnorm_fwd_kernel", "soupk_rmsnorm_fwd",
-                      16 * M * H + 4 * (PT - M) * H + 4 * H + 4 * M + 8 * M, rfsets, lib=lib))
+                      16 * M * H + 4 * (PT - M) * H + 4 * H + 4 * M + 8 * M + 4 * PT, rfsets,
+                      lib=lib))
     cases.append(Case("rmsnorm_bwd_ragged888", "rmsnorm_bwd_kernel", "soupk_rmsnorm_bwd",
                       20 * M * H + 4 * H + 4 * M + 8 * M, rbsets, lib=lib))
     rows, V = 2048, workloads.VOCAB

@@ -368,6 +368,9 @@ constexpr int kMaxCpl = 16;  // H <= 4 * 64 * WPR * 16 on the register-resident 
 // / 8.42 us at 2048 rows with 8 / 4 / 2 rows per workgroup, and 5.80 / 5.42 / 5.21 us at 888.
 constexpr int64_t kFullWaveRows = 8 * 256;   // 8 rows per workgroup fill the 256 CUs once
 int fwd_rows_per_block(int64_t rows) {
+#ifdef SOUPK_NORM_FWD_RPB
+  if (SOUPK_NORM_FWD_RPB) return SOUPK_NORM_FWD_RPB;
+#endif
   return rows >= kFullWaveRows ? 8 : rows >= kFullWaveRows / 2 ? 4 : 2;
 }
 int bwd_rows_per_block(int64_t rows) { return rows >= kFullWaveRows ? 8 : 4; }
