@@ -113,3 +113,20 @@ def test_step_summary_reports_host_issue_time_of_the_slowest_step():
     assert st["mean"] == round(sum(per) / 5, 1) and st["gc_collections"] == 0
     plain = bench.step_summary(per, sum(per), bench.GcWatch())    # no host times recorded
     assert "host_issue_median" not in plain and plain["slowest_step"] == 2
+
+
+def test_attention_block_steps_count_the_causal_key_blocks():
+    """The attention counter table divides by the key-block steps a launch performs: a
+    sequence of nb 64-row blocks has nb(nb+1)/2 (query block, key block) steps per head in the
+    forward, and the backward's dK/dV and dQ workgroups walk that many each."""
+    assert bench.attn_block_steps([64], 1) == (1, 2)
+    assert bench.attn_block_steps([65], 1) == (3, 6)          # 2 blocks: (0,0), (1,0), (1,1)
+    assert bench.attn_block_steps([512] * 4, 12) == (12 * 4 * 36, 2 * 12 * 4 * 36)
+    assert bench.attn_block_steps([512, 152, 128, 96], 12) == (12 * (36 + 6 + 3 + 3),
+                                                               2 * 12 * 48)
+    assert bench.attn_block_steps([0, 1], 2) == (2, 4)
+    # brute force over (query block, key block <= query block) pairs
+    for n in (1, 63, 64, 200, 511):
+        nb = -(-n // 64)
+        pairs = sum(1 for q in range(nb) for k in range(q + 1))
+        assert bench.attn_block_steps([n], 3) == (3 * pairs, 6 * pairs)
