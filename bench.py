@@ -789,8 +789,9 @@ def time_nf4_gemm(dev, calls=40):
     projections of a layer (q|k|v and gate|up as stacked parts): the fused kernel on fp16 and
     on NF4 weights, hipBLASLt (torch.matmul) on fp16 weights, the standalone unpack
     (nf4.unpack_concat) and unpack + hipBLASLt; and the input gradient dx = dy W fused
-    (nf4_gemm.nf4_grad_input), on hipBLASLt and unpack + hipBLASLt.  Each variant: 5 untimed
-    calls, then `calls`
+    (nf4_gemm.nf4_grad_input), on hipBLASLt and unpack + hipBLASLt; then the fused forward and
+    input gradient against unpack + hipBLASLt at the smaller row counts SWEEP_ROWS
+    (`rows_sweep`).  Each variant: 5 untimed calls, then `calls`
     calls queued behind a DeviceHold and timed as one span (torch events), so host overhead is
     not in the figure.  Synthetic NF4 weights (workloads.nf4_weight), x ~ N(0, 1)."""
     from testt_amd import nf4, nf4_gemm
@@ -839,8 +840,25 @@ def time_nf4_gemm(dev, calls=40):
             "bwd_unpack_then_hipblaslt_us": span_us(
                 lambda: torch.matmul(dy, nf4.unpack_concat(ws, dev))),
         }
+        # smaller row counts (decode- and eval-sized batches): the fused forward and input
+        # gradient against unpack + hipBLASLt
+        sweep = {}
+        for m in SWEEP_ROWS:
+            xm, dym = x[:m].contiguous(), dy[:m].contiguous()
+            sweep[m] = {
+                "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(xm, ws)),
+                "unpack_then_hipblaslt_us": span_us(
+                    lambda: torch.matmul(xm, nf4.unpack_concat(ws, dev).t())),
+                "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dym, ws)),
+                "bwd_unpack_then_hipblaslt_us": span_us(
+                    lambda: torch.matmul(dym, nf4.unpack_concat(ws, dev))),
+            }
+        out[name]["rows_sweep"] = sweep
         del ws, x, w16, dy
     return out
+
+
+SWEEP_ROWS = (16, 64, 256, 512, 1024)   # row counts of the fused NF4 GEMM sweep
 
 
 def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
@@ -1177,6 +1195,106 @@ def summarize_trace(trace_csv, title, command):
     return "\n".join(out) + "\n"
 
 
+NF4_GEMM_VARIANTS = ("fused_fp16_w_us", "fused_nf4_w_us", "hipblaslt_fp16_w_us", "unpack_us",
+                     "unpack_then_hipblaslt_us", "bwd_fused_nf4_w_us", "bwd_hipblaslt_fp16_w_us",
+                     "bwd_unpack_then_hipblaslt_us")
+NF4_GEMM_SWEEP_VARIANTS = ("fused_nf4_w_us", "unpack_then_hipblaslt_us", "bwd_fused_nf4_w_us",
+                           "bwd_unpack_then_hipblaslt_us")
+
+
+def nf4_gemm_spans(trace_csv, bench, calls=40):
+    """Mean kernel time per call of each timed group of a `bench.py --nf4-gemm` kernel trace.
+    Every group is `calls` calls queued behind one device-side wait, so the dispatches between
+    two waits are one group's timed calls followed by the next group's untimed ones; a call is
+    one kernel, or two for the unpack + hipBLASLt groups (their means are added).  Returns
+    {(shape, rows, variant): (kernel names, microseconds)} in the order time_nf4_gemm runs them."""
+    spans, cur = [], None
+    for r in sorted(_read_csv(trace_csv), key=lambda r: int(r["Dispatch_Id"])):
+        name = r["Kernel_Name"]
+        if "bench_hold_kernel" in name:
+            cur = []
+            spans.append(cur)
+        elif cur is not None:
+            cur.append(r)
+    order = []
+    for shape, v in bench.items():
+        order += [(shape, v["M"], k) for k in NF4_GEMM_VARIANTS]
+        for m in v.get("rows_sweep", {}):
+            order += [(shape, int(m), k) for k in NF4_GEMM_SWEEP_VARIANTS]
+    if len(spans) != len(order):
+        raise ValueError(f"{len(spans)} timed spans in the trace, {len(order)} groups expected")
+    out = {}
+    for key, rs in zip(order, spans):
+        per_call = 2 if key[2].endswith("unpack_then_hipblaslt_us") else 1
+        timed = rs[:calls * per_call]
+        by = {}
+        for r in timed:
+            n = r["Kernel_Name"]
+            short = _kernel_base(n) if "soupk" in n else n.split("(")[0][:60]
+            by.setdefault(short, []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out[key] = (sorted(by), sum(sum(d) / len(d) for d in by.values()))
+    return out
+
+
+def summarize_nf4_gemm(trace_csv, bench_json, command):
+    """Markdown tables of a rocprofv3 --kernel-trace run of `bench.py --nf4-gemm`: per
+    projection the fused NF4-dequant GEMM (forward, input gradient) against hipBLASLt and
+    unpack + hipBLASLt at 2048 rows, then the fused kernels against unpack + hipBLASLt over
+    the smaller row counts, each figure the mean kernel time of its 40 timed calls."""
+    bench = json.loads(open(bench_json).read().strip().splitlines()[-1])["nf4_gemm"]
+    spans = nf4_gemm_spans(trace_csv, bench)
+    t = lambda shape, m, k: spans[(shape, m, k)][1]
+    label = {"qkv": "q\\|k\\|v", "o": "o", "gate_up": "gate\\|up", "down": "down"}
+    out = [f"# rocprofv3 kernel trace: fused NF4-dequant GEMM (forward and input gradient) "
+           "against hipBLASLt and unpack + hipBLASLt (bench.py --nf4-gemm)", "",
+           "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```", command, "```",
+           "", "Per projection shape (q|k|v: N 2048 as 1536 + 256 + 256, K 1536; o: N 1536, "
+           "K 1536; gate|up: N 17920 as 8960 + 8960, K 1536; down: N 1536, K 8960) bench.py "
+           "times each variant as 5 untimed calls and then 40 calls queued behind a device-side "
+           "wait; every figure below is the mean kernel duration of those 40 calls in this "
+           "trace (unpack + hipBLASLt: the two kernels' means added).  Fused: this build's "
+           "`gemm_tn_kernel` (forward, y = x W^T) and `gemm_nn_nf4_kernel` (input gradient, "
+           "dx = dy W) with W read as NF4 and dequantised in the tile loads.", "",
+           "At 2048 rows (microseconds; **bold**: the faster of fused and unpack + hipBLASLt):",
+           "", "| shape | fused, fp16 W | fused, NF4 W | hipBLASLt, fp16 W | unpack alone | "
+           "unpack + hipBLASLt | fused dx, NF4 W | hipBLASLt dx, fp16 W | unpack + hipBLASLt dx |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    b = lambda x, y: (f"**{x:.2f}**", f"{y:.2f}") if x <= y else (f"{x:.2f}", f"**{y:.2f}**")
+    for shape, v in bench.items():
+        m = v["M"]
+        f, u = b(t(shape, m, "fused_nf4_w_us"), t(shape, m, "unpack_then_hipblaslt_us"))
+        fd, ud = b(t(shape, m, "bwd_fused_nf4_w_us"), t(shape, m, "bwd_unpack_then_hipblaslt_us"))
+        out.append(f"| {label.get(shape, shape)} | {t(shape, m, 'fused_fp16_w_us'):.2f} | {f} | "
+                   f"{t(shape, m, 'hipblaslt_fp16_w_us'):.2f} | {t(shape, m, 'unpack_us'):.2f} | "
+                   f"{u} | {fd} | {t(shape, m, 'bwd_hipblaslt_fp16_w_us'):.2f} | {ud} |")
+    out += ["", "Smaller row counts (decode- and eval-sized batches), microseconds; `*`: the path "
+            "FrozenNF4Linear takes (testt_amd/nf4_gemm.py prefer_fused, "
+            "prefer_fused_grad_input):", "",
+            "| shape | rows | fused | unpack + hipBLASLt | fused dx | unpack + hipBLASLt dx |",
+            "|---|---:|---:|---:|---:|---:|"]
+    from testt_amd import nf4_gemm
+    cus = 256
+    dims = {"qkv": (2048, 1536), "o": (1536, 1536), "gate_up": (17920, 1536),
+            "down": (1536, 8960)}
+    for shape, v in bench.items():
+        n, k = dims.get(shape, (v["N"], v["K"]))
+        for m in sorted(int(x) for x in v.get("rows_sweep", {})):
+            f, u = b(t(shape, m, "fused_nf4_w_us"), t(shape, m, "unpack_then_hipblaslt_us"))
+            fd, ud = b(t(shape, m, "bwd_fused_nf4_w_us"),
+                       t(shape, m, "bwd_unpack_then_hipblaslt_us"))
+            if nf4_gemm.fused_fits(m, n, k, nf4_gemm.FWD_TILE, cus):
+                f += " *"
+            else:
+                u += " *"
+            if nf4_gemm.fused_fits(m, k, n, nf4_gemm.GRAD_TILE, cus):
+                fd += " *"
+            else:
+                ud += " *"
+            out.append(f"| {label.get(shape, shape)} | {m} | {f} | {u} | {fd} | {ud} |")
+    return "\n".join(out) + "\n"
+
+
 def summarize_step(trace_csv, title, command, n_layers=28, top=32):
     """Markdown breakdown of one training step from a rocprofv3 --kernel-trace run of bench.py:
     the launches between the first attention forward of one step and that of the next (steps
@@ -1432,6 +1550,9 @@ def main():
     ap.add_argument("--nf4-gemm", action="store_true",
                     help="time the fused NF4-dequant GEMM against hipBLASLt and unpack + "
                          "hipBLASLt at M = 2048, print one JSON line and exit")
+    ap.add_argument("--summarize-nf4-gemm", nargs=3, metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
+                    help="print the fused NF4 GEMM tables of a rocprofv3 --kernel-trace run of "
+                         "bench.py --nf4-gemm and exit (CPU)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "TITLE", "CMD"),
                     help="print every launch group (kernel, grid) of a rocprofv3 "
                          "--kernel-trace run (CPU)")
@@ -1439,6 +1560,10 @@ def main():
                     help="print the per-kernel breakdown of one training step of a rocprofv3 "
                          "--kernel-trace run (CPU)")
     args = ap.parse_args()
+    if args.summarize_nf4_gemm:
+        a = args.summarize_nf4_gemm
+        sys.stdout.write(summarize_nf4_gemm(a[0], a[1], a[2]))
+        return
     if args.summarize_attn_pmc:
         a = args.summarize_attn_pmc
         sys.stdout.write(summarize_attn_pmc(a[0], a[1], a[2], a[3], a[4:]))

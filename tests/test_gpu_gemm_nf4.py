@@ -90,9 +90,10 @@ def test_rejects_shapes():
 
 
 def test_frozen_linear_fused_switch(monkeypatch):
-    """FrozenNF4Linear with the fused NF4 GEMM forward against its unpack + hipBLASLt forward:
-    the same fp16 weights, sums in another order (relative L2 < 1e-3); the backward is the same
-    path either way."""
+    """FrozenNF4Linear with the fused NF4 GEMM forward and input gradient (forced on for this
+    shape) against its unpack + hipBLASLt path: the same fp16 weights, sums in another order
+    (relative L2 < 1e-3 for the output and the input gradient)."""
+    from testt_amd import nf4_gemm
     ws = [workloads.nf4_weight(r, 512, seed=70 + i, device=DEV, absmax2_range=(0.005, 0.02),
                                offset=0.01) for i, r in enumerate((256, 128))]
     g = torch.Generator().manual_seed(6)
@@ -100,12 +101,20 @@ def test_frozen_linear_fused_switch(monkeypatch):
     b = (0.1 * torch.randn(384, generator=g)).to(torch.float16).to(DEV)
     gout = (1e-2 * torch.randn(200, 384, generator=g)).to(torch.float16).to(DEV)
     res = []
+    calls = []
+    grad = nf4_gemm.nf4_grad_input
+    monkeypatch.setattr(nf4_gemm, "prefer_fused", lambda x, w: True)
+    monkeypatch.setattr(nf4_gemm, "prefer_fused_grad_input", lambda dy, w: True)
+    monkeypatch.setattr(nf4_gemm, "nf4_grad_input",
+                        lambda dy, w: calls.append(dy.shape) or grad(dy, w))
     for fused in (False, True):
         monkeypatch.setattr(nf4, "USE_FUSED_NF4_GEMM", fused)
         x = x0.clone().requires_grad_(True)
         out = nf4.frozen_linear(x, ws, b)
         out.backward(gout)
         res.append((out.detach(), x.grad))
-    rel = float((res[1][0].double() - res[0][0].double()).norm() / res[0][0].double().norm())
-    assert rel < 1e-3, rel
-    assert torch.equal(res[0][1], res[1][1])
+    assert calls == [(200, 384)]          # the fused input gradient ran in the fused pass only
+    for i in (0, 1):
+        ref = res[0][i].double()
+        rel = float((res[1][i].double() - ref).norm() / ref.norm())
+        assert rel < 1e-3, (i, rel)

@@ -34,16 +34,15 @@ BYTES_PER_PROGRAM = 16384
 # deterministic).  False restores the reference's memory profile.
 KEEP_UNPACKED_FOR_BACKWARD = True
 
-# FrozenNF4Linear's forward through the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py: W read
-# as NF4, dequantised in the GEMM's tile loads, no fp16 W in HBM) where it measured ahead of
-# unpack + hipBLASLt on MI355X (nf4_gemm.prefer_fused: the q|k|v and o projections of
-# Qwen2.5-1.5B with at most one wave of 128 x 128 tiles, M <= 2048: q|k|v 27.1 against 28.0 us
-# at M = 2048, 2-3% ahead from M = 768 on; o level); elsewhere (gate|up, down, larger M) it is
-# behind and the unpack + hipBLASLt path runs.  Only a forward that unpacks W itself uses it: a
-# caller that passes the unpacked weight (the decoder layer's one-launch unpack of all seven
-# projections) keeps hipBLASLt.  The backward unpacks W and runs hipBLASLt, as the reference
-# does: the fused input-gradient GEMM (nf4_gemm.nf4_grad_input) measured behind it
-# (40.9 / 28.8 against 34.0 / 28.3 us at the q|k|v / o shapes).
+# FrozenNF4Linear through the fused NF4-dequant GEMM (testt_amd/nf4_gemm.py: W read as NF4,
+# dequantised in the GEMM's tile loads, no fp16 W in HBM) where it measured ahead of unpack +
+# hipBLASLt on MI355X (nf4_gemm.prefer_fused, prefer_fused_grad_input: a grid of half to one
+# wave of the compute units and a contraction of at most 2048, e.g. the q|k|v and o forward at
+# 1024-2048 rows, the gate|up forward at up to 128 rows, the q|k|v and o input gradient at
+# 1024 rows, down's input gradient at up to 128 rows); elsewhere unpack + hipBLASLt runs.  Only
+# a forward that unpacks W itself uses it: a caller that passes the unpacked weight (the
+# decoder layer's one-launch unpack of all seven projections) keeps hipBLASLt, and so does a
+# backward that has the forward's unpacked weight (KEEP_UNPACKED_FOR_BACKWARD).
 USE_FUSED_NF4_GEMM = True
 
 
@@ -430,8 +429,17 @@ class FrozenNF4Linear(torch.autograd.Function):
     def backward(ctx, grad_out):
         grad_x = None
         if ctx.needs_input_grad[0]:
-            weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
             g = grad_out.to(torch.float16)
+            if getattr(ctx, "unpacked", None) is None and USE_FUSED_NF4_GEMM:
+                # no unpacked weight kept: the fused input gradient where it is the faster path
+                from . import nf4_gemm
+
+                g2 = g.reshape(-1, g.shape[-1])
+                if nf4_gemm.grad_input_supported(g2, ctx.weights) and \
+                        nf4_gemm.prefer_fused_grad_input(g2, ctx.weights):
+                    dx = nf4_gemm.nf4_grad_input(g2, ctx.weights)
+                    return dx.view(*g.shape[:-1], dx.shape[-1]), None, None, None
+            weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
             grad_x = torch.mm(g, weight) if g.dim() == 2 else g @ weight
         return grad_x, None, None, None
 

@@ -40,11 +40,26 @@ def supported(x, weights, bias=None):
     return K % 64 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
 
 
-# Where the fused forward measured ahead of unpack + hipBLASLt on MI355X: weights of at most
-# this many elements (Qwen2.5-1.5B's q|k|v, 3.1 M, and o, 2.4 M; not gate|up, 27.5 M, or down,
-# 13.8 M) and at most one 128 x 128 tile per compute unit (M <= 2048 at those shapes; with a
-# second round of tiles it fell 26-34% behind).
-FUSED_MAX_WEIGHT_ELEMS = 4 << 20
+# Where the fused kernels measured ahead of unpack + hipBLASLt on MI355X (bench.py --nf4-gemm,
+# Qwen2.5-1.5B's projections at 16 to 2048 rows): where their grid fills between half and one
+# wave of the compute units and the contraction is short.  With fewer tiles a workgroup walks
+# its whole contraction alone (q|k|v forward at 16 rows: 21.6 against 14.1 us); with a second
+# wave of tiles, or a long contraction (down's forward over 8960 columns, gate|up's input
+# gradient over 17920 rows), this build's MFMA core is behind hipBLASLt's.  Inside the window:
+# gate|up forward at 16 / 64 rows 23.3 / 23.8 against 57.2 / 38.1 us; q|k|v and o forward at
+# 2048 rows 27.1 / 25.3 against 28.0 / 25.6 us; q|k|v and o input gradient at 1024 rows
+# 30.4 / 19.9 against 32.7 / 25.3 us; down's input gradient at 16 / 64 rows 19.2 / 19.6
+# against 24.8 / 26.6 us.
+FUSED_MAX_CONTRACTION = 2048
+FWD_TILE = (128, 128)    # rows of x, rows of W per workgroup of soupk_gemm_tn_nf4
+GRAD_TILE = (128, 64)    # rows of dy, columns of W per workgroup of soupk_gemm_nn_nf4
+
+
+def fused_fits(rows, out_cols, contraction, tile, cus):
+    """The fused kernels' window: a grid of half to one wave of the `cus` compute units and a
+    contraction of at most FUSED_MAX_CONTRACTION."""
+    tiles = -(-rows // tile[0]) * -(-out_cols // tile[1])
+    return contraction <= FUSED_MAX_CONTRACTION and cus // 2 <= tiles <= cus
 
 
 def _cu_count(device):
@@ -59,12 +74,18 @@ _cu_count.cache = {}
 
 
 def prefer_fused(x, weights):
-    """True where the fused NF4 forward is the faster path (FUSED_MAX_WEIGHT_ELEMS, one wave of
-    tiles)."""
+    """True where the fused NF4 forward y = x W^T is the faster path (fused_fits)."""
     M, K = x.shape
     N = sum(_nf4.weight_shape(w)[0] for w in weights)
-    tiles = -(-M // 128) * (N // 128)
-    return N * K <= FUSED_MAX_WEIGHT_ELEMS and tiles <= _cu_count(x.device)
+    return fused_fits(M, N, K, FWD_TILE, _cu_count(x.device))
+
+
+def prefer_fused_grad_input(dy, weights):
+    """True where the fused NF4 input gradient dx = dy W is the faster path (fused_fits: dx has
+    W's columns, the contraction runs over W's rows)."""
+    M, N = dy.shape
+    K = _nf4.weight_shape(weights[0])[1]
+    return fused_fits(M, K, N, GRAD_TILE, _cu_count(dy.device))
 
 
 def gemm_tn(x, w16, bias=None):
