@@ -791,7 +791,8 @@ def time_nf4_gemm(dev, calls=40):
     (nf4.unpack_concat) and unpack + hipBLASLt; and the input gradient dx = dy W fused
     (nf4_gemm.nf4_grad_input), on hipBLASLt and unpack + hipBLASLt; then the fused forward and
     input gradient against unpack + hipBLASLt at the smaller row counts SWEEP_ROWS
-    (`rows_sweep`).  Each variant: 5 untimed calls, then `calls`
+    (`rows_sweep`; the forward there also with its contraction split as
+    nf4_gemm.split_count picks, `splits` of them).  Each variant: 5 untimed calls, then `calls`
     calls queued behind a DeviceHold and timed as one span (torch events), so host overhead is
     not in the figure.  Synthetic NF4 weights (workloads.nf4_weight), x ~ N(0, 1)."""
     from testt_amd import nf4, nf4_gemm
@@ -828,14 +829,14 @@ def time_nf4_gemm(dev, calls=40):
         out[name] = {
             "N": sum(rows), "K": K, "M": M,
             "fused_fp16_w_us": span_us(lambda: nf4_gemm.gemm_tn(x, w16)),
-            "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(x, ws)),
+            "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(x, ws, splits=1)),
             "hipblaslt_fp16_w_us": span_us(lambda: torch.matmul(x, w16.t())),
             "unpack_us": span_us(lambda: nf4.unpack_concat(ws, dev)),
             "unpack_then_hipblaslt_us": span_us(
                 lambda: torch.matmul(x, nf4.unpack_concat(ws, dev).t())),
             # the input gradient dx = dy W: fused (W dequantised in the GEMM) against
             # hipBLASLt on the fp16 weight and unpack + hipBLASLt
-            "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dy, ws)),
+            "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dy, ws, splits=1)),
             "bwd_hipblaslt_fp16_w_us": span_us(lambda: torch.matmul(dy, w16)),
             "bwd_unpack_then_hipblaslt_us": span_us(
                 lambda: torch.matmul(dy, nf4.unpack_concat(ws, dev))),
@@ -843,13 +844,22 @@ def time_nf4_gemm(dev, calls=40):
         # smaller row counts (decode- and eval-sized batches): the fused forward and input
         # gradient against unpack + hipBLASLt
         sweep = {}
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
         for m in SWEEP_ROWS:
             xm, dym = x[:m].contiguous(), dy[:m].contiguous()
+            splits = nf4_gemm.split_count(m, sum(rows), K, cus)
+            bwd_splits = nf4_gemm.split_count(m, K, sum(rows), cus, nf4_gemm.GRAD_TILE)
             sweep[m] = {
-                "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(xm, ws)),
+                "splits": splits,
+                "bwd_splits": bwd_splits,
+                "fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_linear(xm, ws, splits=1)),
+                "fused_split_nf4_w_us": span_us(
+                    lambda: nf4_gemm.nf4_linear(xm, ws, splits=splits)),
                 "unpack_then_hipblaslt_us": span_us(
                     lambda: torch.matmul(xm, nf4.unpack_concat(ws, dev).t())),
-                "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dym, ws)),
+                "bwd_fused_nf4_w_us": span_us(lambda: nf4_gemm.nf4_grad_input(dym, ws, splits=1)),
+                "bwd_fused_split_nf4_w_us": span_us(
+                    lambda: nf4_gemm.nf4_grad_input(dym, ws, splits=bwd_splits)),
                 "bwd_unpack_then_hipblaslt_us": span_us(
                     lambda: torch.matmul(dym, nf4.unpack_concat(ws, dev))),
             }
@@ -1198,15 +1208,19 @@ def summarize_trace(trace_csv, title, command):
 NF4_GEMM_VARIANTS = ("fused_fp16_w_us", "fused_nf4_w_us", "hipblaslt_fp16_w_us", "unpack_us",
                      "unpack_then_hipblaslt_us", "bwd_fused_nf4_w_us", "bwd_hipblaslt_fp16_w_us",
                      "bwd_unpack_then_hipblaslt_us")
-NF4_GEMM_SWEEP_VARIANTS = ("fused_nf4_w_us", "unpack_then_hipblaslt_us", "bwd_fused_nf4_w_us",
+NF4_GEMM_SWEEP_VARIANTS = ("fused_nf4_w_us", "fused_split_nf4_w_us", "unpack_then_hipblaslt_us",
+                           "bwd_fused_nf4_w_us", "bwd_fused_split_nf4_w_us",
                            "bwd_unpack_then_hipblaslt_us")
+# sweep variant -> the key of its split count
+_SPLIT_KEY = {"fused_split_nf4_w_us": "splits", "bwd_fused_split_nf4_w_us": "bwd_splits"}
 
 
 def nf4_gemm_spans(trace_csv, bench, calls=40):
     """Mean kernel time per call of each timed group of a `bench.py --nf4-gemm` kernel trace.
     Every group is `calls` calls queued behind one device-side wait, so the dispatches between
     two waits are one group's timed calls followed by the next group's untimed ones; a call is
-    one kernel, or two for the unpack + hipBLASLt groups (their means are added).  Returns
+    one kernel, or two for the unpack + hipBLASLt groups and the split kernels with more than
+    one split (their means are added).  Returns
     {(shape, rows, variant): (kernel names, microseconds)} in the order time_nf4_gemm runs them."""
     spans, cur = [], None
     for r in sorted(_read_csv(trace_csv), key=lambda r: int(r["Dispatch_Id"])):
@@ -1216,16 +1230,17 @@ def nf4_gemm_spans(trace_csv, bench, calls=40):
             spans.append(cur)
         elif cur is not None:
             cur.append(r)
-    order = []
+    order = []   # (key, kernels per call)
+    two = lambda k: 2 if k.endswith("unpack_then_hipblaslt_us") else 1
     for shape, v in bench.items():
-        order += [(shape, v["M"], k) for k in NF4_GEMM_VARIANTS]
-        for m in v.get("rows_sweep", {}):
-            order += [(shape, int(m), k) for k in NF4_GEMM_SWEEP_VARIANTS]
+        order += [((shape, v["M"], k), two(k)) for k in NF4_GEMM_VARIANTS]
+        for m, sv in v.get("rows_sweep", {}).items():
+            order += [((shape, int(m), k), 2 if sv.get(_SPLIT_KEY.get(k), 1) > 1 else two(k))
+                      for k in NF4_GEMM_SWEEP_VARIANTS]
     if len(spans) != len(order):
         raise ValueError(f"{len(spans)} timed spans in the trace, {len(order)} groups expected")
     out = {}
-    for key, rs in zip(order, spans):
-        per_call = 2 if key[2].endswith("unpack_then_hipblaslt_us") else 1
+    for (key, per_call), rs in zip(order, spans):
         timed = rs[:calls * per_call]
         by = {}
         for r in timed:
@@ -1261,6 +1276,7 @@ def summarize_nf4_gemm(trace_csv, bench_json, command):
            "unpack + hipBLASLt | fused dx, NF4 W | hipBLASLt dx, fp16 W | unpack + hipBLASLt dx |",
            "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
     b = lambda x, y: (f"**{x:.2f}**", f"{y:.2f}") if x <= y else (f"{x:.2f}", f"**{y:.2f}**")
+    bold = lambda *xs: [f"**{x:.2f}**" if x == min(xs) else f"{x:.2f}" for x in xs]
     for shape, v in bench.items():
         m = v["M"]
         f, u = b(t(shape, m, "fused_nf4_w_us"), t(shape, m, "unpack_then_hipblaslt_us"))
@@ -1270,28 +1286,43 @@ def summarize_nf4_gemm(trace_csv, bench_json, command):
                    f"{u} | {fd} | {t(shape, m, 'bwd_hipblaslt_fp16_w_us'):.2f} | {ud} |")
     out += ["", "Smaller row counts (decode- and eval-sized batches), microseconds; `*`: the path "
             "FrozenNF4Linear takes (testt_amd/nf4_gemm.py prefer_fused, "
-            "prefer_fused_grad_input):", "",
-            "| shape | rows | fused | unpack + hipBLASLt | fused dx | unpack + hipBLASLt dx |",
-            "|---|---:|---:|---:|---:|---:|"]
+            "prefer_fused_grad_input); fused, K split: soupk_gemm_tn_nf4_split with the split "
+            "count nf4_gemm.split_count picks (in parentheses; 1: the unsplit kernel), its "
+            "figure the sum of its two kernels' means:", "",
+            "| shape | rows | fused | fused, K split (splits) | unpack + hipBLASLt | fused dx | "
+            "fused dx, split (splits) | unpack + hipBLASLt dx |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|"]
     from testt_amd import nf4_gemm
     cus = 256
     dims = {"qkv": (2048, 1536), "o": (1536, 1536), "gate_up": (17920, 1536),
             "down": (1536, 8960)}
     for shape, v in bench.items():
         n, k = dims.get(shape, (v["N"], v["K"]))
-        for m in sorted(int(x) for x in v.get("rows_sweep", {})):
-            f, u = b(t(shape, m, "fused_nf4_w_us"), t(shape, m, "unpack_then_hipblaslt_us"))
-            fd, ud = b(t(shape, m, "bwd_fused_nf4_w_us"),
-                       t(shape, m, "bwd_unpack_then_hipblaslt_us"))
-            if nf4_gemm.fused_fits(m, n, k, nf4_gemm.FWD_TILE, cus):
-                f += " *"
-            else:
+        sweep = {int(a): c for a, c in v.get("rows_sweep", {}).items()}
+        for m in sorted(sweep):
+            f, fs, u = bold(t(shape, m, "fused_nf4_w_us"), t(shape, m, "fused_split_nf4_w_us"),
+                            t(shape, m, "unpack_then_hipblaslt_us"))
+            fs += f" ({sweep[m].get('splits', 1)})"
+            fd, fds, ud = bold(t(shape, m, "bwd_fused_nf4_w_us"),
+                               t(shape, m, "bwd_fused_split_nf4_w_us"),
+                               t(shape, m, "bwd_unpack_then_hipblaslt_us"))
+            fds += f" ({sweep[m].get('bwd_splits', 1)})"
+            if not nf4_gemm.fused_fits(m, n, k, nf4_gemm.FWD_TILE, cus,
+                                       nf4_gemm.forward_split_tiles(k, cus)):
                 u += " *"
-            if nf4_gemm.fused_fits(m, k, n, nf4_gemm.GRAD_TILE, cus):
-                fd += " *"
+            elif sweep[m].get("splits", 1) > 1:
+                fs += " *"
             else:
+                f += " *"
+            if not nf4_gemm.fused_fits(m, k, n, nf4_gemm.GRAD_TILE, cus,
+                                       nf4_gemm.grad_split_tiles(n, cus)):
                 ud += " *"
-            out.append(f"| {label.get(shape, shape)} | {m} | {f} | {u} | {fd} | {ud} |")
+            elif sweep[m].get("bwd_splits", 1) > 1:
+                fds += " *"
+            else:
+                fd += " *"
+            out.append(f"| {label.get(shape, shape)} | {m} | {f} | {fs} | {u} | {fd} | {fds} | "
+                       f"{ud} |")
     return "\n".join(out) + "\n"
 
 

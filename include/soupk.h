@@ -26,7 +26,8 @@ extern "C" {
 #endif
 
 /* ABI version of this header; soupk_abi_version() returns the library's.  4 adds
-   soupk_lora_rope_fwd, soupk_gemm_nn_nf4 and soupk_init_device to version 3's entry points. */
+   soupk_lora_rope_fwd, soupk_gemm_nn_nf4, soupk_gemm_tn_nf4_split, soupk_gemm_nn_nf4_split
+   and soupk_init_device to version 3's entry points. */
 #define SOUPK_ABI_VERSION 4
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
@@ -442,6 +443,24 @@ int soupk_gemm_tn_nf4(const uint16_t* x, int64_t ldx, int32_t n_parts,
                       void* stream);
 
 /*
+ * soupk_gemm_tn_nf4 with the contraction split (widening, for grids of few tiles: few rows of x
+ * against a small W, or a long K): the K tiles are cut into `splits` (1..32, at most K/64)
+ * consecutive ranges, each workgroup writes the fp32 product of its range into `workspace`
+ * ([used splits, M, N] floats, used = ceil(K/64 / ceil(K/64 / splits)) <= splits), and a second
+ * launch writes y = fp16(((p[0] + p[1]) + ...) + bias) in split order (deterministic; one
+ * rounding, as the unsplit kernel, with another order of the fp32 sums).  workspace: 16-byte
+ * aligned, at least used * M * N floats; y 16-byte aligned; bias (optional) 8-byte aligned.
+ */
+int soupk_gemm_tn_nf4_split(const uint16_t* x, int64_t ldx, int32_t n_parts,
+                            const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+                            const float* const* code2, const float* const* absmax2,
+                            const float* const* offset, const float* const* nf4,
+                            const int32_t* part_rows, int32_t qblock, int32_t qblock2,
+                            const uint16_t* bias, uint16_t* y, int64_t M, int32_t N, int32_t K,
+                            int32_t splits, float* workspace, int64_t workspace_floats,
+                            void* stream);
+
+/*
  * Its input gradient (the backward of the same projection): dx = dy W, dy [M, K] fp16 (row
  * pitch lddy), W [K, N] the NF4 row stack (n_parts parts of part_rows[i] rows, K in all, each a
  * multiple of 128; N, W's columns, a multiple of 128; K a multiple of 64) dequantised as it is
@@ -456,6 +475,22 @@ int soupk_gemm_nn_nf4(const uint16_t* dy, int64_t lddy, int32_t n_parts,
                       const float* const* offset, const float* const* nf4,
                       const int32_t* part_rows, int32_t qblock, int32_t qblock2, uint16_t* dx,
                       int64_t M, int32_t N, int32_t K, void* stream);
+
+/*
+ * soupk_gemm_nn_nf4 with the contraction (W's rows) split, as soupk_gemm_tn_nf4_split: each
+ * workgroup writes the fp32 product of its range of 64-row steps into `workspace`
+ * ([used splits, M, N] floats), and a second launch writes dx = fp16((p[0] + p[1]) + ...) in
+ * split order.  splits 1..32, at most K/64; workspace 16-byte aligned, at least used * M * N
+ * floats (used = ceil(K/64 / ceil(K/64 / splits))).  No counterpart in the reference beyond its
+ * stated next step (README.md:190-192); the widening for batches of few rows.
+ */
+int soupk_gemm_nn_nf4_split(const uint16_t* dy, int64_t lddy, int32_t n_parts,
+                            const uint8_t* const* packed, const uint8_t* const* absmax_u8,
+                            const float* const* code2, const float* const* absmax2,
+                            const float* const* offset, const float* const* nf4,
+                            const int32_t* part_rows, int32_t qblock, int32_t qblock2,
+                            uint16_t* dx, int64_t M, int32_t N, int32_t K, int32_t splits,
+                            float* workspace, int64_t workspace_floats, void* stream);
 
 #ifdef __cplusplus
 }

@@ -125,6 +125,59 @@ def test_empty_work_is_a_no_op(lib, name, args):
     _ext.call(name, *args)
 
 
+def _split_args(M=16, N=256, K=256, splits=2, ws=None, bias=None):
+    """soupk_gemm_tn_nf4_split arguments for one NF4 part of N rows: host arrays of fake,
+    16-byte aligned device addresses (the checks below reject before any launch)."""
+    one = lambda: (ctypes.c_void_p * 1)(4096)
+    keep = [one() for _ in range(6)] + [(ctypes.c_int32 * 1)(N)]
+    ws = 2 * M * N if ws is None else ws
+    args = (4096, K, 1, *[ctypes.addressof(a) for a in keep], 64, 256, bias, 8192, M, N, K,
+            splits, 16384, ws, None)
+    return keep, args
+
+
+@pytest.mark.parametrize("kw", [
+    dict(splits=0), dict(splits=33, K=64 * 40, ws=1 << 30), dict(splits=5),   # 4 K tiles
+    dict(splits=2, ws=2 * 16 * 256 - 1), dict(bias=4100),
+])
+def test_split_gemm_rejects_bad_splits_workspace_and_bias(lib, kw):
+    keep, args = _split_args(**kw)
+    with pytest.raises(_ext.SoupkError, match="status 1"):
+        _ext.call("soupk_gemm_tn_nf4_split", *args)
+
+
+def test_split_gemm_workspace_counts_used_splits(lib):
+    """K = 320 (5 tiles) cut 4 ways runs 2 tiles per split, so 3 splits are used and the
+    workspace needs 3 * M * N floats: 3 M N - 1 is rejected; with M = 0 nothing runs."""
+    keep, args = _split_args(K=320, splits=4, ws=3 * 16 * 256 - 1)
+    with pytest.raises(_ext.SoupkError, match="status 1"):
+        _ext.call("soupk_gemm_tn_nf4_split", *args)
+    keep, args = _split_args(M=0, K=320, splits=4, ws=0)
+    _ext.call("soupk_gemm_tn_nf4_split", *args)
+
+
+def _nn_split_args(M=16, N=128, K=256, splits=2, ws=None):
+    """soupk_gemm_nn_nf4_split arguments for one NF4 part of K rows and N columns (fake device
+    addresses, as _split_args)."""
+    one = lambda: (ctypes.c_void_p * 1)(4096)
+    keep = [one() for _ in range(6)] + [(ctypes.c_int32 * 1)(K)]
+    ws = 2 * M * N if ws is None else ws
+    args = (4096, K, 1, *[ctypes.addressof(a) for a in keep], 64, 256, 8192, M, N, K, splits,
+            16384, ws, None)
+    return keep, args
+
+
+@pytest.mark.parametrize("kw", [
+    dict(splits=0), dict(splits=33, K=64 * 40, ws=1 << 30), dict(splits=5),   # 4 steps
+    dict(splits=2, ws=2 * 16 * 128 - 1), dict(N=96)])
+def test_nn_split_gemm_rejects_bad_splits_and_workspace(lib, kw):
+    keep, args = _nn_split_args(**kw)
+    with pytest.raises(_ext.SoupkError, match="status 1"):
+        _ext.call("soupk_gemm_nn_nf4_split", *args)
+    keep, args = _nn_split_args(M=0, K=384, splits=4, ws=0)   # 3 of 4 splits used; no rows
+    _ext.call("soupk_gemm_nn_nf4_split", *args)
+
+
 def test_noalloc_rejects_problems_beyond_its_scratch(lib):
     """soupk_lora_bwd_params_noalloc returns SOUPK_STATUS_SCRATCH_LIMIT, before any HIP call,
     for a problem whose partial sums exceed its static scratch (6785 rows at the Qwen2.5-1.5B

@@ -50,11 +50,39 @@ def test_gemm_tn_nf4(rows, K, M):
     g = torch.Generator().manual_seed(M + K)
     x = torch.randn(M, K, generator=g).to(torch.float16).to(DEV)
     b = (0.1 * torch.randn(sum(rows), generator=g)).to(torch.float16).to(DEV)
-    y = nf4_gemm.nf4_linear(x, ws, b)
+    y = nf4_gemm.nf4_linear(x, ws, b, splits=1)
     w16 = nf4.unpack_concat(ws, DEV)
     assert torch.equal(y, nf4_gemm.gemm_tn(x, w16, b))        # same values, same sums
     wd = torch.from_numpy(np.concatenate([dequant_state(w) for w in ws]).astype(np.float64)).to(DEV)
     within(y, x.double() @ wd.t() + b.double(), x.double().abs() @ wd.abs().t() + b.double().abs())
+
+
+@pytest.mark.parametrize("rows,K,M,splits", [
+    ((256,), 1536, 16, 8), ((256, 128, 128), 320, 77, 4),   # 5 K tiles in 4 ways: 3 splits used
+    ((128,), 8960, 16, 32), ((1536, 256, 256), 1536, 2048, 2), ((128,), 256, 3, 4),
+    ((256,), 1536, 1, None)])                                # the split count split_count picks
+def test_gemm_tn_nf4_split(rows, K, M, splits):
+    """The contraction split: fp32 partials added in split order, bias added, one fp16 rounding.
+    Against float64 sums over the oracle's dequantised weights (within 1 ulp plus
+    32 * 2^-24 * sum|terms|, as the unsplit kernel), within twice that of the unsplit kernel
+    (the same rounding of another order of fp32 sums), and the same bits on a second call."""
+    print(f"gemm_tn_nf4_split parts={rows} K={K} M={M} splits={splits}", flush=True)
+    ws = [workloads.nf4_weight(r, K, seed=70 + i, device=DEV, absmax2_range=(0.005, 0.02),
+                               offset=0.01) for i, r in enumerate(rows)]
+    g = torch.Generator().manual_seed(M + K + 7)
+    x = torch.randn(M, K, generator=g).to(torch.float16).to(DEV)
+    b = (0.1 * torch.randn(sum(rows), generator=g)).to(torch.float16).to(DEV)
+    y = nf4_gemm.nf4_linear(x, ws, b, splits=splits)
+    wd = torch.from_numpy(np.concatenate([dequant_state(w) for w in ws]).astype(np.float64)).to(DEV)
+    terms = x.double().abs() @ wd.abs().t() + b.double().abs()
+    within(y, x.double() @ wd.t() + b.double(), terms)
+    one = nf4_gemm.nf4_linear(x, ws, b, splits=1)
+    inf = torch.tensor(float("inf"), dtype=torch.float16, device=DEV)
+    ulp = (torch.nextafter(one.abs(), inf) - one.abs()).double()
+    assert bool(((y.double() - one.double()).abs() <= 2 * ulp + 64 * 2.0 ** -24 * terms).all())
+    assert torch.equal(nf4_gemm.nf4_linear(x, ws, b, splits=splits), y)
+    assert torch.equal(nf4_gemm.nf4_linear(x, ws, None, splits=splits),
+                       nf4_gemm.nf4_linear(x, ws, torch.zeros_like(b), splits=splits))
 
 
 @pytest.mark.parametrize("rows,K,M", [((1536, 256, 256), 1536, 2048), ((1536,), 1536, 2048),
@@ -76,6 +104,29 @@ def test_gemm_nn_nf4_grad_input(rows, K, M):
     wide = torch.zeros(M, sum(rows) + 64, dtype=torch.float16, device=DEV)
     wide[:, :sum(rows)] = dy
     assert torch.equal(nf4_gemm.nf4_grad_input(wide[:, :sum(rows)], ws), dx)
+
+
+@pytest.mark.parametrize("rows,K,M,splits", [
+    ((1536, 256, 256), 1536, 16, 8), ((256, 128, 128), 512, 77, 3),   # 8 steps in 3: 3 used
+    ((8960, 8960), 1536, 16, 10), ((1536,), 1536, 300, 2), ((128,), 128, 1, None)])
+def test_gemm_nn_nf4_split(rows, K, M, splits):
+    """The input gradient with its contraction (W's rows, across the parts) split: against
+    float64 sums over the oracle's dequantised weights (within 1 ulp plus 32 * 2^-24 *
+    sum|terms|), within twice that of the unsplit kernel, and the same bits on a second call."""
+    print(f"gemm_nn_nf4_split parts={rows} K={K} M={M} splits={splits}", flush=True)
+    ws = [workloads.nf4_weight(r, K, seed=110 + i, device=DEV, absmax2_range=(0.005, 0.02),
+                               offset=0.01) for i, r in enumerate(rows)]
+    g = torch.Generator().manual_seed(M + K + 11)
+    dy = (0.1 * torch.randn(M, sum(rows), generator=g)).to(torch.float16).to(DEV)
+    dx = nf4_gemm.nf4_grad_input(dy, ws, splits=splits)
+    wd = torch.from_numpy(np.concatenate([dequant_state(w) for w in ws]).astype(np.float64)).to(DEV)
+    terms = dy.double().abs() @ wd.abs()
+    within(dx, dy.double() @ wd, terms)
+    one = nf4_gemm.nf4_grad_input(dy, ws, splits=1)
+    inf = torch.tensor(float("inf"), dtype=torch.float16, device=DEV)
+    ulp = (torch.nextafter(one.abs(), inf) - one.abs()).double()
+    assert bool(((dx.double() - one.double()).abs() <= 2 * ulp + 64 * 2.0 ** -24 * terms).all())
+    assert torch.equal(nf4_gemm.nf4_grad_input(dy, ws, splits=splits), dx)
 
 
 def test_rejects_shapes():

@@ -1,8 +1,10 @@
 """CPU: the window in which FrozenNF4Linear takes the fused NF4-dequant GEMM
-(testt_amd/nf4_gemm.py fused_fits), checked against every comparison of the fused kernels with
-unpack + hipBLASLt that `bench.py --nf4-gemm` measured on MI355X (256 CUs) at Qwen2.5-1.5B's
-projections: the rule picks the faster path in each, and the two wins it leaves to unpack +
-hipBLASLt (256 rows, 280 tiles, just past one wave) are listed as such."""
+(testt_amd/nf4_gemm.py fused_fits, forward_split_tiles, grad_split_tiles) and the split count
+of the kernels that cut the contraction (split_count), checked against what `bench.py
+--nf4-gemm` measured on MI355X (256 CUs, kernel trace of 40 queued calls) at Qwen2.5-1.5B's
+projections, 16 to 2048 rows: the rule takes the faster path wherever the two differ by more
+than 4%; the two wins it leaves to unpack + hipBLASLt (256 rows, 280 tiles, just past one wave)
+are listed as such."""
 
 import pytest
 
@@ -10,30 +12,54 @@ from testt_amd import nf4_gemm
 
 CUS = 256
 QKV, O, GU, DOWN = (2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)   # (W rows, cols)
+LEVEL = 0.04
 
-# (projection, rows, fused faster?) from the sweep: forward y = x W^T
-FWD = [(QKV, 16, False), (QKV, 64, False), (QKV, 256, False), (QKV, 512, False),
-       (QKV, 1024, True), (QKV, 2048, True),
-       (O, 16, False), (O, 512, False), (O, 2048, True),
-       (GU, 16, True), (GU, 64, True), (GU, 512, False), (GU, 1024, False), (GU, 2048, False),
-       (DOWN, 16, False), (DOWN, 1024, False), (DOWN, 2048, False)]
+# (projection, rows, fused us (split as split_count picks), unpack + hipBLASLt us)
+FWD = [(QKV, 16, 9.64, 14.18), (QKV, 64, 11.66, 14.88), (QKV, 256, 15.99, 17.53),
+       (QKV, 512, 18.98, 18.63), (QKV, 1024, 24.54, 25.06), (QKV, 2048, 27.33, 27.94),
+       (O, 16, 9.36, 13.65), (O, 64, 10.91, 14.19), (O, 256, 14.82, 14.39),
+       (O, 512, 17.87, 17.10), (O, 1024, 24.50, 22.94), (O, 2048, 25.40, 25.35),
+       (GU, 16, 23.41, 57.03), (GU, 64, 23.96, 37.88), (GU, 512, 63.01, 53.71),
+       (GU, 1024, 113.09, 92.02), (GU, 2048, 212.75, 142.05),
+       (DOWN, 16, 14.40, 38.22), (DOWN, 64, 17.21, 40.54), (DOWN, 256, 23.60, 42.36),
+       (DOWN, 512, 36.25, 53.30), (DOWN, 1024, 60.74, 59.07), (DOWN, 2048, 133.31, 88.34)]
 # input gradient dx = dy W
-GRAD = [(QKV, 16, False), (QKV, 512, False), (QKV, 1024, True), (QKV, 2048, False),
-        (O, 64, False), (O, 512, False), (O, 1024, True), (O, 2048, False),
-        (GU, 64, False), (GU, 512, False), (GU, 2048, False),
-        (DOWN, 16, True), (DOWN, 64, True), (DOWN, 512, False), (DOWN, 2048, False)]
+GRAD = [(QKV, 16, 11.08, 17.28), (QKV, 64, 12.89, 21.04), (QKV, 256, 17.47, 20.84),
+        (QKV, 512, 22.80, 22.04), (QKV, 1024, 30.55, 32.77), (QKV, 2048, 41.12, 34.19),
+        (O, 16, 10.08, 14.71), (O, 64, 11.02, 17.87), (O, 256, 14.52, 17.30),
+        (O, 512, 18.26, 18.43), (O, 1024, 19.88, 25.25), (O, 2048, 28.83, 28.20),
+        (GU, 16, 24.90, 74.97), (GU, 64, 26.10, 99.61), (GU, 256, 43.21, 131.81),
+        (GU, 512, 77.15, 161.93), (GU, 1024, 150.66, 219.97), (GU, 2048, 306.10, 187.19),
+        (DOWN, 16, 18.92, 24.73), (DOWN, 64, 19.31, 26.58), (DOWN, 512, 45.12, 41.54),
+        (DOWN, 1024, 77.37, 46.34), (DOWN, 2048, 139.20, 83.91)]
 
 
-@pytest.mark.parametrize("w,rows,faster", FWD)
-def test_forward_window_matches_measurements(w, rows, faster):
+def fwd_fused(rows, w):
     n, k = w
-    assert nf4_gemm.fused_fits(rows, n, k, nf4_gemm.FWD_TILE, CUS) == faster
+    return nf4_gemm.fused_fits(rows, n, k, nf4_gemm.FWD_TILE, CUS,
+                               nf4_gemm.forward_split_tiles(k, CUS))
 
 
-@pytest.mark.parametrize("w,rows,faster", GRAD)
-def test_grad_input_window_matches_measurements(w, rows, faster):
+def grad_fused(rows, w):
     n, k = w
-    assert nf4_gemm.fused_fits(rows, k, n, nf4_gemm.GRAD_TILE, CUS) == faster
+    return nf4_gemm.fused_fits(rows, k, n, nf4_gemm.GRAD_TILE, CUS,
+                               nf4_gemm.grad_split_tiles(n, CUS))
+
+
+def check(takes_fused, fused_us, unpack_us):
+    if abs(fused_us - unpack_us) <= LEVEL * min(fused_us, unpack_us):
+        return                                   # level: either path
+    assert takes_fused == (fused_us < unpack_us)
+
+
+@pytest.mark.parametrize("w,rows,fused_us,unpack_us", FWD)
+def test_forward_window_matches_measurements(w, rows, fused_us, unpack_us):
+    check(fwd_fused(rows, w), fused_us, unpack_us)
+
+
+@pytest.mark.parametrize("w,rows,fused_us,unpack_us", GRAD)
+def test_grad_input_window_matches_measurements(w, rows, fused_us, unpack_us):
+    check(grad_fused(rows, w), fused_us, unpack_us)
 
 
 def test_window_edges():
@@ -44,13 +70,47 @@ def test_window_edges():
     assert not nf4_gemm.fused_fits(256, 129 * 128, 64, (128, 128), 256)
     assert not nf4_gemm.fused_fits(256, 128 * 128, nf4_gemm.FUSED_MAX_CONTRACTION + 64,
                                    (128, 128), 256)
+    # below half a wave only where the split kernels take it
+    assert not nf4_gemm.fused_fits(128, 32 * 128, 64, (128, 128), 256)
+    assert nf4_gemm.fused_fits(128, 32 * 128, 64, (128, 128), 256, split_tiles=32)
+    assert not nf4_gemm.fused_fits(128, 33 * 128, 64, (128, 128), 256, split_tiles=32)
 
 
 def test_wins_left_outside_the_window():
-    """gate|up forward at 256 rows (fused 39.4 against 49.1 us) and down's input gradient at 256
-    rows (27.7 against 35.7 us) fall just past one wave (280 tiles); the rule leaves them to
+    """gate|up forward at 256 rows (fused 40.0 against 48.7 us) and down's input gradient at 256
+    rows (27.8 against 35.7 us) fall just past one wave (280 tiles); the rule leaves them to
     unpack + hipBLASLt rather than widen the window past q|k|v at 2560 rows (320 tiles, fused
     26-34% behind)."""
-    assert not nf4_gemm.fused_fits(256, GU[0], GU[1], nf4_gemm.FWD_TILE, CUS)
-    assert not nf4_gemm.fused_fits(256, DOWN[1], DOWN[0], nf4_gemm.GRAD_TILE, CUS)
-    assert not nf4_gemm.fused_fits(2560, QKV[0], QKV[1], nf4_gemm.FWD_TILE, CUS)
+    assert not fwd_fused(256, GU)
+    assert not grad_fused(256, DOWN)
+    assert not fwd_fused(2560, QKV)
+
+
+# (projection, rows, split count split_count picks: the best of the sweep or within 4% of it)
+@pytest.mark.parametrize("w,rows,splits", [
+    (QKV, 16, 12), (QKV, 64, 8), (QKV, 128, 6), (QKV, 256, 4), (QKV, 512, 3), (QKV, 1024, 1),
+    (O, 16, 12), (O, 64, 12), (O, 256, 6), (O, 512, 4), (DOWN, 16, 20), (DOWN, 64, 20),
+    (DOWN, 128, 20), (DOWN, 256, 10), (DOWN, 512, 5), (GU, 16, 1)])
+def test_forward_split_count(w, rows, splits):
+    """Splits of the forward's contraction (q|k|v at 16 rows: 7.9 us with 12 splits, 21.8 with
+    none; down at 16 rows: 13.3 with 20, 109.0 with none)."""
+    n, k = w
+    assert nf4_gemm.split_count(rows, n, k, CUS) == splits
+
+
+@pytest.mark.parametrize("w,rows,splits", [
+    (QKV, 16, 16), (QKV, 64, 8), (QKV, 512, 4), (QKV, 1024, 1), (O, 16, 8), (O, 64, 8),
+    (O, 512, 2), (GU, 256, 10), (GU, 1024, 8), (DOWN, 16, 1)])
+def test_grad_split_count(w, rows, splits):
+    """Splits of the input gradient's contraction over W's rows (gate|up at 1024 rows: 152 us
+    with 8 splits, 220 with none, though its 192 tiles fill most of a wave)."""
+    n, k = w
+    assert nf4_gemm.split_count(rows, k, n, CUS, nf4_gemm.GRAD_TILE) == splits
+
+
+def test_split_count_small_contraction():
+    assert nf4_gemm.split_count(16, 128, 64, CUS) == 1       # one K tile: nothing to split
+    # four K tiles: two splits would save two steps (1.4 us) for a summing launch (2.5 us)
+    assert nf4_gemm.split_count(16, 128, 256, CUS) == 1
+    assert nf4_gemm.split_count(16, 128, 64 * 2000, CUS) <= nf4_gemm.MAX_SPLITS
+    assert nf4_gemm.split_count(16, 128 * 200, 1536, CUS) == 1   # 200 tiles, a short contraction

@@ -72,6 +72,10 @@ SIGNATURES = {
                           _i32, _i32, _p],
     "soupk_gemm_tn_nf4": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p, _i64,
                           _i32, _i32, _p],
+    "soupk_gemm_tn_nf4_split": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _p,
+                                _i64, _i32, _i32, _i32, _p, _i64, _p],
+    "soupk_gemm_nn_nf4_split": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64,
+                                _i32, _i32, _i32, _p, _i64, _p],
 }
 
 

@@ -112,7 +112,8 @@ __attribute__((amdgpu_waves_per_eu(SOUPK_GEMM_WPE, SOUPK_GEMM_WPE)))
 #endif
 void gemm_tn_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* w16, Nf4Weights nw,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    float* __restrict__ partial, int split_tiles) {
   constexpr int BM = S::BM, BN = S::BN, T = S::kThreads, kBK = S::BK, kLds = S::kLds;
   constexpr int CPR = S::CPR, IPR = S::IPR;
   // Two LDS stages as separate arrays, so that the compiler sees the staging of one and the
@@ -148,9 +149,12 @@ void gemm_tn_kernel(
     offset = P.offset[0];
   }
 
-  const int KT = K / kBK;
+  // Split of the contraction (partial != null): workgroup row blockIdx.y takes K tiles
+  // kt_base .. kt_base + split_tiles - 1 and writes an fp32 partial of its output tile.
+  const int kt_base = static_cast<int>(blockIdx.y) * split_tiles;
+  const int KT = min(split_tiles, K / kBK - kt_base);
   auto load = [&](TileRegs<S>& r, int kt) {
-    const int k0 = kt * kBK;
+    const int k0 = (kt_base + kt) * kBK;
 #pragma unroll
     for (int j = 0; j < S::XC; ++j) {
       const int c = tid + T * j, row = c / CPR, ch = c % CPR;
@@ -283,6 +287,22 @@ void gemm_tn_kernel(
 
   // epilogue: element e of acc[i][j] is row TM wm + 32i + 8(e/4) + 4(lane/32) + e%4,
   // column TN wn + 32j + lane%32
+  if (partial != nullptr) {   // the split's fp32 partial, no bias
+    float* pz = partial + static_cast<int64_t>(blockIdx.y) * M * N;
+#pragma unroll
+    for (int j = 0; j < S::FN; ++j) {
+      const int n = n0 + S::TN * wn + 32 * j + lane % 32;
+#pragma unroll
+      for (int i = 0; i < S::FM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + S::TM * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+          if (m < M) pz[static_cast<int64_t>(m) * N + n] = acc[i][j][e];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < S::FN; ++j) {
     const int n = n0 + S::TN * wn + 32 * j + lane % 32;
@@ -329,7 +349,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 template <class S>
 __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
     const uint16_t* __restrict__ dy, int64_t lddy, Nf4Weights nw, uint16_t* __restrict__ dx,
-    int M, int N /* W columns: dx columns */, int K /* W rows: the contraction */) {
+    int M, int N /* W columns: dx columns */, int K /* W rows: the contraction */,
+    float* __restrict__ partial, int split_tiles) {
   constexpr int BM = S::BM, BN = S::BN, T = S::kThreads, kBK = 64, kLds = kBK + 8;
   constexpr int kLdw = BN + 8;                   // W tile row stride (halves)
   constexpr int CPR = kBK / 8;
@@ -354,7 +375,10 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
       pair_s[p][i] = float2{nw.part[p].nf4[i >> 4], nw.part[p].nf4[i & 15]};
     }
 
-  const int KT = K / kBK;
+  // Split of the contraction (partial != null): workgroup row blockIdx.y takes contraction
+  // steps kt_base .. kt_base + split_tiles - 1 and writes an fp32 partial of its output tile.
+  const int kt_base = static_cast<int>(blockIdx.y) * split_tiles;
+  const int KT = min(split_tiles, K / kBK - kt_base);
   // the part holding W rows k0 .. k0 + 63, and the row of that part (wave-uniform)
   auto part_of = [&](int k0, int& prow) {
     int part = 0;
@@ -366,7 +390,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
     return part;
   };
   auto load = [&](TileRegsNN<S>& r, int kt) {
-    const int k0 = kt * kBK;
+    const int k0 = (kt_base + kt) * kBK;
 #pragma unroll
     for (int j = 0; j < S::XC; ++j) {
       const int c = tid + T * j, row = c / CPR, ch = c % CPR;
@@ -392,7 +416,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
       *reinterpret_cast<u32x4*>(&Xs[row * kLds + 8 * ch]) = r.x[j];
     }
     int prow0;
-    const int part = part_of(kt * kBK, prow0);
+    const int part = part_of((kt_base + kt) * kBK, prow0);
     const float offset = nw.part[part].offset[0];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
@@ -482,6 +506,22 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
     step(kt, ra, rb, Xs0, Ws0, Xs1, Ws1);
     if (kt + 1 < KT) step(kt + 1, rb, ra, Xs1, Ws1, Xs0, Ws0);
   }
+  if (partial != nullptr) {   // the split's fp32 partial
+    float* pz = partial + static_cast<int64_t>(blockIdx.y) * M * N;
+#pragma unroll
+    for (int j = 0; j < S::FN; ++j) {
+      const int n = n0 + S::TN * wn + 32 * j + lane % 32;
+#pragma unroll
+      for (int i = 0; i < S::FM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + S::TM * wm + 32 * i + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+          if (m < M) pz[static_cast<int64_t>(m) * N + n] = acc[i][j][e];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < S::FN; ++j) {
     const int n = n0 + S::TN * wn + 32 * j + lane % 32;
@@ -559,6 +599,48 @@ int nf4_parts(int32_t n_parts, const uint8_t* const* packed, const uint8_t* cons
 }  // namespace
 }  // namespace soupk
 
+namespace soupk {
+namespace {
+
+constexpr int kMaxSplits = 32;
+
+// y = fp16(((p[0] + p[1]) + ...) + bias) over the splits' fp32 partials [splits, M, N], four
+// consecutive outputs per thread (N is a multiple of 64), partials added in split order.  All
+// of a thread's loads are issued before the first add (unrolled to kMaxSplits under a uniform
+// test), so the kernel waits on memory once, not once per split.
+__global__ __launch_bounds__(256) void split_sum_kernel(
+    const f32x4* __restrict__ parts, int splits, int64_t stride4, int64_t n4, int n_cols4,
+    const uint16_t* __restrict__ bias, u32x2* __restrict__ y) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n4) return;
+  f32x4 v[kMaxSplits];
+#pragma unroll
+  for (int p = 0; p < kMaxSplits; ++p)
+    if (p < splits) v[p] = parts[p * stride4 + i];
+  f32x4 s = v[0];
+#pragma unroll
+  for (int p = 1; p < kMaxSplits; ++p)
+    if (p < splits) s = s + v[p];
+  if (bias != nullptr) {
+    const int c = static_cast<int>(i % n_cols4) * 4;
+    const u32x2 bw = *reinterpret_cast<const u32x2*>(bias + c);
+    s = s + f32x4{lo_h(bw.x), hi_h(bw.x), lo_h(bw.y), hi_h(bw.y)};
+  }
+  y[i] = u32x2{pack_h2(s[0], s[1]), pack_h2(s[2], s[3])};
+}
+
+// Contraction steps per split and the splits that leaves non-empty, for `kt` 64-wide steps cut
+// `splits` ways (kInvalid unless 1 <= splits <= min(kMaxSplits, kt)).
+int split_plan(int kt, int32_t splits, int& per, int& used) {
+  if (splits < 1 || splits > kMaxSplits || splits > kt) return kInvalid;
+  per = (kt + splits - 1) / splits;
+  used = (kt + per - 1) / per;
+  return kOk;
+}
+
+}  // namespace
+}  // namespace soupk
+
 using namespace soupk;
 
 extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
@@ -572,7 +654,7 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<Shape, false>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
-                       static_cast<int>(M), N, K);
+                       static_cast<int>(M), N, K, nullptr, K / kBK);
 }
 
 extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
@@ -594,15 +676,43 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
-                       static_cast<int>(M), N, K);
+                       static_cast<int>(M), N, K, nullptr, K / kBK);
 }
 
-extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4(
-    const uint16_t* dy, int64_t lddy, int32_t n_parts, const uint8_t* const* packed,
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4_split(
+    const uint16_t* x, int64_t ldx, int32_t n_parts, const uint8_t* const* packed,
     const uint8_t* const* absmax_u8, const float* const* code2, const float* const* absmax2,
     const float* const* offset, const float* const* nf4, const int32_t* part_rows,
-    int32_t qblock, int32_t qblock2, uint16_t* dx, int64_t M, int32_t N, int32_t K,
-    void* stream) {
+    int32_t qblock, int32_t qblock2, const uint16_t* bias, uint16_t* y, int64_t M, int32_t N,
+    int32_t K, int32_t splits, float* workspace, int64_t workspace_floats, void* stream) {
+  const int rc = check_gemm(M, N, K, ldx);
+  if (rc != kOk) return rc;
+  Nf4Weights nw;
+  const int rp = nf4_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4, part_rows,
+                           qblock, qblock2, N, nw);
+  if (rp != kOk) return rp;
+  for (int i = 0; i < n_parts; ++i)
+    if (part_rows[i] % kBN) return kInvalid;
+  int per, used;
+  if (split_plan(K / kBK, splits, per, used) != kOk) return kInvalid;
+  if (workspace_floats < static_cast<int64_t>(used) * M * N) return kInvalid;
+  if (M == 0) return kOk;
+  if (bad_ptr(x) || bad_ptr(y) || bad_ptr(workspace)) return kInvalid;
+  if (reinterpret_cast<uintptr_t>(bias) & 7) return kInvalid;   // read 4 halves at a time
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)),
+                  static_cast<unsigned>(used));
+  int r = launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads), st, x, ldx,
+                        nullptr, nw, bias, y, static_cast<int>(M), N, K, workspace, per);
+  if (r != kOk) return r;
+  const int64_t n4 = M * static_cast<int64_t>(N) / 4;
+  return launch_kernel(split_sum_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
+                       dim3(256), st, reinterpret_cast<const f32x4*>(workspace), used,
+                       M * static_cast<int64_t>(N) / 4, n4, N / 4, bias,
+                       reinterpret_cast<u32x2*>(y));
+}
+
+namespace {
 // Tile shape of the input gradient (measured at M = 2048 on MI355X: 128 x 64 on 4 wavefronts
 // 40.9 / 28.8 us at the q|k|v / o shapes; 128 x 128 on 8, 44.9 / 32.2 us, fills only 192 of the
 // 256 CUs there; 64 x 128, 54.1 / 39.6 us).
@@ -610,26 +720,71 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4(
 #define SOUPK_GEMM_NN_SHAPE 1
 #endif
 #if SOUPK_GEMM_NN_SHAPE == 0
-  using NS = GemmShape<128, 128, 4, 2>;
+using NS = GemmShape<128, 128, 4, 2>;
 #elif SOUPK_GEMM_NN_SHAPE == 1
-  using NS = GemmShape<128, 64, 2, 2>;
+using NS = GemmShape<128, 64, 2, 2>;
 #elif SOUPK_GEMM_NN_SHAPE == 2
-  using NS = GemmShape<64, 128, 2, 2>;
+using NS = GemmShape<64, 128, 2, 2>;
 #else
-  using NS = GemmShape<128, 64, 4, 2>;
+using NS = GemmShape<128, 64, 4, 2>;
 #endif
-  // N: W's columns (dx's), K: W's rows (the contraction, dy's columns)
+
+// The input gradient's arguments, checked; N: W's columns (dx's), K: W's rows (the
+// contraction, dy's columns).
+int check_nn(const uint16_t* dy, int64_t lddy, int32_t n_parts, const uint8_t* const* packed,
+             const uint8_t* const* absmax_u8, const float* const* code2,
+             const float* const* absmax2, const float* const* offset, const float* const* nf4,
+             const int32_t* part_rows, int32_t qblock, int32_t qblock2, int64_t M, int32_t N,
+             int32_t K, Nf4Weights& nw) {
   if (M < 0 || N <= 0 || K <= 0 || N % NS::BN || K % 64 || lddy < K || lddy % 8) return kInvalid;
   if ((M + NS::BM - 1) / NS::BM * static_cast<int64_t>(N / NS::BN) > 0x7fffffff) return kInvalid;
   if (M * static_cast<int64_t>(N) >= (int64_t{1} << 40)) return kInvalid;
+  return nf4_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4, part_rows, qblock,
+                   qblock2, K, nw);
+}
+}  // namespace
+
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4(
+    const uint16_t* dy, int64_t lddy, int32_t n_parts, const uint8_t* const* packed,
+    const uint8_t* const* absmax_u8, const float* const* code2, const float* const* absmax2,
+    const float* const* offset, const float* const* nf4, const int32_t* part_rows,
+    int32_t qblock, int32_t qblock2, uint16_t* dx, int64_t M, int32_t N, int32_t K,
+    void* stream) {
   Nf4Weights nw;
-  const int rp = nf4_parts(n_parts, packed, absmax_u8, code2, absmax2, offset, nf4, part_rows,
-                           qblock, qblock2, K, nw);
-  if (rp != kOk) return rp;
+  const int rc = check_nn(dy, lddy, n_parts, packed, absmax_u8, code2, absmax2, offset, nf4,
+                          part_rows, qblock, qblock2, M, N, K, nw);
+  if (rc != kOk) return rc;
   if (M == 0) return kOk;
   if (bad_ptr(dy) || bad_ptr(dx)) return kInvalid;
   const dim3 grid(static_cast<unsigned>((N / NS::BN) * ((M + NS::BM - 1) / NS::BM)));
   return launch_kernel(gemm_nn_nf4_kernel<NS>, grid, dim3(NS::kThreads),
                        static_cast<hipStream_t>(stream), dy, lddy, nw, dx, static_cast<int>(M),
-                       N, K);
+                       N, K, nullptr, K / 64);
+}
+
+extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4_split(
+    const uint16_t* dy, int64_t lddy, int32_t n_parts, const uint8_t* const* packed,
+    const uint8_t* const* absmax_u8, const float* const* code2, const float* const* absmax2,
+    const float* const* offset, const float* const* nf4, const int32_t* part_rows,
+    int32_t qblock, int32_t qblock2, uint16_t* dx, int64_t M, int32_t N, int32_t K,
+    int32_t splits, float* workspace, int64_t workspace_floats, void* stream) {
+  Nf4Weights nw;
+  const int rc = check_nn(dy, lddy, n_parts, packed, absmax_u8, code2, absmax2, offset, nf4,
+                          part_rows, qblock, qblock2, M, N, K, nw);
+  if (rc != kOk) return rc;
+  int per, used;
+  if (split_plan(K / 64, splits, per, used) != kOk) return kInvalid;
+  if (workspace_floats < static_cast<int64_t>(used) * M * N) return kInvalid;
+  if (M == 0) return kOk;
+  if (bad_ptr(dy) || bad_ptr(dx) || bad_ptr(workspace)) return kInvalid;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((N / NS::BN) * ((M + NS::BM - 1) / NS::BM)),
+                  static_cast<unsigned>(used));
+  int r = launch_kernel(gemm_nn_nf4_kernel<NS>, grid, dim3(NS::kThreads), st, dy, lddy, nw, dx,
+                        static_cast<int>(M), N, K, workspace, per);
+  if (r != kOk) return r;
+  const int64_t n4 = M * static_cast<int64_t>(N) / 4;
+  return launch_kernel(split_sum_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
+                       dim3(256), st, reinterpret_cast<const f32x4*>(workspace), used, n4, n4,
+                       N / 4, nullptr, reinterpret_cast<u32x2*>(dx));
 }

@@ -39,7 +39,9 @@ KEEP_UNPACKED_FOR_BACKWARD = True
 # hipBLASLt on MI355X (nf4_gemm.prefer_fused, prefer_fused_grad_input: a grid of half to one
 # wave of the compute units and a contraction of at most 2048, e.g. the q|k|v and o forward at
 # 1024-2048 rows, the gate|up forward at up to 128 rows, the q|k|v and o input gradient at
-# 1024 rows, down's input gradient at up to 128 rows); elsewhere unpack + hipBLASLt runs.  Only
+# 1024 rows, down's input gradient at up to 128 rows; and below half a wave with the
+# contraction split, e.g. the q|k|v, o and down forward and the q|k|v, o and gate|up input
+# gradient at up to 256 rows); elsewhere unpack + hipBLASLt runs.  Only
 # a forward that unpacks W itself uses it: a caller that passes the unpacked weight (the
 # decoder layer's one-launch unpack of all seven projections) keeps hipBLASLt, and so does a
 # backward that has the forward's unpacked weight (KEEP_UNPACKED_FOR_BACKWARD).
