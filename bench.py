@@ -592,14 +592,10 @@ def step_summary(per, total, gcw, unit_scale=1.0, digits=1):
     return out
 
 
-def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
-    """One Qwen2.5-1.5B decoder layer (testt_amd/layer.py) at B=4 x T=512 = 2048 real tokens:
-    forward and forward+backward time per step on the GPU (a torch event pair around each
-    step: every kernel, GEMM and the attention).  With reference_profile, the layer runs with
-    the reference's memory profile: gate|up recomputed in backward (mlp.RECOMPUTE_GATE_UP) and
-    the NF4 weights unpacked again in backward (nf4.KEEP_UNPACKED_FOR_BACKWARD = False), the
-    work the reference's own layer does."""
-    from testt_amd import layer, mlp, nf4
+def layer_inputs(dev, lengths=None):
+    """A synthetic decoder layer and its inputs at B=4 x T=512: every position real, or the
+    first lengths[b] of row b (then key_valid is the key mask and pos the real positions)."""
+    from testt_amd import layer
 
     B, T, H = workloads.BATCH, workloads.SEQ, workloads.HIDDEN
     w = layer.synthetic_layer(dev)
@@ -617,6 +613,22 @@ def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
     d0 = (0.5 * torch.randn(M, H, generator=g)).to(torch.float16).to(dev)
     gs = (1e-2 * torch.randn(M, H, generator=g)).to(dev)
     gd = (1e-2 * torch.randn(M, H, generator=g)).to(torch.float16).to(dev)
+    return w, pos, key_valid, cos, sin, s0, d0, gs, gd
+
+
+def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
+    """One Qwen2.5-1.5B decoder layer (testt_amd/layer.py) at B=4 x T=512 = 2048 real tokens
+    (or the first `lengths` of each row): forward and forward+backward time per step of the
+    eager loop (a torch event pair around each step: every kernel, GEMM and the attention).
+    With reference_profile, the layer runs with the reference's memory profile: gate|up
+    recomputed in backward (mlp.RECOMPUTE_GATE_UP) and the NF4 weights unpacked again in
+    backward (nf4.KEEP_UNPACKED_FOR_BACKWARD = False), the work the reference's own layer
+    does."""
+    from testt_amd import layer, mlp, nf4
+
+    B, T = workloads.BATCH, workloads.SEQ
+    w, pos, key_valid, cos, sin, s0, d0, gs, gd = layer_inputs(dev, lengths)
+    M = pos.numel()
 
     def step(backward):
         s_in = s0.detach().requires_grad_(True)
@@ -636,8 +648,6 @@ def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
             out[f"{name}_us"] = st["mean"]
             out[f"{name}_us_median"] = st["median"]
             out[f"{name}_steps"] = st
-        if not reference_profile and lengths is None:
-            out.update(graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps))
     finally:
         mlp.RECOMPUTE_GATE_UP, nf4.KEEP_UNPACKED_FOR_BACKWARD = saved
     out.update(tokens=M, batch=B, seq=T, lora_rank=16)
@@ -658,19 +668,20 @@ def time_layer(dev, steps, warmup, reference_profile=False, lengths=None):
     return out
 
 
-def graph_layer(dev, w, pos, cos, sin, s0, d0, gs, gd, steps):
+def graph_layer(dev, steps, lengths=None):
     """The layer's forward+backward (and forward alone) captured in a HIP graph
     (torch.cuda.graph) and replayed `steps` times between torch events: the launches and their
     work without the Python and dispatch time of the eager loop."""
     from testt_amd import layer
 
     B, T = workloads.BATCH, workloads.SEQ
+    w, pos, key_valid, cos, sin, s0, d0, gs, gd = layer_inputs(dev, lengths)
     s_in = s0.clone().requires_grad_(True)
     d_in = d0.clone().requires_grad_(True)
     leaves = (s_in, d_in, *w.lora_q, *w.lora_v)
 
     def step(backward):
-        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, None)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, key_valid)
         if backward:
             torch.autograd.backward([s, d], [gs, gd])
         for t in leaves:
@@ -1701,10 +1712,14 @@ def main():
         log(f"layer, reference work profile: fwd {layer_ref['fwd_us']} us, fwd+bwd "
             f"{layer_ref['fwd_bwd_us']} us (median {layer_ref['fwd_bwd_us_median']})")
         layer_t = time_layer(dev, n_layer_steps, 5)
+        # the HIP-graph replays after every eager timing
+        layer_t.update(graph_layer(dev, n_layer_steps))
+        layer_ragged.update(graph_layer(dev, n_layer_steps, lengths=(512, 152, 128, 96)))
         log(f"layer fwd {layer_t['fwd_us']} us (median {layer_t['fwd_us_median']}), fwd+bwd "
             f"{layer_t['fwd_bwd_us']} us (median {layer_t['fwd_bwd_us_median']}) (eager); "
             f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
-            f"{layer_t['graph_fwd_bwd_us']} us")
+            f"{layer_t['graph_fwd_bwd_us']} us; ragged graph-replayed fwd+bwd "
+            f"{layer_ragged['graph_fwd_bwd_us']} us")
     kernels = {}
     total_us = 0.0
     total_bytes = 0

@@ -26,8 +26,8 @@ extern "C" {
 #endif
 
 /* ABI version of this header; soupk_abi_version() returns the library's.  4 adds
-   soupk_lora_rope_fwd, soupk_gemm_nn_nf4, soupk_gemm_tn_nf4_split, soupk_gemm_nn_nf4_split
-   and soupk_init_device to version 3's entry points. */
+   soupk_lora_rope_fwd, soupk_gemm_nn_nf4, soupk_gemm_tn_nf4_split, soupk_gemm_nn_nf4_split,
+   soupk_gemm_lt, soupk_gemm_lt_index and soupk_init_device to version 3's entry points. */
 #define SOUPK_ABI_VERSION 4
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
@@ -491,6 +491,31 @@ int soupk_gemm_nn_nf4_split(const uint16_t* dy, int64_t lddy, int32_t n_parts,
                             const int32_t* part_rows, int32_t qblock, int32_t qblock2,
                             uint16_t* dx, int64_t M, int32_t N, int32_t K, int32_t splits,
                             float* workspace, int64_t workspace_floats, void* stream);
+
+/*
+ * D = op(A) op(B) (+ D with accumulate = 1) (+ bias[m] along D's columns), column-major as BLAS,
+ * fp16 A and B, fp16 D or fp32 D (d_f32 = 1), fp32 accumulation, `batch` problems strided by
+ * stride_a / stride_b / stride_d elements, on hipBLASLt: the library that runs the step's dense
+ * GEMMs, called without its per-call setup.  A problem's descriptor, layouts and algorithm are
+ * made on its first call and kept (per device); the algorithm is hipBLASLt solution
+ * `algo_index` when it supports the problem within `workspace_bytes`, else the heuristic's
+ * first choice (algo_index -1: always).  Replaces the per-call setup of torch.matmul, through
+ * which the reference runs these GEMMs (solution/nf4.py:108-127, solution/mlp.py:80-113).
+ * bias: fp16, one problem, fp16 D.  Returns hipErrorLaunchFailure when hipBLASLt fails.
+ */
+int soupk_gemm_lt(int32_t trans_a, int32_t trans_b, int64_t m, int64_t n, int64_t k,
+                  const uint16_t* A, int64_t lda, int64_t stride_a, const uint16_t* B,
+                  int64_t ldb, int64_t stride_b, void* D, int64_t ldd, int64_t stride_d,
+                  int32_t d_f32, int32_t batch, int32_t accumulate, const uint16_t* bias,
+                  int32_t algo_index, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The hipBLASLt solution index a soupk_gemm_lt problem runs with, -1 before its first call
+   (the same arguments, without the pointers and the stream; has_bias for the bias). */
+int soupk_gemm_lt_index(int32_t trans_a, int32_t trans_b, int64_t m, int64_t n, int64_t k,
+                        int64_t lda, int64_t stride_a, int64_t ldb, int64_t stride_b,
+                        int64_t ldd, int64_t stride_d, int32_t d_f32, int32_t batch,
+                        int32_t has_bias, int32_t accumulate, int32_t algo_index,
+                        int64_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,10 @@ SIGNATURES = {
                                 _i64, _i32, _i32, _i32, _p, _i64, _p],
     "soupk_gemm_nn_nf4_split": [_p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64,
                                 _i32, _i32, _i32, _p, _i64, _p],
+    "soupk_gemm_lt": [_i32, _i32, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,
+                      _i32, _i32, _i32, _p, _i32, _p, _i64, _p],
+    "soupk_gemm_lt_index": [_i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i32, _i32, _i32, _i32, _i32, _i64],
 }
 
 

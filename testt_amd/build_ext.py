@@ -71,7 +71,8 @@ def build(verbose=False, defines=(), out=None):
     with ThreadPoolExecutor(jobs) as pool:
         objs = list(pool.map(lambda s: _compile(hipcc, s, build_dir, defines), srcs))
     tmp = lib_path + ".tmp"
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+           "-lhipblaslt"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link of {LIB_NAME} failed:\n{proc.stderr}")

@@ -1,7 +1,7 @@
 """hipBLASLt solution choices for the GEMMs of the QLoRA training step, replayed through PyTorch's
-TunableOp: torch.matmul stays the entry point and hipBLASLt the library, only the solution
-hipBLASLt's heuristic would pick is replaced by the one that timed fastest for the problem on an
-MI355X.
+TunableOp (and by the layer's direct hipBLASLt calls, testt_amd/blas.py): hipBLASLt stays the
+library, only the solution hipBLASLt's heuristic would pick is replaced by the one that timed
+fastest for the problem on an MI355X.
 
 hipBLASLt's first heuristic choice is far from its best solution on some of the step's shapes,
 the worst being the gate|up input gradient ([2048 x 17920] @ [17920 x 1536]): 221 us with the
@@ -31,16 +31,28 @@ def enable(path=RESULTS):
     TunableOp accepted the table."""
     import torch
 
+    from . import blas
+
     torch.cuda.tunable.enable(True)
     torch.cuda.tunable.tuning_enable(False)
     torch.cuda.tunable.record_untuned_enable(False)
-    return bool(torch.cuda.tunable.read_file(path))
+    accepted = bool(torch.cuda.tunable.read_file(path))
+    # the direct hipBLASLt GEMMs (testt_amd/blas.py) run the same solutions, once TunableOp
+    # has checked the table's validators against this system
+    if accepted:
+        blas.load_table(path)
+    else:
+        blas.clear_table()
+    return accepted
 
 
 def disable():
     import torch
 
+    from . import blas
+
     torch.cuda.tunable.enable(False)
+    blas.clear_table()
 
 
 def _write_table(path):

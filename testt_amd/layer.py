@@ -33,6 +33,7 @@ from dataclasses import dataclass
 import torch
 
 from . import attention as _attention
+from . import blas as _blas
 from . import lora as _lora
 from . import workloads
 from .mlp import fused_mlp
@@ -120,7 +121,7 @@ class QKVLora(torch.autograd.Function):
     @staticmethod
     def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16=None, staged=None):
         w = w16 if w16 is not None else unpack_concat(weights, y16.device)
-        qkv = torch.nn.functional.linear(y16, w, bias)
+        qkv = _blas.linear(y16, w, bias)
         keep_for_backward(ctx, w)
         del w
         ctx.weights, ctx.scaling = weights, scaling
@@ -169,7 +170,7 @@ class QKVLora(torch.autograd.Function):
         dy = dt @ a16
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
-            dy.addmm_(g_qkv.to(torch.float16), w)
+            _blas.matmul(g_qkv.to(torch.float16), w, out=dy, accumulate=True)
         return dy, None, grads[0], grads[1], grads[2], grads[3], None, None, None, None
 
     @staticmethod
@@ -183,7 +184,7 @@ class QKVLora(torch.autograd.Function):
         d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
         if g_qkv is not None:
             w = unpacked_for_backward(ctx, ctx.weights, y16.device)
-            dy.addmm_(g_qkv.to(torch.float16), w)
+            _blas.matmul(g_qkv.to(torch.float16), w, out=dy, accumulate=True)
         return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None, None
 
 
@@ -207,7 +208,7 @@ class QKVLoraRopeAttention(torch.autograd.Function):
     def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16, staged, cos, sin,
                 pos_idx, cu_seqlens, batch, seq, n_heads, n_kv, scale):
         w = w16 if w16 is not None else unpack_concat(weights, y16.device)
-        qkv = torch.nn.functional.linear(y16, w, bias)
+        qkv = _blas.linear(y16, w, bias)
         keep_for_backward(ctx, w)
         del w
         params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
@@ -240,7 +241,7 @@ class QKVLoraRopeAttention(torch.autograd.Function):
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
         d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
         w = unpacked_for_backward(ctx, ctx.weights, dev)
-        dy.addmm_(dqkv, w)
+        _blas.matmul(dqkv, w, out=dy, accumulate=True)
         return (dy, None, d_aq, d_bq, d_av, d_bv) + (None,) * 13
 
 

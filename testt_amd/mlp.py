@@ -21,6 +21,7 @@ raises instead of reading gradients as activations.
 import torch
 
 from . import _ext
+from . import blas as _blas
 from ._common import kernels_ok
 from .nf4 import keep_for_backward, unpack_concat
 
@@ -66,9 +67,9 @@ def gated_silu_backward_(dact, gu):
 
 
 def _mm(a, b):
-    """a @ b: torch.mm for the 2-d operands of the layer (the same hipBLASLt GEMM as
-    torch.matmul, without its shape dispatch on the host), torch.matmul otherwise."""
-    return torch.mm(a, b) if a.dim() == 2 else torch.matmul(a, b)
+    """a @ b: the direct hipBLASLt GEMM (testt_amd/blas.py: torch.matmul's solution without
+    its per-call setup) for the 2-d operands of the layer, torch.matmul otherwise."""
+    return _blas.matmul(a, b) if a.dim() == 2 and b.dim() == 2 else torch.matmul(a, b)
 
 
 def matmul_split_k(a, b, parts):
@@ -82,7 +83,7 @@ def matmul_split_k(a, b, parts):
     c = K // parts
     a3 = a.as_strided((parts, M, c), (c, a.stride(0), 1))
     b3 = b.as_strided((parts, c, N), (c * b.stride(0), b.stride(0), 1))
-    partial = torch.ops.aten.bmm.dtype(a3, b3, torch.float32)      # [parts, M, N] fp32
+    partial = _blas.bmm_f32(a3, b3)                                 # [parts, M, N] fp32
     out = torch.empty((M, N), dtype=torch.float16, device=a.device)
     if M * N:
         _ext.call("soupk_sum_partials", partial.data_ptr(), parts, M * N, M * N,

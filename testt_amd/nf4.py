@@ -20,6 +20,7 @@ import weakref
 import torch
 
 from . import _ext
+from . import blas
 from ._common import kernels_ok
 
 # One workgroup step of the unpack kernel: 256 threads x 4 chunks x 16 packed bytes.
@@ -423,7 +424,11 @@ class FrozenNF4Linear(torch.autograd.Function):
                 out = nf4_gemm.nf4_linear(x2, weights, bias)
                 return out.view(*x.shape[:-1], out.shape[-1])
         weight = w16 if w16 is not None else unpack_concat(weights, x.device)
-        out = torch.nn.functional.linear(x, weight, bias)
+        if x.dim() == 2 or x.is_contiguous():
+            out = blas.linear(x.reshape(-1, x.shape[-1]), weight, bias)
+            out = out.view(*x.shape[:-1], out.shape[-1])
+        else:
+            out = torch.nn.functional.linear(x, weight, bias)
         keep_for_backward(ctx, weight)
         return out
 
@@ -442,7 +447,10 @@ class FrozenNF4Linear(torch.autograd.Function):
                     dx = nf4_gemm.nf4_grad_input(g2, ctx.weights)
                     return dx.view(*g.shape[:-1], dx.shape[-1]), None, None, None
             weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
-            grad_x = torch.mm(g, weight) if g.dim() == 2 else g @ weight
+            if g.dim() == 2:
+                grad_x = blas.matmul(g, weight)
+            else:
+                grad_x = g @ weight
         return grad_x, None, None, None
 
 
