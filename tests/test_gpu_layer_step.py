@@ -226,3 +226,44 @@ def test_unpacked_weights_freed_after_forward_without_keep(monkeypatch, keep):
         assert per_layer < 0.5 * unpacked
     (s.float().sum() + d.float().sum()).backward()
     assert w.lora_q[0].grad is not None
+
+
+@pytest.mark.parametrize("lengths,with_delta", [((64, 37), True), ((64, 64), True),
+                                               ((64, 37), False)])
+def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
+    """The layer as one autograd node (layer.DecoderLayer, calling the five nodes' forward and
+    backward in order) against the five nodes themselves: the same outputs and gradients, bit
+    for bit, and the same parameter gradients after two steps accumulate; also for the first
+    layer, whose input norm has no residual delta."""
+    batch, seq = 2, 64
+    w = layer.synthetic_layer(DEV, seed=12)
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(6)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    runs = []
+    for one_node in (True, False):
+        monkeypatch.setattr(layer, "ONE_NODE_LAYER", one_node)
+        out = []
+        for _ in range(2):
+            s_in = s0.clone().requires_grad_(True)
+            d_in = d0.clone().requires_grad_(True) if with_delta else None
+            s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                                       layer.key_valid_of(amask))
+            assert (type(s.grad_fn).__name__ == "DecoderLayerBackward") == one_node
+            torch.autograd.backward([s, d], [gs, gd])
+            out += [s.detach(), d.detach(), s_in.grad,
+                    d_in.grad if with_delta else torch.zeros(())]
+        runs.append(out + [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+    names = ["s", "d", "d s_in", "d delta"] * 2 + ["d A_q", "d B_q", "d A_v", "d B_v"]
+    for name, a, b in zip(names, *runs):
+        assert torch.equal(a, b), name

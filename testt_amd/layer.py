@@ -36,10 +36,10 @@ from . import attention as _attention
 from . import blas as _blas
 from . import lora as _lora
 from . import workloads
-from .mlp import fused_mlp
-from .nf4 import (frozen_linear, keep_for_backward, unpack_concat, unpack_groups,
+from .mlp import FusedNF4MLP, fused_mlp
+from .nf4 import (FrozenNF4Linear, frozen_linear, keep_for_backward, unpack_concat, unpack_groups,
                   unpack_groups_lora, unpacked_for_backward)
-from .rmsnorm import add_rmsnorm
+from .rmsnorm import AddRMSNorm, RMSNormNoAdd, add_rmsnorm
 from .rope import rope_pack
 
 
@@ -323,6 +323,85 @@ def lora_without_dropout(w):
     return w.dropout == 0.0
 
 
+# The layer's five autograd nodes (input norm, q|k|v + LoRA + RoPE + attention, o projection,
+# post-attention norm, MLP) as one node whose forward and backward call theirs in order: the
+# same kernels and the same values, bit for bit, with one node for the autograd engine to run
+# instead of five (measured on the eager layer: the engine's per-node work and the Python around
+# each node are host time the GPU waits for at the ragged batch).
+ONE_NODE_LAYER = True
+
+
+class _SubCtx:
+    """The ctx of a node run inside another node's forward and backward: records what the node
+    saves (the outer node saves it, so that outputs among it hold no reference cycle)."""
+
+    def __init__(self, need):
+        self.needs_input_grad = (need,) * 32
+        self.saved = ()
+
+    def save_for_backward(self, *tensors):
+        self.saved = tensors
+
+
+class DecoderLayer(torch.autograd.Function):
+    """(s, d) of the fused path of decoder_layer as one autograd node."""
+
+    @staticmethod
+    def forward(ctx, s_in, delta, a_q, b_q, a_v, b_v, w, w_qkv, w_o, w_gu, w_d, staged, cos, sin,
+                pos_idx, cu, batch, seq, scale):
+        need = any(ctx.needs_input_grad)
+        subs = [_SubCtx(need) for _ in range(5)]
+        ctx.no_add = delta is None      # the first layer: the input norm without a residual add
+        if ctx.no_add:
+            s1 = s_in
+            y, _ = RMSNormNoAdd.forward(subs[0], s_in, w.input_norm, w.eps, None, 0)
+        else:
+            s1, y, _ = AddRMSNorm.forward(subs[0], s_in, delta, w.input_norm, w.eps, None, 0)
+        a = QKVLoraRopeAttention.forward(subs[1], y, w.qkv_bias, a_q, b_q, a_v, b_v, w.scaling,
+                                         (w.q, w.k, w.v), w_qkv, staged, cos, sin, pos_idx, cu,
+                                         batch, seq, w.n_heads, w.n_kv, scale)
+        del y
+        o = FrozenNF4Linear.forward(subs[2], a, w.o_bias, (w.o,), w_o)
+        del a
+        s2, y2, _ = AddRMSNorm.forward(subs[3], s1, o, w.post_norm, w.eps, None, 0)
+        del s1, o
+        d = FusedNF4MLP.forward(subs[4], y2, w.gate, w.up, w.down, w_gu, w_d)
+        flat, counts = [], []
+        for c in subs:
+            flat.extend(c.saved)
+            counts.append(len(c.saved))
+            c.saved = ()
+        ctx.save_for_backward(*flat)
+        ctx.subs, ctx.counts = subs, counts
+        return s2, d
+
+    @staticmethod
+    def backward(ctx, g_s, g_d):
+        subs, saved, i = ctx.subs, ctx.saved_tensors, 0
+        ctx.subs = None
+        for c, n in zip(subs, ctx.counts):
+            c.saved_tensors = saved[i:i + n]
+            i += n
+        del saved
+        # each gradient in the dtype of the tensor it belongs to, as the engine casts it between
+        # nodes: s fp32; the norm outputs, a and o fp16
+        g_y2 = FusedNF4MLP.backward(subs[4], g_d)[0]
+        g_s1, g_o = AddRMSNorm.backward(subs[3], g_s, g_y2.to(torch.float16), None)[:2]
+        del g_y2
+        g_a = FrozenNF4Linear.backward(subs[2], g_o.to(torch.float16))[0]
+        del g_o
+        r = QKVLoraRopeAttention.backward(subs[1], g_a.to(torch.float16))
+        del g_a
+        if ctx.no_add:
+            # s_in is also the residual: its gradient adds the norm's (two terms, either order)
+            g_s_in = RMSNormNoAdd.backward(subs[0], r[0].to(torch.float16), None)[0] + g_s1
+            g_delta = None
+        else:
+            g_s_in, g_delta = AddRMSNorm.backward(subs[0], g_s1.to(torch.float32),
+                                                  r[0].to(torch.float16), None)[:2]
+        return (g_s_in, g_delta, r[2], r[3], r[4], r[5]) + (None,) * 13
+
+
 def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     """(s, d): the residual stream and the MLP output of one layer (the next layer's delta).
     key_valid: uint8 [batch, seq] (key_valid_of(attention_mask)), or None when nothing is
@@ -344,9 +423,15 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
             hd == _attention.HEAD_DIM and nkv > 0 and nh % nkv == 0 and \
             w.lora_q[1].shape[0] == nh * hd and w.lora_v[1].shape[0] == nkv * hd and \
             _lora.params_supported(*params, s.device):
-        s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
         scale = 1.0 / math.sqrt(hd) if w.attn_scale is None else float(w.attn_scale)
+        if ONE_NODE_LAYER and w_o is not None and w_gu is not None and w_d is not None:
+            return DecoderLayer.apply(s.contiguous(),
+                                      None if delta is None else delta.contiguous(),
+                                      *w.lora_q, *w.lora_v,
+                                      w, w_qkv, w_o, w_gu, w_d, staged, cos, sin, pos_idx, cu,
+                                      batch, seq, scale)
+        s, y, _ = add_rmsnorm(s, delta, w.input_norm, w.eps)
         a = QKVLoraRopeAttention.apply(y, w.qkv_bias, *w.lora_q, *w.lora_v, w.scaling,
                                        (w.q, w.k, w.v), w_qkv, staged, cos, sin, pos_idx, cu,
                                        batch, seq, nh, nkv, scale)
