@@ -27,7 +27,8 @@ extern "C" {
 
 /* ABI version of this header; soupk_abi_version() returns the library's.  4 adds
    soupk_lora_rope_fwd, soupk_gemm_nn_nf4, soupk_gemm_tn_nf4_split, soupk_gemm_nn_nf4_split,
-   soupk_gemm_lt, soupk_gemm_lt_index and soupk_init_device to version 3's entry points. */
+   soupk_gemm_lt, soupk_gemm_lt_index, soupk_layer_fwd, soupk_layer_bwd and soupk_init_device
+   to version 3's entry points. */
 #define SOUPK_ABI_VERSION 4
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
@@ -516,6 +517,111 @@ int soupk_gemm_lt_index(int32_t trans_a, int32_t trans_b, int64_t m, int64_t n, 
                         int64_t ldd, int64_t stride_d, int32_t d_f32, int32_t batch,
                         int32_t has_bias, int32_t accumulate, int32_t algo_index,
                         int64_t workspace_bytes);
+
+/*
+ * One Qwen2 decoder layer of the QLoRA step, forward and backward, each as one call that issues
+ * the layer's kernels and hipBLASLt GEMMs in order on `stream` (widening: the reference's
+ * layer, solution/model.py:209-279, runs them from Python one operation at a time).  The layer
+ * is the fused path of testt_amd/layer.py: input RMSNorm (with the residual add unless delta is
+ * NULL), q|k|v GEMM + bias, the rank-16 LoRA forward fused with RoPE, varlen causal GQA
+ * attention, o GEMM, residual add + post-attention RMSNorm, gate|up GEMM, gated SiLU, down GEMM
+ * (split over K into p_down slices when p_down > 1); the backward mirrors it (the gate|up input
+ * gradient split into p_gu slices; the attention backward with RoPE's backward fused in; the
+ * LoRA backward).  Every value is the one the same kernels give when called one by one: the
+ * calls are the entry points above with the arguments testt_amd/layer.py passes them.  The
+ * caller owns every buffer; the unpacked weights (row stacks q|k|v [W, H], o [H, NH*D],
+ * gate|up [2I, H], down [H, I], W = (NH + 2 NKV) * D) and the staged LoRA parameters are the
+ * layer's soupk_nf4_unpack_multi_lora output.  algo_*: hipBLASLt solution indices (-1: the
+ * heuristic's) of the GEMMs as soupk_gemm_lt takes them.  Returns the first failing call's
+ * status; nothing is launched after it.
+ */
+typedef struct SoupkLayerDims {
+  int64_t M;                                   /* tokens (rows) */
+  int32_t H, NH, NKV, D, I, r, batch, seq;     /* D = 128, r = 16 */
+  int32_t p_down, p_gu;                        /* K slices of the split products (1: none) */
+  float eps, scaling, scale;
+  const float* norm1;                          /* fp32 [H] RMSNorm weights */
+  const float* norm2;
+  const uint16_t* qkv_bias;                    /* fp16 [W] or NULL */
+  const uint16_t* w_qkv;
+  const uint16_t* w_o;
+  const uint16_t* w_gu;
+  const uint16_t* w_d;
+  const uint16_t* staged;
+  const float* cos;                            /* fp32 [>= seq, D] */
+  const float* sin;
+  const int64_t* pos;                          /* int64 [M]: padded positions b * seq + t */
+  const int32_t* cu;                           /* int32 [batch + 1] */
+  void* gemm_ws;                               /* hipBLASLt workspace */
+  int64_t gemm_ws_bytes;
+} SoupkLayerDims;
+
+typedef struct SoupkLayerFwd {
+  const float* s_in;                           /* fp32 [M, H] residual stream */
+  const uint16_t* delta;                       /* fp16 [M, H], or NULL (the first layer) */
+  int32_t algo_qkv, algo_o, algo_gu, algo_down;
+  /* saved for the backward */
+  float* s1;                                   /* fp32 [M, H] (unused when delta is NULL) */
+  uint16_t* y;                                 /* fp16 [M, H] */
+  float* rstd1;                                /* fp32 [M] */
+  uint16_t* t;                                 /* fp16 [M, 2r] */
+  uint16_t* qkv_r;                             /* fp16 [M, W] */
+  uint16_t* attn;                              /* fp16 [M, NH*D] */
+  float* lse;                                  /* fp32 [NH, M] */
+  float* s2;                                   /* fp32 [M, H] (output) */
+  uint16_t* y2;                                /* fp16 [M, H] */
+  float* rstd2;                                /* fp32 [M] */
+  uint16_t* gu;                                /* fp16 [M, 2I] */
+  /* transient */
+  uint16_t* qkv;                               /* fp16 [M, W] */
+  uint16_t* o;                                 /* fp16 [M, H] */
+  uint16_t* act;                               /* fp16 [M, I] */
+  float* down_part;                            /* fp32 [p_down, M, H] when p_down > 1 */
+  uint16_t* d;                                 /* fp16 [M, H] (output) */
+} SoupkLayerFwd;
+
+typedef struct SoupkLayerBwd {
+  const float* s_in;                           /* the forward's input, and its saved tensors */
+  const float* s1;
+  const float* rstd1;
+  const uint16_t* y;
+  const uint16_t* t;
+  const uint16_t* qkv_r;
+  const uint16_t* attn;
+  const float* lse;
+  const float* s2;
+  const float* rstd2;
+  const uint16_t* y2;
+  uint16_t* gu;                                /* overwritten with its gradient */
+  int32_t has_delta;                           /* 0: the forward's delta was NULL */
+  int32_t algo_down_dx, algo_gu_dx, algo_o_dx, algo_qkv_dx;
+  const float* g_s;                            /* fp32 [M, H] gradient of s2 */
+  const uint16_t* g_d;                         /* fp16 [M, H] gradient of d */
+  /* scratch */
+  uint16_t* dact;                              /* fp16 [M, I] */
+  float* gu_part;                              /* fp32 [p_gu, M, H] when p_gu > 1 */
+  uint16_t* g_y2;                              /* fp16 [M, H] */
+  float* g_s1;                                 /* fp32 [M, H] */
+  uint16_t* g_o;                               /* fp16 [M, H] */
+  uint16_t* g_a;                               /* fp16 [M, NH*D] */
+  float* attn_ws;                              /* soupk_attention_varlen_bwd's workspace */
+  uint16_t* dqkv;                              /* fp16 [M, W] */
+  uint16_t* dt;                                /* fp16 [M, 2r] */
+  uint16_t* dy;                                /* fp16 [M, H] */
+  float* lora_ws;                              /* soupk_lora_bwd_params' workspace */
+  int64_t lora_ws_floats;
+  /* outputs */
+  float* g_s_in;                               /* fp32 [M, H]; without delta, the norm's part
+                                                  only (the caller adds g_s1) */
+  uint16_t* g_delta;                           /* fp16 [M, H], or NULL without delta */
+  float* d_aq;                                 /* fp32 [r, H] */
+  float* d_av;
+  float* d_bq;                                 /* fp32 [NH*D, r] */
+  float* d_bv;                                 /* fp32 [NKV*D, r] */
+} SoupkLayerBwd;
+
+int soupk_layer_fwd(const SoupkLayerDims* dims, const SoupkLayerFwd* a, void* stream);
+int soupk_layer_bwd(const SoupkLayerDims* dims, const SoupkLayerBwd* a, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import torch
 
 from oracle.nf4 import dequant_state
 from oracle.rope import apply_rotary
-from testt_amd import layer, nf4, workloads
+from testt_amd import layer, layer_native, nf4, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -231,10 +231,11 @@ def test_unpacked_weights_freed_after_forward_without_keep(monkeypatch, keep):
 @pytest.mark.parametrize("lengths,with_delta", [((64, 37), True), ((64, 64), True),
                                                ((64, 37), False)])
 def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
-    """The layer as one autograd node (layer.DecoderLayer, calling the five nodes' forward and
-    backward in order) against the five nodes themselves: the same outputs and gradients, bit
-    for bit, and the same parameter gradients after two steps accumulate; also for the first
-    layer, whose input norm has no residual delta."""
+    """The layer as one autograd node -- issued from C (layer_native.NativeDecoderLayer,
+    soupk_layer_fwd / _bwd) or from Python (layer.DecoderLayer, calling the five nodes' forward
+    and backward in order) -- against the five nodes themselves: the same outputs and
+    gradients, bit for bit, and the same parameter gradients after two steps accumulate; also
+    for the first layer, whose input norm has no residual delta."""
     batch, seq = 2, 64
     w = layer.synthetic_layer(DEV, seed=12)
     amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
@@ -249,15 +250,18 @@ def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
     gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
     gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
     runs = []
-    for one_node in (True, False):
+    for one_node, native in ((True, True), (True, False), (False, False)):
         monkeypatch.setattr(layer, "ONE_NODE_LAYER", one_node)
+        monkeypatch.setattr(layer_native, "NATIVE_LAYER", native)
+        node = ("NativeDecoderLayerBackward" if native else
+                "DecoderLayerBackward" if one_node else None)
         out = []
         for _ in range(2):
             s_in = s0.clone().requires_grad_(True)
             d_in = d0.clone().requires_grad_(True) if with_delta else None
             s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
                                        layer.key_valid_of(amask))
-            assert (type(s.grad_fn).__name__ == "DecoderLayerBackward") == one_node
+            assert (type(s.grad_fn).__name__ == node) == one_node
             torch.autograd.backward([s, d], [gs, gd])
             out += [s.detach(), d.detach(), s_in.grad,
                     d_in.grad if with_delta else torch.zeros(())]
@@ -265,5 +269,6 @@ def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
         for p in (*w.lora_q, *w.lora_v):
             p.grad = None
     names = ["s", "d", "d s_in", "d delta"] * 2 + ["d A_q", "d B_q", "d A_v", "d B_v"]
-    for name, a, b in zip(names, *runs):
-        assert torch.equal(a, b), name
+    for ref in runs[1:]:
+        for name, a, b in zip(names, runs[0], ref):
+            assert torch.equal(a, b), name

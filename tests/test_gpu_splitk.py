@@ -1,5 +1,6 @@
-"""GPU: the split-K gate|up input gradient of the MLP backward (testt_amd/mlp.py
-matmul_split_k: batched hipBLASLt GEMMs with fp32 partials + soupk_sum_partials).
+"""GPU: the split-K products of the MLP, the gate|up input gradient and the down projection's
+forward (testt_amd/mlp.py matmul_split_k: batched hipBLASLt GEMMs with fp32 partials +
+soupk_sum_partials).
 
 soupk_sum_partials is checked bit for bit against the same fp32 additions in the same order
 (torch elementwise adds) and one fp16 rounding.  The split product is checked against the exact
@@ -58,6 +59,11 @@ def test_matmul_split_k(M, K, N, parts):
     out = mlp.matmul_split_k(a, b, parts)
     assert out.dtype == torch.float16 and out.shape == (M, N)
     within_bound(out, a, b)
+    # b as the transpose of a row-major [N, K] (the down projection's forward, act @ W^T)
+    w = b.t().contiguous()
+    out_t = mlp.matmul_split_k(a, w.t(), parts)
+    within_bound(out_t, a, b)
+    assert torch.equal(out_t, mlp.matmul_split_k(a, w.t(), parts))   # deterministic
     within_bound(torch.matmul(a, b), a, b)          # the single GEMM obeys the same bound
     with pytest.raises(ValueError):
         mlp.matmul_split_k(a, b, 3 if K % 3 else 5)

@@ -114,3 +114,15 @@ def test_split_count_small_contraction():
     assert nf4_gemm.split_count(16, 128, 256, CUS) == 1
     assert nf4_gemm.split_count(16, 128, 64 * 2000, CUS) <= nf4_gemm.MAX_SPLITS
     assert nf4_gemm.split_count(16, 128 * 200, 1536, CUS) == 1   # 200 tiles, a short contraction
+
+
+@pytest.mark.parametrize("rows,gate_up,down", [
+    (256, 8, 2), (888, 8, 2), (1024, 8, 2), (1536, 4, 2), (2048, 4, 2), (3072, 2, 1),
+    (8192, 1, 1), (0, 1, 1)])
+def test_mlp_split_parts(rows, gate_up, down):
+    """The K slices of the MLP's split products by row count (testt_amd/mlp.py split_parts),
+    at Qwen2.5-1.5B's shapes: the gate|up input gradient [rows, 17920] @ [17920, 1536] and the
+    down projection's forward [rows, 8960] @ [8960, 1536]."""
+    from testt_amd import mlp
+    assert mlp.split_parts(rows, 1536, 17920, "gate_up") == gate_up
+    assert mlp.split_parts(rows, 1536, 8960, "down") == down

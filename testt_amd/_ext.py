@@ -80,6 +80,8 @@ SIGNATURES = {
                       _i32, _i32, _i32, _p, _i32, _p, _i64, _p],
     "soupk_gemm_lt_index": [_i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i32, _i32, _i32, _i32, _i32, _i64],
+    "soupk_layer_fwd": [_p, _p, _p],
+    "soupk_layer_bwd": [_p, _p, _p],
 }
 
 

@@ -135,26 +135,62 @@ def linear(x, w, bias=None):
 
 
 def bmm_f32(a3, b3):
-    """Batched a3 [P, M, K] @ b3 [P, K, N] -> fp32 [P, M, N]: a3 and b3 with unit column
-    stride and row strides of their own (slices of one matrix, as matmul_split_k makes)."""
+    """Batched a3 [P, M, K] @ b3 [P, K, N] -> fp32 [P, M, N]: a3 with unit column stride, b3
+    with unit column stride or unit row stride (slices of a transposed matrix), each with
+    strides of its own (slices of one matrix, as matmul_split_k makes)."""
     P, M, K = a3.shape
     N = b3.shape[2]
+    b_rows = b3.stride(2) == 1 and b3.stride(1) >= N     # each slice row-major [K, N]
+    b_cols = not b_rows and b3.stride(1) == 1 and b3.stride(2) >= K   # transposed [N, K]
     ok = (USE_GEMM_LT and a3.is_cuda and a3.dtype == torch.float16 and
           b3.dtype == torch.float16 and a3.dim() == 3 and b3.dim() == 3 and
-          b3.shape[:2] == (P, K) and a3.stride(2) == 1 and b3.stride(2) == 1 and K > 0 and
-          a3.stride(1) >= K and b3.stride(1) >= N and P > 0)
+          b3.shape[:2] == (P, K) and a3.stride(2) == 1 and (b_rows or b_cols) and K > 0 and
+          a3.stride(1) >= K and P > 0)
+    ld_b = b3.stride(1) if b_rows else b3.stride(2)
     if not ok or not _aligned(a3, b3) or (a3.stride(0) | a3.stride(1) | b3.stride(0) |
-                                          b3.stride(1)) % 8:
+                                          ld_b) % 8:
         return torch.ops.aten.bmm.dtype(a3, b3, torch.float32)
     out = torch.empty((P, M, N), dtype=torch.float32, device=a3.device)
     if M == 0 or N == 0:
         return out
     st = _ext.stream_of(a3)
     ws = _ws(a3.device, st)
-    # column-major per problem: out_p^T [N, M] = b3_p^T [N, K] @ a3_p^T [K, M]
-    _ext.call("soupk_gemm_lt", 0, 0, N, M, K, b3.data_ptr(), b3.stride(1), b3.stride(0),
-              a3.data_ptr(), a3.stride(1), a3.stride(0), out.data_ptr(), N, M * N, 1, P, 0,
-              None, -1, ws.data_ptr(), WORKSPACE_BYTES, st)
+    # column-major per problem: out_p^T [N, M] = op(b3_p^T) [N, K] @ a3_p^T [K, M]
+    _ext.call("soupk_gemm_lt", 0 if b_rows else 1, 0, N, M, K, b3.data_ptr(), ld_b,
+              b3.stride(0), a3.data_ptr(), a3.stride(1), a3.stride(0), out.data_ptr(), N, M * N,
+              1, P, 0, None, -1, ws.data_ptr(), WORKSPACE_BYTES, st)
+    return out
+
+
+def split_k(a, b, parts):
+    """fp16 a [M, K] @ b [K, N] as `parts` batched GEMMs over equal slices of K with fp32
+    partials, summed in slice order and rounded once (soupk_sum_partials) -> fp16 [M, N]; b
+    row-major or the transpose of a row-major [N, K].  None where the operands do not fit
+    (mlp.matmul_split_k then builds the slices as views).  The same two launches as the views
+    through bmm_f32, with the slices' strides computed here rather than by two as_strided
+    views and their checks (host time: the layer issues two of these per step)."""
+    M, K = a.shape
+    N = b.shape[1]
+    if not (USE_GEMM_LT and parts > 0 and K % parts == 0 and M > 0 and N > 0 and _fits(a)
+            and _fits(b) and a.device == b.device and a.stride(1) == 1 and a.stride(0) >= K):
+        return None
+    c = K // parts
+    if b.stride(1) == 1 and b.stride(0) >= N:
+        ta, ld_b = 0, b.stride(0)          # slice p: rows p*c .. of b
+    elif b.stride(0) == 1 and b.stride(1) >= K:
+        ta, ld_b = 1, b.stride(1)          # slice p: columns p*c .. of b^T
+    else:
+        return None
+    if not _aligned(a, b) or (a.stride(0) | ld_b | c) % 8:
+        return None
+    st = _ext.stream_of(a)
+    ws = _ws(a.device, st)
+    part = torch.empty((parts, M, N), dtype=torch.float32, device=a.device)
+    out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    _ext.call("soupk_gemm_lt", ta, 0, N, M, c, b.data_ptr(), ld_b, c * b.stride(0), a.data_ptr(),
+              a.stride(0), c, part.data_ptr(), N, M * N, 1, parts, 0, None, -1, ws.data_ptr(),
+              WORKSPACE_BYTES, st)
+    _ext.call("soupk_sum_partials", part.data_ptr(), parts, M * N, M * N, out.data_ptr(), st)
     return out
 
 

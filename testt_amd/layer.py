@@ -34,6 +34,7 @@ import torch
 
 from . import attention as _attention
 from . import blas as _blas
+from . import layer_native as _native
 from . import lora as _lora
 from . import workloads
 from .mlp import FusedNF4MLP, fused_mlp
@@ -425,6 +426,14 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
             _lora.params_supported(*params, s.device):
         cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
         scale = 1.0 / math.sqrt(hd) if w.attn_scale is None else float(w.attn_scale)
+        if ONE_NODE_LAYER and _native.supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
+            from .rope import _table
+            from ._index import as_index
+
+            return _native.NativeDecoderLayer.apply(
+                s.contiguous(), None if delta is None else delta.contiguous(), *w.lora_q,
+                *w.lora_v, w, w_qkv, w_o, w_gu, w_d, staged, _table(cos, seq, hd, "cos", s.device),
+                _table(sin, seq, hd, "sin", s.device), as_index(pos_idx), cu, batch, seq, scale)
         if ONE_NODE_LAYER and w_o is not None and w_gu is not None and w_d is not None:
             return DecoderLayer.apply(s.contiguous(),
                                       None if delta is None else delta.contiguous(),

@@ -1,0 +1,203 @@
+"""The decoder layer's fused path as one native call each way (soupk_layer_fwd / _bwd).
+
+testt_amd/layer.py's DecoderLayer runs the layer's five autograd nodes inside one, each
+operation still issued from Python: its checks, its allocation, its ctypes call.  On the
+MI355X box that made the eager layer host-bound at the ragged batch (about 485 us of issue time
+against 420 us of GPU time).  NativeDecoderLayer issues the same launches from C with the same
+arguments (csrc/layer_exec.hip), so the values are DecoderLayer's bit for bit; Python allocates
+the buffers (one arena for what the backward reads, one for the forward's temporaries, one for
+the backward's scratch) and fills two argument structs.
+
+Used by layer.decoder_layer when NATIVE_LAYER is set and the layer takes the fused path with its
+weights unpacked once for forward and backward (the default): LoRA rank 16 on q and v without
+dropout, head dim 128, no o-projection bias, the direct hipBLASLt GEMMs on, the unpacked weights
+kept for backward and the gate|up buffer kept (not recomputed).
+"""
+
+import ctypes
+
+import torch
+
+from . import _ext
+from . import blas as _blas
+from . import mlp as _mlp
+
+NATIVE_LAYER = True
+
+_p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+
+
+class LayerDims(ctypes.Structure):
+    _fields_ = ([("M", _i64)] +
+                [(n, _i32) for n in ("H", "NH", "NKV", "D", "I", "r", "batch", "seq", "p_down",
+                                     "p_gu")] +
+                [(n, _f32) for n in ("eps", "scaling", "scale")] +
+                [(n, _p) for n in ("norm1", "norm2", "qkv_bias", "w_qkv", "w_o", "w_gu", "w_d",
+                                   "staged", "cos", "sin", "pos", "cu", "gemm_ws")] +
+                [("gemm_ws_bytes", _i64)])
+
+
+class LayerFwd(ctypes.Structure):
+    _fields_ = ([("s_in", _p), ("delta", _p)] +
+                [(n, _i32) for n in ("algo_qkv", "algo_o", "algo_gu", "algo_down")] +
+                [(n, _p) for n in ("s1", "y", "rstd1", "t", "qkv_r", "attn", "lse", "s2", "y2",
+                                   "rstd2", "gu", "qkv", "o", "act", "down_part", "d")])
+
+
+class LayerBwd(ctypes.Structure):
+    _fields_ = ([(n, _p) for n in ("s_in", "s1", "rstd1", "y", "t", "qkv_r", "attn", "lse", "s2",
+                                   "rstd2", "y2", "gu")] +
+                [(n, _i32) for n in ("has_delta", "algo_down_dx", "algo_gu_dx", "algo_o_dx",
+                                     "algo_qkv_dx")] +
+                [(n, _p) for n in ("g_s", "g_d", "dact", "gu_part", "g_y2", "g_s1", "g_o", "g_a",
+                                   "attn_ws", "dqkv", "dt", "dy", "lora_ws")] +
+                [("lora_ws_floats", _i64)] +
+                [(n, _p) for n in ("g_s_in", "g_delta", "d_aq", "d_av", "d_bq", "d_bv")])
+
+
+_F16, _F32 = 2, 4
+
+
+def _arena(device, parts):
+    """One uint8 allocation holding `parts` ([(name, bytes)], each 256-byte aligned): the
+    tensor and {name: device address}."""
+    offs, total = {}, 0
+    for name, nbytes in parts:
+        offs[name] = total
+        total += (nbytes + 255) // 256 * 256
+    buf = torch.empty(max(total, 256), dtype=torch.uint8, device=device)
+    base = buf.data_ptr()
+    return buf, {n: base + o for n, o in offs.items()}
+
+
+def supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
+    from . import lora as _lora
+    from . import mlp, nf4
+
+    return (NATIVE_LAYER and _blas.USE_GEMM_LT and nf4.KEEP_UNPACKED_FOR_BACKWARD and
+            not mlp.RECOMPUTE_GATE_UP and staged is not None and w.o_bias is None and
+            None not in (w_qkv, w_o, w_gu, w_d) and s.dtype == torch.float32 and
+            (delta is None or delta.dtype == torch.float16) and w.head_dim == 128 and
+            _lora.RANK == 16 and s.dim() == 2 and s.shape[1] % 8 == 0 and
+            w_d.dim() == 2 and w_d.shape[1] % 8 == 0 and s.is_cuda)
+
+
+class NativeDecoderLayer(torch.autograd.Function):
+    """(s, d) of the layer's fused path, forward and backward each one soupk call."""
+
+    @staticmethod
+    def forward(ctx, s_in, delta, a_q, b_q, a_v, b_v, w, w_qkv, w_o, w_gu, w_d, staged, cos32,
+                sin32, pos, cu, batch, seq, scale):
+        from .rmsnorm import _weight32
+
+        dev = s_in.device
+        M, H = s_in.shape
+        NH, NKV, D, I, r = w.n_heads, w.n_kv, 128, w_d.shape[1], 16
+        NQ, NV = NH * D, NKV * D
+        W = NQ + 2 * NV
+        p_down = _mlp.SPLIT_K_DOWN or _mlp.split_parts(M, H, I, "down")
+        p_gu = _mlp.SPLIT_K_GATE_UP or _mlp.split_parts(M, H, 2 * I, "gate_up")
+        if I % p_down:
+            p_down = 1
+        if (2 * I) % p_gu:
+            p_gu = 1
+        st = _ext.stream_of(s_in)
+        ws = _blas._ws(dev, st)
+        norm1, norm2 = _weight32(w.input_norm, H, dev), _weight32(w.post_norm, H, dev)
+        bias = w.qkv_bias
+        dims = LayerDims(M, H, NH, NKV, D, I, r, batch, seq, p_down, p_gu, float(w.eps),
+                         float(w.scaling), float(scale), norm1.data_ptr(), norm2.data_ptr(),
+                         _ext.ptr(bias), w_qkv.data_ptr(), w_o.data_ptr(), w_gu.data_ptr(),
+                         w_d.data_ptr(), staged.data_ptr(), cos32.data_ptr(), sin32.data_ptr(),
+                         pos.data_ptr(), cu.data_ptr(), ws.data_ptr(), _blas.WORKSPACE_BYTES)
+        has_delta = delta is not None
+        keep, kp = _arena(dev, [("s1", M * H * _F32 if has_delta else 0), ("y", M * H * _F16),
+                                ("rstd1", M * _F32), ("t", M * 2 * r * _F16),
+                                ("qkv_r", M * W * _F16), ("attn", M * NQ * _F16),
+                                ("lse", NH * M * _F32), ("y2", M * H * _F16),
+                                ("rstd2", M * _F32), ("gu", M * 2 * I * _F16)])
+        tmp, tp = _arena(dev, [("qkv", M * W * _F16), ("o", M * H * _F16),
+                               ("act", M * I * _F16),
+                               ("down_part", p_down * M * H * _F32 if p_down > 1 else 0)])
+        s2 = torch.empty((M, H), dtype=torch.float32, device=dev)
+        d = torch.empty((M, H), dtype=torch.float16, device=dev)
+        t = _blas._table
+        args = LayerFwd(
+            s_in.data_ptr(), _ext.ptr(delta),
+            t.get(("tn", W, M, H, H, H, W, bias is not None), -1),
+            t.get(("tn", H, M, NQ, NQ, NQ, H, False), -1),
+            t.get(("tn", 2 * I, M, H, H, H, 2 * I, False), -1),
+            t.get(("tn", H, M, I, I, I, H, False), -1),
+            kp["s1"], kp["y"], kp["rstd1"], kp["t"], kp["qkv_r"], kp["attn"], kp["lse"],
+            s2.data_ptr(), kp["y2"], kp["rstd2"], kp["gu"], tp["qkv"], tp["o"], tp["act"],
+            tp["down_part"], d.data_ptr())
+        _ext.call("soupk_layer_fwd", ctypes.addressof(dims), ctypes.addressof(args), st)
+        del tmp
+        ctx.save_for_backward(s_in, s2)
+        ctx.keep, ctx.kp = keep, kp
+        # what the backward reads besides: the weights, LoRA parameters and tables (inputs)
+        ctx.inputs = (w_qkv, w_o, w_gu, w_d, staged, cos32, sin32, pos, cu, norm1, norm2, bias,
+                      a_q, a_v, b_q, b_v)
+        ctx.dims = dims
+        ctx.has_delta = has_delta
+        ctx.consumed = False
+        return s2, d
+
+    @staticmethod
+    def backward(ctx, g_s, g_d):
+        if ctx.consumed:
+            raise RuntimeError("NativeDecoderLayer: backward ran twice through a graph whose kept "
+                               "gate/up buffer the first backward overwrote; set "
+                               "mlp.RECOMPUTE_GATE_UP = True to backpropagate twice")
+        ctx.consumed = True
+        s_in, s2 = ctx.saved_tensors
+        dims, kp, keep = ctx.dims, ctx.kp, ctx.keep
+        dev = s_in.device
+        M, H, NH, NKV, I, r = dims.M, dims.H, dims.NH, dims.NKV, dims.I, dims.r
+        NQ, NV = NH * 128, NKV * 128
+        W = NQ + 2 * NV
+        p_gu = dims.p_gu
+        g_s = g_s.to(torch.float32).contiguous()
+        g_d = g_d.to(torch.float16).contiguous()
+        slices = (M + 127) // 128
+        lora_ws_floats = max(slices * (2 * r * H + r * (NQ + NV)), 4)
+        n_delta = (M * NH + 3) // 4 * 4
+        scratch, sp = _arena(dev, [
+            ("dact", M * I * _F16), ("gu_part", p_gu * M * H * _F32 if p_gu > 1 else 0),
+            ("g_y2", M * H * _F16), ("g_s1", M * H * _F32), ("g_o", M * H * _F16),
+            ("g_a", M * NQ * _F16), ("attn_ws", (n_delta + 2 * M * NQ) * _F32),
+            ("dqkv", M * W * _F16), ("dt", M * 2 * r * _F16), ("dy", M * H * _F16),
+            ("lora_ws", lora_ws_floats * _F32)])
+        g_s_in = torch.empty((M, H), dtype=torch.float32, device=dev)
+        g_delta = torch.empty((M, H), dtype=torch.float16, device=dev) if ctx.has_delta else None
+        d_aq = torch.empty((r, H), dtype=torch.float32, device=dev)
+        d_av = torch.empty((r, H), dtype=torch.float32, device=dev)
+        d_bq = torch.empty((NQ, r), dtype=torch.float32, device=dev)
+        d_bv = torch.empty((NV, r), dtype=torch.float32, device=dev)
+        t = _blas._table
+        args = LayerBwd(
+            s_in.data_ptr(), kp["s1"], kp["rstd1"], kp["y"], kp["t"], kp["qkv_r"], kp["attn"],
+            kp["lse"], s2.data_ptr(), kp["rstd2"], kp["y2"], kp["gu"], int(ctx.has_delta),
+            t.get(("nn", I, M, H, I, H, I, False), -1),
+            t.get(("nn", H, M, 2 * I, H, 2 * I, H, False), -1),
+            t.get(("nn", NQ, M, H, NQ, H, NQ, False), -1),
+            t.get(("nn", H, M, W, H, W, H, False), -1),
+            g_s.data_ptr(), g_d.data_ptr(), sp["dact"], sp["gu_part"], sp["g_y2"], sp["g_s1"],
+            sp["g_o"], sp["g_a"], sp["attn_ws"], sp["dqkv"], sp["dt"], sp["dy"], sp["lora_ws"],
+            lora_ws_floats, g_s_in.data_ptr(), _ext.ptr(g_delta), d_aq.data_ptr(),
+            d_av.data_ptr(), d_bq.data_ptr(), d_bv.data_ptr())
+        _ext.call("soupk_layer_bwd", ctypes.addressof(dims), ctypes.addressof(args),
+                  _ext.stream_of(g_s_in))
+        if not ctx.has_delta:
+            # s_in is also the residual: its gradient adds the residual's (two terms, so the
+            # order the engine would sum them in does not matter)
+            g_s_in.add_(_view_f32(scratch, sp["g_s1"], M, H))
+        ctx.keep = ctx.kp = ctx.inputs = None
+        del keep, scratch
+        return (g_s_in, g_delta, d_aq, d_bq, d_av, d_bv) + (None,) * 13
+
+
+def _view_f32(buf, addr, rows, cols):
+    """The fp32 [rows, cols] tensor at device address `addr` inside the uint8 arena `buf`."""
+    off = addr - buf.data_ptr()
+    return buf[off:off + rows * cols * _F32].view(torch.float32).view(rows, cols)

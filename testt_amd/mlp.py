@@ -6,7 +6,8 @@ Drop-in for solution/mlp.py.
   (computed in fp32, rounded once to fp16 where the down projection reads it);
 - backward turns the incoming gradient into the gate/up gradients in place, in the [tokens, 2I]
   gate/up buffer, so the input gradient is again a single product (split along K over
-  batched GEMMs with fp32 partials, SPLIT_K_GATE_UP, and summed by a HIP kernel).
+  batched GEMMs with fp32 partials, summed by a HIP kernel; split_parts, as the down
+  projection's forward).
 
 RECOMPUTE_GATE_UP (solution/mlp.py:27) chooses where that buffer comes from.  The reference
 recomputes it in backward (one more [tokens, H] x [H, 2I] GEMM) to keep nothing of size
@@ -28,10 +29,32 @@ from .nf4 import keep_for_backward, unpack_concat
 RECOMPUTE_GATE_UP = False  # True: keep only the [tokens, H] input, recompute gate/up
 
 # Split of the gate|up input-gradient GEMM (d(gate|up) [tokens, 2I] @ [W_gate; W_up] [2I, H])
-# along K into this many batched hipBLASLt GEMMs with fp32 outputs, summed in order and rounded
-# once to fp16 by soupk_sum_partials.  The [tokens, H] output of the 2048-token step is 192
-# tiles of 128 x 128 for 256 CUs; four K slices make 768.  1 = one fp16 GEMM (the reference's).
-SPLIT_K_GATE_UP = 4
+# along K into batched hipBLASLt GEMMs with fp32 outputs, summed in order and rounded once to
+# fp16 by soupk_sum_partials, and of the down projection's forward (act [tokens, I] @ W_down^T)
+# the same way: both contract deep (17,920 / 8,960) into a [tokens, H] output of few tiles.
+# None: split_parts() picks the count by rows; an int forces it (1 = one fp16 GEMM, the
+# reference's).
+SPLIT_K_GATE_UP = None
+SPLIT_K_DOWN = None
+
+
+def split_parts(rows, out_cols, depth, kind):
+    """Slices of K for the split products, measured on MI355X (hipBLASLt's tuned or heuristic
+    solutions, 256 to 4096 rows at Qwen2.5-1.5B's shapes):
+    - the gate|up input gradient: the largest of 1, 2, 4, 8 that keeps the output's
+      256 x 256 tiles times the slices within 256 (8 up to 1024 rows: 888 rows 67.8 us against
+      88.3 with 4 and 202.3 unsplit; 4 at 2048 rows: 130.7 against 161.1 / 146.8 with 2 / 8);
+    - the down projection's forward: 2 up to 2048 rows (2048 rows 63.4 against 69.7 us
+      unsplit, 888 rows 38.7 against 43.7), one GEMM above (3072 rows 92.5 against 97.3)."""
+    if rows <= 0:
+        return 1
+    if kind == "gate_up":
+        tiles = -(-rows // 256) * -(-out_cols // 256)
+        parts = 1
+        while parts < 8 and tiles * parts * 2 <= 256 and depth % (parts * 2) == 0:
+            parts *= 2
+        return parts
+    return 2 if rows <= 2048 and depth % 2 == 0 else 1
 # Columns one workgroup step covers per row in the reference's tiling (solution/mlp.py:28);
 # the HIP kernels stream the flat [rows, I] space in 16-byte chunks instead.
 COLS_PER_PROGRAM = 1024
@@ -74,15 +97,18 @@ def _mm(a, b):
 
 def matmul_split_k(a, b, parts):
     """fp16 a [M, K] @ b [K, N] as `parts` GEMMs over equal slices of K (batched, fp32
-    outputs), summed in slice order and rounded once to fp16.  K % parts == 0; a and b must
-    have unit column stride."""
+    outputs), summed in slice order and rounded once to fp16.  K % parts == 0; a with unit
+    column stride, b with unit column stride or the transpose of such a matrix."""
     M, K = a.shape
     N = b.shape[1]
-    if K % parts or a.stride(1) != 1 or b.stride(1) != 1:
+    if K % parts or a.stride(1) != 1 or (b.stride(1) != 1 and b.stride(0) != 1):
         raise ValueError(f"matmul_split_k: K={K} must split into {parts} slices, unit strides")
+    out = _blas.split_k(a, b, parts)
+    if out is not None:
+        return out
     c = K // parts
     a3 = a.as_strided((parts, M, c), (c, a.stride(0), 1))
-    b3 = b.as_strided((parts, c, N), (c * b.stride(0), b.stride(0), 1))
+    b3 = b.as_strided((parts, c, N), (c * b.stride(0), b.stride(0), b.stride(1)))
     partial = _blas.bmm_f32(a3, b3)                                 # [parts, M, N] fp32
     out = torch.empty((M, N), dtype=torch.float16, device=a.device)
     if M * N:
@@ -105,7 +131,14 @@ class FusedNF4MLP(torch.autograd.Function):
         else:
             ctx.save_for_backward(x, gu)
         down = down16 if down16 is not None else unpack_concat((down_w,), x.device)
-        out = _mm(act, down.t())
+        parts = SPLIT_K_DOWN
+        if parts is None and act.dim() == 2:
+            parts = split_parts(act.shape[0], down.shape[0], act.shape[1], "down")
+        if parts and parts > 1 and act.dim() == 2 and act.shape[1] % parts == 0 and \
+                act.shape[0] > 0:
+            out = matmul_split_k(act, down.t(), parts)
+        else:
+            out = _mm(act, down.t())
         ctx.weights = (gate_w, up_w, down_w)
         keep_for_backward(ctx, (gate_up, down))
         return out
@@ -139,6 +172,8 @@ class FusedNF4MLP(torch.autograd.Function):
         gated_silu_backward_(dact, gu)
         del dact
         parts = SPLIT_K_GATE_UP
+        if parts is None:
+            parts = split_parts(gu.shape[0], gate_up.shape[1], gu.shape[1], "gate_up")
         if parts > 1 and gu.shape[1] % parts == 0 and gu.shape[0] > 0:
             grad_x = matmul_split_k(gu, gate_up, parts)
         else:
