@@ -186,8 +186,11 @@ class NativeDecoderLayer(torch.autograd.Function):
             sp["g_o"], sp["g_a"], sp["attn_ws"], sp["dqkv"], sp["dt"], sp["dy"], sp["lora_ws"],
             lora_ws_floats, g_s_in.data_ptr(), _ext.ptr(g_delta), d_aq.data_ptr(),
             d_av.data_ptr(), d_bq.data_ptr(), d_bv.data_ptr())
-        _ext.call("soupk_layer_bwd", ctypes.addressof(dims), ctypes.addressof(args),
-                  _ext.stream_of(g_s_in))
+        st = _ext.stream_of(g_s_in)
+        # the hipBLASLt workspace of the stream the backward runs on (GEMMs of one stream run in
+        # order; another stream's may be in use)
+        dims.gemm_ws = _blas._ws(dev, st).data_ptr()
+        _ext.call("soupk_layer_bwd", ctypes.addressof(dims), ctypes.addressof(args), st)
         if not ctx.has_delta:
             # s_in is also the residual: its gradient adds the residual's (two terms, so the
             # order the engine would sum them in does not matter)
