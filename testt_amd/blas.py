@@ -30,7 +30,6 @@ WORKSPACE_BYTES = 64 << 20
 USE_GEMM_LT = True
 
 _lock = threading.Lock()
-_workspace = {}    # (device index, stream) -> uint8 tensor: GEMMs of one stream run in order
 _table = {}        # ("tn" | "nn", m, n, k, lda, ldb, ldd, bias) -> hipBLASLt solution index
 
 
@@ -65,16 +64,11 @@ def clear_table():
         _table.clear()
 
 
-def _ws(device, stream):
-    key = (device.index, stream)
-    ws = _workspace.get(key)
-    if ws is None:
-        with _lock:
-            ws = _workspace.get(key)
-            if ws is None:
-                ws = _workspace[key] = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8,
-                                                   device=device)
-    return ws
+def _ws(device):
+    """hipBLASLt's workspace for one call, from torch's caching allocator on the current stream
+    (about 1 us: a cached block; freed when the caller drops it, and reused only in that
+    stream's order, so that no two streams' GEMMs share it)."""
+    return torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
 
 
 def _aligned(*ts):
@@ -122,7 +116,7 @@ def matmul(a, b, bias=None, out=None, accumulate=False):
         return _torch_matmul(a, b, bias, out, accumulate)
     key = ("tn" if ta else "nn", N, M, K, lda, ldb, ldd, bias is not None)
     st = _ext.stream_of(a)
-    ws = _ws(a.device, st)
+    ws = _ws(a.device)
     _ext.call("soupk_gemm_lt", ta, 0, N, M, K, b.data_ptr(), lda, 0, a.data_ptr(), ldb, 0,
               out.data_ptr(), ldd, 0, 0, 1, 1 if accumulate else 0, _ext.ptr(bias),
               _table.get(key, -1), ws.data_ptr(), WORKSPACE_BYTES, st)
@@ -154,7 +148,7 @@ def bmm_f32(a3, b3):
     if M == 0 or N == 0:
         return out
     st = _ext.stream_of(a3)
-    ws = _ws(a3.device, st)
+    ws = _ws(a3.device)
     # column-major per problem: out_p^T [N, M] = op(b3_p^T) [N, K] @ a3_p^T [K, M]
     _ext.call("soupk_gemm_lt", 0 if b_rows else 1, 0, N, M, K, b3.data_ptr(), ld_b,
               b3.stride(0), a3.data_ptr(), a3.stride(1), a3.stride(0), out.data_ptr(), N, M * N,
@@ -184,7 +178,7 @@ def split_k(a, b, parts):
     if not _aligned(a, b) or (a.stride(0) | ld_b | c) % 8:
         return None
     st = _ext.stream_of(a)
-    ws = _ws(a.device, st)
+    ws = _ws(a.device)
     part = torch.empty((parts, M, N), dtype=torch.float32, device=a.device)
     out = torch.empty((M, N), dtype=torch.float16, device=a.device)
     _ext.call("soupk_gemm_lt", ta, 0, N, M, c, b.data_ptr(), ld_b, c * b.stride(0), a.data_ptr(),

@@ -37,6 +37,7 @@ struct LtPlan {
   int index = -1;
 };
 
+constexpr size_t kMaxPlans = 4096;            // problems kept (all dropped when full)
 std::mutex g_mu;                              // guards the maps and a plan's bias attribute
 std::map<int, hipblasLtHandle_t> g_handles;   // per device
 std::map<PlanKey, LtPlan> g_plans;
@@ -156,6 +157,11 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_lt(
                     d_f32,    batch,   bias != nullptr, accumulate, workspace_bytes, algo_index};
   auto it = g_plans.find(key);
   if (it == g_plans.end()) {
+    // a bounded cache: a training run whose batches vary in tokens meets a new M each step
+    if (g_plans.size() >= kMaxPlans) {
+      for (auto& kv : g_plans) destroy(kv.second);
+      g_plans.clear();
+    }
     LtPlan p;
     const int rc = build_plan(h, trans_a, trans_b, m, n, k, lda, stride_a, ldb, stride_b, ldd,
                               stride_d, d_f32, batch, bias != nullptr, accumulate, algo_index,

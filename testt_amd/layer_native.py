@@ -102,7 +102,7 @@ class NativeDecoderLayer(torch.autograd.Function):
         if (2 * I) % p_gu:
             p_gu = 1
         st = _ext.stream_of(s_in)
-        ws = _blas._ws(dev, st)
+        ws = _blas._ws(dev)
         norm1, norm2 = _weight32(w.input_norm, H, dev), _weight32(w.post_norm, H, dev)
         bias = w.qkv_bias
         dims = LayerDims(M, H, NH, NKV, D, I, r, batch, seq, p_down, p_gu, float(w.eps),
@@ -132,7 +132,7 @@ class NativeDecoderLayer(torch.autograd.Function):
             s2.data_ptr(), kp["y2"], kp["rstd2"], kp["gu"], tp["qkv"], tp["o"], tp["act"],
             tp["down_part"], d.data_ptr())
         _ext.call("soupk_layer_fwd", ctypes.addressof(dims), ctypes.addressof(args), st)
-        del tmp
+        del tmp, ws
         ctx.save_for_backward(s_in, s2)
         ctx.keep, ctx.kp = keep, kp
         # what the backward reads besides: the weights, LoRA parameters and tables (inputs)
@@ -187,10 +187,10 @@ class NativeDecoderLayer(torch.autograd.Function):
             lora_ws_floats, g_s_in.data_ptr(), _ext.ptr(g_delta), d_aq.data_ptr(),
             d_av.data_ptr(), d_bq.data_ptr(), d_bv.data_ptr())
         st = _ext.stream_of(g_s_in)
-        # the hipBLASLt workspace of the stream the backward runs on (GEMMs of one stream run in
-        # order; another stream's may be in use)
-        dims.gemm_ws = _blas._ws(dev, st).data_ptr()
+        ws = _blas._ws(dev)           # a workspace of the stream the backward runs on
+        dims.gemm_ws = ws.data_ptr()
         _ext.call("soupk_layer_bwd", ctypes.addressof(dims), ctypes.addressof(args), st)
+        del ws
         if not ctx.has_delta:
             # s_in is also the residual: its gradient adds the residual's (two terms, so the
             # order the engine would sum them in does not matter)
