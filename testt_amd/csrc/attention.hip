@@ -504,16 +504,21 @@ __device__ __forceinline__ bool rope_rows(const AttnParams& p, int64_t tok, cons
 // The transposed rotation of RoPE's backward (solution/rope.py:78-128) on fp16-rounded
 // gradients g1 (dims d..d+3 of the first half) and g2 (the same dims of the second half):
 // (g1*c1 + g2*s2, g2*c2 - g1*s1), each product rounded.
-__device__ __forceinline__ void rope_bwd4(const float* c, const float* sn, int d, const f4& g1,
-                                          const f4& g2, f4& o1, f4& o2) {
-  const f4 c1 = *reinterpret_cast<const f4*>(c + d), c2 = *reinterpret_cast<const f4*>(c + d + 64);
-  const f4 s1 = *reinterpret_cast<const f4*>(sn + d);
-  const f4 s2 = *reinterpret_cast<const f4*>(sn + d + 64);
+__device__ __forceinline__ void rope_bwd4(const f4& c1, const f4& c2, const f4& s1, const f4& s2,
+                                          const f4& g1, const f4& g2, f4& o1, f4& o2) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     o1[i] = g1[i] * c1[i] + g2[i] * s2[i];
     o2[i] = g2[i] * c2[i] - g1[i] * s1[i];
   }
+}
+
+__device__ __forceinline__ void rope_bwd4(const float* c, const float* sn, int d, const f4& g1,
+                                          const f4& g2, f4& o1, f4& o2) {
+  const f4 c1 = *reinterpret_cast<const f4*>(c + d), c2 = *reinterpret_cast<const f4*>(c + d + 64);
+  const f4 s1 = *reinterpret_cast<const f4*>(sn + d);
+  const f4 s2 = *reinterpret_cast<const f4*>(sn + d + 64);
+  rope_bwd4(c1, c2, s1, s2, g1, g2, o1, o2);
 }
 
 template <bool VARLEN>
@@ -791,6 +796,10 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
   reinterpret_cast<u32x2*>(dv)[i] = u32x2{pack_h2(sv[0], sv[1]), pack_h2(sv[2], sv[3])};
 }
 
+// Query heads per key/value head whose partials the reduce kernels load all at once (more take
+// a loop that waits on each head's loads in turn).
+constexpr int kMaxRep = 8;
+
 // The varlen form of the reduce: item (token, key/value head g, 4-dim slice j of the first half)
 // sums dims 4j..4j+3 and 4j+64..+67 of the dK and dV partials of the group's query heads (head
 // order, as above), rounds to fp16 and writes them into the token's dq|dk|dv row, dK rotated
@@ -805,27 +814,63 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_varlen_kernel(AttnParams 
   const int g = static_cast<int>(tg - tok * p.NKV);
   const int rep = p.NH / p.NKV;
   const int d = 4 * j;
+  // The table rows first, so that the position load and then the rows' go out beside the
+  // partials' instead of after their sums (a token without a row reads row 0 and discards it).
+  const float* c = p.cos;
+  const float* sn = p.sin;
+  const bool rope = p.cos != nullptr;
+  const bool rope_row = rope && rope_rows(p, tok, &c, &sn);
+  f4 c1 = {0.f, 0.f, 0.f, 0.f}, c2 = c1, s1 = c1, s2 = c1;
+  if (rope) {
+    c1 = *reinterpret_cast<const f4*>(c + d);
+    c2 = *reinterpret_cast<const f4*>(c + d + 64);
+    s1 = *reinterpret_cast<const f4*>(sn + d);
+    s2 = *reinterpret_cast<const f4*>(sn + d + 64);
+  }
   f4 k1 = {0.f, 0.f, 0.f, 0.f}, k2 = k1, v1 = k1, v2 = k1;
-  for (int r = 0; r < rep; ++r) {
-    const int64_t row = (static_cast<int64_t>(g * rep + r) * p.M + tok) * kD;
-    k1 = k1 + *reinterpret_cast<const f4*>(p.dk_part + row + d);
-    k2 = k2 + *reinterpret_cast<const f4*>(p.dk_part + row + d + 64);
-    v1 = v1 + *reinterpret_cast<const f4*>(p.dv_part + row + d);
-    v2 = v2 + *reinterpret_cast<const f4*>(p.dv_part + row + d + 64);
+  if (rep <= kMaxRep) {
+    // every partial's loads issued before the first add (a loop of loads and adds waited on
+    // memory once per query head), unconditionally at a clamped head (loads under a test
+    // were issued one test at a time), the adds then in head order as in the loop
+    f4 a[kMaxRep][4];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      const int rr = r < rep ? r : rep - 1;
+      const int64_t row = (static_cast<int64_t>(g * rep + rr) * p.M + tok) * kD;
+      a[r][0] = *reinterpret_cast<const f4*>(p.dk_part + row + d);
+      a[r][1] = *reinterpret_cast<const f4*>(p.dk_part + row + d + 64);
+      a[r][2] = *reinterpret_cast<const f4*>(p.dv_part + row + d);
+      a[r][3] = *reinterpret_cast<const f4*>(p.dv_part + row + d + 64);
+    }
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r < rep) {
+        k1 = k1 + a[r][0];
+        k2 = k2 + a[r][1];
+        v1 = v1 + a[r][2];
+        v2 = v2 + a[r][3];
+      }
+    }
+  } else {
+    for (int r = 0; r < rep; ++r) {
+      const int64_t row = (static_cast<int64_t>(g * rep + r) * p.M + tok) * kD;
+      k1 = k1 + *reinterpret_cast<const f4*>(p.dk_part + row + d);
+      k2 = k2 + *reinterpret_cast<const f4*>(p.dk_part + row + d + 64);
+      v1 = v1 + *reinterpret_cast<const f4*>(p.dv_part + row + d);
+      v2 = v2 + *reinterpret_cast<const f4*>(p.dv_part + row + d + 64);
+    }
   }
   uint16_t* krow = p.dq + tok * p.W + (p.NH + g) * kD;
   uint16_t* vrow = p.dq + tok * p.W + (p.NH + p.NKV + g) * kD;
-  if (p.cos != nullptr) {
-    const float* c = nullptr;
-    const float* sn = nullptr;
-    if (rope_rows(p, tok, &c, &sn)) {
+  if (rope) {
+    if (rope_row) {
       f4 g1, g2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         g1[i] = round_h(k1[i]);
         g2[i] = round_h(k2[i]);
       }
-      rope_bwd4(c, sn, d, g1, g2, k1, k2);
+      rope_bwd4(c1, c2, s1, s2, g1, g2, k1, k2);
     } else {
       k1 = k2 = f4{0.f, 0.f, 0.f, 0.f};   // no table row: no gradient reaches the input
     }
