@@ -542,7 +542,8 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
 //   0: 128 x 128, 2 x 2 waves of 64 x 64      1: 128 x 128, 4 x 2 waves of 32 x 64
 //   2: 128 x 128, 2 x 4 waves of 64 x 32      3: 128 x 64, 2 x 2 waves of 64 x 32
 //   4: 64 x 128, 2 x 2 waves of 32 x 64       5: 256 x 128, 4 x 2 waves of 64 x 64
-//   6: as 1 with K tiles of 128
+//   6: as 1 with K tiles of 128               7: 256 x 256, 2 x 4 waves of 128 x 64
+//   8: 256 x 256, 4 x 2 waves of 64 x 128     9: 256 x 128, 2 x 2 waves of 128 x 64
 #ifndef SOUPK_GEMM_SHAPE
 #define SOUPK_GEMM_SHAPE 1
 #endif
@@ -558,6 +559,12 @@ using Shape = GemmShape<128, 64, 2, 2>;
 using Shape = GemmShape<64, 128, 2, 2>;
 #elif SOUPK_GEMM_SHAPE == 5
 using Shape = GemmShape<256, 128, 4, 2>;
+#elif SOUPK_GEMM_SHAPE == 7
+using Shape = GemmShape<256, 256, 2, 4>;
+#elif SOUPK_GEMM_SHAPE == 8
+using Shape = GemmShape<256, 256, 4, 2>;
+#elif SOUPK_GEMM_SHAPE == 9
+using Shape = GemmShape<256, 128, 2, 2>;
 #else
 using Shape = GemmShape<128, 128, 4, 2, 128>;
 #endif
