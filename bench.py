@@ -881,6 +881,36 @@ def time_nf4_gemm(dev, calls=40):
 
 SWEEP_ROWS = (16, 64, 256, 512, 1024)   # row counts of the fused NF4 GEMM sweep
 
+# token counts (B=4 rows of T=512) of the NF4-resident layer comparison
+RESIDENT_LENGTHS = ((16, 0, 0, 0), (64, 0, 0, 0), (32, 32, 32, 32))
+
+
+def time_nf4_resident(dev, steps=40, warmup=5):
+    """The decoder layer at few tokens with its products on the NF4 weights (the fused
+    NF4-dequant GEMM in each direction, no fp16 weight in memory:
+    layer.NF4_RESIDENT_SMALL_BATCHES) against the same layer unpacking its seven projections
+    in one launch for hipBLASLt: forward+backward per step, the eager loop's median step
+    (time_layer) and a captured HIP graph's replay (graph_layer, the GPU time)."""
+    from testt_amd import layer
+
+    out = {}
+    saved = layer.NF4_RESIDENT_SMALL_BATCHES
+    try:
+        for lengths in RESIDENT_LENGTHS:
+            row = {"lengths": list(lengths)}
+            for resident in (True, False):
+                layer.NF4_RESIDENT_SMALL_BATCHES = resident
+                tag = "nf4" if resident else "unpacked"
+                log(f"layer at {sum(lengths)} tokens, {tag} weights")
+                t = time_layer(dev, steps, warmup, lengths=lengths)
+                row[f"{tag}_eager_fwd_bwd_median_us"] = t["fwd_bwd_us_median"]
+                row[f"{tag}_graph_fwd_bwd_us"] = graph_layer(dev, steps, lengths)[
+                    "graph_fwd_bwd_us"]
+            out[str(sum(lengths))] = row
+    finally:
+        layer.NF4_RESIDENT_SMALL_BATCHES = saved
+    return out
+
 
 def time_step(dev, steps, warmup, n_layers=28, reference_profile=False):
     """One QLoRA training step of the whole Qwen2.5-1.5B-shaped model at B=4 x T=512 = 2048
@@ -1592,6 +1622,9 @@ def main():
     ap.add_argument("--nf4-gemm", action="store_true",
                     help="time the fused NF4-dequant GEMM against hipBLASLt and unpack + "
                          "hipBLASLt at M = 2048, print one JSON line and exit")
+    ap.add_argument("--nf4-resident", action="store_true",
+                    help="time the decoder layer at few tokens on its NF4 weights (the fused "
+                         "NF4-dequant GEMM) against unpacked weights + hipBLASLt, then exit")
     ap.add_argument("--summarize-nf4-gemm", nargs=3, metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
                     help="print the fused NF4 GEMM tables of a rocprofv3 --kernel-trace run of "
                          "bench.py --nf4-gemm and exit (CPU)")
@@ -1657,6 +1690,10 @@ def main():
                                                       varlen_only=True),
                           "timing": "GPU time per call: calls queued behind a device-side "
                                     "wait and timed as one span"}), flush=True)
+        return
+    if args.nf4_resident:
+        print(json.dumps({"nf4_resident_layer": time_nf4_resident(dev),
+                          "gemm_selection": gemm_table}), flush=True)
         return
     if args.nf4_gemm:
         print(json.dumps({"nf4_gemm": time_nf4_gemm(dev), "gemm_selection": gemm_table,

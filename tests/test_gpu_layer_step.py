@@ -12,7 +12,7 @@ import torch
 
 from oracle.nf4 import dequant_state
 from oracle.rope import apply_rotary
-from testt_amd import layer, layer_native, nf4, workloads
+from testt_amd import layer, layer_native, mlp, nf4, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -237,6 +237,9 @@ def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
     gradients, bit for bit, and the same parameter gradients after two steps accumulate; also
     for the first layer, whose input norm has no residual delta."""
     batch, seq = 2, 64
+    # the one-node forms take the unpacked weights; at this token count the layer would run on
+    # its NF4 weights (test_nf4_resident_layer)
+    monkeypatch.setattr(layer, "NF4_RESIDENT_SMALL_BATCHES", False)
     w = layer.synthetic_layer(DEV, seed=12)
     amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
     for b, n in enumerate(lengths):
@@ -272,3 +275,64 @@ def test_one_node_layer_is_bit_identical(monkeypatch, lengths, with_delta):
     for ref in runs[1:]:
         for name, a, b in zip(names, runs[0], ref):
             assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("lengths", [(64, 37), (16, 0)])
+def test_nf4_resident_layer(monkeypatch, lengths):
+    """At few tokens the layer runs its products on the NF4 weights (the fused NF4-dequant GEMM
+    forward and input gradient, layer.NF4_RESIDENT_SMALL_BATCHES): no unpack in the forward or
+    the backward, and outputs and gradients within fp16 rounding of the same layer on unpacked
+    weights (the fused kernels sum in another order than hipBLASLt, and the q|k|v input
+    gradient is added to the LoRA part after its own rounding).  The fp32 comparison of
+    test_decoder_layer_matches_fp32_eager covers this path too (104 tokens)."""
+    print(f"nf4-resident layer lengths={lengths}", flush=True)
+    batch, seq = len(lengths), 64
+    w = layer.synthetic_layer(DEV, seed=14)
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(8)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    calls = []
+
+    def counting(mod, name):
+        real = getattr(mod, name)
+
+        def wrapped(*a, **k):
+            calls.append(name)
+            return real(*a, **k)
+        monkeypatch.setattr(mod, name, wrapped)
+
+    for mod, name in ((nf4, "unpack_concat"), (mlp, "unpack_concat"), (layer, "unpack_concat"),
+                      (layer, "unpack_groups"), (layer, "unpack_groups_lora")):
+        counting(mod, name)
+    assert layer.nf4_resident(m, ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,)),
+                              s0.device)
+    runs = []
+    for resident in (True, False):
+        monkeypatch.setattr(layer, "NF4_RESIDENT_SMALL_BATCHES", resident)
+        calls.clear()
+        s_in = s0.clone().requires_grad_(True)
+        d_in = d0.clone().requires_grad_(True)
+        s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                                   layer.key_valid_of(amask))
+        torch.autograd.backward([s, d], [gs, gd])
+        torch.cuda.synchronize()
+        if resident:
+            assert calls == [], calls
+        else:
+            assert calls, "the unpacked run unpacks"
+        runs.append([s.detach(), d.detach(), s_in.grad, d_in.grad] +
+                    [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+    for name, a, b in zip(("s", "d", "d s_in", "d delta", "d A_q", "d B_q", "d A_v", "d B_v"),
+                          *runs):
+        assert torch.isfinite(a.float()).all(), name
+        assert rel_err(a, b) < 5e-3, (name, rel_err(a, b))

@@ -4,7 +4,9 @@ Mirrors the per-layer body of the reference's fused_forward (solution/model.py:2
 real (non-pad) tokens:
 
   s, y, y_pad = add_rmsnorm(s, d)               residual add + input RMSNorm (HIP)
-  (all seven NF4 projections unpacked by one HIP launch: UNPACK_PER_LAYER)
+  (all seven NF4 projections unpacked by one HIP launch: UNPACK_PER_LAYER; with few tokens
+   the products read the NF4 weights through the fused NF4-dequant GEMM instead:
+   NF4_RESIDENT_SMALL_BATCHES)
   qkv        = y @ [Wq;Wk;Wv]^T + b               one hipBLASLt GEMM
   lq, lv     = B(A(dropout(y_pad))) * scaling     LoRA on q/v (HIP, or fp16 GEMMs with dropout)
   a          = rope_attention(qkv, lq, lv)        LoRA add + RoPE into token-major rows, then
@@ -38,7 +40,8 @@ from . import layer_native as _native
 from . import lora as _lora
 from . import workloads
 from .mlp import FusedNF4MLP, fused_mlp
-from .nf4 import (FrozenNF4Linear, frozen_linear, keep_for_backward, unpack_concat, unpack_groups,
+from .nf4 import (FrozenNF4Linear, frozen_linear, fused_grad_input, fused_linear,
+                  keep_for_backward, unpack_concat, unpack_groups,
                   unpack_groups_lora, unpacked_for_backward)
 from .rmsnorm import AddRMSNorm, RMSNormNoAdd, add_rmsnorm
 from .rope import rope_pack
@@ -110,6 +113,51 @@ USE_VARLEN_ATTENTION = True
 # values are the same; the whole buffer lives until the last stack is released (the backward
 # of q|k|v when the weights are kept for backward, the end of the layer's forward otherwise).
 UNPACK_PER_LAYER = True
+# A layer whose token count is small enough that each of its products takes the fused
+# NF4-dequant GEMM, forward and input gradient (nf4_gemm's measured window: up to 128 rows at
+# Qwen2.5-1.5B's shapes on MI355X), skips that unpack and runs on the NF4 weights: no fp16 copy
+# of the layer's weights (94 MB in Qwen2.5-1.5B) is written or read.  Measured (bench.py
+# --nf4-resident, forward + backward): 186 / 203 / 216 us of GPU time at 16 / 64 / 128 tokens
+# against 231 / 217 / 232 us unpacked, but through the per-operation Python nodes, whose host
+# time (~530 us) exceeds the layer issued from C on unpacked weights (~360 us, itself
+# host-bound at these sizes); off until the C-issued layer takes NF4 weights.
+NF4_RESIDENT_SMALL_BATCHES = False
+
+
+def nf4_resident(tokens, groups, device):
+    """True when a layer of `tokens` rows runs on its NF4 weights (NF4_RESIDENT_SMALL_BATCHES)."""
+    from . import nf4, nf4_gemm
+
+    return (tokens > 0 and nf4.USE_FUSED_NF4_GEMM and
+            nf4_gemm.prefers_fused_all(tokens, groups, device))
+
+
+def _qkv_forward(ctx, y16, weights, w16, bias):
+    """y16 @ [Wq;Wk;Wv]^T + b: without the caller's unpacked stack `w16`, the fused NF4-dequant
+    GEMM where it is the faster path (few rows); else hipBLASLt on the unpacked stack, which is
+    kept for backward (nf4.KEEP_UNPACKED_FOR_BACKWARD)."""
+    qkv = fused_linear(y16, weights, bias) if w16 is None else None
+    if qkv is not None:
+        ctx.unpacked = None
+        return qkv
+    w = w16 if w16 is not None else unpack_concat(weights, y16.device)
+    qkv = _blas.linear(y16, w, bias)
+    keep_for_backward(ctx, w)
+    return qkv
+
+
+def _add_qkv_input_grad(ctx, g_qkv, dy):
+    """dy += g_qkv @ [Wq;Wk;Wv] (fp16): one accumulating hipBLASLt GEMM on the kept or
+    re-unpacked stack, or, where no stack was kept and it is the faster path, the fused NF4
+    input gradient added to dy (rounded twice: the product, then the sum)."""
+    g = g_qkv.to(torch.float16)
+    dx = fused_grad_input(g, ctx.weights) if getattr(ctx, "unpacked", None) is None else None
+    if dx is not None:
+        dy += dx
+        return dy
+    w = unpacked_for_backward(ctx, ctx.weights, dy.device)
+    _blas.matmul(g, w, out=dy, accumulate=True)
+    return dy
 
 
 class QKVLora(torch.autograd.Function):
@@ -121,10 +169,7 @@ class QKVLora(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16=None, staged=None):
-        w = w16 if w16 is not None else unpack_concat(weights, y16.device)
-        qkv = _blas.linear(y16, w, bias)
-        keep_for_backward(ctx, w)
-        del w
+        qkv = _qkv_forward(ctx, y16, weights, w16, bias)
         ctx.weights, ctx.scaling = weights, scaling
         params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
         ctx.fused = USE_FUSED_LORA and _lora.supported(y16, *params)
@@ -170,8 +215,7 @@ class QKVLora(torch.autograd.Function):
         grads[0], grads[2] = da[:r], da[r:]
         dy = dt @ a16
         if g_qkv is not None:
-            w = unpacked_for_backward(ctx, ctx.weights, y16.device)
-            _blas.matmul(g_qkv.to(torch.float16), w, out=dy, accumulate=True)
+            _add_qkv_input_grad(ctx, g_qkv, dy)
         return dy, None, grads[0], grads[1], grads[2], grads[3], None, None, None, None
 
     @staticmethod
@@ -184,8 +228,7 @@ class QKVLora(torch.autograd.Function):
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
         d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
         if g_qkv is not None:
-            w = unpacked_for_backward(ctx, ctx.weights, y16.device)
-            _blas.matmul(g_qkv.to(torch.float16), w, out=dy, accumulate=True)
+            _add_qkv_input_grad(ctx, g_qkv, dy)
         return dy, None, d_aq, d_bq, d_av, d_bv, None, None, None, None
 
 
@@ -208,10 +251,7 @@ class QKVLoraRopeAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, y16, bias, a_q, b_q, a_v, b_v, scaling, weights, w16, staged, cos, sin,
                 pos_idx, cu_seqlens, batch, seq, n_heads, n_kv, scale):
-        w = w16 if w16 is not None else unpack_concat(weights, y16.device)
-        qkv = _blas.linear(y16, w, bias)
-        keep_for_backward(ctx, w)
-        del w
+        qkv = _qkv_forward(ctx, y16, weights, w16, bias)
         params = (a_q.detach(), a_v.detach(), b_q.detach(), b_v.detach())
         if staged is None:
             staged = _lora.stage(*params)
@@ -241,8 +281,7 @@ class QKVLoraRopeAttention(torch.autograd.Function):
         dt, dy = _lora.lora_bwd_rows(g_lq, g_lv, a_q, a_v, b_q, b_v, ctx.scaling, staged=staged)
         # fp16 products cast to the fp32 parameters, as autocast's backward gives them
         d_aq, d_av, d_bq, d_bv = _lora.lora_bwd_params(y16, t, dt, g_lq, g_lv, ctx.scaling)
-        w = unpacked_for_backward(ctx, ctx.weights, dev)
-        _blas.matmul(dqkv, w, out=dy, accumulate=True)
+        _add_qkv_input_grad(ctx, dqkv, dy)
         return (dy, None, d_aq, d_bq, d_av, d_bv) + (None,) * 13
 
 
@@ -412,8 +451,9 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     plain = lora_without_dropout(w)
     params = (w.lora_q[0], w.lora_v[0], w.lora_q[1], w.lora_v[1]) if plain else None
     w_qkv = w_o = w_gu = w_d = staged = None
-    if UNPACK_PER_LAYER:
-        groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
+    groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
+    if UNPACK_PER_LAYER and not (NF4_RESIDENT_SMALL_BATCHES and
+                                 nf4_resident(s.shape[0], groups, s.device)):
         if plain and USE_FUSED_LORA and _lora.params_supported(*params, s.device):
             # the LoRA parameters' fp16 staging rides on the same launch as the unpack
             (w_qkv, w_o, w_gu, w_d), staged = unpack_groups_lora(

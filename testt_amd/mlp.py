@@ -1,7 +1,9 @@
 """The Qwen2 MLP, down(silu(gate(x)) * up(x)), with frozen NF4 weights, as one autograd node.
 Drop-in for solution/mlp.py.
 
-- gate and up are one hipBLASLt GEMM against both weights unpacked into one [2I, H] buffer;
+- gate and up are one hipBLASLt GEMM against both weights unpacked into one [2I, H] buffer
+  (with few rows, where the fused NF4-dequant GEMM of testt_amd/nf4_gemm.py is the faster
+  path, each product runs on the NF4 weights instead: nf4.fused_linear / fused_grad_input);
 - testt_amd/csrc/swiglu.hip reads the fp16 [tokens, 2I] result and writes silu(g) * u in fp16
   (computed in fp32, rounded once to fp16 where the down projection reads it);
 - backward turns the incoming gradient into the gate/up gradients in place, in the [tokens, 2I]
@@ -24,7 +26,7 @@ import torch
 from . import _ext
 from . import blas as _blas
 from ._common import kernels_ok
-from .nf4 import keep_for_backward, unpack_concat
+from .nf4 import fused_grad_input, fused_linear, keep_for_backward, unpack_concat
 
 RECOMPUTE_GATE_UP = False  # True: keep only the [tokens, H] input, recompute gate/up
 
@@ -120,8 +122,15 @@ def matmul_split_k(a, b, parts):
 class FusedNF4MLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, gate_up16=None, down16=None):
-        gate_up = gate_up16 if gate_up16 is not None else unpack_concat((gate_w, up_w), x.device)
-        gu = _mm(x, gate_up.t())
+        # Without the caller's unpacked stacks, each product runs on the NF4 weights through
+        # the fused NF4-dequant GEMM where that is the faster path (nf4.fused_linear: few
+        # rows), else on W unpacked here.
+        gate_up = gate_up16
+        gu = fused_linear(x, (gate_w, up_w)) if gate_up is None and x.dim() == 2 else None
+        if gu is None:
+            if gate_up is None:
+                gate_up = unpack_concat((gate_w, up_w), x.device)
+            gu = _mm(x, gate_up.t())
         act = gated_silu(gu)
         ctx.recompute = RECOMPUTE_GATE_UP
         ctx.consumed = False
@@ -130,15 +139,19 @@ class FusedNF4MLP(torch.autograd.Function):
             ctx.save_for_backward(x)
         else:
             ctx.save_for_backward(x, gu)
-        down = down16 if down16 is not None else unpack_concat((down_w,), x.device)
-        parts = SPLIT_K_DOWN
-        if parts is None and act.dim() == 2:
-            parts = split_parts(act.shape[0], down.shape[0], act.shape[1], "down")
-        if parts and parts > 1 and act.dim() == 2 and act.shape[1] % parts == 0 and \
-                act.shape[0] > 0:
-            out = matmul_split_k(act, down.t(), parts)
-        else:
-            out = _mm(act, down.t())
+        down = down16
+        out = fused_linear(act, (down_w,)) if down is None and act.dim() == 2 else None
+        if out is None:
+            if down is None:
+                down = unpack_concat((down_w,), x.device)
+            parts = SPLIT_K_DOWN
+            if parts is None and act.dim() == 2:
+                parts = split_parts(act.shape[0], down.shape[0], act.shape[1], "down")
+            if parts and parts > 1 and act.dim() == 2 and act.shape[1] % parts == 0 and \
+                    act.shape[0] > 0:
+                out = matmul_split_k(act, down.t(), parts)
+            else:
+                out = _mm(act, down.t())
         ctx.weights = (gate_w, up_w, down_w)
         keep_for_backward(ctx, (gate_up, down))
         return out
@@ -154,14 +167,22 @@ class FusedNF4MLP(torch.autograd.Function):
         kept = getattr(ctx, "unpacked", None)
         ctx.unpacked = None
         gate_up, down = kept if kept is not None else (None, None)
+        # a stack the forward did not unpack: the fused input gradient where it is the faster
+        # path, else W unpacked here
+        dact = None
         if down is None:
-            down = unpack_concat((down_w,), grad_out.device)
-        dact = _mm(grad_out, down)
+            dact = fused_grad_input(grad_out, (down_w,)) if grad_out.dim() == 2 else None
+            if dact is None:
+                down = unpack_concat((down_w,), grad_out.device)
+        if dact is None:
+            dact = _mm(grad_out, down)
         del down
-        if gate_up is None:
-            gate_up = unpack_concat((gate_w, up_w), grad_out.device)
         if ctx.recompute:
-            gu = _mm(x, gate_up.t())
+            gu = fused_linear(x, (gate_w, up_w)) if gate_up is None else None
+            if gu is None:
+                if gate_up is None:
+                    gate_up = unpack_concat((gate_w, up_w), grad_out.device)
+                gu = _mm(x, gate_up.t())
         else:
             if ctx.consumed:
                 raise RuntimeError("FusedNF4MLP: backward ran twice through a graph whose kept "
@@ -171,13 +192,19 @@ class FusedNF4MLP(torch.autograd.Function):
             gu = saved[1]
         gated_silu_backward_(dact, gu)
         del dact
-        parts = SPLIT_K_GATE_UP
-        if parts is None:
-            parts = split_parts(gu.shape[0], gate_up.shape[1], gu.shape[1], "gate_up")
-        if parts > 1 and gu.shape[1] % parts == 0 and gu.shape[0] > 0:
-            grad_x = matmul_split_k(gu, gate_up, parts)
-        else:
-            grad_x = _mm(gu, gate_up)
+        grad_x = None
+        if gate_up is None:
+            grad_x = fused_grad_input(gu, (gate_w, up_w)) if gu.dim() == 2 else None
+            if grad_x is None:
+                gate_up = unpack_concat((gate_w, up_w), grad_out.device)
+        if grad_x is None:
+            parts = SPLIT_K_GATE_UP
+            if parts is None:
+                parts = split_parts(gu.shape[0], gate_up.shape[1], gu.shape[1], "gate_up")
+            if parts > 1 and gu.shape[1] % parts == 0 and gu.shape[0] > 0:
+                grad_x = matmul_split_k(gu, gate_up, parts)
+            else:
+                grad_x = _mm(gu, gate_up)
         return grad_x, None, None, None, None, None
 
 

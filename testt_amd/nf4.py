@@ -405,6 +405,33 @@ def _unpack_groups_generic(groups, device):
     return stacks
 
 
+def fused_linear(x2, weights, bias=None):
+    """x2 [M, K] @ W^T (+ bias), W the row stack of the NF4 `weights`, through the fused
+    NF4-dequant GEMM where that is the faster path for this problem (nf4_gemm.prefer_fused);
+    None elsewhere, and the caller unpacks W."""
+    if not USE_FUSED_NF4_GEMM:
+        return None
+    from . import nf4_gemm
+
+    if nf4_gemm.supported(x2, weights, bias) and nf4_gemm.prefer_fused(x2, weights):
+        return nf4_gemm.nf4_linear(x2, weights, bias)
+    return None
+
+
+def fused_grad_input(g2, weights):
+    """g2 [M, N] @ W (the input gradient of fused_linear's product) through the fused NF4
+    input-gradient GEMM where that is the faster path (nf4_gemm.prefer_fused_grad_input); None
+    elsewhere."""
+    if not USE_FUSED_NF4_GEMM:
+        return None
+    from . import nf4_gemm
+
+    if nf4_gemm.grad_input_supported(g2, weights) and \
+            nf4_gemm.prefer_fused_grad_input(g2, weights):
+        return nf4_gemm.nf4_grad_input(g2, weights)
+    return None
+
+
 class FrozenNF4Linear(torch.autograd.Function):
     """y = x @ W^T (+ b) for frozen 4-bit weights stacked by rows, fp16 in and out.
 
@@ -415,13 +442,10 @@ class FrozenNF4Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, bias, weights, w16=None):
         ctx.weights = weights
-        if w16 is None and USE_FUSED_NF4_GEMM:
-            from . import nf4_gemm
-
-            x2 = x.reshape(-1, x.shape[-1])
-            if nf4_gemm.supported(x2, weights, bias) and nf4_gemm.prefer_fused(x2, weights):
+        if w16 is None:
+            out = fused_linear(x.reshape(-1, x.shape[-1]), weights, bias)
+            if out is not None:
                 ctx.unpacked = None
-                out = nf4_gemm.nf4_linear(x2, weights, bias)
                 return out.view(*x.shape[:-1], out.shape[-1])
         weight = w16 if w16 is not None else unpack_concat(weights, x.device)
         if x.dim() == 2 or x.is_contiguous():
@@ -437,14 +461,10 @@ class FrozenNF4Linear(torch.autograd.Function):
         grad_x = None
         if ctx.needs_input_grad[0]:
             g = grad_out.to(torch.float16)
-            if getattr(ctx, "unpacked", None) is None and USE_FUSED_NF4_GEMM:
+            if getattr(ctx, "unpacked", None) is None:
                 # no unpacked weight kept: the fused input gradient where it is the faster path
-                from . import nf4_gemm
-
-                g2 = g.reshape(-1, g.shape[-1])
-                if nf4_gemm.grad_input_supported(g2, ctx.weights) and \
-                        nf4_gemm.prefer_fused_grad_input(g2, ctx.weights):
-                    dx = nf4_gemm.nf4_grad_input(g2, ctx.weights)
+                dx = fused_grad_input(g.reshape(-1, g.shape[-1]), ctx.weights)
+                if dx is not None:
                     return dx.view(*g.shape[:-1], dx.shape[-1]), None, None, None
             weight = unpacked_for_backward(ctx, ctx.weights, grad_out.device)
             if g.dim() == 2:
