@@ -27,8 +27,9 @@ extern "C" {
 
 /* ABI version of this header; soupk_abi_version() returns the library's.  4 adds
    soupk_lora_rope_fwd, soupk_gemm_nn_nf4, soupk_gemm_tn_nf4_split, soupk_gemm_nn_nf4_split,
-   soupk_gemm_lt, soupk_gemm_lt_index, soupk_layer_fwd, soupk_layer_bwd and soupk_init_device
-   to version 3's entry points. */
+   soupk_gemm_lt, soupk_gemm_lt_index, soupk_layer_fwd, soupk_layer_bwd (with the layer's
+   products on NF4 weights: SoupkLayerNf4) and soupk_init_device to version 3's entry
+   points. */
 #define SOUPK_ABI_VERSION 4
 
 /* Status of soupk_lora_bwd_params_noalloc for a problem beyond its static scratch (no launch). */
@@ -534,7 +535,33 @@ int soupk_gemm_lt_index(int32_t trans_a, int32_t trans_b, int64_t m, int64_t n, 
  * layer's soupk_nf4_unpack_multi_lora output.  algo_*: hipBLASLt solution indices (-1: the
  * heuristic's) of the GEMMs as soupk_gemm_lt takes them.  Returns the first failing call's
  * status; nothing is launched after it.
+ *
+ * With dims->nf4 set, the weights stay in NF4 (w_* unused, may be NULL; p_down = p_gu = 1):
+ * each product is the fused NF4-dequant GEMM, soupk_gemm_tn_nf4 forward and soupk_gemm_nn_nf4
+ * for the input gradients, or their contraction-split forms where split_fwd / split_bwd > 1
+ * (partials in nf4->partials); the q|k|v input gradient is formed in g_o's buffer and added to
+ * the LoRA part of dy (fp16 + fp16 in fp32, rounded once more), as testt_amd/layer.py's
+ * per-operation path does on NF4 weights.
  */
+typedef struct SoupkNf4Group {                 /* one product's weight: 1-4 row parts */
+  int32_t n_parts;
+  int32_t rows[4];
+  const uint8_t* packed[4];                    /* as soupk_gemm_tn_nf4 takes them */
+  const uint8_t* absmax[4];
+  const float* code2[4];
+  const float* absmax2[4];
+  const float* offset[4];
+  const float* nf4[4];
+} SoupkNf4Group;
+
+typedef struct SoupkLayerNf4 {
+  SoupkNf4Group qkv, o, gu, down;              /* [Wq;Wk;Wv], Wo, [Wgate;Wup], Wdown */
+  int32_t split_fwd[4];                        /* contraction splits (1: none), same order */
+  int32_t split_bwd[4];
+  float* partials;                             /* fp32 scratch of the split products */
+  int64_t partials_floats;
+} SoupkLayerNf4;
+
 typedef struct SoupkLayerDims {
   int64_t M;                                   /* tokens (rows) */
   int32_t H, NH, NKV, D, I, r, batch, seq;     /* D = 128, r = 16 */
@@ -554,6 +581,7 @@ typedef struct SoupkLayerDims {
   const int32_t* cu;                           /* int32 [batch + 1] */
   void* gemm_ws;                               /* hipBLASLt workspace */
   int64_t gemm_ws_bytes;
+  const SoupkLayerNf4* nf4;                    /* NULL: w_* are the unpacked fp16 stacks */
 } SoupkLayerDims;
 
 typedef struct SoupkLayerFwd {

@@ -336,3 +336,46 @@ def test_nf4_resident_layer(monkeypatch, lengths):
                           *runs):
         assert torch.isfinite(a.float()).all(), name
         assert rel_err(a, b) < 5e-3, (name, rel_err(a, b))
+
+
+@pytest.mark.parametrize("lengths,with_delta", [((64, 37), True), ((16, 0), True),
+                                               ((64, 37), False)])
+def test_nf4_resident_native_is_bit_identical(monkeypatch, lengths, with_delta):
+    """The layer on its NF4 weights issued from C (NativeDecoderLayer with dims.nf4:
+    soupk_layer_fwd / _bwd calling the fused NF4 GEMMs) against the same layer's per-operation
+    nodes on the NF4 weights: the same outputs and gradients, bit for bit, over two steps
+    (parameter gradients accumulating), also for a first layer without residual delta."""
+    print(f"nf4-resident native layer lengths={lengths} delta={with_delta}", flush=True)
+    monkeypatch.setattr(layer, "NF4_RESIDENT_SMALL_BATCHES", True)
+    batch, seq = len(lengths), 64
+    w = layer.synthetic_layer(DEV, seed=15)
+    amask = torch.zeros(batch, seq, dtype=torch.int64, device=DEV)
+    for b, n in enumerate(lengths):
+        amask[b, :n] = 1
+    pos = amask.reshape(-1).nonzero().squeeze(1)
+    m = pos.numel()
+    cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq, w.head_dim))
+    g = torch.Generator().manual_seed(9)
+    s0 = torch.randn(m, workloads.HIDDEN, generator=g).to(DEV)
+    d0 = (0.5 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    gs = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(DEV)
+    gd = (1e-2 * torch.randn(m, workloads.HIDDEN, generator=g)).to(torch.float16).to(DEV)
+    runs = []
+    for native in (True, False):
+        monkeypatch.setattr(layer_native, "NATIVE_LAYER", native)
+        out = []
+        for _ in range(2):
+            s_in = s0.clone().requires_grad_(True)
+            d_in = d0.clone().requires_grad_(True) if with_delta else None
+            s, d = layer.decoder_layer(s_in, d_in, w, pos, batch, seq, cos, sin,
+                                       layer.key_valid_of(amask))
+            assert (type(s.grad_fn).__name__ == "NativeDecoderLayerBackward") == native
+            torch.autograd.backward([s, d], [gs, gd])
+            out += [s.detach(), d.detach(), s_in.grad,
+                    d_in.grad if with_delta else torch.zeros(())]
+        runs.append(out + [p.grad.clone() for p in (*w.lora_q, *w.lora_v)])
+        for p in (*w.lora_q, *w.lora_v):
+            p.grad = None
+    names = ["s", "d", "d s_in", "d delta"] * 2 + ["d A_q", "d B_q", "d A_v", "d B_v"]
+    for name, a, b in zip(names, *runs):
+        assert torch.equal(a, b), name

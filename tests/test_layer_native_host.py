@@ -13,7 +13,8 @@ from testt_amd import layer_native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 STRUCTS = {"SoupkLayerDims": layer_native.LayerDims, "SoupkLayerFwd": layer_native.LayerFwd,
-           "SoupkLayerBwd": layer_native.LayerBwd}
+           "SoupkLayerBwd": layer_native.LayerBwd, "SoupkNf4Group": layer_native.Nf4Group,
+           "SoupkLayerNf4": layer_native.LayerNf4}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc is needed to lay out the header")

@@ -116,12 +116,11 @@ UNPACK_PER_LAYER = True
 # A layer whose token count is small enough that each of its products takes the fused
 # NF4-dequant GEMM, forward and input gradient (nf4_gemm's measured window: up to 128 rows at
 # Qwen2.5-1.5B's shapes on MI355X), skips that unpack and runs on the NF4 weights: no fp16 copy
-# of the layer's weights (94 MB in Qwen2.5-1.5B) is written or read.  Measured (bench.py
-# --nf4-resident, forward + backward): 186 / 203 / 216 us of GPU time at 16 / 64 / 128 tokens
-# against 231 / 217 / 232 us unpacked, but through the per-operation Python nodes, whose host
-# time (~530 us) exceeds the layer issued from C on unpacked weights (~360 us, itself
-# host-bound at these sizes); off until the C-issued layer takes NF4 weights.
-NF4_RESIDENT_SMALL_BATCHES = False
+# of the layer's weights (94 MB in Qwen2.5-1.5B) is written or read.  Issued from C like the
+# unpacked layer (layer_native, dims.nf4).  Measured (bench.py --nf4-resident, forward +
+# backward at 16 / 64 / 128 tokens): eager 281 / 271 / 269 us against 363 / 366 / 365 us
+# unpacked, GPU time (graph replay) 185 / 201 / 218 us against 232 / 218 / 233 us.
+NF4_RESIDENT_SMALL_BATCHES = True
 
 
 def nf4_resident(tokens, groups, device):
@@ -452,8 +451,8 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
     params = (w.lora_q[0], w.lora_v[0], w.lora_q[1], w.lora_v[1]) if plain else None
     w_qkv = w_o = w_gu = w_d = staged = None
     groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
-    if UNPACK_PER_LAYER and not (NF4_RESIDENT_SMALL_BATCHES and
-                                 nf4_resident(s.shape[0], groups, s.device)):
+    on_nf4 = NF4_RESIDENT_SMALL_BATCHES and nf4_resident(s.shape[0], groups, s.device)
+    if UNPACK_PER_LAYER and not on_nf4:
         if plain and USE_FUSED_LORA and _lora.params_supported(*params, s.device):
             # the LoRA parameters' fp16 staging rides on the same launch as the unpack
             (w_qkv, w_o, w_gu, w_d), staged = unpack_groups_lora(
@@ -466,7 +465,13 @@ def decoder_layer(s, delta, w, pos_idx, batch, seq, cos, sin, key_valid):
             _lora.params_supported(*params, s.device):
         cu = _attention.cu_seqlens_of(pos_idx, batch, seq)
         scale = 1.0 / math.sqrt(hd) if w.attn_scale is None else float(w.attn_scale)
-        if ONE_NODE_LAYER and _native.supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
+        native = _native.supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged)
+        if on_nf4 and _native.supported_nf4(s, delta, w):
+            # the C-issued layer on the NF4 weights; the LoRA parameters staged here, as the
+            # unpack launch does for the unpacked layer
+            staged = _lora.stage(*(p.detach() for p in params))
+            native = True
+        if ONE_NODE_LAYER and native:
             from .rope import _table
             from ._index import as_index
 

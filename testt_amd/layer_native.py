@@ -27,6 +27,17 @@ NATIVE_LAYER = True
 _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 
 
+class Nf4Group(ctypes.Structure):
+    _fields_ = ([("n_parts", _i32), ("rows", _i32 * 4)] +
+                [(n, _p * 4) for n in ("packed", "absmax", "code2", "absmax2", "offset", "nf4")])
+
+
+class LayerNf4(ctypes.Structure):
+    _fields_ = ([(n, Nf4Group) for n in ("qkv", "o", "gu", "down")] +
+                [("split_fwd", _i32 * 4), ("split_bwd", _i32 * 4), ("partials", _p),
+                 ("partials_floats", _i64)])
+
+
 class LayerDims(ctypes.Structure):
     _fields_ = ([("M", _i64)] +
                 [(n, _i32) for n in ("H", "NH", "NKV", "D", "I", "r", "batch", "seq", "p_down",
@@ -34,7 +45,7 @@ class LayerDims(ctypes.Structure):
                 [(n, _f32) for n in ("eps", "scaling", "scale")] +
                 [(n, _p) for n in ("norm1", "norm2", "qkv_bias", "w_qkv", "w_o", "w_gu", "w_d",
                                    "staged", "cos", "sin", "pos", "cu", "gemm_ws")] +
-                [("gemm_ws_bytes", _i64)])
+                [("gemm_ws_bytes", _i64), ("nf4", _p)])
 
 
 class LayerFwd(ctypes.Structure):
@@ -70,16 +81,66 @@ def _arena(device, parts):
     return buf, {n: base + o for n, o in offs.items()}
 
 
-def supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
+def _common(s, delta, w, inter):
     from . import lora as _lora
-    from . import mlp, nf4
+    from . import mlp
 
-    return (NATIVE_LAYER and _blas.USE_GEMM_LT and nf4.KEEP_UNPACKED_FOR_BACKWARD and
-            not mlp.RECOMPUTE_GATE_UP and staged is not None and w.o_bias is None and
-            None not in (w_qkv, w_o, w_gu, w_d) and s.dtype == torch.float32 and
-            (delta is None or delta.dtype == torch.float16) and w.head_dim == 128 and
-            _lora.RANK == 16 and s.dim() == 2 and s.shape[1] % 8 == 0 and
-            w_d.dim() == 2 and w_d.shape[1] % 8 == 0 and s.is_cuda)
+    return (NATIVE_LAYER and not mlp.RECOMPUTE_GATE_UP and w.o_bias is None and
+            s.dtype == torch.float32 and (delta is None or delta.dtype == torch.float16) and
+            w.head_dim == 128 and _lora.RANK == 16 and s.dim() == 2 and s.shape[1] % 8 == 0 and
+            inter % 8 == 0 and s.is_cuda)
+
+
+def supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
+    """The layer on its unpacked fp16 stacks (hipBLASLt products)."""
+    from . import nf4
+
+    return (_blas.USE_GEMM_LT and nf4.KEEP_UNPACKED_FOR_BACKWARD and staged is not None and
+            None not in (w_qkv, w_o, w_gu, w_d) and w_d.dim() == 2 and
+            _common(s, delta, w, w_d.shape[1]))
+
+
+def supported_nf4(s, delta, w):
+    """The layer on its NF4 weights (fused NF4-dequant products; the caller checked their
+    layout, layer.nf4_resident)."""
+    from . import nf4
+
+    return nf4.USE_FUSED_NF4_GEMM and _common(s, delta, w, nf4.weight_shape(w.down)[1])
+
+
+def _nf4_group(weights, dev):
+    from . import nf4
+
+    g = Nf4Group()
+    g.n_parts = len(weights)
+    for i, x in enumerate(weights):
+        g.rows[i] = nf4.weight_shape(x)[0]
+        (g.packed[i], g.absmax[i], g.code2[i], g.absmax2[i], g.offset[i],
+         g.nf4[i]) = nf4._plan(x, dev)[0]
+    return g
+
+
+def _nf4_layer(w, M, dev):
+    """The LayerNf4 of a layer's NF4 weights at M tokens: the split counts nf4_gemm's
+    nf4_linear and nf4_grad_input pick, and the floats of the largest split's partials."""
+    from . import nf4, nf4_gemm
+
+    groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
+    cus = nf4_gemm._cu_count(dev)
+    n4 = LayerNf4()
+    fwd_floats = bwd_floats = 4
+    for i, (name, weights) in enumerate(zip(("qkv", "o", "gu", "down"), groups)):
+        setattr(n4, name, _nf4_group(weights, dev))
+        rows = sum(nf4.weight_shape(x)[0] for x in weights)
+        cols = nf4.weight_shape(weights[0])[1]
+        fwd = nf4_gemm.split_count(M, rows, cols, cus)
+        bwd = nf4_gemm.split_count(M, cols, rows, cus, nf4_gemm.GRAD_TILE)
+        n4.split_fwd[i], n4.split_bwd[i] = fwd, bwd
+        if fwd > 1:
+            fwd_floats = max(fwd_floats, nf4_gemm._split_used(cols // 64, fwd)[1] * M * rows)
+        if bwd > 1:
+            bwd_floats = max(bwd_floats, nf4_gemm._split_used(rows // 64, bwd)[1] * M * cols)
+    return n4, fwd_floats, bwd_floats
 
 
 class NativeDecoderLayer(torch.autograd.Function):
@@ -88,28 +149,40 @@ class NativeDecoderLayer(torch.autograd.Function):
     @staticmethod
     def forward(ctx, s_in, delta, a_q, b_q, a_v, b_v, w, w_qkv, w_o, w_gu, w_d, staged, cos32,
                 sin32, pos, cu, batch, seq, scale):
+        from . import nf4
         from .rmsnorm import _weight32
 
         dev = s_in.device
         M, H = s_in.shape
-        NH, NKV, D, I, r = w.n_heads, w.n_kv, 128, w_d.shape[1], 16
+        on_nf4 = w_qkv is None          # the products on the NF4 weights (few tokens)
+        I = nf4.weight_shape(w.down)[1] if on_nf4 else w_d.shape[1]
+        NH, NKV, D, r = w.n_heads, w.n_kv, 128, 16
         NQ, NV = NH * D, NKV * D
         W = NQ + 2 * NV
-        p_down = _mlp.SPLIT_K_DOWN or _mlp.split_parts(M, H, I, "down")
-        p_gu = _mlp.SPLIT_K_GATE_UP or _mlp.split_parts(M, H, 2 * I, "gate_up")
-        if I % p_down:
-            p_down = 1
-        if (2 * I) % p_gu:
-            p_gu = 1
+        if on_nf4:
+            p_down = p_gu = 1
+            n4, floats, ctx.bwd_floats = _nf4_layer(w, M, dev)
+            partials = torch.empty(floats, dtype=torch.float32, device=dev)
+            n4.partials, n4.partials_floats = partials.data_ptr(), partials.numel()
+        else:
+            n4 = partials = None
+            p_down = _mlp.SPLIT_K_DOWN or _mlp.split_parts(M, H, I, "down")
+            p_gu = _mlp.SPLIT_K_GATE_UP or _mlp.split_parts(M, H, 2 * I, "gate_up")
+            if I % p_down:
+                p_down = 1
+            if (2 * I) % p_gu:
+                p_gu = 1
         st = _ext.stream_of(s_in)
-        ws = _blas._ws(dev)
+        ws = None if on_nf4 else _blas._ws(dev)
         norm1, norm2 = _weight32(w.input_norm, H, dev), _weight32(w.post_norm, H, dev)
         bias = w.qkv_bias
         dims = LayerDims(M, H, NH, NKV, D, I, r, batch, seq, p_down, p_gu, float(w.eps),
                          float(w.scaling), float(scale), norm1.data_ptr(), norm2.data_ptr(),
-                         _ext.ptr(bias), w_qkv.data_ptr(), w_o.data_ptr(), w_gu.data_ptr(),
-                         w_d.data_ptr(), staged.data_ptr(), cos32.data_ptr(), sin32.data_ptr(),
-                         pos.data_ptr(), cu.data_ptr(), ws.data_ptr(), _blas.WORKSPACE_BYTES)
+                         _ext.ptr(bias), _ext.ptr(w_qkv), _ext.ptr(w_o), _ext.ptr(w_gu),
+                         _ext.ptr(w_d), staged.data_ptr(), cos32.data_ptr(), sin32.data_ptr(),
+                         pos.data_ptr(), cu.data_ptr(), _ext.ptr(ws),
+                         0 if on_nf4 else _blas.WORKSPACE_BYTES,
+                         ctypes.addressof(n4) if on_nf4 else None)
         has_delta = delta is not None
         keep, kp = _arena(dev, [("s1", M * H * _F32 if has_delta else 0), ("y", M * H * _F16),
                                 ("rstd1", M * _F32), ("t", M * 2 * r * _F16),
@@ -132,12 +205,13 @@ class NativeDecoderLayer(torch.autograd.Function):
             s2.data_ptr(), kp["y2"], kp["rstd2"], kp["gu"], tp["qkv"], tp["o"], tp["act"],
             tp["down_part"], d.data_ptr())
         _ext.call("soupk_layer_fwd", ctypes.addressof(dims), ctypes.addressof(args), st)
-        del tmp, ws
+        del tmp, ws, partials
         ctx.save_for_backward(s_in, s2)
         ctx.keep, ctx.kp = keep, kp
+        ctx.nf4 = n4                    # dims.nf4 points at it
         # what the backward reads besides: the weights, LoRA parameters and tables (inputs)
         ctx.inputs = (w_qkv, w_o, w_gu, w_d, staged, cos32, sin32, pos, cu, norm1, norm2, bias,
-                      a_q, a_v, b_q, b_v)
+                      a_q, a_v, b_q, b_v, w)      # w: the NF4 weights dims.nf4 points into
         ctx.dims = dims
         ctx.has_delta = has_delta
         ctx.consumed = False
@@ -187,15 +261,21 @@ class NativeDecoderLayer(torch.autograd.Function):
             lora_ws_floats, g_s_in.data_ptr(), _ext.ptr(g_delta), d_aq.data_ptr(),
             d_av.data_ptr(), d_bq.data_ptr(), d_bv.data_ptr())
         st = _ext.stream_of(g_s_in)
-        ws = _blas._ws(dev)           # a workspace of the stream the backward runs on
-        dims.gemm_ws = ws.data_ptr()
+        n4 = ctx.nf4
+        if n4 is not None:
+            # the split products' partials, from the stream the backward runs on
+            ws = torch.empty(ctx.bwd_floats, dtype=torch.float32, device=dev)
+            n4.partials, n4.partials_floats = ws.data_ptr(), ws.numel()
+        else:
+            ws = _blas._ws(dev)       # a workspace of the stream the backward runs on
+            dims.gemm_ws = ws.data_ptr()
         _ext.call("soupk_layer_bwd", ctypes.addressof(dims), ctypes.addressof(args), st)
         del ws
         if not ctx.has_delta:
             # s_in is also the residual: its gradient adds the residual's (two terms, so the
             # order the engine would sum them in does not matter)
             g_s_in.add_(_view_f32(scratch, sp["g_s1"], M, H))
-        ctx.keep = ctx.kp = ctx.inputs = None
+        ctx.keep = ctx.kp = ctx.inputs = ctx.nf4 = None
         del keep, scratch
         return (g_s_in, g_delta, d_aq, d_bq, d_av, d_bv) + (None,) * 13
 
