@@ -1737,7 +1737,7 @@ def main():
     # Last: the layer timing captures HIP graphs, and eager work of the same process measured
     # after a capture ran slower (the 28-layer step: 36 ms against 25 ms before it); the
     # reference-profile layer (no capture) runs before it.
-    layer_t = layer_ref = layer_ragged = None
+    layer_t = layer_ref = layer_ragged = layer_nf4 = None
     if not args.no_layer:
         log("timing one decoder layer fwd+bwd at 2048 tokens")
         n_layer_steps = max(50, min(100, args.steps // 3))
@@ -1757,6 +1757,7 @@ def main():
             f"graph-replayed fwd {layer_t['graph_fwd_us']} us, fwd+bwd "
             f"{layer_t['graph_fwd_bwd_us']} us; ragged graph-replayed fwd+bwd "
             f"{layer_ragged['graph_fwd_bwd_us']} us")
+        layer_nf4 = time_nf4_resident(dev)
     kernels = {}
     total_us = 0.0
     total_bytes = 0
@@ -1835,6 +1836,7 @@ def main():
         "layer": layer_t,
         "layer_reference_profile": layer_ref,
         "layer_ragged": layer_ragged,
+        "layer_nf4_resident": layer_nf4,
         "attention": attn_t,
         "gemm_selection": gemm_table or "hipBLASLt heuristic (--heuristic-gemms)",
         "step": step_t,
