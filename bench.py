@@ -885,6 +885,43 @@ SWEEP_ROWS = (16, 64, 256, 512, 1024)   # row counts of the fused NF4 GEMM sweep
 RESIDENT_LENGTHS = ((16, 0, 0, 0), (64, 0, 0, 0), (32, 32, 32, 32))
 
 
+def trace_nf4_resident(dev, steps=5, warmup=3):
+    """For a kernel trace of the layer at few tokens, NF4 weights against unpacked: for each
+    token count of RESIDENT_LENGTHS and each mode, `warmup` forward+backward steps, then a
+    DeviceHold, `steps` steps, a DeviceHold (summarize_nf4_resident reads the kernels between
+    the holds).  Returns the segment labels in trace order."""
+    from testt_amd import layer
+
+    hold = DeviceHold(dev)
+    B, T = workloads.BATCH, workloads.SEQ
+    labels = []
+    saved = layer.NF4_RESIDENT_SMALL_BATCHES
+    try:
+        for lengths in RESIDENT_LENGTHS:
+            w, pos, key_valid, cos, sin, s0, d0, gs, gd = layer_inputs(dev, lengths)
+
+            def step():
+                s_in = s0.detach().requires_grad_(True)
+                d_in = d0.detach().requires_grad_(True)
+                s, d = layer.decoder_layer(s_in, d_in, w, pos, B, T, cos, sin, key_valid)
+                torch.autograd.backward([s, d], [gs, gd])
+
+            for resident in (True, False):
+                layer.NF4_RESIDENT_SMALL_BATCHES = resident
+                for _ in range(warmup):
+                    step()
+                torch.cuda.synchronize(dev)
+                hold.hold(50)
+                for _ in range(steps):
+                    step()
+                hold.hold(50)
+                torch.cuda.synchronize(dev)
+                labels.append([sum(lengths), "nf4" if resident else "unpacked", steps])
+    finally:
+        layer.NF4_RESIDENT_SMALL_BATCHES = saved
+    return labels
+
+
 def time_nf4_resident(dev, steps=40, warmup=5):
     """The decoder layer at few tokens with its products on the NF4 weights (the fused
     NF4-dequant GEMM in each direction, no fp16 weight in memory:
@@ -1244,6 +1281,42 @@ def summarize_trace(trace_csv, title, command):
         out.append(f"| `{short}` | {grid} / {wg} | {len(d)} | {sum(d) / len(d):.2f} | "
                    f"{median(d):.2f} |")
     return "\n".join(out) + "\n"
+
+
+def summarize_nf4_resident(trace_csv, bench_json, command):
+    """Per token count and mode (trace_nf4_resident's segments): each kernel's launches and
+    GPU time per forward+backward step of the layer, and the total."""
+    with open(bench_json) as f:
+        labels = json.loads(f.read().strip().splitlines()[-1])["nf4_resident_trace"]
+    spans, cur, held = [], None, 0
+    for r in sorted(_read_csv(trace_csv), key=lambda r: int(r["Dispatch_Id"])):
+        name = r["Kernel_Name"]
+        if "bench_hold_kernel" in name:
+            held += 1
+            cur = {} if held % 2 == 1 else None      # odd holds open a measured span
+            if cur is not None:
+                spans.append(cur)
+            continue
+        if cur is None:
+            continue
+        short = _kernel_base(name) if "soupk" in name else name.split("(")[0][:80]
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        n, t = cur.get(short, (0, 0.0))
+        cur[short] = (n + 1, t + d)
+    out = [f"# rocprofv3 kernel trace: the decoder layer at few tokens, NF4 weights (fused "
+           "NF4-dequant GEMMs) against unpacked weights + hipBLASLt", "",
+           "Command (run from /tmp on the MI355X box, TMPDIR=/tmp):", "", "```", command, "```",
+           "", "Kernel launches and GPU time per forward+backward step of one Qwen2.5-1.5B "
+           "decoder layer (synthetic NF4 weights, LoRA r=16 on q/v), averaged over the measured "
+           "steps of each segment (bench.py trace_nf4_resident).", ""]
+    for (tokens, mode, steps), span in zip(labels, spans):
+        total = sum(t for _, t in span.values()) / steps
+        out += [f"## {tokens} tokens, {mode} weights: {total:.1f} us of kernels per step", "",
+                "| kernel | launches per step | us per step |", "|---|---:|---:|"]
+        for short, (n, t) in sorted(span.items(), key=lambda kv: -kv[1][1]):
+            out.append(f"| `{short}` | {n / steps:g} | {t / steps:.1f} |")
+        out.append("")
+    return "\n".join(out)
 
 
 NF4_GEMM_VARIANTS = ("fused_fp16_w_us", "fused_nf4_w_us", "hipblaslt_fp16_w_us", "unpack_us",
@@ -1625,6 +1698,9 @@ def main():
     ap.add_argument("--nf4-resident", action="store_true",
                     help="time the decoder layer at few tokens on its NF4 weights (the fused "
                          "NF4-dequant GEMM) against unpacked weights + hipBLASLt, then exit")
+    ap.add_argument("--summarize-nf4-resident", nargs=3,
+                    metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
+                    help="print the per-step kernel table of a kernel trace of --nf4-resident")
     ap.add_argument("--summarize-nf4-gemm", nargs=3, metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
                     help="print the fused NF4 GEMM tables of a rocprofv3 --kernel-trace run of "
                          "bench.py --nf4-gemm and exit (CPU)")
@@ -1635,6 +1711,10 @@ def main():
                     help="print the per-kernel breakdown of one training step of a rocprofv3 "
                          "--kernel-trace run (CPU)")
     args = ap.parse_args()
+    if args.summarize_nf4_resident:
+        a = args.summarize_nf4_resident
+        sys.stdout.write(summarize_nf4_resident(a[0], a[1], a[2]))
+        return
     if args.summarize_nf4_gemm:
         a = args.summarize_nf4_gemm
         sys.stdout.write(summarize_nf4_gemm(a[0], a[1], a[2]))
@@ -1693,6 +1773,7 @@ def main():
         return
     if args.nf4_resident:
         print(json.dumps({"nf4_resident_layer": time_nf4_resident(dev),
+                          "nf4_resident_trace": trace_nf4_resident(dev),
                           "gemm_selection": gemm_table}), flush=True)
         return
     if args.nf4_gemm:

@@ -130,3 +130,31 @@ def test_attention_block_steps_count_the_causal_key_blocks():
         nb = -(-n // 64)
         pairs = sum(1 for q in range(nb) for k in range(q + 1))
         assert bench.attn_block_steps([n], 3) == (3 * pairs, 6 * pairs)
+
+
+def test_nf4_resident_summary_reads_the_held_spans(tmp_path):
+    """summarize_nf4_resident: the kernels between each odd and even device-side wait are one
+    labelled segment, reported per step; launches outside the spans (warm-up) are left out."""
+    hdr = ["Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp",
+           "End_Timestamp"]
+    hold = K.format("bench_hold_kernel")
+    rows = [[1, K.format("gemm_tn_kernel<true>"), 64, 256, 0, 99000],       # warm-up
+            [2, hold, 64, 64, 0, 1000],
+            [3, K.format("gemm_tn_kernel<true>"), 64, 256, 0, 10000],
+            [4, K.format("gemm_tn_kernel<true>"), 64, 256, 0, 12000],
+            [5, K.format("split_sum_kernel"), 64, 256, 0, 2000],
+            [6, hold, 64, 64, 0, 1000],
+            [7, "Cijk_Alik_Bljk_HHS_BH_MT128x128x64(args)", 64, 256, 0, 50000],  # warm-up
+            [8, hold, 64, 64, 0, 1000],
+            [9, "Cijk_Alik_Bljk_HHS_BH_MT128x128x64(args)", 64, 256, 0, 8000],
+            [10, hold, 64, 64, 0, 1000]]
+    trace = _write(tmp_path / "trace.csv", hdr, rows)
+    bj = tmp_path / "bench.json"
+    bj.write_text(json.dumps({"nf4_resident_trace": [[16, "nf4", 2], [16, "unpacked", 1]]}) +
+                  "\n")
+    text = bench.summarize_nf4_resident(trace, str(bj), "cmd")
+    assert "## 16 tokens, nf4 weights: 12.0 us of kernels per step" in text
+    assert "| `gemm_tn_kernel<true>` | 1 | 11.0 |" in text
+    assert "| `split_sum_kernel` | 0.5 | 1.0 |" in text
+    assert "## 16 tokens, unpacked weights: 8.0 us of kernels per step" in text
+    assert "99" not in text and "50.0" not in text

@@ -12,6 +12,25 @@
 #include "soupk_common.hpp"
 #include "../../include/soupk.h"
 
+namespace soupk {
+namespace {
+
+// y += x elementwise in fp16 (each sum in fp32, rounded once), n a multiple of 8
+__global__ __launch_bounds__(256) void add_f16_kernel(u32x4* __restrict__ y,
+                                                      const u32x4* __restrict__ x, int64_t n8) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const u32x4 a = y[i], b = x[i];
+  u32x4 out;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    out[k] = pack_h2(lo_h(a[k]) + lo_h(b[k]), hi_h(a[k]) + hi_h(b[k]));
+  y[i] = out;
+}
+
+}  // namespace
+}  // namespace soupk
+
 namespace {
 
 using soupk::u32x4;
@@ -70,25 +89,11 @@ int nf4_bwd(const SoupkLayerNf4* n, const SoupkNf4Group& g, int splits, const ui
                            g.offset, g.nf4, g.rows, 64, 256, dx, M, N, K, stream);
 }
 
-// y += x elementwise in fp16 (each sum in fp32, rounded once), n a multiple of 8
-__global__ __launch_bounds__(256) void add_f16_kernel(u32x4* __restrict__ y,
-                                                      const u32x4* __restrict__ x, int64_t n8) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n8) return;
-  const u32x4 a = y[i], b = x[i];
-  u32x4 out;
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    out[k] = soupk::pack_h2(soupk::lo_h(a[k]) + soupk::lo_h(b[k]),
-                            soupk::hi_h(a[k]) + soupk::hi_h(b[k]));
-  y[i] = out;
-}
-
 int add_f16(uint16_t* y, const uint16_t* x, int64_t n, void* stream) {
   if (n % 8) return soupk::kInvalid;
   const int64_t n8 = n / 8;
   if (n8 == 0) return soupk::kOk;
-  return soupk::launch_kernel(add_f16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)),
+  return soupk::launch_kernel(soupk::add_f16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)),
                               dim3(256), static_cast<hipStream_t>(stream),
                               reinterpret_cast<u32x4*>(y), reinterpret_cast<const u32x4*>(x),
                               n8);
