@@ -124,11 +124,27 @@ NF4_RESIDENT_SMALL_BATCHES = True
 
 
 def nf4_resident(tokens, groups, device):
-    """True when a layer of `tokens` rows runs on its NF4 weights (NF4_RESIDENT_SMALL_BATCHES)."""
+    """True when a layer of `tokens` rows runs on its NF4 weights (NF4_RESIDENT_SMALL_BATCHES).
+    The answer is remembered on the first weight per token count, device and weight state."""
     from . import nf4, nf4_gemm
 
-    return (tokens > 0 and nf4.USE_FUSED_NF4_GEMM and
-            nf4_gemm.prefers_fused_all(tokens, groups, device))
+    if tokens <= 0 or not nf4.USE_FUSED_NF4_GEMM:
+        return False
+    key = (tokens, device, tuple(nf4._plan_key(x, device) for g in groups for x in g))
+    first = groups[0][0]
+    memo = getattr(first, "_soupk_resident", None)
+    if memo is None:
+        memo = {}
+        try:
+            setattr(first, "_soupk_resident", memo)
+        except AttributeError:        # an object that takes no attributes: not remembered
+            pass
+    hit = memo.get(key)
+    if hit is None:
+        if len(memo) > 256:
+            memo.clear()
+        hit = memo[key] = nf4_gemm.prefers_fused_all(tokens, groups, device)
+    return hit
 
 
 def _qkv_forward(ctx, y16, weights, w16, bias):

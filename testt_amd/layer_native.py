@@ -122,7 +122,29 @@ def _nf4_group(weights, dev):
 
 def _nf4_layer(w, M, dev):
     """The LayerNf4 of a layer's NF4 weights at M tokens: the split counts nf4_gemm's
-    nf4_linear and nf4_grad_input pick, and the floats of the largest split's partials."""
+    nf4_linear and nf4_grad_input pick, and the floats of the largest split's partials
+    (partials unset).  Remembered on the q weight per token count, device and weight state (the
+    addresses of the seven weights' NF4 data and tables, as nf4's plan cache keys them), so
+    that it lives as long as the weights whose tables it points at; a fresh copy of the
+    remembered struct per call."""
+    from . import nf4
+
+    weights = (w.q, w.k, w.v, w.o, w.gate, w.up, w.down)
+    key = (M, dev, tuple(nf4._plan_key(x, dev) for x in weights))
+    memo = getattr(w.q, "_soupk_layer_nf4", None)
+    if memo is None:
+        memo = {}
+        setattr(w.q, "_soupk_layer_nf4", memo)
+    hit = memo.get(key)
+    if hit is None:
+        if len(memo) > 64:
+            memo.clear()
+        n4, fwd, bwd = _build_nf4_layer(w, M, dev)
+        hit = memo[key] = (bytes(n4), fwd, bwd)
+    return LayerNf4.from_buffer_copy(hit[0]), hit[1], hit[2]
+
+
+def _build_nf4_layer(w, M, dev):
     from . import nf4, nf4_gemm
 
     groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))

@@ -230,7 +230,23 @@ def _split_used(kt, splits):
     return per, -(-kt // per)
 
 
+_split_memo = {}
+
+
 def split_count(rows, out_cols, contraction, cus, tile=FWD_TILE):
+    """split_count for these arguments and the cost model's present constants, remembered
+    (the decoder layer asks for eight counts per step)."""
+    key = (rows, out_cols, contraction, cus, tuple(tile), SPLIT_STEP_US, SPLIT_SHARED_CU,
+           SPLIT_PARTIAL_US_PER_MB, SPLIT_SUM_US, FUSED_MAX_CONTRACTION, MAX_SPLITS)
+    hit = _split_memo.get(key)
+    if hit is None:
+        if len(_split_memo) > 4096:
+            _split_memo.clear()
+        hit = _split_memo[key] = _split_count(rows, out_cols, contraction, cus, tile)
+    return hit
+
+
+def _split_count(rows, out_cols, contraction, cus, tile=FWD_TILE):
     """Contraction splits of a fused kernel's grid of `tile` tiles (the forward's 128 x 128, the
     input gradient's 128 x 64): 1 when the tiles alone fill half a wave of the `cus` compute
     units and the contraction is at most FUSED_MAX_CONTRACTION, else the count (each split at
