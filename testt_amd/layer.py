@@ -118,8 +118,8 @@ UNPACK_PER_LAYER = True
 # Qwen2.5-1.5B's shapes on MI355X), skips that unpack and runs on the NF4 weights: no fp16 copy
 # of the layer's weights (94 MB in Qwen2.5-1.5B) is written or read.  Issued from C like the
 # unpacked layer (layer_native, dims.nf4).  Measured (bench.py --nf4-resident, forward +
-# backward at 16 / 64 / 128 tokens): eager 281 / 271 / 269 us against 363 / 366 / 365 us
-# unpacked, GPU time (graph replay) 185 / 201 / 218 us against 232 / 218 / 233 us.
+# backward at 16 / 64 / 128 tokens): eager 222 / 220 / 221 us against 303 us unpacked, GPU
+# time (graph replay) 186 / 201 / 218 us against 232 / 218 / 232 us.
 NF4_RESIDENT_SMALL_BATCHES = True
 
 

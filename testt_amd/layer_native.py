@@ -96,7 +96,7 @@ def supported(s, delta, w, w_qkv, w_o, w_gu, w_d, staged):
     from . import nf4
 
     return (_blas.USE_GEMM_LT and nf4.KEEP_UNPACKED_FOR_BACKWARD and staged is not None and
-            None not in (w_qkv, w_o, w_gu, w_d) and w_d.dim() == 2 and
+            all(x is not None for x in (w_qkv, w_o, w_gu, w_d)) and w_d.dim() == 2 and
             _common(s, delta, w, w_d.shape[1]))
 
 
