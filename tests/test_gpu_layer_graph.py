@@ -25,13 +25,17 @@ def inputs(batch, seq, seed):
     return s0, d0, gs, gd
 
 
-def test_layer_graph_replays_match_eager():
-    batch, seq = 2, 128
+@pytest.mark.parametrize("batch,seq", [(2, 128), (2, 32)])
+def test_layer_graph_replays_match_eager(batch, seq):
+    """(2, 128): the layer on unpacked weights + hipBLASLt; (2, 32), 64 tokens: the layer on its
+    NF4 weights (fused NF4-dequant products with split partials, layer.nf4_resident)."""
     print(f"layer graph capture B={batch} T={seq}", flush=True)
     w = layer.synthetic_layer(DEV, seed=9)
     w_other = layer.synthetic_layer(DEV, seed=10)
     params = (*w.lora_q, *w.lora_v)
     pos = torch.arange(batch * seq, device=DEV)
+    groups = ((w.q, w.k, w.v), (w.o,), (w.gate, w.up), (w.down,))
+    assert layer.nf4_resident(batch * seq, groups, pos.device) == (batch * seq <= 128)
     cos, sin = (t.to(DEV) for t in workloads.rope_tables(seq))
     s0, d0, gs, gd = inputs(batch, seq, 1)
     s_in = s0.clone().requires_grad_(True)
