@@ -883,6 +883,9 @@ SWEEP_ROWS = (16, 64, 256, 512, 1024)   # row counts of the fused NF4 GEMM sweep
 
 # token counts (B=4 rows of T=512) of the NF4-resident layer comparison
 RESIDENT_LENGTHS = ((16, 0, 0, 0), (64, 0, 0, 0), (32, 32, 32, 32))
+# and, with --nf4-resident-wide, the layer on NF4 weights forced at larger token counts
+RESIDENT_WIDE_LENGTHS = ((64, 64, 64, 64), (128, 128, 128, 128), (192, 192, 192, 192),
+                         (256, 256, 256, 256))
 
 
 def trace_nf4_resident(dev, steps=5, warmup=3):
@@ -922,7 +925,21 @@ def trace_nf4_resident(dev, steps=5, warmup=3):
     return labels
 
 
-def time_nf4_resident(dev, steps=40, warmup=5):
+def time_nf4_resident_wide(dev, steps=40, warmup=5):
+    """time_nf4_resident's comparison at RESIDENT_WIDE_LENGTHS, the layer put on its NF4
+    weights at every size (layer.NF4_RESIDENT_MAX_TOKENS) although single products there
+    measured faster unpacked: where the layer's sum crosses over."""
+    from testt_amd import layer
+
+    saved = layer.NF4_RESIDENT_MAX_TOKENS
+    try:
+        layer.NF4_RESIDENT_MAX_TOKENS = max(sum(x) for x in RESIDENT_WIDE_LENGTHS)
+        return time_nf4_resident(dev, steps, warmup, RESIDENT_WIDE_LENGTHS)
+    finally:
+        layer.NF4_RESIDENT_MAX_TOKENS = saved
+
+
+def time_nf4_resident(dev, steps=40, warmup=5, lengths_list=RESIDENT_LENGTHS):
     """The decoder layer at few tokens with its products on the NF4 weights (the fused
     NF4-dequant GEMM in each direction, no fp16 weight in memory:
     layer.NF4_RESIDENT_SMALL_BATCHES) against the same layer unpacking its seven projections
@@ -933,7 +950,7 @@ def time_nf4_resident(dev, steps=40, warmup=5):
     out = {}
     saved = layer.NF4_RESIDENT_SMALL_BATCHES
     try:
-        for lengths in RESIDENT_LENGTHS:
+        for lengths in lengths_list:
             row = {"lengths": list(lengths)}
             for resident in (True, False):
                 layer.NF4_RESIDENT_SMALL_BATCHES = resident
@@ -1698,6 +1715,9 @@ def main():
     ap.add_argument("--nf4-resident", action="store_true",
                     help="time the decoder layer at few tokens on its NF4 weights (the fused "
                          "NF4-dequant GEMM) against unpacked weights + hipBLASLt, then exit")
+    ap.add_argument("--nf4-resident-wide", action="store_true",
+                    help="the --nf4-resident comparison at 256-1024 tokens, the layer forced "
+                         "onto its NF4 weights")
     ap.add_argument("--summarize-nf4-resident", nargs=3,
                     metavar=("TRACE_CSV", "BENCH_JSON", "CMD"),
                     help="print the per-step kernel table of a kernel trace of --nf4-resident")
@@ -1770,6 +1790,10 @@ def main():
                                                       varlen_only=True),
                           "timing": "GPU time per call: calls queued behind a device-side "
                                     "wait and timed as one span"}), flush=True)
+        return
+    if args.nf4_resident_wide:
+        print(json.dumps({"nf4_resident_layer_wide": time_nf4_resident_wide(dev),
+                          "gemm_selection": gemm_table}), flush=True)
         return
     if args.nf4_resident:
         print(json.dumps({"nf4_resident_layer": time_nf4_resident(dev),

@@ -121,6 +121,10 @@ UNPACK_PER_LAYER = True
 # backward at 16 / 64 / 128 tokens): eager 222 / 220 / 221 us against 303 us unpacked, GPU
 # time (graph replay) 186 / 201 / 218 us against 232 / 218 / 232 us.
 NF4_RESIDENT_SMALL_BATCHES = True
+# Up to this many tokens the layer runs on its NF4 weights whenever their layout allows, also
+# where single products measured faster through unpack + hipBLASLt (the layer's sum is what
+# counts: it saves the unpack launch, and the products it loses are offset by those it wins).
+NF4_RESIDENT_MAX_TOKENS = 0
 
 
 def nf4_resident(tokens, groups, device):
@@ -139,11 +143,13 @@ def nf4_resident(tokens, groups, device):
             setattr(first, "_soupk_resident", memo)
         except AttributeError:        # an object that takes no attributes: not remembered
             pass
+    key = key + (tokens <= NF4_RESIDENT_MAX_TOKENS,)
     hit = memo.get(key)
     if hit is None:
         if len(memo) > 256:
             memo.clear()
-        hit = memo[key] = nf4_gemm.prefers_fused_all(tokens, groups, device)
+        hit = memo[key] = nf4_gemm.prefers_fused_all(tokens, groups, device,
+                                                     window=not key[-1])
     return hit
 
 

@@ -116,11 +116,12 @@ def prefer_fused_grad_input(dy, weights):
     return fused_fits(M, K, N, GRAD_TILE, cus, grad_split_tiles(N, cus))
 
 
-def prefers_fused_all(rows, groups, device):
+def prefers_fused_all(rows, groups, device, window=True):
     """True when every group of `groups` (each a row stack of NF4 weights, as one product
     reads it) takes the fused kernels at `rows` rows in both directions -- the window of
-    prefer_fused and of prefer_fused_grad_input -- and has the layout they read.  A decoder
-    layer with this token count then runs on its NF4 weights without unpacking them."""
+    prefer_fused and of prefer_fused_grad_input -- and has the layout they read (with
+    window=False: the layout alone).  A decoder layer with this token count then runs on its
+    NF4 weights without unpacking them."""
     cus = _cu_count(device)
     for weights in groups:
         if not 1 <= len(weights) <= MAX_PARTS:
@@ -135,7 +136,8 @@ def prefers_fused_all(rows, groups, device):
                     (cols is not None and c != cols) or _nf4._plan(w, device) is None:
                 return False
             cols, n = c, n + r
-        if not (fused_fits(rows, n, cols, FWD_TILE, cus, forward_split_tiles(cols, cus)) and
+        if window and not (
+                fused_fits(rows, n, cols, FWD_TILE, cus, forward_split_tiles(cols, cus)) and
                 fused_fits(rows, cols, n, GRAD_TILE, cus, grad_split_tiles(n, cus))):
             return False
     return True
