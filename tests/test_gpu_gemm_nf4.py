@@ -129,6 +129,24 @@ def test_gemm_nn_nf4_split(rows, K, M, splits):
     assert torch.equal(nf4_gemm.nf4_grad_input(dy, ws, splits=splits), dx)
 
 
+@pytest.mark.parametrize("rows,K,splits", [((1536, 256, 256), 1536, 1), ((1536, 256, 256), 1536, 8),
+                                           ((8960, 8960), 1536, 1), ((1536,), 8960, 20)])
+def test_few_row_tiles_match_the_128_row_tiles(rows, K, splits):
+    """Up to 32 rows the forward (and the split input gradient) run 32-row tiles: the same
+    products in the same order, so the rows of a 16-row call equal the same rows computed
+    inside a 40-row call (128-row tiles), bit for bit."""
+    print(f"few-row tiles parts={rows} K={K} splits={splits}", flush=True)
+    ws = [workloads.nf4_weight(r, K, seed=130 + i, device=DEV) for i, r in enumerate(rows)]
+    g = torch.Generator().manual_seed(K + 5)
+    x = torch.randn(40, K, generator=g).to(torch.float16).to(DEV)
+    assert torch.equal(nf4_gemm.nf4_linear(x[:16].contiguous(), ws, splits=splits),
+                       nf4_gemm.nf4_linear(x, ws, splits=splits)[:16])
+    dy = (0.1 * torch.randn(40, sum(rows), generator=g)).to(torch.float16).to(DEV)
+    if sum(rows) // 64 >= splits:
+        assert torch.equal(nf4_gemm.nf4_grad_input(dy[:16].contiguous(), ws, splits=splits),
+                           nf4_gemm.nf4_grad_input(dy, ws, splits=splits)[:16])
+
+
 def test_rejects_shapes():
     x = torch.randn(8, 64, device=DEV).to(torch.float16)
     with pytest.raises(Exception):

@@ -544,6 +544,7 @@ __global__ __launch_bounds__(S::kThreads) void gemm_nn_nf4_kernel(
 //   4: 64 x 128, 2 x 2 waves of 32 x 64       5: 256 x 128, 4 x 2 waves of 64 x 64
 //   6: as 1 with K tiles of 128               7: 256 x 256, 2 x 4 waves of 128 x 64
 //   8: 256 x 256, 4 x 2 waves of 64 x 128     9: 256 x 128, 2 x 2 waves of 128 x 64
+//  10: 32 x 128, 1 x 4 waves of 32 x 32
 #ifndef SOUPK_GEMM_SHAPE
 #define SOUPK_GEMM_SHAPE 1
 #endif
@@ -565,11 +566,21 @@ using Shape = GemmShape<256, 256, 2, 4>;
 using Shape = GemmShape<256, 256, 4, 2>;
 #elif SOUPK_GEMM_SHAPE == 9
 using Shape = GemmShape<256, 128, 2, 2>;
+#elif SOUPK_GEMM_SHAPE == 10
+using Shape = GemmShape<32, 128, 1, 4>;
 #else
 using Shape = GemmShape<128, 128, 4, 2, 128>;
 #endif
 constexpr int kBK = Shape::BK;
 constexpr int kBM = Shape::BM, kBN = Shape::BN;
+// Up to 32 rows of x the forward runs 32-row tiles on 4 wavefronts of 32 x 32: the 128-row
+// tile computed three quarters clamped copies of the last row there.  Measured (MI355X, NF4 W,
+// the split counts split_count picks): at 16 rows q|k|v 8.02 -> 7.55 us, o 7.63 -> 7.18,
+// gate|up 23.58 -> 18.38, down 12.77 -> 11.07; slower from 64 rows (gate|up 24.07 -> 26.25).
+// Same products in the same order: identical results.
+using SmallShape = GemmShape<32, 128, 1, 4>;
+constexpr int kSmallRows = 32;
+static_assert(SmallShape::BN == kBN && SmallShape::BK == kBK, "one column tiling for both");
 
 int check_gemm(int64_t M, int32_t N, int32_t K, int64_t ldx) {
   if (M < 0 || N <= 0 || K <= 0 || N % kBN || K % kBK || ldx < K || ldx % 8) return kInvalid;
@@ -658,6 +669,11 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn(
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(w) || bad_ptr(y)) return kInvalid;
   Nf4Weights none{};
+  if (M <= kSmallRows)
+    return launch_kernel(gemm_tn_kernel<SmallShape, false>,
+                         dim3(static_cast<unsigned>(N / kBN)), dim3(SmallShape::kThreads),
+                         static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
+                         static_cast<int>(M), N, K, nullptr, K / kBK);
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<Shape, false>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, w, none, bias, y,
@@ -680,6 +696,11 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4(
     if (part_rows[i] % kBN) return kInvalid;
   if (M == 0) return kOk;
   if (bad_ptr(x) || bad_ptr(y)) return kInvalid;
+  if (M <= kSmallRows)
+    return launch_kernel(gemm_tn_kernel<SmallShape, true>,
+                         dim3(static_cast<unsigned>(N / kBN)), dim3(SmallShape::kThreads),
+                         static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
+                         static_cast<int>(M), N, K, nullptr, K / kBK);
   const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)));
   return launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads),
                        static_cast<hipStream_t>(stream), x, ldx, nullptr, nw, bias, y,
@@ -707,10 +728,18 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_tn_nf4_split(
   if (bad_ptr(x) || bad_ptr(y) || bad_ptr(workspace)) return kInvalid;
   if (reinterpret_cast<uintptr_t>(bias) & 7) return kInvalid;   // read 4 halves at a time
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)),
-                  static_cast<unsigned>(used));
-  int r = launch_kernel(gemm_tn_kernel<Shape, true>, grid, dim3(Shape::kThreads), st, x, ldx,
-                        nullptr, nw, bias, y, static_cast<int>(M), N, K, workspace, per);
+  int r;
+  if (M <= kSmallRows)
+    r = launch_kernel(gemm_tn_kernel<SmallShape, true>,
+                      dim3(static_cast<unsigned>(N / kBN), static_cast<unsigned>(used)),
+                      dim3(SmallShape::kThreads), st, x, ldx, nullptr, nw, bias, y,
+                      static_cast<int>(M), N, K, workspace, per);
+  else
+    r = launch_kernel(gemm_tn_kernel<Shape, true>,
+                      dim3(static_cast<unsigned>((N / kBN) * ((M + kBM - 1) / kBM)),
+                           static_cast<unsigned>(used)),
+                      dim3(Shape::kThreads), st, x, ldx, nullptr, nw, bias, y,
+                      static_cast<int>(M), N, K, workspace, per);
   if (r != kOk) return r;
   const int64_t n4 = M * static_cast<int64_t>(N) / 4;
   return launch_kernel(split_sum_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
@@ -735,6 +764,17 @@ using NS = GemmShape<64, 128, 2, 2>;
 #else
 using NS = GemmShape<128, 64, 4, 2>;
 #endif
+// The split form up to 32 rows of dy: 32-row tiles on 2 wavefronts of 32 x 32 (the column
+// tiling unchanged).  Measured (MI355X, the split counts split_count picks): at 16 rows q|k|v
+// 9.71 -> 9.13 us, o 8.34 -> 7.68, gate|up 23.46 -> 20.70; the unsplit kernel (down's input
+// gradient, 140 tiles walking the whole contraction) was 3% slower on 2 wavefronts and keeps
+// NS.  Same products in the same order: identical results.
+#ifndef SOUPK_GEMM_NN_SMALL
+#define SOUPK_GEMM_NN_SMALL 1
+#endif
+using NSmall = GemmShape<32, 64, 1, 2>;
+static_assert(NSmall::BN == NS::BN, "one column tiling for both");
+constexpr int kNnSmallRows = SOUPK_GEMM_NN_SMALL ? 32 : 0;
 
 // The input gradient's arguments, checked; N: W's columns (dx's), K: W's rows (the
 // contraction, dy's columns).
@@ -785,10 +825,18 @@ extern "C" __attribute__((visibility("default"))) int soupk_gemm_nn_nf4_split(
   if (M == 0) return kOk;
   if (bad_ptr(dy) || bad_ptr(dx) || bad_ptr(workspace)) return kInvalid;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((N / NS::BN) * ((M + NS::BM - 1) / NS::BM)),
-                  static_cast<unsigned>(used));
-  int r = launch_kernel(gemm_nn_nf4_kernel<NS>, grid, dim3(NS::kThreads), st, dy, lddy, nw, dx,
-                        static_cast<int>(M), N, K, workspace, per);
+  int r;
+  if (M <= kNnSmallRows)
+    r = launch_kernel(gemm_nn_nf4_kernel<NSmall>,
+                      dim3(static_cast<unsigned>(N / NS::BN), static_cast<unsigned>(used)),
+                      dim3(NSmall::kThreads), st, dy, lddy, nw, dx, static_cast<int>(M), N, K,
+                      workspace, per);
+  else
+    r = launch_kernel(gemm_nn_nf4_kernel<NS>,
+                      dim3(static_cast<unsigned>((N / NS::BN) * ((M + NS::BM - 1) / NS::BM)),
+                           static_cast<unsigned>(used)),
+                      dim3(NS::kThreads), st, dy, lddy, nw, dx, static_cast<int>(M), N, K,
+                      workspace, per);
   if (r != kOk) return r;
   const int64_t n4 = M * static_cast<int64_t>(N) / 4;
   return launch_kernel(split_sum_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)),
