@@ -15,23 +15,23 @@ QKV, O, GU, DOWN = (2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)   # (
 LEVEL = 0.04
 
 # (projection, rows, fused us (split as split_count picks), unpack + hipBLASLt us)
-FWD = [(QKV, 16, 9.64, 14.18), (QKV, 64, 11.66, 14.88), (QKV, 256, 15.99, 17.53),
-       (QKV, 512, 18.98, 18.63), (QKV, 1024, 24.54, 25.06), (QKV, 2048, 27.33, 27.94),
-       (O, 16, 9.36, 13.65), (O, 64, 10.91, 14.19), (O, 256, 14.82, 14.39),
-       (O, 512, 17.87, 17.10), (O, 1024, 24.50, 22.94), (O, 2048, 25.40, 25.35),
-       (GU, 16, 23.41, 57.03), (GU, 64, 23.96, 37.88), (GU, 512, 63.01, 53.71),
-       (GU, 1024, 113.09, 92.02), (GU, 2048, 212.75, 142.05),
-       (DOWN, 16, 14.40, 38.22), (DOWN, 64, 17.21, 40.54), (DOWN, 256, 23.60, 42.36),
-       (DOWN, 512, 36.25, 53.30), (DOWN, 1024, 60.74, 59.07), (DOWN, 2048, 133.31, 88.34)]
+FWD = [(QKV, 16, 9.36, 14.09), (QKV, 64, 11.79, 14.66), (QKV, 256, 16.23, 17.70),
+       (QKV, 512, 19.27, 18.82), (QKV, 1024, 24.67, 25.09), (QKV, 2048, 27.64, 28.03),
+       (O, 16, 9.36, 13.66), (O, 64, 10.97, 14.30), (O, 256, 14.85, 14.45),
+       (O, 512, 17.81, 17.16), (O, 1024, 24.63, 22.90), (O, 2048, 25.55, 25.54),
+       (GU, 16, 18.37, 57.39), (GU, 64, 24.15, 37.63), (GU, 512, 63.69, 55.27),
+       (GU, 1024, 116.14, 94.18), (GU, 2048, 222.58, 139.78),
+       (DOWN, 16, 12.71, 38.46), (DOWN, 64, 17.66, 40.45), (DOWN, 256, 23.90, 42.16),
+       (DOWN, 512, 37.17, 53.16), (DOWN, 1024, 64.37, 59.81), (DOWN, 2048, 135.95, 88.57)]
 # input gradient dx = dy W
-GRAD = [(QKV, 16, 11.08, 17.28), (QKV, 64, 12.89, 21.04), (QKV, 256, 17.47, 20.84),
-        (QKV, 512, 22.80, 22.04), (QKV, 1024, 30.55, 32.77), (QKV, 2048, 41.12, 34.19),
-        (O, 16, 10.08, 14.71), (O, 64, 11.02, 17.87), (O, 256, 14.52, 17.30),
-        (O, 512, 18.26, 18.43), (O, 1024, 19.88, 25.25), (O, 2048, 28.83, 28.20),
-        (GU, 16, 24.90, 74.97), (GU, 64, 26.10, 99.61), (GU, 256, 43.21, 131.81),
-        (GU, 512, 77.15, 161.93), (GU, 1024, 150.66, 219.97), (GU, 2048, 306.10, 187.19),
-        (DOWN, 16, 18.92, 24.73), (DOWN, 64, 19.31, 26.58), (DOWN, 512, 45.12, 41.54),
-        (DOWN, 1024, 77.37, 46.34), (DOWN, 2048, 139.20, 83.91)]
+GRAD = [(QKV, 16, 10.68, 17.38), (QKV, 64, 13.08, 21.23), (QKV, 256, 17.71, 20.80),
+        (QKV, 512, 23.05, 22.15), (QKV, 1024, 30.66, 32.76), (QKV, 2048, 41.40, 34.36),
+        (O, 16, 9.51, 14.70), (O, 64, 11.11, 17.92), (O, 256, 14.58, 17.43),
+        (O, 512, 18.42, 18.48), (O, 1024, 20.02, 25.34), (O, 2048, 29.09, 28.33),
+        (GU, 16, 22.42, 75.14), (GU, 64, 26.47, 99.31), (GU, 256, 43.96, 131.56),
+        (GU, 512, 77.97, 162.57), (GU, 1024, 158.09, 221.39), (GU, 2048, 313.20, 195.79),
+        (DOWN, 16, 19.02, 24.70), (DOWN, 64, 19.50, 26.50), (DOWN, 512, 46.02, 40.98),
+        (DOWN, 1024, 77.95, 47.08), (DOWN, 2048, 146.22, 85.43)]
 
 
 def fwd_fused(rows, w):
@@ -77,8 +77,8 @@ def test_window_edges():
 
 
 def test_wins_left_outside_the_window():
-    """gate|up forward at 256 rows (fused 40.0 against 48.7 us) and down's input gradient at 256
-    rows (27.8 against 35.7 us) fall just past one wave (280 tiles); the rule leaves them to
+    """gate|up forward at 256 rows (fused 40.2 against 48.8 us) and down's input gradient at 256
+    rows (27.9 against 35.7 us) fall just past one wave (280 tiles); the rule leaves them to
     unpack + hipBLASLt rather than widen the window past q|k|v at 2560 rows (320 tiles, fused
     26-34% behind)."""
     assert not fwd_fused(256, GU)
