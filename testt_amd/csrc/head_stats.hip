@@ -7,7 +7,7 @@
 // Mapping (gfx950): one workgroup of 1024 threads (16 wavefronts, a whole CU) per logits row.
 // Register-resident form (V <= 1024 * 8 * kMaxCpt): each thread loads its share of the row --
 // chunk k*1024 + tid, 16 bytes each, every wave load instruction reading 1 KiB contiguous --
-// into VGPRs (a 151,936-column row is 297 KiB = 19 x 16 B per thread, loads kept 4 deep),
+// into VGPRs (a 151,936-column row is 297 KiB = 19 x 16 B per thread, loads kept 2 deep),
 // computes the statistics from the registers as the loads land -- replacing each chunk by its
 // exponentials -- and after the workgroup reduction writes the gradient from the same
 // registers: the row crosses HBM once in and (for labelled rows) once out, the compulsory
@@ -34,8 +34,9 @@ constexpr int kHeadWaves = kHeadThreads / kWave;
 constexpr int kStreamUnroll = 2;  // 16-byte chunks per thread per step, streaming form
 constexpr int kMaxCpt = 20;       // register-resident form: up to 20 chunks (80 VGPRs) / thread
 #ifndef SOUPK_HEAD_PREFETCH
-#define SOUPK_HEAD_PREFETCH 4
+#define SOUPK_HEAD_PREFETCH 2
 #endif
+
 constexpr int kHeadPrefetch = SOUPK_HEAD_PREFETCH;  // resident form: chunk loads in flight per lane
 constexpr int64_t kIgnoreIndex = -100;
 
