@@ -326,9 +326,6 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   __shared__ f16 chunk_max[CPT * kHeadThreads];  // m_k of chunk k of thread t at [k*1024 + t]
   const int64_t row = blockIdx.x;
   uint16_t* base = logits + row * V;
-  const int64_t tgt = target[row];
-  const bool labelled = tgt != kIgnoreIndex;
-  const bool tgt_ok = tgt >= 0 && tgt < V;
   const int tid = threadIdx.x;
   const RowSpan sp = row_span(base, V);
   // The row's whole chunks as one range-checked buffer: every load is issued unconditionally
@@ -345,8 +342,6 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   const bool has_lead = tid < sp.lead, has_tail = sp.tail0 + tid < V;
   const float zlead = h2f(base[has_lead ? tid : 0]);
   const float ztail = h2f(base[has_tail ? sp.tail0 + tid : V - 1]);
-  const float zt_raw = h2f(base[tgt_ok ? tgt : 0]);
-  const float zt = tgt_ok ? zt_raw : 0.f;
   u32x4 w[CPT];
   // Chunk column k of this thread (at byte offset off0 + k*kChunkStride of the row's chunks).
   auto load_col = [&](int k) -> u32x4 {
@@ -355,6 +350,15 @@ __global__ __launch_bounds__(kHeadThreads) void head_stats_grad_kernel(
   };
 #pragma unroll
   for (int k = 0; k < P; ++k) w[k] = load_col(k);
+  __builtin_amdgcn_sched_barrier(0);
+  // The target, and then its logit, are read only once the first chunk loads are in flight:
+  // the logit's address needs the target's scalar load, and a wait for that load placed
+  // before the chunk loads held every row's first bytes back by one memory round trip.
+  const int64_t tgt = target[row];
+  const bool labelled = tgt != kIgnoreIndex;
+  const bool tgt_ok = tgt >= 0 && tgt < V;
+  const float zt_raw = h2f(base[tgt_ok ? tgt : 0]);
+  const float zt = tgt_ok ? zt_raw : 0.f;
 
   // 32-bit chunk indices (a row has < 2^28 chunks): 64-bit ones would cost a register pair
   // per chunk on top of the row.
